@@ -1,0 +1,150 @@
+/*
+ * malkin-mi355x: C ABI of the gfx950 kernels (libmalkin_hip.so).
+ *
+ * This is the device-side replacement of the reference's per-ISA operator surface, malkin::kern (src/kernels.h) and
+ * the quantization / matmul API of src/quant.h. Each entry point cites the reference interface it replaces. Unlike
+ * the reference's per-panel functions, every call here works on a whole batch in device memory.
+ *
+ * Conventions:
+ *   - every function returns MK_OK (0) or an MK_ERR_* status; mk_last_error() holds the message (thread-local),
+ *     worded like the reference's std::runtime_error texts where one exists;
+ *   - pointers named *_dev, and every tensor argument, are device pointers (mk_malloc); sizes are element counts;
+ *   - all work is queued on the context's one HIP stream, in call order; mk_synchronize waits for it;
+ *   - BlockQ8 activation blocks keep the reference's 40-byte layout (quant.h:11-16): float d; int16 s[2]; int8 qs[32].
+ */
+#ifndef MALKIN_HIP_H
+#define MALKIN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  MK_OK = 0,
+  MK_ERR_INVALID = 1,     /* bad argument; the reference throws std::runtime_error / std::invalid_argument */
+  MK_ERR_HIP = 2,         /* HIP runtime error */
+  MK_ERR_UNSUPPORTED = 3, /* type / shape without a kernel (the reference's panel_bytes == 0 row-path case) */
+  MK_ERR_NO_DEVICE = 4
+};
+
+/* ggml tensor types (gguf.h:12-29) accepted by the kernels. */
+enum { MK_F32 = 0, MK_Q8_0 = 8, MK_Q4_K = 12, MK_Q6_K = 14 };
+
+typedef struct mk_ctx mk_ctx;
+
+/* ---- context (no reference counterpart: the CPU build has no device) ---- */
+int mk_init(int device, mk_ctx** ctx);
+int mk_destroy(mk_ctx* ctx);
+/* Name of the device architecture this library runs on (replaces kern::isa_name, kernels.h:84). */
+const char* mk_device_name(const mk_ctx* ctx);
+const char* mk_last_error(void);
+int mk_synchronize(mk_ctx* ctx);
+/* The context's hipStream_t. */
+void* mk_stream(mk_ctx* ctx);
+
+/* ---- device memory (replaces PackedBuffer / LazyBytes ownership, quant.h:34-42, gguf.h:82-95) ---- */
+int mk_malloc(mk_ctx* ctx, size_t bytes, void** dev);
+int mk_free(mk_ctx* ctx, void* dev);
+int mk_upload(mk_ctx* ctx, void* dev_dst, const void* host_src, size_t bytes);
+int mk_download(mk_ctx* ctx, void* host_dst, const void* dev_src, size_t bytes);
+/* Fills with a kernel (safe inside captured graphs). */
+int mk_fill(mk_ctx* ctx, void* dev, int byte_value, size_t bytes);
+
+/* ---- timing on the context stream (bench) ---- */
+int mk_timer_start(mk_ctx* ctx);
+int mk_timer_stop(mk_ctx* ctx, float* ms);
+
+/* ---- load-time repack (replaces kern::panel_rows / panel_bytes / pack_panel, kernels.h:67-73, and
+ *      quant.h:129-134 packed_bytes / pack_weight_into) ---- */
+/* Bytes of the CDNA-packed form of a rows x cols weight; 0 = no kernel for this type/shape (rows % 8 or block). */
+size_t mk_packed_bytes(int type, int64_t rows, int64_t cols);
+/* src_dev: rows of GGUF blocks, src_row_bytes apart. dst_dev: mk_packed_bytes bytes. */
+int mk_pack_weight(mk_ctx* ctx, int type, const void* src_dev, size_t src_row_bytes, int64_t rows, int64_t cols,
+                   void* dst_dev);
+/* Inverse of mk_pack_weight: GGUF rows, ggml_row_size(type, cols) bytes apart (pack round-trip tests). */
+int mk_unpack_weight(mk_ctx* ctx, int type, const void* packed_dev, int64_t rows, int64_t cols, void* dst_dev);
+
+/* ---- activations ---- */
+/* x [n][k] f32 -> xq [n][k/32] BlockQ8 (replaces kern::quantize_row_q8, kernels.h:28; quantize_acts, quant.h:151). */
+int mk_quantize_q8(mk_ctx* ctx, const float* x, int n, int64_t k, void* xq);
+/* Per row of n floats: q = round(x / d), d = max|x| / 127 (replaces quantize_i8, quant.h:144). */
+int mk_quantize_i8(mk_ctx* ctx, const float* x, int rows, int n, int8_t* q, float* d);
+/* Rows ids[i] of a GGUF matrix (row_bytes apart) dequantized to f32 [n][k] (dequantize_row, quant.h:145; the token
+   embedding lookup of model.cpp:331-334). */
+int mk_dequantize_rows(mk_ctx* ctx, int type, const void* src, size_t row_bytes, const int32_t* ids, int n, int64_t k,
+                       float* dst);
+
+/* ---- matmul (replaces matmul / matmul_group, quant.h:154-161, and kern::gemm_panels, kernels.h:80) ---- */
+typedef struct {
+  int32_t type;  /* MK_Q8_0, MK_Q4_K, MK_Q6_K */
+  int32_t wide;  /* Q6_K only: the weight also has the reference's wide panels, used for n > 16 (quant.h:50) */
+  int64_t rows, cols;
+  const void* data; /* mk_pack_weight output */
+} mk_weight;
+
+/* y[t * y_stride + r] (+)= row r . xq[t] for t < n, r < rows. accumulate != 0 adds to y (the residual add x += h of
+   model.cpp:352-356 fused into the epilogue). Results are bit-identical to the reference's panel kernels. */
+int mk_matmul(mk_ctx* ctx, const mk_weight* w, const void* xq, int n, float* y, int64_t y_stride, int accumulate);
+
+/* ---- elementwise (model.cpp:46-49, kernels.h:39) ---- */
+/* y = rmsnorm(x) * w per row of n floats (model.cpp:46-49). */
+int mk_rmsnorm(mk_ctx* ctx, const float* x, const float* w, int rows, int n, float eps, float* y);
+/* rmsnorm of rows x[rows_idx[i]] (all rows when rows_idx is NULL) quantized straight to BlockQ8 [rows][n/32]. */
+int mk_rmsnorm_q8(mk_ctx* ctx, const float* x, const int32_t* rows_idx, const float* w, int rows, int n, float eps,
+                  void* xq);
+/* g = g / (1 + e^-g) * u (kern::silu_mul, kernels.h:39). */
+int mk_silu_mul(mk_ctx* ctx, int64_t n, float* g, const float* u);
+/* silu_mul of rows of gu = [gate | up] (2n floats per row) quantized to BlockQ8 [rows][n/32] (model.cpp:409-411). */
+int mk_silu_mul_q8(mk_ctx* ctx, const float* gu, int rows, int64_t n, void* xq);
+/* x += h (model.cpp:352-356). */
+int mk_add(mk_ctx* ctx, int64_t n, float* x, const float* h);
+
+/* ---- attention (replaces kern::attend_gqa, kernels.h:55-56) ----
+ * One query token, G heads sharing one KV head; keys/values 0..n-1 at k + j * stride (bytes), then rows extra[i];
+ * value = scale(row) * q, the float scale soff bytes after the row's first value. D % 16 == 0. */
+int mk_attend_gqa(mk_ctx* ctx, const float* q, int G, int D, const int8_t* k, const int8_t* v, size_t stride,
+                  ptrdiff_t soff, int n, float scale, float* out, const int32_t* extra, int ne);
+
+/* ---- device KV cache (replaces the reference's int8 LazyBytes kcache_ / vcache_, model.h:91, model.cpp:105-110) ----
+ * Rows of head_dim int8 values with one float scale per row, indexed [layer][seq][kv_head][position]. */
+typedef struct {
+  int8_t* k;
+  int8_t* v;
+  float* k_scale;
+  float* v_scale;
+  int32_t n_layer, n_seq, n_head_kv, head_dim, n_ctx;
+} mk_kv_cache;
+
+/* model.cpp:370-392, per token t: QK-norm (rmsnorm with q_norm / k_norm) and NeoX RoPE at position rpos[t] on the
+   n_head query heads of q and the key heads of k (in place), then k and v quantized (quantize_i8) into KV row
+   kv_row[t] of sequence seq[t] of `layer`. q, k, v share the token stride; cos_t / sin_t are [n_ctx][head_dim/2]. */
+int mk_qk_norm_rope_kv(mk_ctx* ctx, float* q, float* k, const float* v, int64_t stride, int n, int n_head,
+                       const float* q_norm, const float* k_norm, float eps, const float* cos_t, const float* sin_t,
+                       const int32_t* rpos, const int32_t* seq, const int32_t* kv_row, const mk_kv_cache* kv,
+                       int layer);
+/* Model::attention (model.cpp:204-247) over the device cache: token t attends with its n_head query heads to rows
+   0..n_keys[t]-1 of sequence seq[t], then (tree verification) rows anc[anc_off[t] .. anc_off[t+1]) when anc_off is
+   not NULL. max_keys bounds n_keys[t] + ancestors for every t. */
+int mk_attention(mk_ctx* ctx, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int n_head,
+                 const mk_kv_cache* kv, int layer, const int32_t* seq, const int32_t* n_keys, const int32_t* anc_off,
+                 const int32_t* anc, int max_keys);
+/* Model::move_kv (model.cpp:432-440): row `from` -> row `to` of sequence seq, K and V of every layer. */
+int mk_move_kv(mk_ctx* ctx, const mk_kv_cache* kv, int seq, int from, int to);
+
+/* ---- greedy selection (sampler.cpp:27-30 argmax; engine.cpp:309-318 draft top-2) ---- */
+/* Per row of n_vocab logits: top1 = first maximum, top2 = the reference's runner-up scan. top2 may be NULL. */
+int mk_argmax_top2(mk_ctx* ctx, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2);
+/* Device-resident greedy decode bookkeeping for one sequence (no reference counterpart: the CPU engine does this on
+   the host, engine.cpp:397-421): out_tokens[*counter] = ids[0] = *top1; ++*counter; ++rpos[0], ++kv_row[0],
+   ++n_keys[0]. Lets a captured decode step be replayed without host round trips. */
+int mk_greedy_advance(mk_ctx* ctx, const int32_t* top1, int32_t* ids, int32_t* rpos, int32_t* kv_row, int32_t* n_keys,
+                      int32_t* out_tokens, int32_t* counter);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,287 @@
+"""malkin-mi355x: Python bindings (ctypes) over the C ABI of libmalkin_hip.so.
+
+The C ABI (include/malkin_hip.h, include/malkin_model.h) is the product; this module only loads it for the tests and
+the benchmark. There is no fallback: if the library is missing, load() raises.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmalkin_hip.so")
+
+MK_OK, MK_ERR_INVALID, MK_ERR_HIP, MK_ERR_UNSUPPORTED, MK_ERR_NO_DEVICE = 0, 1, 2, 3, 4
+F32, Q8_0, Q4_K, Q6_K = 0, 8, 12, 14
+MODEL_NO_WIDE = 1
+
+BLOCK_Q8 = np.dtype([("d", "<f4"), ("s", "<i2", (2,)), ("qs", "i1", (32,))])
+BATCH_TOKEN = np.dtype([("id", "<i4"), ("seq", "<i4"), ("pos", "<i4"), ("logits", "<i4"), ("kv", "<i4"),
+                        ("parent", "<i4")])
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_SZ = ctypes.c_size_t
+_F = ctypes.c_float
+
+# name -> (restype, argtypes); the exports of include/malkin_hip.h and include/malkin_model.h
+SIGNATURES = {
+    "mk_init": (_I, [_I, ctypes.POINTER(_P)]),
+    "mk_destroy": (_I, [_P]),
+    "mk_device_name": (ctypes.c_char_p, [_P]),
+    "mk_last_error": (ctypes.c_char_p, []),
+    "mk_synchronize": (_I, [_P]),
+    "mk_stream": (_P, [_P]),
+    "mk_malloc": (_I, [_P, _SZ, ctypes.POINTER(_P)]),
+    "mk_free": (_I, [_P, _P]),
+    "mk_upload": (_I, [_P, _P, _P, _SZ]),
+    "mk_download": (_I, [_P, _P, _P, _SZ]),
+    "mk_fill": (_I, [_P, _P, _I, _SZ]),
+    "mk_timer_start": (_I, [_P]),
+    "mk_timer_stop": (_I, [_P, ctypes.POINTER(_F)]),
+    "mk_packed_bytes": (_SZ, [_I, _I64, _I64]),
+    "mk_pack_weight": (_I, [_P, _I, _P, _SZ, _I64, _I64, _P]),
+    "mk_unpack_weight": (_I, [_P, _I, _P, _I64, _I64, _P]),
+    "mk_quantize_q8": (_I, [_P, _P, _I, _I64, _P]),
+    "mk_quantize_i8": (_I, [_P, _P, _I, _I, _P, _P]),
+    "mk_dequantize_rows": (_I, [_P, _I, _P, _SZ, _P, _I, _I64, _P]),
+    "mk_matmul": (_I, [_P, _P, _P, _I, _P, _I64, _I]),
+    "mk_rmsnorm": (_I, [_P, _P, _P, _I, _I, _F, _P]),
+    "mk_rmsnorm_q8": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),
+    "mk_silu_mul": (_I, [_P, _I64, _P, _P]),
+    "mk_silu_mul_q8": (_I, [_P, _P, _I, _I64, _P]),
+    "mk_add": (_I, [_P, _I64, _P, _P]),
+    "mk_attend_gqa": (_I, [_P, _P, _I, _I, _P, _P, _SZ, ctypes.c_ssize_t, _I, _F, _P, _P, _I]),
+    "mk_qk_norm_rope_kv": (_I, [_P, _P, _P, _P, _I64, _I, _I, _P, _P, _F, _P, _P, _P, _P, _P, _P, _I]),
+    "mk_attention": (_I, [_P, _P, _I64, _P, _I64, _I, _I, _P, _I, _P, _P, _P, _P, _I]),
+    "mk_move_kv": (_I, [_P, _P, _I, _I, _I]),
+    "mk_argmax_top2": (_I, [_P, _P, _I, _I, _P, _P]),
+    "mk_greedy_advance": (_I, [_P, _P, _P, _P, _P, _P, _P, _P]),
+    "mk_model_open": (_I, [_P, ctypes.c_char_p, _I, _I, _I, ctypes.POINTER(_P)]),
+    "mk_model_free": (_I, [_P]),
+    "mk_model_get_config": (_I, [_P, _P]),
+    "mk_model_forward_batch": (_I, [_P, _P, _I, _P]),
+    "mk_model_forward": (_I, [_P, _P, _I, _I, _P, _I, _P, _I]),
+    "mk_model_forward_top2": (_I, [_P, _P, _I, _P, _P]),
+    "mk_model_move_kv": (_I, [_P, _I, _I, _I]),
+    "mk_model_kv_row": (_I, [_P, _I, _I, _I, _I, _P]),
+    "mk_model_generate": (_I, [_P, _P, _I, _I, _I, _I, _P, _P]),
+    "mk_model_weight_bytes": (_I64, [_P]),
+    "mk_model_weight": (_I, [_P, _I, _I, _P]),
+}
+
+_lib = None
+
+
+class MkError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(msg)
+        self.code = code
+
+
+def load():
+    """The native library; raises if it is not built (there is no non-native path)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build()")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(lib, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def check(rc):
+    if rc != MK_OK:
+        raise MkError(rc, load().mk_last_error().decode())
+
+
+def _ptr(a):
+    return ctypes.c_void_p(a.ctypes.data) if a is not None else None
+
+
+class Buffer:
+    """Device allocation (mk_malloc) with numpy upload/download helpers."""
+
+    def __init__(self, ctx, nbytes):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        p = _P()
+        check(load().mk_malloc(ctx.h, max(1, self.nbytes), ctypes.byref(p)))
+        self.p = p.value
+
+    @property
+    def ptr(self):
+        return ctypes.c_void_p(self.p)
+
+    def offset(self, nbytes):
+        return ctypes.c_void_p(self.p + int(nbytes))
+
+    def upload(self, arr, offset=0):
+        arr = np.ascontiguousarray(arr)
+        assert offset + arr.nbytes <= self.nbytes
+        check(load().mk_upload(self.ctx.h, self.offset(offset), _ptr(arr), arr.nbytes))
+        return self
+
+    def download(self, dtype, count=None, offset=0):
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dtype.itemsize
+        out = np.empty(count, dtype=dtype)
+        check(load().mk_download(self.ctx.h, _ptr(out), self.offset(offset), out.nbytes))
+        return out
+
+    def free(self):
+        # After the context is destroyed its allocations are gone with it; nothing left to free.
+        if self.p and self.ctx.h:
+            load().mk_free(self.ctx.h, ctypes.c_void_p(self.p))
+        self.p = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Context:
+    def __init__(self, device=0):
+        p = _P()
+        check(load().mk_init(device, ctypes.byref(p)))
+        self.h = p.value
+
+    def close(self):
+        if self.h:
+            load().mk_destroy(self.h)
+            self.h = None
+
+    @property
+    def device_name(self):
+        return load().mk_device_name(self.h).decode()
+
+    def sync(self):
+        check(load().mk_synchronize(self.h))
+
+    def alloc(self, nbytes):
+        return Buffer(self, nbytes)
+
+    def to_device(self, arr):
+        arr = np.ascontiguousarray(arr)
+        return Buffer(self, arr.nbytes).upload(arr)
+
+    def timer_start(self):
+        check(load().mk_timer_start(self.h))
+
+    def timer_stop(self):
+        ms = _F()
+        check(load().mk_timer_stop(self.h, ctypes.byref(ms)))
+        return ms.value
+
+
+class MkWeight(ctypes.Structure):
+    _fields_ = [("type", ctypes.c_int32), ("wide", ctypes.c_int32), ("rows", ctypes.c_int64),
+                ("cols", ctypes.c_int64), ("data", ctypes.c_void_p)]
+
+
+class MkKvCache(ctypes.Structure):
+    _fields_ = [("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("k_scale", ctypes.c_void_p),
+                ("v_scale", ctypes.c_void_p), ("n_layer", ctypes.c_int32), ("n_seq", ctypes.c_int32),
+                ("n_head_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("n_ctx", ctypes.c_int32)]
+
+
+class MkModelConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("n_layer", "n_embd", "n_ff", "n_head", "n_head_kv", "head_dim",
+                                              "n_vocab", "n_ctx", "n_seq")] + [("rope_base", ctypes.c_float),
+                                                                              ("rms_eps", ctypes.c_float)]
+
+
+class MkGenStats(ctypes.Structure):
+    _fields_ = [("prefill_ms", ctypes.c_double), ("decode_ms", ctypes.c_double), ("decode_forwards", ctypes.c_int32)]
+
+
+class Model:
+    """mk_model_* wrapper: the device counterpart of the reference's Model (model.h)."""
+
+    def __init__(self, ctx, path, n_ctx, n_seq=1, wide=True):
+        self.ctx = ctx
+        p = _P()
+        check(load().mk_model_open(ctx.h, path.encode(), n_ctx, n_seq, 0 if wide else MODEL_NO_WIDE,
+                                   ctypes.byref(p)))
+        self.h = p.value
+        c = MkModelConfig()
+        check(load().mk_model_get_config(self.h, ctypes.byref(c)))
+        self.cfg = {f: getattr(c, f) for f, _ in MkModelConfig._fields_}
+
+    def close(self):
+        if self.h and self.ctx.h:
+            load().mk_model_free(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def weight_bytes(self):
+        return int(load().mk_model_weight_bytes(self.h))
+
+    def weight(self, layer, which):
+        w = MkWeight()
+        check(load().mk_model_weight(self.h, layer, which, ctypes.byref(w)))
+        return w
+
+    def forward_batch(self, batch):
+        batch = np.ascontiguousarray(batch, dtype=BATCH_TOKEN)
+        nl = int((batch["logits"] != 0).sum())
+        logits = np.zeros((max(nl, 1), self.cfg["n_vocab"]), dtype=np.float32)
+        check(load().mk_model_forward_batch(self.h, _ptr(batch), len(batch), _ptr(logits)))
+        return logits[:nl]
+
+    def forward(self, tokens, pos, all_logits=False, parent=None, seq=0):
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        n = len(tokens)
+        logits = np.zeros((n if all_logits else 1, self.cfg["n_vocab"]), dtype=np.float32)
+        par = None if parent is None else np.ascontiguousarray(parent, dtype=np.int32)
+        check(load().mk_model_forward(self.h, _ptr(tokens), n, pos, _ptr(logits), 1 if all_logits else 0, _ptr(par),
+                                      seq))
+        return logits
+
+    def forward_top2(self, batch):
+        batch = np.ascontiguousarray(batch, dtype=BATCH_TOKEN)
+        nl = int((batch["logits"] != 0).sum())
+        t1 = np.zeros(max(nl, 1), dtype=np.int32)
+        t2 = np.zeros(max(nl, 1), dtype=np.int32)
+        check(load().mk_model_forward_top2(self.h, _ptr(batch), len(batch), _ptr(t1), _ptr(t2)))
+        return t1[:nl], t2[:nl]
+
+    def move_kv(self, frm, to, seq=0):
+        check(load().mk_model_move_kv(self.h, frm, to, seq))
+
+    def kv_row(self, layer, seq, pos, k=True):
+        nb = self.cfg["n_head_kv"] * (self.cfg["head_dim"] + 4)
+        out = np.zeros(nb, dtype=np.int8)
+        check(load().mk_model_kv_row(self.h, layer, seq, pos, 1 if k else 0, _ptr(out)))
+        return out
+
+    def generate(self, prompt, n_gen, seq=0, use_graph=True):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.zeros(n_gen, dtype=np.int32)
+        st = MkGenStats()
+        check(load().mk_model_generate(self.h, _ptr(prompt), len(prompt), n_gen, seq, 1 if use_graph else 0,
+                                       _ptr(out), ctypes.byref(st)))
+        return out, {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms, "decode_forwards": st.decode_forwards}
+
+
+def batch(tokens):
+    """Structured BatchToken array from (id, seq, pos, logits[, kv, parent]) tuples."""
+    out = np.zeros(len(tokens), dtype=BATCH_TOKEN)
+    for i, t in enumerate(tokens):
+        t = tuple(t) + (-1, -1)[len(t) - 4:] if len(t) < 6 else tuple(t)
+        out[i] = t[:6]
+    return out

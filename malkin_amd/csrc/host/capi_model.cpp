@@ -1,0 +1,119 @@
+// extern "C" layer of include/malkin_model.h over malkin_hip::Model.
+#include <cstdio>
+#include <exception>
+#include <memory>
+#include <stdexcept>
+#include <vector>
+
+#include "../../../include/malkin_model.h"
+#include "../kernels/ctx.h"
+#include "model.h"
+
+struct mk_model {
+  std::unique_ptr<malkin_hip::GgufFile> file;
+  std::unique_ptr<malkin_hip::Model> model;
+};
+
+namespace {
+
+template <typename F>
+int run(F&& f) {
+  try {
+    f();
+    return MK_OK;
+  } catch (const std::invalid_argument& e) {
+    mk::set_error("%s", e.what());
+    return MK_ERR_INVALID;
+  } catch (const std::exception& e) {
+    mk::set_error("%s", e.what());
+    return MK_ERR_INVALID;
+  }
+}
+
+std::vector<malkin_hip::BatchToken> to_batch(const mk_batch_token* b, int n) {
+  std::vector<malkin_hip::BatchToken> v(static_cast<size_t>(n > 0 ? n : 0));
+  for (int i = 0; i < n; ++i) v[i] = {b[i].id, b[i].seq, b[i].pos, b[i].logits != 0, b[i].kv, b[i].parent};
+  return v;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mk_model_open(mk_ctx* ctx, const char* path, int n_ctx, int n_seq, int flags, mk_model** out) {
+  return run([&] {
+    if (!ctx || !path || !out) throw std::invalid_argument("mk_model_open: null argument");
+    auto m = std::make_unique<mk_model>();
+    m->file = std::make_unique<malkin_hip::GgufFile>(path);
+    m->model = std::make_unique<malkin_hip::Model>(ctx, *m->file, n_ctx, n_seq, (flags & MK_MODEL_NO_WIDE) == 0);
+    *out = m.release();
+  });
+}
+
+int mk_model_free(mk_model* m) {
+  return run([&] { delete m; });
+}
+
+int mk_model_get_config(const mk_model* m, mk_model_config* o) {
+  return run([&] {
+    const auto& c = m->model->cfg();
+    *o = mk_model_config{c.n_layer, c.n_embd, c.n_ff, c.n_head, c.n_head_kv, c.head_dim, c.n_vocab,
+                         m->model->n_ctx(), m->model->n_seq(), c.rope_base, c.rms_eps};
+  });
+}
+
+int mk_model_forward_batch(mk_model* m, const mk_batch_token* batch, int n, float* logits) {
+  return run([&] {
+    if (n > 0 && !batch) throw std::invalid_argument("forward: null batch");
+    auto b = to_batch(batch, n);
+    m->model->forward(b.data(), n, logits);
+  });
+}
+
+int mk_model_forward(mk_model* m, const int32_t* tokens, int n, int pos, float* logits, int all_logits,
+                     const int32_t* parent, int seq) {
+  return run([&] { m->model->forward(tokens, n, pos, logits, all_logits != 0, parent, seq); });
+}
+
+int mk_model_forward_top2(mk_model* m, const mk_batch_token* batch, int n, int32_t* top1, int32_t* top2) {
+  return run([&] {
+    if (n > 0 && !batch) throw std::invalid_argument("forward: null batch");
+    auto b = to_batch(batch, n);
+    m->model->forward_top2(b.data(), n, top1, top2);
+  });
+}
+
+int mk_model_move_kv(mk_model* m, int from, int to, int seq) {
+  return run([&] {
+    if (seq < 0 || seq >= m->model->n_seq() || from < 0 || to < 0 || from >= m->model->n_ctx() ||
+        to >= m->model->n_ctx())
+      throw std::invalid_argument("move_kv: bad row");
+    m->model->move_kv(from, to, seq);
+  });
+}
+
+int mk_model_kv_row(mk_model* m, int layer, int seq, int pos, int k, void* out) {
+  return run([&] {
+    const auto& c = m->model->cfg();
+    if (layer < 0 || layer >= c.n_layer || seq < 0 || seq >= m->model->n_seq() || pos < 0 || pos >= m->model->n_ctx())
+      throw std::invalid_argument("kv_row: bad index");
+    m->model->kv_row(layer, seq, pos, k != 0, static_cast<uint8_t*>(out));
+  });
+}
+
+int mk_model_generate(mk_model* m, const int32_t* prompt, int n_prompt, int n_gen, int seq, int use_graph,
+                      int32_t* out_tokens, mk_gen_stats* stats) {
+  return run([&] {
+    malkin_hip::Model::GenStats st;
+    m->model->generate_greedy(prompt, n_prompt, n_gen, seq, out_tokens, &st, use_graph != 0);
+    if (stats) *stats = mk_gen_stats{st.prefill_ms, st.decode_ms, st.decode_forwards};
+  });
+}
+
+int64_t mk_model_weight_bytes(const mk_model* m) { return m ? static_cast<int64_t>(m->model->weight_bytes()) : 0; }
+
+int mk_model_weight(const mk_model* m, int layer, int which, mk_weight* out) {
+  return run([&] { *out = m->model->weight(layer, which); });
+}
+
+}  // extern "C"

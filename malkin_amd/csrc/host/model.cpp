@@ -1,0 +1,526 @@
+#include "model.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <stdexcept>
+
+namespace malkin_hip {
+
+namespace {
+
+// C-ABI status -> the reference's exception convention.
+void ck(int rc) {
+  if (rc != MK_OK) throw std::runtime_error(mk_last_error());
+}
+
+void hck(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+bool device_type(uint32_t t) { return t == MK_Q8_0 || t == MK_Q4_K || t == MK_Q6_K; }
+
+using Clock = std::chrono::steady_clock;
+double ms_since(Clock::time_point t) { return std::chrono::duration<double, std::milli>(Clock::now() - t).count(); }
+
+}  // namespace
+
+DevBuf::DevBuf(mk_ctx* c, size_t n) : ctx(c), bytes(n) { ck(mk_malloc(c, n, &p)); }
+
+DevBuf& DevBuf::operator=(DevBuf&& o) noexcept {
+  if (this != &o) {
+    if (p) mk_free(ctx, p);
+    ctx = o.ctx;
+    p = o.p;
+    bytes = o.bytes;
+    o.p = nullptr;
+  }
+  return *this;
+}
+
+DevBuf::~DevBuf() {
+  if (p) mk_free(ctx, p);
+}
+
+mk_weight Model::Weight::w() const { return mk_weight{type, 0, rows, cols, packed.p}; }
+
+// model.cpp:78-101
+ModelConfig read_config(const GgufFile& f) {
+  ModelConfig c;
+  c.arch = f.get_str("general.architecture").value_or("");
+  c.name = f.get_str("general.name").value_or("model");
+  if (c.arch != "qwen3") throw std::runtime_error("architecture '" + c.arch + "' unsupported (supported: qwen3)");
+  auto key = [&](const std::string& k) { return c.arch + "." + k; };
+  auto need = [&](const std::string& k) {
+    auto v = f.get_int(key(k));
+    if (!v) throw std::runtime_error("model: metadata " + key(k) + " missing");
+    return static_cast<int>(*v);
+  };
+  c.n_layer = need("block_count");
+  c.n_embd = need("embedding_length");
+  c.n_ff = need("feed_forward_length");
+  c.n_head = need("attention.head_count");
+  c.n_head_kv = static_cast<int>(f.get_int(key("attention.head_count_kv")).value_or(c.n_head));
+  c.head_dim = static_cast<int>(f.get_int(key("attention.key_length")).value_or(c.n_embd / c.n_head));
+  c.n_ctx_train = static_cast<int>(f.get_int(key("context_length")).value_or(4096));
+  c.rope_base = static_cast<float>(f.get_float(key("rope.freq_base")).value_or(10000.0));
+  c.rms_eps = static_cast<float>(f.get_float(key("attention.layer_norm_rms_epsilon")).value_or(1e-6));
+  c.n_vocab = static_cast<int>(f.str_array_size("tokenizer.ggml.tokens"));
+  return c;
+}
+
+// Packs the named GGUF matrices (same type and column count) as one row-concatenated weight.
+void Model::load_weight(const GgufFile& f, const std::vector<std::string>& names, Weight& w) {
+  std::vector<const GgufTensor*> ts;
+  for (const auto& nm : names) {
+    const GgufTensor* t = f.tensor(nm);
+    if (!t) throw std::runtime_error("model: tensor " + nm + " missing");
+    if (!device_type(t->type))
+      throw std::runtime_error("model: tensor " + nm + " has type " + ggml_type_name(t->type) +
+                               ", supported on the device: Q8_0 Q4_K Q6_K");
+    ts.push_back(t);
+  }
+  w.type = static_cast<int>(ts[0]->type);
+  w.cols = ts[0]->ne[0];
+  w.rows = 0;
+  for (const GgufTensor* t : ts) {
+    if (t->type != ts[0]->type || t->ne[0] != w.cols) throw std::runtime_error("model: fused weights differ in type");
+    w.rows += t->rows();
+  }
+  const size_t rb = ggml_row_size(w.type, w.cols);
+  const size_t pb = mk_packed_bytes(w.type, w.rows, w.cols);
+  if (!pb) throw std::runtime_error("model: weight " + names[0] + " has no device layout (rows % 8)");
+  DevBuf staging(ctx_, rb * static_cast<size_t>(w.rows));
+  size_t off = 0;
+  for (const GgufTensor* t : ts) {
+    ck(mk_upload(ctx_, staging.as<uint8_t>() + off, t->data, t->nbytes));
+    off += t->nbytes;
+  }
+  w.packed = DevBuf(ctx_, pb);
+  ck(mk_pack_weight(ctx_, w.type, staging.p, rb, w.rows, w.cols, w.packed.p));
+  ck(mk_synchronize(ctx_));
+  weight_bytes_ += pb;
+}
+
+void Model::load_group(const GgufFile& f, const std::vector<std::string>& names, Group& g) {
+  size_t i = 0;
+  while (i < names.size()) {
+    const GgufTensor* t = f.tensor(names[i]);
+    if (!t) throw std::runtime_error("model: tensor " + names[i] + " missing");
+    std::vector<std::string> run{names[i]};
+    size_t j = i + 1;
+    for (; j < names.size(); ++j) {
+      const GgufTensor* u = f.tensor(names[j]);
+      if (!u) throw std::runtime_error("model: tensor " + names[j] + " missing");
+      if (u->type != t->type) break;
+      run.push_back(names[j]);
+    }
+    Weight w;
+    load_weight(f, run, w);
+    w.out_off = g.rows;
+    g.rows += w.rows;
+    g.parts.push_back(std::move(w));
+    i = j;
+  }
+}
+
+// quant.cpp:287-328 (matmul_group): every part writes its rows of the shared output row [t][g.rows].
+void Model::matmul_group(const Group& g, const void* xq, int n, float* y) {
+  for (const Weight& p : g.parts) {
+    mk_weight w = p.w();
+    w.wide = wide_ ? 1 : 0;
+    ck(mk_matmul(ctx_, &w, xq, n, y + p.out_off, g.rows, 0));
+  }
+}
+
+Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide)
+    : ctx_(ctx), cfg_(read_config(f)), n_ctx_(n_ctx), n_seq_(n_seq), wide_(wide) {
+  auto& c = cfg_;
+  if (c.head_dim % 32 || c.n_head % c.n_head_kv) throw std::runtime_error("model: unsupported head layout");
+  if (n_ctx <= 0 || n_seq <= 0) throw std::runtime_error("model: n_ctx and n_seq must be positive");
+  const int E = c.n_embd, D = c.head_dim, H = c.n_head, KV = c.n_head_kv, F = c.n_ff;
+
+  const GgufTensor* te = f.tensor("token_embd.weight");
+  if (!te) throw std::runtime_error("model: tensor token_embd.weight missing");
+  embd_type_ = static_cast<int>(te->type);
+  if (!device_type(te->type) && te->type != 0)
+    throw std::runtime_error("model: tensor token_embd.weight has unsupported type");
+  embd_row_bytes_ = ggml_row_size(te->type, te->ne[0]);
+  embd_rows_ = DevBuf(ctx_, te->nbytes);
+  ck(mk_upload(ctx_, embd_rows_.p, te->data, te->nbytes));
+  if (f.tensor("output.weight"))
+    load_weight(f, {"output.weight"}, output_);
+  else
+    load_weight(f, {"token_embd.weight"}, output_);  // tied embeddings (model.cpp:116-118)
+  c.n_vocab = static_cast<int>(output_.rows);
+
+  auto upload_norm = [&](const std::string& nm, int64_t n, float* dst) {
+    const GgufTensor* t = f.tensor(nm);
+    if (!t) throw std::runtime_error("model: tensor " + nm + " missing");
+    if (t->type != 0 || t->nelements() != n)
+      throw std::runtime_error("model: norm " + nm + " not F32[" + std::to_string(n) + "]");
+    ck(mk_upload(ctx_, dst, t->data, n * sizeof(float)));
+  };
+  output_norm_ = DevBuf(ctx_, E * sizeof(float));
+  upload_norm("output_norm.weight", E, output_norm_.as<float>());
+  layers_.resize(c.n_layer);
+  for (int i = 0; i < c.n_layer; ++i) {
+    const std::string p = "blk." + std::to_string(i) + ".";
+    Layer& L = layers_[i];
+    L.norms = DevBuf(ctx_, (2 * E + 2 * D) * sizeof(float));
+    upload_norm(p + "attn_norm.weight", E, L.norms.as<float>());
+    upload_norm(p + "ffn_norm.weight", E, L.norms.as<float>() + E);
+    upload_norm(p + "attn_q_norm.weight", D, L.norms.as<float>() + 2 * E);
+    upload_norm(p + "attn_k_norm.weight", D, L.norms.as<float>() + 2 * E + D);
+    load_group(f, {p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"}, L.qkv);
+    load_weight(f, {p + "attn_output.weight"}, L.wo);
+    load_group(f, {p + "ffn_gate.weight", p + "ffn_up.weight"}, L.gateup);
+    load_weight(f, {p + "ffn_down.weight"}, L.down);
+    if (L.qkv.rows != (int64_t)(H + 2 * KV) * D || L.wo.rows != E || L.gateup.rows != 2 * F || L.down.rows != E)
+      throw std::runtime_error("model: layer " + std::to_string(i) + " has unexpected shapes");
+  }
+
+  // RoPE tables (model.cpp:137, 335-339), computed on the host with the same float pow / cos / sin calls.
+  std::vector<float> inv(D / 2), cs(static_cast<size_t>(n_ctx) * D / 2), sn(cs.size());
+  for (int i = 0; i < D / 2; ++i) inv[i] = std::pow(c.rope_base, -2.0f * i / c.head_dim);
+  for (int pos = 0; pos < n_ctx; ++pos)
+    for (int i = 0; i < D / 2; ++i) {
+      const float a = static_cast<float>(pos) * inv[i];
+      cs[static_cast<size_t>(pos) * D / 2 + i] = std::cos(a);
+      sn[static_cast<size_t>(pos) * D / 2 + i] = std::sin(a);
+    }
+  rope_cos_ = DevBuf(ctx_, cs.size() * sizeof(float));
+  rope_sin_ = DevBuf(ctx_, sn.size() * sizeof(float));
+  ck(mk_upload(ctx_, rope_cos_.p, cs.data(), cs.size() * sizeof(float)));
+  ck(mk_upload(ctx_, rope_sin_.p, sn.data(), sn.size() * sizeof(float)));
+
+  const size_t rows = static_cast<size_t>(c.n_layer) * n_seq * KV * n_ctx;
+  kc_ = DevBuf(ctx_, rows * D);
+  vc_ = DevBuf(ctx_, rows * D);
+  ks_ = DevBuf(ctx_, rows * sizeof(float));
+  vs_ = DevBuf(ctx_, rows * sizeof(float));
+  ck(mk_fill(ctx_, kc_.p, 0, kc_.bytes));
+  ck(mk_fill(ctx_, vc_.p, 0, vc_.bytes));
+  ck(mk_fill(ctx_, ks_.p, 0, ks_.bytes));
+  ck(mk_fill(ctx_, vs_.p, 0, vs_.bytes));
+
+  const size_t B = kMaxBatch;
+  const size_t qkv_rows = static_cast<size_t>(H + 2 * KV) * D;
+  const size_t kmax = std::max({static_cast<size_t>(E), static_cast<size_t>(H) * D, static_cast<size_t>(F)});
+  x_ = DevBuf(ctx_, B * E * sizeof(float));
+  qkv_ = DevBuf(ctx_, B * qkv_rows * sizeof(float));
+  att_ = DevBuf(ctx_, B * H * D * sizeof(float));
+  gu_ = DevBuf(ctx_, B * 2 * F * sizeof(float));
+  xq_ = DevBuf(ctx_, B * (kmax / 32) * 40);
+  logits_ = DevBuf(ctx_, B * static_cast<size_t>(c.n_vocab) * sizeof(float));
+  top_ = DevBuf(ctx_, 2 * B * sizeof(int32_t) + 2 * sizeof(int32_t));
+
+  // Layout block: ids rpos seq kv_row n_keys out [B each], anc_off [B + 1], anc [B (B + 1) / 2].
+  const size_t words = 6 * B + (B + 1) + B * (B + 1) / 2;
+  host_block_.assign(words, 0);
+  layout_ = DevBuf(ctx_, words * sizeof(int32_t));
+  int32_t* d = layout_.as<int32_t>();
+  d_ids_ = d;
+  d_rpos_ = d + B;
+  d_seq_ = d + 2 * B;
+  d_kv_row_ = d + 3 * B;
+  d_n_keys_ = d + 4 * B;
+  d_out_ = d + 5 * B;
+  d_anc_off_ = d + 6 * B;
+  d_anc_ = d + 7 * B + 1;
+  ck(mk_synchronize(ctx_));
+}
+
+Model::~Model() = default;
+
+mk_weight Model::weight(int layer, int which) const {
+  if (which == 4) return output_.w();
+  if (layer < 0 || layer >= cfg_.n_layer || which < 0 || which > 3) throw std::invalid_argument("weight: bad index");
+  const Layer& L = layers_[layer];
+  if ((which == 0 && L.qkv.parts.size() != 1) || (which == 2 && L.gateup.parts.size() != 1))
+    throw std::invalid_argument("weight: this group is split by type");
+  const Weight* w[4] = {&L.qkv.parts[0], &L.wo, &L.gateup.parts[0], &L.down};
+  mk_weight r = w[which]->w();
+  r.wide = wide_ ? 1 : 0;
+  return r;
+}
+
+void Model::check_ids(const int32_t* ids, int n) {
+  for (int t = 0; t < n; ++t)
+    if (ids[t] < 0 || ids[t] >= cfg_.n_vocab) throw std::runtime_error("forward: token id out of range");
+}
+
+// model.cpp:280-323 (batch validation and per-token layout)
+void Model::build_layout(const BatchToken* batch, int n) {
+  if (n <= 0 || n > kMaxBatch) throw std::runtime_error("forward: batch size out of range");
+  ids_.resize(n);
+  rpos_.resize(n);
+  seq_.resize(n);
+  kv_row_.resize(n);
+  n_keys_.resize(n);
+  out_.clear();
+  anc_.clear();
+  anc_off_.clear();
+  tree_ = false;
+  for (int t = 0; t < n; ++t) {
+    const BatchToken& b = batch[t];
+    const int kv = b.parent < 0 ? b.pos : b.kv;
+    if (b.seq < 0 || b.seq >= n_seq_ || b.pos < 0 || b.pos >= n_ctx_ || kv < 0 || kv >= n_ctx_)
+      throw std::runtime_error("forward: bad slot");
+    if (b.parent >= t || (b.parent >= 0 && batch[b.parent].seq != b.seq))
+      throw std::runtime_error("forward: bad tree parent");
+    ids_[t] = b.id;
+    rpos_[t] = b.pos;
+    seq_[t] = b.seq;
+    kv_row_[t] = kv;
+    tree_ = tree_ || b.parent >= 0;
+    if (b.logits) out_.push_back(t);
+  }
+  // Keys: plain tokens 0..pos; tree tokens the parent's keys (contiguous part, then its ancestor rows) plus their own
+  // row.
+  if (tree_) anc_off_.push_back(0);
+  for (int t = 0; t < n; ++t) {
+    const BatchToken& b = batch[t];
+    if (b.parent < 0) {
+      n_keys_[t] = b.pos + 1;
+    } else {
+      n_keys_[t] = n_keys_[b.parent];
+      for (int i = anc_off_[b.parent]; i < anc_off_[b.parent + 1]; ++i) {
+        const int32_t row = anc_[i];
+        anc_.push_back(row);
+      }
+      anc_.push_back(kv_row_[t]);
+    }
+    if (tree_) anc_off_.push_back(static_cast<int32_t>(anc_.size()));
+  }
+  check_ids(ids_.data(), n);
+}
+
+void Model::upload_layout(int n) {
+  const int B = kMaxBatch;
+  if (anc_.size() > static_cast<size_t>(B) * (B + 1) / 2) throw std::runtime_error("forward: tree too deep");
+  int32_t* h = host_block_.data();
+  std::copy(ids_.begin(), ids_.end(), h);
+  std::copy(rpos_.begin(), rpos_.end(), h + B);
+  std::copy(seq_.begin(), seq_.end(), h + 2 * B);
+  std::copy(kv_row_.begin(), kv_row_.end(), h + 3 * B);
+  std::copy(n_keys_.begin(), n_keys_.end(), h + 4 * B);
+  std::copy(out_.begin(), out_.end(), h + 5 * B);
+  std::copy(anc_off_.begin(), anc_off_.end(), h + 6 * B);
+  std::copy(anc_.begin(), anc_.end(), h + 7 * B + 1);
+  max_keys_ = 1;
+  for (int t = 0; t < n; ++t) {
+    const int extra = tree_ ? anc_off_[t + 1] - anc_off_[t] : 0;
+    max_keys_ = std::max(max_keys_, n_keys_[t] + extra);
+  }
+  const size_t words = 7 * static_cast<size_t>(B) + 1 + anc_.size();
+  ck(mk_upload(ctx_, layout_.p, h, words * sizeof(int32_t)));
+}
+
+// model.cpp:325-426 on the device.
+void Model::run(int n) {
+  const auto& c = cfg_;
+  const int E = c.n_embd, D = c.head_dim, H = c.n_head, KV = c.n_head_kv, F = c.n_ff;
+  const int64_t QKV = static_cast<int64_t>(H + 2 * KV) * D;
+  float* x = x_.as<float>();
+  float* qkv = qkv_.as<float>();
+  float* att = att_.as<float>();
+  float* gu = gu_.as<float>();
+  void* xq = xq_.p;
+  const mk_kv_cache kv{kc_.as<int8_t>(), vc_.as<int8_t>(), ks_.as<float>(), vs_.as<float>(), c.n_layer, n_seq_, KV, D,
+                       n_ctx_};
+  ck(mk_dequantize_rows(ctx_, embd_type_, embd_rows_.p, embd_row_bytes_, d_ids_, n, E, x));
+  for (int il = 0; il < c.n_layer; ++il) {
+    const Layer& L = layers_[il];
+    const float* norms = L.norms.as<float>();
+    ck(mk_rmsnorm_q8(ctx_, x, nullptr, norms, n, E, c.rms_eps, xq));
+    matmul_group(L.qkv, xq, n, qkv);
+    ck(mk_qk_norm_rope_kv(ctx_, qkv, qkv + static_cast<int64_t>(H) * D, qkv + static_cast<int64_t>(H + KV) * D, QKV, n,
+                          H, norms + 2 * E, norms + 2 * E + D, c.rms_eps, rope_cos_.as<float>(),
+                          rope_sin_.as<float>(), d_rpos_, d_seq_, d_kv_row_, &kv, il));
+    ck(mk_attention(ctx_, qkv, QKV, att, static_cast<int64_t>(H) * D, n, H, &kv, il, d_seq_, d_n_keys_,
+                    tree_ ? d_anc_off_ : nullptr, d_anc_, max_keys_));
+    ck(mk_quantize_q8(ctx_, att, n, static_cast<int64_t>(H) * D, xq));
+    mk_weight wo = L.wo.w();
+    wo.wide = wide_ ? 1 : 0;
+    ck(mk_matmul(ctx_, &wo, xq, n, x, E, 1));  // x += attn_output(att) (model.cpp:398-401)
+    ck(mk_rmsnorm_q8(ctx_, x, nullptr, norms + E, n, E, c.rms_eps, xq));
+    matmul_group(L.gateup, xq, n, gu);
+    ck(mk_silu_mul_q8(ctx_, gu, n, F, xq));
+    mk_weight wd = L.down.w();
+    wd.wide = wide_ ? 1 : 0;
+    ck(mk_matmul(ctx_, &wd, xq, n, x, E, 1));  // x += ffn_down(...) (model.cpp:412-416)
+  }
+  const int m = static_cast<int>(out_.size());
+  if (m == 0) return;
+  ck(mk_rmsnorm_q8(ctx_, x, d_out_, output_norm_.as<float>(), m, E, c.rms_eps, xq));
+  mk_weight wout = output_.w();
+  wout.wide = wide_ ? 1 : 0;
+  ck(mk_matmul(ctx_, &wout, xq, m, logits_.as<float>(), c.n_vocab, 0));
+}
+
+void Model::forward(const BatchToken* batch, int n, float* logits) {
+  build_layout(batch, n);
+  upload_layout(n);
+  run(n);
+  if (!out_.empty() && logits)
+    ck(mk_download(ctx_, logits, logits_.p, out_.size() * static_cast<size_t>(cfg_.n_vocab) * sizeof(float)));
+  ck(mk_synchronize(ctx_));
+}
+
+void Model::forward_top2(const BatchToken* batch, int n, int32_t* top1, int32_t* top2) {
+  build_layout(batch, n);
+  upload_layout(n);
+  run(n);
+  const int m = static_cast<int>(out_.size());
+  if (m > 0) {
+    int32_t* d1 = top_.as<int32_t>();
+    int32_t* d2 = d1 + kMaxBatch;
+    ck(mk_argmax_top2(ctx_, logits_.as<float>(), m, cfg_.n_vocab, d1, d2));
+    if (top1) ck(mk_download(ctx_, top1, d1, m * sizeof(int32_t)));
+    if (top2) ck(mk_download(ctx_, top2, d2, m * sizeof(int32_t)));
+  }
+  ck(mk_synchronize(ctx_));
+}
+
+// model.cpp:249-278
+void Model::forward(const int32_t* tokens, int n, int pos, float* logits, bool all_logits, const int* parent,
+                    int seq) {
+  if (n <= 0 || n > kMaxBatch) throw std::runtime_error("forward: batch size out of range");
+  if (pos + n > n_ctx_) throw std::runtime_error("forward: context full");
+  if (seq < 0 || seq >= n_seq_) throw std::runtime_error("forward: bad sequence");
+  ids_.assign(tokens, tokens + n);
+  rpos_.resize(n);
+  seq_.assign(n, seq);
+  kv_row_.resize(n);
+  n_keys_.resize(n);
+  out_.clear();
+  anc_.clear();
+  anc_off_.clear();
+  tree_ = parent != nullptr;
+  if (parent) {  // tree: depth and ancestor KV positions (self included), root first
+    depth_.assign(n, 0);
+    for (int t = 0; t < n; ++t) {
+      depth_[t] = parent[t] < 0 ? 0 : depth_[parent[t]] + 1;
+      anc_off_.push_back(static_cast<int32_t>(anc_.size()));
+      const size_t start = anc_.size();
+      for (int a = t; a >= 0; a = parent[a]) anc_.push_back(pos + a);
+      std::reverse(anc_.begin() + static_cast<std::ptrdiff_t>(start), anc_.end());
+    }
+    anc_off_.push_back(static_cast<int32_t>(anc_.size()));
+  }
+  for (int t = 0; t < n; ++t) {
+    rpos_[t] = pos + (parent ? depth_[t] : t);
+    kv_row_[t] = pos + t;
+    n_keys_[t] = parent ? pos : pos + t + 1;  // tree: prefix only, ancestors come as extra rows
+    if (all_logits || t == n - 1) out_.push_back(t);
+  }
+  check_ids(ids_.data(), n);
+  upload_layout(n);
+  run(n);
+  if (logits)
+    ck(mk_download(ctx_, logits, logits_.p, out_.size() * static_cast<size_t>(cfg_.n_vocab) * sizeof(float)));
+  ck(mk_synchronize(ctx_));
+}
+
+// model.cpp:432-440
+void Model::move_kv(int from, int to, int seq) {
+  if (from == to) return;
+  const auto& c = cfg_;
+  const mk_kv_cache kv{kc_.as<int8_t>(), vc_.as<int8_t>(), ks_.as<float>(), vs_.as<float>(), c.n_layer, n_seq_,
+                       c.n_head_kv, c.head_dim, n_ctx_};
+  ck(mk_move_kv(ctx_, &kv, seq, from, to));
+  ck(mk_synchronize(ctx_));
+}
+
+void Model::kv_row(int layer, int seq, int pos, bool k, uint8_t* out) {
+  const auto& c = cfg_;
+  const int KV = c.n_head_kv, D = c.head_dim;
+  for (int g = 0; g < KV; ++g) {
+    const size_t row = ((static_cast<size_t>(layer) * n_seq_ + seq) * KV + g) * n_ctx_ + pos;
+    ck(mk_download(ctx_, out + static_cast<size_t>(g) * D, (k ? kc_ : vc_).as<int8_t>() + row * D, D));
+    ck(mk_download(ctx_, out + static_cast<size_t>(KV) * D + 4 * g, (k ? ks_ : vs_).as<float>() + row, 4));
+  }
+}
+
+void Model::generate_greedy(const int32_t* prompt, int n_prompt, int n_gen, int seq, int32_t* out, GenStats* st,
+                            bool use_graph) {
+  if (n_prompt <= 0 || n_gen <= 0) throw std::invalid_argument("generate: empty prompt or no tokens");
+  if (n_prompt + n_gen > n_ctx_) throw std::runtime_error("forward: context full");
+  check_ids(prompt, n_prompt);
+  const int B = kMaxBatch;
+  int32_t* d_top1 = top_.as<int32_t>();
+  int32_t* d_tokens = top_.as<int32_t>() + B;  // generated ids (n_gen <= B per call segment below)
+  int32_t* d_counter = top_.as<int32_t>() + 2 * B;
+  std::vector<BatchToken> batch;
+  hipStream_t s = static_cast<hipStream_t>(mk_stream(ctx_));
+
+  // Prefill: the reference's engine evaluates prompts in kMaxBatch-token forwards (engine.cpp:381-393).
+  const auto t0 = Clock::now();
+  for (int pos = 0; pos < n_prompt; pos += B) {
+    const int m = std::min(B, n_prompt - pos);
+    batch.clear();
+    for (int i = 0; i < m; ++i) batch.push_back({prompt[pos + i], seq, pos + i, pos + i + 1 == n_prompt});
+    build_layout(batch.data(), m);
+    upload_layout(m);
+    run(m);
+  }
+  ck(mk_argmax_top2(ctx_, logits_.as<float>(), 1, cfg_.n_vocab, d_top1, nullptr));
+  int32_t first = 0;
+  ck(mk_download(ctx_, &first, d_top1, sizeof first));
+  if (st) st->prefill_ms = ms_since(t0);
+  out[0] = first;
+  if (n_gen == 1) return;
+
+  // Decode: one-token layout resident on the device; greedy_advance feeds each argmax back as the next input.
+  batch.assign(1, BatchToken{first, seq, n_prompt, true});
+  build_layout(batch.data(), 1);
+  max_keys_ = n_prompt + n_gen;  // attention LDS sized for the last step
+  upload_layout(1);
+  max_keys_ = n_prompt + n_gen;
+  const int32_t zero = 0;
+  const int steps = n_gen - 1;
+  std::vector<int32_t> toks(steps);
+  const auto t1 = Clock::now();
+  for (int done = 0; done < steps;) {
+    const int seg = std::min(B, steps - done);  // d_tokens holds B ids
+    ck(mk_upload(ctx_, d_counter, &zero, sizeof zero));
+    auto step = [&] {
+      run(1);
+      ck(mk_argmax_top2(ctx_, logits_.as<float>(), 1, cfg_.n_vocab, d_top1, nullptr));
+      ck(mk_greedy_advance(ctx_, d_top1, d_ids_, d_rpos_, d_kv_row_, d_n_keys_, d_tokens, d_counter));
+    };
+    if (use_graph) {
+      hipGraph_t g = nullptr;
+      hipGraphExec_t ge = nullptr;
+      hck(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+      try {
+        step();
+      } catch (...) {
+        (void)hipStreamEndCapture(s, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+      }
+      hck(hipStreamEndCapture(s, &g), "hipStreamEndCapture");
+      hck(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+      for (int i = 0; i < seg; ++i) hck(hipGraphLaunch(ge, s), "hipGraphLaunch");
+      hck(hipStreamSynchronize(s), "hipStreamSynchronize");
+      (void)hipGraphExecDestroy(ge);
+      (void)hipGraphDestroy(g);
+    } else {
+      for (int i = 0; i < seg; ++i) step();
+    }
+    ck(mk_download(ctx_, toks.data() + done, d_tokens, seg * sizeof(int32_t)));
+    done += seg;
+  }
+  if (st) {
+    st->decode_ms = ms_since(t1);
+    st->decode_forwards = steps;
+  }
+  std::copy(toks.begin(), toks.end(), out + 1);
+}
+
+}  // namespace malkin_hip

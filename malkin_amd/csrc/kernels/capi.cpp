@@ -1,0 +1,256 @@
+// extern "C" layer of include/malkin_hip.h over the internal launchers.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "ctx.h"
+#include "ops.h"
+
+namespace mk {
+
+namespace {
+thread_local char g_err[512] = "";
+}
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  set_error("%s: %s", what, hipGetErrorString(e));
+  return MK_ERR_HIP;
+}
+
+}  // namespace mk
+
+using mk::check;
+using mk::guard;
+using mk::require;
+
+extern "C" {
+
+const char* mk_last_error(void) { return mk::g_err; }
+
+int mk_init(int device, mk_ctx** out) {
+  return guard([&] {
+    require(out != nullptr, "mk_init: null output");
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0) throw mk::Error(MK_ERR_NO_DEVICE, "no HIP device");
+    require(device >= 0 && device < count, "mk_init: bad device index");
+    check(hipSetDevice(device), "hipSetDevice");
+    auto* c = new mk_ctx;
+    c->device = device;
+    hipDeviceProp_t p;
+    check(hipGetDeviceProperties(&p, device), "hipGetDeviceProperties");
+    std::snprintf(c->name, sizeof c->name, "%s", p.gcnArchName);
+    c->n_cu = p.multiProcessorCount;
+    check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
+    check(hipEventCreate(&c->ev0), "hipEventCreate");
+    check(hipEventCreate(&c->ev1), "hipEventCreate");
+    *out = c;
+  });
+}
+
+int mk_destroy(mk_ctx* c) {
+  return guard([&] {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    (void)hipEventDestroy(c->ev0);
+    (void)hipEventDestroy(c->ev1);
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+  });
+}
+
+const char* mk_device_name(const mk_ctx* c) { return c ? c->name : ""; }
+
+int mk_synchronize(mk_ctx* c) {
+  return guard([&] { check(hipStreamSynchronize(c->stream), "hipStreamSynchronize"); });
+}
+
+void* mk_stream(mk_ctx* c) { return c ? c->stream : nullptr; }
+
+int mk_malloc(mk_ctx* c, size_t bytes, void** dev) {
+  return guard([&] {
+    require(dev != nullptr, "mk_malloc: null output");
+    check(hipSetDevice(c->device), "hipSetDevice");
+    check(hipMalloc(dev, bytes ? bytes : 1), "hipMalloc");
+  });
+}
+
+int mk_free(mk_ctx* c, void* dev) {
+  return guard([&] {
+    if (!dev) return;
+    check(hipSetDevice(c->device), "hipSetDevice");
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    check(hipFree(dev), "hipFree");
+  });
+}
+
+int mk_upload(mk_ctx* c, void* dst, const void* src, size_t bytes) {
+  return guard([&] {
+    if (!bytes) return;
+    check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream), "hipMemcpy H2D");
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  });
+}
+
+int mk_download(mk_ctx* c, void* dst, const void* src, size_t bytes) {
+  return guard([&] {
+    if (!bytes) return;
+    check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream), "hipMemcpy D2H");
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  });
+}
+
+int mk_fill(mk_ctx* c, void* dev, int v, size_t bytes) {
+  return guard([&] { mk::fill(c->stream, dev, v, bytes); });
+}
+
+int mk_timer_start(mk_ctx* c) {
+  return guard([&] { check(hipEventRecord(c->ev0, c->stream), "hipEventRecord"); });
+}
+
+int mk_timer_stop(mk_ctx* c, float* ms) {
+  return guard([&] {
+    check(hipEventRecord(c->ev1, c->stream), "hipEventRecord");
+    check(hipEventSynchronize(c->ev1), "hipEventSynchronize");
+    check(hipEventElapsedTime(ms, c->ev0, c->ev1), "hipEventElapsedTime");
+  });
+}
+
+size_t mk_packed_bytes(int type, int64_t rows, int64_t cols) { return mk::packed_bytes(type, rows, cols); }
+
+int mk_pack_weight(mk_ctx* c, int type, const void* src, size_t srb, int64_t rows, int64_t cols, void* dst) {
+  return guard([&] { mk::pack_weight(c->stream, type, src, srb, rows, cols, dst); });
+}
+
+int mk_unpack_weight(mk_ctx* c, int type, const void* packed, int64_t rows, int64_t cols, void* dst) {
+  return guard([&] { mk::unpack_weight(c->stream, type, packed, rows, cols, dst); });
+}
+
+int mk_quantize_q8(mk_ctx* c, const float* x, int n, int64_t k, void* xq) {
+  return guard([&] { mk::quantize_q8(c->stream, x, n, k, static_cast<mk::BlockQ8*>(xq)); });
+}
+
+int mk_quantize_i8(mk_ctx* c, const float* x, int rows, int n, int8_t* q, float* d) {
+  return guard([&] { mk::quantize_i8_rows(c->stream, x, rows, n, q, d); });
+}
+
+int mk_dequantize_rows(mk_ctx* c, int type, const void* src, size_t row_bytes, const int32_t* ids, int n, int64_t k,
+                       float* dst) {
+  return guard([&] { mk::dequantize_rows(c->stream, type, src, row_bytes, ids, n, k, dst); });
+}
+
+int mk_matmul(mk_ctx* c, const mk_weight* w, const void* xq, int n, float* y, int64_t ys, int accumulate) {
+  return guard([&] {
+    require(w != nullptr, "mk_matmul: null weight");
+    mk::matmul(c->stream, w->type, w->wide != 0, w->data, w->rows, w->cols, static_cast<const mk::BlockQ8*>(xq), n, y,
+               ys, accumulate != 0);
+  });
+}
+
+int mk_rmsnorm(mk_ctx* c, const float* x, const float* w, int rows, int n, float eps, float* y) {
+  return guard([&] { mk::rmsnorm(c->stream, x, w, rows, n, eps, y); });
+}
+
+int mk_rmsnorm_q8(mk_ctx* c, const float* x, const int32_t* rows_idx, const float* w, int rows, int n, float eps,
+                  void* xq) {
+  return guard([&] { mk::rmsnorm_q8(c->stream, x, rows_idx, w, rows, n, eps, static_cast<mk::BlockQ8*>(xq)); });
+}
+
+int mk_silu_mul(mk_ctx* c, int64_t n, float* g, const float* u) {
+  return guard([&] { mk::silu_mul(c->stream, n, g, u); });
+}
+
+int mk_silu_mul_q8(mk_ctx* c, const float* gu, int rows, int64_t n, void* xq) {
+  return guard([&] { mk::silu_mul_q8(c->stream, gu, rows, n, static_cast<mk::BlockQ8*>(xq)); });
+}
+
+int mk_add(mk_ctx* c, int64_t n, float* x, const float* h) {
+  return guard([&] { mk::add(c->stream, n, x, h); });
+}
+
+int mk_attend_gqa(mk_ctx* c, const float* q, int G, int D, const int8_t* k, const int8_t* v, size_t stride,
+                  ptrdiff_t soff, int n, float scale, float* out, const int32_t* extra, int ne) {
+  return guard([&] {
+    require(G > 0 && n >= 0 && ne >= 0 && n + ne > 0, "attend_gqa: bad sizes");
+    // Per-call metadata for the batched kernel: one token of sequence 0 with n contiguous keys plus ne extra rows.
+    const int32_t meta[4] = {0, n, 0, ne};
+    int32_t* dm = nullptr;
+    check(hipMalloc(&dm, sizeof meta), "hipMalloc");
+    check(hipMemcpyAsync(dm, meta, sizeof meta, hipMemcpyHostToDevice, c->stream), "hipMemcpy H2D");
+    mk::AttnAddr a{k, v, reinterpret_cast<const char*>(k) + soff, reinterpret_cast<const char*>(v) + soff,
+                   0, 0, (int64_t)stride, 0, 0, (int64_t)stride};
+    try {
+      mk::attention(c->stream, q, (int64_t)G * D, out, (int64_t)G * D, 1, G, 1, D, scale, a, dm, dm + 1,
+                    ne > 0 ? dm + 2 : nullptr, extra, n + ne);
+      check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    } catch (...) {
+      (void)hipFree(dm);
+      throw;
+    }
+    check(hipFree(dm), "hipFree");
+  });
+}
+
+static mk::KvLayer kv_layer(const mk_kv_cache* kv, int layer) {
+  require(kv != nullptr && layer >= 0 && layer < kv->n_layer, "bad KV cache / layer");
+  const size_t rows = (size_t)layer * kv->n_seq * kv->n_head_kv * kv->n_ctx;
+  return mk::KvLayer{kv->k + rows * kv->head_dim, kv->v + rows * kv->head_dim, kv->k_scale + rows, kv->v_scale + rows};
+}
+
+int mk_qk_norm_rope_kv(mk_ctx* c, float* q, float* k, const float* v, int64_t stride, int n, int n_head,
+                       const float* q_norm, const float* k_norm, float eps, const float* cos_t, const float* sin_t,
+                       const int32_t* rpos, const int32_t* seq, const int32_t* kv_row, const mk_kv_cache* kv,
+                       int layer) {
+  return guard([&] {
+    const mk::KvLayer L = kv_layer(kv, layer);
+    mk::qk_norm_rope_kv(c->stream, q, k, v, stride, n, n_head, kv->n_head_kv, kv->head_dim, q_norm, k_norm, eps, cos_t,
+                        sin_t, rpos, seq, kv_row, L, kv->n_ctx);
+  });
+}
+
+int mk_attention(mk_ctx* c, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int n_head,
+                 const mk_kv_cache* kv, int layer, const int32_t* seq, const int32_t* n_keys, const int32_t* anc_off,
+                 const int32_t* anc, int max_keys) {
+  return guard([&] {
+    const mk::KvLayer L = kv_layer(kv, layer);
+    const int D = kv->head_dim;
+    const int64_t rows = (int64_t)kv->n_ctx;
+    mk::AttnAddr a{L.k, L.v, reinterpret_cast<const char*>(L.ks), reinterpret_cast<const char*>(L.vs),
+                   (int64_t)kv->n_head_kv * rows * D, rows * D, D,
+                   (int64_t)kv->n_head_kv * rows * 4, rows * 4, 4};
+    const float scale = 1.0f / std::sqrt(static_cast<float>(D));  // model.cpp:208
+    mk::attention(c->stream, q, q_stride, out, out_stride, n, n_head, kv->n_head_kv, D, scale, a, seq, n_keys, anc_off,
+                  anc, max_keys);
+  });
+}
+
+int mk_move_kv(mk_ctx* c, const mk_kv_cache* kv, int seq, int from, int to) {
+  return guard([&] {
+    require(kv && seq >= 0 && seq < kv->n_seq && from >= 0 && from < kv->n_ctx && to >= 0 && to < kv->n_ctx,
+            "move_kv: bad row");
+    mk::move_kv_rows(c->stream, kv->k, kv->v, kv->k_scale, kv->v_scale, kv->n_layer, kv->n_seq, kv->n_head_kv,
+                     kv->head_dim, kv->n_ctx, seq, from, to);
+  });
+}
+
+int mk_greedy_advance(mk_ctx* c, const int32_t* top1, int32_t* ids, int32_t* rpos, int32_t* kv_row, int32_t* n_keys,
+                      int32_t* out_tokens, int32_t* counter) {
+  return guard([&] { mk::greedy_advance(c->stream, top1, ids, rpos, kv_row, n_keys, out_tokens, counter); });
+}
+
+int mk_argmax_top2(mk_ctx* c, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2) {
+  return guard([&] { mk::argmax_top2(c->stream, logits, rows, n_vocab, top1, top2); });
+}
+
+}  // extern "C"

@@ -1,0 +1,58 @@
+// Library-internal context, error plumbing and launch helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <stdexcept>
+#include <string>
+
+#include "../../../include/malkin_hip.h"
+
+struct mk_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  int n_cu = 0;
+  char name[64] = {0};
+};
+
+namespace mk {
+
+void set_error(const char* fmt, ...);
+// Records the HIP error and returns MK_ERR_HIP.
+int hip_fail(hipError_t e, const char* what);
+
+// Errors raised inside library code; the extern "C" wrappers turn them into status codes.
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+inline void check(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw Error(MK_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// The launch's own error (bad configuration) and any asynchronous fault reported so far.
+inline void check_launch(const char* what) { check(hipGetLastError(), what); }
+
+template <typename F>
+int guard(F&& f) {
+  try {
+    f();
+    return MK_OK;
+  } catch (const Error& e) {
+    set_error("%s", e.what());
+    return e.code;
+  } catch (const std::exception& e) {
+    set_error("%s", e.what());
+    return MK_ERR_INVALID;
+  }
+}
+
+inline void require(bool ok, const char* msg) {
+  if (!ok) throw Error(MK_ERR_INVALID, msg);
+}
+
+}  // namespace mk

@@ -1,0 +1,86 @@
+// Library-internal launchers (throw mk::Error). The extern "C" layer and the host Model call these.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.h"
+#include "layout.h"
+
+namespace mk {
+
+// Per-token batch layout of one forward pass, resident in device memory (the reference's rpos_, kv_at_, kv_base_,
+// n_keys_, anc_, anc_off_, out_ of model.h:67-83). seq replaces kv_base (= seq * n_ctx).
+struct DevLayout {
+  int32_t* ids;      // [n] token ids
+  int32_t* rpos;     // [n] RoPE position
+  int32_t* seq;      // [n] sequence
+  int32_t* kv_row;   // [n] KV row written (within the sequence)
+  int32_t* n_keys;   // [n] contiguous keys from row 0
+  int32_t* anc_off;  // [n + 1] offsets into anc (tree mode), or null
+  int32_t* anc;      // ancestor rows (within the sequence)
+  int32_t* out;      // [n_out] tokens whose logits are produced
+};
+
+// Device KV cache of one layer: int8 rows [seq][kv_head][n_ctx][D] and float scales [seq][kv_head][n_ctx].
+struct KvLayer {
+  int8_t* k;
+  int8_t* v;
+  float* ks;
+  float* vs;
+};
+
+size_t packed_bytes(int type, int64_t rows, int64_t cols);
+void pack_weight(hipStream_t s, int type, const void* src, size_t src_row_bytes, int64_t rows, int64_t cols, void* dst);
+void unpack_weight(hipStream_t s, int type, const void* packed, int64_t rows, int64_t cols, void* dst);
+
+void quantize_q8(hipStream_t s, const float* x, int n, int64_t k, BlockQ8* xq);
+void quantize_i8_rows(hipStream_t s, const float* x, int rows, int n, int8_t* q, float* d);
+void dequantize_rows(hipStream_t s, int type, const void* src, size_t row_bytes, const int32_t* ids, int n, int64_t k,
+                     float* dst);
+void rmsnorm(hipStream_t s, const float* x, const float* w, int rows, int n, float eps, float* y);
+void rmsnorm_q8(hipStream_t s, const float* x, const int32_t* rows_idx, const float* w, int rows, int n, float eps,
+                BlockQ8* xq);
+void silu_mul(hipStream_t s, int64_t n, float* g, const float* u);
+void silu_mul_q8(hipStream_t s, const float* gu, int rows, int64_t n, BlockQ8* xq);
+void add(hipStream_t s, int64_t n, float* x, const float* h);
+void fill(hipStream_t s, void* p, int value, size_t bytes);
+
+// y[t * ys + r] (+)= W[r] . xq[t]; wide: Q6_K wide-panel arithmetic for n > 16.
+void matmul(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int64_t cols, const BlockQ8* xq, int n,
+            float* y, int64_t ys, bool accumulate);
+
+// Generic attention addressing: key row (t, g, row) at k + seq*k_seq + g*k_head + row*k_row (bytes), its scale at
+// ks + seq*s_seq + g*s_head + row*s_row (bytes); values likewise with v / vs.
+struct AttnAddr {
+  const int8_t* k;
+  const int8_t* v;
+  const char* ks;
+  const char* vs;
+  int64_t k_seq, k_head, k_row;
+  int64_t s_seq, s_head, s_row;
+};
+// q [n][H*D] (token stride q_stride floats), out [n][H*D] (stride out_stride). Per token t: keys rows
+// 0..n_keys[t]-1 of sequence seq[t], then anc[anc_off[t] .. anc_off[t+1]) when anc_off is non-null.
+void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int H, int KV,
+               int D, float scale,
+               const AttnAddr& a, const int32_t* seq, const int32_t* n_keys, const int32_t* anc_off,
+               const int32_t* anc, int max_keys);
+
+// QK-norm + RoPE on q [n][H*D] and k [n][KV*D] (in place), then k, v quantized into the KV cache (model.cpp:370-392).
+// cos/sin tables [n_pos][D/2].
+void qk_norm_rope_kv(hipStream_t s, float* q, float* k, const float* v, int64_t stride, int n, int H, int KV, int D,
+                     const float* q_norm, const float* k_norm, float eps, const float* cos_t, const float* sin_t,
+                     const int32_t* rpos, const int32_t* seq, const int32_t* kv_row, const KvLayer& kv, int n_ctx);
+
+void argmax_top2(hipStream_t s, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2);
+
+void greedy_advance(hipStream_t s, const int32_t* top1, int32_t* ids, int32_t* rpos, int32_t* kv_row, int32_t* n_keys,
+                    int32_t* out_tokens, int32_t* counter);
+
+// Copies KV rows (all layers' K and V of one sequence): row from -> row to (model.cpp:432-440). The cache is one
+// allocation per K / V / K-scale / V-scale: [layer][seq][kv_head][n_ctx] rows.
+void move_kv_rows(hipStream_t s, int8_t* k8, int8_t* v8, float* ks, float* vs, int n_layer, int n_seq, int KV, int D,
+                  int n_ctx, int seq, int from, int to);
+
+}  // namespace mk

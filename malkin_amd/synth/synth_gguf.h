@@ -1,0 +1,33 @@
+/* Deterministic random-init qwen3 GGUF writer (synthetic models for tests and benchmarks). */
+#ifndef MALKIN_SYNTH_GGUF_H
+#define MALKIN_SYNTH_GGUF_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { MKS_MIX_UNIFORM = 0, MKS_MIX_Q4_K_M = 1 };
+
+typedef struct {
+  int n_layer, n_embd, n_ff, n_head, n_head_kv, head_dim, n_vocab, n_ctx_train;
+  float rope_base, rms_eps;
+  int tied;     /* 1: no output.weight (LM head = token_embd, model.cpp:116-118) */
+  int type;     /* ggml type of every matmul weight and token_embd under MKS_MIX_UNIFORM: 8 Q8_0, 12 Q4_K, 14 Q6_K */
+  int mix;      /* MKS_MIX_* */
+  float std;    /* weight standard deviation (0.02) */
+  uint64_t seed;
+  char name[32];
+} mks_config;
+
+/* Size of the file mks_write_gguf writes for c. */
+int64_t mks_file_bytes(const mks_config* c);
+/* 0 on success; -1 I/O error; -2 unsupported shape or type. */
+int mks_write_gguf(const char* path, const mks_config* c, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

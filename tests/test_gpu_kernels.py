@@ -1,0 +1,225 @@
+"""Kernel-level parity: every gfx950 kernel, called through the C ABI, against the CPU oracle and the golden vectors
+written by the reference's own compiled code. Integer and byte work must be bit-exact, and so is every fp32 output:
+the kernels reproduce the reference's rounding steps one for one."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import malkin_amd as mk_
+from malkin_amd import MkWeight
+from oracle import bind
+
+pytestmark = pytest.mark.gpu
+
+L = mk_.load
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def row_bytes(t, k):
+    return bind.row_size(t, k)
+
+
+def test_device_is_gfx950(mk):
+    print("device", mk.device_name)
+    assert mk.device_name.startswith("gfx950")
+
+
+@pytest.mark.parametrize("t,rows,k", [(mk_.Q8_0, 24, 512), (mk_.Q8_0, 8, 96), (mk_.Q4_K, 16, 512),
+                                      (mk_.Q6_K, 24, 768)])
+def test_pack_roundtrip(mk, t, rows, k):
+    import make_golden
+    rng = np.random.default_rng(rows * k + t)
+    w = make_golden.random_rows(rng, t, rows, k)
+    src = mk.to_device(w)
+    pb = L().mk_packed_bytes(t, rows, k)
+    assert pb == w.nbytes
+    packed = mk.alloc(pb)
+    mk_.check(L().mk_pack_weight(mk.h, t, src.ptr, row_bytes(t, k), rows, k, packed.ptr))
+    back = mk.alloc(w.nbytes)
+    mk_.check(L().mk_unpack_weight(mk.h, t, packed.ptr, rows, k, back.ptr))
+    assert np.array_equal(back.download(np.uint8), w.reshape(-1))
+    assert not np.array_equal(packed.download(np.uint8), w.reshape(-1))  # the layout really changes
+
+
+def test_quantize_q8(mk, golden, oracle):
+    g = golden("quant.npz")
+    x = g["x"]
+    dx = mk.to_device(x)
+    out = mk.alloc(x.size // 32 * 40)
+    mk_.check(L().mk_quantize_q8(mk.h, dx.ptr, x.shape[0], x.shape[1], out.ptr))
+    assert np.array_equal(out.download(np.uint8), g["q8"].reshape(-1))
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal((64, 4096)) * 3).astype(np.float32)
+    dx = mk.to_device(x)
+    out = mk.alloc(x.size // 32 * 40)
+    mk_.check(L().mk_quantize_q8(mk.h, dx.ptr, 64, 4096, out.ptr))
+    assert np.array_equal(out.download(np.uint8), oracle.quantize_row_q8(x).view(np.uint8).reshape(-1))
+
+
+def test_quantize_i8(mk, golden):
+    g = golden("quant.npz")
+    xi = g["xi"]
+    dx = mk.to_device(xi)
+    q = mk.alloc(xi.size)
+    d = mk.alloc(4 * xi.shape[0])
+    mk_.check(L().mk_quantize_i8(mk.h, dx.ptr, xi.shape[0], xi.shape[1], q.ptr, d.ptr))
+    assert np.array_equal(q.download(np.int8).reshape(xi.shape), g["qi"])
+    assert np.array_equal(bits(d.download(np.float32)), bits(g["di"]))
+
+
+def test_silu(mk, golden, oracle):
+    g = golden("quant.npz")
+    dg, du = mk.to_device(g["g"]), mk.to_device(g["u"])
+    mk_.check(L().mk_silu_mul(mk.h, g["g"].size, dg.ptr, du.ptr))
+    assert np.array_equal(bits(dg.download(np.float32)), bits(g["silu"]))
+    # fused silu_mul + quantize of [gate | up] rows
+    rng = np.random.default_rng(2)
+    rows, F = 5, 512
+    gu = rng.uniform(-20, 20, (rows, 2 * F)).astype(np.float32)
+    dgu = mk.to_device(gu)
+    out = mk.alloc(rows * F // 32 * 40)
+    mk_.check(L().mk_silu_mul_q8(mk.h, dgu.ptr, rows, F, out.ptr))
+    exp = np.stack([oracle.silu_mul(r[:F], r[F:]) for r in gu])
+    assert np.array_equal(out.download(np.uint8), oracle.quantize_row_q8(exp).view(np.uint8).reshape(-1))
+
+
+def test_rmsnorm(mk, oracle):
+    rng = np.random.default_rng(3)
+    rows, n = 7, 4096
+    x = (rng.standard_normal((rows, n)) * 5).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    dx, dw = mk.to_device(x), mk.to_device(w)
+    y = mk.alloc(x.nbytes)
+    mk_.check(L().mk_rmsnorm(mk.h, dx.ptr, dw.ptr, rows, n, ctypes.c_float(1e-6), y.ptr))
+    exp = np.stack([oracle.rmsnorm(r, w, 1e-6) for r in x])
+    assert np.array_equal(bits(y.download(np.float32).reshape(rows, n)), bits(exp))
+    idx = np.array([6, 0, 3], np.int32)
+    didx = mk.to_device(idx)
+    out = mk.alloc(3 * n // 32 * 40)
+    mk_.check(L().mk_rmsnorm_q8(mk.h, dx.ptr, didx.ptr, dw.ptr, 3, n, ctypes.c_float(1e-6), out.ptr))
+    assert np.array_equal(out.download(np.uint8), oracle.quantize_row_q8(exp[idx]).view(np.uint8).reshape(-1))
+
+
+def _packed(mk, t, w, rows, k):
+    src = mk.to_device(w)
+    packed = mk.alloc(L().mk_packed_bytes(t, rows, k))
+    mk_.check(L().mk_pack_weight(mk.h, t, src.ptr, row_bytes(t, k), rows, k, packed.ptr))
+    return packed
+
+
+def _matmul(mk, t, packed, rows, k, xq, n, wide, y=None, accumulate=False):
+    dxq = mk.to_device(xq)
+    if y is None:
+        y = mk.alloc(n * rows * 4)
+    wt = MkWeight(t, 1 if wide else 0, rows, k, packed.p)
+    mk_.check(L().mk_matmul(mk.h, ctypes.byref(wt), dxq.ptr, n, y.ptr, rows, 1 if accumulate else 0))
+    return y
+
+
+def test_matmul_golden(mk, golden):
+    g = golden("gemm.npz")
+    cases = sorted({key.split("_")[0] for key in g.files})
+    done = 0
+    for c in cases:
+        t = int(g[f"{c}_type"])
+        if t not in (mk_.Q8_0, mk_.Q4_K, mk_.Q6_K):
+            continue
+        w = g[f"{c}_w"]
+        rows = w.shape[0]
+        k = (w.shape[1] // 34) * 32 if t == mk_.Q8_0 else (w.shape[1] // {12: 144, 14: 210}[t]) * 256
+        packed = _packed(mk, t, w, rows, k)
+        for key in g.files:
+            if key.startswith(c + "_n") and key.endswith("_xq"):
+                n = int(key[len(c) + 2:-3])
+                xq = g[key]
+                for wide, suffix in ((True, "_y"), (False, "_y_compact")):
+                    y = _matmul(mk, t, packed, rows, k, xq, n, wide).download(np.float32).reshape(n, rows)
+                    assert np.array_equal(bits(y), bits(g[f"{c}_n{n}{suffix}"])), (c, n, wide)
+                    done += 1
+    assert done >= 20
+
+
+LARGE = [(t, n, 256, 4096) for t in (mk_.Q8_0, mk_.Q4_K, mk_.Q6_K) for n in (1, 3, 8, 17)] + [
+    (mk_.Q8_0, 1, 65536, 1024),   # 2048 row groups of 32: the wide-workgroup shape
+    (mk_.Q8_0, 8, 256, 12288),    # down-projection depth: several LDS chunks per row
+    (mk_.Q6_K, 8, 256, 17408),
+    (mk_.Q4_K, 2, 512, 17408),
+]
+
+
+@pytest.mark.parametrize("t,n,rows,k", LARGE)
+def test_matmul_large_vs_oracle(mk, oracle, t, n, rows, k):
+    """Real widths, several LDS chunks, both workgroup shapes, and the residual-accumulate epilogue."""
+    import make_golden
+    rng = np.random.default_rng(100 * t + n + rows + k)
+    w = make_golden.random_rows(rng, t, rows, k)
+    x = rng.uniform(-2, 2, (n, k)).astype(np.float32)
+    xq = oracle.quantize_row_q8(x)
+    packed = _packed(mk, t, w, rows, k)
+    exp = oracle.matmul(t, w, rows, k, xq.reshape(-1), wide=True)
+    y = _matmul(mk, t, packed, rows, k, xq.view(np.uint8), n, True).download(np.float32).reshape(n, rows)
+    assert np.array_equal(bits(y), bits(exp))
+    base = rng.standard_normal((n, rows)).astype(np.float32)
+    yd = mk.to_device(base)
+    _matmul(mk, t, packed, rows, k, xq.view(np.uint8), n, True, y=yd, accumulate=True)
+    assert np.array_equal(bits(yd.download(np.float32).reshape(n, rows)), bits(base + exp))
+
+
+def test_attend_gqa_golden(mk, golden):
+    g = golden("attention.npz")
+    for i in range(int(g["count"])):
+        G, D, n, ne, stride = (int(v) for v in g[f"a{i}_meta"])
+        dq, dk, dv = mk.to_device(g[f"a{i}_q"]), mk.to_device(g[f"a{i}_k"]), mk.to_device(g[f"a{i}_v"])
+        dex = mk.to_device(g[f"a{i}_extra"]) if ne else None
+        out = mk.alloc(G * D * 4)
+        scale = np.float32(1.0) / np.sqrt(np.float32(D))
+        mk_.check(L().mk_attend_gqa(mk.h, dq.ptr, G, D, dk.ptr, dv.ptr, stride, D + 4, n, ctypes.c_float(scale),
+                                    out.ptr, dex.ptr if dex else None, ne))
+        assert np.array_equal(bits(out.download(np.float32)), bits(g[f"a{i}_out"])), (G, D, n)
+
+
+def test_argmax_top2(mk, oracle):
+    rng = np.random.default_rng(4)
+    rows, V = 6, 151936
+    l = rng.standard_normal((rows, V)).astype(np.float32)
+    l[1, [5, 70000, 151935]] = 99.0      # ties: first index wins
+    l[2, :] = 1.0                       # all equal
+    l[3, 151935] = 50.0                 # max at the end
+    l[4, [0, 1]] = 40.0
+    dl = mk.to_device(l)
+    t1, t2 = mk.alloc(rows * 4), mk.alloc(rows * 4)
+    mk_.check(L().mk_argmax_top2(mk.h, dl.ptr, rows, V, t1.ptr, t2.ptr))
+    a, b = t1.download(np.int32), t2.download(np.int32)
+    for r in range(rows):
+        assert (a[r], b[r]) == oracle.top2(l[r]), r
+        assert a[r] == oracle.argmax(l[r])
+
+
+@pytest.mark.parametrize("t", [mk_.Q8_0, mk_.Q4_K, mk_.Q6_K, mk_.F32])
+def test_dequantize_rows(mk, oracle, t):
+    import make_golden
+    rng = np.random.default_rng(t)
+    k = 512
+    if t == mk_.F32:
+        w = rng.standard_normal((10, k)).astype(np.float32).view(np.uint8).reshape(10, -1)
+    else:
+        w = make_golden.random_rows(rng, t, 10, k)
+    ids = np.array([3, 0, 9, 3], np.int32)
+    dw, di = mk.to_device(w), mk.to_device(ids)
+    out = mk.alloc(len(ids) * k * 4)
+    mk_.check(L().mk_dequantize_rows(mk.h, t, dw.ptr, w.shape[1], di.ptr, len(ids), k, out.ptr))
+    exp = np.stack([oracle.dequantize_row(t, w[i], k) for i in ids])
+    assert np.array_equal(bits(out.download(np.float32).reshape(len(ids), k)), bits(exp))
+
+
+def test_errors_are_statuses(mk):
+    wt = MkWeight(1, 0, 8, 64, None)  # F16: no device kernel
+    rc = L().mk_matmul(mk.h, ctypes.byref(wt), None, 1, None, 8, 0)
+    assert rc == mk_.MK_ERR_INVALID
+    assert b"no kernel" in L().mk_last_error()
+    rc = L().mk_silu_mul(mk.h, 17, None, None)
+    assert rc == mk_.MK_ERR_UNSUPPORTED
