@@ -138,6 +138,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--preset", default="qwen3-8b")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="decode with direct launches instead of the replayed HIP graph (for tracers that do not "
+                         "follow graph launches); same kernels")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -156,13 +159,13 @@ def main():
         cfg = model.cfg
         prompt = prompt_ids(N_PROMPT, cfg["n_vocab"])
         for i in range(args.warmup):
-            toks, st = model.generate(prompt, N_GEN)
+            toks, st = model.generate(prompt, N_GEN, use_graph=not args.no_graph)
             log(f"[bench] warmup {i}: prefill {st['prefill_ms']:.1f} ms, decode {st['decode_ms']:.1f} ms")
         ctx.sync()
         pre, dec = [], []
         t_start = time.perf_counter()
         for i in range(args.steps):
-            toks, st = model.generate(prompt, N_GEN)
+            toks, st = model.generate(prompt, N_GEN, use_graph=not args.no_graph)
             pre.append(st["prefill_ms"])
             dec.append(st["decode_ms"])
             log(f"[bench] step {i}: prefill {st['prefill_ms']:.1f} ms, decode {st['decode_ms']:.1f} ms")
