@@ -11,6 +11,9 @@ namespace mk {
 namespace {
 
 // One wavefront per (token, head): heads [0, H) are query heads, [H, H+KV) key heads, [H+KV, H+2KV) value heads.
+// Every global operand (the head's values, its norm weights, the RoPE row) is loaded up front.
+constexpr int kQkMaxPer = 4;  // D <= 256: up to 4 values per lane
+
 __global__ __launch_bounds__(64) void k_qk_norm_rope_kv(float* __restrict__ q, float* __restrict__ k,
                                                         const float* __restrict__ v, int64_t stride, int H, int KV,
                                                         int D, const float* __restrict__ q_norm,
@@ -27,29 +30,49 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope_kv(float* __restrict__ q, f
   const int head = is_q ? hh : (is_k ? hh - H : hh - H - KV);
   float* vec = is_q ? q + t * stride + (int64_t)head * D : (is_k ? k + t * stride + (int64_t)head * D : nullptr);
   const float* src = is_v ? v + t * stride + (int64_t)head * D : vec;
-  for (int i = lane; i < D; i += 64) sh[i] = src[i];
+  const float* w = is_q ? q_norm : k_norm;
+  const int64_t pos = rpos[t];
+  float xv[kQkMaxPer], wv[kQkMaxPer], cv[kQkMaxPer], sv[kQkMaxPer];
+#pragma unroll
+  for (int c = 0; c < kQkMaxPer; ++c) {
+    const int i = lane + 64 * c;
+    if (i < D) {
+      xv[c] = src[i];
+      if (!is_v) wv[c] = w[i];
+    }
+    if (!is_v && i < D / 2) {
+      cv[c] = cos_t[pos * (D / 2) + i];
+      sv[c] = sin_t[pos * (D / 2) + i];
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < kQkMaxPer; ++c)
+    if (lane + 64 * c < D) sh[lane + 64 * c] = xv[c];
   __syncthreads();
   if (!is_v) {
     // rmsnorm (model.cpp:46-49) over D: 16 fma chains + halving tree.
     if (lane < 16) {
       float acc = 0.0f;
+#pragma unroll 4
       for (int i = lane; i < D; i += 16) acc = fma_(sh[i], sh[i], acc);
       acc = reduce16_lanes(acc);
       if (lane == 0) scale_s = 1.0f / sqrtf(acc / (float)D + eps);
     }
     __syncthreads();
     const float s = scale_s;
-    const float* w = is_q ? q_norm : k_norm;
-    for (int i = lane; i < D; i += 64) sh[i] = sh[i] * s * w[i];
+#pragma unroll
+    for (int c = 0; c < kQkMaxPer; ++c)
+      if (lane + 64 * c < D) sh[lane + 64 * c] = xv[c] * s * wv[c];
     __syncthreads();
     // RoPE on pairs (i, i + D/2): clang contracts x0*c - x1*s to fma(x0, c, -(x1*s)), x0*s + x1*c to fma(x0, s, x1*c).
-    const float* cs = cos_t + (int64_t)rpos[t] * (D / 2);
-    const float* sn = sin_t + (int64_t)rpos[t] * (D / 2);
-    for (int i = lane; i < D / 2; i += 64) {
-      const float x0 = sh[i], x1 = sh[i + D / 2];
-      const float c = cs[i], si = sn[i];
-      sh[i] = fma_(x0, c, -(x1 * si));
-      sh[i + D / 2] = fma_(x0, si, x1 * c);
+#pragma unroll
+    for (int c = 0; c < kQkMaxPer; ++c) {
+      const int i = lane + 64 * c;
+      if (i < D / 2) {
+        const float x0 = sh[i], x1 = sh[i + D / 2];
+        sh[i] = fma_(x0, cv[c], -(x1 * sv[c]));
+        sh[i + D / 2] = fma_(x0, sv[c], x1 * cv[c]);
+      }
     }
     __syncthreads();
     if (is_q) {
@@ -60,41 +83,193 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope_kv(float* __restrict__ q, f
   // quantize_i8 (quant.cpp:134-140) into the cache row.
   float amax = 0.0f;
   for (int i = lane; i < D; i += 64) amax = fmaxf(amax, fabsf(sh[i]));
-  amax_s[lane] = amax;
-  __syncthreads();
-  if (lane == 0) {
-    float m = 0.0f;
-    for (int i = 0; i < 64; ++i) m = fmaxf(m, amax_s[i]);
-    amax_s[0] = m;
-  }
-  __syncthreads();
-  const float d = amax_s[0] / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  const float d = amax / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
   const int64_t row = ((int64_t)seq[t] * KV + head) * n_ctx + kv_row[t];
   int8_t* dst = (is_v ? kv.v : kv.k) + row * D;
   for (int i = lane; i < D; i += 64) dst[i] = (int8_t)(int)__builtin_rintf(sh[i] * id);
   if (lane == 0) (is_v ? kv.vs : kv.ks)[row] = d;
 }
 
-// Attention of one query head per workgroup. kRef: attend_t semantics (D in {64,128,256}, G <= 16); else the
-// per-head path of attend_gqa (kernels_avx512.cpp:296-305).
-template <bool kRef>
-__global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, int64_t q_stride,
-                                                   float* __restrict__ out, int64_t out_stride, int H, int G, int D,
-                                                   float scale,
-                                                   AttnAddr a, const int32_t* __restrict__ seqs,
-                                                   const int32_t* __restrict__ n_keys,
-                                                   const int32_t* __restrict__ anc_off,
-                                                   const int32_t* __restrict__ anc) {
+// Attention of one query head per workgroup, attend_t semantics (D in {64,128,256}, G <= 16):
+//   scores  one key per thread: the 16 lane chains of attend_t (mul, then fma over D/16 chunks) from 16-byte K
+//           loads, the halving tree, times (kv_scale * scale);
+//   softmax exact max, e = exp512(s - max), 16 sequential lane sums + tree;
+//   P.V     one sequential fma chain per output element over all keys in order. V is staged a tile of keys at a
+//           time into LDS as int8, transposed to [d][key]; the staging threads (all but the first D) load chunk c+1
+//           into registers while lanes 0..D-1 run the chains of chunk c from 16-byte LDS reads.
+constexpr int kAttnThreads = 1024;
+
+template <int D>
+struct AttnTile {
+  static constexpr int chunk = D >= 256 ? 128 : 256;  // keys per V tile
+  static constexpr int stride = chunk + 16;            // bytes per tile row [d]: 16-byte aligned, spreads banks
+  static constexpr int tile = D * stride;              // bytes per tile
+  static constexpr int tasks = (chunk / 4) * (D / 16); // staging task: 4 keys x 16 values
+};
+
+__host__ __device__ constexpr size_t attn_lds_bytes(int tile_bytes, int D, int nk_pad) {
+  return 2 * (size_t)tile_bytes + 4 * ((size_t)D + 2 * (size_t)nk_pad);
+}
+
+template <int D>
+__global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restrict__ q, int64_t q_stride,
+                                                            float* __restrict__ out, int64_t out_stride, int G,
+                                                            float scale, AttnAddr a, const int32_t* __restrict__ seqs,
+                                                            const int32_t* __restrict__ n_keys,
+                                                            const int32_t* __restrict__ anc_off,
+                                                            const int32_t* __restrict__ anc) {
+  constexpr int DC = D / 16;
+  using T = AttnTile<D>;
+  const int t = blockIdx.x, h = blockIdx.y, g = h / G, tid = threadIdx.x;
+  const int n0 = n_keys[t];
+  const int e0 = anc_off ? anc_off[t] : 0, ne = anc_off ? anc_off[t + 1] - e0 : 0;
+  const int nk = n0 + ne;
+  const int nk_pad = (nk + 3) & ~3;
+  extern __shared__ int4 smem4[];
+  int8_t* tiles = reinterpret_cast<int8_t*>(smem4);                // 2 x [D][stride] int8
+  float* qs = reinterpret_cast<float*>(tiles + 2 * T::tile);     // D
+  float* sc = qs + D;                                            // nk_pad: scores, then e^(s - max)
+  float* pv = sc + nk_pad;                                       // nk_pad: e * v-scale
+  __shared__ float red[kAttnThreads / 64];
+  __shared__ float inv_s;
+  const int64_t sq = seqs[t];
+  const int8_t* kb = a.k + sq * a.k_seq + g * a.k_head;
+  const int8_t* vb = a.v + sq * a.k_seq + g * a.k_head;
+  const char* ksb = a.ks + sq * a.s_seq + g * a.s_head;
+  const char* vsb = a.vs + sq * a.s_seq + g * a.s_head;
+  auto key_row = [&](int j) -> int64_t { return j < n0 ? j : anc[e0 + j - n0]; };
+
+  // V staging: task = 4 consecutive keys x 16 consecutive values, written as 16 dwords of the transposed tile.
+  const bool stager = tid >= D;
+  const int task = tid - D;
+  uint4 vreg[4];
+  auto load_chunk = [&](int c) {
+    if (!stager || task >= T::tasks) return;
+    const int kq = task % (T::chunk / 4), db = task / (T::chunk / 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = c * T::chunk + 4 * kq + i;
+      vreg[i] = j < nk ? *reinterpret_cast<const uint4*>(vb + key_row(j) * a.k_row + 16 * db) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store_chunk = [&](int c) {
+    if (!stager || task >= T::tasks) return;
+    const int kq = task % (T::chunk / 4), db = task / (T::chunk / 4);
+    int8_t* tile = tiles + (c & 1) * T::tile;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t word = (&vreg[i].x)[v >> 2];
+        w |= ((word >> (8 * (v & 3))) & 0xFFu) << (8 * i);
+      }
+      *reinterpret_cast<uint32_t*>(tile + (16 * db + v) * T::stride + 4 * kq) = w;
+    }
+  };
+  const int chunks = (nk + T::chunk - 1) / T::chunk;
+  load_chunk(0);  // V's first tile is in flight during the scores
+
+  const float* qh = q + t * q_stride + (int64_t)h * D;
+  for (int i = tid; i < D; i += kAttnThreads) qs[i] = qh[i];
+  __syncthreads();
+
+  // Scores (kernels_avx512.cpp:234-244); the value scale of the same key is fetched alongside.
+  for (int j = tid; j < nk; j += kAttnThreads) {
+    const int64_t row = key_row(j);
+    const int4* kr = reinterpret_cast<const int4*>(kb + row * a.k_row);
+    int4 kv[DC];
+#pragma unroll
+    for (int c = 0; c < DC; ++c) kv[c] = kr[c];
+    const float kscale = *reinterpret_cast<const float*>(ksb + row * a.s_row);
+    pv[j] = *reinterpret_cast<const float*>(vsb + row * a.s_row);
+    float lanes[16];
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      const int w[4] = {kv[c].x, kv[c].y, kv[c].z, kv[c].w};
+#pragma unroll
+      for (int l = 0; l < 16; ++l) {
+        const float kf = (float)(int8_t)(w[l >> 2] >> (8 * (l & 3)));
+        lanes[l] = c == 0 ? qs[l] * kf : fma_(qs[16 * c + l], kf, lanes[l]);
+      }
+    }
+    sc[j] = reduce16(lanes) * (kscale * scale);
+  }
+  store_chunk(0);
+  __syncthreads();
+
+  // softmax_inplace (kernels_avx512.cpp:205-226).
+  float m = -INFINITY;
+  for (int j = tid; j < nk; j += kAttnThreads) m = fmaxf(m, sc[j]);
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if ((tid & 63) == 0) red[tid >> 6] = m;
+  __syncthreads();
+  float mx = red[0];
+  for (int i = 1; i < kAttnThreads / 64; ++i) mx = fmaxf(mx, red[i]);
+  for (int j = tid; j < nk; j += kAttnThreads) {
+    const float e = exp512(sc[j] - mx);
+    sc[j] = e;
+    pv[j] = e * pv[j];
+  }
+  for (int j = nk + tid; j < nk_pad; j += kAttnThreads) pv[j] = 0.0f;
+  if (chunks > 1) load_chunk(1);
+  __syncthreads();
+  if (tid < 16) {
+    float s = 0.0f;
+#pragma unroll 8
+    for (int j = tid; j < nk; j += 16) s = s + sc[j];
+    s = reduce16_lanes(s);
+    if (tid == 0) inv_s = 1.0f / s;
+  }
+
+  // P.V (kernels_avx512.cpp:247-265): chunk c from tile c & 1 while chunk c + 1 is stored and c + 2 is loaded.
+  float acc = 0.0f;
+  for (int c = 0; c < chunks; ++c) {
+    if (tid < D) {
+      const int j0 = c * T::chunk;
+      const int len = min(T::chunk, nk - j0);
+      const int8_t* vr = tiles + (c & 1) * T::tile + tid * T::stride;
+      for (int jj = 0; jj < len; jj += 16) {
+        const int4 v16 = *reinterpret_cast<const int4*>(vr + jj);
+        const int w[4] = {v16.x, v16.y, v16.z, v16.w};
+        const int lim = min(16, len - jj);
+        if (lim == 16) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc = fma_(pv[j0 + jj + i], (float)(int8_t)(w[i >> 2] >> (8 * (i & 3))), acc);
+        } else {
+          for (int i = 0; i < lim; ++i) acc = fma_(pv[j0 + jj + i], (float)(int8_t)(w[i >> 2] >> (8 * (i & 3))), acc);
+        }
+      }
+    } else if (c + 1 < chunks) {
+      store_chunk(c + 1);
+      if (c + 2 < chunks) load_chunk(c + 2);
+    }
+    __syncthreads();
+  }
+  if (tid < D) out[t * out_stride + (int64_t)h * D + tid] = acc * inv_s;
+}
+
+// Other head sizes or G > 16: the per-head path of attend_gqa (kernels_avx512.cpp:296-305), one query head per
+// workgroup, byte loads.
+__global__ __launch_bounds__(256) void k_attention_generic(const float* __restrict__ q, int64_t q_stride,
+                                                           float* __restrict__ out, int64_t out_stride, int G, int D,
+                                                           float scale, AttnAddr a,
+                                                           const int32_t* __restrict__ seqs,
+                                                           const int32_t* __restrict__ n_keys,
+                                                           const int32_t* __restrict__ anc_off,
+                                                           const int32_t* __restrict__ anc) {
   const int t = blockIdx.x, h = blockIdx.y, g = h / G, tid = threadIdx.x;
   extern __shared__ float sm[];
-  float* qs = sm;       // D
-  float* sc = qs + D;   // keys: scores, then e^(s - max)
+  float* qs = sm;
+  float* sc = qs + D;
   __shared__ float red[256];
   __shared__ float inv_s;
   const int n0 = n_keys[t];
   const int e0 = anc_off ? anc_off[t] : 0, ne = anc_off ? anc_off[t + 1] - e0 : 0;
   const int nk = n0 + ne;
-  float* pv = sc + nk;  // per key: p * v-scale (kRef) or p * inv * v-scale
+  float* pv = sc + nk;
   const int64_t sq = seqs[t];
   const int8_t* kb = a.k + sq * a.k_seq + g * a.k_head;
   const int8_t* vb = a.v + sq * a.k_seq + g * a.k_head;
@@ -103,22 +278,17 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
   const float* qh = q + t * q_stride + (int64_t)h * D;
   for (int i = tid; i < D; i += 256) qs[i] = qh[i];
   __syncthreads();
-
-  // Scores.
   for (int j = tid; j < nk; j += 256) {
     const int64_t row = j < n0 ? j : anc[e0 + j - n0];
     const int8_t* kr = kb + row * a.k_row;
     const float kscale = *reinterpret_cast<const float*>(ksb + row * a.s_row);
     float lanes[16];
-    for (int l = 0; l < 16; ++l) lanes[l] = kRef ? qs[l] * (float)kr[l] : fma_(qs[l], (float)kr[l], 0.0f);
+    for (int l = 0; l < 16; ++l) lanes[l] = qs[l] * (float)kr[l];
     for (int c = 16; c < D; c += 16)
       for (int l = 0; l < 16; ++l) lanes[l] = fma_(qs[c + l], (float)kr[c + l], lanes[l]);
-    const float dot = reduce16(lanes);
-    sc[j] = kRef ? dot * (kscale * scale) : dot * kscale * scale;
+    sc[j] = reduce16(lanes) * kscale * scale;  // (dot * kv_scale) * scale
   }
   __syncthreads();
-
-  // softmax_inplace (kernels_avx512.cpp:205-226): exact max, e = exp512(s - max), 16 sequential lane sums, tree.
   float m = -INFINITY;
   for (int j = tid; j < nk; j += 256) m = fmaxf(m, sc[j]);
   red[tid] = m;
@@ -141,30 +311,16 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
   const float inv = inv_s;
   for (int j = tid; j < nk; j += 256) {
     const int64_t row = j < n0 ? j : anc[e0 + j - n0];
-    const float vscale = *reinterpret_cast<const float*>(vsb + row * a.s_row);
-    pv[j] = kRef ? sc[j] * vscale : sc[j] * inv * vscale;
+    pv[j] = sc[j] * inv * *reinterpret_cast<const float*>(vsb + row * a.s_row);  // (p * inv) * v-scale
   }
   __syncthreads();
-
-  // P.V: one sequential fma chain per output element, keys in order.
   for (int d = tid; d < D; d += 256) {
     float acc = 0.0f;
-    int j = 0;
-    for (; j + 4 <= nk; j += 4) {
-      int64_t r[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) r[u] = (j + u) < n0 ? (j + u) : anc[e0 + j + u - n0];
-      float vv[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) vv[u] = (float)vb[r[u] * a.k_row + d];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) acc = fma_(pv[j + u], vv[u], acc);
-    }
-    for (; j < nk; ++j) {
+    for (int j = 0; j < nk; ++j) {
       const int64_t r = j < n0 ? j : anc[e0 + j - n0];
       acc = fma_(pv[j], (float)vb[r * a.k_row + d], acc);
     }
-    out[t * out_stride + (int64_t)h * D + d] = kRef ? acc * inv : acc;
+    out[t * out_stride + (int64_t)h * D + d] = acc;
   }
 }
 
@@ -204,16 +360,10 @@ __device__ __forceinline__ void push(Top2& t, float v, int i) {
   }
 }
 
-constexpr int kSelT = 1024;
+constexpr int kSelT = 256;
+constexpr int kSelParts = 64;  // workgroups per logits row
 
-// Top-1 under (value desc, index asc) is std::max_element's first maximum; top-2 is the best of the rest under the
-// same order, which is what the reference's strict-'>' runner-up scan returns.
-__global__ __launch_bounds__(kSelT) void k_argmax_top2(const float* __restrict__ logits, int n, int32_t* top1,
-                                                       int32_t* top2) {
-  const float* l = logits + (int64_t)blockIdx.x * n;
-  Top2 t{-INFINITY, -INFINITY, 0x7fffffff, 0x7fffffff};
-  for (int i = threadIdx.x; i < n; i += kSelT) push(t, l[i], i);
-  __shared__ Top2 red[kSelT];
+__device__ __forceinline__ void block_top2(Top2& t, Top2* red) {
   red[threadIdx.x] = t;
   __syncthreads();
   for (int st = kSelT / 2; st > 0; st >>= 1) {
@@ -226,9 +376,42 @@ __global__ __launch_bounds__(kSelT) void k_argmax_top2(const float* __restrict__
     }
     __syncthreads();
   }
+  t = red[0];
+}
+
+// Top-1 under (value desc, index asc) is std::max_element's first maximum; top-2 is the best of the rest under the
+// same order, which is what the reference's strict-'>' runner-up scan returns. Pass 1: kSelParts workgroups per row
+// each reduce a slice; pass 2 merges the slices (the order is total, so the merge is associative).
+__global__ __launch_bounds__(kSelT) void k_top2_part(const float* __restrict__ logits, int n, Top2* __restrict__ part) {
+  const int row = blockIdx.y, p = blockIdx.x;
+  const float* l = logits + (int64_t)row * n;
+  const int per = (n + kSelParts - 1) / kSelParts, lo = p * per, hi = min(n, lo + per);
+  Top2 t{-INFINITY, -INFINITY, 0x7fffffff, 0x7fffffff};
+  for (int i = lo + threadIdx.x; i < hi; i += kSelT) push(t, l[i], i);
+  __shared__ Top2 red[kSelT];
+  block_top2(t, red);
+  if (threadIdx.x == 0) part[row * kSelParts + p] = t;
+}
+
+__global__ __launch_bounds__(kSelParts) void k_top2_merge(const Top2* __restrict__ part, int32_t* top1,
+                                                          int32_t* top2) {
+  const int row = blockIdx.x;
+  __shared__ Top2 red[kSelParts];
+  red[threadIdx.x] = part[row * kSelParts + threadIdx.x];
+  __syncthreads();
+  for (int st = kSelParts / 2; st > 0; st >>= 1) {
+    if (threadIdx.x < st) {
+      Top2 a = red[threadIdx.x];
+      const Top2 b = red[threadIdx.x + st];
+      push(a, b.v1, b.i1);
+      push(a, b.v2, b.i2);
+      red[threadIdx.x] = a;
+    }
+    __syncthreads();
+  }
   if (threadIdx.x == 0) {
-    top1[blockIdx.x] = red[0].i1;
-    if (top2) top2[blockIdx.x] = red[0].i2;
+    top1[row] = red[0].i1;
+    if (top2) top2[row] = red[0].i2;
   }
 }
 
@@ -255,28 +438,51 @@ void qk_norm_rope_kv(hipStream_t s, float* q, float* k, const float* v, int64_t 
                      const float* q_norm, const float* k_norm, float eps, const float* cos_t, const float* sin_t,
                      const int32_t* rpos, const int32_t* seq, const int32_t* kv_row, const KvLayer& kv, int n_ctx) {
   if (n <= 0) return;
-  require(D % 16 == 0, "qk_norm_rope_kv: head_dim must be a multiple of 16");
+  require(D % 16 == 0 && D <= 64 * kQkMaxPer, "qk_norm_rope_kv: head_dim must be a multiple of 16, at most 256");
   hipLaunchKernelGGL(k_qk_norm_rope_kv, dim3(n, H + 2 * KV), dim3(64), D * sizeof(float), s, q, k, v, stride, H, KV,
                      D, q_norm, k_norm, eps, cos_t, sin_t, rpos, seq, kv_row, kv, n_ctx);
   check_launch("qk_norm_rope_kv");
 }
 
 void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int H, int KV,
-               int D, float scale,
-               const AttnAddr& a, const int32_t* seq, const int32_t* n_keys, const int32_t* anc_off,
-               const int32_t* anc, int max_keys) {
+               int D, float scale, const AttnAddr& a, const int32_t* seq, const int32_t* n_keys,
+               const int32_t* anc_off, const int32_t* anc, int max_keys) {
   if (n <= 0) return;
-  require(D % 16 == 0 && D <= 256 && H % KV == 0, "attention: unsupported head layout");
+  require(D % 16 == 0 && D <= 256 && H % KV == 0 && max_keys > 0, "attention: unsupported head layout");
   const int G = H / KV;
-  const size_t lds = (size_t)(D + 2 * (size_t)max_keys) * sizeof(float);
-  require(lds <= 150 * 1024, "attention: too many keys for one workgroup");
-  const bool ref = G <= 16 && (D == 64 || D == 128 || D == 256);
-  if (ref)
-    hipLaunchKernelGGL(k_attention<true>, dim3(n, H), dim3(256), lds, s, q, q_stride, out, out_stride, H, G, D, scale, a, seq,
-                       n_keys, anc_off, anc);
-  else
-    hipLaunchKernelGGL(k_attention<false>, dim3(n, H), dim3(256), lds, s, q, q_stride, out, out_stride, H, G, D, scale, a, seq,
-                       n_keys, anc_off, anc);
+  const bool aligned = a.k_row % 16 == 0 && a.k_head % 16 == 0 && a.k_seq % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(a.k) % 16 == 0 && reinterpret_cast<uintptr_t>(a.v) % 16 == 0 &&
+                       a.s_row % 4 == 0 && reinterpret_cast<uintptr_t>(a.ks) % 4 == 0 &&
+                       reinterpret_cast<uintptr_t>(a.vs) % 4 == 0;
+  if (G <= 16 && (D == 64 || D == 128 || D == 256) && aligned) {
+    const int tile = D == 64 ? AttnTile<64>::tile : D == 128 ? AttnTile<128>::tile : AttnTile<256>::tile;
+    const size_t lds = attn_lds_bytes(tile, D, (max_keys + 3) & ~3);
+    require(lds <= 160 * 1024 - 1024, "attention: too many keys for one workgroup");
+    auto go = [&](auto kernel) {
+      static bool attr = false;
+      if (!attr) {
+        check(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  160 * 1024 - 1024),
+              "hipFuncSetAttribute");
+        attr = true;
+      }
+      hipLaunchKernelGGL(kernel, dim3(n, H), dim3(kAttnThreads), lds, s, q, q_stride, out, out_stride, G, scale, a,
+                         seq, n_keys, anc_off, anc);
+    };
+    if (D == 64)
+      go(k_attention<64>);
+    else if (D == 128)
+      go(k_attention<128>);
+    else
+      go(k_attention<256>);
+  } else {
+    const size_t lds = (size_t)(D + 2 * (size_t)max_keys) * sizeof(float);
+    require(lds <= 60 * 1024, "attention: too many keys for one workgroup");
+    const bool ref_order = G <= 16 && (D == 64 || D == 128 || D == 256);
+    require(!ref_order, "attention: K/V rows must be 16-byte aligned");
+    hipLaunchKernelGGL(k_attention_generic, dim3(n, H), dim3(256), lds, s, q, q_stride, out, out_stride, G, D, scale,
+                       a, seq, n_keys, anc_off, anc);
+  }
   check_launch("attention");
 }
 
@@ -288,10 +494,16 @@ void move_kv_rows(hipStream_t s, int8_t* k8, int8_t* v8, float* ks, float* vs, i
   check_launch("move_kv");
 }
 
-void argmax_top2(hipStream_t s, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2) {
+size_t argmax_scratch_bytes(int rows) { return (size_t)rows * kSelParts * sizeof(Top2); }
+
+void argmax_top2(hipStream_t s, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2,
+                 void* scratch, size_t scratch_bytes) {
   if (rows <= 0) return;
   require(n_vocab >= 2, "argmax_top2: need at least two logits");
-  hipLaunchKernelGGL(k_argmax_top2, dim3(rows), dim3(kSelT), 0, s, logits, n_vocab, top1, top2);
+  require(argmax_scratch_bytes(rows) <= scratch_bytes, "argmax_top2: too many rows for the context scratch");
+  Top2* part = static_cast<Top2*>(scratch);
+  hipLaunchKernelGGL(k_top2_part, dim3(kSelParts, rows), dim3(kSelT), 0, s, logits, n_vocab, part);
+  hipLaunchKernelGGL(k_top2_merge, dim3(rows), dim3(kSelParts), 0, s, part, top1, top2);
   check_launch("argmax_top2");
 }
 

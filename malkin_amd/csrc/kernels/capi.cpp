@@ -54,6 +54,8 @@ int mk_init(int device, mk_ctx** out) {
     check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
     check(hipEventCreate(&c->ev0), "hipEventCreate");
     check(hipEventCreate(&c->ev1), "hipEventCreate");
+    c->scratch_bytes = 1 << 20;
+    check(hipMalloc(&c->scratch, c->scratch_bytes), "hipMalloc");
     *out = c;
   });
 }
@@ -66,6 +68,7 @@ int mk_destroy(mk_ctx* c) {
     (void)hipEventDestroy(c->ev0);
     (void)hipEventDestroy(c->ev1);
     (void)hipStreamDestroy(c->stream);
+    (void)hipFree(c->scratch);
     delete c;
   });
 }
@@ -250,7 +253,7 @@ int mk_greedy_advance(mk_ctx* c, const int32_t* top1, int32_t* ids, int32_t* rpo
 }
 
 int mk_argmax_top2(mk_ctx* c, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2) {
-  return guard([&] { mk::argmax_top2(c->stream, logits, rows, n_vocab, top1, top2); });
+  return guard([&] { mk::argmax_top2(c->stream, logits, rows, n_vocab, top1, top2, c->scratch, c->scratch_bytes); });
 }
 
 }  // extern "C"

@@ -16,6 +16,8 @@ struct mk_ctx {
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   int n_cu = 0;
   char name[64] = {0};
+  void* scratch = nullptr;  // per-context device scratch (partial reductions), allocated once at init
+  size_t scratch_bytes = 0;
 };
 
 namespace mk {

@@ -125,24 +125,45 @@ __global__ __launch_bounds__(kThreads) void k_gemv(const uint8_t* __restrict__ W
 
   for (int64_t c0 = 0; c0 < nu; c0 += chunk) {
     const int cn = (int)min<int64_t>(chunk, nu - c0);
-    // Stage this chunk's activation blocks.
-    const int words = cn * UQ8 * 10;
-    for (int i = tid; i < nt * words; i += kThreads) {
-      const int t = i / words, rem = i % words;
-      const int* src = reinterpret_cast<const int*>(x + (int64_t)(t0 + t) * nq8 + c0 * UQ8);
-      xs[t * chunk * UQ8 * 10 + rem] = src[rem];
+    // The first group of this chunk's weight loads goes out before the activations are staged, so HBM latency
+    // overlaps the staging and the barrier.
+    Raw raw[kUnroll];
+#pragma unroll
+    for (int k = 0; k < kUnroll; ++k) {
+      const int f = tid + k * kThreads;
+      if (f < R * cn) raw[k] = load_unit<TYPE>(W, rows, cols, g0 + (f % R) / 8, (f % R) % 8, c0 + f / R);
+    }
+    // Stage this chunk's activation blocks: 8-byte loads (BlockQ8 is 8-byte aligned), all issued before any store.
+    const int pairs = cn * UQ8 * 5;  // 8-byte words per token
+    constexpr int kStage = 8;
+    for (int i0 = tid; i0 < nt * pairs; i0 += kThreads * kStage) {
+      uint2 v[kStage];
+#pragma unroll
+      for (int k = 0; k < kStage; ++k) {
+        const int i = i0 + k * kThreads;
+        if (i < nt * pairs) {
+          const int t = i / pairs, rem = i % pairs;
+          v[k] = reinterpret_cast<const uint2*>(x + (int64_t)(t0 + t) * nq8 + c0 * UQ8)[rem];
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kStage; ++k) {
+        const int i = i0 + k * kThreads;
+        if (i < nt * pairs) {
+          const int t = i / pairs, rem = i % pairs;
+          reinterpret_cast<uint2*>(xs + t * chunk * UQ8 * 10)[rem] = v[k];
+        }
+      }
     }
     __syncthreads();
 
     // Phase 1: int dots and per-unit float terms.
     for (int f0 = tid; f0 < R * cn; f0 += kThreads * kUnroll) {
-      Raw raw[kUnroll];
+      if (f0 != tid) {
 #pragma unroll
-      for (int k = 0; k < kUnroll; ++k) {
-        const int f = f0 + k * kThreads;
-        if (f < R * cn) {
-          const int u = f / R, r = f % R;
-          raw[k] = load_unit<TYPE>(W, rows, cols, g0 + r / 8, r % 8, c0 + u);
+        for (int k = 0; k < kUnroll; ++k) {
+          const int f = f0 + k * kThreads;
+          if (f < R * cn) raw[k] = load_unit<TYPE>(W, rows, cols, g0 + (f % R) / 8, (f % R) % 8, c0 + f / R);
         }
       }
 #pragma unroll
@@ -233,6 +254,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv(const uint8_t* __restrict__ W
 
     // Phase 2: the sequential chains, in block order.
     if (chain) {
+#pragma unroll 8
       for (int u = 0; u < cn; ++u) {
         const float* e = res + (((size_t)u * NT + ct) * R + cr) * E;
         if constexpr (TYPE == kQ8_0) {
@@ -308,7 +330,10 @@ void matmul(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int
   require(packed_bytes(type, rows, cols) != 0, "matmul: no kernel for this weight type/shape");
   switch (type) {
     case kQ8_0:
-      launch_r<kQ8_0, false>(s, w, rows, cols, xq, n, y, ys, accumulate);
+      if (gemm_q8_0_supported(rows, cols, n))
+        gemm_q8_0(s, w, rows, cols, xq, n, y, ys, accumulate);  // prefill / batches: int8 MFMA
+      else
+        launch_r<kQ8_0, false>(s, w, rows, cols, xq, n, y, ys, accumulate);
       break;
     case kQ4_K:
       launch_r<kQ4_K, false>(s, w, rows, cols, xq, n, y, ys, accumulate);

@@ -50,6 +50,11 @@ void fill(hipStream_t s, void* p, int value, size_t bytes);
 void matmul(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int64_t cols, const BlockQ8* xq, int n,
             float* y, int64_t ys, bool accumulate);
 
+// Prefill GEMM for Q8_0 on int8 MFMA (same results as matmul's GEMV); supported for rows % 32 == 0 and n > 8.
+bool gemm_q8_0_supported(int64_t rows, int64_t cols, int n);
+void gemm_q8_0(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y, int64_t ys,
+               bool accumulate);
+
 // Generic attention addressing: key row (t, g, row) at k + seq*k_seq + g*k_head + row*k_row (bytes), its scale at
 // ks + seq*s_seq + g*s_head + row*s_row (bytes); values likewise with v / vs.
 struct AttnAddr {
@@ -73,7 +78,10 @@ void qk_norm_rope_kv(hipStream_t s, float* q, float* k, const float* v, int64_t 
                      const float* q_norm, const float* k_norm, float eps, const float* cos_t, const float* sin_t,
                      const int32_t* rpos, const int32_t* seq, const int32_t* kv_row, const KvLayer& kv, int n_ctx);
 
-void argmax_top2(hipStream_t s, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2);
+// Scratch: argmax_scratch_bytes(rows) of device memory (per-row partial results).
+size_t argmax_scratch_bytes(int rows);
+void argmax_top2(hipStream_t s, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2,
+                 void* scratch, size_t scratch_bytes);
 
 void greedy_advance(hipStream_t s, const int32_t* top1, int32_t* ids, int32_t* rpos, int32_t* kv_row, int32_t* n_keys,
                     int32_t* out_tokens, int32_t* counter);

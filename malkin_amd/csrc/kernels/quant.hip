@@ -13,51 +13,33 @@ namespace {
 
 constexpr int kT = 256;
 
-// One 32-value block of f32 activations -> BlockQ8, in one thread.
-__device__ __forceinline__ void quantize_block(const float* v, BlockQ8* out) {
-  float amax = 0.0f;
+// One 32-value block of f32 activations -> BlockQ8 (kernels_avx512.cpp:66-80), one block per 32 lanes (a half
+// wavefront): lane l holds value l of the block. amax is an exact max and the half sums are exact integer sums, so the lane order of the reductions does not matter.
+__device__ __forceinline__ void quantize_block_lanes(float v, int l, BlockQ8* out) {
+  float amax = fabsf(v);
 #pragma unroll
-  for (int l = 0; l < 32; ++l) amax = fmaxf(amax, fabsf(v[l]));
+  for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
   const float d = amax / 127.0f;
   const float id = d != 0.0f ? 1.0f / d : 0.0f;
-  int s0 = 0, s1 = 0;
-  int packed[8];
+  const int q = cvt_rne(v * id);
+  int s = q;
 #pragma unroll
-  for (int w = 0; w < 8; ++w) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int l = 4 * w + b;
-      const int q = cvt_rne(v[l] * id);
-      if (l < 16)
-        s0 += q;
-      else
-        s1 += q;
-      word |= (uint32_t)(uint8_t)(int8_t)sat8(q) << (8 * b);
-    }
-    packed[w] = (int)word;
+  for (int off = 8; off > 0; off >>= 1) s += __shfl_xor(s, off, 16);
+  int8_t* o = reinterpret_cast<int8_t*>(out);
+  o[8 + l] = (int8_t)sat8(q);
+  if (l == 0) {
+    *reinterpret_cast<float*>(o) = d;
+    *reinterpret_cast<int16_t*>(o + 4) = (int16_t)s;
+  } else if (l == 16) {
+    *reinterpret_cast<int16_t*>(o + 6) = (int16_t)s;
   }
-  int* o = reinterpret_cast<int*>(out);
-  o[0] = __float_as_int(d);
-  o[1] = (int)((uint32_t)(uint16_t)(int16_t)s0 | ((uint32_t)(uint16_t)(int16_t)s1 << 16));
-#pragma unroll
-  for (int w = 0; w < 8; ++w) o[2 + w] = packed[w];
 }
 
-__global__ void k_quantize_q8(const float* __restrict__ x, int64_t nblocks, BlockQ8* __restrict__ y) {
+// One element per thread; x has n * k elements, k % 32 == 0.
+__global__ void k_quantize_q8(const float* __restrict__ x, int64_t total, BlockQ8* __restrict__ y) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= nblocks) return;
-  float v[32];
-  const float4* src = reinterpret_cast<const float4*>(x + i * 32);
-#pragma unroll
-  for (int w = 0; w < 8; ++w) {
-    const float4 f = src[w];
-    v[4 * w] = f.x;
-    v[4 * w + 1] = f.y;
-    v[4 * w + 2] = f.z;
-    v[4 * w + 3] = f.w;
-  }
-  quantize_block(v, y + i);
+  if (i >= total) return;
+  quantize_block_lanes(x[i], (int)(i & 31), y + i / 32);
 }
 
 __global__ void k_quantize_i8(const float* __restrict__ x, int n, int8_t* __restrict__ q, float* __restrict__ d) {
@@ -78,33 +60,77 @@ __global__ void k_quantize_i8(const float* __restrict__ x, int n, int8_t* __rest
 }
 
 // rmsnorm of one row per workgroup; the sum of squares follows kern::dot_f32 (kernels_avx512.cpp:82-89): 16 lane
-// accumulators, each a sequential fma chain over the elements i = l (mod 16), then the halving tree.
+// accumulators, each a sequential fma chain over the elements i = l (mod 16), then the halving tree. The row is also
+// kept transposed in LDS (lane l's elements contiguous) so each chain reads four elements per 16-byte access.
 template <bool kQuant>
 __global__ void k_rmsnorm(const float* __restrict__ x, const int32_t* __restrict__ rows_idx,
                           const float* __restrict__ w, int n, float eps, float* __restrict__ y,
                           BlockQ8* __restrict__ xq) {
-  extern __shared__ float row[];  // n floats
+  extern __shared__ float4 sm4[];
+  float* row = reinterpret_cast<float*>(sm4);  // n floats
+  const int per = n / 16, tstride = ((per + 3) & ~3) + 4;  // transposed rows [16][tstride], 16-byte aligned
+  float* tr = row + n;
   __shared__ float scale;
   const int r = blockIdx.x;
   const float* xr = x + (int64_t)(rows_idx ? rows_idx[r] : r) * n;
-  for (int i = threadIdx.x; i < n; i += kT) row[i] = xr[i];
+  // 16-byte loads, all in flight together (n % 16 == 0).
+  constexpr int kMaxVec = 8;  // up to 8 x 4 x 256 = 8192 floats per row
+  float4 v4[kMaxVec], w4[kMaxVec];
+#pragma unroll
+  for (int k = 0; k < kMaxVec; ++k) {
+    const int i = 4 * (threadIdx.x + k * kT);
+    if (i < n) {
+      v4[k] = *reinterpret_cast<const float4*>(xr + i);
+      w4[k] = *reinterpret_cast<const float4*>(w + i);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kMaxVec; ++k) {
+    const int i = 4 * (threadIdx.x + k * kT);
+    if (i < n) {
+      const float e[4] = {v4[k].x, v4[k].y, v4[k].z, v4[k].w};
+      *reinterpret_cast<float4*>(row + i) = v4[k];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) tr[((i + c) & 15) * tstride + ((i + c) >> 4)] = e[c];
+    }
+  }
   __syncthreads();
   if (threadIdx.x < 16) {
     const int l = threadIdx.x;
+    const float* tl = tr + l * tstride;
     float acc = 0.0f;
-    for (int i = l; i < n; i += 16) acc = fma_(row[i], row[i], acc);
+    int i = 0;
+    for (; i + 4 <= per; i += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(tl + i);
+      acc = fma_(v.x, v.x, acc);
+      acc = fma_(v.y, v.y, acc);
+      acc = fma_(v.z, v.z, acc);
+      acc = fma_(v.w, v.w, acc);
+    }
+    for (; i < per; ++i) acc = fma_(tl[i], tl[i], acc);
     acc = reduce16_lanes(acc);
     if (l == 0) scale = 1.0f / sqrtf(acc / (float)n + eps);
   }
   __syncthreads();
   const float s = scale;
-  if (!kQuant) {
-    for (int i = threadIdx.x; i < n; i += kT) y[(int64_t)r * n + i] = row[i] * s * w[i];
-    return;
+  // y = x * s * w from the registers loaded above: thread handles elements 4 (tid + k kT) .. + 3.
+#pragma unroll
+  for (int k = 0; k < kMaxVec; ++k) {
+    const int i = 4 * (threadIdx.x + k * kT);
+    if (i >= n) break;
+    const float4 yv = make_float4(v4[k].x * s * w4[k].x, v4[k].y * s * w4[k].y, v4[k].z * s * w4[k].z,
+                                  v4[k].w * s * w4[k].w);
+    if (!kQuant) {
+      *reinterpret_cast<float4*>(y + (int64_t)r * n + i) = yv;
+    } else {
+      *reinterpret_cast<float4*>(row + i) = yv;
+    }
   }
-  for (int i = threadIdx.x; i < n; i += kT) row[i] = row[i] * s * w[i];
+  if (!kQuant) return;
   __syncthreads();
-  for (int b = threadIdx.x; b < n / 32; b += kT) quantize_block(row + 32 * b, xq + (int64_t)r * (n / 32) + b);
+  // Quantize: element i on lane i % 32 of a half wave.
+  for (int i = threadIdx.x; i < n; i += kT)
+    quantize_block_lanes(row[i], i & 31, xq + (int64_t)r * (n / 32) + i / 32);
 }
 
 __global__ void k_silu_mul(int64_t n, float* __restrict__ g, const float* __restrict__ u) {
@@ -115,21 +141,14 @@ __global__ void k_silu_mul(int64_t n, float* __restrict__ g, const float* __rest
   g[i] = (x / (1.0f + e)) * u[i];
 }
 
-// gu row: [gate(n) | up(n)] -> silu(gate) * up, quantized; one thread per 32-value block.
-__global__ void k_silu_mul_q8(const float* __restrict__ gu, int64_t n, int64_t nblocks, BlockQ8* __restrict__ xq) {
+// gu row: [gate(n) | up(n)] -> silu(gate) * up, quantized; one element per thread, n % 32 == 0.
+__global__ void k_silu_mul_q8(const float* __restrict__ gu, int64_t n, int64_t total, BlockQ8* __restrict__ xq) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= nblocks) return;
-  const int64_t per = n / 32, r = i / per, b = i % per;
-  const float* g = gu + r * 2 * n + b * 32;
-  const float* u = g + n;
-  float v[32];
-#pragma unroll
-  for (int l = 0; l < 32; ++l) {
-    const float x = g[l];
-    const float e = exp512(0.0f - x);
-    v[l] = (x / (1.0f + e)) * u[l];
-  }
-  quantize_block(v, xq + i);
+  if (i >= total) return;
+  const int64_t r = i / n, c = i % n;
+  const float x = gu[r * 2 * n + c];
+  const float e = exp512(0.0f - x);
+  quantize_block_lanes((x / (1.0f + e)) * gu[r * 2 * n + n + c], (int)(c & 31), xq + i / 32);
 }
 
 __global__ void k_add(int64_t n, float* __restrict__ x, const float* __restrict__ h) {
@@ -193,9 +212,9 @@ unsigned grid_for(int64_t n, int t) { return (unsigned)((n + t - 1) / t); }
 
 void quantize_q8(hipStream_t s, const float* x, int n, int64_t k, BlockQ8* xq) {
   require(k % 32 == 0, "quantize_q8: k must be a multiple of 32");
-  const int64_t nb = (int64_t)n * (k / 32);
-  if (nb == 0) return;
-  hipLaunchKernelGGL(k_quantize_q8, dim3(grid_for(nb, kT)), dim3(kT), 0, s, x, nb, xq);
+  const int64_t total = (int64_t)n * k;
+  if (total == 0) return;
+  hipLaunchKernelGGL(k_quantize_q8, dim3(grid_for(total, kT)), dim3(kT), 0, s, x, total, xq);
   check_launch("quantize_q8");
 }
 
@@ -215,18 +234,20 @@ void dequantize_rows(hipStream_t s, int type, const void* src, size_t row_bytes,
   check_launch("dequantize_rows");
 }
 
+static size_t rmsnorm_lds(int n) { return ((size_t)n + 16 * ((((size_t)n / 16 + 3) & ~(size_t)3) + 4)) * sizeof(float); }
+
 void rmsnorm(hipStream_t s, const float* x, const float* w, int rows, int n, float eps, float* y) {
   if (rows <= 0) return;
-  require(n % 16 == 0, "rmsnorm: n must be a multiple of 16");
-  hipLaunchKernelGGL(k_rmsnorm<false>, dim3(rows), dim3(kT), n * sizeof(float), s, x, nullptr, w, n, eps, y, nullptr);
+  require(n % 16 == 0 && n <= 8192 && rmsnorm_lds(n) <= 64 * 1024, "rmsnorm: n must be a multiple of 16, <= 7936");
+  hipLaunchKernelGGL(k_rmsnorm<false>, dim3(rows), dim3(kT), rmsnorm_lds(n), s, x, nullptr, w, n, eps, y, nullptr);
   check_launch("rmsnorm");
 }
 
 void rmsnorm_q8(hipStream_t s, const float* x, const int32_t* rows_idx, const float* w, int rows, int n, float eps,
                 BlockQ8* xq) {
   if (rows <= 0) return;
-  require(n % 32 == 0, "rmsnorm_q8: n must be a multiple of 32");
-  hipLaunchKernelGGL(k_rmsnorm<true>, dim3(rows), dim3(kT), n * sizeof(float), s, x, rows_idx, w, n, eps, nullptr, xq);
+  require(n % 32 == 0 && n <= 8192 && rmsnorm_lds(n) <= 64 * 1024, "rmsnorm_q8: n must be a multiple of 32, <= 7936");
+  hipLaunchKernelGGL(k_rmsnorm<true>, dim3(rows), dim3(kT), rmsnorm_lds(n), s, x, rows_idx, w, n, eps, nullptr, xq);
   check_launch("rmsnorm_q8");
 }
 
@@ -240,9 +261,9 @@ void silu_mul(hipStream_t s, int64_t n, float* g, const float* u) {
 
 void silu_mul_q8(hipStream_t s, const float* gu, int rows, int64_t n, BlockQ8* xq) {
   require(n % 32 == 0, "silu_mul_q8: n must be a multiple of 32");
-  const int64_t nb = (int64_t)rows * (n / 32);
-  if (nb == 0) return;
-  hipLaunchKernelGGL(k_silu_mul_q8, dim3(grid_for(nb, kT)), dim3(kT), 0, s, gu, n, nb, xq);
+  const int64_t total = (int64_t)rows * n;
+  if (total == 0) return;
+  hipLaunchKernelGGL(k_silu_mul_q8, dim3(grid_for(total, kT)), dim3(kT), 0, s, gu, n, total, xq);
   check_launch("silu_mul_q8");
 }
 
