@@ -94,21 +94,32 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope_kv(float* __restrict__ q, f
 
 // Attention of one query head per workgroup, attend_t semantics (D in {64,128,256}, G <= 16):
 //   scores  one key per thread: the 16 lane chains of attend_t (mul, then fma over D/16 chunks) from 16-byte K
-//           loads, the halving tree, times (kv_scale * scale);
-//   softmax exact max, e = exp512(s - max), 16 sequential lane sums + tree;
+//           loads, the halving tree, times (kv_scale * scale); the first round of K rows is issued at entry;
+//   softmax exact max, e = exp512(s - max); the 16 sequential lane sums + tree run on otherwise idle threads while
+//           the P.V chains start;
 //   P.V     one sequential fma chain per output element over all keys in order. V is staged a tile of keys at a
-//           time into LDS as int8, transposed to [d][key]; the staging threads (all but the first D) load chunk c+1
-//           into registers while lanes 0..D-1 run the chains of chunk c from 16-byte LDS reads.
+//           time into LDS, converted to fp32 and transposed to [d][key], so a chain step is one fma fed by 16-byte
+//           LDS reads (a dependent fma takes 9 cycles on gfx950; an int8 convert in the chain nearly doubles that).
+//           Lane i of each 16-lane row reads p of key i of the current 16-key group; DPP broadcasts it to the row.
+//           The staging threads form NG groups; group c % NG owns chunk c, loads it into registers NG chunks ahead and
+//           stores it to LDS while lanes 0..D-1 run the chains of chunk c - 1. Barriers order LDS only, so the staging
+//           loads stay in flight across them (a V load takes about 1 us to return, i.e. some 250 chain steps). Chains run over whole 16-key groups: keys past the end have p = 0 and v = 0, and
+//           fma(0, 0, acc) == acc.
 constexpr int kAttnThreads = 1024;
+constexpr int kSumThread = kAttnThreads - 16;  // threads [1008, 1024) are never stagers (see AttnTile)
 
 template <int D>
 struct AttnTile {
-  static constexpr int chunk = D >= 256 ? 128 : 256;  // keys per V tile
-  static constexpr int stride = chunk + 16;            // bytes per tile row [d]: 16-byte aligned, spreads banks
-  static constexpr int tile = D * stride;              // bytes per tile
-  static constexpr int tasks = (chunk / 4) * (D / 16); // staging task: 4 keys x 16 values
+  static constexpr int chunk = 8192 / D;                 // keys per V tile: 32 KB of fp32 values
+  static constexpr int stride = chunk + 4;               // floats per tile row [d]: 16-byte aligned, spreads banks
+  static constexpr int tile = D * stride * 4;            // bytes per tile
+  static constexpr int tasks = (chunk / 4) * (D / 16);   // staging task: 4 keys x 16 values
+  static constexpr int groups = (kSumThread - D) / tasks;  // staging groups, one chunk in flight each
+  static_assert(groups >= 2, "too few staging threads");
 };
 
+__host__ __device__ constexpr int attn_keys_pad(int nk) { return (nk + 15) & ~15; }
+// LDS: two V tiles, q, scores, p.
 __host__ __device__ constexpr size_t attn_lds_bytes(int tile_bytes, int D, int nk_pad) {
   return 2 * (size_t)tile_bytes + 4 * ((size_t)D + 2 * (size_t)nk_pad);
 }
@@ -119,19 +130,33 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
                                                             float scale, AttnAddr a, const int32_t* __restrict__ seqs,
                                                             const int32_t* __restrict__ n_keys,
                                                             const int32_t* __restrict__ anc_off,
-                                                            const int32_t* __restrict__ anc) {
+                                                            const int32_t* __restrict__ anc, int n, int H) {
   constexpr int DC = D / 16;
   using T = AttnTile<D>;
-  const int t = blockIdx.x, h = blockIdx.y, g = h / G, tid = threadIdx.x;
+  // Workgroups are dealt to the 8 XCDs in turn (workgroup w on XCD w % 8). (token, head) pairs are numbered
+  // KV-group-major (group, token, head in group) and XCD x takes a contiguous run of them: a KV group's K/V rows are
+  // read into one XCD's L2, and in prefill every XCD gets tokens of all lengths.
+  const int tid = threadIdx.x;
+  int t, h;
+  if ((n * H) % 8 == 0) {
+    const int pair = (int)(blockIdx.x % 8) * (n * H / 8) + (int)(blockIdx.x / 8);
+    const int grp = pair / (n * G), rem = pair % (n * G);
+    t = rem / G;
+    h = grp * G + rem % G;
+  } else {
+    t = (int)blockIdx.x / H;
+    h = (int)blockIdx.x % H;
+  }
+  const int g = h / G;
   const int n0 = n_keys[t];
   const int e0 = anc_off ? anc_off[t] : 0, ne = anc_off ? anc_off[t + 1] - e0 : 0;
   const int nk = n0 + ne;
-  const int nk_pad = (nk + 3) & ~3;
+  const int nk_pad = attn_keys_pad(nk);
   extern __shared__ int4 smem4[];
-  int8_t* tiles = reinterpret_cast<int8_t*>(smem4);                // 2 x [D][stride] int8
-  float* qs = reinterpret_cast<float*>(tiles + 2 * T::tile);     // D
+  float* tiles = reinterpret_cast<float*>(smem4);                 // 2 x [D][stride] fp32
+  float* qs = tiles + 2 * T::tile / 4;                           // D
   float* sc = qs + D;                                            // nk_pad: scores, then e^(s - max)
-  float* pv = sc + nk_pad;                                       // nk_pad: e * v-scale
+  float* pv = sc + nk_pad;                                       // nk_pad: e * v-scale, zero past nk
   __shared__ float red[kAttnThreads / 64];
   __shared__ float inv_s;
   const int64_t sq = seqs[t];
@@ -141,12 +166,14 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
   const char* vsb = a.vs + sq * a.s_seq + g * a.s_head;
   auto key_row = [&](int j) -> int64_t { return j < n0 ? j : anc[e0 + j - n0]; };
 
-  // V staging: task = 4 consecutive keys x 16 consecutive values, written as 16 dwords of the transposed tile.
-  const bool stager = tid >= D;
-  const int task = tid - D;
+  // V staging: task = 4 consecutive keys x 16 consecutive values, written as 16 float4 of the transposed tile.
+  constexpr int NG = T::groups;
+  const bool stager = tid >= D && tid < D + NG * T::tasks;
+  const int grp = (tid - D) / T::tasks, task = (tid - D) % T::tasks;
+  auto mine = [&](int c) { return stager && grp == c % NG; };
   uint4 vreg[4];
   auto load_chunk = [&](int c) {
-    if (!stager || task >= T::tasks) return;
+    if (!mine(c)) return;
     const int kq = task % (T::chunk / 4), db = task / (T::chunk / 4);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -155,36 +182,39 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
     }
   };
   auto store_chunk = [&](int c) {
-    if (!stager || task >= T::tasks) return;
+    if (!mine(c)) return;
     const int kq = task % (T::chunk / 4), db = task / (T::chunk / 4);
-    int8_t* tile = tiles + (c & 1) * T::tile;
+    float* tile = tiles + (c & 1) * (T::tile / 4);
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      uint32_t w = 0;
+      float f[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t word = (&vreg[i].x)[v >> 2];
-        w |= ((word >> (8 * (v & 3))) & 0xFFu) << (8 * i);
-      }
-      *reinterpret_cast<uint32_t*>(tile + (16 * db + v) * T::stride + 4 * kq) = w;
+      for (int i = 0; i < 4; ++i) f[i] = (float)(int8_t)((&vreg[i].x)[v >> 2] >> (8 * (v & 3)));
+      *reinterpret_cast<float4*>(tile + (16 * db + v) * T::stride + 4 * kq) = make_float4(f[0], f[1], f[2], f[3]);
     }
   };
   const int chunks = (nk + T::chunk - 1) / T::chunk;
-  load_chunk(0);  // V's first tile is in flight during the scores
+  for (int c = 0; c < NG && c < chunks; ++c) load_chunk(c);  // the first NG tiles are in flight during the scores
 
-  const float* qh = q + t * q_stride + (int64_t)h * D;
-  for (int i = tid; i < D; i += kAttnThreads) qs[i] = qh[i];
-  __syncthreads();
-
-  // Scores (kernels_avx512.cpp:234-244); the value scale of the same key is fetched alongside.
-  for (int j = tid; j < nk; j += kAttnThreads) {
+  // K row, key scale and value scale of key j.
+  int4 kv[DC];
+  float kscale = 0.0f, vscale = 0.0f;
+  auto load_key = [&](int j) {
     const int64_t row = key_row(j);
     const int4* kr = reinterpret_cast<const int4*>(kb + row * a.k_row);
-    int4 kv[DC];
 #pragma unroll
     for (int c = 0; c < DC; ++c) kv[c] = kr[c];
-    const float kscale = *reinterpret_cast<const float*>(ksb + row * a.s_row);
-    pv[j] = *reinterpret_cast<const float*>(vsb + row * a.s_row);
+    kscale = *reinterpret_cast<const float*>(ksb + row * a.s_row);
+    vscale = *reinterpret_cast<const float*>(vsb + row * a.s_row);
+  };
+  if (tid < nk) load_key(tid);
+  const float* qh = q + t * q_stride + (int64_t)h * D;
+  for (int i = tid; i < D; i += kAttnThreads) qs[i] = qh[i];
+  lds_barrier();
+
+  // Scores (kernels_avx512.cpp:234-244).
+  for (int j = tid; j < nk; j += kAttnThreads) {
+    if (j != tid) load_key(j);
     float lanes[16];
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
@@ -196,16 +226,18 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
       }
     }
     sc[j] = reduce16(lanes) * (kscale * scale);
+    pv[j] = vscale;
   }
   store_chunk(0);
-  __syncthreads();
+  if (NG < chunks) load_chunk(NG);
+  lds_barrier();
 
   // softmax_inplace (kernels_avx512.cpp:205-226).
   float m = -INFINITY;
   for (int j = tid; j < nk; j += kAttnThreads) m = fmaxf(m, sc[j]);
   for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
   if ((tid & 63) == 0) red[tid >> 6] = m;
-  __syncthreads();
+  lds_barrier();
   float mx = red[0];
   for (int i = 1; i < kAttnThreads / 64; ++i) mx = fmaxf(mx, red[i]);
   for (int j = tid; j < nk; j += kAttnThreads) {
@@ -214,39 +246,45 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
     pv[j] = e * pv[j];
   }
   for (int j = nk + tid; j < nk_pad; j += kAttnThreads) pv[j] = 0.0f;
-  if (chunks > 1) load_chunk(1);
-  __syncthreads();
-  if (tid < 16) {
-    float s = 0.0f;
-#pragma unroll 8
-    for (int j = tid; j < nk; j += 16) s = s + sc[j];
-    s = reduce16_lanes(s);
-    if (tid == 0) inv_s = 1.0f / s;
-  }
+  lds_barrier();
 
-  // P.V (kernels_avx512.cpp:247-265): chunk c from tile c & 1 while chunk c + 1 is stored and c + 2 is loaded.
+  // P.V (kernels_avx512.cpp:247-265): chunk c from tile c & 1 while chunk c + 1 is stored and c + 1 + NG loaded.
   float acc = 0.0f;
   for (int c = 0; c < chunks; ++c) {
     if (tid < D) {
       const int j0 = c * T::chunk;
-      const int len = min(T::chunk, nk - j0);
-      const int8_t* vr = tiles + (c & 1) * T::tile + tid * T::stride;
+      const int len = min(T::chunk, nk_pad - j0);  // a multiple of 16
+      const float4* vr = reinterpret_cast<const float4*>(tiles + (c & 1) * (T::tile / 4) + tid * T::stride);
       for (int jj = 0; jj < len; jj += 16) {
-        const int4 v16 = *reinterpret_cast<const int4*>(vr + jj);
-        const int w[4] = {v16.x, v16.y, v16.z, v16.w};
-        const int lim = min(16, len - jj);
-        if (lim == 16) {
+        float4 v[4];
 #pragma unroll
-          for (int i = 0; i < 16; ++i) acc = fma_(pv[j0 + jj + i], (float)(int8_t)(w[i >> 2] >> (8 * (i & 3))), acc);
-        } else {
-          for (int i = 0; i < lim; ++i) acc = fma_(pv[j0 + jj + i], (float)(int8_t)(w[i >> 2] >> (8 * (i & 3))), acc);
+        for (int i = 0; i < 4; ++i) v[i] = vr[jj / 4 + i];
+        const float pr = pv[j0 + jj + (tid & 15)];
+        float p[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) p[i] = bcast16(pr, i);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc = fma_(p[4 * i], v[i].x, acc);
+          acc = fma_(p[4 * i + 1], v[i].y, acc);
+          acc = fma_(p[4 * i + 2], v[i].z, acc);
+          acc = fma_(p[4 * i + 3], v[i].w, acc);
         }
+      }
+    } else if (tid >= kSumThread) {
+      if (c == 0) {
+        const int l = tid - kSumThread;
+        float s = 0.0f;
+#pragma unroll 8
+        for (int j = l; j < nk; j += 16) s = s + sc[j];
+        s = reduce16_lanes(s);
+        if (l == 0) inv_s = 1.0f / s;
       }
     } else if (c + 1 < chunks) {
       store_chunk(c + 1);
-      if (c + 2 < chunks) load_chunk(c + 2);
+      if (c + 1 + NG < chunks) load_chunk(c + 1 + NG);
     }
-    __syncthreads();
+    lds_barrier();
   }
   if (tid < D) out[t * out_stride + (int64_t)h * D + tid] = acc * inv_s;
 }
@@ -456,7 +494,7 @@ void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int6
                        reinterpret_cast<uintptr_t>(a.vs) % 4 == 0;
   if (G <= 16 && (D == 64 || D == 128 || D == 256) && aligned) {
     const int tile = D == 64 ? AttnTile<64>::tile : D == 128 ? AttnTile<128>::tile : AttnTile<256>::tile;
-    const size_t lds = attn_lds_bytes(tile, D, (max_keys + 3) & ~3);
+    const size_t lds = attn_lds_bytes(tile, D, attn_keys_pad(max_keys));
     require(lds <= 160 * 1024 - 1024, "attention: too many keys for one workgroup");
     auto go = [&](auto kernel) {
       static bool attr = false;
@@ -466,8 +504,8 @@ void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int6
               "hipFuncSetAttribute");
         attr = true;
       }
-      hipLaunchKernelGGL(kernel, dim3(n, H), dim3(kAttnThreads), lds, s, q, q_stride, out, out_stride, G, scale, a,
-                         seq, n_keys, anc_off, anc);
+      hipLaunchKernelGGL(kernel, dim3(n * H), dim3(kAttnThreads), lds, s, q, q_stride, out, out_stride, G, scale, a,
+                         seq, n_keys, anc_off, anc, n, H);
     };
     if (D == 64)
       go(k_attention<64>);

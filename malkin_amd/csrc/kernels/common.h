@@ -45,6 +45,34 @@ __device__ __forceinline__ float reduce16_lanes(float v) {
   return v;
 }
 
+// Workgroup barrier that orders LDS only. __syncthreads() also waits for every outstanding global load of the
+// calling wave, which would turn loads issued ahead of a barrier (prefetches) into a full memory round trip.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Lane k of each 16-lane row, broadcast to the row (DPP row_newbcast, a register move). k must fold to a constant:
+// call it from fully unrolled loops. Used where every lane needs the same value: gfx950 serialises 16-byte LDS reads
+// that all lanes make at one address, and readlane would go through SGPRs.
+__device__ __forceinline__ float bcast16(float x, int k) {
+  const int v = __builtin_bit_cast(int, x);
+  int r;
+  switch (k) {
+#define MK_BCAST16_CASE(K) \
+  case K:                  \
+    r = __builtin_amdgcn_update_dpp(0, v, 0x150 + K, 0xF, 0xF, true); \
+    break;
+    MK_BCAST16_CASE(0) MK_BCAST16_CASE(1) MK_BCAST16_CASE(2) MK_BCAST16_CASE(3) MK_BCAST16_CASE(4)
+    MK_BCAST16_CASE(5) MK_BCAST16_CASE(6) MK_BCAST16_CASE(7) MK_BCAST16_CASE(8) MK_BCAST16_CASE(9)
+    MK_BCAST16_CASE(10) MK_BCAST16_CASE(11) MK_BCAST16_CASE(12) MK_BCAST16_CASE(13) MK_BCAST16_CASE(14)
+    default: MK_BCAST16_CASE(15)
+#undef MK_BCAST16_CASE
+  }
+  return __builtin_bit_cast(float, r);
+}
+
 // exp512 (kernels_avx512.cpp:186-202), one lane: max(x, -87), Cody-Waite reduction, degree-6 Taylor, scalef.
 // This is the reference's own polynomial, not a library exponential.
 __device__ __forceinline__ float exp512(float x) {

@@ -59,78 +59,132 @@ __global__ void k_quantize_i8(const float* __restrict__ x, int n, int8_t* __rest
   if (threadIdx.x == 0) d[row] = dd;
 }
 
-// rmsnorm of one row per workgroup; the sum of squares follows kern::dot_f32 (kernels_avx512.cpp:82-89): 16 lane
-// accumulators, each a sequential fma chain over the elements i = l (mod 16), then the halving tree. The row is also
-// kept transposed in LDS (lane l's elements contiguous) so each chain reads four elements per 16-byte access.
-template <bool kQuant>
-__global__ void k_rmsnorm(const float* __restrict__ x, const int32_t* __restrict__ rows_idx,
-                          const float* __restrict__ w, int n, float eps, float* __restrict__ y,
-                          BlockQ8* __restrict__ xq) {
-  extern __shared__ float4 sm4[];
-  float* row = reinterpret_cast<float*>(sm4);  // n floats
-  const int per = n / 16, tstride = ((per + 3) & ~3) + 4;  // transposed rows [16][tstride], 16-byte aligned
-  float* tr = row + n;
-  __shared__ float scale;
-  const int r = blockIdx.x;
-  const float* xr = x + (int64_t)(rows_idx ? rows_idx[r] : r) * n;
-  // 16-byte loads, all in flight together (n % 16 == 0).
-  constexpr int kMaxVec = 8;  // up to 8 x 4 x 256 = 8192 floats per row
-  float4 v4[kMaxVec], w4[kMaxVec];
+// Half of one Q8 block (16 consecutive values, h = which half) -> its BlockQ8 bytes (kernels_avx512.cpp:66-80). The
+// two halves sit on neighbouring lanes (h = lane & 1); every lane must call this, as the block max is exchanged between
+// the pair. amax is an exact max and the half sums are exact integer sums, so their order does not matter.
+__device__ __forceinline__ void quantize_half_block(const float (&v)[16], int h, bool store, BlockQ8* out) {
+  float amax = 0.0f;
 #pragma unroll
-  for (int k = 0; k < kMaxVec; ++k) {
-    const int i = 4 * (threadIdx.x + k * kT);
-    if (i < n) {
-      v4[k] = *reinterpret_cast<const float4*>(xr + i);
-      w4[k] = *reinterpret_cast<const float4*>(w + i);
+  for (int c = 0; c < 16; ++c) amax = fmaxf(amax, fabsf(v[c]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  const float d = amax / 127.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  int s = 0;
+  uint32_t packed[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int q = cvt_rne(v[4 * k + c] * id);
+      s += q;
+      word |= (uint32_t)(uint8_t)(int8_t)sat8(q) << (8 * c);
+    }
+    packed[k] = word;
+  }
+  if (!store) return;
+  uint8_t* o = reinterpret_cast<uint8_t*>(out);
+  // BlockQ8 is 8-byte aligned (40-byte blocks), so its quants take two 8-byte stores per half.
+  *reinterpret_cast<uint2*>(o + 8 + 16 * h) = make_uint2(packed[0], packed[1]);
+  *reinterpret_cast<uint2*>(o + 16 + 16 * h) = make_uint2(packed[2], packed[3]);
+  if (h == 0) {
+    *reinterpret_cast<float*>(o) = d;
+    *reinterpret_cast<int16_t*>(o + 4) = (int16_t)s;
+  } else {
+    *reinterpret_cast<int16_t*>(o + 6) = (int16_t)s;
+  }
+}
+
+// rmsnorm of one row per workgroup; the sum of squares follows kern::dot_f32 (kernels_avx512.cpp:82-89): 16 lane
+// accumulators, each a sequential fma chain over the elements i = l (mod 16), then the halving tree.
+// Thread t owns the 16-element chunks t and t + 256 of the row (n <= 8192), held in registers from one round of 16-byte
+// loads. The row goes to LDS transposed (chain lane l's elements contiguous), so a chain reads four elements per
+// 16-byte access; the chain loads the next 32 elements while it runs the current 32. A chunk is half a Q8 block, so the
+// quantized output needs one lane exchange per block.
+template <bool kQuant>
+__global__ __launch_bounds__(kT) void k_rmsnorm(const float* __restrict__ x, const int32_t* __restrict__ rows_idx,
+                                                const float* __restrict__ w, int n, float eps, float* __restrict__ y,
+                                                BlockQ8* __restrict__ xq) {
+  extern __shared__ float4 sm4[];
+  const int per = n / 16, tstride = ((per + 3) & ~3) + 4;
+  float* tr = reinterpret_cast<float*>(sm4);  // [16][tstride]; element i at (i % 16, i / 16)
+  __shared__ float scale;
+  const int r = blockIdx.x, tid = threadIdx.x;
+  const float* xr = x + (int64_t)(rows_idx ? rows_idx[r] : r) * n;
+  constexpr int kPass = 2;
+  float v[kPass][16], wv[kPass][16];
+#pragma unroll
+  for (int p = 0; p < kPass; ++p) {
+    const int c16 = tid + p * kT;
+    if (c16 < per) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float4 a = *reinterpret_cast<const float4*>(xr + 16 * c16 + 4 * k);
+        const float4 b = *reinterpret_cast<const float4*>(w + 16 * c16 + 4 * k);
+        v[p][4 * k] = a.x, v[p][4 * k + 1] = a.y, v[p][4 * k + 2] = a.z, v[p][4 * k + 3] = a.w;
+        wv[p][4 * k] = b.x, wv[p][4 * k + 1] = b.y, wv[p][4 * k + 2] = b.z, wv[p][4 * k + 3] = b.w;
+      }
     }
   }
 #pragma unroll
-  for (int k = 0; k < kMaxVec; ++k) {
-    const int i = 4 * (threadIdx.x + k * kT);
-    if (i < n) {
-      const float e[4] = {v4[k].x, v4[k].y, v4[k].z, v4[k].w};
-      *reinterpret_cast<float4*>(row + i) = v4[k];
+  for (int p = 0; p < kPass; ++p) {
+    const int c16 = tid + p * kT;
+    if (c16 < per) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) tr[((i + c) & 15) * tstride + ((i + c) >> 4)] = e[c];
+      for (int c = 0; c < 16; ++c) tr[c * tstride + c16] = v[p][c];
     }
   }
   __syncthreads();
-  if (threadIdx.x < 16) {
-    const int l = threadIdx.x;
-    const float* tl = tr + l * tstride;
+  if (tid < 16) {
+    const float* tl = tr + tid * tstride;
+    const int f4 = per / 4;
+    constexpr int B = 8;
     float acc = 0.0f;
-    int i = 0;
-    for (; i + 4 <= per; i += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(tl + i);
-      acc = fma_(v.x, v.x, acc);
-      acc = fma_(v.y, v.y, acc);
-      acc = fma_(v.z, v.z, acc);
-      acc = fma_(v.w, v.w, acc);
+    float4 cur[B];
+#pragma unroll
+    for (int k = 0; k < B; ++k)
+      if (k < f4) cur[k] = reinterpret_cast<const float4*>(tl)[k];
+    for (int j = 0; j < f4; j += B) {
+      float4 nxt[B];
+#pragma unroll
+      for (int k = 0; k < B; ++k)
+        if (j + B + k < f4) nxt[k] = reinterpret_cast<const float4*>(tl)[j + B + k];
+#pragma unroll
+      for (int k = 0; k < B; ++k) {
+        if (j + k < f4) {
+          acc = fma_(cur[k].x, cur[k].x, acc);
+          acc = fma_(cur[k].y, cur[k].y, acc);
+          acc = fma_(cur[k].z, cur[k].z, acc);
+          acc = fma_(cur[k].w, cur[k].w, acc);
+        }
+        cur[k] = nxt[k];
+      }
     }
-    for (; i < per; ++i) acc = fma_(tl[i], tl[i], acc);
+    for (int i = 4 * f4; i < per; ++i) acc = fma_(tl[i], tl[i], acc);
     acc = reduce16_lanes(acc);
-    if (l == 0) scale = 1.0f / sqrtf(acc / (float)n + eps);
+    if (tid == 0) scale = 1.0f / sqrtf(acc / (float)n + eps);
   }
   __syncthreads();
   const float s = scale;
-  // y = x * s * w from the registers loaded above: thread handles elements 4 (tid + k kT) .. + 3.
 #pragma unroll
-  for (int k = 0; k < kMaxVec; ++k) {
-    const int i = 4 * (threadIdx.x + k * kT);
-    if (i >= n) break;
-    const float4 yv = make_float4(v4[k].x * s * w4[k].x, v4[k].y * s * w4[k].y, v4[k].z * s * w4[k].z,
-                                  v4[k].w * s * w4[k].w);
+  for (int p = 0; p < kPass; ++p) {
+    const int c16 = tid + p * kT;
+    if (p * kT >= per) break;  // uniform: no chunk of this pass is in the row
+    float yv[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) yv[c] = v[p][c] * s * wv[p][c];
     if (!kQuant) {
-      *reinterpret_cast<float4*>(y + (int64_t)r * n + i) = yv;
+      if (c16 < per) {
+        float* yr = y + (int64_t)r * n + 16 * c16;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          *reinterpret_cast<float4*>(yr + 4 * k) = make_float4(yv[4 * k], yv[4 * k + 1], yv[4 * k + 2], yv[4 * k + 3]);
+      }
     } else {
-      *reinterpret_cast<float4*>(row + i) = yv;
+      // n % 32 == 0, so both halves of a block are in the row or neither is.
+      quantize_half_block(yv, c16 & 1, c16 < per, xq + (int64_t)r * (n / 32) + c16 / 2);
     }
   }
-  if (!kQuant) return;
-  __syncthreads();
-  // Quantize: element i on lane i % 32 of a half wave.
-  for (int i = threadIdx.x; i < n; i += kT)
-    quantize_block_lanes(row[i], i & 31, xq + (int64_t)r * (n / 32) + i / 32);
 }
 
 __global__ void k_silu_mul(int64_t n, float* __restrict__ g, const float* __restrict__ u) {
@@ -234,11 +288,11 @@ void dequantize_rows(hipStream_t s, int type, const void* src, size_t row_bytes,
   check_launch("dequantize_rows");
 }
 
-static size_t rmsnorm_lds(int n) { return ((size_t)n + 16 * ((((size_t)n / 16 + 3) & ~(size_t)3) + 4)) * sizeof(float); }
+static size_t rmsnorm_lds(int n) { return 16 * ((((size_t)n / 16 + 3) & ~(size_t)3) + 4) * sizeof(float); }
 
 void rmsnorm(hipStream_t s, const float* x, const float* w, int rows, int n, float eps, float* y) {
   if (rows <= 0) return;
-  require(n % 16 == 0 && n <= 8192 && rmsnorm_lds(n) <= 64 * 1024, "rmsnorm: n must be a multiple of 16, <= 7936");
+  require(n % 16 == 0 && n <= 8192, "rmsnorm: n must be a multiple of 16, <= 8192");
   hipLaunchKernelGGL(k_rmsnorm<false>, dim3(rows), dim3(kT), rmsnorm_lds(n), s, x, nullptr, w, n, eps, y, nullptr);
   check_launch("rmsnorm");
 }
@@ -246,7 +300,7 @@ void rmsnorm(hipStream_t s, const float* x, const float* w, int rows, int n, flo
 void rmsnorm_q8(hipStream_t s, const float* x, const int32_t* rows_idx, const float* w, int rows, int n, float eps,
                 BlockQ8* xq) {
   if (rows <= 0) return;
-  require(n % 32 == 0 && n <= 8192 && rmsnorm_lds(n) <= 64 * 1024, "rmsnorm_q8: n must be a multiple of 32, <= 7936");
+  require(n % 32 == 0 && n <= 8192, "rmsnorm_q8: n must be a multiple of 32, <= 8192");
   hipLaunchKernelGGL(k_rmsnorm<true>, dim3(rows), dim3(kT), rmsnorm_lds(n), s, x, rows_idx, w, n, eps, nullptr, xq);
   check_launch("rmsnorm_q8");
 }

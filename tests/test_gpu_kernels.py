@@ -87,20 +87,25 @@ def test_silu(mk, golden, oracle):
     assert np.array_equal(out.download(np.uint8), oracle.quantize_row_q8(exp).view(np.uint8).reshape(-1))
 
 
-def test_rmsnorm(mk, oracle):
-    rng = np.random.default_rng(3)
-    rows, n = 7, 4096
+@pytest.mark.parametrize("n", [16, 64, 2560, 4096, 5120, 8176, 8192])
+def test_rmsnorm(mk, oracle, n):
+    rng = np.random.default_rng(3 + n)
+    rows = 7
     x = (rng.standard_normal((rows, n)) * 5).astype(np.float32)
+    x[2] = 0.0  # zero row: scale from eps alone, Q8 blocks with d = 0
+    x[4, : n // 2] *= 1e-30  # tiny values next to ordinary ones
     w = rng.uniform(0.5, 1.5, n).astype(np.float32)
     dx, dw = mk.to_device(x), mk.to_device(w)
     y = mk.alloc(x.nbytes)
     mk_.check(L().mk_rmsnorm(mk.h, dx.ptr, dw.ptr, rows, n, ctypes.c_float(1e-6), y.ptr))
     exp = np.stack([oracle.rmsnorm(r, w, 1e-6) for r in x])
     assert np.array_equal(bits(y.download(np.float32).reshape(rows, n)), bits(exp))
-    idx = np.array([6, 0, 3], np.int32)
+    if n % 32:
+        return
+    idx = np.array([6, 0, 2, 4, 3], np.int32)
     didx = mk.to_device(idx)
-    out = mk.alloc(3 * n // 32 * 40)
-    mk_.check(L().mk_rmsnorm_q8(mk.h, dx.ptr, didx.ptr, dw.ptr, 3, n, ctypes.c_float(1e-6), out.ptr))
+    out = mk.alloc(len(idx) * n // 32 * 40)
+    mk_.check(L().mk_rmsnorm_q8(mk.h, dx.ptr, didx.ptr, dw.ptr, len(idx), n, ctypes.c_float(1e-6), out.ptr))
     assert np.array_equal(out.download(np.uint8), oracle.quantize_row_q8(exp[idx]).view(np.uint8).reshape(-1))
 
 
