@@ -4,11 +4,15 @@
 // The reference accumulates each output as one sequential fp32 chain over the row's blocks:
 //   acc = fma(float(int dot of block b), scale_w(b) * scale_x(b), acc),  b = 0, 1, 2, ...
 // The int dots are exact, so they can be computed in any order and in parallel; only the chain is sequential.
-// A workgroup owns R rows x all columns:
-//   phase 1 (all 256 threads): stream the rows' quants (128-byte-coalesced planes), compute every (row, unit, token)
-//            int dot with v_dot4_i32_i8 and its per-unit float terms, park them in LDS;
-//   phase 2 (R * NT lanes):   run each output's chain over the parked terms in block order.
-// Columns are processed in LDS-sized chunks; the chain state stays in the phase-2 lanes' registers across chunks.
+//
+// A workgroup owns R-row groups g = blockIdx.x, blockIdx.x + gridDim.x, ... (the grid is what fits on the GPU at
+// once) and streams them, all columns of one group after another, as one sequence of chunks of kChunk units:
+//   waves 1-3 (workers): for chunk c, the int dots of every (row, unit, token) with v_dot4_i32_i8 and their per-unit
+//            float terms, parked in LDS slot c % 2; each worker holds two chunks of weights in registers (A/B), so
+//            chunk c + 2 is in flight while chunk c is computed;
+//   wave 0 (chains): the R * NT sequential chains over chunk c - 1 while the workers compute chunk c.
+// Barriers order LDS only (lds_barrier), so the weight loads stay in flight across them. The activation rows of the
+// workgroup's tokens are staged in LDS once, as BlockQ8.
 #include "ctx.h"
 #include "ops.h"
 
@@ -16,8 +20,7 @@ namespace mk {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;  // rows x units in flight per thread in phase 1
-constexpr size_t kLdsBudget = 48 * 1024;
+constexpr int kGemvLdsMax = 128 * 1024;
 
 // Q8 blocks per unit and parked floats per (unit, token, row).
 template <int T>
@@ -35,13 +38,20 @@ struct Unit<kQ6_K> {
   static constexpr int q8 = 1, e = 4;
 };
 
-__device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int& sc, int& m) {  // kernels.h:18-26
+// kernels.h:18-26 over the 12 packed scale bytes held in three words (q0 = bytes 0..3, ...). Byte selection by
+// shifts and selects: indexing the bytes of a register-held header with a runtime j would place it in scratch.
+__device__ __forceinline__ int scale_byte(uint32_t q0, uint32_t q1, uint32_t q2, int i) {
+  const uint32_t w = i < 4 ? q0 : (i < 8 ? q1 : q2);
+  return (int)((w >> (8 * (i & 3))) & 0xFFu);
+}
+__device__ __forceinline__ void scale_min_k4(int j, uint32_t q0, uint32_t q1, uint32_t q2, int& sc, int& m) {
   if (j < 4) {
-    sc = q[j] & 63;
-    m = q[j + 4] & 63;
+    sc = scale_byte(q0, q1, q2, j) & 63;
+    m = scale_byte(q0, q1, q2, j + 4) & 63;
   } else {
-    sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
-    m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    const int hi = scale_byte(q0, q1, q2, j + 4);
+    sc = (hi & 0xF) | ((scale_byte(q0, q1, q2, j - 4) >> 6) << 4);
+    m = (hi >> 4) | ((scale_byte(q0, q1, q2, j) >> 6) << 4);
   }
 }
 
@@ -54,7 +64,7 @@ struct Raw {
 };
 
 template <int TYPE>
-__device__ __forceinline__ Raw load_unit(const uint8_t* __restrict__ W, int64_t rows, int64_t cols, int64_t g, int rr,
+__device__ __forceinline__ Raw load_unit(const uint8_t* W, int64_t rows, int64_t cols, int64_t g, int rr,
                                          int64_t u) {
   Raw w{};
   if constexpr (TYPE == kQ8_0) {
@@ -103,210 +113,375 @@ __device__ __forceinline__ int xs0(const int* xq) { return (int)(int16_t)(xq[1] 
 __device__ __forceinline__ int xs1(const int* xq) { return (int)(int16_t)((uint32_t)xq[1] >> 16); }
 
 template <int TYPE, bool WIDE, int R, int NT>
-__global__ __launch_bounds__(kThreads) void k_gemv(const uint8_t* __restrict__ W, int64_t rows, int64_t cols,
+struct GemvCfg {
+  static constexpr int UQ8 = Unit<TYPE>::q8;
+  static constexpr int E = (TYPE == kQ6_K && WIDE) ? 1 : Unit<TYPE>::e;
+  static constexpr int kWorkers = kThreads - 64;
+  // Units per pipeline step: the (row, unit) pairs of a chunk spread evenly over the workers.
+  static constexpr int kChunk = R == 8 ? (NT <= 2 ? 96 : NT == 4 ? 48 : 24) : 24;
+  static constexpr int kP = kChunk * R / kWorkers;  // pairs per worker per chunk
+  static_assert(kChunk * R % kWorkers == 0, "chunk must split evenly over the workers");
+  static_assert(R * NT <= 64, "one chain per lane of wave 0");
+  // Units the chain reads per group; it runs whole groups, over zero terms past the last unit.
+  static constexpr int kG = (TYPE == kQ4_K || (TYPE == kQ6_K && !WIDE)) ? 4 : 8;
+  static_assert(kChunk % kG == 0, "groups tile the chunk");
+  // Term slot: per chain lane (token t, row r) the chunk's units in order, E floats each, plus one group that the
+  // chain reads ahead past the end, plus 4 floats against bank conflicts (rows stay 16-byte aligned). Q4_K mins:
+  // per row, 2 floats per unit, laid out the same way.
+  static constexpr int kLane = (kChunk + kG) * E + 4;
+  static constexpr int kSlot = NT * R * kLane;
+  static constexpr int kMnRow = TYPE == kQ4_K ? (kChunk + kG) * 2 + 4 : 0;
+  static constexpr int kMnSlot = R * kMnRow;
+  static constexpr bool kXsc = TYPE == kQ4_K || (TYPE == kQ6_K && WIDE);  // per-block activation scale terms
+  __host__ __device__ static int64_t xsc_row(int64_t nq8) { return nq8 + 16; }  // + zero pad: groups read past the end
+  static size_t lds_bytes(int64_t cols) {
+    const int64_t nq8 = cols / 32;
+    return (size_t)NT * nq8 * 40 + 2 * (size_t)(kSlot + kMnSlot) * 4 + (kXsc ? (size_t)NT * xsc_row(nq8) * 4 : 0);
+  }
+};
+
+template <int TYPE, bool WIDE, int R, int NT>
+__global__ __launch_bounds__(kThreads) void k_gemv(const uint8_t* W, int64_t rows, int64_t cols,
                                                    const BlockQ8* __restrict__ x, int n, float* __restrict__ y,
-                                                   int64_t ys, int accumulate, int chunk) {
-  constexpr int UQ8 = Unit<TYPE>::q8;
-  constexpr int E = (TYPE == kQ6_K && WIDE) ? 1 : Unit<TYPE>::e;
+                                                   int64_t ys, int accumulate) {
+  using C = GemvCfg<TYPE, WIDE, R, NT>;
+  constexpr int UQ8 = C::UQ8, E = C::E, kChunk = C::kChunk, kP = C::kP, kG = C::kG;
   extern __shared__ int smem[];
-  const int64_t nq8 = cols / 32, nu = nq8 / UQ8;
-  const int64_t g0 = (int64_t)blockIdx.x * (R / 8);
+  const int nq8 = (int)(cols / 32), nu = nq8 / UQ8;
   const int t0 = blockIdx.y * NT;
   const int nt = min(NT, n - t0);
   const int tid = threadIdx.x;
+  const int nc = (nu + kChunk - 1) / kChunk;                // chunks per row group
+  const int ngroups = (int)(rows / R);
+  const int mine = (ngroups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;  // row groups of this WG
+  const int nq = mine * nc;                                  // chunks of this workgroup, in order
+  // Chunk q of this workgroup: row group rg(q) (in 8-row groups g0(q)), chunk q % nc of its columns.
+  auto rg = [&](int q) { return (int)blockIdx.x + (q / nc) * (int)gridDim.x; };
 
-  int* xs = smem;                                                  // [NT][chunk * UQ8][10]
-  float* res = reinterpret_cast<float*>(xs + NT * chunk * UQ8 * 10);  // [chunk][NT][R][E]
-  float* mnv = res + (size_t)chunk * NT * R * E;                   // Q4_K: [chunk][R][2]
+  int* xs = smem;                                                   // [NT][nq8][10]: BlockQ8 rows
+  float* res = reinterpret_cast<float*>(xs + NT * nq8 * 10);        // [2][kSlot]
+  float* mnv = res + 2 * C::kSlot;                                  // Q4_K: [2][kMnSlot]
+  float* xsc = mnv + 2 * C::kMnSlot;                                // [NT][xsc_row]: Q4_K dx (s0 + s1), Q6_K wide dx
+  const int xrow = (int)C::xsc_row(nq8);
 
+  // Waves 1-3 are the workers: pair f = wi + k * kWorkers of a chunk is (unit f / R, row f % R), and two chunks are
+  // in flight (register sets A/B). Every wave issues the same sequence of loads, never predicated: wave 0 repeats
+  // wave 1's (cache hits, unused), and past the last chunk or unit a load re-reads the last valid one. The compiler's
+  // wait counts are then exact on every path, so waiting for chunk c never waits for chunk c + 1.
+  const bool worker = tid >= 64;
+  const int wi = worker ? tid - 64 : tid;
+  Raw ra[kP], rb[kP];
+  auto load = [&](Raw(&r)[kP], int q) {
+    const int qq = min(q, nq - 1);
+    const int64_t g0 = (int64_t)rg(qq) * (R / 8);
+    const int cc = qq % nc;
+#pragma unroll
+    for (int k = 0; k < kP; ++k) {
+      const int f = wi + k * C::kWorkers;
+      const int u = min(cc * kChunk + f / R, nu - 1);
+      r[k] = load_unit<TYPE>(W, rows, cols, g0 + (f % R) / 8, (f % R) % 8, u);
+    }
+  };
+
+  // Activation rows: 8-byte loads (BlockQ8 is 8-byte aligned), a pass of kStage loads per thread at a time. The
+  // first pass is issued before the first two weight chunks, so storing it to LDS waits for it alone (loads
+  // complete in issue order).
+  constexpr int kStage = 8;
+  const int words = nq8 * 5;  // 8-byte words per token
+  const int total = nt * words;
+  auto stage_load = [&](uint2(&v)[kStage], int i0) {
+#pragma unroll
+    for (int k = 0; k < kStage; ++k) {
+      const int i = i0 + k * kThreads;
+      if (i < total) {
+        const int t = i / words;
+        v[k] = reinterpret_cast<const uint2*>(x + (int64_t)(t0 + t) * nq8)[i - t * words];
+      }
+    }
+  };
+  auto stage_store = [&](const uint2(&v)[kStage], int i0) {
+#pragma unroll
+    for (int k = 0; k < kStage; ++k) {
+      const int i = i0 + k * kThreads;
+      if (i < total) {
+        const int t = i / words;
+        reinterpret_cast<uint2*>(xs + t * nq8 * 10)[i - t * words] = v[k];
+      }
+    }
+  };
+  {
+    uint2 xv[kStage];
+    stage_load(xv, tid);
+    load(ra, 0);
+    load(rb, 1);
+    stage_store(xv, tid);
+  }
+  for (int i0 = tid + kThreads * kStage; i0 < total; i0 += kThreads * kStage) {
+    uint2 v[kStage];
+    stage_load(v, i0);
+    stage_store(v, i0);
+  }
+  lds_barrier();
+  if constexpr (C::kXsc) {
+    for (int i = tid; i < NT * xrow; i += kThreads) {
+      const int t = i / xrow, b = i - t * xrow;
+      float v = 0.0f;
+      if (t < nt && b < nq8) {
+        const int* xq = xs + (t * nq8 + b) * 10;
+        v = TYPE == kQ4_K ? xd(xq) * (float)(xs0(xq) + xs1(xq)) : xd(xq);
+      }
+      xsc[i] = v;
+    }
+    lds_barrier();
+  }
+
+  // Phase 1 of chunk c for one register set; units past the last write zero terms.
+  auto dots = [&](const Raw(&raw)[kP], int q) {
+    const int c = q % nc;
+    float* slot = res + (q & 1) * C::kSlot;
+#pragma unroll
+    for (int k = 0; k < kP; ++k) {
+      const int f = wi + k * C::kWorkers;
+      const int ul = f / R, r = f % R;
+      const int u = c * kChunk + ul;
+      const bool live = u < nu;
+      const Raw& w = raw[k];
+      if constexpr (TYPE == kQ8_0) {
+        const float dw = half_to_float((uint16_t)w.s);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          if (t < nt) {
+            const int* xq = xs + (t * nq8 + (live ? u : 0)) * 10;
+            float* e = slot + (t * R + r) * C::kLane + ul * E;
+            *reinterpret_cast<float2*>(e) =
+                live ? make_float2((float)dot8(w.a, w.b, xq), dw * xd(xq)) : make_float2(0.0f, 0.0f);
+          }
+        }
+      } else if constexpr (TYPE == kQ4_K) {
+        const int j0 = (u & 3) * 2;  // sub-blocks j0 (low nibbles) and j0 + 1 (high nibbles)
+        const float d = half_to_float((uint16_t)(w.h.x & 0xFFFF)), dmin = half_to_float((uint16_t)(w.h.x >> 16));
+        int sc0, m0, sc1, m1;
+        scale_min_k4(j0, w.h.y, w.h.z, w.h.w, sc0, m0);
+        scale_min_k4(j0 + 1, w.h.y, w.h.z, w.h.w, sc1, m1);
+        const float fsc0 = d * (float)sc0, fsc1 = d * (float)sc1;
+        float* mn = mnv + (q & 1) * C::kMnSlot + r * C::kMnRow + ul * 2;
+        *reinterpret_cast<float2*>(mn) = live ? make_float2(dmin * (float)m0, dmin * (float)m1) : make_float2(0.0f, 0.0f);
+        const uint32_t wd[8] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w};
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          if (t < nt) {
+            const int* x0 = xs + (t * nq8 + (live ? u : 0) * 2) * 10;
+            const int* x1 = x0 + 10;
+            int a0 = 0, a1 = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              a0 = dot4((int)(wd[j] & 0x0F0F0F0Fu), x0[2 + j], a0);
+              a1 = dot4((int)((wd[j] >> 4) & 0x0F0F0F0Fu), x1[2 + j], a1);
+            }
+            float* e = slot + (t * R + r) * C::kLane + ul * E;
+            *reinterpret_cast<float4*>(e) = live ? make_float4((float)a0, fsc0 * xd(x0), (float)a1, fsc1 * xd(x1))
+                                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          }
+        }
+      } else {  // Q6_K
+        const uint32_t nw[4] = {w.a.x, w.a.y, w.a.z, w.a.w};
+        const uint32_t hw[2] = {w.b.x, w.b.y};
+        const float d = half_to_float((uint16_t)w.h.y);
+        const float dsc0 = d * (float)(int8_t)(w.h.x & 0xFF), dsc1 = d * (float)(int8_t)((w.h.x >> 8) & 0xFF);
+        int qv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t lo = j < 4 ? (nw[j] & 0x0F0F0F0Fu) : ((nw[j - 4] >> 4) & 0x0F0F0F0Fu);
+          const uint32_t hi = ((hw[j >> 2] >> (2 * (j & 3))) & 0x03030303u) << 4;
+          qv[j] = (int)(lo | hi);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          if (t < nt) {
+            const int* xq = xs + (t * nq8 + (live ? u : 0)) * 10;
+            int a0 = 0, a1 = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a0 = dot4(qv[j], xq[2 + j], a0);
+#pragma unroll
+            for (int j = 4; j < 8; ++j) a1 = dot4(qv[j], xq[2 + j], a1);
+            a0 -= 32 * xs0(xq);
+            a1 -= 32 * xs1(xq);
+            float* e = slot + (t * R + r) * C::kLane + ul * E;
+            if constexpr (WIDE) {
+              e[0] = live ? fma_((float)a1, dsc1, (float)a0 * dsc0) : 0.0f;
+            } else {
+              *reinterpret_cast<float4*>(e) = live ? make_float4((float)a0, dsc0 * xd(xq), (float)a1, dsc1 * xd(xq))
+                                                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+          }
+        }
+      }
+    }
+  };
+
+  // Phase 2 of chunk c: lane (ct, cr) runs the chain of row cr, token ct over the chunk's units in order, kG units
+  // per group read with 16-byte LDS loads, the next group in flight while the current one runs. Groups run whole:
+  // units past the last have zero terms, and fma(0, 0, acc) == acc.
   const int cr = tid % R, ct = tid / R;
-  const bool chain = tid < R * NT && ct < nt;
+  const bool chain_lane = tid < R * NT && ct < nt;
   float acc = 0.0f;
+  struct Terms {
+    float4 e[kG * E / 4 > 0 ? kG * E / 4 : 1];
+    float4 m[TYPE == kQ4_K ? kG * 2 / 4 : 1];
+    float4 s[C::kXsc ? (TYPE == kQ4_K ? kG * 2 / 4 : kG / 4) : 1];
+  };
+  auto fetch = [&](Terms& T, int q, int ul0) {
+    const int c = q % nc;
+    const float4* e = reinterpret_cast<const float4*>(res + (q & 1) * C::kSlot + (ct * R + cr) * C::kLane + ul0 * E);
+#pragma unroll
+    for (int i = 0; i < kG * E / 4; ++i) T.e[i] = e[i];
+    if constexpr (TYPE == kQ4_K) {
+      const float4* m = reinterpret_cast<const float4*>(mnv + (q & 1) * C::kMnSlot + cr * C::kMnRow + ul0 * 2);
+      const float4* q = reinterpret_cast<const float4*>(xsc + ct * xrow + (c * kChunk + ul0) * 2);
+#pragma unroll
+      for (int i = 0; i < kG * 2 / 4; ++i) T.m[i] = m[i], T.s[i] = q[i];
+    } else if constexpr (C::kXsc) {
+      const float4* q = reinterpret_cast<const float4*>(xsc + ct * xrow + c * kChunk + ul0);
+#pragma unroll
+      for (int i = 0; i < kG / 4; ++i) T.s[i] = q[i];
+    }
+  };
+  auto step = [&](const Terms& T) {
+    const float* e = reinterpret_cast<const float*>(T.e);
+    const float* m = reinterpret_cast<const float*>(T.m);
+    const float* q = reinterpret_cast<const float*>(T.s);
+#pragma unroll
+    for (int i = 0; i < kG; ++i) {
+      if constexpr (TYPE == kQ8_0) {
+        acc = fma_(e[2 * i], e[2 * i + 1], acc);
+      } else if constexpr (TYPE == kQ4_K) {
+        acc = fma_(e[4 * i], e[4 * i + 1], acc);
+        acc = fma_(-m[2 * i], q[2 * i], acc);
+        acc = fma_(e[4 * i + 2], e[4 * i + 3], acc);
+        acc = fma_(-m[2 * i + 1], q[2 * i + 1], acc);
+      } else if constexpr (WIDE) {
+        acc = fma_(e[i], q[i], acc);
+      } else {
+        acc = fma_(e[4 * i], e[4 * i + 1], acc);
+        acc = fma_(e[4 * i + 2], e[4 * i + 3], acc);
+      }
+    }
+  };
+  // Chain over chunk q; after a row group's last chunk its results are stored and the chains restart.
+  auto chain = [&](int q) {
+    if (!chain_lane) return;
+    const int c = q % nc;
+    const int cn = min(kChunk, nu - c * kChunk);
+    Terms A, B;
+    fetch(A, q, 0);
+    // The fetches are never predicated (the last one reads the padding group): the wait before each group then
+    // counts exactly the reads issued after it.
+    // Scheduling barriers keep each fetch ahead of the previous group's fmas.
+    for (int ul0 = 0;;) {
+      fetch(B, q, ul0 + kG);
+      __builtin_amdgcn_sched_barrier(0);
+      step(A);
+      __builtin_amdgcn_sched_barrier(0);
+      if ((ul0 += kG) >= cn) break;
+      fetch(A, q, ul0 + kG);
+      __builtin_amdgcn_sched_barrier(0);
+      step(B);
+      __builtin_amdgcn_sched_barrier(0);
+      if ((ul0 += kG) >= cn) break;
+    }
+    if (c == nc - 1) {
+      float* o = y + (int64_t)(t0 + ct) * ys + (int64_t)rg(q) * R + cr;
+      *o = accumulate ? *o + acc : acc;
+      acc = 0.0f;
+    }
+  };
 
-  for (int64_t c0 = 0; c0 < nu; c0 += chunk) {
-    const int cn = (int)min<int64_t>(chunk, nu - c0);
-    // The first group of this chunk's weight loads goes out before the activations are staged, so HBM latency
-    // overlaps the staging and the barrier.
-    Raw raw[kUnroll];
-#pragma unroll
-    for (int k = 0; k < kUnroll; ++k) {
-      const int f = tid + k * kThreads;
-      if (f < R * cn) raw[k] = load_unit<TYPE>(W, rows, cols, g0 + (f % R) / 8, (f % R) % 8, c0 + f / R);
+  // The chains are latency-bound (one dependent fma after another) and share their SIMD with other workgroups'
+  // workers: wave 0 takes issue priority over them.
+  if (!worker) __builtin_amdgcn_s_setprio(2);
+  for (int q = 0; q < nq; q += 2) {
+    if (worker)
+      dots(ra, q);
+    else if (q > 0)
+      chain(q - 1);
+    load(ra, q + 2);
+    lds_barrier();
+    if (q + 1 < nq) {
+      if (worker)
+        dots(rb, q + 1);
+      else
+        chain(q);
+      load(rb, q + 3);
+      lds_barrier();
     }
-    // Stage this chunk's activation blocks: 8-byte loads (BlockQ8 is 8-byte aligned), all issued before any store.
-    const int pairs = cn * UQ8 * 5;  // 8-byte words per token
-    constexpr int kStage = 8;
-    for (int i0 = tid; i0 < nt * pairs; i0 += kThreads * kStage) {
-      uint2 v[kStage];
-#pragma unroll
-      for (int k = 0; k < kStage; ++k) {
-        const int i = i0 + k * kThreads;
-        if (i < nt * pairs) {
-          const int t = i / pairs, rem = i % pairs;
-          v[k] = reinterpret_cast<const uint2*>(x + (int64_t)(t0 + t) * nq8 + c0 * UQ8)[rem];
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < kStage; ++k) {
-        const int i = i0 + k * kThreads;
-        if (i < nt * pairs) {
-          const int t = i / pairs, rem = i % pairs;
-          reinterpret_cast<uint2*>(xs + t * chunk * UQ8 * 10)[rem] = v[k];
-        }
-      }
-    }
-    __syncthreads();
-
-    // Phase 1: int dots and per-unit float terms.
-    for (int f0 = tid; f0 < R * cn; f0 += kThreads * kUnroll) {
-      if (f0 != tid) {
-#pragma unroll
-        for (int k = 0; k < kUnroll; ++k) {
-          const int f = f0 + k * kThreads;
-          if (f < R * cn) raw[k] = load_unit<TYPE>(W, rows, cols, g0 + (f % R) / 8, (f % R) % 8, c0 + f / R);
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < kUnroll; ++k) {
-        const int f = f0 + k * kThreads;
-        if (f >= R * cn) break;
-        const int u = f / R, r = f % R;
-        const Raw& w = raw[k];
-        if constexpr (TYPE == kQ8_0) {
-          const float dw = half_to_float((uint16_t)w.s);
-#pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            if (t < nt) {
-              const int* xq = xs + (t * chunk + u) * 10;
-              float* e = res + (((size_t)u * NT + t) * R + r) * E;
-              e[0] = (float)dot8(w.a, w.b, xq);
-              e[1] = dw * xd(xq);
-            }
-          }
-        } else if constexpr (TYPE == kQ4_K) {
-          const int j0 = (int)((c0 + u) & 3) * 2;  // sub-blocks j0 (low nibbles) and j0 + 1 (high nibbles)
-          const uint8_t* hb = reinterpret_cast<const uint8_t*>(&w.h);
-          const float d = half_to_float((uint16_t)(w.h.x & 0xFFFF)), dmin = half_to_float((uint16_t)(w.h.x >> 16));
-          int sc0, m0, sc1, m1;
-          scale_min_k4(j0, hb + 4, sc0, m0);
-          scale_min_k4(j0 + 1, hb + 4, sc1, m1);
-          const float fsc0 = d * (float)sc0, fsc1 = d * (float)sc1;
-          float* mn = mnv + ((size_t)u * R + r) * 2;
-          mn[0] = dmin * (float)m0;
-          mn[1] = dmin * (float)m1;
-          const uint32_t wd[8] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w};
-#pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            if (t < nt) {
-              const int* x0 = xs + (t * chunk + u) * UQ8 * 10;
-              const int* x1 = x0 + 10;
-              int a0 = 0, a1 = 0;
-#pragma unroll
-              for (int j = 0; j < 8; ++j) {
-                a0 = dot4((int)(wd[j] & 0x0F0F0F0Fu), x0[2 + j], a0);
-                a1 = dot4((int)((wd[j] >> 4) & 0x0F0F0F0Fu), x1[2 + j], a1);
-              }
-              float* e = res + (((size_t)u * NT + t) * R + r) * E;
-              e[0] = (float)a0;
-              e[1] = fsc0 * xd(x0);
-              e[2] = (float)a1;
-              e[3] = fsc1 * xd(x1);
-            }
-          }
-        } else {  // Q6_K
-          const uint32_t nw[4] = {w.a.x, w.a.y, w.a.z, w.a.w};
-          const uint32_t hw[2] = {w.b.x, w.b.y};
-          const float d = half_to_float((uint16_t)w.h.y);
-          const float dsc0 = d * (float)(int8_t)(w.h.x & 0xFF), dsc1 = d * (float)(int8_t)((w.h.x >> 8) & 0xFF);
-          int qv[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const uint32_t lo = j < 4 ? (nw[j] & 0x0F0F0F0Fu) : ((nw[j - 4] >> 4) & 0x0F0F0F0Fu);
-            const uint32_t hi = ((hw[j >> 2] >> (2 * (j & 3))) & 0x03030303u) << 4;
-            qv[j] = (int)(lo | hi);
-          }
-#pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            if (t < nt) {
-              const int* xq = xs + (t * chunk + u) * 10;
-              int a0 = 0, a1 = 0;
-#pragma unroll
-              for (int j = 0; j < 4; ++j) a0 = dot4(qv[j], xq[2 + j], a0);
-#pragma unroll
-              for (int j = 4; j < 8; ++j) a1 = dot4(qv[j], xq[2 + j], a1);
-              a0 -= 32 * xs0(xq);
-              a1 -= 32 * xs1(xq);
-              float* e = res + (((size_t)u * NT + t) * R + r) * E;
-              if constexpr (WIDE) {
-                e[0] = fma_((float)a1, dsc1, (float)a0 * dsc0);
-              } else {
-                e[0] = (float)a0;
-                e[1] = dsc0 * xd(xq);
-                e[2] = (float)a1;
-                e[3] = dsc1 * xd(xq);
-              }
-            }
-          }
-        }
-      }
-    }
-    __syncthreads();
-
-    // Phase 2: the sequential chains, in block order.
-    if (chain) {
-#pragma unroll 8
-      for (int u = 0; u < cn; ++u) {
-        const float* e = res + (((size_t)u * NT + ct) * R + cr) * E;
-        if constexpr (TYPE == kQ8_0) {
-          acc = fma_(e[0], e[1], acc);
-        } else if constexpr (TYPE == kQ4_K) {
-          const float* mn = mnv + ((size_t)u * R + cr) * 2;
-          const int* x0 = xs + (ct * chunk + u) * UQ8 * 10;
-          const int* x1 = x0 + 10;
-          const float dsx0 = xd(x0) * (float)(xs0(x0) + xs1(x0));
-          const float dsx1 = xd(x1) * (float)(xs0(x1) + xs1(x1));
-          acc = fma_(e[0], e[1], acc);
-          acc = fma_(-mn[0], dsx0, acc);
-          acc = fma_(e[2], e[3], acc);
-          acc = fma_(-mn[1], dsx1, acc);
-        } else if constexpr (WIDE) {
-          acc = fma_(e[0], xd(xs + (ct * chunk + u) * 10), acc);
-        } else {
-          acc = fma_(e[0], e[1], acc);
-          acc = fma_(e[2], e[3], acc);
-        }
-      }
-    }
-    __syncthreads();
   }
-  if (chain) {
-    float* o = y + (int64_t)(t0 + ct) * ys + (int64_t)blockIdx.x * R + cr;
-    *o = accumulate ? *o + acc : acc;
+  chain(nq - 1);
+}
+
+// Compute units of the current device (queried once: the library runs one device per process).
+int device_cus() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0;
+    check(hipGetDevice(&dev), "hipGetDevice");
+    check(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
   }
+  return n;
+}
+
+// Resident workgroups per CU of a kernel at a given dynamic LDS size (cached per size).
+template <typename K>
+int resident_per_cu(K kernel, size_t lds) {
+  static size_t keys[16] = {};
+  static int vals[16] = {};
+  for (int i = 0; i < 16 && keys[i]; ++i)
+    if (keys[i] == lds + 1) return vals[i];
+  int blocks = 0;
+  check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, kThreads, lds),
+        "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+  blocks = blocks > 0 ? blocks : 1;
+  for (int i = 0; i < 16; ++i)
+    if (!keys[i]) {
+      keys[i] = lds + 1;
+      vals[i] = blocks;
+      break;
+    }
+  return blocks;
 }
 
 template <int TYPE, bool WIDE, int R, int NT>
 void launch(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y, int64_t ys,
             bool accumulate) {
-  constexpr int UQ8 = Unit<TYPE>::q8;
-  constexpr int E = (TYPE == kQ6_K && WIDE) ? 1 : Unit<TYPE>::e;
-  const size_t per_unit = (size_t)NT * UQ8 * 40 + (size_t)NT * R * E * 4 + (TYPE == kQ4_K ? (size_t)R * 8 : 0);
-  const int64_t nu = cols / 32 / UQ8;
-  const int chunk = (int)std::min<int64_t>(nu, (int64_t)(kLdsBudget / per_unit));
-  const size_t lds = per_unit * chunk;
-  const dim3 grid((unsigned)(rows / R), (unsigned)((n + NT - 1) / NT));
+  using C = GemvCfg<TYPE, WIDE, R, NT>;
+  const size_t lds = C::lds_bytes(cols);
+  static bool attr = false;  // per instantiation: allow more than the default 64 KB of dynamic LDS
+  if (!attr) {
+    check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv<TYPE, WIDE, R, NT>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kGemvLdsMax),
+          "hipFuncSetAttribute");
+    attr = true;
+  }
+  // Persistent over row groups: as many workgroups as are resident at once (per token group), each streaming its
+  // share of the row groups.
+  const int per_cu = resident_per_cu(k_gemv<TYPE, WIDE, R, NT>, lds);
+  const int64_t groups = rows / R, tgroups = (n + NT - 1) / NT;
+  const int64_t resident = (int64_t)per_cu * device_cus();
+  const int64_t gx = std::max<int64_t>(1, std::min<int64_t>(groups, resident / tgroups));
+  const dim3 grid((unsigned)gx, (unsigned)tgroups);
   hipLaunchKernelGGL((k_gemv<TYPE, WIDE, R, NT>), grid, dim3(kThreads), lds, s, static_cast<const uint8_t*>(w), rows,
-                     cols, x, n, y, ys, accumulate ? 1 : 0, chunk);
+                     cols, x, n, y, ys, accumulate ? 1 : 0);
 }
 
+// Tokens per workgroup: up to 8, fewer when the activation rows and term slots would not fit in LDS.
 template <int TYPE, bool WIDE, int R>
 void launch_nt(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y, int64_t ys,
                bool acc) {
-  if (n <= 1)
+  auto fits = [&](size_t bytes) { return bytes <= (size_t)kGemvLdsMax; };
+  if (n <= 1 || !fits(GemvCfg<TYPE, WIDE, R, 2>::lds_bytes(cols)))
     launch<TYPE, WIDE, R, 1>(s, w, rows, cols, x, n, y, ys, acc);
-  else if (n <= 2)
+  else if (n <= 2 || !fits(GemvCfg<TYPE, WIDE, R, 4>::lds_bytes(cols)))
     launch<TYPE, WIDE, R, 2>(s, w, rows, cols, x, n, y, ys, acc);
-  else if (n <= 4)
+  else if (n <= 4 || !fits(GemvCfg<TYPE, WIDE, R, 8>::lds_bytes(cols)))
     launch<TYPE, WIDE, R, 4>(s, w, rows, cols, x, n, y, ys, acc);
   else
     launch<TYPE, WIDE, R, 8>(s, w, rows, cols, x, n, y, ys, acc);
@@ -315,9 +490,10 @@ void launch_nt(hipStream_t s, const void* w, int64_t rows, int64_t cols, const B
 template <int TYPE, bool WIDE>
 void launch_r(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y, int64_t ys,
               bool acc) {
-  // Wide workgroups amortise the activation staging; narrow ones keep >= 2048 workgroups in flight.
-  if (rows % 32 == 0 && rows / 32 >= 2048)
-    launch_nt<TYPE, WIDE, 32>(s, w, rows, cols, x, n, y, ys, acc);
+  // One-token GEMVs over very many rows (the LM head) take 32 rows per workgroup: a quarter of the activation
+  // staging per weight byte.
+  if (n == 1 && rows % 32 == 0 && rows / 32 >= 2048 && GemvCfg<TYPE, WIDE, 32, 1>::lds_bytes(cols) <= kGemvLdsMax)
+    launch<TYPE, WIDE, 32, 1>(s, w, rows, cols, x, n, y, ys, acc);
   else
     launch_nt<TYPE, WIDE, 8>(s, w, rows, cols, x, n, y, ys, acc);
 }
