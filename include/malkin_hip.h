@@ -88,6 +88,16 @@ typedef struct {
 /* y[t * y_stride + r] (+)= row r . xq[t] for t < n, r < rows. accumulate != 0 adds to y (the residual add x += h of
    model.cpp:352-356 fused into the epilogue). Results are bit-identical to the reference's panel kernels. */
 int mk_matmul(mk_ctx* ctx, const mk_weight* w, const void* xq, int n, float* y, int64_t y_stride, int accumulate);
+/* The same matmul from fp32 activations x[t * x_stride + i]: rmsnorm with norm_w (when not NULL, eps) and
+   quantize_row_q8 run inside the matmul, bit-identical to mk_rmsnorm_q8 / mk_quantize_q8 followed by mk_matmul
+   (replaces the rmsnorm -> quantize_acts -> matmul sequences of model.cpp:362-365, 403-406 and the quantize_acts ->
+   matmul of 397-399). For 1 or 2 tokens and a multiple of 32 columns (<= 8192 with rmsnorm); MK_ERR_UNSUPPORTED
+   otherwise.
+   silu_pairs != 0: the weight's rows are gate/up pairs interleaved by 4 (each 8-row group: 4 ffn_gate rows, then
+   the 4 ffn_up rows of the same outputs) and y[t * y_stride + i] = silu(gate_i) * up_i for i < rows / 2, the
+   kern::silu_mul of model.cpp:409 fused into the gate/up matmul (no accumulate). */
+int mk_matmul_f32(mk_ctx* ctx, const mk_weight* w, const float* x, int64_t x_stride, const float* norm_w, float eps,
+                  int n, float* y, int64_t y_stride, int accumulate, int silu_pairs);
 
 /* ---- elementwise (model.cpp:46-49, kernels.h:39) ---- */
 /* y = rmsnorm(x) * w per row of n floats (model.cpp:46-49). */
@@ -97,8 +107,9 @@ int mk_rmsnorm_q8(mk_ctx* ctx, const float* x, const int32_t* rows_idx, const fl
                   void* xq);
 /* g = g / (1 + e^-g) * u (kern::silu_mul, kernels.h:39). */
 int mk_silu_mul(mk_ctx* ctx, int64_t n, float* g, const float* u);
-/* silu_mul of rows of gu = [gate | up] (2n floats per row) quantized to BlockQ8 [rows][n/32] (model.cpp:409-411). */
-int mk_silu_mul_q8(mk_ctx* ctx, const float* gu, int rows, int64_t n, void* xq);
+/* silu_mul of rows of gu (2n floats per row) quantized to BlockQ8 [rows][n/32] (model.cpp:409-411). gu rows are
+   [gate | up], or, with interleave4, gate/up rows interleaved by 4 as in mk_matmul_f32's silu_pairs weights. */
+int mk_silu_mul_q8(mk_ctx* ctx, const float* gu, int rows, int64_t n, int interleave4, void* xq);
 /* x += h (model.cpp:352-356). */
 int mk_add(mk_ctx* ctx, int64_t n, float* x, const float* h);
 

@@ -67,7 +67,8 @@ int mk_model_generate(mk_model* m, const int32_t* prompt, int n_prompt, int n_ge
 /* Bytes of packed weights the model holds in HBM. */
 int64_t mk_model_weight_bytes(const mk_model* m);
 /* Descriptor of a packed matmul weight of the model (benchmarks, tests): which = 0 q|k|v (rows concatenated),
-   1 attn_output, 2 ffn_gate|ffn_up, 3 ffn_down of layer `layer`; which = 4 (layer ignored): the LM head. */
+   1 attn_output, 2 ffn_gate|ffn_up (rows interleaved by 4 when both have one type, see mk_matmul_f32 silu_pairs),
+   3 ffn_down of layer `layer`; which = 4 (layer ignored): the LM head. */
 int mk_model_weight(const mk_model* m, int layer, int which, mk_weight* out);
 
 #ifdef __cplusplus

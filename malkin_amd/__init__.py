@@ -47,10 +47,11 @@ SIGNATURES = {
     "mk_quantize_i8": (_I, [_P, _P, _I, _I, _P, _P]),
     "mk_dequantize_rows": (_I, [_P, _I, _P, _SZ, _P, _I, _I64, _P]),
     "mk_matmul": (_I, [_P, _P, _P, _I, _P, _I64, _I]),
+    "mk_matmul_f32": (_I, [_P, _P, _P, _I64, _P, _F, _I, _P, _I64, _I, _I]),
     "mk_rmsnorm": (_I, [_P, _P, _P, _I, _I, _F, _P]),
     "mk_rmsnorm_q8": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),
     "mk_silu_mul": (_I, [_P, _I64, _P, _P]),
-    "mk_silu_mul_q8": (_I, [_P, _P, _I, _I64, _P]),
+    "mk_silu_mul_q8": (_I, [_P, _P, _I, _I64, _I, _P]),
     "mk_add": (_I, [_P, _I64, _P, _P]),
     "mk_attend_gqa": (_I, [_P, _P, _I, _I, _P, _P, _SZ, ctypes.c_ssize_t, _I, _F, _P, _P, _I]),
     "mk_qk_norm_rope_kv": (_I, [_P, _P, _P, _P, _I64, _I, _I, _P, _P, _F, _P, _P, _P, _P, _P, _P, _I]),

@@ -73,7 +73,8 @@ ModelConfig read_config(const GgufFile& f) {
 }
 
 // Packs the named GGUF matrices (same type and column count) as one row-concatenated weight.
-void Model::load_weight(const GgufFile& f, const std::vector<std::string>& names, Weight& w) {
+// interleave4 (two matrices of equal shape): rows 4k..4k+3 of the first, then rows 4k..4k+3 of the second.
+void Model::load_weight(const GgufFile& f, const std::vector<std::string>& names, Weight& w, bool interleave4) {
   std::vector<const GgufTensor*> ts;
   for (const auto& nm : names) {
     const GgufTensor* t = f.tensor(nm);
@@ -94,15 +95,42 @@ void Model::load_weight(const GgufFile& f, const std::vector<std::string>& names
   const size_t pb = mk_packed_bytes(w.type, w.rows, w.cols);
   if (!pb) throw std::runtime_error("model: weight " + names[0] + " has no device layout (rows % 8)");
   DevBuf staging(ctx_, rb * static_cast<size_t>(w.rows));
-  size_t off = 0;
-  for (const GgufTensor* t : ts) {
-    ck(mk_upload(ctx_, staging.as<uint8_t>() + off, t->data, t->nbytes));
-    off += t->nbytes;
+  if (interleave4) {
+    if (ts.size() != 2 || ts[0]->rows() != ts[1]->rows() || ts[0]->rows() % 4)
+      throw std::runtime_error("model: interleaved weights need two matrices of equal rows, a multiple of 4");
+    std::vector<uint8_t> host(rb * static_cast<size_t>(w.rows));
+    const int64_t half = ts[0]->rows();
+    for (int64_t k = 0; k < half / 4; ++k)
+      for (int m = 0; m < 2; ++m)
+        std::memcpy(host.data() + (8 * k + 4 * m) * rb, static_cast<const uint8_t*>(ts[m]->data) + 4 * k * rb, 4 * rb);
+    ck(mk_upload(ctx_, staging.p, host.data(), host.size()));
+  } else {
+    size_t off = 0;
+    for (const GgufTensor* t : ts) {
+      ck(mk_upload(ctx_, staging.as<uint8_t>() + off, t->data, t->nbytes));
+      off += t->nbytes;
+    }
   }
   w.packed = DevBuf(ctx_, pb);
   ck(mk_pack_weight(ctx_, w.type, staging.p, rb, w.rows, w.cols, w.packed.p));
   ck(mk_synchronize(ctx_));
   weight_bytes_ += pb;
+}
+
+// ffn_gate | ffn_up: interleaved (silu fused into the decode matmul) when both have one type and the row count
+// allows; otherwise the plain group.
+void Model::load_gateup(const GgufFile& f, const std::string& gate, const std::string& up, Group& g) {
+  const GgufTensor* a = f.tensor(gate);
+  const GgufTensor* b = f.tensor(up);
+  if (a && b && a->type == b->type && a->ne[0] == b->ne[0] && a->rows() == b->rows() && a->rows() % 4 == 0) {
+    Weight w;
+    load_weight(f, {gate, up}, w, true);
+    g.rows = w.rows;
+    g.parts.push_back(std::move(w));
+    g.silu_pairs = true;
+    return;
+  }
+  load_group(f, {gate, up}, g);
 }
 
 void Model::load_group(const GgufFile& f, const std::vector<std::string>& names, Group& g) {
@@ -127,6 +155,14 @@ void Model::load_group(const GgufFile& f, const std::vector<std::string>& names,
   }
 }
 
+// Whether mk_matmul_f32 has a fused kernel for this weight at n tokens (the library's own rule, mirrored to pick the
+// path without a failing call).
+static bool matmul_f32_ok(const mk_weight& w, int n, bool norm) {
+  return n >= 1 && n <= 2 && w.cols % 32 == 0 && (!norm || w.cols <= 8192) &&
+         static_cast<int64_t>(n) * (w.cols / 32) * 40 <= 64 * 1024 &&
+         (w.type == MK_Q8_0 || w.type == MK_Q4_K || w.type == MK_Q6_K);
+}
+
 // quant.cpp:287-328 (matmul_group): every part writes its rows of the shared output row [t][g.rows].
 void Model::matmul_group(const Group& g, const void* xq, int n, float* y) {
   for (const Weight& p : g.parts) {
@@ -134,6 +170,19 @@ void Model::matmul_group(const Group& g, const void* xq, int n, float* y) {
     w.wide = wide_ ? 1 : 0;
     ck(mk_matmul(ctx_, &w, xq, n, y + p.out_off, g.rows, 0));
   }
+}
+
+bool Model::matmul_group_f32(const Group& g, const float* x, int64_t xs, const float* norm_w, int n, float* y) {
+  for (const Weight& p : g.parts) {
+    const mk_weight w = p.w();
+    if (!matmul_f32_ok(w, n, norm_w != nullptr)) return false;
+  }
+  for (const Weight& p : g.parts) {
+    mk_weight w = p.w();
+    w.wide = wide_ ? 1 : 0;
+    ck(mk_matmul_f32(ctx_, &w, x, xs, norm_w, cfg_.rms_eps, n, y + p.out_off, g.rows, 0, 0));
+  }
+  return true;
 }
 
 Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide)
@@ -177,7 +226,7 @@ Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide)
     upload_norm(p + "attn_k_norm.weight", D, L.norms.as<float>() + 2 * E + D);
     load_group(f, {p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"}, L.qkv);
     load_weight(f, {p + "attn_output.weight"}, L.wo);
-    load_group(f, {p + "ffn_gate.weight", p + "ffn_up.weight"}, L.gateup);
+    load_gateup(f, p + "ffn_gate.weight", p + "ffn_up.weight", L.gateup);
     load_weight(f, {p + "ffn_down.weight"}, L.down);
     if (L.qkv.rows != (int64_t)(H + 2 * KV) * D || L.wo.rows != E || L.gateup.rows != 2 * F || L.down.rows != E)
       throw std::runtime_error("model: layer " + std::to_string(i) + " has unexpected shapes");
@@ -336,23 +385,40 @@ void Model::run(int n) {
   for (int il = 0; il < c.n_layer; ++il) {
     const Layer& L = layers_[il];
     const float* norms = L.norms.as<float>();
-    ck(mk_rmsnorm_q8(ctx_, x, nullptr, norms, n, E, c.rms_eps, xq));
-    matmul_group(L.qkv, xq, n, qkv);
+    // Decode steps (n <= 2) fuse rmsnorm / quantization into the matmuls (mk_matmul_f32); same results.
+    if (!matmul_group_f32(L.qkv, x, E, norms, n, qkv)) {
+      ck(mk_rmsnorm_q8(ctx_, x, nullptr, norms, n, E, c.rms_eps, xq));
+      matmul_group(L.qkv, xq, n, qkv);
+    }
     ck(mk_qk_norm_rope_kv(ctx_, qkv, qkv + static_cast<int64_t>(H) * D, qkv + static_cast<int64_t>(H + KV) * D, QKV, n,
                           H, norms + 2 * E, norms + 2 * E + D, c.rms_eps, rope_cos_.as<float>(),
                           rope_sin_.as<float>(), d_rpos_, d_seq_, d_kv_row_, &kv, il));
     ck(mk_attention(ctx_, qkv, QKV, att, static_cast<int64_t>(H) * D, n, H, &kv, il, d_seq_, d_n_keys_,
                     tree_ ? d_anc_off_ : nullptr, d_anc_, max_keys_));
-    ck(mk_quantize_q8(ctx_, att, n, static_cast<int64_t>(H) * D, xq));
     mk_weight wo = L.wo.w();
     wo.wide = wide_ ? 1 : 0;
-    ck(mk_matmul(ctx_, &wo, xq, n, x, E, 1));  // x += attn_output(att) (model.cpp:398-401)
-    ck(mk_rmsnorm_q8(ctx_, x, nullptr, norms + E, n, E, c.rms_eps, xq));
-    matmul_group(L.gateup, xq, n, gu);
-    ck(mk_silu_mul_q8(ctx_, gu, n, F, xq));
+    if (matmul_f32_ok(wo, n, false)) {
+      ck(mk_matmul_f32(ctx_, &wo, att, static_cast<int64_t>(H) * D, nullptr, 0.0f, n, x, E, 1, 0));
+    } else {
+      ck(mk_quantize_q8(ctx_, att, n, static_cast<int64_t>(H) * D, xq));
+      ck(mk_matmul(ctx_, &wo, xq, n, x, E, 1));  // x += attn_output(att) (model.cpp:398-401)
+    }
     mk_weight wd = L.down.w();
     wd.wide = wide_ ? 1 : 0;
-    ck(mk_matmul(ctx_, &wd, xq, n, x, E, 1));  // x += ffn_down(...) (model.cpp:412-416)
+    if (L.gateup.silu_pairs && matmul_f32_ok(L.gateup.parts[0].w(), n, true) && matmul_f32_ok(wd, n, false)) {
+      // h = silu(gate) * up straight from the gate|up matmul, quantized inside the down matmul.
+      mk_weight wg = L.gateup.parts[0].w();
+      wg.wide = wide_ ? 1 : 0;
+      ck(mk_matmul_f32(ctx_, &wg, x, E, norms + E, c.rms_eps, n, gu, F, 0, 1));
+      ck(mk_matmul_f32(ctx_, &wd, gu, F, nullptr, 0.0f, n, x, E, 1, 0));  // x += ffn_down(h)
+    } else {
+      if (!matmul_group_f32(L.gateup, x, E, norms + E, n, gu)) {
+        ck(mk_rmsnorm_q8(ctx_, x, nullptr, norms + E, n, E, c.rms_eps, xq));
+        matmul_group(L.gateup, xq, n, gu);
+      }
+      ck(mk_silu_mul_q8(ctx_, gu, n, F, L.gateup.silu_pairs ? 1 : 0, xq));
+      ck(mk_matmul(ctx_, &wd, xq, n, x, E, 1));  // x += ffn_down(...) (model.cpp:412-416)
+    }
   }
   const int m = static_cast<int>(out_.size());
   if (m == 0) return;

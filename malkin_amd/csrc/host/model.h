@@ -104,6 +104,9 @@ class Model {
   struct Group {
     std::vector<Weight> parts;
     int64_t rows = 0;
+    // gate|up packed as one weight with rows interleaved by 4 (4 gate rows, then the 4 up rows of the same outputs):
+    // the decode matmul then applies silu_mul itself (mk_matmul_f32 silu_pairs).
+    bool silu_pairs = false;
   };
   struct Layer {
     DevBuf norms;  // attn_norm[E], ffn_norm[E], q_norm[D], k_norm[D]
@@ -111,9 +114,13 @@ class Model {
     Weight wo, down;
   };
 
-  void load_weight(const GgufFile& f, const std::vector<std::string>& names, Weight& w);
+  void load_weight(const GgufFile& f, const std::vector<std::string>& names, Weight& w, bool interleave4 = false);
+  void load_gateup(const GgufFile& f, const std::string& gate, const std::string& up, Group& g);
   void load_group(const GgufFile& f, const std::vector<std::string>& names, Group& g);
   void matmul_group(const Group& g, const void* xq, int n, float* y);
+  // The group from fp32 rows x (token stride xs) with rmsnorm (norm_w) / quantization inside each matmul; false when
+  // a part has no fused kernel for n tokens (nothing launched then).
+  bool matmul_group_f32(const Group& g, const float* x, int64_t xs, const float* norm_w, int n, float* y);
   void build_layout(const BatchToken* batch, int n);
   void upload_layout(int n);
   void run(int n);  // device forward over the uploaded layout

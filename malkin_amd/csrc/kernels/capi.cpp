@@ -161,6 +161,18 @@ int mk_matmul(mk_ctx* c, const mk_weight* w, const void* xq, int n, float* y, in
   });
 }
 
+int mk_matmul_f32(mk_ctx* c, const mk_weight* w, const float* x, int64_t x_stride, const float* norm_w, float eps,
+                  int n, float* y, int64_t ys, int accumulate, int silu_pairs) {
+  return guard([&] {
+    require(w != nullptr, "mk_matmul_f32: null weight");
+    if (!mk::matmul_f32_supported(w->type, w->wide != 0, w->rows, w->cols, n, norm_w != nullptr))
+      throw mk::Error(MK_ERR_UNSUPPORTED, "mk_matmul_f32: no fused kernel (needs 1 or 2 tokens, a multiple of 32 "
+                                          "columns, <= 8192 with rmsnorm, a Q8_0/Q4_K/Q6_K weight)");
+    mk::matmul_f32(c->stream, w->type, w->wide != 0, w->data, w->rows, w->cols, x, x_stride, norm_w, eps, n, y, ys,
+                   accumulate != 0, silu_pairs != 0);
+  });
+}
+
 int mk_rmsnorm(mk_ctx* c, const float* x, const float* w, int rows, int n, float eps, float* y) {
   return guard([&] { mk::rmsnorm(c->stream, x, w, rows, n, eps, y); });
 }
@@ -174,8 +186,8 @@ int mk_silu_mul(mk_ctx* c, int64_t n, float* g, const float* u) {
   return guard([&] { mk::silu_mul(c->stream, n, g, u); });
 }
 
-int mk_silu_mul_q8(mk_ctx* c, const float* gu, int rows, int64_t n, void* xq) {
-  return guard([&] { mk::silu_mul_q8(c->stream, gu, rows, n, static_cast<mk::BlockQ8*>(xq)); });
+int mk_silu_mul_q8(mk_ctx* c, const float* gu, int rows, int64_t n, int interleave4, void* xq) {
+  return guard([&] { mk::silu_mul_q8(c->stream, gu, rows, n, static_cast<mk::BlockQ8*>(xq), interleave4 != 0); });
 }
 
 int mk_add(mk_ctx* c, int64_t n, float* x, const float* h) {

@@ -108,4 +108,75 @@ __device__ __forceinline__ int cvt_rne(float x) {
 
 __device__ __forceinline__ int sat8(int v) { return v > 127 ? 127 : (v < -128 ? -128 : v); }
 
+// Half of one Q8 block (16 consecutive values, h = which half) -> its BlockQ8 bytes (kernels_avx512.cpp:66-80). The
+// two halves sit on neighbouring lanes (h = lane & 1); every lane must call this, as the block max is exchanged between
+// the pair. amax is an exact max and the half sums are exact integer sums, so their order does not matter.
+__device__ __forceinline__ void quantize_half_block(const float (&v)[16], int h, bool store, BlockQ8* out) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 16; ++c) amax = fmaxf(amax, fabsf(v[c]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  const float d = amax / 127.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  int s = 0;
+  uint32_t packed[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int q = cvt_rne(v[4 * k + c] * id);
+      s += q;
+      word |= (uint32_t)(uint8_t)(int8_t)sat8(q) << (8 * c);
+    }
+    packed[k] = word;
+  }
+  if (!store) return;
+  uint8_t* o = reinterpret_cast<uint8_t*>(out);
+  // BlockQ8 is 8-byte aligned (40-byte blocks), so its quants take two 8-byte stores per half.
+  *reinterpret_cast<uint2*>(o + 8 + 16 * h) = make_uint2(packed[0], packed[1]);
+  *reinterpret_cast<uint2*>(o + 16 + 16 * h) = make_uint2(packed[2], packed[3]);
+  if (h == 0) {
+    *reinterpret_cast<float*>(o) = d;
+    *reinterpret_cast<int16_t*>(o + 4) = (int16_t)s;
+  } else {
+    *reinterpret_cast<int16_t*>(o + 6) = (int16_t)s;
+  }
+}
+
+
+// One lane of kern::dot_f32(x, x) (kernels_avx512.cpp:82-89): the sequential fma chain over x[l], x[l + 16], ...
+// given as the lane's contiguous row tl[0 .. per) of a transposed copy (16-byte aligned). 32 values per step, the
+// next 32 read while the current ones run.
+__device__ __forceinline__ float sumsq_lane_chain(const float* tl, int per) {
+  const int f4 = per / 4;
+  constexpr int B = 8;
+  float acc = 0.0f;
+  float4 cur[B];
+#pragma unroll
+  for (int k = 0; k < B; ++k)
+    if (k < f4) cur[k] = reinterpret_cast<const float4*>(tl)[k];
+  for (int j = 0; j < f4; j += B) {
+    float4 nxt[B];
+#pragma unroll
+    for (int k = 0; k < B; ++k)
+      if (j + B + k < f4) nxt[k] = reinterpret_cast<const float4*>(tl)[j + B + k];
+#pragma unroll
+    for (int k = 0; k < B; ++k) {
+      if (j + k < f4) {
+        acc = fma_(cur[k].x, cur[k].x, acc);
+        acc = fma_(cur[k].y, cur[k].y, acc);
+        acc = fma_(cur[k].z, cur[k].z, acc);
+        acc = fma_(cur[k].w, cur[k].w, acc);
+      }
+      cur[k] = nxt[k];
+    }
+  }
+  for (int i = 4 * f4; i < per; ++i) acc = fma_(tl[i], tl[i], acc);
+  return acc;
+}
+
+// Floats per row of the transposed copy used by sumsq_lane_chain: per = n / 16 values, 16-byte aligned, padded.
+__host__ __device__ constexpr int sumsq_tstride(int per) { return ((per + 3) & ~3) + 4; }
+
 }  // namespace mk

@@ -12,7 +12,11 @@
 //            chunk c + 2 is in flight while chunk c is computed;
 //   wave 0 (chains): the R * NT sequential chains over chunk c - 1 while the workers compute chunk c.
 // Barriers order LDS only (lds_barrier), so the weight loads stay in flight across them. The activation rows of the
-// workgroup's tokens are staged in LDS once, as BlockQ8.
+// workgroup's tokens are staged in LDS once, as BlockQ8: copied (kProQ8), or made here from fp32 rows, which fuses
+// the reference's quantize_acts (kProF32) or rmsnorm + quantize_acts (kProNorm, model.cpp:46-49, 362-364, 403-405)
+// into the matmul, saving a launch per use on the decode path. With kEpiSilu the rows come in gate/up pairs (each
+// 8-row group = 4 gate rows, then the 4 up rows of the same outputs) and the workgroup stores silu(gate) * up
+// (kernels_avx512.cpp:271-280) in place of the two dot products.
 #include "ctx.h"
 #include "ops.h"
 
@@ -112,7 +116,11 @@ __device__ __forceinline__ float xd(const int* xq) { return __int_as_float(xq[0]
 __device__ __forceinline__ int xs0(const int* xq) { return (int)(int16_t)(xq[1] & 0xFFFF); }
 __device__ __forceinline__ int xs1(const int* xq) { return (int)(int16_t)((uint32_t)xq[1] >> 16); }
 
-template <int TYPE, bool WIDE, int R, int NT>
+enum : int { kProQ8 = 0, kProF32 = 1, kProNorm = 2 };
+enum : int { kEpiStore = 0, kEpiSilu = 1 };
+constexpr int kProPass = 2;  // fp32 prologues: 2 x 256 threads x 16 values = up to 8192 columns
+
+template <int TYPE, bool WIDE, int R, int NT, int PRO = kProQ8>
 struct GemvCfg {
   static constexpr int UQ8 = Unit<TYPE>::q8;
   static constexpr int E = (TYPE == kQ6_K && WIDE) ? 1 : Unit<TYPE>::e;
@@ -134,17 +142,22 @@ struct GemvCfg {
   static constexpr int kMnSlot = R * kMnRow;
   static constexpr bool kXsc = TYPE == kQ4_K || (TYPE == kQ6_K && WIDE);  // per-block activation scale terms
   __host__ __device__ static int64_t xsc_row(int64_t nq8) { return nq8 + 16; }  // + zero pad: groups read past the end
+  // kProNorm: the rows, transposed for the sum-of-squares chains ([NT][16][sumsq_tstride]).
+  static size_t norm_floats(int64_t cols) {
+    return PRO == kProNorm ? (size_t)NT * 16 * sumsq_tstride((int)(cols / 16)) : 0;
+  }
   static size_t lds_bytes(int64_t cols) {
     const int64_t nq8 = cols / 32;
-    return (size_t)NT * nq8 * 40 + 2 * (size_t)(kSlot + kMnSlot) * 4 + (kXsc ? (size_t)NT * xsc_row(nq8) * 4 : 0);
+    return (size_t)NT * nq8 * 40 + 2 * (size_t)(kSlot + kMnSlot) * 4 + (kXsc ? (size_t)NT * xsc_row(nq8) * 4 : 0) +
+           norm_floats(cols) * 4;
   }
 };
 
-template <int TYPE, bool WIDE, int R, int NT>
-__global__ __launch_bounds__(kThreads) void k_gemv(const uint8_t* W, int64_t rows, int64_t cols,
-                                                   const BlockQ8* __restrict__ x, int n, float* __restrict__ y,
-                                                   int64_t ys, int accumulate) {
-  using C = GemvCfg<TYPE, WIDE, R, NT>;
+template <int TYPE, bool WIDE, int R, int NT, int PRO, int EPI>
+__global__ __launch_bounds__(kThreads) void k_gemv(const uint8_t* W, int64_t rows, int64_t cols, GemvIn in, int n,
+                                                   float* __restrict__ y, int64_t ys, int accumulate) {
+  using C = GemvCfg<TYPE, WIDE, R, NT, PRO>;
+  const BlockQ8* __restrict__ x = in.xq;
   constexpr int UQ8 = C::UQ8, E = C::E, kChunk = C::kChunk, kP = C::kP, kG = C::kG;
   extern __shared__ int smem[];
   const int nq8 = (int)(cols / 32), nu = nq8 / UQ8;
@@ -163,6 +176,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv(const uint8_t* W, int64_t row
   float* mnv = res + 2 * C::kSlot;                                  // Q4_K: [2][kMnSlot]
   float* xsc = mnv + 2 * C::kMnSlot;                                // [NT][xsc_row]: Q4_K dx (s0 + s1), Q6_K wide dx
   const int xrow = (int)C::xsc_row(nq8);
+  float* tr = xsc + (C::kXsc ? NT * xrow : 0);                      // kProNorm: [NT][16][tstride]
 
   // Waves 1-3 are the workers: pair f = wi + k * kWorkers of a chunk is (unit f / R, row f % R), and two chunks are
   // in flight (register sets A/B). Every wave issues the same sequence of loads, never predicated: wave 0 repeats
@@ -209,19 +223,133 @@ __global__ __launch_bounds__(kThreads) void k_gemv(const uint8_t* W, int64_t row
       }
     }
   };
-  {
-    uint2 xv[kStage];
-    stage_load(xv, tid);
+  if constexpr (PRO == kProQ8) {
+    {
+      uint2 xv[kStage];
+      stage_load(xv, tid);
+      load(ra, 0);
+      load(rb, 1);
+      stage_store(xv, tid);
+    }
+    for (int i0 = tid + kThreads * kStage; i0 < total; i0 += kThreads * kStage) {
+      uint2 v[kStage];
+      stage_load(v, i0);
+      stage_store(v, i0);
+    }
+    lds_barrier();
+  } else if constexpr (PRO == kProF32) {
+    // fp32 rows, quantized pass by pass: thread tid takes the 16-value chunk c16 = tid + 256 p (half a Q8 block) of
+    // every token row. The first pass is loaded before the weight loads, so it waits for nothing else.
+    const int per = nq8 * 2;  // 16-value chunks per row
+    auto pass = [&](float (&v)[NT][16], int p, bool fetch) {
+      const int c16 = tid + p * kThreads;
+      if (fetch) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          if (t < nt && c16 < per) {
+            const float* xr = in.xf + (int64_t)(t0 + t) * in.xfs + 16 * c16;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              const float4 a = *reinterpret_cast<const float4*>(xr + 4 * k);
+              v[t][4 * k] = a.x, v[t][4 * k + 1] = a.y, v[t][4 * k + 2] = a.z, v[t][4 * k + 3] = a.w;
+            }
+          }
+        }
+        return;
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        if (t >= nt) break;  // uniform
+        // per is even (cols % 32 == 0): both halves of a block are in the row or neither is.
+        quantize_half_block(v[t], c16 & 1, c16 < per, reinterpret_cast<BlockQ8*>(xs + t * nq8 * 10) + c16 / 2);
+      }
+    };
+    {
+      float v[NT][16];
+      pass(v, 0, true);
+      load(ra, 0);
+      load(rb, 1);
+      pass(v, 0, false);
+    }
+    for (int p = 1; p * kThreads < per; ++p) {  // uniform
+      float v[NT][16];
+      pass(v, p, true);
+      pass(v, p, false);
+    }
+    lds_barrier();
+  } else {
+    // rmsnorm + quantization: thread tid owns the 16-value chunks c16 = tid + 256 p (half a Q8 block each) of every
+    // token row, read with 16-byte loads issued before the weight loads. The rows go to LDS (transposed, for the
+    // chains) and are read back for the scaling, with the norm weights read then: neither occupies registers
+    // meanwhile, and the norm weights' wait coincides with the first weight chunks'.
+    const int per = nq8 * 2;  // 16-value chunks per row
+    const int tstride = sumsq_tstride(per);
+    float v[NT][kProPass][16];
+#pragma unroll
+    for (int p = 0; p < kProPass; ++p) {
+      const int c16 = tid + p * kThreads;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        if (t < nt && c16 < per) {
+          const float* xr = in.xf + (int64_t)(t0 + t) * in.xfs + 16 * c16;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const float4 a = *reinterpret_cast<const float4*>(xr + 4 * k);
+            v[t][p][4 * k] = a.x, v[t][p][4 * k + 1] = a.y, v[t][p][4 * k + 2] = a.z, v[t][p][4 * k + 3] = a.w;
+          }
+        }
+      }
+    }
     load(ra, 0);
     load(rb, 1);
-    stage_store(xv, tid);
+    __shared__ float scale_s[NT];
+    {
+      // rmsnorm (model.cpp:46-49): 16 sequential lane chains per token over the transposed copy, halving tree.
+#pragma unroll
+      for (int p = 0; p < kProPass; ++p) {
+        const int c16 = tid + p * kThreads;
+        if (c16 < per) {
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+            if (t < nt) {
+#pragma unroll
+              for (int c = 0; c < 16; ++c) tr[(t * 16 + c) * tstride + c16] = v[t][p][c];
+            }
+        }
+      }
+      lds_barrier();
+      if (tid < 16 * nt) {
+        float acc = sumsq_lane_chain(tr + tid * tstride, per);  // token tid / 16, lane tid % 16
+        acc = reduce16_lanes(acc);
+        if ((tid & 15) == 0) scale_s[tid >> 4] = 1.0f / sqrtf(acc / (float)cols + in.eps);
+      }
+      lds_barrier();
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if (t >= nt) break;  // uniform
+      BlockQ8* row = reinterpret_cast<BlockQ8*>(xs + t * nq8 * 10);
+#pragma unroll
+      for (int p = 0; p < kProPass; ++p) {
+        if (p * kThreads >= per) break;  // uniform
+        const int c16 = tid + p * kThreads;
+        float yv[16];
+        const float sc = scale_s[t];
+        if (c16 < per) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const float4 w4 = reinterpret_cast<const float4*>(in.nw + 16 * c16)[k];
+            const float wk[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) yv[4 * k + c] = tr[(t * 16 + 4 * k + c) * tstride + c16] * sc * wk[c];
+          }
+        }
+        // per is even (cols % 32 == 0): both halves of a block are in the row or neither is.
+        quantize_half_block(yv, c16 & 1, c16 < per, row + c16 / 2);
+      }
+    }
+    lds_barrier();
   }
-  for (int i0 = tid + kThreads * kStage; i0 < total; i0 += kThreads * kStage) {
-    uint2 v[kStage];
-    stage_load(v, i0);
-    stage_store(v, i0);
-  }
-  lds_barrier();
   if constexpr (C::kXsc) {
     for (int i = tid; i < NT * xrow; i += kThreads) {
       const int t = i / xrow, b = i - t * xrow;
@@ -390,8 +518,17 @@ __global__ __launch_bounds__(kThreads) void k_gemv(const uint8_t* W, int64_t row
       if ((ul0 += kG) >= cn) break;
     }
     if (c == nc - 1) {
-      float* o = y + (int64_t)(t0 + ct) * ys + (int64_t)rg(q) * R + cr;
-      *o = accumulate ? *o + acc : acc;
+      if constexpr (EPI == kEpiSilu) {
+        // Lanes cr and cr + 4 of an 8-lane group hold gate and up of output 4 * group + cr.
+        const float up = __shfl_down(acc, 4, 8);
+        if (cr < 4) {
+          const float e = exp512(0.0f - acc);
+          y[(int64_t)(t0 + ct) * ys + (int64_t)rg(q) * (R / 2) + cr] = (acc / (1.0f + e)) * up;
+        }
+      } else {
+        float* o = y + (int64_t)(t0 + ct) * ys + (int64_t)rg(q) * R + cr;
+        *o = accumulate ? *o + acc : acc;
+      }
       acc = 0.0f;
     }
   };
@@ -449,53 +586,79 @@ int resident_per_cu(K kernel, size_t lds) {
   return blocks;
 }
 
-template <int TYPE, bool WIDE, int R, int NT>
-void launch(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y, int64_t ys,
+template <int TYPE, bool WIDE, int R, int NT, int PRO, int EPI = kEpiStore>
+void launch(hipStream_t s, const void* w, int64_t rows, int64_t cols, const GemvIn& in, int n, float* y, int64_t ys,
             bool accumulate) {
-  using C = GemvCfg<TYPE, WIDE, R, NT>;
+  using C = GemvCfg<TYPE, WIDE, R, NT, PRO>;
   const size_t lds = C::lds_bytes(cols);
   static bool attr = false;  // per instantiation: allow more than the default 64 KB of dynamic LDS
   if (!attr) {
-    check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv<TYPE, WIDE, R, NT>),
+    check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv<TYPE, WIDE, R, NT, PRO, EPI>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, kGemvLdsMax),
           "hipFuncSetAttribute");
     attr = true;
   }
   // Persistent over row groups: as many workgroups as are resident at once (per token group), each streaming its
   // share of the row groups.
-  const int per_cu = resident_per_cu(k_gemv<TYPE, WIDE, R, NT>, lds);
+  const int per_cu = resident_per_cu(k_gemv<TYPE, WIDE, R, NT, PRO, EPI>, lds);
   const int64_t groups = rows / R, tgroups = (n + NT - 1) / NT;
   const int64_t resident = (int64_t)per_cu * device_cus();
   const int64_t gx = std::max<int64_t>(1, std::min<int64_t>(groups, resident / tgroups));
   const dim3 grid((unsigned)gx, (unsigned)tgroups);
-  hipLaunchKernelGGL((k_gemv<TYPE, WIDE, R, NT>), grid, dim3(kThreads), lds, s, static_cast<const uint8_t*>(w), rows,
-                     cols, x, n, y, ys, accumulate ? 1 : 0);
+  hipLaunchKernelGGL((k_gemv<TYPE, WIDE, R, NT, PRO, EPI>), grid, dim3(kThreads), lds, s, static_cast<const uint8_t*>(w),
+                     rows, cols, in, n, y, ys, accumulate ? 1 : 0);
 }
 
 // Tokens per workgroup: up to 8, fewer when the activation rows and term slots would not fit in LDS.
 template <int TYPE, bool WIDE, int R>
-void launch_nt(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y, int64_t ys,
+void launch_nt(hipStream_t s, const void* w, int64_t rows, int64_t cols, const GemvIn& in, int n, float* y, int64_t ys,
                bool acc) {
   auto fits = [&](size_t bytes) { return bytes <= (size_t)kGemvLdsMax; };
   if (n <= 1 || !fits(GemvCfg<TYPE, WIDE, R, 2>::lds_bytes(cols)))
-    launch<TYPE, WIDE, R, 1>(s, w, rows, cols, x, n, y, ys, acc);
+    launch<TYPE, WIDE, R, 1, kProQ8>(s, w, rows, cols, in, n, y, ys, acc);
   else if (n <= 2 || !fits(GemvCfg<TYPE, WIDE, R, 4>::lds_bytes(cols)))
-    launch<TYPE, WIDE, R, 2>(s, w, rows, cols, x, n, y, ys, acc);
+    launch<TYPE, WIDE, R, 2, kProQ8>(s, w, rows, cols, in, n, y, ys, acc);
   else if (n <= 4 || !fits(GemvCfg<TYPE, WIDE, R, 8>::lds_bytes(cols)))
-    launch<TYPE, WIDE, R, 4>(s, w, rows, cols, x, n, y, ys, acc);
+    launch<TYPE, WIDE, R, 4, kProQ8>(s, w, rows, cols, in, n, y, ys, acc);
   else
-    launch<TYPE, WIDE, R, 8>(s, w, rows, cols, x, n, y, ys, acc);
+    launch<TYPE, WIDE, R, 8, kProQ8>(s, w, rows, cols, in, n, y, ys, acc);
 }
 
 template <int TYPE, bool WIDE>
-void launch_r(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y, int64_t ys,
+void launch_r(hipStream_t s, const void* w, int64_t rows, int64_t cols, const GemvIn& in, int n, float* y, int64_t ys,
               bool acc) {
   // One-token GEMVs over very many rows (the LM head) take 32 rows per workgroup: a quarter of the activation
   // staging per weight byte.
   if (n == 1 && rows % 32 == 0 && rows / 32 >= 2048 && GemvCfg<TYPE, WIDE, 32, 1>::lds_bytes(cols) <= kGemvLdsMax)
-    launch<TYPE, WIDE, 32, 1>(s, w, rows, cols, x, n, y, ys, acc);
+    launch<TYPE, WIDE, 32, 1, kProQ8>(s, w, rows, cols, in, n, y, ys, acc);
   else
-    launch_nt<TYPE, WIDE, 8>(s, w, rows, cols, x, n, y, ys, acc);
+    launch_nt<TYPE, WIDE, 8>(s, w, rows, cols, in, n, y, ys, acc);
+}
+
+// fp32 activations, one or two tokens per workgroup.
+template <int TYPE, bool WIDE, int PRO, int EPI>
+void launch_f32(hipStream_t s, const void* w, int64_t rows, int64_t cols, const GemvIn& in, int n, float* y,
+                int64_t ys, bool acc) {
+  if (n == 1)
+    launch<TYPE, WIDE, 8, 1, PRO, EPI>(s, w, rows, cols, in, n, y, ys, acc);
+  else
+    launch<TYPE, WIDE, 8, 2, PRO, EPI>(s, w, rows, cols, in, n, y, ys, acc);
+}
+
+template <int PRO, int EPI>
+void matmul_f32_type(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int64_t cols, const GemvIn& in,
+                     int n, float* y, int64_t ys, bool acc) {
+  switch (type) {
+    case kQ8_0:
+      launch_f32<kQ8_0, false, PRO, EPI>(s, w, rows, cols, in, n, y, ys, acc);
+      break;
+    case kQ4_K:
+      launch_f32<kQ4_K, false, PRO, EPI>(s, w, rows, cols, in, n, y, ys, acc);
+      break;
+    default:  // Q6_K; n <= 2, so never the wide panels (quant.cpp:256)
+      launch_f32<kQ6_K, false, PRO, EPI>(s, w, rows, cols, in, n, y, ys, acc);
+      break;
+  }
 }
 
 }  // namespace
@@ -504,27 +667,52 @@ void matmul(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int
             float* y, int64_t ys, bool accumulate) {
   require(n > 0, "matmul: no tokens");
   require(packed_bytes(type, rows, cols) != 0, "matmul: no kernel for this weight type/shape");
+  const GemvIn in{xq, nullptr, 0, nullptr, 0.0f};
   switch (type) {
     case kQ8_0:
       if (gemm_q8_0_supported(rows, cols, n))
         gemm_q8_0(s, w, rows, cols, xq, n, y, ys, accumulate);  // prefill / batches: int8 MFMA
       else
-        launch_r<kQ8_0, false>(s, w, rows, cols, xq, n, y, ys, accumulate);
+        launch_r<kQ8_0, false>(s, w, rows, cols, in, n, y, ys, accumulate);
       break;
     case kQ4_K:
-      launch_r<kQ4_K, false>(s, w, rows, cols, xq, n, y, ys, accumulate);
+      launch_r<kQ4_K, false>(s, w, rows, cols, in, n, y, ys, accumulate);
       break;
     case kQ6_K:
       // The reference switches Q6_K to its wide panels above kWideMinTokens = 16 tokens (quant.cpp:256).
       if (wide && n > 16)
-        launch_r<kQ6_K, true>(s, w, rows, cols, xq, n, y, ys, accumulate);
+        launch_r<kQ6_K, true>(s, w, rows, cols, in, n, y, ys, accumulate);
       else
-        launch_r<kQ6_K, false>(s, w, rows, cols, xq, n, y, ys, accumulate);
+        launch_r<kQ6_K, false>(s, w, rows, cols, in, n, y, ys, accumulate);
       break;
     default:
       throw Error(MK_ERR_UNSUPPORTED, "matmul: unsupported weight type");
   }
   check_launch("matmul");
+}
+
+bool matmul_f32_supported(int type, bool, int64_t rows, int64_t cols, int n, bool norm) {
+  return n >= 1 && n <= 2 && cols % 32 == 0 && (!norm || cols <= kThreads * 16 * kProPass) &&
+         (int64_t)n * (cols / 32) * 40 <= 64 * 1024 && packed_bytes(type, rows, cols) != 0 &&
+         (type == kQ8_0 || type == kQ4_K || type == kQ6_K);
+}
+
+void matmul_f32(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int64_t cols, const float* xf,
+                int64_t xfs, const float* nw, float eps, int n, float* y, int64_t ys, bool accumulate,
+                bool silu_pairs) {
+  require(matmul_f32_supported(type, wide, rows, cols, n, nw != nullptr),
+          "matmul_f32: needs 1 or 2 tokens, a multiple of 32 columns (<= 8192 with rmsnorm) and a quantized weight");
+  require(!silu_pairs || !accumulate, "matmul_f32: the silu epilogue does not accumulate");
+  const GemvIn in{nullptr, xf, xfs, nw, eps};
+  if (nw && silu_pairs)
+    matmul_f32_type<kProNorm, kEpiSilu>(s, type, wide, w, rows, cols, in, n, y, ys, false);
+  else if (nw)
+    matmul_f32_type<kProNorm, kEpiStore>(s, type, wide, w, rows, cols, in, n, y, ys, accumulate);
+  else if (silu_pairs)
+    matmul_f32_type<kProF32, kEpiSilu>(s, type, wide, w, rows, cols, in, n, y, ys, false);
+  else
+    matmul_f32_type<kProF32, kEpiStore>(s, type, wide, w, rows, cols, in, n, y, ys, accumulate);
+  check_launch("matmul_f32");
 }
 
 }  // namespace mk

@@ -42,13 +42,32 @@ void rmsnorm(hipStream_t s, const float* x, const float* w, int rows, int n, flo
 void rmsnorm_q8(hipStream_t s, const float* x, const int32_t* rows_idx, const float* w, int rows, int n, float eps,
                 BlockQ8* xq);
 void silu_mul(hipStream_t s, int64_t n, float* g, const float* u);
-void silu_mul_q8(hipStream_t s, const float* gu, int rows, int64_t n, BlockQ8* xq);
+// gu rows of 2n floats: [gate | up], or (interleave4) gate/up interleaved by 4 as matmul_f32's silu_pairs rows.
+void silu_mul_q8(hipStream_t s, const float* gu, int rows, int64_t n, BlockQ8* xq, bool interleave4 = false);
 void add(hipStream_t s, int64_t n, float* x, const float* h);
 void fill(hipStream_t s, void* p, int value, size_t bytes);
 
 // y[t * ys + r] (+)= W[r] . xq[t]; wide: Q6_K wide-panel arithmetic for n > 16.
 void matmul(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int64_t cols, const BlockQ8* xq, int n,
             float* y, int64_t ys, bool accumulate);
+
+// Activations of a decode GEMV given as fp32 rows xf[t * xfs + i]: quantized to BlockQ8 inside the matmul, after
+// rmsnorm with weights nw (eps) when nw is not null (model.cpp:46-49, 362-364, 403-405). Same results as
+// rmsnorm_q8 / quantize_q8 followed by matmul.
+struct GemvIn {
+  const BlockQ8* xq;
+  const float* xf;
+  int64_t xfs;
+  const float* nw;
+  float eps;
+};
+// Whether matmul_f32 has a fused kernel for this shape (decode: n <= 2, cols % 32 == 0; with rmsnorm cols <= 8192).
+bool matmul_f32_supported(int type, bool wide, int64_t rows, int64_t cols, int n, bool norm);
+// silu_pairs: the rows are gate/up pairs interleaved by 4 (each 8-row group: 4 gate rows, then the 4 up rows of the
+// same outputs); y[t * ys + i] = silu(gate_i) * up_i for i < rows / 2 (kernels_avx512.cpp:271-280).
+void matmul_f32(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int64_t cols, const float* xf,
+                int64_t xfs, const float* nw, float eps, int n, float* y, int64_t ys, bool accumulate,
+                bool silu_pairs);
 
 // Prefill GEMM for Q8_0 on int8 MFMA (same results as matmul's GEMV); supported for rows % 32 == 0 and n > 8.
 bool gemm_q8_0_supported(int64_t rows, int64_t cols, int n);

@@ -59,42 +59,6 @@ __global__ void k_quantize_i8(const float* __restrict__ x, int n, int8_t* __rest
   if (threadIdx.x == 0) d[row] = dd;
 }
 
-// Half of one Q8 block (16 consecutive values, h = which half) -> its BlockQ8 bytes (kernels_avx512.cpp:66-80). The
-// two halves sit on neighbouring lanes (h = lane & 1); every lane must call this, as the block max is exchanged between
-// the pair. amax is an exact max and the half sums are exact integer sums, so their order does not matter.
-__device__ __forceinline__ void quantize_half_block(const float (&v)[16], int h, bool store, BlockQ8* out) {
-  float amax = 0.0f;
-#pragma unroll
-  for (int c = 0; c < 16; ++c) amax = fmaxf(amax, fabsf(v[c]));
-  amax = fmaxf(amax, __shfl_xor(amax, 1));
-  const float d = amax / 127.0f;
-  const float id = d != 0.0f ? 1.0f / d : 0.0f;
-  int s = 0;
-  uint32_t packed[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    uint32_t word = 0;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int q = cvt_rne(v[4 * k + c] * id);
-      s += q;
-      word |= (uint32_t)(uint8_t)(int8_t)sat8(q) << (8 * c);
-    }
-    packed[k] = word;
-  }
-  if (!store) return;
-  uint8_t* o = reinterpret_cast<uint8_t*>(out);
-  // BlockQ8 is 8-byte aligned (40-byte blocks), so its quants take two 8-byte stores per half.
-  *reinterpret_cast<uint2*>(o + 8 + 16 * h) = make_uint2(packed[0], packed[1]);
-  *reinterpret_cast<uint2*>(o + 16 + 16 * h) = make_uint2(packed[2], packed[3]);
-  if (h == 0) {
-    *reinterpret_cast<float*>(o) = d;
-    *reinterpret_cast<int16_t*>(o + 4) = (int16_t)s;
-  } else {
-    *reinterpret_cast<int16_t*>(o + 6) = (int16_t)s;
-  }
-}
-
 // rmsnorm of one row per workgroup; the sum of squares follows kern::dot_f32 (kernels_avx512.cpp:82-89): 16 lane
 // accumulators, each a sequential fma chain over the elements i = l (mod 16), then the halving tree.
 // Thread t owns the 16-element chunks t and t + 256 of the row (n <= 8192), held in registers from one round of 16-byte
@@ -106,7 +70,7 @@ __global__ __launch_bounds__(kT) void k_rmsnorm(const float* __restrict__ x, con
                                                 const float* __restrict__ w, int n, float eps, float* __restrict__ y,
                                                 BlockQ8* __restrict__ xq) {
   extern __shared__ float4 sm4[];
-  const int per = n / 16, tstride = ((per + 3) & ~3) + 4;
+  const int per = n / 16, tstride = sumsq_tstride(per);
   float* tr = reinterpret_cast<float*>(sm4);  // [16][tstride]; element i at (i % 16, i / 16)
   __shared__ float scale;
   const int r = blockIdx.x, tid = threadIdx.x;
@@ -136,31 +100,7 @@ __global__ __launch_bounds__(kT) void k_rmsnorm(const float* __restrict__ x, con
   }
   __syncthreads();
   if (tid < 16) {
-    const float* tl = tr + tid * tstride;
-    const int f4 = per / 4;
-    constexpr int B = 8;
-    float acc = 0.0f;
-    float4 cur[B];
-#pragma unroll
-    for (int k = 0; k < B; ++k)
-      if (k < f4) cur[k] = reinterpret_cast<const float4*>(tl)[k];
-    for (int j = 0; j < f4; j += B) {
-      float4 nxt[B];
-#pragma unroll
-      for (int k = 0; k < B; ++k)
-        if (j + B + k < f4) nxt[k] = reinterpret_cast<const float4*>(tl)[j + B + k];
-#pragma unroll
-      for (int k = 0; k < B; ++k) {
-        if (j + k < f4) {
-          acc = fma_(cur[k].x, cur[k].x, acc);
-          acc = fma_(cur[k].y, cur[k].y, acc);
-          acc = fma_(cur[k].z, cur[k].z, acc);
-          acc = fma_(cur[k].w, cur[k].w, acc);
-        }
-        cur[k] = nxt[k];
-      }
-    }
-    for (int i = 4 * f4; i < per; ++i) acc = fma_(tl[i], tl[i], acc);
+    float acc = sumsq_lane_chain(tr + tid * tstride, per);
     acc = reduce16_lanes(acc);
     if (tid == 0) scale = 1.0f / sqrtf(acc / (float)n + eps);
   }
@@ -195,14 +135,17 @@ __global__ void k_silu_mul(int64_t n, float* __restrict__ g, const float* __rest
   g[i] = (x / (1.0f + e)) * u[i];
 }
 
-// gu row: [gate(n) | up(n)] -> silu(gate) * up, quantized; one element per thread, n % 32 == 0.
-__global__ void k_silu_mul_q8(const float* __restrict__ gu, int64_t n, int64_t total, BlockQ8* __restrict__ xq) {
+// gu row: [gate(n) | up(n)], or gate/up interleaved by 4 (row 8k + j: gate 4k + j for j < 4, else up 4k + j - 4)
+// -> silu(gate) * up, quantized; one element per thread, n % 32 == 0.
+__global__ void k_silu_mul_q8(const float* __restrict__ gu, int64_t n, int64_t total, int interleave4,
+                              BlockQ8* __restrict__ xq) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
   const int64_t r = i / n, c = i % n;
-  const float x = gu[r * 2 * n + c];
+  const int64_t gi = interleave4 ? 8 * (c / 4) + c % 4 : c, ui = interleave4 ? gi + 4 : n + c;
+  const float x = gu[r * 2 * n + gi];
   const float e = exp512(0.0f - x);
-  quantize_block_lanes((x / (1.0f + e)) * gu[r * 2 * n + n + c], (int)(c & 31), xq + i / 32);
+  quantize_block_lanes((x / (1.0f + e)) * gu[r * 2 * n + ui], (int)(c & 31), xq + i / 32);
 }
 
 __global__ void k_add(int64_t n, float* __restrict__ x, const float* __restrict__ h) {
@@ -288,7 +231,7 @@ void dequantize_rows(hipStream_t s, int type, const void* src, size_t row_bytes,
   check_launch("dequantize_rows");
 }
 
-static size_t rmsnorm_lds(int n) { return 16 * ((((size_t)n / 16 + 3) & ~(size_t)3) + 4) * sizeof(float); }
+static size_t rmsnorm_lds(int n) { return 16 * (size_t)sumsq_tstride(n / 16) * sizeof(float); }
 
 void rmsnorm(hipStream_t s, const float* x, const float* w, int rows, int n, float eps, float* y) {
   if (rows <= 0) return;
@@ -313,11 +256,11 @@ void silu_mul(hipStream_t s, int64_t n, float* g, const float* u) {
   check_launch("silu_mul");
 }
 
-void silu_mul_q8(hipStream_t s, const float* gu, int rows, int64_t n, BlockQ8* xq) {
+void silu_mul_q8(hipStream_t s, const float* gu, int rows, int64_t n, BlockQ8* xq, bool interleave4) {
   require(n % 32 == 0, "silu_mul_q8: n must be a multiple of 32");
   const int64_t total = (int64_t)rows * n;
   if (total == 0) return;
-  hipLaunchKernelGGL(k_silu_mul_q8, dim3(grid_for(total, kT)), dim3(kT), 0, s, gu, n, total, xq);
+  hipLaunchKernelGGL(k_silu_mul_q8, dim3(grid_for(total, kT)), dim3(kT), 0, s, gu, n, total, interleave4 ? 1 : 0, xq);
   check_launch("silu_mul_q8");
 }
 

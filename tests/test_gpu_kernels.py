@@ -82,9 +82,23 @@ def test_silu(mk, golden, oracle):
     gu = rng.uniform(-20, 20, (rows, 2 * F)).astype(np.float32)
     dgu = mk.to_device(gu)
     out = mk.alloc(rows * F // 32 * 40)
-    mk_.check(L().mk_silu_mul_q8(mk.h, dgu.ptr, rows, F, out.ptr))
+    mk_.check(L().mk_silu_mul_q8(mk.h, dgu.ptr, rows, F, 0, out.ptr))
     exp = np.stack([oracle.silu_mul(r[:F], r[F:]) for r in gu])
     assert np.array_equal(out.download(np.uint8), oracle.quantize_row_q8(exp).view(np.uint8).reshape(-1))
+    # the same rows with gate/up interleaved by 4
+    gi = interleave4(gu[:, :F], gu[:, F:])
+    dgi = mk.to_device(gi)
+    out2 = mk.alloc(rows * F // 32 * 40)
+    mk_.check(L().mk_silu_mul_q8(mk.h, dgi.ptr, rows, F, 1, out2.ptr))
+    assert np.array_equal(out2.download(np.uint8), out.download(np.uint8))
+
+
+def interleave4(gate, up):
+    """[.., F] gate and up -> [.., 2F] rows interleaved by 4: 4 gate values, then the 4 up values of the same outputs."""
+    lead = gate.shape[:-1]
+    g4 = gate.reshape(*lead, -1, 4)
+    u4 = up.reshape(*lead, -1, 4)
+    return np.concatenate([g4, u4], axis=-1).reshape(*lead, -1)
 
 
 @pytest.mark.parametrize("n", [16, 64, 2560, 4096, 5120, 8176, 8192])
@@ -175,6 +189,91 @@ def test_matmul_large_vs_oracle(mk, oracle, t, n, rows, k):
     yd = mk.to_device(base)
     _matmul(mk, t, packed, rows, k, xq.view(np.uint8), n, True, y=yd, accumulate=True)
     assert np.array_equal(bits(yd.download(np.float32).reshape(n, rows)), bits(base + exp))
+
+
+F32_CASES = [(t, n, rows, k) for t in (mk_.Q8_0, mk_.Q4_K, mk_.Q6_K) for n in (1, 2) for rows, k in ((64, 256), (96, 4096))] + [
+    (mk_.Q8_0, 1, 512, 8192),    # widest fused row: two 16-value chunks per thread
+    (mk_.Q8_0, 2, 48, 2560),     # a width that is not a multiple of 256
+    (mk_.Q6_K, 1, 40, 12288 // 2),
+]
+
+
+@pytest.mark.parametrize("t,n,rows,k", F32_CASES)
+def test_matmul_f32_matches_unfused(mk, oracle, t, n, rows, k):
+    """mk_matmul_f32 (rmsnorm / quantization inside the matmul) == mk_rmsnorm_q8 / mk_quantize_q8 + mk_matmul, and
+    both == the oracle."""
+    import make_golden
+    rng = np.random.default_rng(7 * t + 3 * n + rows + k)
+    w = make_golden.random_rows(rng, t, rows, k)
+    packed = _packed(mk, t, w, rows, k)
+    stride = k + 32  # a token stride wider than the row
+    x = np.zeros((n, stride), np.float32)
+    x[:, :k] = (rng.standard_normal((n, k)) * 3).astype(np.float32)
+    if n == 2:
+        x[1, :k] = 0.0  # zero row: rmsnorm scale from eps alone, d = 0 blocks
+    nw = rng.uniform(0.5, 1.5, k).astype(np.float32)
+    dx, dnw = mk.to_device(x), mk.to_device(nw)
+    wt = MkWeight(t, 1, rows, k, packed.p)
+    for norm in (True, False):
+        xq = mk.alloc(n * k // 32 * 40)
+        if norm:
+            for i in range(n):
+                mk_.check(L().mk_rmsnorm_q8(mk.h, ctypes.c_void_p(dx.p + i * stride * 4), None, dnw.ptr, 1, k,
+                                            ctypes.c_float(1e-6), ctypes.c_void_p(xq.p + i * (k // 32) * 40)))
+        else:
+            for i in range(n):
+                mk_.check(L().mk_quantize_q8(mk.h, ctypes.c_void_p(dx.p + i * stride * 4), 1, k,
+                                             ctypes.c_void_p(xq.p + i * (k // 32) * 40)))
+        base = rng.standard_normal((n, rows)).astype(np.float32)
+        y_ref = mk.to_device(base)
+        mk_.check(L().mk_matmul(mk.h, ctypes.byref(wt), xq.ptr, n, y_ref.ptr, rows, 1))
+        y = mk.to_device(base)
+        mk_.check(L().mk_matmul_f32(mk.h, ctypes.byref(wt), dx.ptr, stride, dnw.ptr if norm else None,
+                                    ctypes.c_float(1e-6), n, y.ptr, rows, 1, 0))
+        got, exp = y.download(np.float32), y_ref.download(np.float32)
+        assert np.array_equal(bits(got), bits(exp)), (norm, t, n, rows, k)
+        # and the unfused path against the oracle
+        xs = np.stack([oracle.rmsnorm(x[i, :k], nw, 1e-6) if norm else x[i, :k] for i in range(n)])
+        oq = oracle.quantize_row_q8(xs)
+        assert np.array_equal(xq.download(np.uint8), oq.view(np.uint8).reshape(-1))
+        ref = oracle.matmul(t, w, rows, k, oq.reshape(-1), wide=True)
+        assert np.array_equal(bits(got.reshape(n, rows)), bits(base + ref))
+
+
+@pytest.mark.parametrize("t,n,F,k", [(mk_.Q8_0, 1, 96, 4096), (mk_.Q8_0, 2, 64, 512), (mk_.Q4_K, 1, 64, 2048),
+                                     (mk_.Q6_K, 2, 32, 1024)])
+def test_matmul_f32_silu_pairs(mk, oracle, t, n, F, k):
+    """Gate/up rows interleaved by 4 with the silu epilogue == the plain matmul of the same rows, then the oracle's
+    silu_mul (kernels_avx512.cpp:271-280) on the de-interleaved gate and up."""
+    import make_golden
+    rng = np.random.default_rng(11 * t + n + F + k)
+    gate = make_golden.random_rows(rng, t, F, k)
+    up = make_golden.random_rows(rng, t, F, k)
+    rows = np.concatenate([np.concatenate([gate[4 * j:4 * j + 4], up[4 * j:4 * j + 4]]) for j in range(F // 4)])
+    packed = _packed(mk, t, rows, 2 * F, k)
+    x = (rng.standard_normal((n, k)) * 2).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, k).astype(np.float32)
+    dx, dnw = mk.to_device(x), mk.to_device(nw)
+    wt = MkWeight(t, 1, 2 * F, k, packed.p)
+    h = mk.alloc(n * F * 4)
+    mk_.check(L().mk_matmul_f32(mk.h, ctypes.byref(wt), dx.ptr, k, dnw.ptr, ctypes.c_float(1e-6), n, h.ptr, F, 0, 1))
+    gu = mk.alloc(n * 2 * F * 4)
+    mk_.check(L().mk_matmul_f32(mk.h, ctypes.byref(wt), dx.ptr, k, dnw.ptr, ctypes.c_float(1e-6), n, gu.ptr, 2 * F,
+                                0, 0))
+    gu = gu.download(np.float32).reshape(n, F // 4, 8)
+    g_, u_ = gu[:, :, :4].reshape(n, F), gu[:, :, 4:].reshape(n, F)
+    exp = np.stack([oracle.silu_mul(g_[i], u_[i]) for i in range(n)])
+    assert np.array_equal(bits(h.download(np.float32).reshape(n, F)), bits(exp))
+    # accumulate with the silu epilogue is refused
+    rc = L().mk_matmul_f32(mk.h, ctypes.byref(wt), dx.ptr, k, None, ctypes.c_float(0), n, h.ptr, F, 1, 1)
+    assert rc == mk_.MK_ERR_INVALID
+
+
+def test_matmul_f32_unsupported(mk):
+    wt = MkWeight(mk_.Q8_0, 0, 8, 64, None)
+    rc = L().mk_matmul_f32(mk.h, ctypes.byref(wt), None, 64, None, ctypes.c_float(0), 3, None, 8, 0, 0)
+    assert rc == mk_.MK_ERR_UNSUPPORTED
+    assert b"no fused kernel" in L().mk_last_error()
 
 
 def test_attend_gqa_golden(mk, golden):
