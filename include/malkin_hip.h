@@ -120,7 +120,9 @@ int mk_attend_gqa(mk_ctx* ctx, const float* q, int G, int D, const int8_t* k, co
                   ptrdiff_t soff, int n, float scale, float* out, const int32_t* extra, int ne);
 
 /* ---- device KV cache (replaces the reference's int8 LazyBytes kcache_ / vcache_, model.h:91, model.cpp:105-110) ----
- * Rows of head_dim int8 values with one float scale per row, indexed [layer][seq][kv_head][position]. */
+ * Rows of head_dim int8 values with one float scale per row, indexed [layer][seq][kv_head][position]. V rows hold
+ * the values in order; K rows are permuted so that the head_dim / 16 values one lane of the reference's scoring loop
+ * multiplies are contiguous: element e sits at byte (head_dim / 16) * (e % 16) + e / 16. */
 typedef struct {
   int8_t* k;
   int8_t* v;

@@ -508,6 +508,11 @@ void Model::kv_row(int layer, int seq, int pos, bool k, uint8_t* out) {
   for (int g = 0; g < KV; ++g) {
     const size_t row = ((static_cast<size_t>(layer) * n_seq_ + seq) * KV + g) * n_ctx_ + pos;
     ck(mk_download(ctx_, out + static_cast<size_t>(g) * D, (k ? kc_ : vc_).as<int8_t>() + row * D, D));
+    if (k) {  // device K rows are permuted (malkin_hip.h, mk_kv_cache): back to element order
+      std::vector<uint8_t> tmp(out + static_cast<size_t>(g) * D, out + static_cast<size_t>(g + 1) * D);
+      const int DC = D / 16;
+      for (int e = 0; e < D; ++e) out[static_cast<size_t>(g) * D + e] = tmp[DC * (e % 16) + e / 16];
+    }
     ck(mk_download(ctx_, out + static_cast<size_t>(KV) * D + 4 * g, (k ? ks_ : vs_).as<float>() + row, 4));
   }
 }

@@ -88,13 +88,16 @@ __global__ __launch_bounds__(64) void k_qk_norm_rope_kv(float* __restrict__ q, f
   const float d = amax / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
   const int64_t row = ((int64_t)seq[t] * KV + head) * n_ctx + kv_row[t];
   int8_t* dst = (is_v ? kv.v : kv.k) + row * D;
-  for (int i = lane; i < D; i += 64) dst[i] = (int8_t)(int)__builtin_rintf(sh[i] * id);
+  for (int i = lane; i < D; i += 64) dst[is_v ? i : kv_perm(i, D / 16)] = (int8_t)(int)__builtin_rintf(sh[i] * id);
   if (lane == 0) (is_v ? kv.vs : kv.ks)[row] = d;
 }
 
 // Attention of one query head per workgroup, attend_t semantics (D in {64,128,256}, G <= 16):
-//   scores  one key per thread: the 16 lane chains of attend_t (mul, then fma over D/16 chunks) from 16-byte K
-//           loads, the halving tree, times (kv_scale * scale); the first round of K rows is issued at entry;
+//   scores  the 16 lane chains of attend_t (mul, then fma over D/16 chunks), the halving tree, times
+//           (kv_scale * scale). Permuted K rows (the device cache): 16 lanes per key, lane l holding the D/16 values
+//           of chain l contiguously, so a wave reads 4 whole rows per instruction and the halving tree is a 16-lane
+//           shuffle tree. Rows in element order: one key per thread, from 16-byte loads. The first round of K rows
+//           is issued at entry;
 //   softmax exact max, e = exp512(s - max); the 16 sequential lane sums + tree run on otherwise idle threads while
 //           the P.V chains start;
 //   P.V     one sequential fma chain per output element over all keys in order. V is staged a tile of keys at a
@@ -119,12 +122,31 @@ struct AttnTile {
 };
 
 __host__ __device__ constexpr int attn_keys_pad(int nk) { return (nk + 15) & ~15; }
-// LDS: two V tiles, q, scores, p.
+// LDS: two V tiles, q, scores, p, the token's tree-ancestor rows.
 __host__ __device__ constexpr size_t attn_lds_bytes(int tile_bytes, int D, int nk_pad) {
-  return 2 * (size_t)tile_bytes + 4 * ((size_t)D + 2 * (size_t)nk_pad);
+  return 2 * (size_t)tile_bytes + 4 * ((size_t)D + 3 * (size_t)nk_pad);
 }
 
-template <int D>
+// DC = D / 16 bytes of a permuted K row: the values of one reference lane.
+template <int DC>
+struct KLane;
+template <>
+struct KLane<4> {
+  using T = uint32_t;
+  __device__ static int8_t at(T w, int c) { return (int8_t)(w >> (8 * c)); }
+};
+template <>
+struct KLane<8> {
+  using T = uint2;
+  __device__ static int8_t at(T w, int c) { return (int8_t)((c < 4 ? w.x : w.y) >> (8 * (c & 3))); }
+};
+template <>
+struct KLane<16> {
+  using T = uint4;
+  __device__ static int8_t at(T w, int c) { return (int8_t)((&w.x)[c >> 2] >> (8 * (c & 3))); }
+};
+
+template <int D, bool PERM>
 __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restrict__ q, int64_t q_stride,
                                                             float* __restrict__ out, int64_t out_stride, int G,
                                                             float scale, AttnAddr a, const int32_t* __restrict__ seqs,
@@ -157,6 +179,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
   float* qs = tiles + 2 * T::tile / 4;                           // D
   float* sc = qs + D;                                            // nk_pad: scores, then e^(s - max)
   float* pv = sc + nk_pad;                                       // nk_pad: e * v-scale, zero past nk
+  int* anc_s = reinterpret_cast<int*>(pv + nk_pad);              // ne: KV rows of keys n0 .. nk - 1
   __shared__ float red[kAttnThreads / 64];
   __shared__ float inv_s;
   const int64_t sq = seqs[t];
@@ -164,7 +187,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
   const int8_t* vb = a.v + sq * a.k_seq + g * a.k_head;
   const char* ksb = a.ks + sq * a.s_seq + g * a.s_head;
   const char* vsb = a.vs + sq * a.s_seq + g * a.s_head;
-  auto key_row = [&](int j) -> int64_t { return j < n0 ? j : anc[e0 + j - n0]; };
+  // Tree ancestors go to LDS first: a key row read from global memory would make every later load wait for all
+  // earlier ones (the compiler's wait counts are per wave and in order), serialising the K and V prefetches.
+  if (ne > 0) {
+    for (int i = tid; i < ne; i += kAttnThreads) anc_s[i] = anc[e0 + i];
+    lds_barrier();
+  }
+  auto key_row = [&](int j) -> int64_t { return j < n0 ? j : anc_s[j - n0]; };
 
   // V staging: task = 4 consecutive keys x 16 consecutive values, written as 16 float4 of the transposed tile.
   constexpr int NG = T::groups;
@@ -194,39 +223,95 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
     }
   };
   const int chunks = (nk + T::chunk - 1) / T::chunk;
-  for (int c = 0; c < NG && c < chunks; ++c) load_chunk(c);  // the first NG tiles are in flight during the scores
-
-  // K row, key scale and value scale of key j.
-  int4 kv[DC];
-  float kscale = 0.0f, vscale = 0.0f;
-  auto load_key = [&](int j) {
-    const int64_t row = key_row(j);
-    const int4* kr = reinterpret_cast<const int4*>(kb + row * a.k_row);
-#pragma unroll
-    for (int c = 0; c < DC; ++c) kv[c] = kr[c];
-    kscale = *reinterpret_cast<const float*>(ksb + row * a.s_row);
-    vscale = *reinterpret_cast<const float*>(vsb + row * a.s_row);
-  };
-  if (tid < nk) load_key(tid);
+  // q first (its wait then covers it alone), then each staging group's first tile: in flight during the scores.
   const float* qh = q + t * q_stride + (int64_t)h * D;
-  for (int i = tid; i < D; i += kAttnThreads) qs[i] = qh[i];
-  lds_barrier();
+  const float qv = tid < D ? qh[tid] : 0.0f;
+  if (stager && grp < chunks) load_chunk(grp);
 
-  // Scores (kernels_avx512.cpp:234-244).
-  for (int j = tid; j < nk; j += kAttnThreads) {
-    if (j != tid) load_key(j);
-    float lanes[16];
+  if constexpr (PERM) {
+    // 16 lanes per key: group grp of the workgroup takes keys grp, grp + 64, ...; KB keys per group in flight.
+    // Loads are never predicated (past the last key they re-read it, unused), so the compiler's wait counts stay
+    // exact and the next round's loads overlap this round's arithmetic.
+    using KL = KLane<DC>;
+    constexpr int NGR = kAttnThreads / 16, KB = DC >= 16 ? 4 : 8;
+    const int gl = tid & 15, grp = tid >> 4;
+    struct Round {
+      typename KL::T k[KB];
+      float ks[KB], vs[KB];
+    };
+    auto fetch = [&](Round& R, int r) {
 #pragma unroll
-    for (int c = 0; c < DC; ++c) {
-      const int w[4] = {kv[c].x, kv[c].y, kv[c].z, kv[c].w};
-#pragma unroll
-      for (int l = 0; l < 16; ++l) {
-        const float kf = (float)(int8_t)(w[l >> 2] >> (8 * (l & 3)));
-        lanes[l] = c == 0 ? qs[l] * kf : fma_(qs[16 * c + l], kf, lanes[l]);
+      for (int b = 0; b < KB; ++b) {
+        const int j = min((r * KB + b) * NGR + grp, nk - 1);
+        const int64_t row = key_row(j);
+        R.k[b] = *reinterpret_cast<const typename KL::T*>(kb + row * a.k_row + DC * gl);
+        R.ks[b] = *reinterpret_cast<const float*>(ksb + row * a.s_row);
+        R.vs[b] = *reinterpret_cast<const float*>(vsb + row * a.s_row);
       }
+    };
+    const int rounds = (nk + NGR * KB - 1) / (NGR * KB);
+    Round RA, RB;
+    fetch(RA, 0);
+    if (tid < D) qs[tid] = qv;
+    lds_barrier();
+    float qr[DC];  // q of chain gl: q[16 c + gl]
+#pragma unroll
+    for (int c = 0; c < DC; ++c) qr[c] = qs[16 * c + gl];
+    auto score = [&](const Round& R, int r) {
+#pragma unroll
+      for (int b = 0; b < KB; ++b) {
+        const int j = (r * KB + b) * NGR + grp;
+        if (j < nk) {  // uniform over the 16 lanes of the key
+          float acc = qr[0] * (float)KL::at(R.k[b], 0);
+#pragma unroll
+          for (int c = 1; c < DC; ++c) acc = fma_(qr[c], (float)KL::at(R.k[b], c), acc);
+          acc = reduce16_lanes(acc);
+          if (gl == 0) {
+            sc[j] = acc * (R.ks[b] * scale);
+            pv[j] = R.vs[b];
+          }
+        }
+      }
+    };
+    for (int r = 0; r < rounds; r += 2) {
+      fetch(RB, min(r + 1, rounds - 1));
+      score(RA, r);
+      if (r + 1 >= rounds) break;
+      fetch(RA, min(r + 2, rounds - 1));
+      score(RB, r + 1);
     }
-    sc[j] = reduce16(lanes) * (kscale * scale);
-    pv[j] = vscale;
+  } else {
+    // K row, key scale and value scale of key j.
+    int4 kv[DC];
+    float kscale = 0.0f, vscale = 0.0f;
+    auto load_key = [&](int j) {
+      const int64_t row = key_row(j);
+      const int4* kr = reinterpret_cast<const int4*>(kb + row * a.k_row);
+#pragma unroll
+      for (int c = 0; c < DC; ++c) kv[c] = kr[c];
+      kscale = *reinterpret_cast<const float*>(ksb + row * a.s_row);
+      vscale = *reinterpret_cast<const float*>(vsb + row * a.s_row);
+    };
+    if (tid < nk) load_key(tid);
+    if (tid < D) qs[tid] = qv;
+    lds_barrier();
+
+    // Scores (kernels_avx512.cpp:234-244).
+    for (int j = tid; j < nk; j += kAttnThreads) {
+      if (j != tid) load_key(j);
+      float lanes[16];
+#pragma unroll
+      for (int c = 0; c < DC; ++c) {
+        const int w[4] = {kv[c].x, kv[c].y, kv[c].z, kv[c].w};
+#pragma unroll
+        for (int l = 0; l < 16; ++l) {
+          const float kf = (float)(int8_t)(w[l >> 2] >> (8 * (l & 3)));
+          lanes[l] = c == 0 ? qs[l] * kf : fma_(qs[16 * c + l], kf, lanes[l]);
+        }
+      }
+      sc[j] = reduce16(lanes) * (kscale * scale);
+      pv[j] = vscale;
+    }
   }
   store_chunk(0);
   if (NG < chunks) load_chunk(NG);
@@ -320,10 +405,11 @@ __global__ __launch_bounds__(256) void k_attention_generic(const float* __restri
     const int64_t row = j < n0 ? j : anc[e0 + j - n0];
     const int8_t* kr = kb + row * a.k_row;
     const float kscale = *reinterpret_cast<const float*>(ksb + row * a.s_row);
+    auto kat = [&](int e) { return (float)kr[a.k_perm ? kv_perm(e, D / 16) : e]; };
     float lanes[16];
-    for (int l = 0; l < 16; ++l) lanes[l] = qs[l] * (float)kr[l];
+    for (int l = 0; l < 16; ++l) lanes[l] = qs[l] * kat(l);
     for (int c = 16; c < D; c += 16)
-      for (int l = 0; l < 16; ++l) lanes[l] = fma_(qs[c + l], (float)kr[c + l], lanes[l]);
+      for (int l = 0; l < 16; ++l) lanes[l] = fma_(qs[c + l], kat(c + l), lanes[l]);
     sc[j] = reduce16(lanes) * kscale * scale;  // (dot * kv_scale) * scale
   }
   __syncthreads();
@@ -508,11 +594,11 @@ void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int6
                          seq, n_keys, anc_off, anc, n, H);
     };
     if (D == 64)
-      go(k_attention<64>);
+      a.k_perm ? go(k_attention<64, true>) : go(k_attention<64, false>);
     else if (D == 128)
-      go(k_attention<128>);
+      a.k_perm ? go(k_attention<128, true>) : go(k_attention<128, false>);
     else
-      go(k_attention<256>);
+      a.k_perm ? go(k_attention<256, true>) : go(k_attention<256, false>);
   } else {
     const size_t lds = (size_t)(D + 2 * (size_t)max_keys) * sizeof(float);
     require(lds <= 60 * 1024, "attention: too many keys for one workgroup");

@@ -204,7 +204,7 @@ int mk_attend_gqa(mk_ctx* c, const float* q, int G, int D, const int8_t* k, cons
     check(hipMalloc(&dm, sizeof meta), "hipMalloc");
     check(hipMemcpyAsync(dm, meta, sizeof meta, hipMemcpyHostToDevice, c->stream), "hipMemcpy H2D");
     mk::AttnAddr a{k, v, reinterpret_cast<const char*>(k) + soff, reinterpret_cast<const char*>(v) + soff,
-                   0, 0, (int64_t)stride, 0, 0, (int64_t)stride};
+                   0, 0, (int64_t)stride, 0, 0, (int64_t)stride, 0};
     try {
       mk::attention(c->stream, q, (int64_t)G * D, out, (int64_t)G * D, 1, G, 1, D, scale, a, dm, dm + 1,
                     ne > 0 ? dm + 2 : nullptr, extra, n + ne);
@@ -243,7 +243,7 @@ int mk_attention(mk_ctx* c, const float* q, int64_t q_stride, float* out, int64_
     const int64_t rows = (int64_t)kv->n_ctx;
     mk::AttnAddr a{L.k, L.v, reinterpret_cast<const char*>(L.ks), reinterpret_cast<const char*>(L.vs),
                    (int64_t)kv->n_head_kv * rows * D, rows * D, D,
-                   (int64_t)kv->n_head_kv * rows * 4, rows * 4, 4};
+                   (int64_t)kv->n_head_kv * rows * 4, rows * 4, 4, 1};
     const float scale = 1.0f / std::sqrt(static_cast<float>(D));  // model.cpp:208
     mk::attention(c->stream, q, q_stride, out, out_stride, n, n_head, kv->n_head_kv, D, scale, a, seq, n_keys, anc_off,
                   anc, max_keys);

@@ -76,6 +76,7 @@ void gemm_q8_0(hipStream_t s, const void* w, int64_t rows, int64_t cols, const B
 
 // Generic attention addressing: key row (t, g, row) at k + seq*k_seq + g*k_head + row*k_row (bytes), its scale at
 // ks + seq*s_seq + g*s_head + row*s_row (bytes); values likewise with v / vs.
+// k_perm: K rows are stored permuted (kv_perm below), as the device KV cache keeps them; else in element order.
 struct AttnAddr {
   const int8_t* k;
   const int8_t* v;
@@ -83,7 +84,12 @@ struct AttnAddr {
   const char* vs;
   int64_t k_seq, k_head, k_row;
   int64_t s_seq, s_head, s_row;
+  int k_perm;
 };
+
+// Byte position of element e in a permuted K row of D = 16 * DC values: the DC values a reference lane l
+// (kernels_avx512.cpp:234-244) multiplies, e = 16 c + l for c < DC, are contiguous at DC * l.
+__host__ __device__ constexpr int kv_perm(int e, int DC) { return DC * (e & 15) + (e >> 4); }
 // q [n][H*D] (token stride q_stride floats), out [n][H*D] (stride out_stride). Per token t: keys rows
 // 0..n_keys[t]-1 of sequence seq[t], then anc[anc_off[t] .. anc_off[t+1]) when anc_off is non-null.
 void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int H, int KV,
