@@ -37,6 +37,12 @@ HIP_FLAGS = [
     f"-I{ROOT}/include",
 ]
 
+# Per-source extra flags. gemm.hip: MFMA results in ordinary VGPRs (its epilogue reads every accumulator element
+# with VALU instructions; the AGPR form would add one v_accvgpr_read per element and block).
+EXTRA_FLAGS = {
+    "csrc/kernels/gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
 LIB = os.path.join(HERE, "libmalkin_hip.so")
 SYNTH = os.path.join(HERE, "libmalkin_synth.so")
 
@@ -59,7 +65,7 @@ def build_hip(jobs=None, verbose=False):
 
     def compile_one(s):
         lang = ["-x", "hip"] if s.endswith(".hip") else []
-        cmd = [HIPCC] + HIP_FLAGS + lang + ["-c", os.path.join(HERE, s), "-o", _obj(s)]
+        cmd = [HIPCC] + HIP_FLAGS + EXTRA_FLAGS.get(s, []) + lang + ["-c", os.path.join(HERE, s), "-o", _obj(s)]
         out = _run(cmd)
         if verbose and out.strip():
             print(out)
