@@ -10,6 +10,8 @@
 namespace mk {
 namespace {
 
+typedef int v4i __attribute__((ext_vector_type(4)));
+
 // One wavefront per (token, head): heads [0, H) are query heads, [H, H+KV) key heads, [H+KV, H+2KV) value heads.
 // Every global operand (the head's values, its norm weights, the RoPE row) is loaded up front.
 constexpr int kQkMaxPer = 4;  // D <= 256: up to 4 values per lane
@@ -374,6 +376,225 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
   if (tid < D) out[t * out_stride + (int64_t)h * D + tid] = acc * inv_s;
 }
 
+// Attention of many query rows at once (prefill and other long plain batches), attend_t semantics for D in {64, 128}
+// and G <= 16, bit-identical to k_attention. A workgroup takes the 16 / G consecutive tokens of one token block and
+// the G query heads of one KV group: up to 16 query rows that share every K and V row they read, so each key is
+// loaded and converted once per 16 rows instead of once per row.
+//   scores  one thread per key: its K row converted to fp32 in registers once, then for each row the 16 lane chains
+//           (mul, then fma over the D/16 chunks), the halving tree, times (kv_scale * scale). q is uniform over the
+//           workgroup and is read through the scalar unit;
+//   softmax 16 threads per row: the row's exact max (keys < n_keys of its token), then the 16 sequential lane sums
+//           of e = exp512(s - max), each thread one lane l (keys l, l + 16, ...), and the halving tree; the row's
+//           P.V coefficient e * v_scale replaces the score in LDS, 0 past the row's last key;
+//   P.V     one sequential fma chain per (row, value) over all keys in order; a lane owns 2 rows x D/32 values. V is
+//           staged a tile of keys at a time into LDS as fp32 (double-buffered, one 16-byte load per thread per tile)
+//           and read as D/32 consecutive floats per key; the row's coefficients come from LDS once per 16 keys and
+//           are broadcast by DPP. Keys past a row's end have coefficient 0 and fma(0, v, acc) == acc.
+// Tokens of a block that belong to different sequences are handled one sequence at a time (the rows of the other
+// sequences sit out that pass).
+constexpr int kRowsThreads = 256;
+constexpr int kRowsMax = 16;       // query rows per workgroup
+constexpr int kRowsMinTokens = 16; // shorter batches take the per-token kernel (decode, small multi-sequence batches)
+
+template <int D>
+struct RowsCfg {
+  static constexpr int DC = D / 16;
+  static constexpr int ck = 4096 / D;      // keys per V tile: one 16-byte load per thread
+  static constexpr int stride = D + 4;     // floats per tile row
+  static constexpr int tile = ck * stride; // floats per tile
+  static constexpr int dl = D / 32;        // P.V values per lane
+};
+
+// LDS: two V tiles, scores [16][nk_pad], v scales [nk_pad].
+__host__ __device__ constexpr size_t rows_lds_bytes(int D, int nk_pad) {
+  return 4 * (2 * (size_t)(4096 / D) * (size_t)(D + 4) + (size_t)(kRowsMax + 1) * (size_t)nk_pad);
+}
+
+template <int D, bool PERM>
+__global__ __launch_bounds__(kRowsThreads) void k_attention_rows(const float* __restrict__ q, int64_t q_stride,
+                                                                 float* __restrict__ out, int64_t out_stride, int G,
+                                                                 float scale, AttnAddr a,
+                                                                 const int32_t* __restrict__ seqs,
+                                                                 const int32_t* __restrict__ n_keys, int n, int KV,
+                                                                 int nk_pad) {
+  using C = RowsCfg<D>;
+  constexpr int DC = C::DC;
+  const int tid = threadIdx.x;
+  const int TQ = kRowsMax / G, nblk = (n + TQ - 1) / TQ;
+  // Workgroup -> (KV group, token block). XCD x (workgroups x, x + 8, ...) takes a contiguous run of
+  // (group, block) pairs, so a group's K/V rows are read into one L2; within a group the blocks with the most keys
+  // start first.
+  int g, blk;
+  {
+    const int total = nblk * KV, w = (int)blockIdx.x;
+    const int pair = total % 8 == 0 ? (w % 8) * (total / 8) + w / 8 : w;
+    g = pair / nblk;
+    blk = nblk - 1 - pair % nblk;
+  }
+  const int t0 = blk * TQ, tq = min(TQ, n - t0), R = tq * G;
+  extern __shared__ int4 smem4[];
+  float* tiles = reinterpret_cast<float*>(smem4);  // 2 x [ck][stride]
+  float* sc = tiles + 2 * C::tile;                 // [16][nk_pad]: scores, then P.V coefficients
+  float* vsc = sc + kRowsMax * nk_pad;             // [nk_pad]: v scales
+  __shared__ int seq_s[kRowsMax], nk_s[kRowsMax];
+  __shared__ float inv_s[kRowsMax];
+  // Row r: token t0 + r / G, query head g * G + r % G.
+  if (tid < kRowsMax) {
+    const int t = t0 + min(tid / G, tq - 1);
+    const int sv = seqs[t], kv = n_keys[t];
+    seq_s[tid] = tid < R ? sv : -1;
+    nk_s[tid] = tid < R ? kv : 0;
+  }
+  lds_barrier();
+
+  const int LR = tid >> 4, dl = tid & 15;
+  const int ra = 2 * (LR >> 1), rb = ra + 1;               // P.V rows of this lane
+  const int d0 = (LR & 1) * (D / 2) + dl * C::dl;          // P.V values d0 .. d0 + dl - 1
+  const int kk = tid / (D / 16), seg = tid % (D / 16);     // V staging: key kk of the tile, bytes 16 seg ..
+  const uint32_t all = R >= 32 ? ~0u : (1u << R) - 1;
+  uint32_t done = 0;
+  while (done != all) {
+    // The pass's sequence: that of the first row not done; its rows and their longest key range.
+    const int s = __builtin_amdgcn_readfirstlane(seq_s[__builtin_ctz(~done)]);
+    uint32_t act = 0;
+    int nkb = 1;
+    for (int r = 0; r < R; ++r) {
+      const int sr = __builtin_amdgcn_readfirstlane(seq_s[r]);
+      if (sr == s) {
+        act |= 1u << r;
+        nkb = max(nkb, __builtin_amdgcn_readfirstlane(nk_s[r]));
+      }
+    }
+    nkb = min(nkb, nk_pad);  // nk_pad covers max_keys, which bounds every token's keys
+    const int nkb_pad = attn_keys_pad(nkb);
+    const int8_t* kb = a.k + (int64_t)s * a.k_seq + g * a.k_head;
+    const int8_t* vb = a.v + (int64_t)s * a.k_seq + g * a.k_head;
+    const char* ksb = a.ks + (int64_t)s * a.s_seq + g * a.s_head;
+    const char* vsb = a.vs + (int64_t)s * a.s_seq + g * a.s_head;
+
+    // Scores (kernels_avx512.cpp:234-244). Loads are never predicated: past the last key they re-read it, unused.
+    for (int j0 = 0; j0 < nkb; j0 += kRowsThreads) {
+      const int j = min(j0 + tid, nkb - 1);
+      const bool live = j0 + tid < nkb;
+      v4i kw[D / 16];
+#pragma unroll
+      for (int u = 0; u < D / 16; ++u) kw[u] = *reinterpret_cast<const v4i*>(kb + (int64_t)j * a.k_row + 16 * u);
+      const float ksv = *reinterpret_cast<const float*>(ksb + (int64_t)j * a.s_row);
+      const float vsv = *reinterpret_cast<const float*>(vsb + (int64_t)j * a.s_row);
+      float kf[16][DC];  // kf[l][c] = k[16 c + l]
+#pragma unroll
+      for (int l = 0; l < 16; ++l)
+#pragma unroll
+        for (int c = 0; c < DC; ++c) {
+          const int e = PERM ? DC * l + c : 16 * c + l;  // byte of element 16 c + l
+          kf[l][c] = (float)(int8_t)(kw[e >> 4][(e >> 2) & 3] >> (8 * (e & 3)));
+        }
+      if (live) vsc[j] = vsv;
+      const float kss = ksv * scale;
+      for (int r = 0; r < R; ++r) {
+        if (!((act >> r) & 1)) continue;
+        const float* qr = q + (int64_t)(t0 + r / G) * q_stride + (int64_t)(g * G + r % G) * D;
+        float lanes[16];
+#pragma unroll
+        for (int l = 0; l < 16; ++l) lanes[l] = qr[l] * kf[l][0];
+#pragma unroll
+        for (int c = 1; c < DC; ++c)
+#pragma unroll
+          for (int l = 0; l < 16; ++l) lanes[l] = fma_(qr[16 * c + l], kf[l][c], lanes[l]);
+        const float sres = reduce16(lanes) * kss;
+        if (live) sc[r * nk_pad + j] = sres;
+      }
+    }
+    lds_barrier();
+
+    // softmax_inplace (kernels_avx512.cpp:205-226): thread (row LR, lane dl).
+    {
+      const bool on = LR < R && ((act >> LR) & 1);
+      const int nkr = on ? nk_s[LR] : 0;
+      float* srow = sc + LR * nk_pad;
+      float m = -INFINITY;
+      for (int j = dl; j < nkr; j += 16) m = fmaxf(m, srow[j]);
+#pragma unroll
+      for (int off = 8; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
+      float sum = 0.0f;
+      if (on) {
+        for (int j = dl; j < nkb_pad; j += 16) {
+          const bool in = j < nkr;
+          const float e = in ? exp512(srow[j] - m) : 0.0f;
+          sum = sum + e;  // past the row's end e = +0: the sum is unchanged
+          srow[j] = in ? e * vsc[j] : 0.0f;
+        }
+      }
+      sum = reduce16_lanes(sum);
+      if (dl == 0) inv_s[LR] = 1.0f / sum;
+    }
+
+    // P.V (kernels_avx512.cpp:247-265).
+    v4i vr;
+    auto vload = [&](int c) {
+      const int j = min(c * C::ck + kk, nkb - 1);
+      vr = *reinterpret_cast<const v4i*>(vb + (int64_t)j * a.k_row + 16 * seg);
+    };
+    auto vstore = [&](int c) {
+      float* dst = tiles + (c & 1) * C::tile + kk * C::stride + 16 * seg;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t x = (uint32_t)vr[w];
+        *reinterpret_cast<float4*>(dst + 4 * w) =
+            make_float4((float)(int8_t)x, (float)(int8_t)(x >> 8), (float)(int8_t)(x >> 16), (float)(int8_t)(x >> 24));
+      }
+    };
+    const int nch = (nkb_pad + C::ck - 1) / C::ck;
+    vload(0);
+    vstore(0);
+    vload(1);
+    lds_barrier();
+    float acc0[C::dl], acc1[C::dl];
+#pragma unroll
+    for (int k = 0; k < C::dl; ++k) acc0[k] = acc1[k] = 0.0f;
+    for (int c = 0; c < nch; ++c) {
+      const float* tile = tiles + (c & 1) * C::tile + d0;
+      const int j0 = c * C::ck;
+      const int len = min(C::ck, nkb_pad - j0);  // a multiple of 16
+      for (int jj = 0; jj < len; jj += 16) {
+        const float pa = sc[ra * nk_pad + j0 + jj + dl], pb = sc[rb * nk_pad + j0 + jj + dl];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float p0 = bcast16(pa, i), p1 = bcast16(pb, i);
+          float v[C::dl];
+          if constexpr (C::dl == 4) {
+            const float4 t = *reinterpret_cast<const float4*>(tile + (jj + i) * C::stride);
+            v[0] = t.x, v[1] = t.y, v[2] = t.z, v[3] = t.w;
+          } else {
+            const float2 t = *reinterpret_cast<const float2*>(tile + (jj + i) * C::stride);
+            v[0] = t.x, v[1] = t.y;
+          }
+#pragma unroll
+          for (int k = 0; k < C::dl; ++k) {
+            acc0[k] = fma_(p0, v[k], acc0[k]);
+            acc1[k] = fma_(p1, v[k], acc1[k]);
+          }
+        }
+      }
+      if (c + 1 < nch) vstore(c + 1);
+      lds_barrier();
+      vload(c + 2);
+    }
+    auto put = [&](int r, const float* acc) {
+      if (r < R && ((act >> r) & 1)) {
+        float* o = out + (int64_t)(t0 + r / G) * out_stride + (int64_t)(g * G + r % G) * D + d0;
+        const float inv = inv_s[r];
+#pragma unroll
+        for (int k = 0; k < C::dl; ++k) o[k] = acc[k] * inv;
+      }
+    };
+    put(ra, acc0);
+    put(rb, acc1);
+    done |= act;
+    lds_barrier();  // the next pass rewrites sc, vsc and the tiles
+  }
+}
+
 // Other head sizes or G > 16: the per-head path of attend_gqa (kernels_avx512.cpp:296-305), one query head per
 // workgroup, byte loads.
 __global__ __launch_bounds__(256) void k_attention_generic(const float* __restrict__ q, int64_t q_stride,
@@ -578,7 +799,27 @@ void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int6
                        reinterpret_cast<uintptr_t>(a.k) % 16 == 0 && reinterpret_cast<uintptr_t>(a.v) % 16 == 0 &&
                        a.s_row % 4 == 0 && reinterpret_cast<uintptr_t>(a.ks) % 4 == 0 &&
                        reinterpret_cast<uintptr_t>(a.vs) % 4 == 0;
-  if (G <= 16 && (D == 64 || D == 128 || D == 256) && aligned) {
+  if (!anc_off && n >= kRowsMinTokens && G <= 16 && (D == 64 || D == 128) && aligned &&
+      rows_lds_bytes(D, attn_keys_pad(max_keys)) <= 160 * 1024 - 1024) {
+    const int nk_pad = attn_keys_pad(max_keys);
+    const size_t lds = rows_lds_bytes(D, nk_pad);
+    auto go = [&](auto kernel) {
+      static bool attr = false;
+      if (!attr) {
+        check(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  160 * 1024 - 1024),
+              "hipFuncSetAttribute");
+        attr = true;
+      }
+      const int TQ = kRowsMax / G;
+      hipLaunchKernelGGL(kernel, dim3(((n + TQ - 1) / TQ) * KV), dim3(kRowsThreads), lds, s, q, q_stride, out,
+                         out_stride, G, scale, a, seq, n_keys, n, KV, nk_pad);
+    };
+    if (D == 64)
+      a.k_perm ? go(k_attention_rows<64, true>) : go(k_attention_rows<64, false>);
+    else
+      a.k_perm ? go(k_attention_rows<128, true>) : go(k_attention_rows<128, false>);
+  } else if (G <= 16 && (D == 64 || D == 128 || D == 256) && aligned) {
     const int tile = D == 64 ? AttnTile<64>::tile : D == 128 ? AttnTile<128>::tile : AttnTile<256>::tile;
     const size_t lds = attn_lds_bytes(tile, D, attn_keys_pad(max_keys));
     require(lds <= 160 * 1024 - 1024, "attention: too many keys for one workgroup");

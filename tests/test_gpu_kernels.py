@@ -332,3 +332,65 @@ def test_errors_are_statuses(mk):
     assert b"no kernel" in L().mk_last_error()
     rc = L().mk_silu_mul(mk.h, 17, None, None)
     assert rc == mk_.MK_ERR_UNSUPPORTED
+
+
+class KvCache(ctypes.Structure):
+    _fields_ = [("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("k_scale", ctypes.c_void_p),
+                ("v_scale", ctypes.c_void_p), ("n_layer", ctypes.c_int32), ("n_seq", ctypes.c_int32),
+                ("n_head_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("n_ctx", ctypes.c_int32)]
+
+
+def _kv_perm(D):
+    """Element e of a K row sits at byte D/16 * (e % 16) + e // 16 of the device cache's permuted row."""
+    e = np.arange(D)
+    return (D // 16) * (e % 16) + e // 16
+
+
+# (D, H, KV, token seqs, token key counts, n_ctx): the multi-row kernel for plain batches of 16+ tokens, and the
+# per-token kernel past its LDS limit.
+ROWS_CASES = [
+    (128, 32, 8, [0] * 64, [600 + t + 1 for t in range(64)], 700),                  # prefill continuation, G = 4
+    (64, 8, 2, [0] * 13 + [1] * 24, [40 + t for t in range(13)] + [5 + t for t in range(24)], 64),  # mixed blocks
+    (128, 16, 1, [1] * 20, [t + 1 for t in range(20)], 32),                           # G = 16: one token per block
+    (128, 5, 1, [0] * 17, [100 + 3 * t for t in range(17)], 160),                     # G = 5: 15 rows per block
+    (64, 4, 4, [t % 3 for t in range(40)], [1 + t for t in range(40)], 48),          # G = 1, 3 sequences per block
+    (128, 8, 4, [0] * 16, [1840 - t for t in range(16)], 1840),                       # longest rows in LDS
+    (128, 8, 4, [0] * 16, [1900 - t for t in range(16)], 1900),                       # per-token kernel
+]
+
+
+@pytest.mark.parametrize("case", range(len(ROWS_CASES)))
+def test_attention_batch_vs_oracle(mk, oracle, case):
+    D, H, KV, seqs, nks, n_ctx = ROWS_CASES[case]
+    G, n, n_seq = H // KV, len(seqs), max(seqs) + 1
+    print("attention case", case, dict(D=D, H=H, KV=KV, n=n), flush=True)
+    rng = np.random.default_rng(300 + case)
+    k8 = rng.integers(-127, 128, (n_seq, KV, n_ctx, D), dtype=np.int8)
+    v8 = rng.integers(-127, 128, (n_seq, KV, n_ctx, D), dtype=np.int8)
+    ks = rng.uniform(0.001, 0.05, (n_seq, KV, n_ctx)).astype(np.float32)
+    vs = rng.uniform(0.001, 0.05, (n_seq, KV, n_ctx)).astype(np.float32)
+    q = rng.standard_normal((n, H * D)).astype(np.float32)
+    dk = mk.to_device(np.ascontiguousarray(k8[..., np.argsort(_kv_perm(D))]))
+    dv, dks, dvs, dq = mk.to_device(v8), mk.to_device(ks), mk.to_device(vs), mk.to_device(q)
+    dseq, dnk = mk.to_device(np.array(seqs, np.int32)), mk.to_device(np.array(nks, np.int32))
+    out = mk.alloc(n * H * D * 4)
+    kv = KvCache(dk.ptr, dv.ptr, dks.ptr, dvs.ptr, 1, n_seq, KV, D, n_ctx)
+    mk_.check(L().mk_attention(mk.h, dq.ptr, H * D, out.ptr, H * D, n, H, ctypes.byref(kv), 0, dseq.ptr, dnk.ptr,
+                               None, None, max(nks)))
+    got = out.download(np.float32).reshape(n, H * D)
+    # The reference's KV rows: KV heads x D int8, then KV float scales (model.cpp:105-110).
+    row = KV * D + 4 * KV
+    scale = np.float32(1.0) / np.sqrt(np.float32(D))
+    for s in sorted(set(seqs)):
+        kb = np.zeros((n_ctx, row), np.uint8)
+        vb = np.zeros((n_ctx, row), np.uint8)
+        kb[:, :KV * D] = k8[s].transpose(1, 0, 2).reshape(n_ctx, KV * D).view(np.uint8)
+        vb[:, :KV * D] = v8[s].transpose(1, 0, 2).reshape(n_ctx, KV * D).view(np.uint8)
+        kb[:, KV * D:] = ks[s].T.copy().view(np.uint8).reshape(n_ctx, 4 * KV)
+        vb[:, KV * D:] = vs[s].T.copy().view(np.uint8).reshape(n_ctx, 4 * KV)
+        kf, vf = kb.reshape(-1), vb.reshape(-1)
+        for t in (t for t in range(n) if seqs[t] == s):
+            for g in range(KV):
+                exp = oracle.attend_gqa(q[t, g * G * D:(g + 1) * G * D], G, D, kf[g * D:], vf[g * D:], row,
+                                        (KV - g) * D + 4 * g, nks[t], scale)
+                assert np.array_equal(bits(got[t, g * G * D:(g + 1) * G * D]), bits(exp)), (case, t, g)
