@@ -6,11 +6,13 @@ head_dim 128, FFN 12288, vocab 151936, untied LM head), ctx 4096, batch 1 — a 
 from the prompt's logits, 127 decode forwards), as `malkin bench` does (main.cpp:126-143).
 
 value = (512 + 128) tokens / wall time of the step, inputs (weights, prompt) resident in HBM before the timed region.
-The JSON line also carries pp512 and tg128 rates, the live roofline of the dominant kernel (the Q8_0 decode GEMV,
-timed with HIP events on the library's stream) and the reference's own AVX-512 path timed on this host's cores on a
-bounded sample of the same workload (cpu_baseline).
+The JSON line also carries pp512 and tg128 rates, the prefill's fraction of the int8 MFMA peak, the live roofline of
+the dominant kernel (the Q8_0 decode GEMV, timed with HIP events on the library's stream; its HBM traffic from the
+committed counter summary), the kernel-level configurations 1 and 2 of BASELINE.json (kernel_configs), and the
+reference's own AVX-512 path timed on this host's cores on a bounded sample of the same workload (cpu_baseline).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-kernel-configs]
+    python bench.py --probe traffic     # launch sequence for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
 """
 import argparse
 import json
@@ -86,9 +88,146 @@ def gemv_roofline(ctx, model, cfg, reps=3):
     per_launch_s = best / 1e3 / launches
     achieved = algo / launches / per_launch_s / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": roofline_traffic(),
             "kernel": "k_gemv<Q8_0, n=1> (decode GEMV, 144 launches per token)",
             "bytes_per_launch": int(algo / launches), "us_per_launch": round(per_launch_s * 1e6, 2)}
+
+
+# GGUF block geometry: (values per block, bytes per block, byte offsets of the f16 scales).
+_BLOCKS = {8: (32, 34, (0,)), 12: (256, 144, (0, 2)), 14: (256, 210, (208,))}
+INT8_PEAK_TOPS = 5000.0
+
+
+def random_weight(rng, t, rows, cols):
+    """Random GGUF rows of type t (timing input): random quant bytes, f16 scales drawn from [0.001, 0.02]."""
+    qk, bs, offs = _BLOCKS[t]
+    nb = cols // qk
+    data = rng.integers(0, 256, size=(rows, nb, bs), dtype=np.uint8)
+    for o in offs:
+        data[:, :, o:o + 2] = rng.uniform(0.001, 0.02, (rows, nb)).astype(np.float16).view(np.uint8).reshape(
+            rows, nb, 2)
+    return data.reshape(rows, nb * bs)
+
+
+def pack_copies(ctx, t, host_rows, rows, cols, copies):
+    """`copies` packed device copies of one weight (distinct addresses, so rotating them defeats the 256 MB cache)."""
+    import ctypes
+    import malkin_amd as mk
+    L = mk.load()
+    src = ctx.to_device(host_rows)
+    out = []
+    for _ in range(copies):
+        b = ctx.alloc(L.mk_packed_bytes(t, rows, cols))
+        mk.check(L.mk_pack_weight(ctx.h, t, src.ptr, host_rows.shape[1], rows, cols, b.ptr))
+        out.append((b, mk.MkWeight(t, 1, rows, cols, b.p)))
+    src.free()
+    return out
+
+
+def random_acts(ctx, rng, n, k):
+    """n rows of N(0, 1) activations, quantized to BlockQ8 on the device (quantize_acts)."""
+    import malkin_amd as mk
+    x = ctx.to_device(rng.standard_normal((n, k)).astype(np.float32))
+    xq = ctx.alloc(n * (k // 32) * 40)
+    mk.check(mk.load().mk_quantize_q8(ctx.h, x.ptr, n, k, xq.ptr))
+    x.free()
+    return xq
+
+
+def time_matmuls(ctx, ws, xq, n, y, reps):
+    """Average time (s) of one mk_matmul launch, cycling through the weights ws, HIP events on the library stream."""
+    import ctypes
+    import malkin_amd as mk
+    L = mk.load()
+    for _, w in ws:
+        mk.check(L.mk_matmul(ctx.h, ctypes.byref(w), xq.ptr, n, y.ptr, w.rows, 0))
+    ctx.sync()
+    ctx.timer_start()
+    for i in range(reps):
+        w = ws[i % len(ws)][1]
+        mk.check(L.mk_matmul(ctx.h, ctypes.byref(w), xq.ptr, n, y.ptr, w.rows, 0))
+    return ctx.timer_stop() / 1e3 / reps
+
+
+def kernel_configs(ctx):
+    """The kernel-level configurations of BASELINE.json:
+    config 1: one Q8_0 GEMM, W 9728x2560, X 512x2560 (int8 MFMA prefill kernel): time, TOPS, fraction of int8 peak;
+    config 2: decode GEMV, Qwen3-14B FFN shapes (gate/up 5120->17408, down 17408->5120) in Q4_K and Q6_K at n = 1, 4,
+    8, cycling through 8 packed copies of each matrix (more than the 256 MB Infinity Cache holds): GB/s of algorithmic
+    bytes (GGUF weight bytes + BlockQ8 input + f32 output) and fraction of the 8 TB/s HBM peak."""
+    import malkin_amd as mk
+    rng = np.random.default_rng(7)
+    out = {}
+    rows, cols, n = 9728, 2560, 512
+    ws = pack_copies(ctx, mk.Q8_0, random_weight(rng, mk.Q8_0, rows, cols), rows, cols, 1)
+    xq, y = random_acts(ctx, rng, n, cols), ctx.alloc(n * rows * 4)
+    t = time_matmuls(ctx, ws, xq, n, y, 20)
+    ops = 2.0 * n * rows * cols
+    out["gemm_q8_0_9728x2560_n512"] = {"us": round(t * 1e6, 2), "tops": round(ops / t / 1e12, 1),
+                                       "mfma_frac": round(ops / t / 1e12 / INT8_PEAK_TOPS, 4)}
+    for b, _w in ws:
+        b.free()
+    xq.free()
+    y.free()
+    for t_name, t in (("q4_k", mk.Q4_K), ("q6_k", mk.Q6_K)):
+        for rows, cols in ((17408, 5120), (5120, 17408)):
+            qk, bs, _ = _BLOCKS[t]
+            wbytes = rows * (cols // qk) * bs
+            ws = pack_copies(ctx, t, random_weight(rng, t, rows, cols), rows, cols, 8)
+            y = ctx.alloc(8 * rows * 4)
+            for n in (1, 4, 8):
+                xq = random_acts(ctx, rng, n, cols)
+                sec = time_matmuls(ctx, ws, xq, n, y, 32)
+                gbs = (wbytes + n * (cols // 32) * 40 + n * rows * 4) / sec / 1e9
+                out[f"gemv_{t_name}_{rows}x{cols}_n{n}"] = {"us": round(sec * 1e6, 2), "gbs": round(gbs, 1),
+                                                           "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+                xq.free()
+            y.free()
+            for b, _w in ws:
+                b.free()
+    return out
+
+
+def traffic_probe():
+    """Launch sequence for the HBM-traffic counters of the roofline kernel (run under rocprofv3 --pmc FETCH_SIZE, then
+    WRITE_SIZE): the four Q8_0 decode GEMV shapes of the Qwen3-8B layer (q|k|v 6144x4096, attn_output 4096x4096,
+    gate|up 24576x4096, down 4096x12288) at n = 1, each launched 4 times over 2 packed copies, then one plain 256 MiB
+    device-to-device copy (the counter scale: it reads and writes exactly 256 MiB)."""
+    import ctypes
+    import malkin_amd as mk
+    ctx = mk.Context(0)
+    rng = np.random.default_rng(3)
+    for rows, cols in ((6144, 4096), (4096, 4096), (24576, 4096), (4096, 12288)):
+        ws = pack_copies(ctx, mk.Q8_0, random_weight(rng, mk.Q8_0, rows, cols), rows, cols, 2)
+        xq, y = random_acts(ctx, rng, 1, cols), ctx.alloc(rows * 4)
+        ctx.sync()
+        time_matmuls(ctx, ws, xq, 1, y, 2)
+        ctx.sync()
+        log(f"[probe] k_gemv Q8_0 {rows}x{cols} n=1: 4 launches, algorithmic bytes "
+            f"{rows * cols // 32 * 34 + cols // 32 * 40 + rows * 4}")
+        for b, _w in ws:
+            b.free()
+        xq.free()
+        y.free()
+    hip = ctypes.CDLL("libamdhip64.so")
+    nbytes = 256 << 20
+    a, b = ctx.alloc(nbytes), ctx.alloc(nbytes)
+    ctx.sync()
+    rc = hip.hipMemcpy(ctypes.c_void_p(b.p), ctypes.c_void_p(a.p), ctypes.c_size_t(nbytes), 3)
+    hip.hipDeviceSynchronize()
+    log(f"[probe] hipMemcpy device-to-device {nbytes} bytes (rc {rc})")
+    ctx.close()
+
+
+def roofline_traffic():
+    """HBM bytes per launch of the roofline kernel, from the committed counter summary (profiles/), or None."""
+    f = os.path.join(ROOT, "profiles", "k_gemv_q8_0_decode_n1_hbm_traffic.md")
+    if not os.path.exists(f):
+        return None
+    for line in open(f):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1])
+    return None
 
 
 def cpu_baseline(path, vocab, budget_s=30.0):
@@ -141,7 +280,14 @@ def main():
     ap.add_argument("--no-graph", action="store_true",
                     help="decode with direct launches instead of the replayed HIP graph (for tracers that do not "
                          "follow graph launches); same kernels")
+    ap.add_argument("--no-kernel-configs", action="store_true",
+                    help="skip the kernel-level configurations (config 1 GEMM, config 2 GEMV)")
+    ap.add_argument("--probe", choices=["traffic"],
+                    help="only run the launch sequence for the roofline kernel's HBM counters")
     args = ap.parse_args()
+    if args.probe == "traffic":
+        traffic_probe()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
@@ -174,8 +320,11 @@ def main():
         ms_step = wall * 1e3 / args.steps
         roof = gemv_roofline(ctx, model, cfg)
         log(f"[bench] decode GEMV: {roof['achieved']} GB/s ({roof['us_per_launch']} us per launch)")
-        cpu = None if args.no_cpu_baseline else cpu_baseline(path, cfg["n_vocab"])
         model.close()
+        kern = None if args.no_kernel_configs else kernel_configs(ctx)
+        if kern:
+            log("[bench] kernel configs: " + json.dumps(kern))
+        cpu = None if args.no_cpu_baseline else cpu_baseline(path, cfg["n_vocab"])
         ctx.close()
     finally:
         if os.path.exists(path):
@@ -201,10 +350,19 @@ def main():
         "tg128_tok_s": round((N_GEN - 1) * 1e3 / dec_ms, 2),
         "decode_ms_per_token": round(dec_ms / (N_GEN - 1), 4),
         "decode_hbm_frac": round(model_bytes_per_token(cfg) / (dec_ms / (N_GEN - 1) / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+        "pp512_mfma_frac": round(prefill_ops(cfg) / (pp_ms / 1e3) / 1e12 / INT8_PEAK_TOPS, 4),
         "roofline": roof,
         "cpu_baseline": cpu,
+        "kernel_configs": kern,
     }
     print(json.dumps(line), flush=True)
+
+
+def prefill_ops(cfg):
+    """Algorithmic int8 ops of the pp512 prefill: 2 * 512 * (weights of the layer matmuls); the LM head runs on the
+    last token only."""
+    E, F, H, KV, D, L = (cfg[k] for k in ("n_embd", "n_ff", "n_head", "n_head_kv", "head_dim", "n_layer"))
+    return 2.0 * N_PROMPT * L * ((H + 2 * KV) * D * E + E * H * D + 3 * F * E)
 
 
 def model_bytes_per_token(cfg):

@@ -334,12 +334,6 @@ def test_errors_are_statuses(mk):
     assert rc == mk_.MK_ERR_UNSUPPORTED
 
 
-class KvCache(ctypes.Structure):
-    _fields_ = [("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("k_scale", ctypes.c_void_p),
-                ("v_scale", ctypes.c_void_p), ("n_layer", ctypes.c_int32), ("n_seq", ctypes.c_int32),
-                ("n_head_kv", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("n_ctx", ctypes.c_int32)]
-
-
 def _kv_perm(D):
     """Element e of a K row sits at byte D/16 * (e % 16) + e // 16 of the device cache's permuted row."""
     e = np.arange(D)
@@ -374,7 +368,7 @@ def test_attention_batch_vs_oracle(mk, oracle, case):
     dv, dks, dvs, dq = mk.to_device(v8), mk.to_device(ks), mk.to_device(vs), mk.to_device(q)
     dseq, dnk = mk.to_device(np.array(seqs, np.int32)), mk.to_device(np.array(nks, np.int32))
     out = mk.alloc(n * H * D * 4)
-    kv = KvCache(dk.ptr, dv.ptr, dks.ptr, dvs.ptr, 1, n_seq, KV, D, n_ctx)
+    kv = mk_.MkKvCache(dk.ptr, dv.ptr, dks.ptr, dvs.ptr, 1, n_seq, KV, D, n_ctx)
     mk_.check(L().mk_attention(mk.h, dq.ptr, H * D, out.ptr, H * D, n, H, ctypes.byref(kv), 0, dseq.ptr, dnk.ptr,
                                None, None, max(nks)))
     got = out.download(np.float32).reshape(n, H * D)
