@@ -237,19 +237,20 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
     using KL = KLane<DC>;
     constexpr int NGR = kAttnThreads / 16, KB = DC >= 16 ? 4 : 8;
     const int gl = tid & 15, grp = tid >> 4;
+    // A round's scales take one load per lane: lane b < 8 of the 16 holds the key scale of key b, lane 8 + b its
+    // value scale (KB = 4: lanes 4-7 and 12-15 repeat keys 0-3); DPP broadcasts them at scoring time.
     struct Round {
       typename KL::T k[KB];
-      float ks[KB], vs[KB];
+      float sv;
     };
     auto fetch = [&](Round& R, int r) {
 #pragma unroll
       for (int b = 0; b < KB; ++b) {
         const int j = min((r * KB + b) * NGR + grp, nk - 1);
-        const int64_t row = key_row(j);
-        R.k[b] = *reinterpret_cast<const typename KL::T*>(kb + row * a.k_row + DC * gl);
-        R.ks[b] = *reinterpret_cast<const float*>(ksb + row * a.s_row);
-        R.vs[b] = *reinterpret_cast<const float*>(vsb + row * a.s_row);
+        R.k[b] = *reinterpret_cast<const typename KL::T*>(kb + key_row(j) * a.k_row + DC * gl);
       }
+      const int js = min((r * KB + (gl & 7) % KB) * NGR + grp, nk - 1);
+      R.sv = *reinterpret_cast<const float*>((gl < 8 ? ksb : vsb) + key_row(js) * a.s_row);
     };
     const int rounds = (nk + NGR * KB - 1) / (NGR * KB);
     Round RA, RB;
@@ -268,9 +269,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
 #pragma unroll
           for (int c = 1; c < DC; ++c) acc = fma_(qr[c], (float)KL::at(R.k[b], c), acc);
           acc = reduce16_lanes(acc);
+          const float ksv = bcast16(R.sv, b), vsv = bcast16(R.sv, 8 + b);
           if (gl == 0) {
-            sc[j] = acc * (R.ks[b] * scale);
-            pv[j] = R.vs[b];
+            sc[j] = acc * (ksv * scale);
+            pv[j] = vsv;
           }
         }
       }
@@ -336,27 +338,53 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
   lds_barrier();
 
   // P.V (kernels_avx512.cpp:247-265): chunk c from tile c & 1 while chunk c + 1 is stored and c + 1 + NG loaded.
+  // The chain waves are latency-bound: at raised priority they issue as soon as their operands are ready instead of
+  // queueing behind the staging waves of their SIMD.
+  if (tid < D) __builtin_amdgcn_s_setprio(3);
   float acc = 0.0f;
   for (int c = 0; c < chunks; ++c) {
     if (tid < D) {
       const int j0 = c * T::chunk;
       const int len = min(T::chunk, nk_pad - j0);  // a multiple of 16
       const float4* vr = reinterpret_cast<const float4*>(tiles + (c & 1) * (T::tile / 4) + tid * T::stride);
-      for (int jj = 0; jj < len; jj += 16) {
-        float4 v[4];
+      const float* pc = pv + j0 + (tid & 15);
+      // Two register sets alternate: a 16-key group's LDS reads are issued while the previous group's chain runs
+      // (past the last group they re-read it). The scheduling barriers keep the reads ahead of the chain.
+      float4 a[4], b[4];
+      float pa, pb;
+      auto ld = [&](float4(&v)[4], float& p, int jj) {
+        const int j = min(jj, len - 16);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = vr[jj / 4 + i];
-        const float pr = pv[j0 + jj + (tid & 15)];
-        float p[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) p[i] = bcast16(pr, i);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc = fma_(p[4 * i], v[i].x, acc);
-          acc = fma_(p[4 * i + 1], v[i].y, acc);
-          acc = fma_(p[4 * i + 2], v[i].z, acc);
-          acc = fma_(p[4 * i + 3], v[i].w, acc);
-        }
+        for (int i = 0; i < 4; ++i) v[i] = vr[j / 4 + i];
+        p = pc[j];
+      };
+      auto chain = [&](const float4(&v)[4], float p) {
+        acc = fma_bcast16<0>(p, v[0].x, acc);
+        acc = fma_bcast16<1>(p, v[0].y, acc);
+        acc = fma_bcast16<2>(p, v[0].z, acc);
+        acc = fma_bcast16<3>(p, v[0].w, acc);
+        acc = fma_bcast16<4>(p, v[1].x, acc);
+        acc = fma_bcast16<5>(p, v[1].y, acc);
+        acc = fma_bcast16<6>(p, v[1].z, acc);
+        acc = fma_bcast16<7>(p, v[1].w, acc);
+        acc = fma_bcast16<8>(p, v[2].x, acc);
+        acc = fma_bcast16<9>(p, v[2].y, acc);
+        acc = fma_bcast16<10>(p, v[2].z, acc);
+        acc = fma_bcast16<11>(p, v[2].w, acc);
+        acc = fma_bcast16<12>(p, v[3].x, acc);
+        acc = fma_bcast16<13>(p, v[3].y, acc);
+        acc = fma_bcast16<14>(p, v[3].z, acc);
+        acc = fma_bcast16<15>(p, v[3].w, acc);
+      };
+      ld(a, pa, 0);
+      for (int jj = 0; jj < len; jj += 32) {
+        ld(b, pb, jj + 16);
+        __builtin_amdgcn_sched_barrier(0);
+        chain(a, pa);
+        if (jj + 16 >= len) break;
+        ld(a, pa, jj + 32);
+        __builtin_amdgcn_sched_barrier(0);
+        chain(b, pb);
       }
     } else if (tid >= kSumThread) {
       if (c == 0) {
@@ -373,6 +401,257 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
     }
     lds_barrier();
   }
+  if (tid < D) out[t * out_stride + (int64_t)h * D + tid] = acc * inv_s;
+}
+
+// Attention of one query head of one token per workgroup for plain tokens (decode steps and other short plain
+// batches), attend_t semantics for D in {64, 128} and G <= 16, bit-identical to k_attention, over the permuted K
+// rows of the device cache. Its keys' V rows are staged once, transposed to [value][key] int8 in LDS, while the
+// scores are computed, so the P.V chains run without further barriers:
+//   scores  as in k_attention (16 lanes per key, KB keys per 16-lane group in flight, the scales of a round in one
+//           load per lane, broadcast by DPP);
+//   V       a staging task = 4 keys x 16 values: four 16-byte loads issued at entry (the D/16 tasks of a key quad on
+//           consecutive lanes, so each load instruction reads whole rows), a 4 x 4 byte transpose per word
+//           (v_perm_b32), four-key words written to the [value][key] rows. Rows are 16 bytes longer than a multiple of
+//           128, so the 16-byte reads of the chains (lane = value) fall in distinct banks, and the 16-key blocks of
+//           row i sit at block b ^ ((i / 16) % 8), so the writes of the D/16 segments of a quad do too;
+//   P.V     lane i runs the chain of value i: per 16 keys one 16-byte LDS read of its row, a DPP-broadcast p per key
+//           folded into the fma, the int8 convert off the chain (SDWA). Reads run one 16-key group ahead. Keys past
+//           the end have p = 0 and finite v, and fma(0, v, acc) == acc;
+//   sum     16 otherwise idle threads run the 16 sequential lane sums of softmax_inplace during the chains.
+constexpr int kDecThreads = 1024;
+constexpr int kDecMaxTasks = 3;  // V staging tasks per thread
+
+__host__ __device__ constexpr int dec_vstride(int nk_pad) { return ((nk_pad + 127) & ~127) + 16; }
+// LDS: the transposed V rows, scores, p, q.
+__host__ __device__ constexpr size_t dec_lds_bytes(int D, int nk_pad) {
+  return (size_t)D * (size_t)dec_vstride(nk_pad) + 4 * (2 * (size_t)nk_pad + (size_t)D);
+}
+__host__ __device__ constexpr int dec_slots(int D, int nk) { return (((nk + 3) / 4) * (D / 16) + kDecThreads - 1) / kDecThreads; }
+__host__ __device__ constexpr bool dec_fits(int D, int nk) {
+  return dec_lds_bytes(D, attn_keys_pad(nk)) <= 160 * 1024 - 1024 &&
+         ((nk + 3) / 4) * (D / 16) <= kDecMaxTasks * kDecThreads;
+}
+
+template <int D, int NSLOT>
+__global__ __launch_bounds__(kDecThreads) void k_attention_dec(const float* __restrict__ q, int64_t q_stride,
+                                                               float* __restrict__ out, int64_t out_stride, int G,
+                                                               float scale, AttnAddr a,
+                                                               const int32_t* __restrict__ seqs,
+                                                               const int32_t* __restrict__ n_keys, int n, int H) {
+  constexpr int DC = D / 16;
+  const int tid = threadIdx.x;
+  int t, h;
+  if ((n * H) % 8 == 0) {
+    const int pair = (int)(blockIdx.x % 8) * (n * H / 8) + (int)(blockIdx.x / 8);
+    const int grp = pair / (n * G), rem = pair % (n * G);
+    t = rem / G;
+    h = grp * G + rem % G;
+  } else {
+    t = (int)blockIdx.x / H;
+    h = (int)blockIdx.x % H;
+  }
+  const int g = h / G;
+  const int nk = n_keys[t];
+  const int nk_pad = attn_keys_pad(nk);
+  const int vstride = dec_vstride(nk_pad);
+  extern __shared__ int4 smem4[];
+  uint8_t* vt = reinterpret_cast<uint8_t*>(smem4);          // [D][vstride] int8: V transposed
+  float* sc = reinterpret_cast<float*>(vt + D * vstride);   // nk_pad: scores, then e^(s - max)
+  float* pv = sc + nk_pad;                                  // nk_pad: v scales, then e * v-scale, 0 past nk
+  float* qs = pv + nk_pad;                                  // D
+  __shared__ float red[kDecThreads / 64];
+  __shared__ float inv_s;
+  const int64_t sq = seqs[t];
+  const int8_t* kb = a.k + sq * a.k_seq + g * a.k_head;
+  const int8_t* vb = a.v + sq * a.k_seq + g * a.k_head;
+  const char* ksb = a.ks + sq * a.s_seq + g * a.s_head;
+  const char* vsb = a.vs + sq * a.s_seq + g * a.s_head;
+  const float* qh = q + t * q_stride + (int64_t)h * D;
+  const float qv = tid < D ? qh[tid] : 0.0f;
+
+  // Scores (kernels_avx512.cpp:234-244): LPK = D/16 lanes per key, each with one 16-byte load of the permuted row,
+  // i.e. CPL = 16/LPK of the reference's lane chains (chains CPL m .. CPL m + CPL - 1 in lane m). KB keys per group
+  // and round (512 keys per round); the round's key and value scales take one load per lane (lane b < KB: key scale
+  // of key b, lane KB + b: its value scale). Loads are never predicated: past the last key they re-read it, unused.
+  constexpr int LPK = D / 16, CPL = 16 / LPK, NGR = kDecThreads / LPK, KB = LPK / 2;
+  const int gl = tid % LPK, grp = tid / LPK;
+  struct Round {
+    v4i k[KB];
+    float sv;
+  };
+  auto fetch = [&](Round& R, int r) {
+#pragma unroll
+    for (int b = 0; b < KB; ++b) {
+      const int j = min((r * KB + b) * NGR + grp, nk - 1);
+      R.k[b] = *reinterpret_cast<const v4i*>(kb + (int64_t)j * a.k_row + 16 * gl);
+    }
+    const int js = min((r * KB + gl % KB) * NGR + grp, nk - 1);
+    R.sv = *reinterpret_cast<const float*>((gl < KB ? ksb : vsb) + (int64_t)js * a.s_row);
+  };
+  const int rounds = (nk + NGR * KB - 1) / (NGR * KB);
+  Round RA, RB;
+  fetch(RA, 0);
+
+  // V staging: task k = (quad kq = k / (D/16) of 4 keys, segment sg = k % (D/16) of 16 values), NSLOT tasks per
+  // thread. Past the last task the loads re-read it (the same rows: no extra lines), unused.
+  constexpr int SEG = D / 16;
+  const int ntask = ((nk + 3) / 4) * SEG;
+  v4i vr[NSLOT][4];
+#pragma unroll
+  for (int i = 0; i < NSLOT; ++i) {
+    const int tk = min(tid + kDecThreads * i, ntask - 1);
+    const int sg = tk % SEG, kq = tk / SEG;
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+      vr[i][x] = *reinterpret_cast<const v4i*>(vb + (int64_t)min(4 * kq + x, nk - 1) * a.k_row + 16 * sg);
+  }
+
+  if (tid < D) qs[tid] = qv;
+  lds_barrier();
+  float qr[CPL][DC];  // qr[k][c] = q[16 c + CPL gl + k]
+#pragma unroll
+  for (int k = 0; k < CPL; ++k)
+#pragma unroll
+    for (int c = 0; c < DC; ++c) qr[k][c] = qs[16 * c + CPL * gl + k];
+  auto score = [&](const Round& R, int r) {
+#pragma unroll
+    for (int b = 0; b < KB; ++b) {
+      const int j = (r * KB + b) * NGR + grp;
+      if (j < nk) {  // uniform over the LPK lanes of the key
+        float sl[CPL];
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) {
+#pragma unroll
+          for (int c = 0; c < DC; ++c) {
+            const int e = k * DC + c;  // byte of chain CPL gl + k, value c
+            const float kf = (float)(int8_t)((uint32_t)R.k[b][e >> 2] >> (8 * (e & 3)));
+            sl[k] = c == 0 ? qr[k][0] * kf : fma_(qr[k][c], kf, sl[k]);
+          }
+        }
+        // The halving tree of _mm512_reduce_add_ps over the 16 chains: pairs 8, 4, 2, 1 chains apart, across lanes
+        // while the distance spans whole lanes, then within lane 0.
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) sl[k] = sl[k] + shl16<8 / CPL>(sl[k]);
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) sl[k] = sl[k] + shl16<(4 / CPL > 0 ? 4 / CPL : 1)>(sl[k]);
+        float tot;
+        if constexpr (CPL == 2) {
+#pragma unroll
+          for (int k = 0; k < 2; ++k) sl[k] = sl[k] + shl16<1>(sl[k]);
+          tot = sl[0] + sl[1];
+        } else {  // CPL == 4: the second step above crossed one lane; the last two are in-lane
+          tot = (sl[0] + sl[2]) + (sl[1] + sl[3]);
+        }
+        const float ksv = shl16_k(R.sv, b), vsv = shl16_k(R.sv, KB + b);  // valid in lane 0 of the key
+        if (gl == 0) {
+          sc[j] = tot * (ksv * scale);
+          pv[j] = vsv;
+        }
+      }
+    }
+  };
+  for (int r = 0; r < rounds; r += 2) {
+    fetch(RB, min(r + 1, rounds - 1));
+    score(RA, r);
+    if (r + 1 >= rounds) break;
+    fetch(RA, min(r + 2, rounds - 1));
+    score(RB, r + 1);
+  }
+
+  // V: 4 x 4 byte transposes into the [value][key] rows; rows of segment sg hold their 16-key blocks XOR sg % 8.
+#pragma unroll
+  for (int i = 0; i < NSLOT; ++i) {
+    const int tk = tid + kDecThreads * i;
+    const int sg = tk % SEG, kq = tk / SEG;
+    if (tk < ntask) {
+      const int col = 16 * ((kq >> 2) ^ (sg & 7)) + 4 * (kq & 3);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t A = (uint32_t)vr[i][0][u], B = (uint32_t)vr[i][1][u];
+        const uint32_t C = (uint32_t)vr[i][2][u], E = (uint32_t)vr[i][3][u];
+        const uint32_t t0 = __builtin_amdgcn_perm(B, A, 0x05010400u), t1 = __builtin_amdgcn_perm(B, A, 0x07030602u);
+        const uint32_t t2 = __builtin_amdgcn_perm(E, C, 0x05010400u), t3 = __builtin_amdgcn_perm(E, C, 0x07030602u);
+        uint8_t* row = vt + (16 * sg + 4 * u) * vstride + col;
+        *reinterpret_cast<uint32_t*>(row) = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+        *reinterpret_cast<uint32_t*>(row + vstride) = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+        *reinterpret_cast<uint32_t*>(row + 2 * vstride) = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+        *reinterpret_cast<uint32_t*>(row + 3 * vstride) = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+      }
+    }
+  }
+  lds_barrier();
+
+  // softmax_inplace (kernels_avx512.cpp:205-226).
+  float m = -INFINITY;
+  for (int j = tid; j < nk; j += kDecThreads) m = fmaxf(m, sc[j]);
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if ((tid & 63) == 0) red[tid >> 6] = m;
+  lds_barrier();
+  float mx = red[0];
+  for (int i = 1; i < kDecThreads / 64; ++i) mx = fmaxf(mx, red[i]);
+  for (int j = tid; j < nk_pad; j += kDecThreads) {
+    if (j < nk) {
+      const float e = exp512(sc[j] - mx);
+      sc[j] = e;
+      pv[j] = e * pv[j];
+    } else {
+      pv[j] = 0.0f;
+    }
+  }
+  lds_barrier();
+
+  // P.V (kernels_avx512.cpp:247-265).
+  float acc = 0.0f;
+  if (tid < D) {
+    __builtin_amdgcn_s_setprio(3);
+    const uint8_t* vrow = vt + tid * vstride;
+    const int swz = (tid >> 4) & 7;
+    const float* pc = pv + (tid & 15);
+    v4i va, vb2;
+    float pa, pb;
+    auto ld = [&](v4i& v, float& p, int jj) {
+      const int j = min(jj, nk_pad - 16);
+      v = *reinterpret_cast<const v4i*>(vrow + 16 * ((j >> 4) ^ swz));
+      p = pc[j];
+    };
+    auto chain = [&](const v4i& v, float p) {
+      const uint32_t w[4] = {(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
+      acc = fma_bcast16<0>(p, i8_to_f32<0>(w[0]), acc);
+      acc = fma_bcast16<1>(p, i8_to_f32<1>(w[0]), acc);
+      acc = fma_bcast16<2>(p, i8_to_f32<2>(w[0]), acc);
+      acc = fma_bcast16<3>(p, i8_to_f32<3>(w[0]), acc);
+      acc = fma_bcast16<4>(p, i8_to_f32<0>(w[1]), acc);
+      acc = fma_bcast16<5>(p, i8_to_f32<1>(w[1]), acc);
+      acc = fma_bcast16<6>(p, i8_to_f32<2>(w[1]), acc);
+      acc = fma_bcast16<7>(p, i8_to_f32<3>(w[1]), acc);
+      acc = fma_bcast16<8>(p, i8_to_f32<0>(w[2]), acc);
+      acc = fma_bcast16<9>(p, i8_to_f32<1>(w[2]), acc);
+      acc = fma_bcast16<10>(p, i8_to_f32<2>(w[2]), acc);
+      acc = fma_bcast16<11>(p, i8_to_f32<3>(w[2]), acc);
+      acc = fma_bcast16<12>(p, i8_to_f32<0>(w[3]), acc);
+      acc = fma_bcast16<13>(p, i8_to_f32<1>(w[3]), acc);
+      acc = fma_bcast16<14>(p, i8_to_f32<2>(w[3]), acc);
+      acc = fma_bcast16<15>(p, i8_to_f32<3>(w[3]), acc);
+    };
+    ld(va, pa, 0);
+    for (int jj = 0; jj < nk_pad; jj += 32) {
+      ld(vb2, pb, jj + 16);
+      __builtin_amdgcn_sched_barrier(0);
+      chain(va, pa);
+      if (jj + 16 >= nk_pad) break;
+      ld(va, pa, jj + 32);
+      __builtin_amdgcn_sched_barrier(0);
+      chain(vb2, pb);
+    }
+  } else if (tid >= kDecThreads - 16) {
+    const int l = tid - (kDecThreads - 16);
+    float s = 0.0f;
+    for (int j = l; j < nk; j += 16) s = s + sc[j];
+    s = reduce16_lanes(s);
+    if (l == 0) inv_s = 1.0f / s;
+  }
+  lds_barrier();
   if (tid < D) out[t * out_stride + (int64_t)h * D + tid] = acc * inv_s;
 }
 
@@ -819,6 +1098,25 @@ void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int6
       a.k_perm ? go(k_attention_rows<64, true>) : go(k_attention_rows<64, false>);
     else
       a.k_perm ? go(k_attention_rows<128, true>) : go(k_attention_rows<128, false>);
+  } else if (!anc_off && G <= 16 && (D == 64 || D == 128) && aligned && a.k_perm &&
+             dec_fits(D, max_keys)) {
+    const size_t lds = dec_lds_bytes(D, attn_keys_pad(max_keys));
+    auto go = [&](auto kernel) {
+      static bool attr = false;
+      if (!attr) {
+        check(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  160 * 1024 - 1024),
+              "hipFuncSetAttribute");
+        attr = true;
+      }
+      hipLaunchKernelGGL(kernel, dim3(n * H), dim3(kDecThreads), lds, s, q, q_stride, out, out_stride, G, scale, a,
+                         seq, n_keys, n, H);
+    };
+    const int slots = dec_slots(D, max_keys);
+    if (D == 64)
+      slots == 1 ? go(k_attention_dec<64, 1>) : slots == 2 ? go(k_attention_dec<64, 2>) : go(k_attention_dec<64, 3>);
+    else
+      slots == 1 ? go(k_attention_dec<128, 1>) : slots == 2 ? go(k_attention_dec<128, 2>) : go(k_attention_dec<128, 3>);
   } else if (G <= 16 && (D == 64 || D == 128 || D == 256) && aligned) {
     const int tile = D == 64 ? AttnTile<64>::tile : D == 128 ? AttnTile<128>::tile : AttnTile<256>::tile;
     const size_t lds = attn_lds_bytes(tile, D, attn_keys_pad(max_keys));

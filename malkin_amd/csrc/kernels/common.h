@@ -35,13 +35,40 @@ __device__ __forceinline__ float reduce16(const float* v) {
   return c0 + c1;
 }
 
+// Lane l gets lane l + K of its 16-lane row; lanes past the row's end keep their own value (the semantics of
+// __shfl_down(v, K, 16)), by DPP row_shl: a register move instead of an LDS permute round trip.
+template <int K>
+__device__ __forceinline__ float shl16(float v) {
+  const int x = __builtin_bit_cast(int, v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(x, x, 0x100 + K, 0xF, 0xF, false));
+}
+
+// shl16 with a shift that folds to a constant only after unrolling (0 = the lane's own value).
+__device__ __forceinline__ float shl16_k(float v, int k) {
+  const int x = __builtin_bit_cast(int, v);
+  int r = x;
+  switch (k) {
+#define MK_SHL16_CASE(K) \
+  case K:                \
+    r = __builtin_amdgcn_update_dpp(x, x, 0x100 + K, 0xF, 0xF, false); \
+    break;
+    MK_SHL16_CASE(1) MK_SHL16_CASE(2) MK_SHL16_CASE(3) MK_SHL16_CASE(4) MK_SHL16_CASE(5) MK_SHL16_CASE(6)
+    MK_SHL16_CASE(7) MK_SHL16_CASE(8) MK_SHL16_CASE(9) MK_SHL16_CASE(10) MK_SHL16_CASE(11) MK_SHL16_CASE(12)
+    MK_SHL16_CASE(13) MK_SHL16_CASE(14) MK_SHL16_CASE(15)
+#undef MK_SHL16_CASE
+    default:
+      break;
+  }
+  return __builtin_bit_cast(float, r);
+}
+
 // The same tree over 16 consecutive lanes of a wavefront: lane l (l % 16 == 0 after the call holds the sum of lanes
 // l..l+15). Valid in lanes whose 16-lane group is fully active.
 __device__ __forceinline__ float reduce16_lanes(float v) {
-  v = v + __shfl_down(v, 8, 16);
-  v = v + __shfl_down(v, 4, 16);
-  v = v + __shfl_down(v, 2, 16);
-  v = v + __shfl_down(v, 1, 16);
+  v = v + shl16<8>(v);
+  v = v + shl16<4>(v);
+  v = v + shl16<2>(v);
+  v = v + shl16<1>(v);
   return v;
 }
 
@@ -71,6 +98,30 @@ __device__ __forceinline__ float bcast16(float x, int k) {
 #undef MK_BCAST16_CASE
   }
   return __builtin_bit_cast(float, r);
+}
+
+// fma(p, v, acc) with p = lane K of x's 16-lane row: the DPP row_newbcast broadcast folded into the fma, one VALU
+// instruction per chain step (a dependent step takes 12 cycles, as a plain fma; a separate DPP move adds 5). For K = 0
+// an s_nop provides the 2 wait states a DPP source needs after a VALU write of it; later K of the same x follow other
+// instructions. The nop is not placed on every step: it adds its cycles to the chain's latency.
+template <int K>
+__device__ __forceinline__ float fma_bcast16(float x, float v, float acc) {
+  if constexpr (K == 0)
+    asm("s_nop 1\n\tv_fmac_f32_dpp %0, %1, %2 row_newbcast:0 row_mask:0xf bank_mask:0xf"
+        : "+v"(acc)
+        : "v"(x), "v"(v));
+  else
+    asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(x), "v"(v), "i"(K));
+  return acc;
+}
+
+// (float)(int8_t)(w >> 8 K): one SDWA convert of byte K (the compiler otherwise emits shift, extract and convert
+// where the source word is live across a scheduling barrier).
+template <int K>
+__device__ __forceinline__ float i8_to_f32(uint32_t w) {
+  float r;
+  asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_%2" : "=v"(r) : "v"(w), "i"(K));
+  return r;
 }
 
 // exp512 (kernels_avx512.cpp:186-202), one lane: max(x, -87), Cody-Waite reduction, degree-6 Taylor, scalef.
