@@ -138,6 +138,17 @@ int mk_qk_norm_rope_kv(mk_ctx* ctx, float* q, float* k, const float* v, int64_t 
                        const float* q_norm, const float* k_norm, float eps, const float* cos_t, const float* sin_t,
                        const int32_t* rpos, const int32_t* seq, const int32_t* kv_row, const mk_kv_cache* kv,
                        int layer);
+/* mk_qk_norm_rope_kv followed by mk_attention in one launch (model.cpp:370-392 then 204-247), for batches whose
+   tokens are all plain (no tree: keys 0..n_keys[t]-1, the last being the token's own row kv_row[t]) and belong to
+   distinct sequences, so that no token attends to another token's new KV row. qkv[t * stride ...]: the n_head query
+   heads, then the n_head_kv key heads, then the n_head_kv value heads, raw (before QK-norm and RoPE; not modified).
+   The KV rows kv_row[t] are written as mk_qk_norm_rope_kv writes them; out as mk_attention. MK_ERR_UNSUPPORTED
+   (nothing launched) where the fused kernel does not apply (head_dim other than 64 / 128, more than 16 query heads per
+   KV head, or max_keys beyond its LDS capacity); the caller then uses the two calls. */
+int mk_attention_decode(mk_ctx* ctx, const float* qkv, int64_t stride, int n, int n_head, const float* q_norm,
+                        const float* k_norm, float eps, const float* cos_t, const float* sin_t, const int32_t* rpos,
+                        const int32_t* seq, const int32_t* kv_row, const int32_t* n_keys, const mk_kv_cache* kv,
+                        int layer, float* out, int64_t out_stride, int max_keys);
 /* Model::attention (model.cpp:204-247) over the device cache: token t attends with its n_head query heads to rows
    0..n_keys[t]-1 of sequence seq[t], then (tree verification) rows anc[anc_off[t] .. anc_off[t+1]) when anc_off is
    not NULL. max_keys bounds n_keys[t] + ancestors for every t. */

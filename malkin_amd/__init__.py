@@ -56,6 +56,7 @@ SIGNATURES = {
     "mk_attend_gqa": (_I, [_P, _P, _I, _I, _P, _P, _SZ, ctypes.c_ssize_t, _I, _F, _P, _P, _I]),
     "mk_qk_norm_rope_kv": (_I, [_P, _P, _P, _P, _I64, _I, _I, _P, _P, _F, _P, _P, _P, _P, _P, _P, _I]),
     "mk_attention": (_I, [_P, _P, _I64, _P, _I64, _I, _I, _P, _I, _P, _P, _P, _P, _I]),
+    "mk_attention_decode": (_I, [_P, _P, _I64, _I, _I, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I64, _I]),
     "mk_move_kv": (_I, [_P, _P, _I, _I, _I]),
     "mk_argmax_top2": (_I, [_P, _P, _I, _I, _P, _P]),
     "mk_greedy_advance": (_I, [_P, _P, _P, _P, _P, _P, _P, _P]),

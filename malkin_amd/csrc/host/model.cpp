@@ -365,6 +365,14 @@ void Model::upload_layout(int n) {
     const int extra = tree_ ? anc_off_[t + 1] - anc_off_[t] : 0;
     max_keys_ = std::max(max_keys_, n_keys_[t] + extra);
   }
+  // Every forward path (batch, tokens, generate) uploads through here: the flag always describes this batch.
+  distinct_seqs_ = true;
+  for (int t = 1; t < n && distinct_seqs_; ++t)
+    for (int u = 0; u < t; ++u)
+      if (seq_[u] == seq_[t]) {
+        distinct_seqs_ = false;
+        break;
+      }
   const size_t words = 7 * static_cast<size_t>(B) + 1 + anc_.size();
   ck(mk_upload(ctx_, layout_.p, h, words * sizeof(int32_t)));
 }
@@ -390,11 +398,22 @@ void Model::run(int n) {
       ck(mk_rmsnorm_q8(ctx_, x, nullptr, norms, n, E, c.rms_eps, xq));
       matmul_group(L.qkv, xq, n, qkv);
     }
-    ck(mk_qk_norm_rope_kv(ctx_, qkv, qkv + static_cast<int64_t>(H) * D, qkv + static_cast<int64_t>(H + KV) * D, QKV, n,
-                          H, norms + 2 * E, norms + 2 * E + D, c.rms_eps, rope_cos_.as<float>(),
-                          rope_sin_.as<float>(), d_rpos_, d_seq_, d_kv_row_, &kv, il));
-    ck(mk_attention(ctx_, qkv, QKV, att, static_cast<int64_t>(H) * D, n, H, &kv, il, d_seq_, d_n_keys_,
-                    tree_ ? d_anc_off_ : nullptr, d_anc_, max_keys_));
+    // Short plain batches of distinct sequences (decode steps): QK-norm, RoPE, the KV write and attention in one
+    // launch; otherwise (prompt chunks, trees, shared sequences) the KV rows are written before any token attends.
+    int rc = MK_ERR_UNSUPPORTED;
+    if (!tree_ && distinct_seqs_ && n < 16)
+      rc = mk_attention_decode(ctx_, qkv, QKV, n, H, norms + 2 * E, norms + 2 * E + D, c.rms_eps,
+                               rope_cos_.as<float>(), rope_sin_.as<float>(), d_rpos_, d_seq_, d_kv_row_, d_n_keys_,
+                               &kv, il, att, static_cast<int64_t>(H) * D, max_keys_);
+    if (rc == MK_ERR_UNSUPPORTED) {
+      ck(mk_qk_norm_rope_kv(ctx_, qkv, qkv + static_cast<int64_t>(H) * D, qkv + static_cast<int64_t>(H + KV) * D, QKV,
+                            n, H, norms + 2 * E, norms + 2 * E + D, c.rms_eps, rope_cos_.as<float>(),
+                            rope_sin_.as<float>(), d_rpos_, d_seq_, d_kv_row_, &kv, il));
+      ck(mk_attention(ctx_, qkv, QKV, att, static_cast<int64_t>(H) * D, n, H, &kv, il, d_seq_, d_n_keys_,
+                      tree_ ? d_anc_off_ : nullptr, d_anc_, max_keys_));
+    } else {
+      ck(rc);
+    }
     mk_weight wo = L.wo.w();
     wo.wide = wide_ ? 1 : 0;
     if (matmul_f32_ok(wo, n, false)) {

@@ -144,6 +144,7 @@ class Model {
   std::vector<int32_t> ids_, rpos_, seq_, kv_row_, n_keys_, anc_off_, anc_, out_;
   std::vector<int> depth_;
   bool tree_ = false;
+  bool distinct_seqs_ = false;  // no two tokens of the batch share a sequence
   int max_keys_ = 0;
   std::vector<int32_t> host_block_;
   DevBuf layout_;

@@ -433,12 +433,123 @@ __host__ __device__ constexpr bool dec_fits(int D, int nk) {
          ((nk + 3) / 4) * (D / 16) <= kDecMaxTasks * kDecThreads;
 }
 
-template <int D, int NSLOT>
+// The fused QK-norm / RoPE / KV-write step of k_attention_dec (model.cpp:370-392, the arithmetic of
+// k_qk_norm_rope_kv): one wave per role (0: query head h, 1: key head g, 2: value head g), D/64 values per lane.
+// Role 0 leaves q in qs; roles 1 and 2 leave the quantized rows (K permuted) and their scales in LDS and, in the
+// group's writer workgroup, in the cache row kv_row[t] of the token's sequence.
+// 16-byte K/V row loads and 4-byte scale loads are legal for this cache layout.
+bool attn_aligned(const AttnAddr& a) {
+  return a.k_row % 16 == 0 && a.k_head % 16 == 0 && a.k_seq % 16 == 0 && reinterpret_cast<uintptr_t>(a.k) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(a.v) % 16 == 0 && a.s_row % 4 == 0 && reinterpret_cast<uintptr_t>(a.ks) % 4 == 0 &&
+         reinterpret_cast<uintptr_t>(a.vs) % 4 == 0;
+}
+
+struct DecFuse {
+  const float* qkv;  // token t: the H query heads, then KV key heads, then KV value heads (raw), at qkv + t * stride
+  int64_t stride;
+  const float* q_norm;
+  const float* k_norm;
+  float eps;
+  const float* cos_t;  // [n_pos][D / 2]
+  const float* sin_t;
+  const int32_t* rpos;
+  const int32_t* kv_row;
+  KvLayer kv;
+  int n_ctx, KV;
+};
+
+template <int D, int role>
+__device__ __forceinline__ void fuse_qkv(const DecFuse& f, int t, int h, int g, int lane, int H, int64_t sq, int jo,
+                                         bool writer, float* qs, float* kscratch, int8_t* own_k, int8_t* own_v,
+                                         float* own_sc) {
+  constexpr int NPL = D / 64, DC = D / 16;
+  const float* row = f.qkv + t * f.stride + (int64_t)(role == 0 ? h * D : role == 1 ? (H + g) * D : (H + f.KV + g) * D);
+  const float* w = role == 0 ? f.q_norm : f.k_norm;
+  const int64_t pos = f.rpos[t];
+  float x[NPL], wv[NPL], cv = 0.0f, sv = 0.0f;
+#pragma unroll
+  for (int u = 0; u < NPL; ++u) x[u] = row[lane + 64 * u];
+  if constexpr (role < 2) {
+#pragma unroll
+    for (int u = 0; u < NPL; ++u) wv[u] = w[lane + 64 * u];
+    if (lane < D / 2) {
+      cv = f.cos_t[pos * (D / 2) + lane];
+      sv = f.sin_t[pos * (D / 2) + lane];
+    }
+    // rmsnorm over D (model.cpp:46-49): lane l < 16 runs the chain over x[l], x[l + 16], ..., then the halving tree.
+    float* sh = role == 0 ? qs : kscratch;  // D floats of LDS per role
+#pragma unroll
+    for (int u = 0; u < NPL; ++u) sh[lane + 64 * u] = x[u];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    float acc = 0.0f;
+    if (lane < 16) {
+#pragma unroll
+      for (int c = 0; c < DC; ++c) acc = fma_(sh[16 * c + lane], sh[16 * c + lane], acc);
+    }
+    acc = reduce16_lanes(acc);
+    const float tot = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, acc)));
+    const float s = 1.0f / sqrtf(tot / (float)D + f.eps);
+#pragma unroll
+    for (int u = 0; u < NPL; ++u) x[u] = x[u] * s * wv[u];
+    // NeoX RoPE on pairs (i, i + D/2) as clang contracts it: fma(x0, c, -(x1 * s)), fma(x0, s, x1 * c).
+    if constexpr (NPL == 2) {  // the pair (lane, lane + 64) is this lane's own two values
+      const float x0 = x[0], x1 = x[1];
+      x[0] = fma_(x0, cv, -(x1 * sv));
+      x[1] = fma_(x0, sv, x1 * cv);
+    } else {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+      sh[lane] = x[0];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+      const float other = sh[lane ^ 32];
+      const float cp = __shfl(cv, lane & 31), sp = __shfl(sv, lane & 31);  // the pair's angle (lane i < 32 loaded it)
+      x[0] = lane < 32 ? fma_(x[0], cp, -(other * sp)) : fma_(other, sp, x[0] * cp);
+    }
+    if constexpr (role == 0) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+#pragma unroll
+      for (int u = 0; u < NPL; ++u) qs[lane + 64 * u] = x[u];
+      return;
+    }
+  }
+  // quantize_i8 (quant.cpp:134-140) of the key (after norm and RoPE) or the raw value.
+  float amax = 0.0f;
+#pragma unroll
+  for (int u = 0; u < NPL; ++u) amax = fmaxf(amax, fabsf(x[u]));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  const float d = amax / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
+  const int64_t crow = (sq * f.KV + g) * f.n_ctx + jo;
+  int8_t* dst = (role == 1 ? f.kv.k : f.kv.v) + crow * D;
+  int8_t* own = role == 1 ? own_k : own_v;
+#pragma unroll
+  for (int u = 0; u < NPL; ++u) {
+    const int i = lane + 64 * u;
+    const int8_t qv = (int8_t)(int)__builtin_rintf(x[u] * id);
+    const int at = role == 1 ? kv_perm(i, DC) : i;
+    own[at] = qv;
+    if (writer) dst[at] = qv;
+  }
+  if (lane == 0) {
+    own_sc[role - 1] = d;
+    if (writer) (role == 1 ? f.kv.ks : f.kv.vs)[crow] = d;
+  }
+}
+
+template <int D, int NSLOT, bool FUSE>
 __global__ __launch_bounds__(kDecThreads) void k_attention_dec(const float* __restrict__ q, int64_t q_stride,
                                                                float* __restrict__ out, int64_t out_stride, int G,
                                                                float scale, AttnAddr a,
                                                                const int32_t* __restrict__ seqs,
-                                                               const int32_t* __restrict__ n_keys, int n, int H) {
+                                                               const int32_t* __restrict__ n_keys, int n, int H,
+                                                               DecFuse f) {
   constexpr int DC = D / 16;
   const int tid = threadIdx.x;
   int t, h;
@@ -467,8 +578,12 @@ __global__ __launch_bounds__(kDecThreads) void k_attention_dec(const float* __re
   const int8_t* vb = a.v + sq * a.k_seq + g * a.k_head;
   const char* ksb = a.ks + sq * a.s_seq + g * a.s_head;
   const char* vsb = a.vs + sq * a.s_seq + g * a.s_head;
-  const float* qh = q + t * q_stride + (int64_t)h * D;
-  const float qv = tid < D ? qh[tid] : 0.0f;
+  float qv = 0.0f;
+  if constexpr (!FUSE) qv = tid < D ? q[t * q_stride + (int64_t)h * D + tid] : 0.0f;
+  // FUSE: this token's own K and V rows (key jo), made here from the raw projections.
+  __shared__ __align__(16) int8_t own_k[FUSE ? D : 16], own_v[FUSE ? D : 16];
+  __shared__ float own_sc[2];
+  const int jo = FUSE ? f.kv_row[t] : -1;
 
   // Scores (kernels_avx512.cpp:234-244): LPK = D/16 lanes per key, each with one 16-byte load of the permuted row,
   // i.e. CPL = 16/LPK of the reference's lane chains (chains CPL m .. CPL m + CPL - 1 in lane m). KB keys per group
@@ -507,7 +622,19 @@ __global__ __launch_bounds__(kDecThreads) void k_attention_dec(const float* __re
       vr[i][x] = *reinterpret_cast<const v4i*>(vb + (int64_t)min(4 * kq + x, nk - 1) * a.k_row + 16 * sg);
   }
 
-  if (tid < D) qs[tid] = qv;
+  if constexpr (FUSE) {
+    // One wave per role; the key role's scratch is the V rows' LDS, written only after the scores.
+    const int wv = tid >> 6;
+    float* ksc = reinterpret_cast<float*>(vt);
+    if (wv == 0)
+      fuse_qkv<D, 0>(f, t, h, g, tid & 63, H, (int64_t)seqs[t], jo, h % G == 0, qs, ksc, own_k, own_v, own_sc);
+    else if (wv == 1)
+      fuse_qkv<D, 1>(f, t, h, g, tid & 63, H, (int64_t)seqs[t], jo, h % G == 0, qs, ksc, own_k, own_v, own_sc);
+    else if (wv == 2)
+      fuse_qkv<D, 2>(f, t, h, g, tid & 63, H, (int64_t)seqs[t], jo, h % G == 0, qs, ksc, own_k, own_v, own_sc);
+  } else {
+    if (tid < D) qs[tid] = qv;
+  }
   lds_barrier();
   float qr[CPL][DC];  // qr[k][c] = q[16 c + CPL gl + k]
 #pragma unroll
@@ -519,13 +646,15 @@ __global__ __launch_bounds__(kDecThreads) void k_attention_dec(const float* __re
     for (int b = 0; b < KB; ++b) {
       const int j = (r * KB + b) * NGR + grp;
       if (j < nk) {  // uniform over the LPK lanes of the key
+        v4i kw = R.k[b];
+        if (FUSE && j == jo) kw = *reinterpret_cast<const v4i*>(own_k + 16 * gl);
         float sl[CPL];
 #pragma unroll
         for (int k = 0; k < CPL; ++k) {
 #pragma unroll
           for (int c = 0; c < DC; ++c) {
             const int e = k * DC + c;  // byte of chain CPL gl + k, value c
-            const float kf = (float)(int8_t)((uint32_t)R.k[b][e >> 2] >> (8 * (e & 3)));
+            const float kf = (float)(int8_t)((uint32_t)kw[e >> 2] >> (8 * (e & 3)));
             sl[k] = c == 0 ? qr[k][0] * kf : fma_(qr[k][c], kf, sl[k]);
           }
         }
@@ -543,7 +672,8 @@ __global__ __launch_bounds__(kDecThreads) void k_attention_dec(const float* __re
         } else {  // CPL == 4: the second step above crossed one lane; the last two are in-lane
           tot = (sl[0] + sl[2]) + (sl[1] + sl[3]);
         }
-        const float ksv = shl16_k(R.sv, b), vsv = shl16_k(R.sv, KB + b);  // valid in lane 0 of the key
+        float ksv = shl16_k(R.sv, b), vsv = shl16_k(R.sv, KB + b);  // valid in lane 0 of the key
+        if (FUSE && j == jo) ksv = own_sc[0], vsv = own_sc[1];
         if (gl == 0) {
           sc[j] = tot * (ksv * scale);
           pv[j] = vsv;
@@ -565,6 +695,12 @@ __global__ __launch_bounds__(kDecThreads) void k_attention_dec(const float* __re
     const int tk = tid + kDecThreads * i;
     const int sg = tk % SEG, kq = tk / SEG;
     if (tk < ntask) {
+      if (FUSE && (jo >> 2) == kq) {
+        const v4i ov = *reinterpret_cast<const v4i*>(own_v + 16 * sg);
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+          if ((jo & 3) == x) vr[i][x] = ov;
+      }
       const int col = 16 * ((kq >> 2) ^ (sg & 7)) + 4 * (kq & 3);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -1068,16 +1204,62 @@ void qk_norm_rope_kv(hipStream_t s, float* q, float* k, const float* v, int64_t 
   check_launch("qk_norm_rope_kv");
 }
 
+namespace {
+
+bool dec_ok(int G, int D, const AttnAddr& a, int max_keys) {
+  return G <= 16 && (D == 64 || D == 128) && a.k_perm && attn_aligned(a) && dec_fits(D, max_keys);
+}
+
+template <bool FUSE>
+void launch_dec(hipStream_t s, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int H, int D,
+                int G, float scale, const AttnAddr& a, const int32_t* seq, const int32_t* n_keys, int max_keys,
+                const DecFuse& f) {
+  const size_t lds = dec_lds_bytes(D, attn_keys_pad(max_keys));
+  auto go = [&](auto kernel) {
+    static bool attr = false;
+    if (!attr) {
+      check(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                160 * 1024 - 1024),
+            "hipFuncSetAttribute");
+      attr = true;
+    }
+    hipLaunchKernelGGL(kernel, dim3(n * H), dim3(kDecThreads), lds, s, q, q_stride, out, out_stride, G, scale, a, seq,
+                       n_keys, n, H, f);
+  };
+  const int slots = dec_slots(D, max_keys);
+  if (D == 64) {
+    slots == 1   ? go(k_attention_dec<64, 1, FUSE>)
+    : slots == 2 ? go(k_attention_dec<64, 2, FUSE>)
+                 : go(k_attention_dec<64, 3, FUSE>);
+  } else {
+    slots == 1   ? go(k_attention_dec<128, 1, FUSE>)
+    : slots == 2 ? go(k_attention_dec<128, 2, FUSE>)
+                 : go(k_attention_dec<128, 3, FUSE>);
+  }
+}
+
+}  // namespace
+
+bool attention_decode_fused(hipStream_t s, const float* qkv, int64_t stride, float* out, int64_t out_stride, int n,
+                            int H, int KV, int D, float scale, const AttnAddr& a, const float* q_norm,
+                            const float* k_norm, float eps, const float* cos_t, const float* sin_t,
+                            const int32_t* rpos, const int32_t* seq, const int32_t* kv_row, const int32_t* n_keys,
+                            const KvLayer& kv, int n_ctx, int max_keys) {
+  if (n <= 0) return true;
+  if (H % KV != 0 || !dec_ok(H / KV, D, a, max_keys)) return false;
+  const DecFuse f{qkv, stride, q_norm, k_norm, eps, cos_t, sin_t, rpos, kv_row, kv, n_ctx, KV};
+  launch_dec<true>(s, nullptr, 0, out, out_stride, n, H, D, H / KV, scale, a, seq, n_keys, max_keys, f);
+  check_launch("attention_decode_fused");
+  return true;
+}
+
 void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int H, int KV,
                int D, float scale, const AttnAddr& a, const int32_t* seq, const int32_t* n_keys,
                const int32_t* anc_off, const int32_t* anc, int max_keys) {
   if (n <= 0) return;
   require(D % 16 == 0 && D <= 256 && H % KV == 0 && max_keys > 0, "attention: unsupported head layout");
   const int G = H / KV;
-  const bool aligned = a.k_row % 16 == 0 && a.k_head % 16 == 0 && a.k_seq % 16 == 0 &&
-                       reinterpret_cast<uintptr_t>(a.k) % 16 == 0 && reinterpret_cast<uintptr_t>(a.v) % 16 == 0 &&
-                       a.s_row % 4 == 0 && reinterpret_cast<uintptr_t>(a.ks) % 4 == 0 &&
-                       reinterpret_cast<uintptr_t>(a.vs) % 4 == 0;
+  const bool aligned = attn_aligned(a);
   if (!anc_off && n >= kRowsMinTokens && G <= 16 && (D == 64 || D == 128) && aligned &&
       rows_lds_bytes(D, attn_keys_pad(max_keys)) <= 160 * 1024 - 1024) {
     const int nk_pad = attn_keys_pad(max_keys);
@@ -1098,25 +1280,8 @@ void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int6
       a.k_perm ? go(k_attention_rows<64, true>) : go(k_attention_rows<64, false>);
     else
       a.k_perm ? go(k_attention_rows<128, true>) : go(k_attention_rows<128, false>);
-  } else if (!anc_off && G <= 16 && (D == 64 || D == 128) && aligned && a.k_perm &&
-             dec_fits(D, max_keys)) {
-    const size_t lds = dec_lds_bytes(D, attn_keys_pad(max_keys));
-    auto go = [&](auto kernel) {
-      static bool attr = false;
-      if (!attr) {
-        check(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  160 * 1024 - 1024),
-              "hipFuncSetAttribute");
-        attr = true;
-      }
-      hipLaunchKernelGGL(kernel, dim3(n * H), dim3(kDecThreads), lds, s, q, q_stride, out, out_stride, G, scale, a,
-                         seq, n_keys, n, H);
-    };
-    const int slots = dec_slots(D, max_keys);
-    if (D == 64)
-      slots == 1 ? go(k_attention_dec<64, 1>) : slots == 2 ? go(k_attention_dec<64, 2>) : go(k_attention_dec<64, 3>);
-    else
-      slots == 1 ? go(k_attention_dec<128, 1>) : slots == 2 ? go(k_attention_dec<128, 2>) : go(k_attention_dec<128, 3>);
+  } else if (!anc_off && dec_ok(G, D, a, max_keys)) {
+    launch_dec<false>(s, q, q_stride, out, out_stride, n, H, D, G, scale, a, seq, n_keys, max_keys, DecFuse{});
   } else if (G <= 16 && (D == 64 || D == 128 || D == 256) && aligned) {
     const int tile = D == 64 ? AttnTile<64>::tile : D == 128 ? AttnTile<128>::tile : AttnTile<256>::tile;
     const size_t lds = attn_lds_bytes(tile, D, attn_keys_pad(max_keys));

@@ -250,6 +250,24 @@ int mk_attention(mk_ctx* c, const float* q, int64_t q_stride, float* out, int64_
   });
 }
 
+int mk_attention_decode(mk_ctx* c, const float* qkv, int64_t stride, int n, int n_head, const float* q_norm,
+                        const float* k_norm, float eps, const float* cos_t, const float* sin_t, const int32_t* rpos,
+                        const int32_t* seq, const int32_t* kv_row, const int32_t* n_keys, const mk_kv_cache* kv,
+                        int layer, float* out, int64_t out_stride, int max_keys) {
+  return guard([&] {
+    const mk::KvLayer L = kv_layer(kv, layer);
+    const int D = kv->head_dim, KV = kv->n_head_kv;
+    require(n_head > 0 && n_head % KV == 0 && max_keys > 0, "mk_attention_decode: bad head layout");
+    const int64_t rows = (int64_t)kv->n_ctx;
+    mk::AttnAddr a{L.k, L.v, reinterpret_cast<const char*>(L.ks), reinterpret_cast<const char*>(L.vs),
+                   (int64_t)KV * rows * D, rows * D, D, (int64_t)KV * rows * 4, rows * 4, 4, 1};
+    const float scale = 1.0f / std::sqrt(static_cast<float>(D));  // model.cpp:208
+    if (!mk::attention_decode_fused(c->stream, qkv, stride, out, out_stride, n, n_head, KV, D, scale, a, q_norm,
+                                    k_norm, eps, cos_t, sin_t, rpos, seq, kv_row, n_keys, L, kv->n_ctx, max_keys))
+      throw mk::Error(MK_ERR_UNSUPPORTED, "mk_attention_decode: no fused kernel for this head layout / key count");
+  });
+}
+
 int mk_move_kv(mk_ctx* c, const mk_kv_cache* kv, int seq, int from, int to) {
   return guard([&] {
     require(kv && seq >= 0 && seq < kv->n_seq && from >= 0 && from < kv->n_ctx && to >= 0 && to < kv->n_ctx,

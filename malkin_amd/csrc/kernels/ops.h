@@ -97,6 +97,15 @@ void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int6
                const AttnAddr& a, const int32_t* seq, const int32_t* n_keys, const int32_t* anc_off,
                const int32_t* anc, int max_keys);
 
+// qk_norm_rope_kv followed by attention in one launch, for batches whose tokens are plain (no tree) and belong to
+// distinct sequences, so that no token reads another's new KV row. qkv rows: H query heads, KV key heads, KV value
+// heads (raw), token stride `stride`. Returns false (nothing launched) where the fused kernel does not apply.
+bool attention_decode_fused(hipStream_t s, const float* qkv, int64_t stride, float* out, int64_t out_stride, int n,
+                            int H, int KV, int D, float scale, const AttnAddr& a, const float* q_norm,
+                            const float* k_norm, float eps, const float* cos_t, const float* sin_t,
+                            const int32_t* rpos, const int32_t* seq, const int32_t* kv_row, const int32_t* n_keys,
+                            const KvLayer& kv, int n_ctx, int max_keys);
+
 // QK-norm + RoPE on q [n][H*D] and k [n][KV*D] (in place), then k, v quantized into the KV cache (model.cpp:370-392).
 // cos/sin tables [n_pos][D/2].
 void qk_norm_rope_kv(hipStream_t s, float* q, float* k, const float* v, int64_t stride, int n, int H, int KV, int D,

@@ -388,3 +388,62 @@ def test_attention_batch_vs_oracle(mk, oracle, case):
                 exp = oracle.attend_gqa(q[t, g * G * D:(g + 1) * G * D], G, D, kf[g * D:], vf[g * D:], row,
                                         (KV - g) * D + 4 * g, nks[t], scale)
                 assert np.array_equal(bits(got[t, g * G * D:(g + 1) * G * D]), bits(exp)), (case, t, g)
+
+
+# (D, H, KV, token seqs, positions, n_ctx, max_keys): the fused decode kernel against the two-launch path.
+DECODE_CASES = [
+    (128, 32, 8, [0], [575], 640, 640),              # decode step of the north-star shape, G = 4
+    (128, 32, 8, [0, 2, 1], [5, 900, 301], 1024, 1000),  # three sequences, three slot counts' worth of keys
+    (64, 8, 2, [1, 0], [0, 63], 64, 64),             # D = 64 (a pair's RoPE partner in another lane), first position
+    (128, 40, 8, [0], [129], 256, 256),              # G = 5
+    (128, 32, 8, [0], [10], 4096, 4096),             # beyond the LDS capacity: MK_ERR_UNSUPPORTED
+]
+
+
+@pytest.mark.parametrize("case", range(len(DECODE_CASES)))
+def test_attention_decode_fused(mk, case):
+    """mk_attention_decode == mk_qk_norm_rope_kv + mk_attention: outputs bit for bit, every cache byte identical."""
+    D, H, KV, seqs, pos, n_ctx, max_keys = DECODE_CASES[case]
+    n, n_seq = len(seqs), max(seqs) + 1
+    print("decode case", case, dict(D=D, H=H, KV=KV, n=n, max_keys=max_keys), flush=True)
+    rng = np.random.default_rng(500 + case)
+    QKV = (H + 2 * KV) * D
+    qkv = rng.standard_normal((n, QKV)).astype(np.float32)
+    norms = rng.uniform(0.5, 1.5, 2 * D).astype(np.float32)
+    ang = np.arange(n_ctx, dtype=np.float32)[:, None] * np.float32(1e-3) * (np.arange(D // 2, dtype=np.float32) + 1)
+    cos_t, sin_t = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    k8 = rng.integers(-127, 128, (n_seq, KV, n_ctx, D), dtype=np.int8)
+    v8 = rng.integers(-127, 128, (n_seq, KV, n_ctx, D), dtype=np.int8)
+    ksc = rng.uniform(0.001, 0.05, (n_seq, KV, n_ctx)).astype(np.float32)
+    vsc = rng.uniform(0.001, 0.05, (n_seq, KV, n_ctx)).astype(np.float32)
+    meta = {name: mk.to_device(np.array(v, np.int32)) for name, v in
+            (("rpos", pos), ("seq", seqs), ("kv_row", pos), ("n_keys", [p + 1 for p in pos]))}
+    dnorm, dcos, dsin = mk.to_device(norms), mk.to_device(cos_t), mk.to_device(sin_t)
+
+    def cache():
+        bufs = [mk.to_device(k8), mk.to_device(v8), mk.to_device(ksc), mk.to_device(vsc)]
+        return bufs, mk_.MkKvCache(bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, bufs[3].ptr, 1, n_seq, KV, D, n_ctx)
+
+    eps = ctypes.c_float(1e-6)
+    # two launches (q, k written in place)
+    ba, kva = cache()
+    dqa, outa = mk.to_device(qkv), mk.alloc(n * H * D * 4)
+    mk_.check(L().mk_qk_norm_rope_kv(mk.h, dqa.ptr, dqa.offset(H * D * 4), dqa.offset((H + KV) * D * 4), QKV, n, H,
+                                     dnorm.ptr, dnorm.offset(D * 4), eps, dcos.ptr, dsin.ptr, meta["rpos"].ptr,
+                                     meta["seq"].ptr, meta["kv_row"].ptr, ctypes.byref(kva), 0))
+    mk_.check(L().mk_attention(mk.h, dqa.ptr, QKV, outa.ptr, H * D, n, H, ctypes.byref(kva), 0, meta["seq"].ptr,
+                               meta["n_keys"].ptr, None, None, max_keys))
+    # fused
+    bb, kvb = cache()
+    dqb, outb = mk.to_device(qkv), mk.alloc(n * H * D * 4)
+    rc = L().mk_attention_decode(mk.h, dqb.ptr, QKV, n, H, dnorm.ptr, dnorm.offset(D * 4), eps, dcos.ptr, dsin.ptr,
+                                 meta["rpos"].ptr, meta["seq"].ptr, meta["kv_row"].ptr, meta["n_keys"].ptr,
+                                 ctypes.byref(kvb), 0, outb.ptr, H * D, max_keys)
+    if max_keys >= 4096:
+        assert rc == mk_.MK_ERR_UNSUPPORTED
+        return
+    mk_.check(rc)
+    assert np.array_equal(bits(outa.download(np.float32)), bits(outb.download(np.float32)))
+    for x, y in zip(ba, bb):
+        assert np.array_equal(x.download(np.uint8), y.download(np.uint8))
+    assert np.array_equal(dqb.download(np.float32), qkv.reshape(-1))  # raw projections untouched

@@ -141,3 +141,18 @@ def test_no_wide_q6k(mk, oracle, model_files):
     assert np.array_equal(bits(a), bits(b))
     dm.close()
     om.close()
+
+
+def test_fused_decode_only_for_distinct_sequences(mk, oracle, model_files):
+    """A one-token batch (fused QK-norm/RoPE/KV-write/attention) followed by a several-token forward of one sequence
+    through the other entry point: the second must not take the fused path (its tokens read each other's new rows)."""
+    dm = mk_.Model(mk, model_files["tiny"], 64, 2)
+    om = oracle.model(model_files["tiny"], 64, 2)
+    b = np.array([(7, 1, 0, 1, -1, -1)], dtype=mk_.BATCH_TOKEN)
+    assert np.array_equal(bits(dm.forward_batch(b)), bits(om.forward_batch(b)))
+    p = np.array([3, 1, 4], np.int32)
+    assert np.array_equal(bits(dm.forward(p, 0, all_logits=True)), bits(om.forward(p, 0, all_logits=True)))
+    b2 = np.array([(5, 0, 3, 1, -1, -1), (9, 1, 1, 1, -1, -1)], dtype=mk_.BATCH_TOKEN)  # two sequences: fused
+    assert np.array_equal(bits(dm.forward_batch(b2)), bits(om.forward_batch(b2)))
+    dm.close()
+    om.close()
