@@ -1,0 +1,54 @@
+/*
+ * malkin-mi355x: C ABI of the device token loop (libmalkin_hip.so): continuous batching and greedy speculative
+ * decoding over mk_model, the greedy part of the reference's malkin::Engine (engine.h:51-141, engine.cpp:242-479)
+ * without tokenizer or text: requests are token ids in, token ids out.
+ *
+ * A request is admitted into the idle slot (model sequence) whose cached tokens share the longest prefix with its
+ * prompt (that prefix's KV is reused); each step is one target forward over all busy slots: decoding slots put their
+ * next token, with a draft model also the draft's greedy tree [next, chain0, alt0, chain1, alt1, ...], then prompt
+ * chunks fill the batch up to 256 tokens. Accepted tree nodes move their KV rows (Model::move_kv). Greedy picks run
+ * on the device (first maximum, strict-> runner-up for the draft alternative). Status codes and mk_last_error() as
+ * in malkin_hip.h.
+ */
+#ifndef MALKIN_ENGINE_H
+#define MALKIN_ENGINE_H
+
+#include <stdint.h>
+
+#include "malkin_model.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mk_engine mk_engine;
+
+/* GenResult (engine.h:36-42) without text. finish: 0 = "length" (budget or context end), 1 = "stop" (an
+   end-of-generation id, which is not part of the tokens). */
+typedef struct {
+  int32_t prompt_tokens, cached_tokens, completion_tokens, drafted, accepted, finish, done;
+  double prefill_ms, decode_ms;
+} mk_request_info;
+
+/* Engine::Engine (engine.cpp:94-191) over loaded models: target has one slot per sequence (mk_model_open n_seq);
+   draft (NULL: no speculation) must have the same vocabulary and at least as many sequences and context; n_draft:
+   maximum draft tokens per step (0: 8). The engine does not own the models. */
+int mk_engine_create(mk_model* target, mk_model* draft, int n_draft, mk_engine** out);
+int mk_engine_free(mk_engine* e);
+/* Engine::generate's request (engine.cpp:226-240) queued: prompt ids, max_tokens (0: until the context ends), eog
+   ids (may be NULL). Errors as the reference: empty prompt, prompt not shorter than the context. */
+int mk_engine_submit(mk_engine* e, const int32_t* prompt, int n_prompt, int max_tokens, const int32_t* eog, int n_eog,
+                     int32_t* request_id);
+/* The worker loop's iteration (engine.cpp:193-224): pending requests into idle slots, then one step. busy (may be
+   NULL): slots still in flight. */
+int mk_engine_step(mk_engine* e, int32_t* busy);
+/* Steps until no request is pending or in flight. */
+int mk_engine_run(mk_engine* e);
+/* Generated ids of a request (up to cap) and its counters. */
+int mk_engine_result(mk_engine* e, int32_t request_id, int32_t* tokens, int32_t cap, mk_request_info* info);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -71,6 +71,12 @@ SIGNATURES = {
     "mk_model_generate": (_I, [_P, _P, _I, _I, _I, _I, _P, _P]),
     "mk_model_weight_bytes": (_I64, [_P]),
     "mk_model_weight": (_I, [_P, _I, _I, _P]),
+    "mk_engine_create": (_I, [_P, _P, _I, ctypes.POINTER(_P)]),
+    "mk_engine_free": (_I, [_P]),
+    "mk_engine_submit": (_I, [_P, _P, _I, _I, _P, _I, _P]),
+    "mk_engine_step": (_I, [_P, _P]),
+    "mk_engine_run": (_I, [_P]),
+    "mk_engine_result": (_I, [_P, _I, _P, _I, _P]),
 }
 
 _lib = None
@@ -278,6 +284,56 @@ class Model:
         check(load().mk_model_generate(self.h, _ptr(prompt), len(prompt), n_gen, seq, 1 if use_graph else 0,
                                        _ptr(out), ctypes.byref(st)))
         return out, {"prefill_ms": st.prefill_ms, "decode_ms": st.decode_ms, "decode_forwards": st.decode_forwards}
+
+
+class MkRequestInfo(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("prompt_tokens", "cached_tokens", "completion_tokens", "drafted",
+                                              "accepted", "finish", "done")] + [("prefill_ms", ctypes.c_double),
+                                                                                 ("decode_ms", ctypes.c_double)]
+
+
+class Engine:
+    """mk_engine_* wrapper: continuous batching and greedy speculative decoding over Model (engine.h)."""
+
+    def __init__(self, target, draft=None, n_draft=0):
+        self.target, self.draft = target, draft  # keep the models alive
+        p = _P()
+        check(load().mk_engine_create(target.h, draft.h if draft is not None else None, n_draft, ctypes.byref(p)))
+        self.h = p.value
+
+    def close(self):
+        if self.h:
+            load().mk_engine_free(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def submit(self, prompt, max_tokens=0, eog=()):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        eog = np.ascontiguousarray(list(eog), dtype=np.int32)
+        rid = ctypes.c_int32()
+        check(load().mk_engine_submit(self.h, _ptr(prompt), len(prompt), max_tokens, _ptr(eog) if len(eog) else None,
+                                      len(eog), ctypes.byref(rid)))
+        return rid.value
+
+    def step(self):
+        busy = ctypes.c_int32()
+        check(load().mk_engine_step(self.h, ctypes.byref(busy)))
+        return busy.value
+
+    def run(self):
+        check(load().mk_engine_run(self.h))
+
+    def result(self, rid):
+        info = MkRequestInfo()
+        check(load().mk_engine_result(self.h, rid, None, 0, ctypes.byref(info)))
+        toks = np.zeros(max(info.completion_tokens, 1), dtype=np.int32)
+        check(load().mk_engine_result(self.h, rid, _ptr(toks), len(toks), ctypes.byref(info)))
+        return toks[:info.completion_tokens], {f: getattr(info, f) for f, _ in MkRequestInfo._fields_}
 
 
 def batch(tokens):

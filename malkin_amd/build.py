@@ -26,6 +26,7 @@ HIP_SOURCES = [
     "csrc/kernels/capi.cpp",
     "csrc/host/gguf.cpp",
     "csrc/host/model.cpp",
+    "csrc/host/engine.cpp",
     "csrc/host/capi_model.cpp",
 ]
 

@@ -5,13 +5,19 @@
 #include <stdexcept>
 #include <vector>
 
+#include "../../../include/malkin_engine.h"
 #include "../../../include/malkin_model.h"
 #include "../kernels/ctx.h"
+#include "engine.h"
 #include "model.h"
 
 struct mk_model {
   std::unique_ptr<malkin_hip::GgufFile> file;
   std::unique_ptr<malkin_hip::Model> model;
+};
+
+struct mk_engine {
+  std::unique_ptr<malkin_hip::Engine> engine;
 };
 
 namespace {
@@ -114,6 +120,60 @@ int64_t mk_model_weight_bytes(const mk_model* m) { return m ? static_cast<int64_
 
 int mk_model_weight(const mk_model* m, int layer, int which, mk_weight* out) {
   return run([&] { *out = m->model->weight(layer, which); });
+}
+
+int mk_engine_create(mk_model* target, mk_model* draft, int n_draft, mk_engine** out) {
+  return run([&] {
+    if (!target || !out) throw std::invalid_argument("mk_engine_create: null argument");
+    auto e = std::make_unique<mk_engine>();
+    e->engine = std::make_unique<malkin_hip::Engine>(target->model.get(), draft ? draft->model.get() : nullptr,
+                                                      n_draft);
+    *out = e.release();
+  });
+}
+
+int mk_engine_free(mk_engine* e) {
+  return run([&] { delete e; });
+}
+
+int mk_engine_submit(mk_engine* e, const int32_t* prompt, int n_prompt, int max_tokens, const int32_t* eog, int n_eog,
+                     int32_t* request_id) {
+  return run([&] {
+    if (!e || (n_prompt > 0 && !prompt) || (n_eog > 0 && !eog)) throw std::invalid_argument("mk_engine_submit: null argument");
+    malkin_hip::EngineRequest r;
+    if (n_prompt > 0) r.prompt.assign(prompt, prompt + n_prompt);
+    if (n_eog > 0) r.eog.assign(eog, eog + n_eog);
+    r.max_tokens = max_tokens;
+    const int id = e->engine->submit(r);
+    if (request_id) *request_id = id;
+  });
+}
+
+int mk_engine_step(mk_engine* e, int32_t* busy) {
+  return run([&] {
+    if (!e) throw std::invalid_argument("mk_engine_step: null engine");
+    const int b = e->engine->step_once();
+    if (busy) *busy = b;
+  });
+}
+
+int mk_engine_run(mk_engine* e) {
+  return run([&] {
+    if (!e) throw std::invalid_argument("mk_engine_run: null engine");
+    e->engine->run();
+  });
+}
+
+int mk_engine_result(mk_engine* e, int32_t request_id, int32_t* tokens, int32_t cap, mk_request_info* info) {
+  return run([&] {
+    if (!e) throw std::invalid_argument("mk_engine_result: null engine");
+    const malkin_hip::EngineResult& r = e->engine->result(request_id);
+    if (tokens)
+      for (size_t i = 0; i < r.tokens.size() && static_cast<int32_t>(i) < cap; ++i) tokens[i] = r.tokens[i];
+    if (info)
+      *info = mk_request_info{r.prompt_tokens, r.cached_tokens, r.completion_tokens, r.drafted, r.accepted,
+                               r.finish_reason == "stop" ? 1 : 0, r.done ? 1 : 0, r.prefill_ms, r.decode_ms};
+  });
 }
 
 }  // extern "C"

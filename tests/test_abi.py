@@ -1,5 +1,6 @@
 """The C-ABI library loads and exports every symbol include/*.h declares (no compute calls: no GPU needed)."""
 import ctypes
+import glob
 import os
 import re
 
@@ -12,8 +13,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def declared():
     names = set()
-    for h in ("malkin_hip.h", "malkin_model.h"):
-        text = open(os.path.join(ROOT, "include", h)).read()
+    for h in sorted(glob.glob(os.path.join(ROOT, "include", "*.h"))):
+        text = open(h).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         names |= set(re.findall(r"\b(mk_\w+)\s*\(", text))
     return names
