@@ -196,38 +196,44 @@ __device__ __forceinline__ void quantize_half_block(const float (&v)[16], int h,
 }
 
 
-// One lane of kern::dot_f32(x, x) (kernels_avx512.cpp:82-89): the sequential fma chain over x[l], x[l + 16], ...
-// given as the lane's contiguous row tl[0 .. per) of a transposed copy (16-byte aligned). 32 values per step, the
-// next 32 read while the current ones run.
+// Values per row of the transposed copy used by sumsq_lane_chain (per = n / 16, zero-padded to a multiple of 64), and
+// its row stride in floats (4 more, against bank conflicts; rows stay 16-byte aligned).
+__host__ __device__ constexpr int sumsq_padded(int per) { return (per + 63) & ~63; }
+__host__ __device__ constexpr int sumsq_tstride(int per) { return sumsq_padded(per) + 4; }
+
+// One lane chain of kern::dot_f32(x, x) (kernels_avx512.cpp:82-89): acc = fma(x_i, x_i, acc) over the lane's values
+// in order, given as the lane's contiguous row tl of a transposed copy, zero-padded to a multiple of 64 values
+// (fma(0, 0, acc) == acc: the sum of squares is never -0). 16 values per step in two alternating register sets: the
+// next 16 are read while the current ones run, and the scheduling barriers keep the reads ahead of the fmas.
 __device__ __forceinline__ float sumsq_lane_chain(const float* tl, int per) {
-  const int f4 = per / 4;
-  constexpr int B = 8;
+  const int nh = sumsq_padded(per) / 16;  // 16-value quarters of the padded row, an even count
+  const float4* p4 = reinterpret_cast<const float4*>(tl);
   float acc = 0.0f;
-  float4 cur[B];
+  float4 a[4], b[4];
+  auto ld = [&](float4(&r)[4], int h) {
 #pragma unroll
-  for (int k = 0; k < B; ++k)
-    if (k < f4) cur[k] = reinterpret_cast<const float4*>(tl)[k];
-  for (int j = 0; j < f4; j += B) {
-    float4 nxt[B];
+    for (int k = 0; k < 4; ++k) r[k] = p4[4 * h + k];
+  };
+  auto run = [&](const float4(&r)[4]) {
 #pragma unroll
-    for (int k = 0; k < B; ++k)
-      if (j + B + k < f4) nxt[k] = reinterpret_cast<const float4*>(tl)[j + B + k];
-#pragma unroll
-    for (int k = 0; k < B; ++k) {
-      if (j + k < f4) {
-        acc = fma_(cur[k].x, cur[k].x, acc);
-        acc = fma_(cur[k].y, cur[k].y, acc);
-        acc = fma_(cur[k].z, cur[k].z, acc);
-        acc = fma_(cur[k].w, cur[k].w, acc);
-      }
-      cur[k] = nxt[k];
+    for (int k = 0; k < 4; ++k) {
+      acc = fma_(r[k].x, r[k].x, acc);
+      acc = fma_(r[k].y, r[k].y, acc);
+      acc = fma_(r[k].z, r[k].z, acc);
+      acc = fma_(r[k].w, r[k].w, acc);
     }
+  };
+  ld(a, 0);
+  for (int h = 0; h < nh; h += 2) {
+    ld(b, h + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    run(a);
+    ld(a, min(h + 2, nh - 1));  // past the end: the last quarter again, unused
+    __builtin_amdgcn_sched_barrier(0);
+    run(b);
   }
-  for (int i = 4 * f4; i < per; ++i) acc = fma_(tl[i], tl[i], acc);
   return acc;
 }
 
-// Floats per row of the transposed copy used by sumsq_lane_chain: per = n / 16 values, 16-byte aligned, padded.
-__host__ __device__ constexpr int sumsq_tstride(int per) { return ((per + 3) & ~3) + 4; }
 
 }  // namespace mk

@@ -279,9 +279,8 @@ __global__ __launch_bounds__(kThreads) void k_gemv(const uint8_t* W, int64_t row
     lds_barrier();
   } else {
     // rmsnorm + quantization: thread tid owns the 16-value chunks c16 = tid + 256 p (half a Q8 block each) of every
-    // token row, read with 16-byte loads issued before the weight loads. The rows go to LDS (transposed, for the
-    // chains) and are read back for the scaling, with the norm weights read then: neither occupies registers
-    // meanwhile, and the norm weights' wait coincides with the first weight chunks'.
+    // token row, read with 16-byte loads, then its norm weights. The rows go to LDS (transposed, for the chains) and
+    // are read back for the scaling.
     const int per = nq8 * 2;  // 16-value chunks per row
     const int tstride = sumsq_tstride(per);
     float v[NT][kProPass][16];
@@ -300,23 +299,38 @@ __global__ __launch_bounds__(kThreads) void k_gemv(const uint8_t* W, int64_t row
         }
       }
     }
-    load(ra, 0);
-    load(rb, 1);
+    // The norm weights next (never predicated: past the row they re-read its last chunk, unused). Both wait for
+    // nothing else: the weight chunks are issued only once the rows are stored, so that no workgroup's rows queue
+    // behind the other workgroups' weight streams (the norm's dependent chain is the critical path here).
+    float wv[kProPass][16];
+#pragma unroll
+    for (int p = 0; p < kProPass; ++p) {
+      const int c16 = min(tid + p * kThreads, per - 1);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float4 w4 = reinterpret_cast<const float4*>(in.nw + 16 * c16)[k];
+        wv[p][4 * k] = w4.x, wv[p][4 * k + 1] = w4.y, wv[p][4 * k + 2] = w4.z, wv[p][4 * k + 3] = w4.w;
+      }
+    }
     __shared__ float scale_s[NT];
     {
-      // rmsnorm (model.cpp:46-49): 16 sequential lane chains per token over the transposed copy, halving tree.
+      // rmsnorm (model.cpp:46-49): 16 sequential lane chains per token over the transposed copy (zero-padded),
+      // halving tree.
+      const int padded = sumsq_padded(per);
 #pragma unroll
       for (int p = 0; p < kProPass; ++p) {
         const int c16 = tid + p * kThreads;
-        if (c16 < per) {
+        if (c16 < padded) {
 #pragma unroll
           for (int t = 0; t < NT; ++t)
             if (t < nt) {
 #pragma unroll
-              for (int c = 0; c < 16; ++c) tr[(t * 16 + c) * tstride + c16] = v[t][p][c];
+              for (int c = 0; c < 16; ++c) tr[(t * 16 + c) * tstride + c16] = c16 < per ? v[t][p][c] : 0.0f;
             }
         }
       }
+      load(ra, 0);
+      load(rb, 1);
       lds_barrier();
       if (tid < 16 * nt) {
         float acc = sumsq_lane_chain(tr + tid * tstride, per);  // token tid / 16, lane tid % 16
@@ -337,12 +351,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv(const uint8_t* W, int64_t row
         const float sc = scale_s[t];
         if (c16 < per) {
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const float4 w4 = reinterpret_cast<const float4*>(in.nw + 16 * c16)[k];
-            const float wk[4] = {w4.x, w4.y, w4.z, w4.w};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) yv[4 * k + c] = tr[(t * 16 + 4 * k + c) * tstride + c16] * sc * wk[c];
-          }
+          for (int c = 0; c < 16; ++c) yv[c] = tr[(t * 16 + c) * tstride + c16] * sc * wv[p][c];
         }
         // per is even (cols % 32 == 0): both halves of a block are in the row or neither is.
         quantize_half_block(yv, c16 & 1, c16 < per, row + c16 / 2);
@@ -569,16 +578,20 @@ int device_cus() {
 // Resident workgroups per CU of a kernel at a given dynamic LDS size (cached per size).
 template <typename K>
 int resident_per_cu(K kernel, size_t lds) {
-  static size_t keys[16] = {};
-  static int vals[16] = {};
-  for (int i = 0; i < 16 && keys[i]; ++i)
-    if (keys[i] == lds + 1) return vals[i];
+  // Cached per (kernel, LDS size): every k_gemv instantiation has the same function type.
+  static const void* fns[64] = {};
+  static size_t keys[64] = {};
+  static int vals[64] = {};
+  const void* fn = reinterpret_cast<const void*>(kernel);
+  for (int i = 0; i < 64 && keys[i]; ++i)
+    if (fns[i] == fn && keys[i] == lds + 1) return vals[i];
   int blocks = 0;
   check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, kThreads, lds),
         "hipOccupancyMaxActiveBlocksPerMultiprocessor");
   blocks = blocks > 0 ? blocks : 1;
-  for (int i = 0; i < 16; ++i)
+  for (int i = 0; i < 64; ++i)
     if (!keys[i]) {
+      fns[i] = fn;
       keys[i] = lds + 1;
       vals[i] = blocks;
       break;
@@ -603,7 +616,10 @@ void launch(hipStream_t s, const void* w, int64_t rows, int64_t cols, const Gemv
   const int per_cu = resident_per_cu(k_gemv<TYPE, WIDE, R, NT, PRO, EPI>, lds);
   const int64_t groups = rows / R, tgroups = (n + NT - 1) / NT;
   const int64_t resident = (int64_t)per_cu * device_cus();
-  const int64_t gx = std::max<int64_t>(1, std::min<int64_t>(groups, resident / tgroups));
+  // The rmsnorm prologue (16 KB of rows and norm weights, a dependent chain) is paid once per workgroup: at least
+  // two row groups per workgroup. (The quantize-only prologue measured faster with one.)
+  const int64_t per_wg = PRO == kProNorm ? 2 : 1;
+  const int64_t gx = std::max<int64_t>(1, std::min<int64_t>((groups + per_wg - 1) / per_wg, resident / tgroups));
   const dim3 grid((unsigned)gx, (unsigned)tgroups);
   hipLaunchKernelGGL((k_gemv<TYPE, WIDE, R, NT, PRO, EPI>), grid, dim3(kThreads), lds, s, static_cast<const uint8_t*>(w),
                      rows, cols, in, n, y, ys, accumulate ? 1 : 0);

@@ -90,12 +90,13 @@ __global__ __launch_bounds__(kT) void k_rmsnorm(const float* __restrict__ x, con
       }
     }
   }
+  const int padded = sumsq_padded(per);
 #pragma unroll
   for (int p = 0; p < kPass; ++p) {
     const int c16 = tid + p * kT;
-    if (c16 < per) {
+    if (c16 < padded) {
 #pragma unroll
-      for (int c = 0; c < 16; ++c) tr[c * tstride + c16] = v[p][c];
+      for (int c = 0; c < 16; ++c) tr[c * tstride + c16] = c16 < per ? v[p][c] : 0.0f;
     }
   }
   __syncthreads();
