@@ -2,22 +2,36 @@
 // (gemm_avx512.cpp:67-102):
 //   y[t][r] = sum over blocks b, in order, of fma(float(int dot of block b), f16(dw[r][b]) * dx[t][b], acc).
 // K = 32 of the MFMA is exactly one Q8_0 block, so every MFMA yields the exact int32 dots of one block for a 32 x 32
-// (rows x tokens) tile, and the epilogue folds them into the fp32 chains with the reference's rounding. The epilogue
-// (convert, scale product, fma per output and block) is VALU work that outweighs the MFMA itself, so the kernel is
-// built to keep the VALU busy: operands come from LDS, never from a global load in the inner loop.
+// (rows x tokens) tile, and the epilogue folds them into the fp32 chains with the reference's rounding. Per output and
+// block that epilogue is a conversion, a scale product and an fma. On the VALU (4 cycles per wave instruction) those
+// three cost 6x the int8 MFMA itself, so two of them run on the matrix cores instead:
+//   conversion: the int8 MFMA starts from C = 0x4B400000, the bits of 12582912.0f = 1.5 * 2^23. |dot| <= 32 * 128 *
+//     128 < 2^22 keeps the sum inside that binade, so its bits read as the float 12582912 + dot, and an fp32 MFMA
+//     outer product adding (-12582912) * 1 to every element (v_mfma_f32_16x16x1_4b_f32, C = those bits) leaves
+//     float(dot) exactly;
+//   scale product: v_mfma_f32_32x32x1_2b_f32 with A = dw (one row per lane) and B = dx (one token per lane) yields
+//     round(dw * dx) for a 32 x 64 tile, in the accumulator layout of the two int8 MFMAs; no other product is added
+//     (K = 1), so the rounding is that of one fp32 multiply. A zero product may come out as +0 where the VALU gives
+//     -0; the fma that consumes it returns the same value either way, because the chain never holds -0 (it starts at
+//     +0 and an exact cancellation rounds to +0).
+// That leaves one VALU fma per output and block.
 //
-// A workgroup (4 waves) owns a 64-row x 64-token tile, one 32 x 32 quarter per wave, and walks the K dimension in
-// stages of kKB blocks. A stage holds, in LDS:
-//   A  [kKB][64 rows][32 B]   the rows' quants (copied from the CDNA planes of layout.h),
+// A workgroup (4 waves) owns a 128-row x 64-token tile, 32 rows x 64 tokens per wave, and walks the K dimension in
+// stages of kKB blocks held in a ring of kNS LDS buffers. A stage holds:
+//   A  [kKB][128 rows][32 B]  the rows' quants (from the CDNA planes of layout.h),
 //   B  [kKB][64 tok][32 B]    the tokens' BlockQ8 quants,
-//   dw [kKB][64 rows] f32     weight scales, converted from f16 once per stage,
-//   dx [kKB][64 tok]  f32     activation scales.
+//   dx [kKB][64 tok]  f32     activation scales,
+//   dw [kKB][128 rows] f16    weight scales.
 // Rows of A and B are 32 bytes with their two 16-byte halves swapped on every other group of 8 rows, so the MFMA
-// operand reads (lane l: row l % 32, half l / 32) hit distinct banks. Two stages alternate: while the waves compute
-// stage s, the next stage's global loads are in flight in registers and are stored after the compute.
+// operand reads (lane l: row l % 32, half l / 32) hit distinct banks. All copies are direct global -> LDS loads
+// (global_load_lds_dwordx4 / _dword: lane i of a wave instruction writes bytes [size * i, size * (i + 1)) after the
+// instruction's LDS base), issued two stages ahead, so the data of kNS - 1 stages is in flight while a stage is
+// computed and no register holds it on the way.
 //
 // Accumulator layout of v_mfma_i32_32x32x32_i8 (checked on gfx950): lane l, element i holds
 //   row 8 * (i / 4) + 4 * (l / 32) + i % 4, column l % 32.
+// v_mfma_f32_32x32x1_2b_f32 holds block j in elements 16 j .. 16 j + 15 in the same layout, block j taking A and B
+// from lanes 32 j .. 32 j + 31 (checked on gfx950, together with the conversion and the product rounding).
 #include "ctx.h"
 #include "ops.h"
 
@@ -26,30 +40,52 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
-typedef int v2i __attribute__((ext_vector_type(2)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void glb_void;
 
 constexpr int kThreads = 256;
-constexpr int kRowsT = 64, kTokT = 64;  // workgroup tile
-constexpr int kKB = 8;                  // blocks per stage
+constexpr int kRowsT = 128, kTokT = 64;  // workgroup tile
+constexpr int kKB = 4;                   // blocks per stage
+constexpr int kNS = 3;                   // stages in the LDS ring
+constexpr int kMagic = 0x4B400000;       // bits of 12582912.0f
+constexpr float kMagicF = 12582912.0f;
 
 struct StageLds {
-  static constexpr int a = 0;                           // kKB * 64 * 32 bytes
-  static constexpr int b = a + kKB * kRowsT * 32;       // kKB * 64 * 32
-  static constexpr int dw = b + kKB * kTokT * 32;       // kKB * 64 floats
-  static constexpr int dx = dw + kKB * kRowsT * 4;      // kKB * 64 floats
-  static constexpr int bytes = dx + kKB * kTokT * 4;
+  static constexpr int a = 0;                       // kKB * 128 * 32 bytes
+  static constexpr int b = a + kKB * kRowsT * 32;   // kKB * 64 * 32
+  static constexpr int dx = b + kKB * kTokT * 32;   // kKB * 64 floats
+  static constexpr int dw = dx + kKB * kTokT * 4;   // kKB * 128 halves
+  static constexpr int bytes = dw + kKB * kRowsT * 2;
 };
+constexpr int kLoadsPerStage = kKB + 4;  // per wave: kKB A pieces, 2 B halves, 1 dx, 1 dw (wave w: block w of B/dx/dw)
+static_assert(kKB == 4, "one wave per block copies the B, dx and dw parts; a stage is two pairs of steps");
+static_assert(kNS == 3, "the main loop is unrolled over a ring of 3 buffers");
 
-// Byte offset of half h (0/1) of row r within a [64][32 B] operand slab.
+// Byte offset of half h (0/1) of row r within a [rows][32 B] operand slab.
 __device__ __forceinline__ int slab_off(int r, int h) { return r * 32 + ((h ^ ((r >> 3) & 1)) << 4); }
 
+__device__ __forceinline__ void load_lds16(const void* g, uint8_t* l) {
+  __builtin_amdgcn_global_load_lds((glb_void*)g, (lds_void*)l, 16, 0, 0);
+}
+// Workgroup barrier for the LDS ring. The loads into LDS are tracked by vmcnt and waited for explicitly (the stage
+// being computed only); a fenced barrier would make the compiler wait for every one of them, prefetches included.
+// Reads of a buffer finish before the barrier that precedes its next fill, because each read feeds an MFMA of the
+// same iteration.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-__global__ __launch_bounds__(kThreads) void k_gemm_q8_0(const uint8_t* W, int64_t rows, int64_t cols,
-                                                        const BlockQ8* x, int n, float* __restrict__ y,
-                                                        int64_t ys, int accumulate, int n_rt, int n_tt) {
+__device__ __forceinline__ void load_lds4(const void* g, uint8_t* l) {
+  __builtin_amdgcn_global_load_lds((glb_void*)g, (lds_void*)l, 4, 0, 0);
+}
+
+// waves_per_eu(1): the register budget of one wave per SIMD, so the two pipeline register sets never spill (the
+// kernel needs about 230 VGPRs, so two waves per SIMD still fit when the grid has them).
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm_q8_0(
+    const uint8_t* W, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* __restrict__ y, int64_t ys,
+    int accumulate, int n_rt, int n_tt, int vec) {
   extern __shared__ __align__(16) uint8_t smem[];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int wr = w & 1, wt = w >> 1;  // wave quarter: rows 32 wr, tokens 32 wt
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;  // wave w: rows 32 w .. 32 w + 31 of the tile
   // Workgroup -> (row tile, token tile). Consecutive workgroups go to consecutive XCDs; the token tiles of a row tile
   // are placed 8 apart so they share an XCD and its L2 holds the rows once.
   int rt, tt;
@@ -67,121 +103,182 @@ __global__ __launch_bounds__(kThreads) void k_gemm_q8_0(const uint8_t* W, int64_
   const int nb = (int)(cols / 32);
   const PackedQ8_0 L{rows, nb};
   const int64_t g0 = (int64_t)rt * (kRowsT / 8);                  // first 8-row group of the tile
-  const int ngroups = (int)min<int64_t>(kRowsT / 8, rows / 8 - g0);  // 8 or 4 (rows % 64 == 32)
+  const int ngroups = (int)min<int64_t>(kRowsT / 8, rows / 8 - g0);  // 4 .. 16 (rows % 32 == 0)
   const int t0 = tt * kTokT;
   const int nstages = (nb + kKB - 1) / kKB;
 
-  // Copy mapping (loads never predicated: past the matrix they re-read valid data, unused).
-  //   A piece p = tid + 256 k: block p / 128, group (p / 16) % 8, plane (p / 8) % 2, row-in-group p % 8.
-  //   B word  q = tid + 256 k: token q / 40, word q % 40 of its 8 consecutive BlockQ8 (5 words each).
-  //   scales: thread tid < 64: block tid / 8, group tid % 8.
-  // One stage's global data, in registers between the load and the store to LDS: A, 1024 16-byte pieces per stage
-  // (4 per thread); B, 512 (token, block) BlockQ8 = 2560 8-byte words (10 per thread); weight scales, 64 (group,
-  // block) pieces of 8 f16 (threads 0..63).
-  v4i ra[4];
-  v2i rb[10];
-  v4i rs;
-  auto load_stage = [&](int s) __attribute__((always_inline)) {
-    const int b0 = min(s, nstages - 1) * kKB;
+  // Copy mapping. Loads are never predicated: past the matrix they re-read valid data, unused.
+  //   A: wave w copies its own 32 rows, one 1 KB instruction per block: lane -> row 32 w + lane / 2, physical half
+  //      lane % 2 (logical half (lane % 2) ^ ((lane / 16) & 1)), 16 bytes of plane h of the row's group unit.
+  //   B: wave w copies block w: two instructions, tokens 32 c + lane / 2, the same half mapping, 16 qs bytes.
+  //   dx: wave w, block w: lane -> token lane, the BlockQ8 d.
+  //   dw: wave w, block w: lane -> the f16 scales of rows 2 lane, 2 lane + 1 (4 bytes of a group's 16-byte entry).
+  // Addresses are a wave-uniform base that moves with the block plus a fixed 32-bit per-lane offset.
+  const int a_row = 32 * w + (lane >> 1);
+  const int a_gi = min(a_row >> 3, ngroups - 1);
+  const int half_sw = (lane & 1) ^ ((lane >> 4) & 1);
+  const uint32_t a_off = (uint32_t)(a_gi * nb * 256 + (half_sw << 7) + (a_row & 7) * 16);
+  const uint32_t b_off0 = (uint32_t)((min(t0 + (lane >> 1), n - 1) - t0) * nb * 40 + 8 + 16 * half_sw);
+  const uint32_t b_off1 = (uint32_t)((min(t0 + 32 + (lane >> 1), n - 1) - t0) * nb * 40 + 8 + 16 * half_sw);
+  const uint32_t dx_off = (uint32_t)((min(t0 + lane, n - 1) - t0) * nb * 40);
+  const uint32_t dw_off = (uint32_t)(min(lane >> 2, ngroups - 1) * nb * 16 + 4 * (lane & 3));
+  const uint8_t* a_base = W + L.quants(g0, 0);
+  const uint8_t* x_base = reinterpret_cast<const uint8_t*>(x + (int64_t)t0 * nb);
+  const uint8_t* dw_base = W + L.scales(g0, 0);
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  // Stage sn into LDS buffer BUF.
+  auto issue = [&]<int BUF>(int sn) __attribute__((always_inline)) {
+    uint8_t* st = smem + BUF * StageLds::bytes;
+    const int b0 = sn * kKB;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int p = tid + kThreads * k;
-      const int b = min(b0 + p / 128, nb - 1), gi = min((p / 16) % 8, ngroups - 1), pl = (p / 8) % 2, r8 = p % 8;
-      ra[k] = *reinterpret_cast<const v4i*>(W + L.quants(g0 + gi, b) + pl * 128 + r8 * 16);
-    }
-#pragma unroll
-    for (int k = 0; k < 10; ++k) {
-      const int q = tid + kThreads * k;
-      const int tok = min(t0 + q / 40, n - 1), wd = q % 40;
-      const int b = min(b0 + wd / 5, nb - 1);
-      rb[k] = reinterpret_cast<const v2i*>(x + (int64_t)tok * nb + b)[wd % 5];
-    }
-    {
-      const int b = min(b0 + (tid & 63) / 8, nb - 1), gi = min(tid % 8, ngroups - 1);
-      rs = *reinterpret_cast<const v4i*>(W + L.scales(g0 + gi, b));
-    }
-  };
-  auto store_stage = [&](int buf) __attribute__((always_inline)) {
-    uint8_t* st = smem + buf * StageLds::bytes;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int p = tid + kThreads * k;
-      const int bl = p / 128, gi = (p / 16) % 8, pl = (p / 8) % 2, r8 = p % 8;
-      *reinterpret_cast<v4i*>(st + StageLds::a + bl * kRowsT * 32 + slab_off(gi * 8 + r8, pl)) = ra[k];
-    }
-#pragma unroll
-    for (int k = 0; k < 10; ++k) {
-      const int q = tid + kThreads * k;
-      const int tok = q / 40, wd = q % 40, bl = wd / 5, part = wd % 5;
-      if (part == 0) {
-        reinterpret_cast<float*>(st + StageLds::dx)[bl * kTokT + tok] = __int_as_float(rb[k].x);  // d; s unused
-      } else {
-        // qs bytes 8 (part - 1) .. + 7: half (part - 1) / 2, 8-byte word (part - 1) % 2 of it
-        const int h = (part - 1) >> 1, wi = (part - 1) & 1;
-        *reinterpret_cast<v2i*>(st + StageLds::b + bl * kTokT * 32 + slab_off(tok, h) + 8 * wi) = rb[k];
-      }
-    }
-    if (tid < 64) {
-      const int bl = tid / 8, gi = tid % 8;
-      const uint32_t hw[4] = {(uint32_t)rs.x, (uint32_t)rs.y, (uint32_t)rs.z, (uint32_t)rs.w};
-      float f[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) f[i] = half_to_float((uint16_t)(hw[i >> 1] >> (16 * (i & 1))));
-      float4* d = reinterpret_cast<float4*>(st + StageLds::dw + (bl * kRowsT + gi * 8) * 4);
-      d[0] = make_float4(f[0], f[1], f[2], f[3]);
-      d[1] = make_float4(f[4], f[5], f[6], f[7]);
-    }
+    for (int k = 0; k < kKB; ++k)
+      load_lds16(a_base + (size_t)min(b0 + k, nb - 1) * 256 + a_off, st + StageLds::a + k * kRowsT * 32 + wu * 1024);
+    const int b = min(b0 + wu, nb - 1);
+    load_lds16(x_base + (size_t)b * 40 + b_off0, st + StageLds::b + wu * kTokT * 32);
+    load_lds16(x_base + (size_t)b * 40 + b_off1, st + StageLds::b + wu * kTokT * 32 + 32 * 32);
+    load_lds4(x_base + (size_t)b * 40 + dx_off, st + StageLds::dx + wu * kTokT * 4);
+    load_lds4(dw_base + (size_t)b * 16 + dw_off, st + StageLds::dw + wu * kRowsT * 2);
   };
 
-  float acc[16];
+  v16f acc0 = {}, acc1 = {};  // tokens 0..31, 32..63
+  v16i magic;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-  const v16i zero = {};
+  for (int i = 0; i < 16; ++i) magic[i] = kMagic;
+  asm volatile("" : "+v"(magic));  // keep it in VGPRs: as a uniform value it would be copied from SGPRs per MFMA
+  const v32f zero = {};
   const int li = lane & 31, h = lane >> 5;
-  const int arow = 32 * wr + li, btok = 32 * wt + li;
+  const int arow = 32 * w + li;
+  // LDS byte offsets of this lane's operands within a stage buffer, block 0.
+  const int off_a = StageLds::a + slab_off(arow, h), off_b0 = StageLds::b + slab_off(li, h),
+            off_b1 = StageLds::b + slab_off(32 + li, h), off_dw = StageLds::dw + 2 * arow,
+            off_dx = StageLds::dx + 4 * lane;
 
-  // Block bl of a stage: MFMA, then the epilogue in block order.
-  auto block = [&](const uint8_t* st, int bl) __attribute__((always_inline)) {
-    const v4i a = *reinterpret_cast<const v4i*>(st + StageLds::a + bl * kRowsT * 32 + slab_off(arow, h));
-    const v4i bv = *reinterpret_cast<const v4i*>(st + StageLds::b + bl * kTokT * 32 + slab_off(btok, h));
-    const float dx = reinterpret_cast<const float*>(st + StageLds::dx)[bl * kTokT + btok];
-    const float4* dw = reinterpret_cast<const float4*>(st + StageLds::dw + (bl * kRowsT + 32 * wr + 4 * h) * 4);
-    float dwv[16];
+  // Software pipeline over blocks j = 0, 1, ..., two register sets (X = even j, Y = odd j). Step j:
+  //   read the operands of block j + 1 (the first block of a stage: entered between the steps),
+  //   MFMAs of block j (scale products, int8 dots, their conversions; operands read in step j - 1),
+  //   fmas of block j - 1, interleaved with those MFMAs.
+  // A wave issues one instruction every few cycles, in order, and one wave per SIMD is the common case here, so the
+  // overlap of matrix and vector work has to be in the instruction stream itself, and the stream has to be short:
+  // each MFMA is followed by about as many VALU instructions as cover its time in the matrix pipe, and the loop is
+  // unrolled over the whole LDS ring (kNS stages of kKB blocks) so every LDS offset is an immediate. Blocks past the
+  // end (nb % kKB != 0) read a copy of the last block with dw = dx = 0: their products are 0 and fma(f, 0, acc) ==
+  // acc (the chain never holds -0), so they add nothing. The results of "block -1" start at zero for the same reason.
+  auto read = [&]<int BUF, int BL>(v4i& ra, v4i& rb0, v4i& rb1, uint16_t& rdw, float& rdx)
+      __attribute__((always_inline)) {
+    const uint8_t* st = smem + BUF * StageLds::bytes;
+    ra = *reinterpret_cast<const v4i*>(st + off_a + BL * kRowsT * 32);
+    rb0 = *reinterpret_cast<const v4i*>(st + off_b0 + BL * kTokT * 32);
+    rb1 = *reinterpret_cast<const v4i*>(st + off_b1 + BL * kTokT * 32);
+    rdw = *reinterpret_cast<const uint16_t*>(st + off_dw + BL * kRowsT * 2);
+    rdx = *reinterpret_cast<const float*>(st + off_dx + BL * kTokT * 4);
+  };
+  // fmas i0 .. i1 - 1 of one 16-output half. The empty asm keeps them in their region: without it the compiler moves
+  // them into a later one, past the MFMAs they are meant to overlap.
+  auto fold = [&](v16f& acc, const v16f& f, const v32f& pp, int t, int i0, int i1) __attribute__((always_inline)) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float4 d4 = dw[2 * q];  // rows 32 wr + 8 q + 4 h .. + 3
-      dwv[4 * q] = d4.x, dwv[4 * q + 1] = d4.y, dwv[4 * q + 2] = d4.z, dwv[4 * q + 3] = d4.w;
+    for (int i = i0; i < i1; ++i) acc[i] = fma_(f[i], pp[16 * t + i], acc[i]);
+    asm volatile("" : "+v"(acc));
+  };
+  // One step: the MFMAs of a block (operands o*, results r*) and the fmas of the previous block (pf*, pp), in five
+  // regions of one MFMA each; the VALU work of a region covers its MFMA's time in the matrix pipe (64 or 32 cycles).
+  // `next` reads the following block's operands at the start. live: the block is inside the matrix (else its
+  // scales are zeroed).
+  auto step = [&](const v4i& oa, const v4i& ob0, const v4i& ob1, uint16_t odw, float odx, bool live, v16f& rf0,
+                  v16f& rf1, v32f& rp, const v16f& pf0, const v16f& pf1, const v32f& pp, auto&& next)
+      __attribute__((always_inline)) {
+    const float dw = live ? half_to_float(odw) : 0.0f, dx = live ? odx : 0.0f;
+    next();
+    rp = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, dx, zero, 0, 0, 0);
+    fold(acc0, pf0, pp, 0, 0, 16);
+    __builtin_amdgcn_sched_barrier(0);
+    rf0 = __builtin_bit_cast(v16f, __builtin_amdgcn_mfma_i32_32x32x32_i8(oa, ob0, magic, 0, 0, 0));
+    fold(acc1, pf1, pp, 1, 0, 8);
+    __builtin_amdgcn_sched_barrier(0);
+    rf1 = __builtin_bit_cast(v16f, __builtin_amdgcn_mfma_i32_32x32x32_i8(oa, ob1, magic, 0, 0, 0));
+    fold(acc1, pf1, pp, 1, 8, 16);
+    __builtin_amdgcn_sched_barrier(0);
+    rf0 = __builtin_amdgcn_mfma_f32_16x16x1f32(-kMagicF, 1.0f, rf0, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    rf1 = __builtin_amdgcn_mfma_f32_16x16x1f32(-kMagicF, 1.0f, rf1, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  v4i xa, xb0, xb1, ya, yb0, yb1;
+  uint16_t xdw, ydw;  // f16 weight scales as read
+  float xdx, ydx;
+  v16f xf0, xf1, yf0 = {}, yf1 = {};
+  v32f xp, yp = {};
+
+  // Stage s (blocks 4 s .. 4 s + 3) from buffer BUF; on entry X holds block 4 s's operands, Y block 4 s - 1's results.
+  // Between its third and fourth step the next stage is entered: it has landed (at most the one after it is
+  // outstanding), every wave is done reading the buffer that stage s + 3 will overwrite (this one: its reads were
+  // issued before and are waited for here), and stage s + 3 is issued into it.
+  auto stage = [&]<int BUF>(int s) __attribute__((always_inline)) {
+    constexpr int NBUF = (BUF + 1) % kNS;
+    const int j = s * kKB;
+    step(xa, xb0, xb1, xdw, xdx, j < nb, xf0, xf1, xp, yf0, yf1, yp,
+         [&]() __attribute__((always_inline)) { read.template operator()<BUF, 1>(ya, yb0, yb1, ydw, ydx); });
+    step(ya, yb0, yb1, ydw, ydx, j + 1 < nb, yf0, yf1, yp, xf0, xf1, xp,
+         [&]() __attribute__((always_inline)) { read.template operator()<BUF, 2>(xa, xb0, xb1, xdw, xdx); });
+    step(xa, xb0, xb1, xdw, xdx, j + 2 < nb, xf0, xf1, xp, yf0, yf1, yp,
+         [&]() __attribute__((always_inline)) { read.template operator()<BUF, 3>(ya, yb0, yb1, ydw, ydx); });
+    if (s + 1 < nstages) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      if (s + 2 < nstages)
+        __builtin_amdgcn_s_waitcnt(0x0F70 | kLoadsPerStage);  // vmcnt(kLoadsPerStage); expcnt, lgkmcnt at max
+      else
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      ring_barrier();
+      if (s + 3 < nstages) issue.template operator()<BUF>(s + 3);
     }
-    const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bv, zero, 0, 0, 0);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] = fma_((float)c[i], dwv[i] * dx, acc[i]);
+    step(ya, yb0, yb1, ydw, ydx, j + 3 < nb, yf0, yf1, yp, xf0, xf1, xp,
+         [&]() __attribute__((always_inline)) { read.template operator()<NBUF, 0>(xa, xb0, xb1, xdw, xdx); });
   };
 
-  load_stage(0);
-  store_stage(0);
-  load_stage(1);
-  lds_barrier();
-  for (int s = 0; s < nstages; ++s) {
-    const uint8_t* st = smem + (s & 1) * StageLds::bytes;
-    const int kb = min(kKB, nb - s * kKB);
-    if (kb == kKB) {
-#pragma unroll
-      for (int bl = 0; bl < kKB; ++bl) block(st, bl);
-    } else {
-      for (int bl = 0; bl < kb; ++bl) block(st, bl);
-    }
-    if (s + 1 < nstages) store_stage((s + 1) & 1);
-    lds_barrier();
-    load_stage(s + 2);
+  issue.template operator()<0>(0);
+  if (nstages > 1) issue.template operator()<1>(1);
+  if (nstages > 1)
+    __builtin_amdgcn_s_waitcnt(0x0F70 | kLoadsPerStage);
+  else
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+  ring_barrier();
+  if (nstages > 2) issue.template operator()<2>(2);
+  read.template operator()<0, 0>(xa, xb0, xb1, xdw, xdx);
+  // Whole ring cycles: up to two stages past the end run with every block's scales zeroed (exact no-ops), which
+  // keeps one loop exit and the register sets in place.
+  for (int s = 0; s < nstages; s += kNS) {
+    stage.template operator()<0>(s);
+    stage.template operator()<1>(s + 1);
+    stage.template operator()<2>(s + 2);
   }
+  fold(acc0, yf0, yp, 0, 0, 16);
+  fold(acc1, yf1, yp, 1, 0, 16);
+  // The last stage's loads were waited for (vmcnt(0)) when it was entered; nothing is in flight past the loop.
 
-  const int t = t0 + btok;
-  if (t < n && 32 * wr < 8 * ngroups) {
-    float* yt = y + (int64_t)t * ys + (int64_t)rt * kRowsT + 32 * wr;
+  // Element i of tile j: row 32 w + 8 (i / 4) + 4 h + i % 4, token 32 j + li.
+  if (32 * w < 8 * ngroups) {
+    float* yr = y + (int64_t)rt * kRowsT + 32 * w + 4 * h;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int m = 8 * (i >> 2) + 4 * h + (i & 3);
-      yt[m] = accumulate ? yt[m] + acc[i] : acc[i];
+    for (int j = 0; j < 2; ++j) {
+      const int t = t0 + 32 * j + li;
+      if (t >= n) continue;
+      float* yt = yr + (int64_t)t * ys;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const v16f& av = j ? acc1 : acc0;
+        const float v[4] = {av[4 * q], av[4 * q + 1], av[4 * q + 2], av[4 * q + 3]};
+        if (vec) {
+          float4* p = reinterpret_cast<float4*>(yt + 8 * q);
+          float4 o = make_float4(v[0], v[1], v[2], v[3]);
+          if (accumulate) {
+            const float4 e = *p;
+            o = make_float4(e.x + o.x, e.y + o.y, e.z + o.z, e.w + o.w);
+          }
+          *p = o;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) yt[8 * q + e] = accumulate ? yt[8 * q + e] + v[e] : v[e];
+        }
+      }
     }
   }
 }
@@ -195,7 +292,8 @@ void gemm_q8_0(hipStream_t s, const void* w, int64_t rows, int64_t cols, const B
   require(gemm_q8_0_supported(rows, cols, n), "gemm_q8_0: rows must be a multiple of 32, n > 8");
   const int n_rt = (int)((rows + kRowsT - 1) / kRowsT);
   const int n_tt = (n + kTokT - 1) / kTokT;
-  const size_t lds = 2 * (size_t)StageLds::bytes;
+  const size_t lds = kNS * (size_t)StageLds::bytes;
+  const int vec = (reinterpret_cast<uintptr_t>(y) % 16 == 0 && ys % 4 == 0) ? 1 : 0;
   static bool attr = false;
   if (!attr) {
     check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_q8_0), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -204,7 +302,7 @@ void gemm_q8_0(hipStream_t s, const void* w, int64_t rows, int64_t cols, const B
     attr = true;
   }
   hipLaunchKernelGGL(k_gemm_q8_0, dim3((unsigned)((int64_t)n_rt * n_tt)), dim3(kThreads), lds, s,
-                     static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0, n_rt, n_tt);
+                     static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0, n_rt, n_tt, vec);
   check_launch("gemm_q8_0");
 }
 

@@ -172,6 +172,9 @@ LARGE = [(t, n, 256, 4096) for t in (mk_.Q8_0, mk_.Q4_K, mk_.Q6_K) for n in (1, 
     (mk_.Q8_0, 40, 96, 512),      # a full and a half-height row tile: the plain tile order
     (mk_.Q8_0, 24, 64, 416),      # 13 blocks: a partial last K stage
     (mk_.Q8_0, 70, 32, 96),       # one half-height row tile, a single short K stage, two token tiles
+    (mk_.Q8_0, 9, 1024, 256),     # the smallest GEMM batch: 8 row tiles (XCD-mapped), 55 idle token columns
+    (mk_.Q8_0, 100, 160, 1024),   # a full and a quarter-height 128-row tile; second token tile 36 tokens
+    (mk_.Q8_0, 65, 1120, 320),    # 9 row tiles (plain order), 10 blocks: a 2-block last K stage
 ]
 
 
@@ -191,6 +194,29 @@ def test_matmul_large_vs_oracle(mk, oracle, t, n, rows, k):
     yd = mk.to_device(base)
     _matmul(mk, t, packed, rows, k, xq.view(np.uint8), n, True, y=yd, accumulate=True)
     assert np.array_equal(bits(yd.download(np.float32).reshape(n, rows)), bits(base + exp))
+
+
+@pytest.mark.parametrize("t,n,rows,k", [(mk_.Q8_0, 40, 96, 512), (mk_.Q8_0, 3, 64, 256)])
+def test_matmul_strided_output(mk, oracle, t, n, rows, k):
+    """y at a 4-byte offset with an odd token stride: the GEMM's scalar store path and the GEMV's strided stores."""
+    import make_golden
+    rng = np.random.default_rng(11 * n + rows)
+    w = make_golden.random_rows(rng, t, rows, k)
+    x = rng.uniform(-2, 2, (n, k)).astype(np.float32)
+    xq = oracle.quantize_row_q8(x)
+    packed = _packed(mk, t, w, rows, k)
+    exp = oracle.matmul(t, w, rows, k, xq.reshape(-1), wide=True)
+    ys = rows + 3
+    base = rng.standard_normal(n * ys + 1).astype(np.float32)
+    yd = mk.to_device(base)
+    dxq = mk.to_device(xq.view(np.uint8))
+    wt = MkWeight(t, 1, rows, k, packed.p)
+    mk_.check(L().mk_matmul(mk.h, ctypes.byref(wt), dxq.ptr, n, ctypes.c_void_p(yd.p + 4), ys, 1))
+    got = yd.download(np.float32)
+    want = base.copy()
+    view = want[1:].reshape(n, ys)
+    view[:, :rows] += exp
+    assert np.array_equal(bits(got), bits(want))
 
 
 F32_CASES = [(t, n, rows, k) for t in (mk_.Q8_0, mk_.Q4_K, mk_.Q6_K) for n in (1, 2) for rows, k in ((64, 256), (96, 4096))] + [
