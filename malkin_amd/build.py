@@ -21,6 +21,7 @@ HIP_SOURCES = [
     "csrc/kernels/pack.hip",
     "csrc/kernels/gemv.hip",
     "csrc/kernels/gemm.hip",
+    "csrc/kernels/gemm_kq.hip",
     "csrc/kernels/quant.hip",
     "csrc/kernels/attn.hip",
     "csrc/kernels/capi.cpp",
@@ -45,6 +46,7 @@ HIP_FLAGS = [
 # with VALU instructions; the AGPR form would add one v_accvgpr_read per element and block).
 EXTRA_FLAGS = {
     "csrc/kernels/gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "csrc/kernels/gemm_kq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 LIB = os.path.join(HERE, "libmalkin_hip.so")

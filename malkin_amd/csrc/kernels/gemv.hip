@@ -677,6 +677,11 @@ void matmul_f32_type(hipStream_t s, int type, bool wide, const void* w, int64_t 
   }
 }
 
+// K-quant batches: the int8-MFMA GEMM walks K serially per 128-row tile, so with few row tiles and few tokens the
+// GEMV (rows spread over every CU) is faster. Measured crossover on MI355X, 4096..12288 columns: the GEMM wins from
+// 6144 rows at any n > 8, and from n > 16 (Q4_K) / n > 32 (Q6_K) at 4096 rows.
+bool kq_gemm_first(int type, int64_t rows, int n) { return rows >= 6144 || n > 32 || (type == kQ4_K && n > 16); }
+
 }  // namespace
 
 void matmul(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int64_t cols, const BlockQ8* xq, int n,
@@ -692,11 +697,16 @@ void matmul(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int
         launch_r<kQ8_0, false>(s, w, rows, cols, in, n, y, ys, accumulate);
       break;
     case kQ4_K:
-      launch_r<kQ4_K, false>(s, w, rows, cols, in, n, y, ys, accumulate);
+      if (gemm_kq_supported(type, rows, cols, n) && kq_gemm_first(type, rows, n))
+        gemm_kq(s, type, wide, w, rows, cols, xq, n, y, ys, accumulate);  // batches: int8 MFMA
+      else
+        launch_r<kQ4_K, false>(s, w, rows, cols, in, n, y, ys, accumulate);
       break;
     case kQ6_K:
       // The reference switches Q6_K to its wide panels above kWideMinTokens = 16 tokens (quant.cpp:256).
-      if (wide && n > 16)
+      if (gemm_kq_supported(type, rows, cols, n) && kq_gemm_first(type, rows, n))
+        gemm_kq(s, type, wide, w, rows, cols, xq, n, y, ys, accumulate);
+      else if (wide && n > 16)
         launch_r<kQ6_K, true>(s, w, rows, cols, in, n, y, ys, accumulate);
       else
         launch_r<kQ6_K, false>(s, w, rows, cols, in, n, y, ys, accumulate);

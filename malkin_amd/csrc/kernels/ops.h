@@ -73,6 +73,10 @@ void matmul_f32(hipStream_t s, int type, bool wide, const void* w, int64_t rows,
 bool gemm_q8_0_supported(int64_t rows, int64_t cols, int n);
 void gemm_q8_0(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y, int64_t ys,
                bool accumulate);
+// The same for Q4_K and Q6_K (Q6_K: wide-panel arithmetic when wide and n > 16); rows % 32 == 0, cols % 256 == 0, n > 8.
+bool gemm_kq_supported(int type, int64_t rows, int64_t cols, int n);
+void gemm_kq(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n,
+             float* y, int64_t ys, bool accumulate);
 
 // Generic attention addressing: key row (t, g, row) at k + seq*k_seq + g*k_head + row*k_row (bytes), its scale at
 // ks + seq*s_seq + g*s_head + row*s_row (bytes); values likewise with v / vs.

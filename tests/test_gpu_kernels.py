@@ -175,6 +175,18 @@ LARGE = [(t, n, 256, 4096) for t in (mk_.Q8_0, mk_.Q4_K, mk_.Q6_K) for n in (1, 
     (mk_.Q8_0, 9, 1024, 256),     # the smallest GEMM batch: 8 row tiles (XCD-mapped), 55 idle token columns
     (mk_.Q8_0, 100, 160, 1024),   # a full and a quarter-height 128-row tile; second token tile 36 tokens
     (mk_.Q8_0, 65, 1120, 320),    # 9 row tiles (plain order), 10 blocks: a 2-block last K stage
+    # K-quant int8-MFMA GEMM (n > 32, or 6144+ rows): partial row tiles, several token tiles, XCD-mapped grids, 1..4
+    # ring cycles; below that the GEMV takes the batch (the 9- and 17-token cases on few rows)
+    (mk_.Q4_K, 9, 128, 512),
+    (mk_.Q4_K, 100, 160, 1024),
+    (mk_.Q4_K, 64, 1024, 1536),
+    (mk_.Q4_K, 9, 6144, 256),     # the smallest GEMM batch
+    (mk_.Q6_K, 9, 128, 512),
+    (mk_.Q6_K, 9, 6144, 256),     # n <= 16: compact arithmetic in the GEMM
+    (mk_.Q6_K, 16, 6176, 512),    # 49 row tiles (plain order), the last a quarter tile
+    (mk_.Q6_K, 17, 6144, 512),    # the tree-verify batch size: wide arithmetic in the GEMM
+    (mk_.Q6_K, 17, 1024, 1024),   # ... and in the GEMV
+    (mk_.Q6_K, 100, 160, 2560),
 ]
 
 
@@ -217,6 +229,20 @@ def test_matmul_strided_output(mk, oracle, t, n, rows, k):
     view = want[1:].reshape(n, ys)
     view[:, :rows] += exp
     assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("t,n,rows,k", [(mk_.Q6_K, 40, 160, 1024), (mk_.Q6_K, 33, 64, 512), (mk_.Q4_K, 40, 64, 512)])
+def test_matmul_compact_batches(mk, oracle, t, n, rows, k):
+    """wide = 0 (MALKIN_NO_WIDE): the compact arithmetic at every batch size, through the K-quant GEMM."""
+    import make_golden
+    rng = np.random.default_rng(5 * n + rows + t)
+    w = make_golden.random_rows(rng, t, rows, k)
+    x = rng.uniform(-2, 2, (n, k)).astype(np.float32)
+    xq = oracle.quantize_row_q8(x)
+    packed = _packed(mk, t, w, rows, k)
+    exp = oracle.matmul(t, w, rows, k, xq.reshape(-1), wide=False)
+    y = _matmul(mk, t, packed, rows, k, xq.view(np.uint8), n, False).download(np.float32).reshape(n, rows)
+    assert np.array_equal(bits(y), bits(exp))
 
 
 F32_CASES = [(t, n, rows, k) for t in (mk_.Q8_0, mk_.Q4_K, mk_.Q6_K) for n in (1, 2) for rows, k in ((64, 256), (96, 4096))] + [
