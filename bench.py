@@ -40,14 +40,16 @@ def prompt_ids(n, vocab):
     return np.array([1000 + (i * 7919) % 20000 for i in range(n)], dtype=np.int32) % vocab
 
 
-def model_file(preset, seed):
+def model_file(preset, seed, wtype=None, mix=None):
     from malkin_amd import synth
-    cfg = synth.make_config(preset, synth.Q8_0, seed=seed)
+    wtype = synth.Q8_0 if wtype is None else wtype
+    mix = synth.MIX_UNIFORM if mix is None else mix
+    cfg = synth.make_config(preset, wtype, mix=mix, seed=seed)
     d = "/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir()
     st = os.statvfs(d)
     if st.f_bavail * st.f_frsize < synth.file_bytes(cfg) * 1.1:
         d = tempfile.gettempdir()
-    path = os.path.join(d, f"malkin_bench_{preset}_q8_0_s{seed}_{os.getpid()}.gguf")
+    path = os.path.join(d, f"malkin_bench_{preset}_t{wtype}_m{mix}_s{seed}_{os.getpid()}.gguf")
     t0 = time.time()
     synth.write_gguf(path, cfg, threads=min(16, os.cpu_count() or 1))
     log(f"[bench] wrote {path} ({os.path.getsize(path) / 1e9:.2f} GB) in {time.time() - t0:.1f} s")
@@ -270,6 +272,105 @@ def cpu_baseline(path, vocab, budget_s=30.0):
             "pp512_tok_s": round(N_PROMPT / pp_s, 2), "tg_tok_s": round(1.0 / per_tok, 3)}
 
 
+def config4(ctx, path):
+    """the Qwen3-8B Q8_0 model, 8 concurrent sequences with random-id prompts of 256..1024 tokens,
+    128 greedy tokens each, continuous batching on the device engine (one batched forward per step: decode rows of
+    every decoding sequence plus prompt chunks up to 256 tokens), KV cache ctx 4096 per sequence."""
+    import malkin_amd as mk
+    rng = np.random.default_rng(4)
+    m = mk.Model(ctx, path, N_CTX, 8)
+    try:
+        V = m.cfg["n_vocab"]
+        prompts = [rng.integers(0, V, size=int(L)).astype(np.int32) for L in rng.integers(256, 1025, size=8)]
+        warm = mk.Engine(m)
+        warm.submit(prompts[0][:64], 4)
+        warm.run()
+        warm.close()
+        e = mk.Engine(m)
+        ctx.sync()
+        t0 = time.perf_counter()
+        ids = [e.submit(p, 128) for p in prompts]
+        steps = 0
+        while e.step() > 0:
+            steps += 1
+        ctx.sync()
+        wall = time.perf_counter() - t0
+        infos = [e.result(i)[1] for i in ids]
+        e.close()
+    finally:
+        m.close()
+    n_prompt = int(sum(len(p) for p in prompts))
+    n_gen = int(sum(i["completion_tokens"] for i in infos))
+    return {"workload": "qwen3-8b-q8_0, 8 sequences, prompts 256..1024 (random ids), 128 greedy tokens each, "
+                        "continuous batching, ctx 4096",
+            "prompt_tokens": n_prompt, "gen_tokens": n_gen, "engine_steps": steps + 1, "wall_s": round(wall, 3),
+            "tokens_per_s": round((n_prompt + n_gen) / wall, 1), "gen_tokens_per_s": round(n_gen / wall, 1),
+            "mean_prefill_ms": round(float(np.mean([i["prefill_ms"] for i in infos])), 1),
+            "mean_decode_ms": round(float(np.mean([i["decode_ms"] for i in infos])), 1)}
+
+
+def config5(ctx):
+    """target Qwen3-14B in Q6_K, draft Qwen3-0.6B in Q4_K_M, 2048-token prefix. (a) One tree
+    verification: the target forward of 17 nodes (next token + a chain of 8 drafts + one runner-up per depth, the
+    engine's tree layout) with the tree attention mask over the 2048-token KV prefix, greedy picks on the device; (b)
+    the speculative engine (draft chain / runner-up tree, n_draft 8) generating 64 tokens after that prompt."""
+    import malkin_amd as mk
+    from malkin_amd import synth
+    rng = np.random.default_rng(5)
+    tpath, _ = model_file("qwen3-14b", seed=5, wtype=synth.Q6_K)
+    dpath, _ = model_file("qwen3-0.6b", seed=6, wtype=synth.Q4_K, mix=synth.MIX_Q4_K_M)
+    try:
+        t = mk.Model(ctx, tpath, N_CTX, 1)
+        d = mk.Model(ctx, dpath, N_CTX, 1)
+        V = t.cfg["n_vocab"]
+        P = 2048
+        prompt = rng.integers(0, V, size=P).astype(np.int32)
+        ctx.sync()
+        t0 = time.perf_counter()
+        for i in range(0, P, 256):
+            t.forward(prompt[i:i + 256], i)
+        ctx.sync()
+        prefill_s = time.perf_counter() - t0
+        ids = rng.integers(0, V, size=17)
+        nodes = [(int(ids[0]), 0, P, 1)]
+        for k in range(8):
+            par = 0 if k == 0 else 2 * k - 1
+            nodes.append((int(ids[1 + 2 * k]), 0, P + 1 + k, 1, P + 1 + 2 * k, par))
+            nodes.append((int(ids[2 + 2 * k]), 0, P + 1 + k, 1, P + 2 + 2 * k, par))
+        tree = mk.batch(nodes)
+        t.forward_top2(tree)
+        ctx.sync()
+        reps = 10
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            t.forward_top2(tree)
+        ctx.sync()
+        verify_ms = (time.perf_counter() - t0) * 1e3 / reps
+        e = mk.Engine(t, d, 8)
+        ctx.sync()
+        t0 = time.perf_counter()
+        rid = e.submit(prompt, 64)
+        e.run()
+        ctx.sync()
+        wall = time.perf_counter() - t0
+        _, info = e.result(rid)
+        e.close()
+        d.close()
+        t.close()
+    finally:
+        for p in (tpath, dpath):
+            if os.path.exists(p):
+                os.remove(p)
+    return {"workload": "qwen3-14b-q6_k target + qwen3-0.6b-q4_k_m draft, 2048-token prompt (random ids), tree of "
+                        "17 nodes per verification",
+            "verify_ms": round(verify_ms, 3), "verify_nodes": 17, "prefix_prefill_tok_s": round(P / prefill_s, 1),
+            "spec_gen_tokens": info["completion_tokens"], "spec_wall_s": round(wall, 3),
+            "spec_decode_tok_s": round(info["completion_tokens"] * 1e3 / max(info["decode_ms"], 1e-9), 1),
+            "drafted": info["drafted"], "accepted": info["accepted"],
+            "note": "random-init target and draft agree on almost no token, so nearly every verification accepts "
+                    "only its root; verify_ms is the per-pass cost"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -282,6 +383,8 @@ def main():
                          "follow graph launches); same kernels")
     ap.add_argument("--no-kernel-configs", action="store_true",
                     help="skip the kernel-level configurations (config 1 GEMM, config 2 GEMV)")
+    ap.add_argument("--no-engine-configs", action="store_true",
+                    help="skip BASELINE configs 4 (continuous batching) and 5 (speculative tree verification)")
     ap.add_argument("--probe", choices=["traffic"],
                     help="only run the launch sequence for the roofline kernel's HBM counters")
     args = ap.parse_args()
@@ -324,6 +427,12 @@ def main():
         kern = None if args.no_kernel_configs else kernel_configs(ctx)
         if kern:
             log("[bench] kernel configs: " + json.dumps(kern))
+        engine = None
+        if not args.no_engine_configs:
+            engine = {"config4": config4(ctx, path)}
+            log("[bench] config 4: " + json.dumps(engine["config4"]))
+            engine["config5"] = config5(ctx)
+            log("[bench] config 5: " + json.dumps(engine["config5"]))
         cpu = None if args.no_cpu_baseline else cpu_baseline(path, cfg["n_vocab"])
         ctx.close()
     finally:
@@ -354,6 +463,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "kernel_configs": kern,
+        "engine_configs": engine,
     }
     print(json.dumps(line), flush=True)
 
