@@ -125,8 +125,10 @@ struct GemvCfg {
   static constexpr int UQ8 = Unit<TYPE>::q8;
   static constexpr int E = (TYPE == kQ6_K && WIDE) ? 1 : Unit<TYPE>::e;
   static constexpr int kWorkers = kThreads - 64;
-  // Units per pipeline step: the (row, unit) pairs of a chunk spread evenly over the workers.
-  static constexpr int kChunk = R == 8 ? (NT <= 2 ? 96 : NT == 4 ? 48 : 24) : 24;
+  // Units per pipeline step: the (row, unit) pairs of a chunk spread evenly over the workers. Measured on MI355X
+  // (Qwen3-8B decode shapes, one token): 48 units beat 24, 96 and 144 (a shorter fill and drain per row group), and
+  // a third or fourth register set in flight did not help.
+  static constexpr int kChunk = R == 8 ? (NT <= 4 ? 48 : 24) : 24;
   static constexpr int kP = kChunk * R / kWorkers;  // pairs per worker per chunk
   static_assert(kChunk * R % kWorkers == 0, "chunk must split evenly over the workers");
   static_assert(R * NT <= 64, "one chain per lane of wave 0");
@@ -264,14 +266,21 @@ __global__ __launch_bounds__(kThreads) void k_gemv(const uint8_t* W, int64_t row
         quantize_half_block(v[t], c16 & 1, c16 < per, reinterpret_cast<BlockQ8*>(xs + t * nq8 * 10) + c16 / 2);
       }
     };
+    // One token: the first kPre passes (12288 columns) are all loaded before the weights, so the row costs one
+    // memory round trip instead of one per pass.
+    constexpr int kPre = NT == 1 ? 3 : 1;
     {
-      float v[NT][16];
-      pass(v, 0, true);
+      float v[kPre][NT][16];
+#pragma unroll
+      for (int p = 0; p < kPre; ++p)
+        if (p == 0 || p * kThreads < per) pass(v[p], p, true);  // uniform
       load(ra, 0);
       load(rb, 1);
-      pass(v, 0, false);
+#pragma unroll
+      for (int p = 0; p < kPre; ++p)
+        if (p == 0 || p * kThreads < per) pass(v[p], p, false);
     }
-    for (int p = 1; p * kThreads < per; ++p) {  // uniform
+    for (int p = kPre; p * kThreads < per; ++p) {  // uniform
       float v[NT][16];
       pass(v, p, true);
       pass(v, p, false);
@@ -616,10 +625,7 @@ void launch(hipStream_t s, const void* w, int64_t rows, int64_t cols, const Gemv
   const int per_cu = resident_per_cu(k_gemv<TYPE, WIDE, R, NT, PRO, EPI>, lds);
   const int64_t groups = rows / R, tgroups = (n + NT - 1) / NT;
   const int64_t resident = (int64_t)per_cu * device_cus();
-  // The rmsnorm prologue (16 KB of rows and norm weights, a dependent chain) is paid once per workgroup: at least
-  // two row groups per workgroup. (The quantize-only prologue measured faster with one.)
-  const int64_t per_wg = PRO == kProNorm ? 2 : 1;
-  const int64_t gx = std::max<int64_t>(1, std::min<int64_t>((groups + per_wg - 1) / per_wg, resident / tgroups));
+  const int64_t gx = std::max<int64_t>(1, std::min<int64_t>(groups, resident / tgroups));
   const dim3 grid((unsigned)gx, (unsigned)tgroups);
   hipLaunchKernelGGL((k_gemv<TYPE, WIDE, R, NT, PRO, EPI>), grid, dim3(kThreads), lds, s, static_cast<const uint8_t*>(w),
                      rows, cols, in, n, y, ys, accumulate ? 1 : 0);
