@@ -20,6 +20,7 @@ ARCH = os.environ.get("MALKIN_ARCH", "gfx950")
 HIP_SOURCES = [
     "csrc/kernels/pack.hip",
     "csrc/kernels/gemv.hip",
+    "csrc/kernels/gemv_mma.hip",
     "csrc/kernels/gemm.hip",
     "csrc/kernels/gemm_kq.hip",
     "csrc/kernels/quant.hip",

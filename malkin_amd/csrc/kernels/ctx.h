@@ -39,6 +39,17 @@ inline void check(hipError_t e, const char* what) {
 // The launch's own error (bad configuration) and any asynchronous fault reported so far.
 inline void check_launch(const char* what) { check(hipGetLastError(), what); }
 
+// Compute units of the current device (queried once: the library runs one device per process).
+inline int device_cus() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0;
+    check(hipGetDevice(&dev), "hipGetDevice");
+    check(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
+  }
+  return n;
+}
+
 template <typename F>
 int guard(F&& f) {
   try {

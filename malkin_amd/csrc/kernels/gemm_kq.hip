@@ -18,6 +18,8 @@
 //
 // A workgroup (4 waves) owns a 128-row x 32-token tile, 32 rows per wave, and walks K in stages of half a super-block
 // (4 units of 32 weights) held in a ring of 3 LDS buffers filled by direct global -> LDS loads two stages ahead.
+#include <utility>
+
 #include "ctx.h"
 #include "ops.h"
 
@@ -34,7 +36,6 @@ typedef __attribute__((address_space(1))) void glb_void;
 constexpr int kThreads = 256;
 constexpr int kRowsT = 128, kTokT = 32;  // workgroup tile
 constexpr int kKB = 4;                   // 32-weight units per stage (half a super-block)
-constexpr int kNS = 3;                   // stages in the LDS ring
 constexpr int kMagic = 0x4B400000;       // bits of 12582912.0f
 constexpr float kMagicF = 12582912.0f;
 
@@ -72,6 +73,26 @@ __device__ __forceinline__ void load_lds4(const void* g, uint8_t* l) {
 // prefetches too.
 __device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
+// s_waitcnt vmcnt(N) (N < 64: bits 3:0 and 15:14), expcnt and lgkmcnt left at their maximum.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+// vmcnt(k * PER) for a runtime k in [0, KMAX].
+template <int PER, int KMAX>
+__device__ __forceinline__ void wait_vm_stages(int k) {
+  if constexpr (KMAX > 0) {
+    if (k >= KMAX) {
+      wait_vm<KMAX * PER>();
+      return;
+    }
+    wait_vm_stages<PER, KMAX - 1>(k);
+  } else {
+    wait_vm<0>();
+  }
+}
+
 // float(int8 byte K of v)
 template <int K>
 __device__ __forceinline__ float sbyte_f(uint32_t v) {
@@ -101,7 +122,9 @@ __device__ __forceinline__ void scale_min(int j, uint32_t q0, uint32_t q1, uint3
   }
 }
 
-template <int TYPE, bool WIDE>
+// NS: stages in the LDS ring, NS - 1 of them in flight. 3 when the grid takes several workgroups per CU (prefill);
+// deeper rings when few row tiles cover the matrix (short batches), where the stream is latency-bound otherwise.
+template <int TYPE, bool WIDE, int NS>
 __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t rows, int64_t cols,
                                                       const BlockQ8* x, int n, float* __restrict__ y, int64_t ys,
                                                       int accumulate, int n_rt, int n_tt) {
@@ -232,15 +255,13 @@ __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t 
   };
 
   auto stage = [&]<int BUF>(int s) __attribute__((always_inline)) {
-    // Stage s has landed once at most stage s + 1's loads are outstanding; the buffer stage s + 2 goes into was read
-    // in stage s - 1, finished by every wave before this barrier.
+    // Stage s has landed once at most the loads of the stages issued after it (s + 1 .. s + NS - 2, fewer at the
+    // end) are outstanding; the buffer stage s + NS - 1 goes into was read in stage s - 1, finished by every wave
+    // before this barrier.
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    if (s + 1 < nstages)
-      __builtin_amdgcn_s_waitcnt(0x0F70 | S::loads);  // vmcnt(S::loads)
-    else
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    wait_vm_stages<S::loads, NS - 2>(min(NS - 2, nstages - 1 - s));
     ring_barrier();
-    if (s + 2 < nstages) issue.template operator()<(BUF + 2) % kNS>(s + 2);
+    if (s + NS - 1 < nstages) issue.template operator()<(BUF + NS - 1) % NS>(s + NS - 1);
     uint8_t* st = smem + BUF * S::bytes;
     const int hf = s & 1;
     if constexpr (TYPE == kQ6_K) {
@@ -332,12 +353,13 @@ __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t 
     }
   };
 
-  issue.template operator()<0>(0);
-  if (nstages > 1) issue.template operator()<1>(1);
-  for (int s = 0; s < nstages; s += kNS) {
-    stage.template operator()<0>(s);
-    if (s + 1 < nstages) stage.template operator()<1>(s + 1);
-    if (s + 2 < nstages) stage.template operator()<2>(s + 2);
+  [&]<int... B>(std::integer_sequence<int, B...>) __attribute__((always_inline)) {
+    ((B < nstages ? issue.template operator()<B>(B) : void()), ...);
+  }(std::make_integer_sequence<int, NS - 1>{});
+  for (int s = 0; s < nstages; s += NS) {
+    [&]<int... B>(std::integer_sequence<int, B...>) __attribute__((always_inline)) {
+      ((s + B < nstages ? stage.template operator()<B>(s + B) : void()), ...);
+    }(std::make_integer_sequence<int, NS>{});
   }
 
   // Element i: token t0 + 8 (i / 4) + 4 h + i % 4, row 128 rt + 32 w + li.
@@ -354,14 +376,35 @@ __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t 
   }
 }
 
+template <int TYPE, bool WIDE, int NS>
+void launch_kq_ns(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
+                  int64_t ys, bool accumulate, int n_rt, int n_tt) {
+  const size_t lds = NS * (size_t)KqLds<TYPE>::bytes;
+  static bool attr = false;  // per instantiation: rings past 64 KB of dynamic LDS
+  if (!attr) {
+    check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_kq<TYPE, WIDE, NS>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+          "hipFuncSetAttribute");
+    attr = true;
+  }
+  hipLaunchKernelGGL((k_gemm_kq<TYPE, WIDE, NS>), dim3((unsigned)((int64_t)n_rt * n_tt)), dim3(kThreads), lds, s,
+                     static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0, n_rt, n_tt);
+}
+
+// Ring depth by grid size: one workgroup per CU takes an 8-stage ring (7 stages, about 130 KB, in flight), two per CU
+// a 4-stage ring; larger grids (prefill) keep 3 stages and several workgroups per CU.
 template <int TYPE, bool WIDE>
 void launch_kq(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y, int64_t ys,
                bool accumulate) {
   const int n_rt = (int)((rows + kRowsT - 1) / kRowsT);
   const int n_tt = (n + kTokT - 1) / kTokT;
-  const size_t lds = kNS * (size_t)KqLds<TYPE>::bytes;
-  hipLaunchKernelGGL((k_gemm_kq<TYPE, WIDE>), dim3((unsigned)((int64_t)n_rt * n_tt)), dim3(kThreads), lds, s,
-                     static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0, n_rt, n_tt);
+  const int64_t wgs = (int64_t)n_rt * n_tt, cus = device_cus();
+  if (wgs <= cus)
+    launch_kq_ns<TYPE, WIDE, 8>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt);
+  else if (wgs <= 2 * cus)
+    launch_kq_ns<TYPE, WIDE, 4>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt);
+  else
+    launch_kq_ns<TYPE, WIDE, 3>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt);
 }
 
 }  // namespace

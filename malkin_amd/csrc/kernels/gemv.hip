@@ -573,17 +573,6 @@ __global__ __launch_bounds__(kThreads) void k_gemv(const uint8_t* W, int64_t row
   chain(nq - 1);
 }
 
-// Compute units of the current device (queried once: the library runs one device per process).
-int device_cus() {
-  static int n = 0;
-  if (n == 0) {
-    int dev = 0;
-    check(hipGetDevice(&dev), "hipGetDevice");
-    check(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
-  }
-  return n;
-}
-
 // Resident workgroups per CU of a kernel at a given dynamic LDS size (cached per size).
 template <typename K>
 int resident_per_cu(K kernel, size_t lds) {
@@ -683,10 +672,20 @@ void matmul_f32_type(hipStream_t s, int type, bool wide, const void* w, int64_t 
   }
 }
 
-// K-quant batches: the int8-MFMA GEMM walks K serially per 128-row tile, so with few row tiles and few tokens the
-// GEMV (rows spread over every CU) is faster. Measured crossover on MI355X, 4096..12288 columns: the GEMM wins from
-// 6144 rows at any n > 8, and from n > 16 (Q4_K) / n > 32 (Q6_K) at 4096 rows.
-bool kq_gemm_first(int type, int64_t rows, int n) { return rows >= 6144 || n > 32 || (type == kQ4_K && n > 16); }
+// K-quant batches past mmv's range (or where mmv_first declines): the int8-MFMA GEMM walks K serially per 128-row
+// tile, so it needs many rows or many tokens to beat the GEMV.
+bool kq_gemm_first(int type, int64_t rows, int n) { return n > 16 && (rows >= 16384 || n > 32); }
+
+// Short batches on the MFMA short-batch kernel (mmv). Measured on MI355X over the Qwen3-8B/14B shapes (Q8_0, Q4_K,
+// Q6_K; results of all three kernels compared bit for bit): the GEMV wins up to 4 tokens, and up to 8 on matrices of
+// fewer than 12288 rows; mmv from there to 16 tokens; from 17 to 32 tokens mmv, except on the widest matrices, where
+// the GEMMs' 32- and 64-token tiles win.
+bool mmv_first(int type, int64_t rows, int64_t cols, int n) {
+  if (n <= 4 || n > 32 || !mmv_supported(type, rows, cols, n)) return false;
+  if (n <= 8) return rows >= 12288;
+  if (n <= 16) return true;
+  return rows < (type == kQ6_K ? 24576 : 16384);
+}
 
 }  // namespace
 
@@ -695,6 +694,10 @@ void matmul(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int
   require(n > 0, "matmul: no tokens");
   require(packed_bytes(type, rows, cols) != 0, "matmul: no kernel for this weight type/shape");
   const GemvIn in{xq, nullptr, 0, nullptr, 0.0f};
+  if (mmv_first(type, rows, cols, n)) {
+    mmv(s, type, wide, w, rows, cols, xq, n, y, ys, accumulate);
+    return;
+  }
   switch (type) {
     case kQ8_0:
       if (gemm_q8_0_supported(rows, cols, n))

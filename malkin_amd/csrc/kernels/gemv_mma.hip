@@ -1,0 +1,394 @@
+// Short-batch matmul (2..32 tokens) on int8 MFMA, bit-identical to the reference's panel kernels: the continuous-
+// batching decode steps, tree verification batches and short prompt tails, where the batch is too small for the
+// prefill GEMMs' 32- and 64-token tiles and too large for the decode GEMV's per-token VALU dot products.
+//
+// Per output (row r, token t) the reference keeps one fp32 chain over the row's 32-weight units in order
+// (gemm_avx512.cpp:67-102 Q8_0, 104-155 Q4_K, 157-205 Q6_K, 268-316 Q6_K wide):
+//   Q8_0            acc = fma(float(ai), f16(dw) * dx, acc)
+//   Q4_K (sub-block j)  acc = fma(float(ai), (d sc_j) * dx, acc);  acc = fma(-(dmin m_j), dx * (s0 + s1), acc)
+//   Q6_K compact (halves h = 0, 1)  acc = fma(float(ai_h), (d sc_h) * dx, acc)
+//   Q6_K wide       acc = fma(fma(float(ai_1), d sc_1, float(ai_0) * (d sc_0)), dx, acc)
+// where ai is the exact int32 dot of the unit (of its 16-value half for Q6_K) with the BlockQ8 activation quants.
+//
+// A workgroup is two waves; wave w owns 16 rows (two 8-row groups of the packed layout) and computes, per unit, the
+// 16 x 16 (tokens x rows) int dots with one v_mfma_i32_16x16x32_i8 (two for Q6_K: one per half, the other half's
+// operand bytes zeroed) per 16-token tile, then applies the reference's epilogue to the 4 accumulator elements of
+// each lane (tokens 4 (l / 16) + i, row l % 16): every chain lives in one accumulator element and advances unit by
+// unit in order. The operands stream through a ring of NS LDS stages of 8 units (256 weights), filled by direct
+// global -> LDS loads NS - 1 stages ahead: each wave copies its own rows' packed records (whole 1 KB pieces of the
+// layout.h planes) and half of the stage's activation quants and scales, shared by both waves.
+//
+// Operand layouts of v_mfma_i32_16x16x32_i8 (A: tokens x K, B: K x rows): lane l holds A[l % 16][8 (l / 16) ..
+// 8 (l / 16) + 7] and B[8 (l / 16) .. + 7][l % 16]; result element i of lane l is (token 4 (l / 16) + i, row l % 16).
+// The int dot of a unit is independent of the order of its K index, so each lane may take any 8 of the unit's 32
+// weights as long as its A bytes are the matching activations; here lane quarter c = l / 16 takes weights
+// 8 c .. 8 c + 7 in natural order.
+#include <utility>
+
+#include "ctx.h"
+#include "ops.h"
+
+namespace mk {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void glb_void;
+
+constexpr int kWaves = 2, kThreads = 64 * kWaves;
+constexpr int kRowsW = 16;                // rows per wave (MFMA N)
+constexpr int kRowsT = kRowsW * kWaves;   // rows per workgroup
+constexpr int kUnits = 8;                 // 32-weight units per stage
+
+__device__ __forceinline__ void ld16(const void* g, uint8_t* l) {
+  __builtin_amdgcn_global_load_lds((glb_void*)g, (lds_void*)l, 16, 0, 0);
+}
+__device__ __forceinline__ void ld4(const void* g, uint8_t* l) {
+  __builtin_amdgcn_global_load_lds((glb_void*)g, (lds_void*)l, 4, 0, 0);
+}
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+template <int PER, int KMAX>
+__device__ __forceinline__ void wait_vm_stages(int k) {
+  if constexpr (KMAX > 0) {
+    if (k >= KMAX) {
+      wait_vm<KMAX * PER>();
+      return;
+    }
+    wait_vm_stages<PER, KMAX - 1>(k);
+  } else {
+    wait_vm<0>();
+  }
+}
+
+// q - 32 per byte for bytes q < 64 (never borrows across bytes).
+__device__ __forceinline__ uint32_t minus32(uint32_t q) { return ((q | 0x80808080u) - 0x20202020u) ^ 0x80808080u; }
+
+// scale_min_k4 (kernels.h:18-26) over the 12 packed scale bytes of a Q4_K header held in q0..q2.
+__device__ __forceinline__ int hbyte(uint32_t q0, uint32_t q1, uint32_t q2, int i) {
+  const uint32_t w = i < 4 ? q0 : (i < 8 ? q1 : q2);
+  return (int)((w >> (8 * (i & 3))) & 0xFFu);
+}
+__device__ __forceinline__ void scale_min(int j, uint32_t q0, uint32_t q1, uint32_t q2, int& sc, int& m) {
+  if (j < 4) {
+    sc = hbyte(q0, q1, q2, j) & 63;
+    m = hbyte(q0, q1, q2, j + 4) & 63;
+  } else {
+    const int hi = hbyte(q0, q1, q2, j + 4);
+    sc = (hi & 0xF) | ((hbyte(q0, q1, q2, j - 4) >> 6) << 4);
+    m = (hi >> 4) | ((hbyte(q0, q1, q2, j) >> 6) << 4);
+  }
+}
+
+// Stage layout (bytes) for NTT 16-token tiles. Per wave: W (its 16 rows' packed quants for the stage's 8 units), S (the
+// rows' scale records: Q8_0 f16 scales, Q6_K int8 sub-scales, Q4_K headers), D (Q6_K: f16 d; 256 B because the copy
+// is lane-linear). Shared: X [unit][token][32 B] quants, DX [unit][token] f32 d, XS [unit][token] (s0, s1) (Q4_K).
+template <int TYPE, int NTT>
+struct MmvLds {
+  static constexpr int w_bytes = TYPE == kQ8_0 ? 2 * 8 * 256 : TYPE == kQ6_K ? 2 * 1536 : 2 * 1024;
+  static constexpr int per_wave = w_bytes + 256 + (TYPE == kQ6_K ? 256 : 0);
+  static constexpr int s_off = w_bytes, d_off = w_bytes + 256;
+  static constexpr int x = kWaves * per_wave;
+  static constexpr int dx = x + kUnits * 16 * NTT * 32;
+  static constexpr int xs = dx + kUnits * 16 * NTT * 4;
+  static constexpr int bytes = xs + (TYPE == kQ4_K ? kUnits * 16 * NTT * 4 : 0);
+  // global -> LDS loads per wave per stage (every wave issues the same count)
+  static constexpr int loads = w_bytes / 1024 + 1 + (TYPE == kQ6_K ? 1 : 0) + 2 * NTT + NTT + (TYPE == kQ4_K ? NTT : 0);
+};
+
+template <int TYPE, bool WIDE, int NTT, int NS>
+__global__ __launch_bounds__(kThreads) void k_mmv(const uint8_t* W, int64_t rows, int64_t cols, const BlockQ8* x,
+                                                  int n, float* __restrict__ y, int64_t ys, int accumulate) {
+  using S = MmvLds<TYPE, NTT>;
+  static_assert((NS - 1) * S::loads < 64, "the ring's loads must fit the vmcnt counter");
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wu = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rt = blockIdx.x;                        // 32-row tile
+  const int t0 = blockIdx.y * 16 * NTT;             // first token of the tile
+  const int ntok = min(16 * NTT, n - t0);           // tokens present (>= 1)
+  const int nq8 = (int)(cols / 32);
+  const int nst = nq8 / kUnits;                     // stages (cols % 256 == 0)
+  const int64_t g0w = (int64_t)rt * 4 + 2 * wu;     // first 8-row group of this wave
+
+  // Per-lane constant source offsets of the copies (bytes); the moving part is a wave-uniform base per stage.
+  //   W: lane-linear 16-byte pieces of the wave's W region; S/D: 4-byte pieces of its scale records;
+  //   X: WG pieces 2 NTT wu + k (k < 2 NTT): 1 KB each of [unit][token][32 B]; DX/XS: 256-byte pieces NTT wu + k.
+  const uint8_t* xb = reinterpret_cast<const uint8_t*>(x + (int64_t)t0 * nq8);
+  uint32_t x_off[2 * NTT], dx_off[NTT];
+#pragma unroll
+  for (int k = 0; k < 2 * NTT; ++k) {
+    const int p = 1024 * (2 * NTT * wu + k) + 16 * lane;
+    const int unit = p / (512 * NTT), rem = p % (512 * NTT);
+    const int tok = min(rem / 32, ntok - 1), half = (rem % 32) / 16;
+    x_off[k] = (uint32_t)((tok * nq8 + unit) * 40 + 8 + 16 * half);
+  }
+#pragma unroll
+  for (int k = 0; k < NTT; ++k) {
+    const int p = 256 * (NTT * wu + k) + 4 * lane;
+    const int unit = p / (64 * NTT), tok = min((p % (64 * NTT)) / 4, ntok - 1);
+    dx_off[k] = (uint32_t)((tok * nq8 + unit) * 40);
+  }
+  const uint8_t* wq;  // quants of group g0w at stage 0
+  const uint8_t* ws;  // scale records of group g0w at stage 0
+  const uint8_t* wd = nullptr;
+  uint32_t w_off[S::w_bytes / 1024], s_off, d_off = 0;
+  int64_t wq_step, ws_step;  // bytes per stage
+  if constexpr (TYPE == kQ8_0) {
+    const PackedQ8_0 L{rows, nq8};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int p = 1024 * k + 16 * lane;
+      w_off[k] = (uint32_t)((p / 2048) * nq8 * 256 + p % 2048);
+    }
+    s_off = (uint32_t)((lane / 32) * nq8 * 16 + 4 * (lane % 32));
+    wq = W + L.quants(g0w, 0);
+    ws = W + L.scales(g0w, 0);
+    wq_step = 8 * 256;
+    ws_step = 8 * 16;
+  } else if constexpr (TYPE == kQ6_K) {
+    const int nsb = nq8 / 8;
+    const PackedQ6_K L{rows, nsb};
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const int p = 1024 * k + 16 * lane;
+      w_off[k] = (uint32_t)((p / 1536) * nsb * 1536 + p % 1536);
+    }
+    s_off = (uint32_t)((lane / 32) * nsb * 128 + 4 * (lane % 32));
+    {
+      const int p = 4 * min(lane, 7);
+      d_off = (uint32_t)((p / 16) * nsb * 16 + p % 16);
+    }
+    wq = W + L.quants(g0w, 0, 0);
+    ws = W + L.scales(g0w, 0);
+    wd = W + L.dscale(g0w, 0);
+    wq_step = 1536;
+    ws_step = 128;
+  } else {
+    const int nsb = nq8 / 8;
+    const PackedQ4_K L{rows, nsb};
+#pragma unroll
+    for (int k = 0; k < 2; ++k) w_off[k] = (uint32_t)(k * nsb * 1024 + 16 * lane);
+    s_off = (uint32_t)((lane / 32) * nsb * 128 + 4 * (lane % 32));
+    wq = W + L.quants(g0w, 0, 0);
+    ws = W + L.headers(g0w, 0);
+    wq_step = 1024;
+    ws_step = 128;
+  }
+
+  auto issue = [&]<int BUF>(int sn) __attribute__((always_inline)) {
+    uint8_t* st = smem + BUF * S::bytes;
+    uint8_t* wv = st + wu * S::per_wave;
+    const uint8_t* q = wq + (size_t)sn * wq_step;
+#pragma unroll
+    for (int k = 0; k < S::w_bytes / 1024; ++k) ld16(q + w_off[k], wv + 1024 * k);
+    ld4(ws + (size_t)sn * ws_step + s_off, wv + S::s_off);
+    if constexpr (TYPE == kQ6_K) ld4(wd + (size_t)sn * 16 + d_off, wv + S::d_off);
+    const uint8_t* xs = xb + (size_t)sn * kUnits * 40;
+#pragma unroll
+    for (int k = 0; k < 2 * NTT; ++k) ld16(xs + x_off[k], st + S::x + 1024 * (2 * NTT * wu + k));
+#pragma unroll
+    for (int k = 0; k < NTT; ++k) ld4(xs + dx_off[k], st + S::dx + 256 * (NTT * wu + k));
+    if constexpr (TYPE == kQ4_K) {
+#pragma unroll
+      for (int k = 0; k < NTT; ++k) ld4(xs + dx_off[k] + 4, st + S::xs + 256 * (NTT * wu + k));
+    }
+  };
+
+  // This lane: row r = lane % 16 of the wave's 16 (group gi = r / 8, row rr = r % 8), weight quarter c = lane / 16;
+  // accumulator elements i: tokens 4 c + i (+ 16 m for tile m).
+  const int r = lane & 15, c = lane >> 4, gi = r >> 3, rr = r & 7;
+  float acc[NTT][4];
+#pragma unroll
+  for (int m = 0; m < NTT; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[m][i] = 0.0f;
+  const v4i zero4 = {0, 0, 0, 0};
+
+  auto stage = [&]<int BUF>(int s) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the buffer refilled below are done
+    wait_vm_stages<S::loads, NS - 2>(min(NS - 2, nst - 1 - s));
+    ring_barrier();
+    if (s + NS - 1 < nst) issue.template operator()<(BUF + NS - 1) % NS>(s + NS - 1);
+    const uint8_t* st = smem + BUF * S::bytes;
+    const uint8_t* wv = st + wu * S::per_wave;
+    if constexpr (TYPE == kQ8_0) {
+#pragma unroll
+      for (int u = 0; u < kUnits; ++u) {
+        const long b = *reinterpret_cast<const long*>(wv + gi * 2048 + u * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
+        const float dw = half_to_float(*reinterpret_cast<const uint16_t*>(wv + S::s_off + gi * 128 + u * 16 + rr * 2));
+#pragma unroll
+        for (int m = 0; m < NTT; ++m) {
+          const long a = *reinterpret_cast<const long*>(st + S::x + ((u * NTT + m) * 16 + r) * 32 + 8 * c);
+          const float4 dx = *reinterpret_cast<const float4*>(st + S::dx + ((u * NTT + m) * 16 + 4 * c) * 4);
+          const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero4, 0, 0, 0);
+          acc[m][0] = fma_((float)d[0], dw * dx.x, acc[m][0]);
+          acc[m][1] = fma_((float)d[1], dw * dx.y, acc[m][1]);
+          acc[m][2] = fma_((float)d[2], dw * dx.z, acc[m][2]);
+          acc[m][3] = fma_((float)d[3], dw * dx.w, acc[m][3]);
+        }
+      }
+    } else if constexpr (TYPE == kQ6_K) {
+      const float dd = half_to_float(*reinterpret_cast<const uint16_t*>(wv + S::d_off + gi * 16 + rr * 2));
+      const int hw = c >> 1, h = c & 1;
+#pragma unroll
+      for (int u = 0; u < kUnits; ++u) {
+        const uint8_t* au = wv + gi * 1536 + u * 192;
+        const uint2 nib = *reinterpret_cast<const uint2*>(au + rr * 16 + 8 * h);
+        const uint2 hb = *reinterpret_cast<const uint2*>(au + 128 + rr * 8);
+        // weights 8 c .. 8 c + 7 = q[16 hw + 8 h + 0..7] of the unit
+        const uint32_t hv = (hw ? hb.y : hb.x) >> (4 * h);
+        const uint32_t q0 = ((nib.x >> (4 * hw)) & 0x0F0F0F0Fu) | ((hv & 0x03030303u) << 4);
+        const uint32_t q1 = ((nib.y >> (4 * hw)) & 0x0F0F0F0Fu) | (((hv >> 2) & 0x03030303u) << 4);
+        const long bq = (long)(((uint64_t)minus32(q1) << 32) | minus32(q0));
+        const long b0 = hw ? 0 : bq, b1 = hw ? bq : 0;
+        const uint32_t scw = *reinterpret_cast<const uint16_t*>(wv + S::s_off + gi * 128 + rr * 16 + 2 * u);
+        const float dsc0 = dd * (float)(int8_t)(scw & 0xFF), dsc1 = dd * (float)(int8_t)(scw >> 8);
+#pragma unroll
+        for (int m = 0; m < NTT; ++m) {
+          const long a = *reinterpret_cast<const long*>(st + S::x + ((u * NTT + m) * 16 + r) * 32 + 8 * c);
+          const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + ((u * NTT + m) * 16 + 4 * c) * 4);
+          const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+          const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b0, zero4, 0, 0, 0);
+          const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, zero4, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if constexpr (WIDE) {
+              const float sm = fma_((float)d1[i], dsc1, (float)d0[i] * dsc0);
+              acc[m][i] = fma_(sm, dx[i], acc[m][i]);
+            } else {
+              acc[m][i] = fma_((float)d0[i], dsc0 * dx[i], acc[m][i]);
+              acc[m][i] = fma_((float)d1[i], dsc1 * dx[i], acc[m][i]);
+            }
+          }
+        }
+      }
+    } else {  // Q4_K: unit u = sub-block j = u of the stage's super-block; chunk j2 = u / 2, nibble u % 2
+      const uint4 hd = *reinterpret_cast<const uint4*>(wv + S::s_off + gi * 128 + rr * 16);
+      const float d = half_to_float((uint16_t)(hd.x & 0xFFFF)), dmin = half_to_float((uint16_t)(hd.x >> 16));
+#pragma unroll
+      for (int j2 = 0; j2 < 4; ++j2) {
+        const uint2 raw =
+            *reinterpret_cast<const uint2*>(wv + gi * 1024 + j2 * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int u = 2 * j2 + e;
+          const long bq = (long)(((uint64_t)((raw.y >> (4 * e)) & 0x0F0F0F0Fu) << 32) | ((raw.x >> (4 * e)) & 0x0F0F0F0Fu));
+          int sc, mn;
+          scale_min(u, hd.y, hd.z, hd.w, sc, mn);
+          const float fsc = d * (float)sc, nmn = -(dmin * (float)mn);
+#pragma unroll
+          for (int m = 0; m < NTT; ++m) {
+            const long a = *reinterpret_cast<const long*>(st + S::x + ((u * NTT + m) * 16 + r) * 32 + 8 * c);
+            const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + ((u * NTT + m) * 16 + 4 * c) * 4);
+            const uint4 sx4 = *reinterpret_cast<const uint4*>(st + S::xs + ((u * NTT + m) * 16 + 4 * c) * 4);
+            const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+            const uint32_t sx[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
+            const v4i dq = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq, zero4, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float xsum = dx[i] * (float)((int)(int16_t)(sx[i] & 0xFFFF) + (int)(int16_t)(sx[i] >> 16));
+              acc[m][i] = fma_((float)dq[i], fsc * dx[i], acc[m][i]);
+              acc[m][i] = fma_(nmn, xsum, acc[m][i]);
+            }
+          }
+        }
+      }
+    }
+  };
+
+  [&]<int... B>(std::integer_sequence<int, B...>) __attribute__((always_inline)) {
+    ((B < nst ? issue.template operator()<B>(B) : void()), ...);
+  }(std::make_integer_sequence<int, NS - 1>{});
+  for (int s = 0; s < nst; s += NS) {
+    [&]<int... B>(std::integer_sequence<int, B...>) __attribute__((always_inline)) {
+      ((s + B < nst ? stage.template operator()<B>(s + B) : void()), ...);
+    }(std::make_integer_sequence<int, NS>{});
+  }
+
+  const int64_t row = (int64_t)rt * kRowsT + wu * kRowsW + r;
+#pragma unroll
+  for (int m = 0; m < NTT; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * m + 4 * c + i;
+      if (t < ntok) {
+        float* o = y + (int64_t)(t0 + t) * ys + row;
+        *o = accumulate ? *o + acc[m][i] : acc[m][i];
+      }
+    }
+}
+
+template <int TYPE, bool WIDE, int NTT, int NS>
+void launch_ns(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
+               int64_t ys, bool accumulate) {
+  const size_t lds = NS * (size_t)MmvLds<TYPE, NTT>::bytes;
+  static bool attr = false;  // per instantiation: rings past 64 KB of dynamic LDS
+  if (!attr) {
+    check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_mmv<TYPE, WIDE, NTT, NS>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+          "hipFuncSetAttribute");
+    attr = true;
+  }
+  const int tiles = (n + 16 * NTT - 1) / (16 * NTT);
+  hipLaunchKernelGGL((k_mmv<TYPE, WIDE, NTT, NS>), dim3((unsigned)(rows / kRowsT), (unsigned)tiles), dim3(kThreads),
+                     lds, s, static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0);
+}
+
+// Ring depth by grid size: with at most one workgroup per CU the deepest ring the vmcnt counter allows; with more,
+// rings small enough for 2..4 resident workgroups per CU.
+template <int TYPE, bool WIDE, int NTT>
+void launch_ntt(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
+                int64_t ys, bool accumulate) {
+  const int64_t wgs = rows / kRowsT * ((n + 16 * NTT - 1) / (16 * NTT)), cus = device_cus();
+  constexpr int kDeep = NTT == 1 ? 8 : 6;
+  if (wgs <= cus)
+    launch_ns<TYPE, WIDE, NTT, kDeep>(s, w, rows, cols, x, n, y, ys, accumulate);
+  else if (wgs <= 2 * cus)
+    launch_ns<TYPE, WIDE, NTT, 5>(s, w, rows, cols, x, n, y, ys, accumulate);
+  else
+    launch_ns<TYPE, WIDE, NTT, 3>(s, w, rows, cols, x, n, y, ys, accumulate);
+}
+
+template <int TYPE, bool WIDE>
+void launch_mmv(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
+                int64_t ys, bool accumulate) {
+  if (n <= 16)
+    launch_ntt<TYPE, WIDE, 1>(s, w, rows, cols, x, n, y, ys, accumulate);
+  else
+    launch_ntt<TYPE, WIDE, 2>(s, w, rows, cols, x, n, y, ys, accumulate);
+}
+
+}  // namespace
+
+bool mmv_supported(int type, int64_t rows, int64_t cols, int n) {
+  return (type == kQ8_0 || type == kQ4_K || type == kQ6_K) && n >= 1 && n <= 32 && rows % kRowsT == 0 &&
+         cols % (32 * kUnits) == 0;
+}
+
+void mmv(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n,
+         float* y, int64_t ys, bool accumulate) {
+  require(mmv_supported(type, rows, cols, n), "mmv: Q8_0/Q4_K/Q6_K, 1..32 tokens, rows % 32 == 0, cols % 256 == 0");
+  switch (type) {
+    case kQ8_0:
+      launch_mmv<kQ8_0, false>(s, w, rows, cols, x, n, y, ys, accumulate);
+      break;
+    case kQ4_K:
+      launch_mmv<kQ4_K, false>(s, w, rows, cols, x, n, y, ys, accumulate);
+      break;
+    default:  // Q6_K: the reference's wide panels above 16 tokens (quant.cpp:256)
+      if (wide && n > 16)
+        launch_mmv<kQ6_K, true>(s, w, rows, cols, x, n, y, ys, accumulate);
+      else
+        launch_mmv<kQ6_K, false>(s, w, rows, cols, x, n, y, ys, accumulate);
+      break;
+  }
+  check_launch("mmv");
+}
+
+}  // namespace mk

@@ -78,6 +78,12 @@ bool gemm_kq_supported(int type, int64_t rows, int64_t cols, int n);
 void gemm_kq(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n,
              float* y, int64_t ys, bool accumulate);
 
+// Short batches (1..32 tokens) of any quantized type on int8 MFMA, 16-row x 16-token tiles streamed through a deep LDS
+// ring (same results as matmul's other kernels); rows % 32 == 0, cols % 256 == 0.
+bool mmv_supported(int type, int64_t rows, int64_t cols, int n);
+void mmv(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n,
+         float* y, int64_t ys, bool accumulate);
+
 // Generic attention addressing: key row (t, g, row) at k + seq*k_seq + g*k_head + row*k_row (bytes), its scale at
 // ks + seq*s_seq + g*s_head + row*s_row (bytes); values likewise with v / vs.
 // k_perm: K rows are stored permuted (kv_perm below), as the device KV cache keeps them; else in element order.
