@@ -72,6 +72,26 @@ __device__ __forceinline__ float reduce16_lanes(float v) {
   return v;
 }
 
+// Direct global -> LDS copies: lane i writes its 16 (or 4) bytes at the wave-uniform LDS address + 16 i (4 i). They
+// are issued as inline assembly so that the compiler does not track them as LDS stores: it cannot tell a copy into a
+// later pipeline stage from the stage being read and would wait for every copy in flight (vmcnt(0)) before each LDS
+// read, which empties a prefetch ring. Kernels using them order them explicitly: a stage is read only after its own
+// copies are waited for (s_waitcnt vmcnt) and a barrier, and a buffer is refilled only after the barrier that follows
+// its last reads. M0 is named as clobbered (the copies set it); the compiler warns about clobbering a register it
+// reserves, which is the intent here.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ uint32_t lds_addr(const void* l) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)l;
+}
+__device__ __forceinline__ void lds_copy16(const void* g, void* l) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_addr(l)) : "m0");
+}
+__device__ __forceinline__ void lds_copy4(const void* g, void* l) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_addr(l)) : "m0");
+}
+#pragma clang diagnostic pop
+
 // Workgroup barrier that orders LDS only. __syncthreads() also waits for every outstanding global load of the
 // calling wave, which would turn loads issued ahead of a barrier (prefetches) into a full memory round trip.
 __device__ __forceinline__ void lds_barrier() {

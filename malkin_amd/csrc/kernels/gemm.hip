@@ -66,18 +66,14 @@ static_assert(kNS == 3, "the main loop is unrolled over a ring of 3 buffers");
 // Byte offset of half h (0/1) of row r within a [rows][32 B] operand slab.
 __device__ __forceinline__ int slab_off(int r, int h) { return r * 32 + ((h ^ ((r >> 3) & 1)) << 4); }
 
-__device__ __forceinline__ void load_lds16(const void* g, uint8_t* l) {
-  __builtin_amdgcn_global_load_lds((glb_void*)g, (lds_void*)l, 16, 0, 0);
-}
+__device__ __forceinline__ void load_lds16(const void* g, uint8_t* l) { lds_copy16(g, l); }
 // Workgroup barrier for the LDS ring. The loads into LDS are tracked by vmcnt and waited for explicitly (the stage
 // being computed only); a fenced barrier would make the compiler wait for every one of them, prefetches included.
 // Reads of a buffer finish before the barrier that precedes its next fill, because each read feeds an MFMA of the
 // same iteration.
 __device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-__device__ __forceinline__ void load_lds4(const void* g, uint8_t* l) {
-  __builtin_amdgcn_global_load_lds((glb_void*)g, (lds_void*)l, 4, 0, 0);
-}
+__device__ __forceinline__ void load_lds4(const void* g, uint8_t* l) { lds_copy4(g, l); }
 
 // waves_per_eu(1): the register budget of one wave per SIMD, so the two pipeline register sets never spill (the
 // kernel needs about 230 VGPRs, so two waves per SIMD still fit when the grid has them).

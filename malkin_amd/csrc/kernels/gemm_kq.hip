@@ -63,12 +63,8 @@ struct KqLds<kQ4_K> {
   static constexpr int loads = 5;
 };
 
-__device__ __forceinline__ void load_lds16(const void* g, uint8_t* l) {
-  __builtin_amdgcn_global_load_lds((glb_void*)g, (lds_void*)l, 16, 0, 0);
-}
-__device__ __forceinline__ void load_lds4(const void* g, uint8_t* l) {
-  __builtin_amdgcn_global_load_lds((glb_void*)g, (lds_void*)l, 4, 0, 0);
-}
+__device__ __forceinline__ void load_lds16(const void* g, uint8_t* l) { lds_copy16(g, l); }
+__device__ __forceinline__ void load_lds4(const void* g, uint8_t* l) { lds_copy4(g, l); }
 // Barrier for the LDS ring: the loads into LDS are waited for explicitly (vmcnt), a fenced barrier would wait for the
 // prefetches too.
 __device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }

@@ -676,16 +676,17 @@ void matmul_f32_type(hipStream_t s, int type, bool wide, const void* w, int64_t 
 // tile, so it needs many rows or many tokens to beat the GEMV.
 bool kq_gemm_first(int type, int64_t rows, int n) { return n > 16 && (rows >= 16384 || n > 32); }
 
-// Short batches on the MFMA short-batch kernel (mmv). Measured on MI355X over the Qwen3-8B/14B shapes (Q8_0, Q4_K,
-// Q6_K; results of all three kernels compared bit for bit): the GEMV wins up to 4 tokens, and up to 8 on matrices of
-// fewer than 12288 rows; mmv from there to 16 tokens; from 17 to 32 tokens mmv, except on the widest matrices, where
-// the GEMMs' 32- and 64-token tiles win.
+// Short batches on the MFMA short-batch kernels (mmv). Measured on MI355X over the Qwen3-8B/14B shapes (Q8_0, Q4_K,
+// Q6_K; results of every kernel compared bit for bit): the GEMV wins up to 4 tokens; from 5 to 16 tokens mmv, with
+// four waves per 16-row tile (K split inside the workgroup) on matrices of up to 8192 rows and one wave per tile on
+// wider ones; from 17 to 32 tokens the same, except that the GEMMs' 32- and 64-token tiles win on the widest
+// matrices and the one-wave form on Q4_K.
 bool mmv_first(int type, int64_t rows, int64_t cols, int n) {
   if (n <= 4 || n > 32 || !mmv_supported(type, rows, cols, n)) return false;
-  if (n <= 8) return rows >= 12288;
   if (n <= 16) return true;
-  return rows < (type == kQ6_K ? 24576 : 16384);
+  return rows < (type == kQ8_0 ? 16384 : 24576);
 }
+bool mmv_ksplit(int type, int64_t rows, int64_t cols, int n) { return rows <= 8192 && (n <= 16 || type != kQ4_K); }
 
 }  // namespace
 
@@ -695,7 +696,7 @@ void matmul(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int
   require(packed_bytes(type, rows, cols) != 0, "matmul: no kernel for this weight type/shape");
   const GemvIn in{xq, nullptr, 0, nullptr, 0.0f};
   if (mmv_first(type, rows, cols, n)) {
-    mmv(s, type, wide, w, rows, cols, xq, n, y, ys, accumulate);
+    mmv(s, type, wide, w, rows, cols, xq, n, y, ys, accumulate, mmv_ksplit(type, rows, cols, n));
     return;
   }
   switch (type) {

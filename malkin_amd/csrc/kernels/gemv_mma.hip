@@ -32,20 +32,14 @@ namespace mk {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(1))) void glb_void;
 
 constexpr int kWaves = 2, kThreads = 64 * kWaves;
 constexpr int kRowsW = 16;                // rows per wave (MFMA N)
 constexpr int kRowsT = kRowsW * kWaves;   // rows per workgroup
 constexpr int kUnits = 8;                 // 32-weight units per stage
 
-__device__ __forceinline__ void ld16(const void* g, uint8_t* l) {
-  __builtin_amdgcn_global_load_lds((glb_void*)g, (lds_void*)l, 16, 0, 0);
-}
-__device__ __forceinline__ void ld4(const void* g, uint8_t* l) {
-  __builtin_amdgcn_global_load_lds((glb_void*)g, (lds_void*)l, 4, 0, 0);
-}
+__device__ __forceinline__ void ld16(const void* g, uint8_t* l) { lds_copy16(g, l); }
+__device__ __forceinline__ void ld4(const void* g, uint8_t* l) { lds_copy4(g, l); }
 __device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 template <int N>
@@ -324,6 +318,299 @@ __global__ __launch_bounds__(kThreads) void k_mmv(const uint8_t* W, int64_t rows
     }
 }
 
+// K-split form for matrices with few rows (down and attn_output projections): four waves share one 16-row tile.
+// Per stage of 8 units, wave w computes the MFMA dots of units 2 w and 2 w + 1 and their per-unit float terms
+// (the operands of the reference's fmas, rounded as the reference rounds them) into LDS; after a barrier every
+// lane runs the sequential chains of NTT (row, token) outputs over the stage's 8 units in order. Terms per unit and
+// output, E floats: Q8_0 {float(ai), dw dx}; Q6_K compact {float(ai_0), (d sc_0) dx, float(ai_1), (d sc_1) dx};
+// Q6_K wide {fma(float(ai_1), d sc_1, float(ai_0) (d sc_0)), dx}; Q4_K {float(ai), (d sc) dx, -(dmin m),
+// dx (s0 + s1)}; the chain applies acc = fma(e0, e1, acc) (and acc = fma(e2, e3, acc)).
+template <int TYPE, bool WIDE>
+struct Ks {
+  static constexpr int E = (TYPE == kQ8_0 || (TYPE == kQ6_K && WIDE)) ? 2 : 4;
+};
+template <int TYPE, bool WIDE, int NTT>
+struct KsLds {
+  static constexpr int w_bytes = TYPE == kQ8_0 ? 2 * 8 * 256 : TYPE == kQ6_K ? 2 * 1536 : 2 * 1024;
+  static constexpr int s_off = w_bytes, d_off = w_bytes + 256;
+  static constexpr int x = w_bytes + 256 + (TYPE == kQ6_K ? 256 : 0);
+  static constexpr int dx = x + kUnits * 16 * NTT * 32;
+  static constexpr int xs = dx + kUnits * 16 * NTT * 4;
+  static constexpr int bytes = xs + (TYPE == kQ4_K ? kUnits * 16 * NTT * 4 : 0);  // one ring stage
+  static constexpr int terms = kUnits * 16 * NTT * 16 * Ks<TYPE, WIDE>::E * 4;    // the term buffer
+  // loads per wave per stage: W, S, (D), X, DX, (XS); pieces past a wave's share repeat another wave's copy
+  static constexpr int loads = 1 + 1 + (TYPE == kQ6_K ? 1 : 0) + NTT + 1 + (TYPE == kQ4_K ? 1 : 0);
+};
+
+template <int TYPE, bool WIDE, int NTT, int NS>
+__global__ __launch_bounds__(256) void k_mmv_ks(const uint8_t* W, int64_t rows, int64_t cols, const BlockQ8* x,
+                                                 int n, float* __restrict__ y, int64_t ys, int accumulate) {
+  using S = KsLds<TYPE, WIDE, NTT>;
+  constexpr int E = Ks<TYPE, WIDE>::E;
+  static_assert((NS - 1) * S::loads < 64, "the ring's loads must fit the vmcnt counter");
+  extern __shared__ __align__(16) uint8_t smem[];
+  float* terms = reinterpret_cast<float*>(smem + NS * S::bytes);  // [unit][token][row][E]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wu = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rt = blockIdx.x;                        // 16-row tile
+  const int t0 = blockIdx.y * 16 * NTT;
+  const int ntok = min(16 * NTT, n - t0);
+  const int nq8 = (int)(cols / 32);
+  const int nst = nq8 / kUnits;
+  const int64_t g0 = (int64_t)rt * 2;               // first 8-row group
+
+  // Copies. W: 1 KB pieces, wave w takes piece min(w, pieces - 1); S, D: one 256-byte piece, every wave; X: NTT
+  // 1 KB pieces per wave; DX, XS: 256-byte pieces, wave w takes piece w % (2 NTT).
+  constexpr int WP = S::w_bytes / 1024;
+  const uint8_t* xb = reinterpret_cast<const uint8_t*>(x + (int64_t)t0 * nq8);
+  uint32_t x_off[NTT], dx_off;
+#pragma unroll
+  for (int k = 0; k < NTT; ++k) {
+    const int p = 1024 * (NTT * wu + k) + 16 * lane;
+    const int unit = p / (512 * NTT), rem = p % (512 * NTT);
+    const int tok = min(rem / 32, ntok - 1), half = (rem % 32) / 16;
+    x_off[k] = (uint32_t)((tok * nq8 + unit) * 40 + 8 + 16 * half);
+  }
+  const int dxp = wu % (2 * NTT);
+  {
+    const int p = 256 * dxp + 4 * lane;
+    const int unit = p / (64 * NTT), tok = min((p % (64 * NTT)) / 4, ntok - 1);
+    dx_off = (uint32_t)((tok * nq8 + unit) * 40);
+  }
+  const int wp = min(wu, WP - 1);
+  const uint8_t *wq, *ws, *wd = nullptr;
+  uint32_t w_off, s_off, d_off = 0;
+  int64_t wq_step, ws_step;
+  if constexpr (TYPE == kQ8_0) {
+    const PackedQ8_0 L{rows, nq8};
+    const int p = 1024 * wp + 16 * lane;
+    w_off = (uint32_t)((p / 2048) * nq8 * 256 + p % 2048);
+    s_off = (uint32_t)((lane / 32) * nq8 * 16 + 4 * (lane % 32));
+    wq = W + L.quants(g0, 0);
+    ws = W + L.scales(g0, 0);
+    wq_step = 8 * 256;
+    ws_step = 8 * 16;
+  } else if constexpr (TYPE == kQ6_K) {
+    const int nsb = nq8 / 8;
+    const PackedQ6_K L{rows, nsb};
+    const int p = 1024 * wp + 16 * lane;
+    w_off = (uint32_t)((p / 1536) * nsb * 1536 + p % 1536);
+    s_off = (uint32_t)((lane / 32) * nsb * 128 + 4 * (lane % 32));
+    {
+      const int q = 4 * min(lane, 7);
+      d_off = (uint32_t)((q / 16) * nsb * 16 + q % 16);
+    }
+    wq = W + L.quants(g0, 0, 0);
+    ws = W + L.scales(g0, 0);
+    wd = W + L.dscale(g0, 0);
+    wq_step = 1536;
+    ws_step = 128;
+  } else {
+    const int nsb = nq8 / 8;
+    const PackedQ4_K L{rows, nsb};
+    w_off = (uint32_t)(wp * nsb * 1024 + 16 * lane);
+    s_off = (uint32_t)((lane / 32) * nsb * 128 + 4 * (lane % 32));
+    wq = W + L.quants(g0, 0, 0);
+    ws = W + L.headers(g0, 0);
+    wq_step = 1024;
+    ws_step = 128;
+  }
+
+  auto issue = [&]<int BUF>(int sn) __attribute__((always_inline)) {
+    uint8_t* st = smem + BUF * S::bytes;
+    ld16(wq + (size_t)sn * wq_step + w_off, st + 1024 * wp);
+    ld4(ws + (size_t)sn * ws_step + s_off, st + S::s_off);
+    if constexpr (TYPE == kQ6_K) ld4(wd + (size_t)sn * 16 + d_off, st + S::d_off);
+    const uint8_t* xs = xb + (size_t)sn * kUnits * 40;
+#pragma unroll
+    for (int k = 0; k < NTT; ++k) ld16(xs + x_off[k], st + S::x + 1024 * (NTT * wu + k));
+    ld4(xs + dx_off, st + S::dx + 256 * dxp);
+    if constexpr (TYPE == kQ4_K) ld4(xs + dx_off + 4, st + S::xs + 256 * dxp);
+  };
+
+  // MFMA lane roles: row r = lane % 16 (group gi = r / 8, row rr = r % 8), weight quarter c = lane / 16, result
+  // elements i: tokens 4 c + i (+ 16 m). Chain role: row cr = tid % 16, token ct = tid / 16 (+ 16 m).
+  const int r = lane & 15, c = lane >> 4, gi = r >> 3, rr = r & 7;
+  const int cr = tid & 15, ct = tid >> 4;
+  float acc[NTT];
+#pragma unroll
+  for (int m = 0; m < NTT; ++m) acc[m] = 0.0f;
+  const v4i zero4 = {0, 0, 0, 0};
+  auto put = [&](int u, int tok, const float (&e)[E]) __attribute__((always_inline)) {
+    float* p = terms + (((u * 16 * NTT) + tok) * 16 + r) * E;
+    if constexpr (E == 2)
+      *reinterpret_cast<float2*>(p) = make_float2(e[0], e[1]);
+    else
+      *reinterpret_cast<float4*>(p) = make_float4(e[0], e[1], e[2], e[3]);
+  };
+
+  auto stage = [&]<int BUF>(int s) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    wait_vm_stages<S::loads, NS - 2>(min(NS - 2, nst - 1 - s));
+    ring_barrier();  // stage s landed everywhere; every chain of stage s - 1 is done with the term buffer
+    if (s + NS - 1 < nst) issue.template operator()<(BUF + NS - 1) % NS>(s + NS - 1);
+    const uint8_t* st = smem + BUF * S::bytes;
+    if constexpr (TYPE == kQ8_0) {
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int u = 2 * wu + k;
+        const long b = *reinterpret_cast<const long*>(st + gi * 2048 + u * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
+        const float dw = half_to_float(*reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + u * 16 + rr * 2));
+#pragma unroll
+        for (int m = 0; m < NTT; ++m) {
+          const long a = *reinterpret_cast<const long*>(st + S::x + ((u * NTT + m) * 16 + r) * 32 + 8 * c);
+          const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + ((u * NTT + m) * 16 + 4 * c) * 4);
+          const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+          const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero4, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) put(u, 16 * m + 4 * c + i, {(float)d[i], dw * dx[i]});
+        }
+      }
+    } else if constexpr (TYPE == kQ6_K) {
+      const float dd = half_to_float(*reinterpret_cast<const uint16_t*>(st + S::d_off + gi * 16 + rr * 2));
+      const int hw = c >> 1, h = c & 1;
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int u = 2 * wu + k;
+        const uint8_t* au = st + gi * 1536 + u * 192;
+        const uint2 nib = *reinterpret_cast<const uint2*>(au + rr * 16 + 8 * h);
+        const uint2 hb = *reinterpret_cast<const uint2*>(au + 128 + rr * 8);
+        const uint32_t hv = (hw ? hb.y : hb.x) >> (4 * h);
+        const uint32_t q0 = ((nib.x >> (4 * hw)) & 0x0F0F0F0Fu) | ((hv & 0x03030303u) << 4);
+        const uint32_t q1 = ((nib.y >> (4 * hw)) & 0x0F0F0F0Fu) | (((hv >> 2) & 0x03030303u) << 4);
+        const long bq = (long)(((uint64_t)minus32(q1) << 32) | minus32(q0));
+        const long b0 = hw ? 0 : bq, b1 = hw ? bq : 0;
+        const uint32_t scw = *reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + rr * 16 + 2 * u);
+        const float dsc0 = dd * (float)(int8_t)(scw & 0xFF), dsc1 = dd * (float)(int8_t)(scw >> 8);
+#pragma unroll
+        for (int m = 0; m < NTT; ++m) {
+          const long a = *reinterpret_cast<const long*>(st + S::x + ((u * NTT + m) * 16 + r) * 32 + 8 * c);
+          const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + ((u * NTT + m) * 16 + 4 * c) * 4);
+          const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+          const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b0, zero4, 0, 0, 0);
+          const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, zero4, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if constexpr (WIDE)
+              put(u, 16 * m + 4 * c + i, {fma_((float)d1[i], dsc1, (float)d0[i] * dsc0), dx[i]});
+            else
+              put(u, 16 * m + 4 * c + i, {(float)d0[i], dsc0 * dx[i], (float)d1[i], dsc1 * dx[i]});
+          }
+        }
+      }
+    } else {  // Q4_K: wave w takes chunk j2 = w: units 2 w (low nibbles) and 2 w + 1 (high nibbles)
+      const uint4 hd = *reinterpret_cast<const uint4*>(st + S::s_off + gi * 128 + rr * 16);
+      const float d = half_to_float((uint16_t)(hd.x & 0xFFFF)), dmin = half_to_float((uint16_t)(hd.x >> 16));
+      const uint2 raw =
+          *reinterpret_cast<const uint2*>(st + gi * 1024 + wu * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int u = 2 * wu + e;
+        const long bq = (long)(((uint64_t)((raw.y >> (4 * e)) & 0x0F0F0F0Fu) << 32) | ((raw.x >> (4 * e)) & 0x0F0F0F0Fu));
+        int sc, mn;
+        scale_min(u, hd.y, hd.z, hd.w, sc, mn);
+        const float fsc = d * (float)sc, nmn = -(dmin * (float)mn);
+#pragma unroll
+        for (int m = 0; m < NTT; ++m) {
+          const long a = *reinterpret_cast<const long*>(st + S::x + ((u * NTT + m) * 16 + r) * 32 + 8 * c);
+          const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + ((u * NTT + m) * 16 + 4 * c) * 4);
+          const uint4 sx4 = *reinterpret_cast<const uint4*>(st + S::xs + ((u * NTT + m) * 16 + 4 * c) * 4);
+          const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+          const uint32_t sx[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
+          const v4i dq = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq, zero4, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float xsum = dx[i] * (float)((int)(int16_t)(sx[i] & 0xFFFF) + (int)(int16_t)(sx[i] >> 16));
+            put(u, 16 * m + 4 * c + i, {(float)dq[i], fsc * dx[i], nmn, xsum});
+          }
+        }
+      }
+    }
+    // Terms written (LDS only): then every lane runs its chains over the stage's units in order.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+#pragma unroll
+    for (int m = 0; m < NTT; ++m) {
+#pragma unroll
+      for (int u = 0; u < kUnits; ++u) {
+        const float* p = terms + (((u * 16 * NTT) + ct + 16 * m) * 16 + cr) * E;
+        if constexpr (E == 2) {
+          const float2 e = *reinterpret_cast<const float2*>(p);
+          acc[m] = fma_(e.x, e.y, acc[m]);
+        } else {
+          const float4 e = *reinterpret_cast<const float4*>(p);
+          acc[m] = fma_(e.x, e.y, acc[m]);
+          acc[m] = fma_(e.z, e.w, acc[m]);
+        }
+      }
+    }
+  };
+
+  [&]<int... B>(std::integer_sequence<int, B...>) __attribute__((always_inline)) {
+    ((B < nst ? issue.template operator()<B>(B) : void()), ...);
+  }(std::make_integer_sequence<int, NS - 1>{});
+  for (int s = 0; s < nst; s += NS) {
+    [&]<int... B>(std::integer_sequence<int, B...>) __attribute__((always_inline)) {
+      ((s + B < nst ? stage.template operator()<B>(s + B) : void()), ...);
+    }(std::make_integer_sequence<int, NS>{});
+  }
+
+  const int64_t row = (int64_t)rt * 16 + cr;
+#pragma unroll
+  for (int m = 0; m < NTT; ++m) {
+    const int t = ct + 16 * m;
+    if (t < ntok) {
+      float* o = y + (int64_t)(t0 + t) * ys + row;
+      *o = accumulate ? *o + acc[m] : acc[m];
+    }
+  }
+}
+
+template <int TYPE, bool WIDE, int NTT, int NS>
+void launch_ks_ns(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
+                  int64_t ys, bool accumulate) {
+  using S = KsLds<TYPE, WIDE, NTT>;
+  const size_t lds = NS * (size_t)S::bytes + S::terms;
+  static bool attr = false;
+  if (!attr) {
+    check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_mmv_ks<TYPE, WIDE, NTT, NS>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+          "hipFuncSetAttribute");
+    attr = true;
+  }
+  const int tiles = (n + 16 * NTT - 1) / (16 * NTT);
+  hipLaunchKernelGGL((k_mmv_ks<TYPE, WIDE, NTT, NS>), dim3((unsigned)(rows / 16), (unsigned)tiles), dim3(256), lds, s,
+                     static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0);
+}
+
+// Ring depth: the deepest ring that fits one workgroup per CU when the grid fits the GPU once, else one that lets
+// two workgroups share a CU (80 KB each).
+template <int TYPE, bool WIDE, int NTT>
+void launch_ks_ntt(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
+                   int64_t ys, bool accumulate) {
+  using S = KsLds<TYPE, WIDE, NTT>;
+  const int64_t wgs = rows / 16 * ((n + 16 * NTT - 1) / (16 * NTT)), cus = device_cus();
+  constexpr int kDeep = (150 * 1024 - S::terms) / S::bytes >= 8 ? 8 : (150 * 1024 - S::terms) / S::bytes;
+  constexpr int kTwo = (80 * 1024 - S::terms) / S::bytes;
+  if constexpr (kTwo >= 3) {
+    if (wgs > cus) {
+      launch_ks_ns<TYPE, WIDE, NTT, (kTwo > 6 ? 6 : kTwo)>(s, w, rows, cols, x, n, y, ys, accumulate);
+      return;
+    }
+  }
+  launch_ks_ns<TYPE, WIDE, NTT, kDeep>(s, w, rows, cols, x, n, y, ys, accumulate);
+}
+
+template <int TYPE, bool WIDE>
+void launch_ks(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
+               int64_t ys, bool accumulate) {
+  if (n <= 16)
+    launch_ks_ntt<TYPE, WIDE, 1>(s, w, rows, cols, x, n, y, ys, accumulate);
+  else
+    launch_ks_ntt<TYPE, WIDE, 2>(s, w, rows, cols, x, n, y, ys, accumulate);
+}
+
 template <int TYPE, bool WIDE, int NTT, int NS>
 void launch_ns(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
                int64_t ys, bool accumulate) {
@@ -372,8 +659,26 @@ bool mmv_supported(int type, int64_t rows, int64_t cols, int n) {
 }
 
 void mmv(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n,
-         float* y, int64_t ys, bool accumulate) {
+         float* y, int64_t ys, bool accumulate, bool ksplit) {
   require(mmv_supported(type, rows, cols, n), "mmv: Q8_0/Q4_K/Q6_K, 1..32 tokens, rows % 32 == 0, cols % 256 == 0");
+  if (ksplit) {
+    switch (type) {
+      case kQ8_0:
+        launch_ks<kQ8_0, false>(s, w, rows, cols, x, n, y, ys, accumulate);
+        break;
+      case kQ4_K:
+        launch_ks<kQ4_K, false>(s, w, rows, cols, x, n, y, ys, accumulate);
+        break;
+      default:
+        if (wide && n > 16)
+          launch_ks<kQ6_K, true>(s, w, rows, cols, x, n, y, ys, accumulate);
+        else
+          launch_ks<kQ6_K, false>(s, w, rows, cols, x, n, y, ys, accumulate);
+        break;
+    }
+    check_launch("mmv");
+    return;
+  }
   switch (type) {
     case kQ8_0:
       launch_mmv<kQ8_0, false>(s, w, rows, cols, x, n, y, ys, accumulate);

@@ -79,10 +79,11 @@ void gemm_kq(hipStream_t s, int type, bool wide, const void* w, int64_t rows, in
              float* y, int64_t ys, bool accumulate);
 
 // Short batches (1..32 tokens) of any quantized type on int8 MFMA, 16-row x 16-token tiles streamed through a deep LDS
-// ring (same results as matmul's other kernels); rows % 32 == 0, cols % 256 == 0.
+// ring (same results as matmul's other kernels); rows % 32 == 0, cols % 256 == 0. ksplit: four waves per 16-row tile
+// (matrices with few rows), else one.
 bool mmv_supported(int type, int64_t rows, int64_t cols, int n);
 void mmv(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n,
-         float* y, int64_t ys, bool accumulate);
+         float* y, int64_t ys, bool accumulate, bool ksplit);
 
 // Generic attention addressing: key row (t, g, row) at k + seq*k_seq + g*k_head + row*k_row (bytes), its scale at
 // ks + seq*s_seq + g*s_head + row*s_row (bytes); values likewise with v / vs.

@@ -172,20 +172,20 @@ LARGE = [(t, n, 256, 4096) for t in (mk_.Q8_0, mk_.Q4_K, mk_.Q6_K) for n in (1, 
     (mk_.Q8_0, 40, 96, 512),      # a full and a half-height row tile: the plain tile order
     (mk_.Q8_0, 24, 64, 416),      # 13 blocks: a partial last K stage
     (mk_.Q8_0, 70, 32, 96),       # one half-height row tile, a single short K stage, two token tiles
-    (mk_.Q8_0, 9, 1024, 256),     # the smallest GEMM batch: 8 row tiles (XCD-mapped), 55 idle token columns
+    (mk_.Q8_0, 9, 1024, 256),     # short-batch kernel, K split: 64 row tiles, 7 idle token columns
     (mk_.Q8_0, 100, 160, 1024),   # a full and a quarter-height 128-row tile; second token tile 36 tokens
     (mk_.Q8_0, 65, 1120, 320),    # 9 row tiles (plain order), 10 blocks: a 2-block last K stage
-    # K-quant int8-MFMA GEMM (n > 32, or 6144+ rows): partial row tiles, several token tiles, XCD-mapped grids, 1..4
-    # ring cycles; below that the GEMV takes the batch (the 9- and 17-token cases on few rows)
+    # K-quant int8-MFMA GEMM (n > 32): partial row tiles, several token tiles, XCD-mapped grids, 1..4 ring cycles;
+    # the 5..32-token cases go to the short-batch kernels (K split over four waves up to 8192 rows)
     (mk_.Q4_K, 9, 128, 512),
     (mk_.Q4_K, 100, 160, 1024),
     (mk_.Q4_K, 64, 1024, 1536),
-    (mk_.Q4_K, 9, 6144, 256),     # the smallest GEMM batch
+    (mk_.Q4_K, 9, 6144, 256),     # 384 K-split row tiles
     (mk_.Q6_K, 9, 128, 512),
-    (mk_.Q6_K, 9, 6144, 256),     # n <= 16: compact arithmetic in the GEMM
-    (mk_.Q6_K, 16, 6176, 512),    # 49 row tiles (plain order), the last a quarter tile
-    (mk_.Q6_K, 17, 6144, 512),    # the tree-verify batch size: wide arithmetic in the GEMM
-    (mk_.Q6_K, 17, 1024, 1024),   # ... and in the GEMV
+    (mk_.Q6_K, 9, 6144, 256),     # n <= 16: compact arithmetic
+    (mk_.Q6_K, 16, 6176, 512),    # 386 row tiles: two workgroups per CU
+    (mk_.Q6_K, 17, 6144, 512),    # the tree-verify batch size: wide arithmetic, two token tiles
+    (mk_.Q6_K, 17, 1024, 1024),   # ... on fewer rows
     (mk_.Q6_K, 100, 160, 2560),
 ]
 
@@ -243,6 +243,39 @@ def test_matmul_compact_batches(mk, oracle, t, n, rows, k):
     exp = oracle.matmul(t, w, rows, k, xq.reshape(-1), wide=False)
     y = _matmul(mk, t, packed, rows, k, xq.view(np.uint8), n, False).download(np.float32).reshape(n, rows)
     assert np.array_equal(bits(y), bits(exp))
+
+
+# Short batches (5..32 tokens) on the MFMA short-batch kernels: one wave per 16-row tile on matrices of more than
+# 8192 rows (and on Q4_K above 16 tokens), four waves splitting each stage's K units otherwise; one or two 16-token
+# tiles, token tails inside a tile, the wide and compact Q6_K arithmetic.
+SHORT = [
+    (mk_.Q8_0, 5, 8224, 256), (mk_.Q8_0, 23, 8224, 512),         # one wave per tile, one and two token tiles
+    (mk_.Q4_K, 12, 8224, 512), (mk_.Q4_K, 20, 8224, 512), (mk_.Q4_K, 20, 256, 1024),
+    (mk_.Q6_K, 12, 8224, 512), (mk_.Q6_K, 20, 8224, 512),
+    (mk_.Q8_0, 6, 96, 2048), (mk_.Q8_0, 30, 160, 1024),           # K split over four waves
+    (mk_.Q4_K, 7, 64, 1536), (mk_.Q4_K, 16, 192, 512),
+    (mk_.Q6_K, 13, 96, 1024), (mk_.Q6_K, 25, 64, 512), (mk_.Q6_K, 32, 4096, 256),
+]
+
+
+@pytest.mark.parametrize("t,n,rows,k", SHORT)
+def test_matmul_short_batches(mk, oracle, t, n, rows, k):
+    """The short-batch kernels bit for bit against the oracle, both Q6_K arithmetics, and the accumulate epilogue."""
+    import make_golden
+    print("short batch", dict(t=t, n=n, rows=rows, k=k), flush=True)
+    rng = np.random.default_rng(7 * t + n + rows + k)
+    w = make_golden.random_rows(rng, t, rows, k)
+    x = rng.uniform(-2, 2, (n, k)).astype(np.float32)
+    xq = oracle.quantize_row_q8(x)
+    packed = _packed(mk, t, w, rows, k)
+    for wide in ((True, False) if t == mk_.Q6_K else (True,)):
+        exp = oracle.matmul(t, w, rows, k, xq.reshape(-1), wide=wide)
+        y = _matmul(mk, t, packed, rows, k, xq.view(np.uint8), n, wide).download(np.float32).reshape(n, rows)
+        assert np.array_equal(bits(y), bits(exp)), wide
+        base = rng.standard_normal((n, rows)).astype(np.float32)
+        yd = mk.to_device(base)
+        _matmul(mk, t, packed, rows, k, xq.view(np.uint8), n, wide, y=yd, accumulate=True)
+        assert np.array_equal(bits(yd.download(np.float32).reshape(n, rows)), bits(base + exp)), wide
 
 
 F32_CASES = [(t, n, rows, k) for t in (mk_.Q8_0, mk_.Q4_K, mk_.Q6_K) for n in (1, 2) for rows, k in ((64, 256), (96, 4096))] + [
