@@ -78,17 +78,19 @@ __device__ __forceinline__ float reduce16_lanes(float v) {
 // read, which empties a prefetch ring. Kernels using them order them explicitly: a stage is read only after its own
 // copies are waited for (s_waitcnt vmcnt) and a barrier, and a buffer is refilled only after the barrier that follows
 // its last reads. M0 is named as clobbered (the copies set it); the compiler warns about clobbering a register it
-// reserves, which is the intent here.
+// reserves, which is the intent here. On GFX9 an LDS DMA instruction reads M0 one wait state after an SALU write of
+// it at the earliest (the hazard the compiler's own LDS DMA code respects): the s_nop between them is that state,
+// without which a copy can land at the previous copy's LDS address.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ uint32_t lds_addr(const void* l) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)l;
 }
 __device__ __forceinline__ void lds_copy16(const void* g, void* l) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_addr(l)) : "m0");
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_addr(l)) : "m0");
 }
 __device__ __forceinline__ void lds_copy4(const void* g, void* l) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_addr(l)) : "m0");
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_addr(l)) : "m0");
 }
 #pragma clang diagnostic pop
 
