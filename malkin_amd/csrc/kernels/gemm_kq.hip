@@ -17,7 +17,7 @@
 // never borrows across bytes for q < 64.
 //
 // A workgroup (4 waves) owns a 128-row x 32-token tile, 32 rows per wave, and walks K in stages of half a super-block
-// (4 units of 32 weights) held in a ring of 3 LDS buffers filled by direct global -> LDS loads two stages ahead.
+// (4 units of 32 weights) held in a ring of NS LDS buffers filled by direct global -> LDS loads NS - 1 stages ahead.
 #include <utility>
 
 #include "ctx.h"
