@@ -744,41 +744,58 @@ __global__ __launch_bounds__(kDecThreads) void k_attention_dec(const float* __re
     const uint8_t* vrow = vt + tid * vstride;
     const int swz = (tid >> 4) & 7;
     const float* pc = pv + (tid & 15);
-    v4i va, vb2;
-    float pa, pb;
     auto ld = [&](v4i& v, float& p, int jj) {
       const int j = min(jj, nk_pad - 16);
       v = *reinterpret_cast<const v4i*>(vrow + 16 * ((j >> 4) ^ swz));
       p = pc[j];
     };
-    auto chain = [&](const v4i& v, float p) {
-      const uint32_t w[4] = {(uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]};
-      acc = fma_bcast16<0>(p, i8_to_f32<0>(w[0]), acc);
-      acc = fma_bcast16<1>(p, i8_to_f32<1>(w[0]), acc);
-      acc = fma_bcast16<2>(p, i8_to_f32<2>(w[0]), acc);
-      acc = fma_bcast16<3>(p, i8_to_f32<3>(w[0]), acc);
-      acc = fma_bcast16<4>(p, i8_to_f32<0>(w[1]), acc);
-      acc = fma_bcast16<5>(p, i8_to_f32<1>(w[1]), acc);
-      acc = fma_bcast16<6>(p, i8_to_f32<2>(w[1]), acc);
-      acc = fma_bcast16<7>(p, i8_to_f32<3>(w[1]), acc);
-      acc = fma_bcast16<8>(p, i8_to_f32<0>(w[2]), acc);
-      acc = fma_bcast16<9>(p, i8_to_f32<1>(w[2]), acc);
-      acc = fma_bcast16<10>(p, i8_to_f32<2>(w[2]), acc);
-      acc = fma_bcast16<11>(p, i8_to_f32<3>(w[2]), acc);
-      acc = fma_bcast16<12>(p, i8_to_f32<0>(w[3]), acc);
-      acc = fma_bcast16<13>(p, i8_to_f32<1>(w[3]), acc);
-      acc = fma_bcast16<14>(p, i8_to_f32<2>(w[3]), acc);
-      acc = fma_bcast16<15>(p, i8_to_f32<3>(w[3]), acc);
+    // One 16-key group: the chain over the group's converted values fc (coefficients p), with the converts of the
+    // next group's raw bytes w into fn issued in the fmas' latency, one per step.
+    auto group = [&](const float (&fc)[16], float p, const v4i& w, float (&fn)[16]) {
+      const uint32_t w0 = (uint32_t)w[0], w1 = (uint32_t)w[1], w2 = (uint32_t)w[2], w3 = (uint32_t)w[3];
+      acc = fma_bcast16_cvt<0, 0>(p, fc[0], acc, w0, fn[0]);
+      acc = fma_bcast16_cvt<1, 1>(p, fc[1], acc, w0, fn[1]);
+      acc = fma_bcast16_cvt<2, 2>(p, fc[2], acc, w0, fn[2]);
+      acc = fma_bcast16_cvt<3, 3>(p, fc[3], acc, w0, fn[3]);
+      acc = fma_bcast16_cvt<4, 0>(p, fc[4], acc, w1, fn[4]);
+      acc = fma_bcast16_cvt<5, 1>(p, fc[5], acc, w1, fn[5]);
+      acc = fma_bcast16_cvt<6, 2>(p, fc[6], acc, w1, fn[6]);
+      acc = fma_bcast16_cvt<7, 3>(p, fc[7], acc, w1, fn[7]);
+      acc = fma_bcast16_cvt<8, 0>(p, fc[8], acc, w2, fn[8]);
+      acc = fma_bcast16_cvt<9, 1>(p, fc[9], acc, w2, fn[9]);
+      acc = fma_bcast16_cvt<10, 2>(p, fc[10], acc, w2, fn[10]);
+      acc = fma_bcast16_cvt<11, 3>(p, fc[11], acc, w2, fn[11]);
+      acc = fma_bcast16_cvt<12, 0>(p, fc[12], acc, w3, fn[12]);
+      acc = fma_bcast16_cvt<13, 1>(p, fc[13], acc, w3, fn[13]);
+      acc = fma_bcast16_cvt<14, 2>(p, fc[14], acc, w3, fn[14]);
+      acc = fma_bcast16_cvt<15, 3>(p, fc[15], acc, w3, fn[15]);
     };
-    ld(va, pa, 0);
+    // Group g's values are converted during group g - 1's chain; its raw bytes are read during group g - 2's.
+    v4i ra, rb;
+    float pa, pb, qa, qb;
+    float fa[16], fb[16];
+    ld(ra, pa, 0);
+    ld(rb, pb, 16);
+    {
+      const uint32_t w[4] = {(uint32_t)ra[0], (uint32_t)ra[1], (uint32_t)ra[2], (uint32_t)ra[3]};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        fa[4 * k] = i8_to_f32<0>(w[k]);
+        fa[4 * k + 1] = i8_to_f32<1>(w[k]);
+        fa[4 * k + 2] = i8_to_f32<2>(w[k]);
+        fa[4 * k + 3] = i8_to_f32<3>(w[k]);
+      }
+    }
     for (int jj = 0; jj < nk_pad; jj += 32) {
-      ld(vb2, pb, jj + 16);
+      ld(ra, qa, jj + 32);
       __builtin_amdgcn_sched_barrier(0);
-      chain(va, pa);
+      group(fa, pa, rb, fb);
       if (jj + 16 >= nk_pad) break;
-      ld(va, pa, jj + 32);
+      ld(rb, qb, jj + 48);
       __builtin_amdgcn_sched_barrier(0);
-      chain(vb2, pb);
+      group(fb, pb, ra, fa);
+      pa = qa;
+      pb = qb;
     }
   } else if (tid >= kDecThreads - 16) {
     const int l = tid - (kDecThreads - 16);

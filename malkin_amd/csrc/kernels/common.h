@@ -137,6 +137,24 @@ __device__ __forceinline__ float fma_bcast16(float x, float v, float acc) {
   return acc;
 }
 
+// fma_bcast16<K>, then the SDWA convert of byte B of w into cvt (as i8_to_f32<B>), as one pair of instructions: a
+// chain that converts the next group of values while it runs the current one puts each convert, which does not
+// depend on the chain, in the dependent fma's latency instead of in front of the fma that consumes it.
+template <int K, int B>
+__device__ __forceinline__ float fma_bcast16_cvt(float x, float v, float acc, uint32_t w, float& cvt) {
+  if constexpr (K == 0)
+    asm("s_nop 1\n\tv_fmac_f32_dpp %0, %2, %3 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+        "v_cvt_f32_i32_sdwa %1, sext(%4) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_%5"
+        : "+v"(acc), "=&v"(cvt)
+        : "v"(x), "v"(v), "v"(w), "i"(B));
+  else
+    asm("v_fmac_f32_dpp %0, %2, %3 row_newbcast:%6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_cvt_f32_i32_sdwa %1, sext(%4) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_%5"
+        : "+v"(acc), "=&v"(cvt)
+        : "v"(x), "v"(v), "v"(w), "i"(B), "i"(K));
+  return acc;
+}
+
 // (float)(int8_t)(w >> 8 K): one SDWA convert of byte K (the compiler otherwise emits shift, extract and convert
 // where the source word is live across a scheduling barrier).
 template <int K>
