@@ -94,6 +94,29 @@ __device__ __forceinline__ void lds_copy4(const void* g, void* l) {
 }
 #pragma clang diagnostic pop
 
+// Ring staging with the copies above. ring_barrier: a plain s_barrier (the copies are waited for explicitly; a fenced
+// barrier would make the compiler wait for every one in flight, prefetches included). wait_vm<N>: s_waitcnt vmcnt(N)
+// (N < 64: bits 3:0 and 15:14), expcnt and lgkmcnt left at their maximum. wait_vm_stages<PER, KMAX>(k): vmcnt(k PER)
+// for a runtime k in [0, KMAX], i.e. "at most k stages of PER copies each still in flight".
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+template <int PER, int KMAX>
+__device__ __forceinline__ void wait_vm_stages(int k) {
+  if constexpr (KMAX > 0) {
+    if (k >= KMAX) {
+      wait_vm<KMAX * PER>();
+      return;
+    }
+    wait_vm_stages<PER, KMAX - 1>(k);
+  } else {
+    wait_vm<0>();
+  }
+}
+
 // Workgroup barrier that orders LDS only. __syncthreads() also waits for every outstanding global load of the
 // calling wave, which would turn loads issued ahead of a barrier (prefetches) into a full memory round trip.
 __device__ __forceinline__ void lds_barrier() {

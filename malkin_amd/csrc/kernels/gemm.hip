@@ -17,7 +17,7 @@
 // That leaves one VALU fma per output and block.
 //
 // A workgroup (4 waves) owns a 128-row x 64-token tile, 32 rows x 64 tokens per wave, and walks the K dimension in
-// stages of kKB blocks held in a ring of kNS LDS buffers. A stage holds:
+// stages of kKB blocks held in a ring of NS LDS buffers (26 KB each). A stage holds:
 //   A  [kKB][128 rows][32 B]  the rows' quants (from the CDNA planes of layout.h),
 //   B  [kKB][64 tok][32 B]    the tokens' BlockQ8 quants,
 //   dx [kKB][64 tok]  f32     activation scales,
@@ -25,13 +25,17 @@
 // Rows of A and B are 32 bytes with their two 16-byte halves swapped on every other group of 8 rows, so the MFMA
 // operand reads (lane l: row l % 32, half l / 32) hit distinct banks. All copies are direct global -> LDS loads
 // (global_load_lds_dwordx4 / _dword: lane i of a wave instruction writes bytes [size * i, size * (i + 1)) after the
-// instruction's LDS base), issued two stages ahead, so the data of kNS - 1 stages is in flight while a stage is
-// computed and no register holds it on the way.
+// instruction's LDS base), issued NS - 1 stages ahead, so the data of NS - 1 stages is in flight while a stage is
+// computed and no register holds it on the way. NS by grid size: a grid that fits the CUs once (the few-row shapes
+// of a 256-token prompt chunk: one wave per SIMD, nothing else to hide the copies' latency) takes a 6-stage ring
+// (156 KB); larger grids keep 3 stages and two workgroups per CU.
 //
 // Accumulator layout of v_mfma_i32_32x32x32_i8 (checked on gfx950): lane l, element i holds
 //   row 8 * (i / 4) + 4 * (l / 32) + i % 4, column l % 32.
 // v_mfma_f32_32x32x1_2b_f32 holds block j in elements 16 j .. 16 j + 15 in the same layout, block j taking A and B
 // from lanes 32 j .. 32 j + 31 (checked on gfx950, together with the conversion and the product rounding).
+#include <utility>
+
 #include "ctx.h"
 #include "ops.h"
 
@@ -48,7 +52,6 @@ typedef __attribute__((address_space(1))) void glb_void;
 constexpr int kThreads = 256;
 constexpr int kRowsT = 128, kTokT = 64;  // workgroup tile
 constexpr int kKB = 4;                   // blocks per stage
-constexpr int kNS = 3;                   // stages in the LDS ring
 constexpr int kMagic = 0x4B400000;       // bits of 12582912.0f
 constexpr float kMagicF = 12582912.0f;
 
@@ -61,22 +64,19 @@ struct StageLds {
 };
 constexpr int kLoadsPerStage = kKB + 4;  // per wave: kKB A pieces, 2 B halves, 1 dx, 1 dw (wave w: block w of B/dx/dw)
 static_assert(kKB == 4, "one wave per block copies the B, dx and dw parts; a stage is two pairs of steps");
-static_assert(kNS == 3, "the main loop is unrolled over a ring of 3 buffers");
 
 // Byte offset of half h (0/1) of row r within a [rows][32 B] operand slab.
 __device__ __forceinline__ int slab_off(int r, int h) { return r * 32 + ((h ^ ((r >> 3) & 1)) << 4); }
 
 __device__ __forceinline__ void load_lds16(const void* g, uint8_t* l) { lds_copy16(g, l); }
-// Workgroup barrier for the LDS ring. The loads into LDS are tracked by vmcnt and waited for explicitly (the stage
-// being computed only); a fenced barrier would make the compiler wait for every one of them, prefetches included.
-// Reads of a buffer finish before the barrier that precedes its next fill, because each read feeds an MFMA of the
-// same iteration.
-__device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
+// The ring's copies are tracked by vmcnt and waited for explicitly (the stage about to be computed only). Reads of a
+// buffer finish before the barrier that precedes its next fill (lgkmcnt(0) before that barrier).
 
 __device__ __forceinline__ void load_lds4(const void* g, uint8_t* l) { lds_copy4(g, l); }
 
 // waves_per_eu(1): the register budget of one wave per SIMD, so the two pipeline register sets never spill (the
 // kernel needs about 230 VGPRs, so two waves per SIMD still fit when the grid has them).
+template <int NS>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm_q8_0(
     const uint8_t* W, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* __restrict__ y, int64_t ys,
     int accumulate, int n_rt, int n_tt, int vec) {
@@ -156,7 +156,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   // A wave issues one instruction every few cycles, in order, and one wave per SIMD is the common case here, so the
   // overlap of matrix and vector work has to be in the instruction stream itself, and the stream has to be short:
   // each MFMA is followed by about as many VALU instructions as cover its time in the matrix pipe, and the loop is
-  // unrolled over the whole LDS ring (kNS stages of kKB blocks) so every LDS offset is an immediate. Blocks past the
+  // unrolled over the whole LDS ring (NS stages of kKB blocks) so every LDS offset is an immediate. Blocks past the
   // end (nb % kKB != 0) read a copy of the last block with dw = dx = 0: their products are 0 and fma(f, 0, acc) ==
   // acc (the chain never holds -0), so they add nothing. The results of "block -1" start at zero for the same reason.
   auto read = [&]<int BUF, int BL>(v4i& ra, v4i& rb0, v4i& rb1, uint16_t& rdw, float& rdx)
@@ -205,11 +205,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   v32f xp, yp = {};
 
   // Stage s (blocks 4 s .. 4 s + 3) from buffer BUF; on entry X holds block 4 s's operands, Y block 4 s - 1's results.
-  // Between its third and fourth step the next stage is entered: it has landed (at most the one after it is
-  // outstanding), every wave is done reading the buffer that stage s + 3 will overwrite (this one: its reads were
-  // issued before and are waited for here), and stage s + 3 is issued into it.
+  // Between its third and fourth step the next stage is entered: it has landed (at most the NS - 2 after it are
+  // outstanding), every wave is done reading the buffer that stage s + NS will overwrite (this one: its reads were
+  // issued before and are waited for here), and stage s + NS is issued into it.
   auto stage = [&]<int BUF>(int s) __attribute__((always_inline)) {
-    constexpr int NBUF = (BUF + 1) % kNS;
+    constexpr int NBUF = (BUF + 1) % NS;
     const int j = s * kKB;
     step(xa, xb0, xb1, xdw, xdx, j < nb, xf0, xf1, xp, yf0, yf1, yp,
          [&]() __attribute__((always_inline)) { read.template operator()<BUF, 1>(ya, yb0, yb1, ydw, ydx); });
@@ -218,33 +218,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     step(xa, xb0, xb1, xdw, xdx, j + 2 < nb, xf0, xf1, xp, yf0, yf1, yp,
          [&]() __attribute__((always_inline)) { read.template operator()<BUF, 3>(ya, yb0, yb1, ydw, ydx); });
     if (s + 1 < nstages) {
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-      if (s + 2 < nstages)
-        __builtin_amdgcn_s_waitcnt(0x0F70 | kLoadsPerStage);  // vmcnt(kLoadsPerStage); expcnt, lgkmcnt at max
-      else
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      __builtin_amdgcn_s_waitcnt(0xC07F);                         // lgkmcnt(0)
+      wait_vm_stages<kLoadsPerStage, NS - 2>(nstages - 2 - s);  // stages s + 2 .. s + NS - 1 may be in flight
       ring_barrier();
-      if (s + 3 < nstages) issue.template operator()<BUF>(s + 3);
+      if (s + NS < nstages) issue.template operator()<BUF>(s + NS);
     }
     step(ya, yb0, yb1, ydw, ydx, j + 3 < nb, yf0, yf1, yp, xf0, xf1, xp,
          [&]() __attribute__((always_inline)) { read.template operator()<NBUF, 0>(xa, xb0, xb1, xdw, xdx); });
   };
 
-  issue.template operator()<0>(0);
-  if (nstages > 1) issue.template operator()<1>(1);
-  if (nstages > 1)
-    __builtin_amdgcn_s_waitcnt(0x0F70 | kLoadsPerStage);
-  else
-    __builtin_amdgcn_s_waitcnt(0x0F70);
+  // Stages 0 .. NS - 2 into buffers 0 .. NS - 2; once stage 0 has landed, stage NS - 1.
+  [&]<int... I>(std::integer_sequence<int, I...>) __attribute__((always_inline)) {
+    ((I < nstages ? issue.template operator()<I>(I) : void()), ...);
+  }(std::make_integer_sequence<int, NS - 1>{});
+  wait_vm_stages<kLoadsPerStage, NS - 2>(nstages - 1);
   ring_barrier();
-  if (nstages > 2) issue.template operator()<2>(2);
+  if (NS - 1 < nstages) issue.template operator()<NS - 1>(NS - 1);
   read.template operator()<0, 0>(xa, xb0, xb1, xdw, xdx);
-  // Whole ring cycles: up to two stages past the end run with every block's scales zeroed (exact no-ops), which
-  // keeps one loop exit and the register sets in place.
-  for (int s = 0; s < nstages; s += kNS) {
-    stage.template operator()<0>(s);
-    stage.template operator()<1>(s + 1);
-    stage.template operator()<2>(s + 2);
+  // Ring cycles, left after the last stage: every stage is four steps, so X and Y are in place at any stage boundary.
+  for (int s = 0; s < nstages; s += NS) {
+    [&]<int... I>(std::integer_sequence<int, I...>) __attribute__((always_inline)) {
+      (void)((s + I < nstages ? (stage.template operator()<I>(s + I), true) : false) && ...);
+    }(std::make_integer_sequence<int, NS>{});
   }
   fold(acc0, yf0, yp, 0, 0, 16);
   fold(acc1, yf1, yp, 1, 0, 16);
@@ -288,17 +283,23 @@ void gemm_q8_0(hipStream_t s, const void* w, int64_t rows, int64_t cols, const B
   require(gemm_q8_0_supported(rows, cols, n), "gemm_q8_0: rows must be a multiple of 32, n > 8");
   const int n_rt = (int)((rows + kRowsT - 1) / kRowsT);
   const int n_tt = (n + kTokT - 1) / kTokT;
-  const size_t lds = kNS * (size_t)StageLds::bytes;
   const int vec = (reinterpret_cast<uintptr_t>(y) % 16 == 0 && ys % 4 == 0) ? 1 : 0;
-  static bool attr = false;
-  if (!attr) {
-    check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_q8_0), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)lds),
-          "hipFuncSetAttribute");
-    attr = true;
-  }
-  hipLaunchKernelGGL(k_gemm_q8_0, dim3((unsigned)((int64_t)n_rt * n_tt)), dim3(kThreads), lds, s,
-                     static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0, n_rt, n_tt, vec);
+  auto go = [&]<int NS>() {
+    const size_t lds = NS * (size_t)StageLds::bytes;
+    static bool attr = false;
+    if (!attr) {
+      check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_q8_0<NS>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+            "hipFuncSetAttribute");
+      attr = true;
+    }
+    hipLaunchKernelGGL(k_gemm_q8_0<NS>, dim3((unsigned)((int64_t)n_rt * n_tt)), dim3(kThreads), lds, s,
+                       static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0, n_rt, n_tt, vec);
+  };
+  if ((int64_t)n_rt * n_tt <= device_cus())
+    go.template operator()<6>();
+  else
+    go.template operator()<3>();
   check_launch("gemm_q8_0");
 }
 

@@ -65,30 +65,6 @@ struct KqLds<kQ4_K> {
 
 __device__ __forceinline__ void load_lds16(const void* g, uint8_t* l) { lds_copy16(g, l); }
 __device__ __forceinline__ void load_lds4(const void* g, uint8_t* l) { lds_copy4(g, l); }
-// Barrier for the LDS ring: the loads into LDS are waited for explicitly (vmcnt), a fenced barrier would wait for the
-// prefetches too.
-__device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
-
-// s_waitcnt vmcnt(N) (N < 64: bits 3:0 and 15:14), expcnt and lgkmcnt left at their maximum.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
-}
-// vmcnt(k * PER) for a runtime k in [0, KMAX].
-template <int PER, int KMAX>
-__device__ __forceinline__ void wait_vm_stages(int k) {
-  if constexpr (KMAX > 0) {
-    if (k >= KMAX) {
-      wait_vm<KMAX * PER>();
-      return;
-    }
-    wait_vm_stages<PER, KMAX - 1>(k);
-  } else {
-    wait_vm<0>();
-  }
-}
-
 // float(int8 byte K of v)
 template <int K>
 __device__ __forceinline__ float sbyte_f(uint32_t v) {

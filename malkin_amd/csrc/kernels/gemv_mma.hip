@@ -40,25 +40,6 @@ constexpr int kUnits = 8;                 // 32-weight units per stage
 
 __device__ __forceinline__ void ld16(const void* g, uint8_t* l) { lds_copy16(g, l); }
 __device__ __forceinline__ void ld4(const void* g, uint8_t* l) { lds_copy4(g, l); }
-__device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
-
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
-}
-template <int PER, int KMAX>
-__device__ __forceinline__ void wait_vm_stages(int k) {
-  if constexpr (KMAX > 0) {
-    if (k >= KMAX) {
-      wait_vm<KMAX * PER>();
-      return;
-    }
-    wait_vm_stages<PER, KMAX - 1>(k);
-  } else {
-    wait_vm<0>();
-  }
-}
 
 // q - 32 per byte for bytes q < 64 (never borrows across bytes).
 __device__ __forceinline__ uint32_t minus32(uint32_t q) { return ((q | 0x80808080u) - 0x20202020u) ^ 0x80808080u; }
