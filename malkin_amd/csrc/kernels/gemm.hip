@@ -16,19 +16,23 @@
 //     +0 and an exact cancellation rounds to +0).
 // That leaves one VALU fma per output and block.
 //
-// A workgroup (4 waves) owns a 128-row x 64-token tile, 32 rows x 64 tokens per wave, and walks the K dimension in
-// stages of kKB blocks held in a ring of NS LDS buffers (26 KB each). A stage holds:
-//   A  [kKB][128 rows][32 B]  the rows' quants (from the CDNA planes of layout.h),
-//   B  [kKB][64 tok][32 B]    the tokens' BlockQ8 quants,
-//   dx [kKB][64 tok]  f32     activation scales,
-//   dw [kKB][128 rows] f16    weight scales.
+// A workgroup (4 waves) owns a 128-row x TOK-token tile, 32 rows x TOK tokens per wave, and walks the K dimension
+// in stages of KB blocks held in a ring of NS LDS buffers. TOK = 64: KB = 4 (26 KB per stage); a step is one block,
+// its two int8 MFMAs the two 32-token halves. TOK = 32: KB = 8 (43 KB per stage); a step is two blocks, its two int8
+// MFMAs one block each, and both fold into the one accumulator in block order; the scale-product MFMA's two halves
+// are then the two blocks. TOK = 32 doubles the waves of a grid: it runs where the grid fits the CUs once (the
+// attn_output and down shapes of a 256-token prompt chunk fill half the SIMDs at TOK = 64). A stage holds:
+//   A  [KB][128 rows][32 B]  the rows' quants (from the CDNA planes of layout.h),
+//   B  [KB][TOK tok][32 B]   the tokens' BlockQ8 quants,
+//   dx [KB][TOK tok]  f32    activation scales,
+//   dw [KB][128 rows] f16    weight scales.
 // Rows of A and B are 32 bytes with their two 16-byte halves swapped on every other group of 8 rows, so the MFMA
 // operand reads (lane l: row l % 32, half l / 32) hit distinct banks. All copies are direct global -> LDS loads
 // (global_load_lds_dwordx4 / _dword: lane i of a wave instruction writes bytes [size * i, size * (i + 1)) after the
 // instruction's LDS base), issued NS - 1 stages ahead, so the data of NS - 1 stages is in flight while a stage is
-// computed and no register holds it on the way. NS by grid size: a grid that fits the CUs once (the few-row shapes
-// of a 256-token prompt chunk: one wave per SIMD, nothing else to hide the copies' latency) takes a 6-stage ring
-// (156 KB); larger grids keep 3 stages and two workgroups per CU.
+// computed and no register holds it on the way. NS by grid size: a TOK = 64 grid that fits the CUs once takes a
+// 6-stage ring (156 KB: one wave per SIMD, nothing else hides the copies' latency); larger grids keep 3 stages and
+// two workgroups per CU; TOK = 32 takes 3 stages (132 KB).
 //
 // Accumulator layout of v_mfma_i32_32x32x32_i8 (checked on gfx950): lane l, element i holds
 //   row 8 * (i / 4) + 4 * (l / 32) + i % 4, column l % 32.
@@ -50,20 +54,23 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void glb_void;
 
 constexpr int kThreads = 256;
-constexpr int kRowsT = 128, kTokT = 64;  // workgroup tile
-constexpr int kKB = 4;                   // blocks per stage
+constexpr int kRowsT = 128;  // workgroup tile rows
 constexpr int kMagic = 0x4B400000;       // bits of 12582912.0f
 constexpr float kMagicF = 12582912.0f;
 
+template <int TOK>
 struct StageLds {
-  static constexpr int a = 0;                       // kKB * 128 * 32 bytes
-  static constexpr int b = a + kKB * kRowsT * 32;   // kKB * 64 * 32
-  static constexpr int dx = b + kKB * kTokT * 32;   // kKB * 64 floats
-  static constexpr int dw = dx + kKB * kTokT * 4;   // kKB * 128 halves
-  static constexpr int bytes = dw + kKB * kRowsT * 2;
+  static constexpr int KB = TOK == 64 ? 4 : 8;         // blocks per stage: four steps either way
+  static constexpr int a = 0;                          // KB * 128 * 32 bytes
+  static constexpr int b = a + KB * kRowsT * 32;       // KB * TOK * 32
+  static constexpr int dx = b + KB * TOK * 32;         // KB * TOK floats
+  static constexpr int dw = dx + KB * TOK * 4;         // KB * 128 halves
+  static constexpr int bytes = dw + KB * kRowsT * 2;
+  // copies per wave and stage: KB A pieces; TOK = 64: B halves 2, dx 1, dw 1 (block w); TOK = 32: B 2, dx 1 (both
+  // blocks), dw 2 (blocks 2 w, 2 w + 1)
+  static constexpr int loads = TOK == 64 ? KB + 4 : KB + 5;
 };
-constexpr int kLoadsPerStage = kKB + 4;  // per wave: kKB A pieces, 2 B halves, 1 dx, 1 dw (wave w: block w of B/dx/dw)
-static_assert(kKB == 4, "one wave per block copies the B, dx and dw parts; a stage is two pairs of steps");
+static_assert(StageLds<64>::KB == 4 && StageLds<32>::KB == 8, "one wave copies the B, dx and dw parts of KB / 4 blocks");
 
 // Byte offset of half h (0/1) of row r within a [rows][32 B] operand slab.
 __device__ __forceinline__ int slab_off(int r, int h) { return r * 32 + ((h ^ ((r >> 3) & 1)) << 4); }
@@ -76,10 +83,12 @@ __device__ __forceinline__ void load_lds4(const void* g, uint8_t* l) { lds_copy4
 
 // waves_per_eu(1): the register budget of one wave per SIMD, so the two pipeline register sets never spill (the
 // kernel needs about 230 VGPRs, so two waves per SIMD still fit when the grid has them).
-template <int NS>
+template <int TOK, int NS>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm_q8_0(
     const uint8_t* W, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* __restrict__ y, int64_t ys,
     int accumulate, int n_rt, int n_tt, int vec) {
+  using S = StageLds<TOK>;
+  constexpr int KB = S::KB;
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;  // wave w: rows 32 w .. 32 w + 31 of the tile
   // Workgroup -> (row tile, token tile). Consecutive workgroups go to consecutive XCDs; the token tiles of a row tile
@@ -100,15 +109,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const PackedQ8_0 L{rows, nb};
   const int64_t g0 = (int64_t)rt * (kRowsT / 8);                  // first 8-row group of the tile
   const int ngroups = (int)min<int64_t>(kRowsT / 8, rows / 8 - g0);  // 4 .. 16 (rows % 32 == 0)
-  const int t0 = tt * kTokT;
-  const int nstages = (nb + kKB - 1) / kKB;
+  const int t0 = tt * TOK;
+  const int nstages = (nb + KB - 1) / KB;
 
   // Copy mapping. Loads are never predicated: past the matrix they re-read valid data, unused.
   //   A: wave w copies its own 32 rows, one 1 KB instruction per block: lane -> row 32 w + lane / 2, physical half
   //      lane % 2 (logical half (lane % 2) ^ ((lane / 16) & 1)), 16 bytes of plane h of the row's group unit.
-  //   B: wave w copies block w: two instructions, tokens 32 c + lane / 2, the same half mapping, 16 qs bytes.
-  //   dx: wave w, block w: lane -> token lane, the BlockQ8 d.
-  //   dw: wave w, block w: lane -> the f16 scales of rows 2 lane, 2 lane + 1 (4 bytes of a group's 16-byte entry).
+  //   B: TOK = 64: wave w copies block w, tokens 32 c + lane / 2 for c = 0, 1; TOK = 32: blocks 2 w and 2 w + 1,
+  //      tokens lane / 2; the same half mapping, 16 qs bytes.
+  //   dx: TOK = 64: block w, lane -> token lane; TOK = 32: lane -> block 2 w + lane / 32, token lane % 32.
+  //   dw: block w (TOK = 32: blocks 2 w, 2 w + 1): lane -> the f16 scales of rows 2 lane, 2 lane + 1 (4 bytes of a
+  //       group's 16-byte entry).
   // Addresses are a wave-uniform base that moves with the block plus a fixed 32-bit per-lane offset.
   const int a_row = 32 * w + (lane >> 1);
   const int a_gi = min(a_row >> 3, ngroups - 1);
@@ -116,7 +127,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const uint32_t a_off = (uint32_t)(a_gi * nb * 256 + (half_sw << 7) + (a_row & 7) * 16);
   const uint32_t b_off0 = (uint32_t)((min(t0 + (lane >> 1), n - 1) - t0) * nb * 40 + 8 + 16 * half_sw);
   const uint32_t b_off1 = (uint32_t)((min(t0 + 32 + (lane >> 1), n - 1) - t0) * nb * 40 + 8 + 16 * half_sw);
-  const uint32_t dx_off = (uint32_t)((min(t0 + lane, n - 1) - t0) * nb * 40);
+  const uint32_t dx_off = (uint32_t)((min(t0 + (TOK == 64 ? lane : lane & 31), n - 1) - t0) * nb * 40);
   const uint32_t dw_off = (uint32_t)(min(lane >> 2, ngroups - 1) * nb * 16 + 4 * (lane & 3));
   const uint8_t* a_base = W + L.quants(g0, 0);
   const uint8_t* x_base = reinterpret_cast<const uint8_t*>(x + (int64_t)t0 * nb);
@@ -124,19 +135,34 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const int wu = __builtin_amdgcn_readfirstlane(w);
   // Stage sn into LDS buffer BUF.
   auto issue = [&]<int BUF>(int sn) __attribute__((always_inline)) {
-    uint8_t* st = smem + BUF * StageLds::bytes;
-    const int b0 = sn * kKB;
+    uint8_t* st = smem + BUF * S::bytes;
+    const int b0 = sn * KB;
 #pragma unroll
-    for (int k = 0; k < kKB; ++k)
-      load_lds16(a_base + (size_t)min(b0 + k, nb - 1) * 256 + a_off, st + StageLds::a + k * kRowsT * 32 + wu * 1024);
-    const int b = min(b0 + wu, nb - 1);
-    load_lds16(x_base + (size_t)b * 40 + b_off0, st + StageLds::b + wu * kTokT * 32);
-    load_lds16(x_base + (size_t)b * 40 + b_off1, st + StageLds::b + wu * kTokT * 32 + 32 * 32);
-    load_lds4(x_base + (size_t)b * 40 + dx_off, st + StageLds::dx + wu * kTokT * 4);
-    load_lds4(dw_base + (size_t)b * 16 + dw_off, st + StageLds::dw + wu * kRowsT * 2);
+    for (int k = 0; k < KB; ++k)
+      load_lds16(a_base + (size_t)min(b0 + k, nb - 1) * 256 + a_off, st + S::a + k * kRowsT * 32 + wu * 1024);
+    if constexpr (TOK == 64) {
+      const int b = min(b0 + wu, nb - 1);
+      load_lds16(x_base + (size_t)b * 40 + b_off0, st + S::b + wu * TOK * 32);
+      load_lds16(x_base + (size_t)b * 40 + b_off1, st + S::b + wu * TOK * 32 + 32 * 32);
+      load_lds4(x_base + (size_t)b * 40 + dx_off, st + S::dx + wu * TOK * 4);
+      load_lds4(dw_base + (size_t)b * 16 + dw_off, st + S::dw + wu * kRowsT * 2);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int b = min(b0 + 2 * wu + e, nb - 1);
+        load_lds16(x_base + (size_t)b * 40 + b_off0, st + S::b + (2 * wu + e) * TOK * 32);
+      }
+      const int bl = min(b0 + 2 * wu + (lane >> 5), nb - 1);  // per lane
+      load_lds4(x_base + (size_t)bl * 40 + dx_off, st + S::dx + 2 * wu * TOK * 4);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int b = min(b0 + 2 * wu + e, nb - 1);
+        load_lds4(dw_base + (size_t)b * 16 + dw_off, st + S::dw + (2 * wu + e) * kRowsT * 2);
+      }
+    }
   };
 
-  v16f acc0 = {}, acc1 = {};  // tokens 0..31, 32..63
+  v16f acc0 = {}, acc1 = {};  // TOK = 64: tokens 0..31, 32..63; TOK = 32: acc0 only
   v16i magic;
 #pragma unroll
   for (int i = 0; i < 16; ++i) magic[i] = kMagic;
@@ -144,10 +170,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const v32f zero = {};
   const int li = lane & 31, h = lane >> 5;
   const int arow = 32 * w + li;
-  // LDS byte offsets of this lane's operands within a stage buffer, block 0.
-  const int off_a = StageLds::a + slab_off(arow, h), off_b0 = StageLds::b + slab_off(li, h),
-            off_b1 = StageLds::b + slab_off(32 + li, h), off_dw = StageLds::dw + 2 * arow,
-            off_dx = StageLds::dx + 4 * lane;
+  // LDS byte offsets of this lane's operands within a stage buffer, block 0. The scale product's operands: TOK = 64,
+  // lane l: dw of row arow, dx of token l; TOK = 32, lane l: block h (of the step's two): dw of row arow, dx of token
+  // li.
+  const int off_a = S::a + slab_off(arow, h), off_b0 = S::b + slab_off(li, h), off_b1 = S::b + slab_off(32 + li, h),
+            off_dw = S::dw + 2 * arow + (TOK == 64 ? 0 : h * kRowsT * 2),
+            off_dx = S::dx + (TOK == 64 ? 4 * lane : 4 * li + h * TOK * 4);
 
   // Software pipeline over blocks j = 0, 1, ..., two register sets (X = even j, Y = odd j). Step j:
   //   read the operands of block j + 1 (the first block of a stage: entered between the steps),
@@ -156,17 +184,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   // A wave issues one instruction every few cycles, in order, and one wave per SIMD is the common case here, so the
   // overlap of matrix and vector work has to be in the instruction stream itself, and the stream has to be short:
   // each MFMA is followed by about as many VALU instructions as cover its time in the matrix pipe, and the loop is
-  // unrolled over the whole LDS ring (NS stages of kKB blocks) so every LDS offset is an immediate. Blocks past the
-  // end (nb % kKB != 0) read a copy of the last block with dw = dx = 0: their products are 0 and fma(f, 0, acc) ==
+  // unrolled over the whole LDS ring (NS stages of KB blocks) so every LDS offset is an immediate. Blocks past the
+  // end (nb % KB != 0) read a copy of the last block with dw = dx = 0: their products are 0 and fma(f, 0, acc) ==
   // acc (the chain never holds -0), so they add nothing. The results of "block -1" start at zero for the same reason.
-  auto read = [&]<int BUF, int BL>(v4i& ra, v4i& rb0, v4i& rb1, uint16_t& rdw, float& rdx)
+  // Operands of step BL of a stage: TOK = 64, block BL (ra1 unused); TOK = 32, blocks 2 BL (ra0, rb0) and 2 BL + 1
+  // (ra1, rb1).
+  auto read = [&]<int BUF, int BL>(v4i& ra0, v4i& ra1, v4i& rb0, v4i& rb1, uint16_t& rdw, float& rdx)
       __attribute__((always_inline)) {
-    const uint8_t* st = smem + BUF * StageLds::bytes;
-    ra = *reinterpret_cast<const v4i*>(st + off_a + BL * kRowsT * 32);
-    rb0 = *reinterpret_cast<const v4i*>(st + off_b0 + BL * kTokT * 32);
-    rb1 = *reinterpret_cast<const v4i*>(st + off_b1 + BL * kTokT * 32);
-    rdw = *reinterpret_cast<const uint16_t*>(st + off_dw + BL * kRowsT * 2);
-    rdx = *reinterpret_cast<const float*>(st + off_dx + BL * kTokT * 4);
+    const uint8_t* st = smem + BUF * S::bytes;
+    if constexpr (TOK == 64) {
+      ra0 = *reinterpret_cast<const v4i*>(st + off_a + BL * kRowsT * 32);
+      rb0 = *reinterpret_cast<const v4i*>(st + off_b0 + BL * TOK * 32);
+      rb1 = *reinterpret_cast<const v4i*>(st + off_b1 + BL * TOK * 32);
+      rdw = *reinterpret_cast<const uint16_t*>(st + off_dw + BL * kRowsT * 2);
+      rdx = *reinterpret_cast<const float*>(st + off_dx + BL * TOK * 4);
+    } else {
+      ra0 = *reinterpret_cast<const v4i*>(st + off_a + 2 * BL * kRowsT * 32);
+      ra1 = *reinterpret_cast<const v4i*>(st + off_a + (2 * BL + 1) * kRowsT * 32);
+      rb0 = *reinterpret_cast<const v4i*>(st + off_b0 + 2 * BL * TOK * 32);
+      rb1 = *reinterpret_cast<const v4i*>(st + off_b0 + (2 * BL + 1) * TOK * 32);
+      rdw = *reinterpret_cast<const uint16_t*>(st + off_dw + 2 * BL * kRowsT * 2);
+      rdx = *reinterpret_cast<const float*>(st + off_dx + 2 * BL * TOK * 4);
+    }
   };
   // fmas i0 .. i1 - 1 of one 16-output half. The empty asm keeps them in their region: without it the compiler moves
   // them into a later one, past the MFMAs they are meant to overlap.
@@ -175,30 +214,32 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     for (int i = i0; i < i1; ++i) acc[i] = fma_(f[i], pp[16 * t + i], acc[i]);
     asm volatile("" : "+v"(acc));
   };
-  // One step: the MFMAs of a block (operands o*, results r*) and the fmas of the previous block (pf*, pp), in five
-  // regions of one MFMA each; the VALU work of a region covers its MFMA's time in the matrix pipe (64 or 32 cycles).
-  // `next` reads the following block's operands at the start. live: the block is inside the matrix (else its
-  // scales are zeroed).
-  auto step = [&](const v4i& oa, const v4i& ob0, const v4i& ob1, uint16_t odw, float odx, bool live, v16f& rf0,
-                  v16f& rf1, v32f& rp, const v16f& pf0, const v16f& pf1, const v32f& pp, auto&& next)
+  // One step: the MFMAs of a block (TOK = 32: two blocks; operands o*, results r*) and the fmas of the previous step
+  // (pf*, pp), in five regions of one MFMA each; the VALU work of a region covers its MFMA's time in the matrix pipe
+  // (64 or 32 cycles). `next` reads the following step's operands at the start. bl: the step's first block; a
+  // lane's scales are zeroed past the matrix (TOK = 32: the lane's block is bl + h).
+  v16f& acc_b = TOK == 64 ? acc1 : acc0;  // the second MFMA's accumulator
+  auto step = [&](const v4i& oa0, const v4i& oa1, const v4i& ob0, const v4i& ob1, uint16_t odw, float odx, int bl,
+                  v16f& rf0, v16f& rf1, v32f& rp, const v16f& pf0, const v16f& pf1, const v32f& pp, auto&& next)
       __attribute__((always_inline)) {
+    const bool live = (TOK == 64 ? bl : bl + h) < nb;
     const float dw = live ? half_to_float(odw) : 0.0f, dx = live ? odx : 0.0f;
     next();
     rp = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, dx, zero, 0, 0, 0);
     fold(acc0, pf0, pp, 0, 0, 16);
     __builtin_amdgcn_sched_barrier(0);
-    rf0 = __builtin_bit_cast(v16f, __builtin_amdgcn_mfma_i32_32x32x32_i8(oa, ob0, magic, 0, 0, 0));
-    fold(acc1, pf1, pp, 1, 0, 8);
+    rf0 = __builtin_bit_cast(v16f, __builtin_amdgcn_mfma_i32_32x32x32_i8(oa0, ob0, magic, 0, 0, 0));
+    fold(acc_b, pf1, pp, 1, 0, 8);
     __builtin_amdgcn_sched_barrier(0);
-    rf1 = __builtin_bit_cast(v16f, __builtin_amdgcn_mfma_i32_32x32x32_i8(oa, ob1, magic, 0, 0, 0));
-    fold(acc1, pf1, pp, 1, 8, 16);
+    rf1 = __builtin_bit_cast(v16f, __builtin_amdgcn_mfma_i32_32x32x32_i8(TOK == 64 ? oa0 : oa1, ob1, magic, 0, 0, 0));
+    fold(acc_b, pf1, pp, 1, 8, 16);
     __builtin_amdgcn_sched_barrier(0);
     rf0 = __builtin_amdgcn_mfma_f32_16x16x1f32(-kMagicF, 1.0f, rf0, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     rf1 = __builtin_amdgcn_mfma_f32_16x16x1f32(-kMagicF, 1.0f, rf1, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
-  v4i xa, xb0, xb1, ya, yb0, yb1;
+  v4i xa, xa1, xb0, xb1, ya, ya1, yb0, yb1;
   uint16_t xdw, ydw;  // f16 weight scales as read
   float xdx, ydx;
   v16f xf0, xf1, yf0 = {}, yf1 = {};
@@ -210,31 +251,36 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   // issued before and are waited for here), and stage s + NS is issued into it.
   auto stage = [&]<int BUF>(int s) __attribute__((always_inline)) {
     constexpr int NBUF = (BUF + 1) % NS;
-    const int j = s * kKB;
-    step(xa, xb0, xb1, xdw, xdx, j < nb, xf0, xf1, xp, yf0, yf1, yp,
-         [&]() __attribute__((always_inline)) { read.template operator()<BUF, 1>(ya, yb0, yb1, ydw, ydx); });
-    step(ya, yb0, yb1, ydw, ydx, j + 1 < nb, yf0, yf1, yp, xf0, xf1, xp,
-         [&]() __attribute__((always_inline)) { read.template operator()<BUF, 2>(xa, xb0, xb1, xdw, xdx); });
-    step(xa, xb0, xb1, xdw, xdx, j + 2 < nb, xf0, xf1, xp, yf0, yf1, yp,
-         [&]() __attribute__((always_inline)) { read.template operator()<BUF, 3>(ya, yb0, yb1, ydw, ydx); });
+    constexpr int BPS = KB / 4;  // blocks per step
+    const int j = s * KB;
+    step(xa, xa1, xb0, xb1, xdw, xdx, j, xf0, xf1, xp, yf0, yf1, yp, [&]() __attribute__((always_inline)) {
+      read.template operator()<BUF, 1>(ya, ya1, yb0, yb1, ydw, ydx);
+    });
+    step(ya, ya1, yb0, yb1, ydw, ydx, j + BPS, yf0, yf1, yp, xf0, xf1, xp, [&]() __attribute__((always_inline)) {
+      read.template operator()<BUF, 2>(xa, xa1, xb0, xb1, xdw, xdx);
+    });
+    step(xa, xa1, xb0, xb1, xdw, xdx, j + 2 * BPS, xf0, xf1, xp, yf0, yf1, yp, [&]() __attribute__((always_inline)) {
+      read.template operator()<BUF, 3>(ya, ya1, yb0, yb1, ydw, ydx);
+    });
     if (s + 1 < nstages) {
       __builtin_amdgcn_s_waitcnt(0xC07F);                         // lgkmcnt(0)
-      wait_vm_stages<kLoadsPerStage, NS - 2>(nstages - 2 - s);  // stages s + 2 .. s + NS - 1 may be in flight
+      wait_vm_stages<S::loads, NS - 2>(nstages - 2 - s);  // stages s + 2 .. s + NS - 1 may be in flight
       ring_barrier();
       if (s + NS < nstages) issue.template operator()<BUF>(s + NS);
     }
-    step(ya, yb0, yb1, ydw, ydx, j + 3 < nb, yf0, yf1, yp, xf0, xf1, xp,
-         [&]() __attribute__((always_inline)) { read.template operator()<NBUF, 0>(xa, xb0, xb1, xdw, xdx); });
+    step(ya, ya1, yb0, yb1, ydw, ydx, j + 3 * BPS, yf0, yf1, yp, xf0, xf1, xp, [&]() __attribute__((always_inline)) {
+      read.template operator()<NBUF, 0>(xa, xa1, xb0, xb1, xdw, xdx);
+    });
   };
 
   // Stages 0 .. NS - 2 into buffers 0 .. NS - 2; once stage 0 has landed, stage NS - 1.
   [&]<int... I>(std::integer_sequence<int, I...>) __attribute__((always_inline)) {
     ((I < nstages ? issue.template operator()<I>(I) : void()), ...);
   }(std::make_integer_sequence<int, NS - 1>{});
-  wait_vm_stages<kLoadsPerStage, NS - 2>(nstages - 1);
+  wait_vm_stages<S::loads, NS - 2>(nstages - 1);
   ring_barrier();
   if (NS - 1 < nstages) issue.template operator()<NS - 1>(NS - 1);
-  read.template operator()<0, 0>(xa, xb0, xb1, xdw, xdx);
+  read.template operator()<0, 0>(xa, xa1, xb0, xb1, xdw, xdx);
   // Ring cycles, left after the last stage: every stage is four steps, so X and Y are in place at any stage boundary.
   for (int s = 0; s < nstages; s += NS) {
     [&]<int... I>(std::integer_sequence<int, I...>) __attribute__((always_inline)) {
@@ -242,14 +288,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     }(std::make_integer_sequence<int, NS>{});
   }
   fold(acc0, yf0, yp, 0, 0, 16);
-  fold(acc1, yf1, yp, 1, 0, 16);
+  fold(acc_b, yf1, yp, 1, 0, 16);
   // The last stage's loads were waited for (vmcnt(0)) when it was entered; nothing is in flight past the loop.
 
   // Element i of tile j: row 32 w + 8 (i / 4) + 4 h + i % 4, token 32 j + li.
   if (32 * w < 8 * ngroups) {
     float* yr = y + (int64_t)rt * kRowsT + 32 * w + 4 * h;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < TOK / 32; ++j) {
       const int t = t0 + 32 * j + li;
       if (t >= n) continue;
       float* yt = yr + (int64_t)t * ys;
@@ -282,24 +328,27 @@ void gemm_q8_0(hipStream_t s, const void* w, int64_t rows, int64_t cols, const B
                bool accumulate) {
   require(gemm_q8_0_supported(rows, cols, n), "gemm_q8_0: rows must be a multiple of 32, n > 8");
   const int n_rt = (int)((rows + kRowsT - 1) / kRowsT);
-  const int n_tt = (n + kTokT - 1) / kTokT;
   const int vec = (reinterpret_cast<uintptr_t>(y) % 16 == 0 && ys % 4 == 0) ? 1 : 0;
-  auto go = [&]<int NS>() {
-    const size_t lds = NS * (size_t)StageLds::bytes;
+  auto go = [&]<int TOK, int NS>() {
+    const int n_tt = (n + TOK - 1) / TOK;
+    const size_t lds = NS * (size_t)StageLds<TOK>::bytes;
     static bool attr = false;
     if (!attr) {
-      check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_q8_0<NS>),
+      check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_q8_0<TOK, NS>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
             "hipFuncSetAttribute");
       attr = true;
     }
-    hipLaunchKernelGGL(k_gemm_q8_0<NS>, dim3((unsigned)((int64_t)n_rt * n_tt)), dim3(kThreads), lds, s,
+    hipLaunchKernelGGL((k_gemm_q8_0<TOK, NS>), dim3((unsigned)((int64_t)n_rt * n_tt)), dim3(kThreads), lds, s,
                        static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0, n_rt, n_tt, vec);
   };
-  if ((int64_t)n_rt * n_tt <= device_cus())
-    go.template operator()<6>();
+  const int64_t cus = device_cus();
+  if ((int64_t)n_rt * ((n + 31) / 32) <= cus)
+    go.template operator()<32, 3>();
+  else if ((int64_t)n_rt * ((n + 63) / 64) <= cus)
+    go.template operator()<64, 6>();
   else
-    go.template operator()<3>();
+    go.template operator()<64, 3>();
   check_launch("gemm_q8_0");
 }
 

@@ -167,7 +167,8 @@ LARGE = [(t, n, 256, 4096) for t in (mk_.Q8_0, mk_.Q4_K, mk_.Q6_K) for n in (1, 
     (mk_.Q8_0, 8, 256, 12288),    # down-projection depth: several LDS chunks per row
     (mk_.Q6_K, 8, 256, 17408),
     (mk_.Q4_K, 2, 512, 17408),
-    (mk_.Q8_0, 256, 512, 4096),   # int8-MFMA prefill GEMM: 2 token groups, XCD-mapped row tiles
+    (mk_.Q8_0, 256, 512, 4096),   # int8-MFMA prefill GEMM, 32-token tiles (the grid fits the CUs once), 16 stages
+    (mk_.Q8_0, 256, 4608, 256),   # 64-token tiles, 144 workgroups: the 6-stage ring
     (mk_.Q8_0, 131, 256, 2560),   # token tail inside a wave tile
     (mk_.Q8_0, 40, 96, 512),      # a full and a half-height row tile: the plain tile order
     (mk_.Q8_0, 24, 64, 416),      # 13 blocks: a partial last K stage
