@@ -610,8 +610,17 @@ void launch(hipStream_t s, const void* w, int64_t rows, int64_t cols, const Gemv
     attr = true;
   }
   // Persistent over row groups: as many workgroups as are resident at once (per token group), each streaming its
-  // share of the row groups.
-  const int per_cu = resident_per_cu(k_gemv<TYPE, WIDE, R, NT, PRO, EPI>, lds);
+  // share of the row groups, capped per CU. Every workgroup repeats the prologue (the fp32 rows' loads, the norm's
+  // chain) and takes a dispatch slot, so fewer, longer-lived workgroups win where the occupancy allows many. Caps
+  // measured on MI355X over the Qwen3-8B Q8_0 decode shapes (q|k|v norm 11.8 -> 10.4 us at 2, gate|up norm + silu
+  // 24.3 -> 23.6 us at 4, plain BlockQ8 input 12.2 -> 11.9 us mean at 3) and the Qwen3-14B K-quant shapes (plain
+  // input: 4 is as fast or faster, 3 and 2 slower).
+  constexpr int kCap = TYPE != kQ8_0 ? (PRO == kProQ8 ? 4 : 64)
+                       : PRO == kProQ8 ? 3
+                       : PRO == kProF32 ? 2
+                       : EPI == kEpiSilu ? 4
+                                         : 2;
+  const int per_cu = std::min(kCap, resident_per_cu(k_gemv<TYPE, WIDE, R, NT, PRO, EPI>, lds));
   const int64_t groups = rows / R, tgroups = (n + NT - 1) / NT;
   const int64_t resident = (int64_t)per_cu * device_cus();
   const int64_t gx = std::max<int64_t>(1, std::min<int64_t>(groups, resident / tgroups));
