@@ -614,8 +614,8 @@ void launch(hipStream_t s, const void* w, int64_t rows, int64_t cols, const Gemv
   // chain) and takes a dispatch slot, so fewer, longer-lived workgroups win where the occupancy allows many. Caps
   // measured on MI355X over the Qwen3-8B Q8_0 decode shapes (q|k|v norm 11.8 -> 10.4 us at 2, gate|up norm + silu
   // 24.3 -> 23.6 us at 4, plain BlockQ8 input 12.2 -> 11.9 us mean at 3) and the Qwen3-14B K-quant shapes (plain
-  // input: 4 is as fast or faster, 3 and 2 slower).
-  constexpr int kCap = TYPE != kQ8_0 ? (PRO == kProQ8 ? 4 : 64)
+  // input: 4 is as fast or faster at one token, 3 and 2 slower; 2 at four tokens, 47.0 -> 45.1 us on 17408 x 5120).
+  constexpr int kCap = TYPE != kQ8_0 ? (PRO == kProQ8 ? (NT >= 4 ? 2 : 4) : 64)
                        : PRO == kProQ8 ? 3
                        : PRO == kProF32 ? 2
                        : EPI == kEpiSilu ? 4
