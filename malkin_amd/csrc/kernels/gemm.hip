@@ -120,7 +120,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   //   dx: TOK = 64: block w, lane -> token lane; TOK = 32: lane -> block 2 w + lane / 32, token lane % 32.
   //   dw: block w (TOK = 32: blocks 2 w, 2 w + 1): lane -> the f16 scales of rows 2 lane, 2 lane + 1 (4 bytes of a
   //       group's 16-byte entry).
-  // Addresses are a wave-uniform base that moves with the block plus a fixed 32-bit per-lane offset.
+  // Addresses are a wave-uniform base that moves with the block plus a fixed 32-bit per-lane offset (the TOK = 32 dx
+  // copy: its block, too, is per lane).
   const int a_row = 32 * w + (lane >> 1);
   const int a_gi = min(a_row >> 3, ngroups - 1);
   const int half_sw = (lane & 1) ^ ((lane >> 4) & 1);
