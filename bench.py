@@ -57,41 +57,55 @@ def model_file(preset, seed, wtype=None, mix=None):
 
 
 def gemv_roofline(ctx, model, cfg, reps=3):
-    """Live roofline of the dominant kernel: the Q8_0 decode GEMV (n = 1) over one decode step's 144 layer matmuls
-    (q|k|v, attn_output, gate|up, down of 36 layers: 7.0 GB, far beyond the 256 MB Infinity Cache), timed with HIP
-    events on the library stream. Algorithmic bytes per launch = GGUF bytes of the weight (34 B per 32 weights) + the
-    BlockQ8 input (40 B per 32) + the f32 output."""
+    """Live roofline of the dominant kernel: the decode GEMV family (n = 1) exactly as the timed decode launches it
+    (Model::run): per layer q|k|v with rmsnorm + quantization in its prologue, attn_output from the fp32 attention
+    rows with the residual add in its epilogue, gate|up with rmsnorm + quantization in the prologue and silu(gate)*up
+    in the epilogue, down from the fp32 SwiGLU rows with the residual add; 144 launches over the 36 layers (7.0 GB,
+    far beyond the 256 MB Infinity Cache), timed with HIP events on the library stream. Algorithmic bytes per launch
+    = GGUF bytes of the weight (34 B per 32 weights) + the fp32 input row (+ norm weights) + the fp32 output (read
+    and written where the epilogue accumulates)."""
     import ctypes
     import malkin_amd as mk
     L = mk.load()
-    E, F = cfg["n_embd"], cfg["n_ff"]
-    xin = ctx.alloc(max(E, F) // 32 * 40)
+    E, F, H, D = cfg["n_embd"], cfg["n_ff"], cfg["n_head"], cfg["head_dim"]
+    eps = ctypes.c_float(cfg["rms_eps"])
     rng = np.random.default_rng(0)
-    xb = np.zeros(max(E, F) // 32, dtype=mk.BLOCK_Q8)
-    xb["d"] = rng.uniform(0.01, 0.05, xb.size)
-    xb["qs"] = rng.integers(-127, 128, (xb.size, 32))
-    xb["s"][:, 0] = xb["qs"][:, :16].sum(1)
-    xb["s"][:, 1] = xb["qs"][:, 16:].sum(1)
-    xin.upload(xb)
-    yout = ctx.alloc(2 * F * 4)
-    ws = [model.weight(l, w) for l in range(cfg["n_layer"]) for w in range(4)]
-    algo = sum(w.rows * w.cols // 32 * 34 + w.cols // 32 * 40 + w.rows * 4 for w in ws)
-    for w in ws:  # warm
-        mk.check(L.mk_matmul(ctx.h, ctypes.byref(w), xin.ptr, 1, yout.ptr, w.rows, 0))
+    x = ctx.to_device(rng.standard_normal(E).astype(np.float32))
+    att = ctx.to_device(rng.standard_normal(H * D).astype(np.float32))
+    norm = ctx.to_device(np.ones(E, np.float32))
+    qkv = ctx.alloc((H + 2 * cfg["n_head_kv"]) * D * 4)
+    gu = ctx.to_device(rng.standard_normal(F).astype(np.float32))
+    res = ctx.to_device(np.zeros(E, np.float32))
+    calls, algo = [], 0
+    for layer in range(cfg["n_layer"]):
+        wq, wo, wg, wd = (model.weight(layer, i) for i in range(4))
+        calls += [(wq, x, E, norm, qkv, wq.rows, 0, 0), (wo, att, H * D, None, res, E, 1, 0),
+                  (wg, x, E, norm, gu, F, 0, 1), (wd, gu, F, None, res, E, 1, 0)]
+        for w, _, k, nw, _, rows_out, acc, silu in calls[-4:]:
+            algo += w.rows * w.cols // 32 * 34 + k * 4 + (k * 4 if nw is not None else 0) + rows_out * 4 * (1 + acc)
+
+    def run():
+        for w, xin, xs, nw, y, ys, acc, silu in calls:
+            mk.check(L.mk_matmul_f32(ctx.h, ctypes.byref(w), xin.ptr, xs, nw.ptr if nw is not None else None, eps, 1,
+                                     y.ptr, ys, acc, silu))
+
+    run()  # warm
     ctx.sync()
     best = None
     for _ in range(reps):
         ctx.timer_start()
-        for w in ws:
-            mk.check(L.mk_matmul(ctx.h, ctypes.byref(w), xin.ptr, 1, yout.ptr, w.rows, 0))
+        run()
         ms = ctx.timer_stop()
         best = ms if best is None else min(best, ms)
-    launches = len(ws)
+    for b in (x, att, norm, qkv, gu, res):
+        b.free()
+    launches = len(calls)
     per_launch_s = best / 1e3 / launches
     achieved = algo / launches / per_launch_s / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": roofline_traffic(),
-            "kernel": "k_gemv<Q8_0, n=1> (decode GEMV, 144 launches per token)",
+            "kernel": "k_gemv<Q8_0, n=1> with the decode's fused prologues/epilogues (q|k|v norm, attn_output "
+                      "residual, gate|up norm + silu, down residual; 144 launches per token)",
             "bytes_per_launch": int(algo / launches), "us_per_launch": round(per_launch_s * 1e6, 2)}
 
 
@@ -101,14 +115,14 @@ INT8_PEAK_TOPS = 5000.0
 
 
 def random_weight(rng, t, rows, cols):
-    """Random GGUF rows of type t (timing input): random quant bytes, f16 scales drawn from [0.001, 0.02]."""
-    qk, bs, offs = _BLOCKS[t]
-    nb = cols // qk
-    data = rng.integers(0, 256, size=(rows, nb, bs), dtype=np.uint8)
-    for o in offs:
-        data[:, :, o:o + 2] = rng.uniform(0.001, 0.02, (rows, nb)).astype(np.float16).view(np.uint8).reshape(
-            rows, nb, 2)
-    return data.reshape(rows, nb * bs)
+    """GGUF rows of type t drawn as BASELINE.json states: entries N(0, 0.02), quantized by the synthetic model
+    writer's quantizer (the reference ships none), in slabs of 1024 rows."""
+    from malkin_amd import synth
+    out = []
+    for r in range(0, rows, 1024):
+        n = min(1024, rows - r)
+        out.append(synth.quantize_rows(t, rng.normal(0.0, 0.02, (n, cols)).astype(np.float32)))
+    return np.concatenate(out)
 
 
 def pack_copies(ctx, t, host_rows, rows, cols, copies):
@@ -192,25 +206,37 @@ def kernel_configs(ctx):
 
 def traffic_probe():
     """Launch sequence for the HBM-traffic counters of the roofline kernel (run under rocprofv3 --pmc FETCH_SIZE, then
-    WRITE_SIZE): the four Q8_0 decode GEMV shapes of the Qwen3-8B layer (q|k|v 6144x4096, attn_output 4096x4096,
-    gate|up 24576x4096, down 4096x12288) at n = 1, each launched 4 times over 2 packed copies, then one plain 256 MiB
+    WRITE_SIZE): the four decode GEMV variants of the Qwen3-8B layer as the decode launches them (q|k|v 6144x4096 with
+    the norm prologue, attn_output 4096x4096 accumulating, gate|up 24576x4096 with the norm prologue and SiLU epilogue,
+    down 4096x12288 accumulating) at n = 1, each launched 4 times over 2 packed copies, then one plain 256 MiB
     device-to-device copy (the counter scale: it reads and writes exactly 256 MiB)."""
     import ctypes
     import malkin_amd as mk
+    L = mk.load()
     ctx = mk.Context(0)
     rng = np.random.default_rng(3)
-    for rows, cols in ((6144, 4096), (4096, 4096), (24576, 4096), (4096, 12288)):
+    eps = ctypes.c_float(1e-6)
+    for rows, cols, norm, acc, silu in ((6144, 4096, 1, 0, 0), (4096, 4096, 0, 1, 0), (24576, 4096, 1, 0, 1),
+                                        (4096, 12288, 0, 1, 0)):
         ws = pack_copies(ctx, mk.Q8_0, random_weight(rng, mk.Q8_0, rows, cols), rows, cols, 2)
-        xq, y = random_acts(ctx, rng, 1, cols), ctx.alloc(rows * 4)
+        x = ctx.to_device(rng.standard_normal(cols).astype(np.float32))
+        nw = ctx.to_device(np.ones(cols, np.float32)) if norm else None
+        out_rows = rows // 2 if silu else rows
+        y = ctx.to_device(np.zeros(out_rows, np.float32))
         ctx.sync()
-        time_matmuls(ctx, ws, xq, 1, y, 2)
+        for i in range(4):
+            w = ws[i % 2][1]
+            mk.check(L.mk_matmul_f32(ctx.h, ctypes.byref(w), x.ptr, cols, nw.ptr if nw else None, eps, 1, y.ptr,
+                                     out_rows, acc, silu))
         ctx.sync()
-        log(f"[probe] k_gemv Q8_0 {rows}x{cols} n=1: 4 launches, algorithmic bytes "
-            f"{rows * cols // 32 * 34 + cols // 32 * 40 + rows * 4}")
+        algo = rows * cols // 32 * 34 + cols * 4 * (2 if norm else 1) + out_rows * 4 * (1 + acc)
+        log(f"[probe] k_gemv Q8_0 {rows}x{cols} n=1 (norm {norm}, accumulate {acc}, silu {silu}): 4 launches, "
+            f"algorithmic bytes {algo}")
         for b, _w in ws:
             b.free()
-        xq.free()
-        y.free()
+        for b in (x, nw, y):
+            if b is not None:
+                b.free()
     hip = ctypes.CDLL("libamdhip64.so")
     nbytes = 256 << 20
     a, b = ctx.alloc(nbytes), ctx.alloc(nbytes)
@@ -232,44 +258,85 @@ def roofline_traffic():
     return None
 
 
-def cpu_baseline(path, vocab, budget_s=30.0):
+def cpu_baseline(path, prompt, gpu_tokens, budget_s=30.0):
     """The reference's own AVX-512 path (oracle/_ref, compiled from its sources), timed on this host's cores with
-    OMP threads = physical cores (the reference's default, engine.cpp:104-109). Sample: the pp512 prompt in two
-    256-token forwards, then decode forwards until about budget_s of CPU work; tg from the measured decode rate."""
+    OMP threads = physical cores (the reference's default, engine.cpp:104-109). Sample: the 512-token prompt in two
+    256-token forwards, then greedy decode forwards until about budget_s of CPU work; tg from the measured decode rate.
+    Its greedy ids are compared with the device's stream on the same model and prompt (tokens_match)."""
     from oracle import bind
     if not bind.ref_available():
         return {"value": None, "unit": "tokens/s", "cores": 0, "kind": "reference",
-                "sample": "oracle/_ref not built on this tree"}
+                "sample": "oracle/_ref not built on this tree", "tokens_match": None}
     ref = bind.Ref()
     if not ref.cpu_ok():
         return {"value": None, "unit": "tokens/s", "cores": 0, "kind": "reference",
-                "sample": f"host CPU ({ref.cpu_model()}) lacks AVX-512 VNNI/BF16"}
+                "sample": f"host CPU ({ref.cpu_model()}) lacks AVX-512 VNNI/BF16", "tokens_match": None}
     cores = ref.physical_cores()
     ref.set_threads(cores)
+    n_prompt, n_gen = len(prompt), len(gpu_tokens)
     t0 = time.time()
-    m = ref.model(path, N_PROMPT + N_GEN, 1)
+    m = ref.model(path, n_prompt + n_gen, 1)
     load_s = time.time() - t0
-    p = prompt_ids(N_PROMPT, vocab)
     t0 = time.time()
-    m.forward(p[:256], 0)
-    logits = m.forward(p[256:], 256)
+    for i in range(0, n_prompt, 256):
+        logits = m.forward(prompt[i:i + 256], i)
     pp_s = time.time() - t0
-    tok = int(np.argmax(logits[0]))
+    ids = [int(np.argmax(logits[0]))]
     t0 = time.time()
     n_dec = 0
-    while n_dec < N_GEN - 1 and (time.time() - t0) < max(1.0, budget_s - pp_s):
-        logits = m.forward(np.array([tok], np.int32), N_PROMPT + n_dec)
-        tok = int(np.argmax(logits[0]))
+    while n_dec < n_gen - 1 and (time.time() - t0) < max(1.0, budget_s - pp_s):
+        logits = m.forward(np.array([ids[-1]], np.int32), n_prompt + n_dec)
+        ids.append(int(np.argmax(logits[0])))
         n_dec += 1
     dec_s = time.time() - t0
     m.close()
-    per_tok = dec_s / n_dec
-    step_s = pp_s + per_tok * (N_GEN - 1)
-    return {"value": round((N_PROMPT + N_GEN) / step_s, 3), "unit": "tokens/s", "cores": cores, "kind": "reference",
-            "sample": f"pp512 (2 x 256-token forwards) + {n_dec} of the 127 decode forwards, the rest extrapolated "
-                      f"at the measured rate; {ref.cpu_model()}, {cores} threads; panel packing {load_s:.1f} s "
-                      f"untimed",
-            "pp512_tok_s": round(N_PROMPT / pp_s, 2), "tg_tok_s": round(1.0 / per_tok, 3)}
+    per_tok = dec_s / max(n_dec, 1)
+    step_s = pp_s + per_tok * (n_gen - 1)
+    match = [int(a) for a in gpu_tokens[:len(ids)]] == ids
+    return {"value": round((n_prompt + n_gen) / step_s, 3), "unit": "tokens/s", "cores": cores, "kind": "reference",
+            "sample": f"pp{n_prompt} ({(n_prompt + 255) // 256} x 256-token forwards) + {n_dec} of the {n_gen - 1} "
+                      f"decode forwards, the rest extrapolated at the measured rate; {ref.cpu_model()}, {cores} "
+                      f"threads; panel packing {load_s:.1f} s untimed",
+            "pp_tok_s": round(n_prompt / pp_s, 2), "tg_tok_s": round(1.0 / per_tok, 3),
+            "tokens_compared": len(ids), "tokens_match": match}
+
+
+def config3(ctx, reps=3, with_cpu=True):
+    """random-init Qwen3-4B architecture in Q8_0 (36 layers, hidden 2560, 32/8 heads, head_dim 128,
+    FFN 9728 SwiGLU, vocab 151936, tied embeddings; synthetic seed 31), a prompt of 512 uniform-random ids (numpy
+    seed 303), 128 greedy tokens, ctx 4096: pp512 + tg128 on the device with the same protocol as the main line, its
+    HBM / int8-MFMA fractions, and the reference's AVX-512 path on the same model and prompt (greedy ids compared)."""
+    import malkin_amd as mk
+    path, _ = model_file("qwen3-4b", seed=31)
+    try:
+        m = mk.Model(ctx, path, N_CTX, 1)
+        cfg = m.cfg
+        prompt = np.random.default_rng(303).integers(0, cfg["n_vocab"], N_PROMPT).astype(np.int32)
+        m.generate(prompt, N_GEN)
+        ctx.sync()
+        pre, dec = [], []
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            toks, st = m.generate(prompt, N_GEN)
+            pre.append(st["prefill_ms"])
+            dec.append(st["decode_ms"])
+        ctx.sync()
+        ms_step = (time.perf_counter() - t0) * 1e3 / reps
+        m.close()
+        pp_ms, dec_ms = float(np.median(pre)), float(np.median(dec))
+        out = {"workload": "qwen3-4b-q8_0 pp512+tg128, 512 uniform-random prompt ids, batch 1, ctx 4096, greedy",
+               "tokens_per_s": round((N_PROMPT + N_GEN) * 1e3 / ms_step, 2), "ms_per_step": round(ms_step, 3),
+               "pp512_tok_s": round(N_PROMPT * 1e3 / pp_ms, 1), "tg128_tok_s": round((N_GEN - 1) * 1e3 / dec_ms, 2),
+               "decode_ms_per_token": round(dec_ms / (N_GEN - 1), 4),
+               "decode_hbm_frac": round(model_bytes_per_token(cfg) / (dec_ms / (N_GEN - 1) / 1e3) / 1e9 / HBM_PEAK_GBS,
+                                        4),
+               "pp512_mfma_frac": round(prefill_ops(cfg) / (pp_ms / 1e3) / 1e12 / INT8_PEAK_TOPS, 4)}
+        if with_cpu:
+            out["cpu_baseline"] = cpu_baseline(path, prompt, toks, budget_s=15.0)
+        return out
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
 
 
 def config4(ctx, path):
@@ -384,7 +451,8 @@ def main():
     ap.add_argument("--no-kernel-configs", action="store_true",
                     help="skip the kernel-level configurations (config 1 GEMM, config 2 GEMV)")
     ap.add_argument("--no-engine-configs", action="store_true",
-                    help="skip BASELINE configs 4 (continuous batching) and 5 (speculative tree verification)")
+                    help="skip BASELINE configs 3 (Qwen3-4B pp512 + tg128), 4 (continuous batching) and 5 "
+                         "(speculative tree verification)")
     ap.add_argument("--probe", choices=["traffic"],
                     help="only run the launch sequence for the roofline kernel's HBM counters")
     args = ap.parse_args()
@@ -429,11 +497,15 @@ def main():
             log("[bench] kernel configs: " + json.dumps(kern))
         engine = None
         if not args.no_engine_configs:
-            engine = {"config4": config4(ctx, path)}
+            engine = {"config3": config3(ctx, with_cpu=not args.no_cpu_baseline)}
+            log("[bench] config 3: " + json.dumps(engine["config3"]))
+            engine["config4"] = config4(ctx, path)
             log("[bench] config 4: " + json.dumps(engine["config4"]))
             engine["config5"] = config5(ctx)
             log("[bench] config 5: " + json.dumps(engine["config5"]))
-        cpu = None if args.no_cpu_baseline else cpu_baseline(path, cfg["n_vocab"])
+        cpu = None if args.no_cpu_baseline else cpu_baseline(path, prompt, toks)
+        if cpu:
+            log("[bench] cpu baseline: " + json.dumps(cpu))
         ctx.close()
     finally:
         if os.path.exists(path):
@@ -460,6 +532,7 @@ def main():
         "decode_ms_per_token": round(dec_ms / (N_GEN - 1), 4),
         "decode_hbm_frac": round(model_bytes_per_token(cfg) / (dec_ms / (N_GEN - 1) / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
         "pp512_mfma_frac": round(prefill_ops(cfg) / (pp_ms / 1e3) / 1e12 / INT8_PEAK_TOPS, 4),
+        "tokens_match": None if cpu is None else cpu.get("tokens_match"),
         "roofline": roof,
         "cpu_baseline": cpu,
         "kernel_configs": kern,

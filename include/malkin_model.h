@@ -20,6 +20,18 @@ extern "C" {
 
 typedef struct mk_model mk_model;
 
+/* What mk_gguf_inspect reports about a GGUF file. */
+typedef struct {
+  int64_t n_tensors;
+  int64_t tensor_bytes; /* sum of the tensors' data bytes */
+  int32_t n_layer;      /* <arch>.block_count, 0 when absent */
+  char arch[32];        /* general.architecture ("" when absent) */
+} mk_gguf_info;
+
+/* Opens and validates a GGUF v3 file without a device: header, metadata and tensor directory, every tensor inside
+   the file (the checks GgufFile's constructor makes, gguf.h:44-69). MK_ERR_INVALID with the reason otherwise. */
+int mk_gguf_inspect(const char* gguf_path, mk_gguf_info* out);
+
 /* BatchToken (model.h:25-30). logits != 0: produce n_vocab logits for this token. kv / parent = -1 for plain
    tokens; a tree token (parent = batch index of an earlier token of the same sequence) writes KV row kv. */
 typedef struct {

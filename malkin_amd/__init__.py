@@ -60,6 +60,7 @@ SIGNATURES = {
     "mk_move_kv": (_I, [_P, _P, _I, _I, _I]),
     "mk_argmax_top2": (_I, [_P, _P, _I, _I, _P, _P]),
     "mk_greedy_advance": (_I, [_P, _P, _P, _P, _P, _P, _P, _P]),
+    "mk_gguf_inspect": (_I, [ctypes.c_char_p, _P]),
     "mk_model_open": (_I, [_P, ctypes.c_char_p, _I, _I, _I, ctypes.POINTER(_P)]),
     "mk_model_free": (_I, [_P]),
     "mk_model_get_config": (_I, [_P, _P]),
@@ -209,6 +210,19 @@ class MkModelConfig(ctypes.Structure):
 
 class MkGenStats(ctypes.Structure):
     _fields_ = [("prefill_ms", ctypes.c_double), ("decode_ms", ctypes.c_double), ("decode_forwards", ctypes.c_int32)]
+
+
+class MkGgufInfo(ctypes.Structure):
+    _fields_ = [("n_tensors", ctypes.c_int64), ("tensor_bytes", ctypes.c_int64), ("n_layer", ctypes.c_int32),
+                ("arch", ctypes.c_char * 32)]
+
+
+def gguf_inspect(path):
+    """mk_gguf_inspect: validates a GGUF file on the host (no device needed); raises MkError with the reason."""
+    info = MkGgufInfo()
+    check(load().mk_gguf_inspect(path.encode(), ctypes.byref(info)))
+    return {"n_tensors": info.n_tensors, "tensor_bytes": info.tensor_bytes, "n_layer": info.n_layer,
+            "arch": info.arch.decode()}
 
 
 class Model:

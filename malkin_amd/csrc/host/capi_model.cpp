@@ -3,6 +3,7 @@
 #include <exception>
 #include <memory>
 #include <stdexcept>
+#include <string>
 #include <vector>
 
 #include "../../../include/malkin_engine.h"
@@ -45,6 +46,20 @@ std::vector<malkin_hip::BatchToken> to_batch(const mk_batch_token* b, int n) {
 }  // namespace
 
 extern "C" {
+
+int mk_gguf_inspect(const char* path, mk_gguf_info* out) {
+  return run([&] {
+    if (!path || !out) throw std::invalid_argument("mk_gguf_inspect: null argument");
+    const malkin_hip::GgufFile f(path);
+    mk_gguf_info info{};
+    info.n_tensors = static_cast<int64_t>(f.tensors().size());
+    for (const auto& kv : f.tensors()) info.tensor_bytes += static_cast<int64_t>(kv.second.nbytes);
+    const std::string arch = f.get_str("general.architecture").value_or("");
+    std::snprintf(info.arch, sizeof info.arch, "%s", arch.c_str());
+    info.n_layer = static_cast<int32_t>(f.get_int(arch + ".block_count").value_or(0));
+    *out = info;
+  });
+}
 
 int mk_model_open(mk_ctx* ctx, const char* path, int n_ctx, int n_seq, int flags, mk_model** out) {
   return run([&] {

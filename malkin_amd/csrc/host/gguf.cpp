@@ -7,239 +7,291 @@
 
 #include <cerrno>
 #include <cstring>
+#include <limits>
 #include <stdexcept>
 
 namespace malkin_hip {
 
 namespace {
 
-struct Traits {
-  int64_t block;
-  size_t bytes;
+// ggml's block geometry per type id (ggml.h type enum; the GGUF tensor type field).
+constexpr GgmlBlock kBlocks[] = {
+    {0, 1, 4, "F32"},       {1, 1, 2, "F16"},       {2, 32, 18, "Q4_0"},    {3, 32, 20, "Q4_1"},
+    {6, 32, 22, "Q5_0"},    {7, 32, 24, "Q5_1"},    {8, 32, 34, "Q8_0"},    {9, 32, 36, "Q8_1"},
+    {10, 256, 84, "Q2_K"},  {11, 256, 110, "Q3_K"}, {12, 256, 144, "Q4_K"}, {13, 256, 176, "Q5_K"},
+    {14, 256, 210, "Q6_K"}, {15, 256, 292, "Q8_K"}, {24, 1, 1, "I8"},       {25, 1, 2, "I16"},
+    {26, 1, 4, "I32"},      {27, 1, 8, "I64"},      {28, 1, 8, "F64"},      {30, 1, 2, "BF16"},
+    {39, 32, 17, "MXFP4"},
 };
 
-Traits traits(uint32_t t) {
+constexpr uint32_t kMagic = 0x46554747;  // "GGUF" read as a little-endian u32
+constexpr int kMaxDims = 4;              // GGML_MAX_DIMS
+constexpr int kMaxArrayNesting = 8;
+
+// GGUF metadata value types.
+enum : uint32_t { kU8, kI8, kU16, kI16, kU32, kI32, kF32, kBool, kStr, kArr, kU64, kI64, kF64, kNumTypes };
+
+// Byte width of a fixed-size value type; 0 for strings, arrays and unknown types.
+size_t fixed_width(uint32_t t) {
   switch (t) {
-    case 0: return {1, 4};      // F32
-    case 1: return {1, 2};      // F16
-    case 30: return {1, 2};     // BF16
-    case 2: return {32, 18};    // Q4_0
-    case 3: return {32, 20};    // Q4_1
-    case 6: return {32, 22};    // Q5_0
-    case 7: return {32, 24};    // Q5_1
-    case 8: return {32, 34};    // Q8_0
-    case 9: return {32, 36};    // Q8_1
-    case 10: return {256, 84};  // Q2_K
-    case 11: return {256, 110}; // Q3_K
-    case 12: return {256, 144}; // Q4_K
-    case 13: return {256, 176}; // Q5_K
-    case 14: return {256, 210}; // Q6_K
-    case 15: return {256, 292}; // Q8_K
-    case 39: return {32, 17};   // MXFP4
-    default: throw std::runtime_error("unknown ggml type " + std::to_string(t));
+    case kU8: case kI8: case kBool: return 1;
+    case kU16: case kI16: return 2;
+    case kU32: case kI32: case kF32: return 4;
+    case kU64: case kI64: case kF64: return 8;
+    default: return 0;
   }
 }
 
-class Cursor {
+// Bounds-checked forward reader over the mapped header. Every check compares a length with the bytes left, so no
+// offset arithmetic can wrap.
+class Reader {
  public:
-  Cursor(const uint8_t* p, size_t n) : p_(p), end_(p + n) {}
+  Reader(const uint8_t* base, size_t size, const std::string& path) : base_(base), size_(size), path_(path) {}
+
+  const uint8_t* take(size_t n, const char* what) {
+    if (n > size_ - at_) fail(std::string(what) + " runs past the end of the file");
+    const uint8_t* p = base_ + at_;
+    at_ += n;
+    return p;
+  }
   template <typename T>
-  T get() {
-    need(sizeof(T));
+  T get(const char* what) {
     T v;
-    std::memcpy(&v, p_, sizeof v);
-    p_ += sizeof v;
+    std::memcpy(&v, take(sizeof v, what), sizeof v);
     return v;
   }
-  std::string str() {
-    const auto n = get<uint64_t>();
-    need(n);
-    std::string s(reinterpret_cast<const char*>(p_), n);
-    p_ += n;
-    return s;
+  std::string text(const char* what) {
+    const uint64_t n = get<uint64_t>(what);
+    const uint8_t* p = take(n, what);
+    return std::string(reinterpret_cast<const char*>(p), n);
   }
-  void skip(size_t n) {
-    need(n);
-    p_ += n;
+  size_t offset() const { return at_; }
+  [[noreturn]] void fail(const std::string& why) const {
+    throw std::runtime_error("gguf " + path_ + ": " + why + " (at byte " + std::to_string(at_) + ")");
   }
-  const uint8_t* pos() const { return p_; }
 
  private:
-  void need(size_t n) const {
-    if (static_cast<size_t>(end_ - p_) < n) throw std::runtime_error("gguf: truncated header");
-  }
-  const uint8_t* p_;
-  const uint8_t* end_;
+  const uint8_t* base_;
+  size_t size_;
+  size_t at_ = 0;
+  const std::string& path_;
 };
 
-// GGUF value types: u8 i8 u16 i16 u32 i32 f32 bool str arr u64 i64 f64.
-size_t scalar_bytes(uint32_t t) {
-  static const size_t b[] = {1, 1, 2, 2, 4, 4, 4, 1, 0, 0, 8, 8, 8};
-  if (t >= 13 || t == 8 || t == 9) return 0;
-  return b[t];
-}
-
-int64_t read_int(Cursor& c, uint32_t t) {
+int64_t read_integer(Reader& r, uint32_t t) {
   switch (t) {
-    case 0: return c.get<uint8_t>();
-    case 1: return c.get<int8_t>();
-    case 2: return c.get<uint16_t>();
-    case 3: return c.get<int16_t>();
-    case 4: return c.get<uint32_t>();
-    case 5: return c.get<int32_t>();
-    case 10: return static_cast<int64_t>(c.get<uint64_t>());
-    case 11: return c.get<int64_t>();
-    default: throw std::runtime_error("gguf: not an int type");
+    case kU8: return r.get<uint8_t>("metadata value");
+    case kI8: return r.get<int8_t>("metadata value");
+    case kU16: return r.get<uint16_t>("metadata value");
+    case kI16: return r.get<int16_t>("metadata value");
+    case kU32: return r.get<uint32_t>("metadata value");
+    case kI32: return r.get<int32_t>("metadata value");
+    case kU64: {
+      const uint64_t v = r.get<uint64_t>("metadata value");
+      if (v > static_cast<uint64_t>(std::numeric_limits<int64_t>::max())) r.fail("u64 metadata value out of range");
+      return static_cast<int64_t>(v);
+    }
+    case kI64: return r.get<int64_t>("metadata value");
+    default: r.fail("metadata value type " + std::to_string(t) + " is not an integer");
   }
 }
 
-void skip_value(Cursor& c, uint32_t t) {
-  if (t == 8) {
-    c.skip(c.get<uint64_t>());
-  } else if (t == 9) {
-    const auto et = c.get<uint32_t>();
-    const auto n = c.get<uint64_t>();
-    for (uint64_t i = 0; i < n; ++i) skip_value(c, et);
-  } else {
-    const size_t b = scalar_bytes(t);
-    if (!b) throw std::runtime_error("gguf: bad value type " + std::to_string(t));
-    c.skip(b);
+// Steps over an array's elements (their contents are not kept).
+void skip_array(Reader& r, uint32_t elem, uint64_t count, int depth) {
+  if (depth > kMaxArrayNesting) r.fail("metadata arrays nested too deeply");
+  if (const size_t w = fixed_width(elem)) {
+    if (count > std::numeric_limits<size_t>::max() / w) r.fail("metadata array too large");
+    r.take(static_cast<size_t>(count) * w, "metadata array");
+    return;
+  }
+  for (uint64_t i = 0; i < count; ++i) {
+    if (elem == kStr) {
+      r.text("metadata array string");
+    } else if (elem == kArr) {
+      const uint32_t e = r.get<uint32_t>("metadata array type");
+      skip_array(r, e, r.get<uint64_t>("metadata array count"), depth + 1);
+    } else {
+      r.fail("metadata array of unknown type " + std::to_string(elem));
+    }
   }
 }
 
 }  // namespace
 
-size_t ggml_row_size(uint32_t type, int64_t n) {
-  const Traits t = traits(type);
-  if (n % t.block) throw std::runtime_error("row not a multiple of the block size");
-  return static_cast<size_t>(n / t.block) * t.bytes;
+const GgmlBlock* ggml_block(uint32_t type) {
+  for (const GgmlBlock& b : kBlocks)
+    if (b.type == type) return &b;
+  return nullptr;
 }
 
-const char* ggml_type_name(uint32_t t) {
-  switch (t) {
-    case 0: return "F32";
-    case 1: return "F16";
-    case 8: return "Q8_0";
-    case 12: return "Q4_K";
-    case 13: return "Q5_K";
-    case 14: return "Q6_K";
-    case 30: return "BF16";
-    default: return "other";
-  }
+size_t ggml_row_size(uint32_t type, int64_t n) {
+  const GgmlBlock* b = ggml_block(type);
+  if (!b) throw std::runtime_error("ggml type " + std::to_string(type) + " is not supported");
+  if (n < 0 || n % b->block)
+    throw std::runtime_error(std::string(b->name) + ": a row of " + std::to_string(n) +
+                             " values is not a whole number of blocks of " + std::to_string(b->block));
+  return static_cast<size_t>(n / b->block) * static_cast<size_t>(b->bytes);
+}
+
+const char* ggml_type_name(uint32_t type) {
+  const GgmlBlock* b = ggml_block(type);
+  return b ? b->name : "unknown";
 }
 
 int64_t GgufTensor::nelements() const {
   int64_t n = 1;
-  for (auto d : ne) n *= d;
+  for (int64_t d : ne) n *= d;
   return n;
 }
 
 GgufFile::GgufFile(const std::string& path) {
-  fd_ = ::open(path.c_str(), O_RDONLY);
-  if (fd_ < 0) throw std::runtime_error("cannot open " + path + ": " + std::strerror(errno));
-  struct stat st{};
-  if (fstat(fd_, &st) != 0) throw std::runtime_error("cannot stat " + path);
-  size_ = static_cast<size_t>(st.st_size);
-  void* m = mmap(nullptr, size_, PROT_READ, MAP_SHARED, fd_, 0);
-  if (m == MAP_FAILED) {
-    ::close(fd_);
-    throw std::runtime_error("mmap failed: " + std::string(std::strerror(errno)));
-  }
-  base_ = static_cast<uint8_t*>(m);
   try {
-    Cursor c(base_, size_);
-    if (c.get<uint32_t>() != 0x46554747) throw std::runtime_error(path + " is not a GGUF file");
-    const auto version = c.get<uint32_t>();
-    if (version < 3) throw std::runtime_error("GGUF v" + std::to_string(version) + " unsupported, need v3");
-    const auto n_tensors = c.get<uint64_t>();
-    const auto n_kv = c.get<uint64_t>();
-    for (uint64_t i = 0; i < n_kv; ++i) {
-      std::string key = c.str();
-      const auto t = c.get<uint32_t>();
-      if (t == 8) {
-        kv_[key] = c.str();
-      } else if (t == 6) {
-        kv_[key] = static_cast<double>(c.get<float>());
-      } else if (t == 12) {
-        kv_[key] = c.get<double>();
-      } else if (t == 7) {
-        kv_[key] = c.get<uint8_t>() != 0;
-      } else if (t == 9) {
-        const auto et = c.get<uint32_t>();
-        const auto n = c.get<uint64_t>();
-        for (uint64_t j = 0; j < n; ++j) skip_value(c, et);
-        kv_[key] = static_cast<size_t>(n);
-      } else {
-        kv_[key] = read_int(c, t);
-      }
-    }
-    struct Info {
-      GgufTensor t;
-      uint64_t off;
-    };
-    std::vector<Info> infos;
-    for (uint64_t i = 0; i < n_tensors; ++i) {
-      Info in;
-      in.t.name = c.str();
-      const auto nd = c.get<uint32_t>();
-      for (uint32_t d = 0; d < nd; ++d) in.t.ne.push_back(static_cast<int64_t>(c.get<uint64_t>()));
-      in.t.type = c.get<uint32_t>();
-      in.off = c.get<uint64_t>();
-      infos.push_back(std::move(in));
-    }
-    const size_t align = static_cast<size_t>(get_int("general.alignment").value_or(32));
-    const size_t start = (static_cast<size_t>(c.pos() - base_) + align - 1) / align * align;
-    for (auto& in : infos) {
-      auto& t = in.t;
-      t.nbytes = ggml_row_size(t.type, t.ne[0]) * static_cast<size_t>(t.rows());
-      if (start + in.off + t.nbytes > size_) throw std::runtime_error("gguf: tensor " + t.name + " out of bounds");
-      t.data = base_ + start + in.off;
-      tensors_[t.name] = std::move(t);
-    }
+    parse(path);
   } catch (...) {
-    munmap(base_, size_);
-    ::close(fd_);
+    if (map_) munmap(map_, size_);
+    if (fd_ >= 0) ::close(fd_);
+    map_ = nullptr;
+    fd_ = -1;
     throw;
   }
 }
 
 GgufFile::~GgufFile() {
-  if (base_) munmap(base_, size_);
+  if (map_) munmap(map_, size_);
   if (fd_ >= 0) ::close(fd_);
 }
 
+void GgufFile::parse(const std::string& path) {
+  fd_ = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+  if (fd_ < 0) throw std::runtime_error("gguf " + path + ": open failed: " + std::strerror(errno));
+  struct stat st {};
+  if (fstat(fd_, &st) != 0) throw std::runtime_error("gguf " + path + ": stat failed: " + std::strerror(errno));
+  size_ = static_cast<size_t>(st.st_size);
+  if (size_ < 24) throw std::runtime_error("gguf " + path + ": file too short for a GGUF header");
+  void* m = mmap(nullptr, size_, PROT_READ, MAP_SHARED, fd_, 0);
+  if (m == MAP_FAILED) throw std::runtime_error("gguf " + path + ": mmap failed: " + std::strerror(errno));
+  map_ = m;
+  const auto* base = static_cast<const uint8_t*>(map_);
+
+  Reader r(base, size_, path);
+  if (r.get<uint32_t>("magic") != kMagic) r.fail("not a GGUF file (bad magic)");
+  const uint32_t version = r.get<uint32_t>("version");
+  if (version < 3) r.fail("GGUF version " + std::to_string(version) + " is not supported (version 3 is)");
+  const uint64_t n_tensors = r.get<uint64_t>("tensor count");
+  const uint64_t n_meta = r.get<uint64_t>("metadata count");
+
+  for (uint64_t i = 0; i < n_meta; ++i) {
+    std::string key = r.text("metadata key");
+    const uint32_t t = r.get<uint32_t>("metadata type");
+    Meta v;
+    if (t == kStr) {
+      v.kind = Meta::kString;
+      v.s = r.text("metadata string");
+    } else if (t == kArr) {
+      const uint32_t elem = r.get<uint32_t>("metadata array type");
+      const uint64_t count = r.get<uint64_t>("metadata array count");
+      skip_array(r, elem, count, 0);
+      v.kind = Meta::kArray;
+      v.i = static_cast<int64_t>(count > static_cast<uint64_t>(std::numeric_limits<int64_t>::max())
+                                     ? std::numeric_limits<int64_t>::max()
+                                     : count);
+    } else if (t == kF32) {
+      v.kind = Meta::kFloat;
+      v.f = r.get<float>("metadata value");
+    } else if (t == kF64) {
+      v.kind = Meta::kFloat;
+      v.f = r.get<double>("metadata value");
+    } else if (t == kBool) {
+      v.kind = Meta::kBool;
+      v.i = r.get<uint8_t>("metadata value") != 0;
+    } else if (t < kNumTypes) {
+      v.kind = Meta::kInt;
+      v.i = read_integer(r, t);
+    } else {
+      r.fail("metadata type " + std::to_string(t) + " is unknown");
+    }
+    meta_[std::move(key)] = std::move(v);
+  }
+
+  // Tensor directory: the entries are kept in file order until the data section's start is known.
+  struct Entry {
+    GgufTensor t;
+    uint64_t offset;
+  };
+  std::vector<Entry> dir;
+  for (uint64_t i = 0; i < n_tensors; ++i) {
+    Entry e;
+    e.t.name = r.text("tensor name");
+    const uint32_t nd = r.get<uint32_t>("tensor rank");
+    if (nd < 1 || nd > kMaxDims) r.fail("tensor " + e.t.name + " has rank " + std::to_string(nd));
+    int64_t count = 1;
+    for (uint32_t d = 0; d < nd; ++d) {
+      const uint64_t n = r.get<uint64_t>("tensor shape");
+      if (n > static_cast<uint64_t>(std::numeric_limits<int64_t>::max() / (count ? count : 1)))
+        r.fail("tensor " + e.t.name + " has too many elements");
+      count *= static_cast<int64_t>(n);
+      e.t.ne.push_back(static_cast<int64_t>(n));
+    }
+    e.t.type = r.get<uint32_t>("tensor type");
+    e.offset = r.get<uint64_t>("tensor offset");
+    if (!ggml_block(e.t.type))
+      r.fail("tensor " + e.t.name + " has unknown ggml type " + std::to_string(e.t.type));
+    dir.push_back(std::move(e));
+  }
+
+  uint64_t align = 32;
+  if (const auto a = get_int("general.alignment")) {
+    if (*a <= 0 || *a > (1 << 20)) r.fail("general.alignment " + std::to_string(*a) + " is not usable");
+    align = static_cast<uint64_t>(*a);
+  }
+  const uint64_t data = (r.offset() + align - 1) / align * align;
+  if (data > size_) r.fail("tensor data section starts past the end of the file");
+  const uint64_t avail = size_ - data;
+  for (Entry& e : dir) {
+    GgufTensor& t = e.t;
+    const size_t row = ggml_row_size(t.type, t.ne[0]);
+    const int64_t rows = t.rows();
+    if (rows > 0 && row > std::numeric_limits<size_t>::max() / static_cast<size_t>(rows))
+      r.fail("tensor " + t.name + " is too large");
+    t.nbytes = row * static_cast<size_t>(rows);
+    if (e.offset > avail || t.nbytes > avail - e.offset)
+      throw std::runtime_error("gguf " + path + ": tensor " + t.name + " lies outside the file");
+    t.data = base + data + e.offset;
+    if (!tensors_.emplace(t.name, t).second)
+      throw std::runtime_error("gguf " + path + ": tensor " + t.name + " appears twice");
+  }
+}
+
 std::optional<int64_t> GgufFile::get_int(const std::string& key) const {
-  auto it = kv_.find(key);
-  if (it == kv_.end()) return std::nullopt;
-  if (auto* i = std::get_if<int64_t>(&it->second)) return *i;
-  if (auto* b = std::get_if<bool>(&it->second)) return *b ? 1 : 0;
+  const auto it = meta_.find(key);
+  if (it == meta_.end()) return std::nullopt;
+  const Meta& v = it->second;
+  if (v.kind == Meta::kInt || v.kind == Meta::kBool) return v.i;
   return std::nullopt;
 }
 
 std::optional<double> GgufFile::get_float(const std::string& key) const {
-  auto it = kv_.find(key);
-  if (it == kv_.end()) return std::nullopt;
-  if (auto* d = std::get_if<double>(&it->second)) return *d;
-  if (auto* i = std::get_if<int64_t>(&it->second)) return static_cast<double>(*i);
+  const auto it = meta_.find(key);
+  if (it == meta_.end()) return std::nullopt;
+  const Meta& v = it->second;
+  if (v.kind == Meta::kFloat) return v.f;
+  if (v.kind == Meta::kInt) return static_cast<double>(v.i);
   return std::nullopt;
 }
 
 std::optional<std::string> GgufFile::get_str(const std::string& key) const {
-  auto it = kv_.find(key);
-  if (it == kv_.end()) return std::nullopt;
-  if (auto* s = std::get_if<std::string>(&it->second)) return *s;
-  return std::nullopt;
+  const auto it = meta_.find(key);
+  if (it == meta_.end() || it->second.kind != Meta::kString) return std::nullopt;
+  return it->second.s;
 }
 
 size_t GgufFile::str_array_size(const std::string& key) const {
-  auto it = kv_.find(key);
-  if (it == kv_.end()) return 0;
-  if (auto* n = std::get_if<size_t>(&it->second)) return *n;
-  return 0;
+  const auto it = meta_.find(key);
+  if (it == meta_.end() || it->second.kind != Meta::kArray) return 0;
+  return static_cast<size_t>(it->second.i);
 }
 
 const GgufTensor* GgufFile::tensor(const std::string& name) const {
-  auto it = tensors_.find(name);
+  const auto it = tensors_.find(name);
   return it == tensors_.end() ? nullptr : &it->second;
 }
 

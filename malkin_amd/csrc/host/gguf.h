@@ -1,29 +1,44 @@
-// GGUF v3 reader (memory-mapped): metadata and tensor table. Plays the role of the reference's GgufFile
-// (gguf.h:44-69): same file format, same lookups, our own implementation.
+// Memory-mapped GGUF v3 file: the metadata table and the tensor directory, with every offset checked against the
+// mapping. Serves the role of the reference's GgufFile (gguf.h:44-69) for the device model: same file format, same
+// key and tensor lookups; the parser is written from the GGUF v3 format description.
+//
+// Format (little endian): magic "GGUF" (u32 0x46554747), version u32 (3), tensor count u64, metadata count u64;
+// metadata entries {string key, u32 value type, value}; tensor entries {string name, u32 n_dims, u64 ne[n_dims],
+// u32 ggml type, u64 offset}; tensor data starts at the next multiple of general.alignment (default 32) after the
+// directory, each tensor at data start + offset. Strings are {u64 length, bytes}; arrays {u32 element type, u64
+// count, elements}.
 #pragma once
 
 #include <cstdint>
 #include <map>
 #include <optional>
 #include <string>
-#include <variant>
 #include <vector>
 
 namespace malkin_hip {
 
+// Block geometry of a ggml tensor type: `block` values in `bytes` bytes.
+struct GgmlBlock {
+  uint32_t type;
+  int block;
+  int bytes;
+  const char* name;
+};
+// nullptr for types this file reader does not know.
+const GgmlBlock* ggml_block(uint32_t type);
+// Bytes of n values of `type`; throws for unknown types and for n not a whole number of blocks.
+size_t ggml_row_size(uint32_t type, int64_t n);
+const char* ggml_type_name(uint32_t type);
+
 struct GgufTensor {
   std::string name;
-  uint32_t type = 0;        // ggml type id
-  std::vector<int64_t> ne;  // ne[0] innermost
+  uint32_t type = 0;
+  std::vector<int64_t> ne;  // ne[0] is the row length
   const uint8_t* data = nullptr;
   size_t nbytes = 0;
   int64_t nelements() const;
-  int64_t rows() const { return ne.empty() ? 0 : nelements() / ne[0]; }
+  int64_t rows() const { return ne.empty() || ne[0] == 0 ? 0 : nelements() / ne[0]; }
 };
-
-// ggml block traits (gguf.cpp:60-95): bytes of n elements of type t; throws for unknown types or partial blocks.
-size_t ggml_row_size(uint32_t type, int64_t n);
-const char* ggml_type_name(uint32_t type);
 
 class GgufFile {
  public:
@@ -32,20 +47,32 @@ class GgufFile {
   GgufFile(const GgufFile&) = delete;
   GgufFile& operator=(const GgufFile&) = delete;
 
+  // Typed metadata lookups; nullopt when the key is absent or holds another kind of value. Integers of every width
+  // and bools read as int; f32 / f64 (and integers) as float.
   std::optional<int64_t> get_int(const std::string& key) const;
   std::optional<double> get_float(const std::string& key) const;
   std::optional<std::string> get_str(const std::string& key) const;
-  size_t str_array_size(const std::string& key) const;  // 0 when absent
+  // Element count of an array value (the tokenizer's vocabulary, tokenizer.ggml.tokens); 0 when absent.
+  size_t str_array_size(const std::string& key) const;
+
   const GgufTensor* tensor(const std::string& name) const;
   const std::map<std::string, GgufTensor>& tensors() const { return tensors_; }
   size_t size() const { return size_; }
 
  private:
-  using Value = std::variant<int64_t, double, bool, std::string, size_t /* array length */>;
+  // One decoded metadata value. Arrays keep only their element count (the device model reads no array contents).
+  struct Meta {
+    enum Kind { kInt, kFloat, kBool, kString, kArray } kind = kInt;
+    int64_t i = 0;
+    double f = 0;
+    std::string s;
+  };
+  void parse(const std::string& path);
+
   int fd_ = -1;
-  uint8_t* base_ = nullptr;
+  void* map_ = nullptr;
   size_t size_ = 0;
-  std::map<std::string, Value> kv_;
+  std::map<std::string, Meta> meta_;
   std::map<std::string, GgufTensor> tensors_;
 };
 

@@ -56,6 +56,7 @@ int mk_init(int device, mk_ctx** out) {
     check(hipEventCreate(&c->ev1), "hipEventCreate");
     c->scratch_bytes = 1 << 20;
     check(hipMalloc(&c->scratch, c->scratch_bytes), "hipMalloc");
+    check(hipMalloc(&c->meta, 64), "hipMalloc");
     *out = c;
   });
 }
@@ -69,6 +70,7 @@ int mk_destroy(mk_ctx* c) {
     (void)hipEventDestroy(c->ev1);
     (void)hipStreamDestroy(c->stream);
     (void)hipFree(c->scratch);
+    (void)hipFree(c->meta);
     delete c;
   });
 }
@@ -198,22 +200,14 @@ int mk_attend_gqa(mk_ctx* c, const float* q, int G, int D, const int8_t* k, cons
                   ptrdiff_t soff, int n, float scale, float* out, const int32_t* extra, int ne) {
   return guard([&] {
     require(G > 0 && n >= 0 && ne >= 0 && n + ne > 0, "attend_gqa: bad sizes");
-    // Per-call metadata for the batched kernel: one token of sequence 0 with n contiguous keys plus ne extra rows.
-    const int32_t meta[4] = {0, n, 0, ne};
-    int32_t* dm = nullptr;
-    check(hipMalloc(&dm, sizeof meta), "hipMalloc");
-    check(hipMemcpyAsync(dm, meta, sizeof meta, hipMemcpyHostToDevice, c->stream), "hipMemcpy H2D");
+    // The batched kernel's layout for one token of sequence 0: n contiguous keys, then ne extra rows. Written into
+    // the context's metadata words by a kernel in stream order: no allocation, no host synchronization.
+    int32_t* dm = c->meta;
+    mk::put4(c->stream, dm, 0, n, 0, ne);
     mk::AttnAddr a{k, v, reinterpret_cast<const char*>(k) + soff, reinterpret_cast<const char*>(v) + soff,
                    0, 0, (int64_t)stride, 0, 0, (int64_t)stride, 0};
-    try {
-      mk::attention(c->stream, q, (int64_t)G * D, out, (int64_t)G * D, 1, G, 1, D, scale, a, dm, dm + 1,
-                    ne > 0 ? dm + 2 : nullptr, extra, n + ne);
-      check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-    } catch (...) {
-      (void)hipFree(dm);
-      throw;
-    }
-    check(hipFree(dm), "hipFree");
+    mk::attention(c->stream, q, (int64_t)G * D, out, (int64_t)G * D, 1, G, 1, D, scale, a, dm, dm + 1,
+                  ne > 0 ? dm + 2 : nullptr, extra, n + ne);
   });
 }
 

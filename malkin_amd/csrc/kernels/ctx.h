@@ -18,6 +18,7 @@ struct mk_ctx {
   char name[64] = {0};
   void* scratch = nullptr;  // per-context device scratch (partial reductions), allocated once at init
   size_t scratch_bytes = 0;
+  int32_t* meta = nullptr;  // 64 bytes of per-call metadata (mk_attend_gqa's token layout), allocated at init
 };
 
 namespace mk {

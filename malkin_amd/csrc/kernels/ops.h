@@ -46,6 +46,8 @@ void silu_mul(hipStream_t s, int64_t n, float* g, const float* u);
 void silu_mul_q8(hipStream_t s, const float* gu, int rows, int64_t n, BlockQ8* xq, bool interleave4 = false);
 void add(hipStream_t s, int64_t n, float* x, const float* h);
 void fill(hipStream_t s, void* p, int value, size_t bytes);
+// p[0..3] = a, b, c, d (p 16-byte aligned), in stream order.
+void put4(hipStream_t s, int32_t* p, int a, int b, int c, int d);
 
 // y[t * ys + r] (+)= W[r] . xq[t]; wide: Q6_K wide-panel arithmetic for n > 16.
 void matmul(hipStream_t s, int type, bool wide, const void* w, int64_t rows, int64_t cols, const BlockQ8* xq, int n,

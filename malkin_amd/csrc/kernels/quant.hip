@@ -159,6 +159,11 @@ __global__ void k_fill(uint8_t* p, int v, size_t n) {
   if (i < n) p[i] = (uint8_t)v;
 }
 
+// Four int32 words from the kernel arguments (small per-call metadata written in stream order, without a host copy).
+__global__ void k_put4(int32_t* p, int a, int b, int c, int d) {
+  if (threadIdx.x == 0) *reinterpret_cast<int4*>(p) = make_int4(a, b, c, d);
+}
+
 __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int& sc, int& m) {
   if (j < 4) {
     sc = q[j] & 63;
@@ -269,6 +274,11 @@ void add(hipStream_t s, int64_t n, float* x, const float* h) {
   if (n <= 0) return;
   hipLaunchKernelGGL(k_add, dim3(grid_for(n, kT)), dim3(kT), 0, s, n, x, h);
   check_launch("add");
+}
+
+void put4(hipStream_t s, int32_t* p, int a, int b, int c, int d) {
+  hipLaunchKernelGGL(k_put4, dim3(1), dim3(64), 0, s, p, a, b, c, d);
+  check_launch("put4");
 }
 
 void fill(hipStream_t s, void* p, int v, size_t n) {

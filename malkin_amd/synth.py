@@ -51,6 +51,9 @@ def lib():
         _lib.mks_write_gguf.restype = ctypes.c_int
         _lib.mks_file_bytes.argtypes = [ctypes.POINTER(_Config)]
         _lib.mks_file_bytes.restype = ctypes.c_int64
+        _lib.mks_quantize_rows.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                           ctypes.c_void_p]
+        _lib.mks_quantize_rows.restype = ctypes.c_int
     return _lib
 
 
@@ -75,6 +78,22 @@ def make_config(preset="tiny", wtype=Q8_0, mix=MIX_UNIFORM, seed=1, std=0.02, ro
 
 def file_bytes(cfg):
     return int(lib().mks_file_bytes(ctypes.byref(cfg)))
+
+
+_BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+
+
+def quantize_rows(wtype, x):
+    """The writer's quantizer on x [rows][k] float32: GGUF rows of type wtype as uint8 [rows][row bytes]."""
+    import numpy as np
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, k = x.shape
+    qk, bs = _BLOCK[wtype]
+    out = np.empty((rows, k // qk * bs), dtype=np.uint8)
+    rc = lib().mks_quantize_rows(wtype, x.ctypes.data, rows, k, out.ctypes.data)
+    if rc != 0:
+        raise ValueError(f"mks_quantize_rows: type {wtype} with {k} columns unsupported")
+    return out
 
 
 def write_gguf(path, cfg, threads=None):

@@ -68,10 +68,16 @@ static uint16_t to_half(float f) {
   return sign | (uint16_t)h;
 }
 
-static float from_half(uint16_t h) { /* normal halves only (the quantizers below produce no subnormal scales) */
+/* IEEE half -> float, exact for normal and subnormal halves (Q6_K's d of N(0, 0.02) weights is a subnormal half:
+   about 1.4e-5 < 2^-14). A subnormal is m * 2^-24, exact in float. */
+static float from_half(uint16_t h) {
   const uint32_t sign = (uint32_t)(h & 0x8000) << 16, e = (h >> 10) & 0x1F, m = h & 0x3FF;
-  uint32_t u = e == 0 ? sign : sign | ((e + 112) << 23) | (m << 13);
   float f;
+  if (e == 0) {
+    f = (float)m * (1.0f / 16777216.0f);
+    return sign ? -f : f;
+  }
+  const uint32_t u = sign | ((e + 112) << 23) | (m << 13);
   memcpy(&f, &u, 4);
   return f;
 }
@@ -359,6 +365,20 @@ static size_t header(wbuf* w, const mks_config* c, const tinfo* t, int nt) {
     w_u64(w, t[i].off);
   }
   return (w->n + 31) / 32 * 32;
+}
+
+int mks_quantize_rows(int type, const float* x, int64_t rows, int64_t k, uint8_t* out) {
+  const size_t rb = row_bytes(type, k);
+  if (!rb || type == T_F32 || k % (type == T_Q8_0 ? 32 : 256)) return -2;
+  for (int64_t r = 0; r < rows; ++r, x += k, out += rb) {
+    if (type == T_Q8_0)
+      quant_q8_0(x, out, k);
+    else if (type == T_Q4_K)
+      quant_q4_k(x, out, k);
+    else
+      quant_q6_k(x, out, k);
+  }
+  return 0;
 }
 
 int64_t mks_file_bytes(const mks_config* c) {

@@ -25,6 +25,9 @@ typedef struct {
 int64_t mks_file_bytes(const mks_config* c);
 /* 0 on success; -1 I/O error; -2 unsupported shape or type. */
 int mks_write_gguf(const char* path, const mks_config* c, int threads);
+/* The writer's quantizer on caller data: rows x k floats -> rows of GGUF blocks of `type` (Q8_0, Q4_K, Q6_K; k a
+   multiple of the block size), out holding rows * row bytes. 0 on success, -2 unsupported type or k. */
+int mks_quantize_rows(int type, const float* x, int64_t rows, int64_t k, uint8_t* out);
 
 #ifdef __cplusplus
 }
