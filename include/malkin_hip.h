@@ -161,6 +161,14 @@ int mk_move_kv(mk_ctx* ctx, const mk_kv_cache* kv, int seq, int from, int to);
 /* ---- greedy selection (sampler.cpp:27-30 argmax; engine.cpp:309-318 draft top-2) ---- */
 /* Per row of n_vocab logits: top1 = first maximum, top2 = the reference's runner-up scan. top2 may be NULL. */
 int mk_argmax_top2(mk_ctx* ctx, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2);
+/* mk_argmax_top2 that allocates nothing and needs no context. No counterpart in the reference: it is for callers
+   that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+   hipMalloc). The per-row partial results live in a file-scope device array of the library sized for 256 rows
+   (256 KiB on each GPU it runs on, held until the process ends); more rows fail with MK_ERR_INVALID. stream: a
+   hipStream_t (NULL: the current device's null stream); the work is queued on it and the call does not wait. Every
+   call on one GPU shares that array, so calls that overlap on one GPU (two streams) race; calls in one stream's
+   order do not. Results are identical to mk_argmax_top2's. */
+int mk_argmax_top2_noalloc(void* stream, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2);
 /* Device-resident greedy decode bookkeeping for one sequence (no reference counterpart: the CPU engine does this on
    the host, engine.cpp:397-421): out_tokens[*counter] = ids[0] = *top1; ++*counter; ++rpos[0], ++kv_row[0],
    ++n_keys[0]. Lets a captured decode step be replayed without host round trips. */

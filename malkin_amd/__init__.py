@@ -60,6 +60,7 @@ SIGNATURES = {
     "mk_move_kv": (_I, [_P, _P, _I, _I, _I]),
     "mk_argmax_top2": (_I, [_P, _P, _I, _I, _P, _P]),
     "mk_greedy_advance": (_I, [_P, _P, _P, _P, _P, _P, _P, _P]),
+    "mk_argmax_top2_noalloc": (_I, [_P, _P, _I, _I, _P, _P]),
     "mk_gguf_inspect": (_I, [ctypes.c_char_p, _P]),
     "mk_model_open": (_I, [_P, ctypes.c_char_p, _I, _I, _I, ctypes.POINTER(_P)]),
     "mk_model_free": (_I, [_P]),

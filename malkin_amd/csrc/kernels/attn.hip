@@ -4,6 +4,8 @@
 //   attention        kernels_avx512.cpp:228-267 (attend_t<D/16>) and 282-306 (other head sizes), model.cpp:204-247
 //   move_kv_rows     model.cpp:432-440
 //   argmax_top2      sampler.cpp:27-30 (first maximum), engine.cpp:309-318 (runner-up scan)
+#include <mutex>
+
 #include "ctx.h"
 #include "ops.h"
 
@@ -1350,6 +1352,51 @@ void argmax_top2(hipStream_t s, const float* logits, int rows, int n_vocab, int3
   hipLaunchKernelGGL(k_top2_part, dim3(kSelParts, rows), dim3(kSelT), 0, s, logits, n_vocab, part);
   hipLaunchKernelGGL(k_top2_merge, dim3(rows), dim3(kSelParts), 0, s, part, top1, top2);
   check_launch("argmax_top2");
+}
+
+}  // namespace mk
+
+// ---- allocation-free greedy selection (mk_argmax_top2_noalloc) ----
+// k_top2_part's per-row partial results for callers that cannot allocate device memory: a file-scope array of
+// kNoAllocSelectRows rows (256 KiB), one copy per GPU the library runs on, held until the process ends. In host code
+// this name is only a stand-in; its device address comes from hipGetSymbolAddress (noalloc_select_scratch).
+static __device__ __align__(256) unsigned char scratch[mk::kNoAllocSelectRows * mk::kSelParts * sizeof(mk::Top2)];
+
+namespace mk {
+
+namespace {
+constexpr int kMaxDevices = 64;
+}
+
+// Device address of `scratch` on the stream's device, resolved once per device with that device current.
+static void* noalloc_select_scratch(hipStream_t s) {
+  int dev = 0;
+  if (s)
+    check(hipStreamGetDevice(s, &dev), "hipStreamGetDevice");
+  else
+    check(hipGetDevice(&dev), "hipGetDevice");
+  require(dev >= 0 && dev < kMaxDevices, "mk_argmax_top2_noalloc: device index out of range");
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    int cur = 0;
+    check(hipGetDevice(&cur), "hipGetDevice");
+    if (cur != dev) check(hipSetDevice(dev), "hipSetDevice");
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    check(e, "hipGetSymbolAddress(scratch)");
+    addr[dev] = p;
+  }
+  return addr[dev];
+}
+
+void argmax_top2_noalloc(hipStream_t s, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2) {
+  require(rows <= kNoAllocSelectRows, "mk_argmax_top2_noalloc: more than 256 rows (its static scratch holds 256)");
+  // k_top2_part writes every (row, part) entry it covers before k_top2_merge reads it: nothing needs clearing.
+  argmax_top2(s, logits, rows, n_vocab, top1, top2, noalloc_select_scratch(s),
+              (size_t)kNoAllocSelectRows * kSelParts * sizeof(Top2));
 }
 
 }  // namespace mk

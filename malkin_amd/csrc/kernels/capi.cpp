@@ -280,4 +280,8 @@ int mk_argmax_top2(mk_ctx* c, const float* logits, int rows, int n_vocab, int32_
   return guard([&] { mk::argmax_top2(c->stream, logits, rows, n_vocab, top1, top2, c->scratch, c->scratch_bytes); });
 }
 
+int mk_argmax_top2_noalloc(void* stream, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2) {
+  return guard([&] { mk::argmax_top2_noalloc(static_cast<hipStream_t>(stream), logits, rows, n_vocab, top1, top2); });
+}
+
 }  // extern "C"

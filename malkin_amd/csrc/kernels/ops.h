@@ -127,6 +127,10 @@ void qk_norm_rope_kv(hipStream_t s, float* q, float* k, const float* v, int64_t 
 
 // Scratch: argmax_scratch_bytes(rows) of device memory (per-row partial results).
 size_t argmax_scratch_bytes(int rows);
+// argmax_top2 with its partial results in a file-scope device array (one per GPU, kNoAllocSelectRows rows): no
+// allocation, no context. Calls that overlap on one GPU race on that array.
+constexpr int kNoAllocSelectRows = 256;
+void argmax_top2_noalloc(hipStream_t s, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2);
 void argmax_top2(hipStream_t s, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2,
                  void* scratch, size_t scratch_bytes);
 
