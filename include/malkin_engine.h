@@ -44,6 +44,8 @@ int mk_engine_submit(mk_engine* e, const int32_t* prompt, int n_prompt, int max_
 int mk_engine_step(mk_engine* e, int32_t* busy);
 /* Steps until no request is pending or in flight. */
 int mk_engine_run(mk_engine* e);
+/* Steps (target forwards) run so far; with mk_host_waits() it bounds the host waits per step (one). */
+int mk_engine_steps(mk_engine* e, uint64_t* steps);
 /* Generated ids of a request (up to cap) and its counters. */
 int mk_engine_result(mk_engine* e, int32_t request_id, int32_t* tokens, int32_t cap, mk_request_info* info);
 

@@ -42,6 +42,9 @@ int mk_destroy(mk_ctx* ctx);
 const char* mk_device_name(const mk_ctx* ctx);
 const char* mk_last_error(void);
 int mk_synchronize(mk_ctx* ctx);
+/* Host waits on the device made by this library so far (stream and event synchronizations, including those inside
+   mk_upload / mk_download / mk_free), for tests that bound the waits of a token loop. */
+uint64_t mk_host_waits(void);
 /* The context's hipStream_t. */
 void* mk_stream(mk_ctx* ctx);
 
@@ -52,6 +55,18 @@ int mk_upload(mk_ctx* ctx, void* dev_dst, const void* host_src, size_t bytes);
 int mk_download(mk_ctx* ctx, void* host_dst, const void* dev_src, size_t bytes);
 /* Fills with a kernel (safe inside captured graphs). */
 int mk_fill(mk_ctx* ctx, void* dev, int byte_value, size_t bytes);
+/* Pinned host memory (hipHostMalloc) for asynchronous copies; mk_host_free waits for the stream first. */
+int mk_host_alloc(mk_ctx* ctx, size_t bytes, void** host);
+int mk_host_free(mk_ctx* ctx, void* host);
+/* Copy of `bytes` in stream order without waiting (any direction; host memory must be pinned and stay untouched until
+   the copy has run: record an event after it and wait for that event before reusing the memory). */
+int mk_copy_async(mk_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* Records *event (created on first use) at the current end of the stream / waits on the host until it has passed. */
+int mk_event_record(mk_ctx* ctx, void** event);
+int mk_event_wait(mk_ctx* ctx, void* event);
+/* 1 when the event has passed (or is NULL), 0 while work before it is pending; never waits. */
+int mk_event_done(void* event);
+int mk_event_free(void* event);
 
 /* ---- timing on the context stream (bench) ---- */
 int mk_timer_start(mk_ctx* ctx);
@@ -169,6 +184,11 @@ int mk_argmax_top2(mk_ctx* ctx, const float* logits, int rows, int n_vocab, int3
    call on one GPU shares that array, so calls that overlap on one GPU (two streams) race; calls in one stream's
    order do not. Results are identical to mk_argmax_top2's. */
 int mk_argmax_top2_noalloc(void* stream, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2);
+/* dst[dst_index[i]] = src[src_index[i]] for i < n, in stream order (a NULL index array is the identity; a negative
+   index skips i). Moves token ids between device arrays without a host round trip: draft picks into a proposal tree,
+   tree ids into a forward's token slots (no reference counterpart: the CPU engine keeps ids in host vectors). */
+int mk_move_ids(mk_ctx* ctx, int32_t* dst, const int32_t* dst_index, const int32_t* src, const int32_t* src_index,
+                int n);
 /* Device-resident greedy decode bookkeeping for one sequence (no reference counterpart: the CPU engine does this on
    the host, engine.cpp:397-421): out_tokens[*counter] = ids[0] = *top1; ++*counter; ++rpos[0], ++kv_row[0],
    ++n_keys[0]. Lets a captured decode step be replayed without host round trips. */

@@ -61,6 +61,15 @@ SIGNATURES = {
     "mk_argmax_top2": (_I, [_P, _P, _I, _I, _P, _P]),
     "mk_greedy_advance": (_I, [_P, _P, _P, _P, _P, _P, _P, _P]),
     "mk_argmax_top2_noalloc": (_I, [_P, _P, _I, _I, _P, _P]),
+    "mk_host_waits": (ctypes.c_uint64, []),
+    "mk_host_alloc": (_I, [_P, _SZ, ctypes.POINTER(_P)]),
+    "mk_host_free": (_I, [_P, _P]),
+    "mk_copy_async": (_I, [_P, _P, _P, _SZ]),
+    "mk_event_record": (_I, [_P, ctypes.POINTER(_P)]),
+    "mk_event_wait": (_I, [_P, _P]),
+    "mk_event_done": (_I, [_P]),
+    "mk_event_free": (_I, [_P]),
+    "mk_move_ids": (_I, [_P, _P, _P, _P, _P, _I]),
     "mk_gguf_inspect": (_I, [ctypes.c_char_p, _P]),
     "mk_model_open": (_I, [_P, ctypes.c_char_p, _I, _I, _I, ctypes.POINTER(_P)]),
     "mk_model_free": (_I, [_P]),
@@ -78,6 +87,7 @@ SIGNATURES = {
     "mk_engine_submit": (_I, [_P, _P, _I, _I, _P, _I, _P]),
     "mk_engine_step": (_I, [_P, _P]),
     "mk_engine_run": (_I, [_P]),
+    "mk_engine_steps": (_I, [_P, ctypes.POINTER(ctypes.c_uint64)]),
     "mk_engine_result": (_I, [_P, _I, _P, _I, _P]),
 }
 
@@ -343,12 +353,23 @@ class Engine:
     def run(self):
         check(load().mk_engine_run(self.h))
 
+    @property
+    def steps(self):
+        n = ctypes.c_uint64()
+        check(load().mk_engine_steps(self.h, ctypes.byref(n)))
+        return n.value
+
     def result(self, rid):
         info = MkRequestInfo()
         check(load().mk_engine_result(self.h, rid, None, 0, ctypes.byref(info)))
         toks = np.zeros(max(info.completion_tokens, 1), dtype=np.int32)
         check(load().mk_engine_result(self.h, rid, _ptr(toks), len(toks), ctypes.byref(info)))
         return toks[:info.completion_tokens], {f: getattr(info, f) for f, _ in MkRequestInfo._fields_}
+
+
+def host_waits():
+    """Host waits on the device the library has made so far (mk_host_waits)."""
+    return int(load().mk_host_waits())
 
 
 def batch(tokens):

@@ -179,6 +179,13 @@ int mk_engine_run(mk_engine* e) {
   });
 }
 
+int mk_engine_steps(mk_engine* e, uint64_t* steps) {
+  return run([&] {
+    if (!e || !steps) throw std::invalid_argument("mk_engine_steps: null argument");
+    *steps = e->engine->steps();
+  });
+}
+
 int mk_engine_result(mk_engine* e, int32_t request_id, int32_t* tokens, int32_t cap, mk_request_info* info) {
   return run([&] {
     if (!e) throw std::invalid_argument("mk_engine_result: null engine");

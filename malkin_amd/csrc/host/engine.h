@@ -1,31 +1,33 @@
-// Continuous-batching and speculative-decoding token loop over the device Model: the greedy part of the reference's
-// malkin::Engine (engine.h:51-141, engine.cpp:242-479), without text, tokenizer, sampling or threads. Requests are
-// token ids in, token ids out; every forward pass and every greedy pick runs on the GPU (forward_top2 returns ids,
-// never logits), and accepted tree nodes move their KV rows on the device.
+// Continuous batching and greedy speculative decoding over the device Model: the token loop of the reference's
+// malkin::Engine (engine.h:51-141, engine.cpp:242-479) for greedy requests, without text, tokenizer or threads.
+// Requests are token ids in, token ids out.
 //
-// Semantics kept from the reference:
-//   admit        a request goes to the idle slot whose cached tokens share the longest prefix with its prompt (ties:
-//                least recently admitted); that prefix's KV is reused, but the last prompt token is always evaluated
-//                (engine.cpp:242-265);
-//   step         one target forward over every busy slot: decoding slots put their next token (plus, with a draft
-//                model, the draft's greedy tree), then prompt chunks follow in slot order up to kMaxBatch tokens
-//                (engine.cpp:360-424);
-//   plan_drafts  draft length per decoding slot: the slot's adaptive k within its budget, its context room and a
-//                share of the batch (engine.cpp:336-357);
-//   propose      the draft catches its KV up to the slot's tokens (prefix reuse), then rounds in which every slot
-//                takes the draft's top-1 (chain) and runner-up (alternative) and feeds the chain token back
-//                (engine.cpp:267-334);
-//   layout       per slot [next, chain0, alt0, chain1, alt1, ...] at KV rows P, P + 1, ...; chain i and alt i sit at
-//                position P + 1 + i under chain i - 1 (engine.cpp:359-381);
-//   accept       walk the tree along the target's argmax, moving each accepted node's KV row to the next cache
-//                position; the first miss becomes the next token; k grows after a fully accepted chain and
-//                shrinks when fewer than half the drafts hold (engine.cpp:441-479);
-//   emit         a token ends the request when it is an end-of-generation id (not emitted), reaches the budget, or
-//                leaves no room in the context (engine.cpp:50-88).
+// Contract (what the reference engine does, and therefore what the streams, KV rows and counters must equal):
+//   * A request waits in FIFO order for an idle lane (one model sequence). It takes the idle lane whose cached
+//     tokens share the longest prefix with its prompt (ties: the lane admitted least recently), keeps that prefix's
+//     KV, and always re-evaluates at least its last prompt token.
+//   * One step = one target forward. Its batch holds, lane by lane, every decoding lane's pending token followed by
+//     its draft tree, then prompt tokens of prefilling lanes in lane order until the batch has 256 tokens.
+//   * Draft depth per decoding lane: its adaptive k (4 to start, at most n_draft), limited by its remaining budget,
+//     half its context room and half its share of the batch. The tree after the pending token at KV row P is
+//     chain_0, alt_0, chain_1, alt_1, ...: chain_i and alt_i are the draft's first and second greedy picks at depth
+//     i, at RoPE position P + 1 + i, KV rows P + 1 + 2i and P + 2 + 2i, both children of chain_{i-1} (of the pending
+//     token for i = 0).
+//   * Acceptance walks down from the pending token: while the target's pick at the current node equals that depth's
+//     chain (or alt) token, that token is accepted, its KV row moves to the next cache position, and the walk goes
+//     on below it (an alt is a leaf); the first pick that matches neither becomes the next pending token. k grows
+//     by one after a fully accepted chain at full depth and shrinks by one when fewer than half the drafts held.
+//   * A generated token ends its request when it is an end-of-generation id (not emitted, finish "stop"), when the
+//     budget is reached, or when the context has no room for another row (finish "length").
+//
+// Device residency: the draft's rounds run back to back on the stream. Each round's tokens are the previous
+// round's picks, read from a device array (Model::enqueue id redirects); picks are scattered into a per-lane tree
+// array on the device; accepted rows move on the device. The host waits once per step, for the target's picks.
 #pragma once
 
 #include <chrono>
 #include <cstdint>
+#include <deque>
 #include <memory>
 #include <string>
 #include <vector>
@@ -51,59 +53,77 @@ struct EngineResult {
 
 class Engine {
  public:
-  // target: n_seq slots (one sequence each). draft (may be null): same vocabulary, at least as many sequences.
-  // n_draft: maximum draft tokens per step (0: 8, the reference's default).
+  // target: one lane per sequence. draft (may be null): same vocabulary, at least as many sequences and context.
+  // n_draft: maximum draft depth (0: 8, the reference's default).
   Engine(Model* target, Model* draft, int n_draft);
+  ~Engine();
+  Engine(const Engine&) = delete;
+  Engine& operator=(const Engine&) = delete;
+
   int submit(const EngineRequest& req);  // request id
-  // Admits pending requests into idle slots, then one step; returns the number of slots still busy.
+  // Admits waiting requests into idle lanes, then one step; returns the number of lanes still busy.
   int step_once();
-  void run();  // steps until no request is pending or in flight
+  void run();  // steps until no request waits or runs
   const EngineResult& result(int id) const;
   int busy() const { return busy_; }
+  uint64_t steps() const { return steps_; }
 
  private:
   using Clock = std::chrono::steady_clock;
-  struct Request {
+  struct Job {
     EngineRequest req;
-    EngineResult* res;
+    EngineResult* res = nullptr;
     int budget = 0, k = 4;
     bool decoding = false;
-    int32_t next = 0;
-    Clock::time_point t0, t1;
+    int32_t pending = 0;  // generated and emitted, not yet in the KV cache
+    Clock::time_point admitted, first_token;
   };
-  struct Slot {
-    std::vector<int32_t> cache;   // tokens whose target KV is valid
-    std::vector<int32_t> dcache;  // tokens whose draft KV is valid
-    std::unique_ptr<Request> req;
-    uint64_t used = 0;
+  struct Lane {
+    std::vector<int32_t> kv;        // tokens whose target KV rows are valid
+    std::vector<int32_t> draft_kv;  // tokens whose draft KV rows are valid
+    std::unique_ptr<Job> job;       // null: idle
+    uint64_t stamp = 0;             // admission counter (least recently admitted wins a tie)
   };
-  struct Proposal {
-    int seq = 0, kk = 0, root = 0;
-    std::vector<int32_t> chain, alt;
+  struct Spec {  // a decoding lane's share of one step
+    int lane = 0, depth = 0, root = 0;  // root: batch index of the lane's pending token
   };
 
-  void admit(std::unique_ptr<Request> r);
+  void admit(std::unique_ptr<Job> job);
   void step();
-  bool plan_drafts();
-  void propose();
-  int build_batch();
-  void accept(const Proposal& p);
-  bool accept_greedy(const Proposal& p, Slot& s, int P);
-  bool emit(Request& q, int32_t id, size_t cached);
-  void finish(Slot& s);
+  void plan_specs();
+  void draft_trees();
+  void draft_forward(const std::vector<BatchToken>& batch, const std::vector<int32_t>& id_from,
+                     const std::vector<int32_t>& chain_slot);
+  int build_target_batch();
+  void settle(const Spec& sp, const int32_t* picks);
+  bool emit(Job& job, int32_t id, size_t cached);
+  void finish(Lane& lane);
+  int32_t* tree_host(int lane) { return tree_h_ + static_cast<size_t>(lane) * 2 * max_depth_; }
+  int tree_slot(int lane, int depth, bool alt) const { return lane * 2 * max_depth_ + 2 * depth + (alt ? 1 : 0); }
 
-  Model* model_;
+  Model* target_;
   Model* draft_;
-  int n_draft_ = 8;
-  std::vector<Slot> slots_;
-  std::vector<std::unique_ptr<Request>> pending_;
+  int max_depth_ = 8;
+  std::vector<Lane> lanes_;
+  std::deque<std::unique_ptr<Job>> waiting_;
   std::vector<std::unique_ptr<EngineResult>> results_;
   int busy_ = 0;
-  uint64_t admitted_ = 0;
-  std::vector<Proposal> props_;
-  std::vector<BatchToken> batch_, dbatch_;
-  std::vector<int> batch_seq_;          // prompt-finishing slot of each logits row after the decode rows
-  std::vector<int32_t> top1_, dtop1_, dtop2_, dslot1_, dslot2_;
+  uint64_t admissions_ = 0, steps_ = 0;
+
+  // Per step.
+  std::vector<Spec> specs_;
+  std::vector<BatchToken> batch_;
+  std::vector<int32_t> id_from_;
+  std::vector<int> finishing_lanes_;  // prefilling lanes whose last prompt token is in this step's batch
+
+  // Device state: the per-lane draft trees (chain / alt ids by depth), the latest draft picks, the target's picks,
+  // and the step's scatter plan (destination slots of each draft forward's picks).
+  DevBuf tree_, draft_top1_, draft_top2_, target_top_, plan_;
+  size_t plan_cap_ = 0, plan_used_ = 0;
+  int32_t* plan_h_ = nullptr;  // pinned host copy of the plan, copied once per step
+  int32_t* tree_h_ = nullptr;  // pinned: trees and target picks read back at the end of a step
+  int32_t* picks_h_ = nullptr;
+  std::vector<std::pair<size_t, int>> pending_scatters_;  // (plan offset, rows) of each queued draft forward
 };
 
 }  // namespace malkin_hip

@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstring>
 #include <stdexcept>
+#include <utility>
 
 namespace malkin_hip {
 
@@ -25,6 +26,8 @@ bool device_type(uint32_t t) { return t == MK_Q8_0 || t == MK_Q4_K || t == MK_Q6
 
 using Clock = std::chrono::steady_clock;
 double ms_since(Clock::time_point t) { return std::chrono::duration<double, std::milli>(Clock::now() - t).count(); }
+
+constexpr size_t kStagingBlocks = 16;  // layout copies in flight before the host waits for the oldest
 
 }  // namespace
 
@@ -47,27 +50,34 @@ DevBuf::~DevBuf() {
 
 mk_weight Model::Weight::w() const { return mk_weight{type, 0, rows, cols, packed.p}; }
 
-// model.cpp:78-101
+// The hyperparameters the qwen3 forward needs, keyed "<arch>.<name>" (the reference reads the same keys with the
+// same defaults, model.cpp:78-101; its error texts are kept because callers report them).
 ModelConfig read_config(const GgufFile& f) {
   ModelConfig c;
   c.arch = f.get_str("general.architecture").value_or("");
   c.name = f.get_str("general.name").value_or("model");
   if (c.arch != "qwen3") throw std::runtime_error("architecture '" + c.arch + "' unsupported (supported: qwen3)");
-  auto key = [&](const std::string& k) { return c.arch + "." + k; };
-  auto need = [&](const std::string& k) {
-    auto v = f.get_int(key(k));
-    if (!v) throw std::runtime_error("model: metadata " + key(k) + " missing");
-    return static_cast<int>(*v);
+  const std::string ns = c.arch + ".";
+  const std::pair<const char*, int*> required[] = {{"block_count", &c.n_layer},
+                                                   {"embedding_length", &c.n_embd},
+                                                   {"feed_forward_length", &c.n_ff},
+                                                   {"attention.head_count", &c.n_head}};
+  for (const auto& [name, field] : required) {
+    const auto v = f.get_int(ns + name);
+    if (!v) throw std::runtime_error("model: metadata " + ns + name + " missing");
+    *field = static_cast<int>(*v);
+  }
+  const auto int_or = [&](const char* name, int fallback) {
+    return static_cast<int>(f.get_int(ns + name).value_or(fallback));
   };
-  c.n_layer = need("block_count");
-  c.n_embd = need("embedding_length");
-  c.n_ff = need("feed_forward_length");
-  c.n_head = need("attention.head_count");
-  c.n_head_kv = static_cast<int>(f.get_int(key("attention.head_count_kv")).value_or(c.n_head));
-  c.head_dim = static_cast<int>(f.get_int(key("attention.key_length")).value_or(c.n_embd / c.n_head));
-  c.n_ctx_train = static_cast<int>(f.get_int(key("context_length")).value_or(4096));
-  c.rope_base = static_cast<float>(f.get_float(key("rope.freq_base")).value_or(10000.0));
-  c.rms_eps = static_cast<float>(f.get_float(key("attention.layer_norm_rms_epsilon")).value_or(1e-6));
+  const auto float_or = [&](const char* name, double fallback) {
+    return static_cast<float>(f.get_float(ns + name).value_or(fallback));
+  };
+  c.n_head_kv = int_or("attention.head_count_kv", c.n_head);
+  c.head_dim = int_or("attention.key_length", c.n_head > 0 ? c.n_embd / c.n_head : 0);
+  c.n_ctx_train = int_or("context_length", 4096);
+  c.rope_base = float_or("rope.freq_base", 10000.0);
+  c.rms_eps = float_or("attention.layer_norm_rms_epsilon", 1e-6);
   c.n_vocab = static_cast<int>(f.str_array_size("tokenizer.ggml.tokens"));
   return c;
 }
@@ -188,7 +198,8 @@ bool Model::matmul_group_f32(const Group& g, const float* x, int64_t xs, const f
 Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide)
     : ctx_(ctx), cfg_(read_config(f)), n_ctx_(n_ctx), n_seq_(n_seq), wide_(wide) {
   auto& c = cfg_;
-  if (c.head_dim % 32 || c.n_head % c.n_head_kv) throw std::runtime_error("model: unsupported head layout");
+  if (c.n_head <= 0 || c.n_head_kv <= 0 || c.head_dim <= 0 || c.head_dim % 32 || c.n_head % c.n_head_kv)
+    throw std::runtime_error("model: unsupported head layout");
   if (n_ctx <= 0 || n_seq <= 0) throw std::runtime_error("model: n_ctx and n_seq must be positive");
   const int E = c.n_embd, D = c.head_dim, H = c.n_head, KV = c.n_head_kv, F = c.n_ff;
 
@@ -198,6 +209,8 @@ Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide)
   if (!device_type(te->type) && te->type != 0)
     throw std::runtime_error("model: tensor token_embd.weight has unsupported type");
   embd_row_bytes_ = ggml_row_size(te->type, te->ne[0]);
+  if (te->ne[0] != c.n_embd) throw std::runtime_error("model: token_embd.weight has the wrong row length");
+  embd_count_ = te->rows();
   embd_rows_ = DevBuf(ctx_, te->nbytes);
   ck(mk_upload(ctx_, embd_rows_.p, te->data, te->nbytes));
   if (f.tensor("output.weight"))
@@ -267,10 +280,12 @@ Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide)
   logits_ = DevBuf(ctx_, B * static_cast<size_t>(c.n_vocab) * sizeof(float));
   top_ = DevBuf(ctx_, 2 * B * sizeof(int32_t) + 2 * sizeof(int32_t));
 
-  // Layout block: ids rpos seq kv_row n_keys out [B each], anc_off [B + 1], anc [B (B + 1) / 2].
-  const size_t words = 6 * B + (B + 1) + B * (B + 1) / 2;
-  host_block_.assign(words, 0);
-  layout_ = DevBuf(ctx_, words * sizeof(int32_t));
+  kv_ = mk_kv_cache{kc_.as<int8_t>(), vc_.as<int8_t>(), ks_.as<float>(), vs_.as<float>(), c.n_layer, n_seq_, KV, D,
+                    n_ctx_};
+
+  // Layout block (see model.h) and its pinned staging ring.
+  layout_words_ = 7 * B + (B + 1) + B * (B + 1) / 2;
+  layout_ = DevBuf(ctx_, layout_words_ * sizeof(int32_t));
   int32_t* d = layout_.as<int32_t>();
   d_ids_ = d;
   d_rpos_ = d + B;
@@ -278,12 +293,25 @@ Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide)
   d_kv_row_ = d + 3 * B;
   d_n_keys_ = d + 4 * B;
   d_out_ = d + 5 * B;
-  d_anc_off_ = d + 6 * B;
-  d_anc_ = d + 7 * B + 1;
+  d_id_from_ = d + 6 * B;
+  d_extra_at_ = d + 7 * B;
+  d_extra_ = d + 8 * B + 1;
+  staging_.resize(kStagingBlocks);
+  for (Staging& st : staging_) {
+    void* h = nullptr;
+    ck(mk_host_alloc(ctx_, layout_words_ * sizeof(int32_t), &h));
+    st.host = static_cast<int32_t*>(h);
+  }
   ck(mk_synchronize(ctx_));
 }
 
-Model::~Model() = default;
+Model::~Model() {
+  if (!staging_.empty()) (void)mk_synchronize(ctx_);
+  for (Staging& st : staging_) {
+    (void)mk_event_free(st.done);
+    (void)mk_host_free(ctx_, st.host);
+  }
+}
 
 mk_weight Model::weight(int layer, int which) const {
   if (which == 4) return output_.w();
@@ -297,88 +325,149 @@ mk_weight Model::weight(int layer, int which) const {
   return r;
 }
 
-void Model::check_ids(const int32_t* ids, int n) {
-  for (int t = 0; t < n; ++t)
-    if (ids[t] < 0 || ids[t] >= cfg_.n_vocab) throw std::runtime_error("forward: token id out of range");
+namespace {
+
+void reset_layout(TokenLayout& L, int n) {
+  L.n = n;
+  L.id.assign(n, 0);
+  L.rope_pos.assign(n, 0);
+  L.seq.assign(n, 0);
+  L.kv_row.assign(n, 0);
+  L.n_keys.assign(n, 0);
+  L.id_from.assign(n, -1);
+  L.logit_rows.clear();
+  L.tree = false;
+  L.extra_at.clear();
+  L.extra.clear();
 }
 
-// model.cpp:280-323 (batch validation and per-token layout)
-void Model::build_layout(const BatchToken* batch, int n) {
+}  // namespace
+
+// A multi-sequence batch (model.cpp:280-323 semantics; validation texts as there). A plain token (parent < 0)
+// writes KV row pos of its sequence and attends to rows 0..pos. A tree token writes row kv and attends to what its
+// parent attends to, then to its own row. Unrolled: follow the parent links up to the plain token the chain starts
+// from; the keys are that token's rows 0..pos, then the rows of the chain's tokens from just below it down to t.
+void Model::layout_batch(const BatchToken* batch, int n) {
   if (n <= 0 || n > kMaxBatch) throw std::runtime_error("forward: batch size out of range");
-  ids_.resize(n);
-  rpos_.resize(n);
-  seq_.resize(n);
-  kv_row_.resize(n);
-  n_keys_.resize(n);
-  out_.clear();
-  anc_.clear();
-  anc_off_.clear();
-  tree_ = false;
+  TokenLayout& L = lay_;
+  reset_layout(L, n);
   for (int t = 0; t < n; ++t) {
     const BatchToken& b = batch[t];
-    const int kv = b.parent < 0 ? b.pos : b.kv;
-    if (b.seq < 0 || b.seq >= n_seq_ || b.pos < 0 || b.pos >= n_ctx_ || kv < 0 || kv >= n_ctx_)
+    const bool child = b.parent >= 0;
+    const int row = child ? b.kv : b.pos;
+    if (b.seq < 0 || b.seq >= n_seq_ || b.pos < 0 || b.pos >= n_ctx_ || row < 0 || row >= n_ctx_)
       throw std::runtime_error("forward: bad slot");
-    if (b.parent >= t || (b.parent >= 0 && batch[b.parent].seq != b.seq))
-      throw std::runtime_error("forward: bad tree parent");
-    ids_[t] = b.id;
-    rpos_[t] = b.pos;
-    seq_[t] = b.seq;
-    kv_row_[t] = kv;
-    tree_ = tree_ || b.parent >= 0;
-    if (b.logits) out_.push_back(t);
+    if (b.parent >= t || (child && batch[b.parent].seq != b.seq)) throw std::runtime_error("forward: bad tree parent");
+    L.id[t] = b.id;
+    L.rope_pos[t] = b.pos;
+    L.seq[t] = b.seq;
+    L.kv_row[t] = row;
+    L.tree = L.tree || child;
+    if (b.logits) L.logit_rows.push_back(t);
   }
-  // Keys: plain tokens 0..pos; tree tokens the parent's keys (contiguous part, then its ancestor rows) plus their own
-  // row.
-  if (tree_) anc_off_.push_back(0);
+  std::vector<int32_t> chain;
   for (int t = 0; t < n; ++t) {
-    const BatchToken& b = batch[t];
-    if (b.parent < 0) {
-      n_keys_[t] = b.pos + 1;
-    } else {
-      n_keys_[t] = n_keys_[b.parent];
-      for (int i = anc_off_[b.parent]; i < anc_off_[b.parent + 1]; ++i) {
-        const int32_t row = anc_[i];
-        anc_.push_back(row);
-      }
-      anc_.push_back(kv_row_[t]);
+    int u = t;
+    chain.clear();
+    while (batch[u].parent >= 0) {  // parents precede their children, so this ends
+      chain.push_back(L.kv_row[u]);
+      u = batch[u].parent;
     }
-    if (tree_) anc_off_.push_back(static_cast<int32_t>(anc_.size()));
+    L.n_keys[t] = batch[u].pos + 1;
+    if (L.tree) {
+      L.extra_at.push_back(static_cast<int32_t>(L.extra.size()));
+      L.extra.insert(L.extra.end(), chain.rbegin(), chain.rend());
+    }
   }
-  check_ids(ids_.data(), n);
+  if (L.tree) L.extra_at.push_back(static_cast<int32_t>(L.extra.size()));
+  finish_layout();
 }
 
-void Model::upload_layout(int n) {
-  const int B = kMaxBatch;
-  if (anc_.size() > static_cast<size_t>(B) * (B + 1) / 2) throw std::runtime_error("forward: tree too deep");
-  int32_t* h = host_block_.data();
-  std::copy(ids_.begin(), ids_.end(), h);
-  std::copy(rpos_.begin(), rpos_.end(), h + B);
-  std::copy(seq_.begin(), seq_.end(), h + 2 * B);
-  std::copy(kv_row_.begin(), kv_row_.end(), h + 3 * B);
-  std::copy(n_keys_.begin(), n_keys_.end(), h + 4 * B);
-  std::copy(out_.begin(), out_.end(), h + 5 * B);
-  std::copy(anc_off_.begin(), anc_off_.end(), h + 6 * B);
-  std::copy(anc_.begin(), anc_.end(), h + 7 * B + 1);
-  max_keys_ = 1;
+// n consecutive tokens of one sequence at positions pos.. (model.cpp:249-278 semantics). With parent links (tree
+// verification) token t writes row pos + t, sits at RoPE position pos + depth(t), and attends to the prefix rows
+// 0..pos-1 and then to the rows of its ancestors from the root down to itself.
+void Model::layout_tokens(const int32_t* tokens, int n, int pos, bool all_logits, const int* parent, int seq) {
+  if (n <= 0 || n > kMaxBatch) throw std::runtime_error("forward: batch size out of range");
+  if (pos + n > n_ctx_) throw std::runtime_error("forward: context full");
+  if (seq < 0 || seq >= n_seq_) throw std::runtime_error("forward: bad sequence");
+  TokenLayout& L = lay_;
+  reset_layout(L, n);
+  L.tree = parent != nullptr;
+  std::vector<int32_t> depth(static_cast<size_t>(n), 0), chain;
   for (int t = 0; t < n; ++t) {
-    const int extra = tree_ ? anc_off_[t + 1] - anc_off_[t] : 0;
-    max_keys_ = std::max(max_keys_, n_keys_[t] + extra);
+    L.id[t] = tokens[t];
+    L.seq[t] = seq;
+    L.kv_row[t] = pos + t;
+    if (all_logits || t == n - 1) L.logit_rows.push_back(t);
+    if (!parent) {
+      L.rope_pos[t] = pos + t;
+      L.n_keys[t] = pos + t + 1;
+      continue;
+    }
+    if (parent[t] >= t) throw std::runtime_error("forward: bad tree parent");
+    depth[t] = parent[t] < 0 ? 0 : depth[parent[t]] + 1;
+    L.rope_pos[t] = pos + depth[t];
+    L.n_keys[t] = pos;
+    chain.clear();
+    for (int a = t; a >= 0; a = parent[a]) chain.push_back(pos + a);
+    L.extra_at.push_back(static_cast<int32_t>(L.extra.size()));
+    L.extra.insert(L.extra.end(), chain.rbegin(), chain.rend());
   }
-  // Every forward path (batch, tokens, generate) uploads through here: the flag always describes this batch.
-  distinct_seqs_ = true;
-  for (int t = 1; t < n && distinct_seqs_; ++t)
-    for (int u = 0; u < t; ++u)
-      if (seq_[u] == seq_[t]) {
-        distinct_seqs_ = false;
-        break;
-      }
-  const size_t words = 7 * static_cast<size_t>(B) + 1 + anc_.size();
-  ck(mk_upload(ctx_, layout_.p, h, words * sizeof(int32_t)));
+  if (L.tree) L.extra_at.push_back(static_cast<int32_t>(L.extra.size()));
+  finish_layout();
+}
+
+void Model::finish_layout() {
+  TokenLayout& L = lay_;
+  const size_t cap = static_cast<size_t>(kMaxBatch) * (kMaxBatch + 1) / 2;
+  if (L.extra.size() > cap) throw std::runtime_error("forward: tree too deep");
+  L.max_keys = 1;
+  for (int t = 0; t < L.n; ++t) {
+    const int extra = L.tree ? L.extra_at[t + 1] - L.extra_at[t] : 0;
+    L.max_keys = std::max(L.max_keys, L.n_keys[t] + extra);
+  }
+  std::vector<int32_t> seqs(L.seq);
+  std::sort(seqs.begin(), seqs.end());
+  L.distinct_seqs = std::adjacent_find(seqs.begin(), seqs.end()) == seqs.end();
+}
+
+void Model::check_ids() {
+  for (int t = 0; t < lay_.n; ++t)
+    if (lay_.id_from[t] < 0 && (lay_.id[t] < 0 || lay_.id[t] >= embd_count_))
+      throw std::runtime_error("forward: token id out of range");  // model.cpp:332
+}
+
+// Copies the layout to the device from the next pinned staging block, without waiting for the device unless that
+// block's previous copy is still pending; then, for tokens whose id is produced on the device, gathers those ids.
+void Model::upload_layout(const int32_t* dev_ids) {
+  check_ids();
+  const TokenLayout& L = lay_;
+  const size_t B = kMaxBatch;
+  Staging& st = staging_[next_staging_];
+  next_staging_ = (next_staging_ + 1) % staging_.size();
+  if (!mk_event_done(st.done)) ck(mk_event_wait(ctx_, st.done));
+  int32_t* h = st.host;
+  std::copy(L.id.begin(), L.id.end(), h);
+  std::copy(L.rope_pos.begin(), L.rope_pos.end(), h + B);
+  std::copy(L.seq.begin(), L.seq.end(), h + 2 * B);
+  std::copy(L.kv_row.begin(), L.kv_row.end(), h + 3 * B);
+  std::copy(L.n_keys.begin(), L.n_keys.end(), h + 4 * B);
+  std::copy(L.logit_rows.begin(), L.logit_rows.end(), h + 5 * B);
+  std::copy(L.id_from.begin(), L.id_from.end(), h + 6 * B);
+  size_t words = 7 * B;
+  if (L.tree) {
+    std::copy(L.extra_at.begin(), L.extra_at.end(), h + 7 * B);
+    std::copy(L.extra.begin(), L.extra.end(), h + 8 * B + 1);
+    words = 8 * B + 1 + L.extra.size();
+  }
+  ck(mk_copy_async(ctx_, layout_.p, h, words * sizeof(int32_t)));
+  ck(mk_event_record(ctx_, &st.done));
+  if (dev_ids) ck(mk_move_ids(ctx_, d_ids_, nullptr, dev_ids, d_id_from_, L.n));
 }
 
 // model.cpp:325-426 on the device.
-void Model::run(int n) {
+void Model::run() {
+  const int n = lay_.n;
   const auto& c = cfg_;
   const int E = c.n_embd, D = c.head_dim, H = c.n_head, KV = c.n_head_kv, F = c.n_ff;
   const int64_t QKV = static_cast<int64_t>(H + 2 * KV) * D;
@@ -387,8 +476,7 @@ void Model::run(int n) {
   float* att = att_.as<float>();
   float* gu = gu_.as<float>();
   void* xq = xq_.p;
-  const mk_kv_cache kv{kc_.as<int8_t>(), vc_.as<int8_t>(), ks_.as<float>(), vs_.as<float>(), c.n_layer, n_seq_, KV, D,
-                       n_ctx_};
+  const mk_kv_cache& kv = kv_;
   ck(mk_dequantize_rows(ctx_, embd_type_, embd_rows_.p, embd_row_bytes_, d_ids_, n, E, x));
   for (int il = 0; il < c.n_layer; ++il) {
     const Layer& L = layers_[il];
@@ -401,16 +489,16 @@ void Model::run(int n) {
     // Short plain batches of distinct sequences (decode steps): QK-norm, RoPE, the KV write and attention in one
     // launch; otherwise (prompt chunks, trees, shared sequences) the KV rows are written before any token attends.
     int rc = MK_ERR_UNSUPPORTED;
-    if (!tree_ && distinct_seqs_ && n < 16)
+    if (!lay_.tree && lay_.distinct_seqs && n < 16)
       rc = mk_attention_decode(ctx_, qkv, QKV, n, H, norms + 2 * E, norms + 2 * E + D, c.rms_eps,
                                rope_cos_.as<float>(), rope_sin_.as<float>(), d_rpos_, d_seq_, d_kv_row_, d_n_keys_,
-                               &kv, il, att, static_cast<int64_t>(H) * D, max_keys_);
+                               &kv, il, att, static_cast<int64_t>(H) * D, lay_.max_keys);
     if (rc == MK_ERR_UNSUPPORTED) {
       ck(mk_qk_norm_rope_kv(ctx_, qkv, qkv + static_cast<int64_t>(H) * D, qkv + static_cast<int64_t>(H + KV) * D, QKV,
                             n, H, norms + 2 * E, norms + 2 * E + D, c.rms_eps, rope_cos_.as<float>(),
                             rope_sin_.as<float>(), d_rpos_, d_seq_, d_kv_row_, &kv, il));
       ck(mk_attention(ctx_, qkv, QKV, att, static_cast<int64_t>(H) * D, n, H, &kv, il, d_seq_, d_n_keys_,
-                      tree_ ? d_anc_off_ : nullptr, d_anc_, max_keys_));
+                      lay_.tree ? d_extra_at_ : nullptr, d_extra_, lay_.max_keys));
     } else {
       ck(rc);
     }
@@ -439,7 +527,7 @@ void Model::run(int n) {
       ck(mk_matmul(ctx_, &wd, xq, n, x, E, 1));  // x += ffn_down(...) (model.cpp:412-416)
     }
   }
-  const int m = static_cast<int>(out_.size());
+  const int m = n_out();
   if (m == 0) return;
   ck(mk_rmsnorm_q8(ctx_, x, d_out_, output_norm_.as<float>(), m, E, c.rms_eps, xq));
   mk_weight wout = output_.w();
@@ -447,78 +535,60 @@ void Model::run(int n) {
   ck(mk_matmul(ctx_, &wout, xq, m, logits_.as<float>(), c.n_vocab, 0));
 }
 
+
 void Model::forward(const BatchToken* batch, int n, float* logits) {
-  build_layout(batch, n);
-  upload_layout(n);
-  run(n);
-  if (!out_.empty() && logits)
-    ck(mk_download(ctx_, logits, logits_.p, out_.size() * static_cast<size_t>(cfg_.n_vocab) * sizeof(float)));
-  ck(mk_synchronize(ctx_));
+  layout_batch(batch, n);
+  upload_layout();
+  run();
+  if (!lay_.logit_rows.empty() && logits)
+    ck(mk_download(ctx_, logits, logits_.p, lay_.logit_rows.size() * static_cast<size_t>(cfg_.n_vocab) * sizeof(float)));
+  else
+    ck(mk_synchronize(ctx_));
+}
+
+void Model::enqueue(const BatchToken* batch, int n, const int32_t* id_from, const int32_t* dev_ids, int32_t* dev_top1,
+                    int32_t* dev_top2) {
+  layout_batch(batch, n);
+  bool from_device = false;
+  if (id_from && dev_ids)
+    for (int t = 0; t < n; ++t)
+      if (id_from[t] >= 0) {
+        lay_.id_from[t] = id_from[t];
+        from_device = true;
+      }
+  upload_layout(from_device ? dev_ids : nullptr);
+  run();
+  const int m = n_out();
+  if (m > 0 && (dev_top1 || dev_top2)) {
+    int32_t* t1 = dev_top1 ? dev_top1 : top_.as<int32_t>();  // the runner-up scan still needs a top-1 output
+    ck(mk_argmax_top2(ctx_, logits_.as<float>(), m, cfg_.n_vocab, t1, dev_top2));
+  }
 }
 
 void Model::forward_top2(const BatchToken* batch, int n, int32_t* top1, int32_t* top2) {
-  build_layout(batch, n);
-  upload_layout(n);
-  run(n);
-  const int m = static_cast<int>(out_.size());
-  if (m > 0) {
-    int32_t* d1 = top_.as<int32_t>();
-    int32_t* d2 = d1 + kMaxBatch;
-    ck(mk_argmax_top2(ctx_, logits_.as<float>(), m, cfg_.n_vocab, d1, d2));
-    if (top1) ck(mk_download(ctx_, top1, d1, m * sizeof(int32_t)));
-    if (top2) ck(mk_download(ctx_, top2, d2, m * sizeof(int32_t)));
-  }
-  ck(mk_synchronize(ctx_));
+  int32_t* d1 = top_.as<int32_t>();
+  int32_t* d2 = d1 + kMaxBatch;
+  enqueue(batch, n, nullptr, nullptr, d1, top2 ? d2 : nullptr);
+  const int m = n_out();
+  if (m > 0 && top1) ck(mk_download(ctx_, top1, d1, m * sizeof(int32_t)));
+  if (m > 0 && top2) ck(mk_download(ctx_, top2, d2, m * sizeof(int32_t)));
+  if (m == 0 || (!top1 && !top2)) ck(mk_synchronize(ctx_));
 }
 
-// model.cpp:249-278
 void Model::forward(const int32_t* tokens, int n, int pos, float* logits, bool all_logits, const int* parent,
                     int seq) {
-  if (n <= 0 || n > kMaxBatch) throw std::runtime_error("forward: batch size out of range");
-  if (pos + n > n_ctx_) throw std::runtime_error("forward: context full");
-  if (seq < 0 || seq >= n_seq_) throw std::runtime_error("forward: bad sequence");
-  ids_.assign(tokens, tokens + n);
-  rpos_.resize(n);
-  seq_.assign(n, seq);
-  kv_row_.resize(n);
-  n_keys_.resize(n);
-  out_.clear();
-  anc_.clear();
-  anc_off_.clear();
-  tree_ = parent != nullptr;
-  if (parent) {  // tree: depth and ancestor KV positions (self included), root first
-    depth_.assign(n, 0);
-    for (int t = 0; t < n; ++t) {
-      depth_[t] = parent[t] < 0 ? 0 : depth_[parent[t]] + 1;
-      anc_off_.push_back(static_cast<int32_t>(anc_.size()));
-      const size_t start = anc_.size();
-      for (int a = t; a >= 0; a = parent[a]) anc_.push_back(pos + a);
-      std::reverse(anc_.begin() + static_cast<std::ptrdiff_t>(start), anc_.end());
-    }
-    anc_off_.push_back(static_cast<int32_t>(anc_.size()));
-  }
-  for (int t = 0; t < n; ++t) {
-    rpos_[t] = pos + (parent ? depth_[t] : t);
-    kv_row_[t] = pos + t;
-    n_keys_[t] = parent ? pos : pos + t + 1;  // tree: prefix only, ancestors come as extra rows
-    if (all_logits || t == n - 1) out_.push_back(t);
-  }
-  check_ids(ids_.data(), n);
-  upload_layout(n);
-  run(n);
+  layout_tokens(tokens, n, pos, all_logits, parent, seq);
+  upload_layout();
+  run();
   if (logits)
-    ck(mk_download(ctx_, logits, logits_.p, out_.size() * static_cast<size_t>(cfg_.n_vocab) * sizeof(float)));
-  ck(mk_synchronize(ctx_));
+    ck(mk_download(ctx_, logits, logits_.p, lay_.logit_rows.size() * static_cast<size_t>(cfg_.n_vocab) * sizeof(float)));
+  else
+    ck(mk_synchronize(ctx_));
 }
 
-// model.cpp:432-440
 void Model::move_kv(int from, int to, int seq) {
   if (from == to) return;
-  const auto& c = cfg_;
-  const mk_kv_cache kv{kc_.as<int8_t>(), vc_.as<int8_t>(), ks_.as<float>(), vs_.as<float>(), c.n_layer, n_seq_,
-                       c.n_head_kv, c.head_dim, n_ctx_};
-  ck(mk_move_kv(ctx_, &kv, seq, from, to));
-  ck(mk_synchronize(ctx_));
+  ck(mk_move_kv(ctx_, &kv_, seq, from, to));
 }
 
 void Model::kv_row(int layer, int seq, int pos, bool k, uint8_t* out) {
@@ -540,7 +610,6 @@ void Model::generate_greedy(const int32_t* prompt, int n_prompt, int n_gen, int 
                             bool use_graph) {
   if (n_prompt <= 0 || n_gen <= 0) throw std::invalid_argument("generate: empty prompt or no tokens");
   if (n_prompt + n_gen > n_ctx_) throw std::runtime_error("forward: context full");
-  check_ids(prompt, n_prompt);
   const int B = kMaxBatch;
   int32_t* d_top1 = top_.as<int32_t>();
   int32_t* d_tokens = top_.as<int32_t>() + B;  // generated ids (n_gen <= B per call segment below)
@@ -554,9 +623,9 @@ void Model::generate_greedy(const int32_t* prompt, int n_prompt, int n_gen, int 
     const int m = std::min(B, n_prompt - pos);
     batch.clear();
     for (int i = 0; i < m; ++i) batch.push_back({prompt[pos + i], seq, pos + i, pos + i + 1 == n_prompt});
-    build_layout(batch.data(), m);
-    upload_layout(m);
-    run(m);
+    layout_batch(batch.data(), m);
+    upload_layout();
+    run();
   }
   ck(mk_argmax_top2(ctx_, logits_.as<float>(), 1, cfg_.n_vocab, d_top1, nullptr));
   int32_t first = 0;
@@ -567,19 +636,17 @@ void Model::generate_greedy(const int32_t* prompt, int n_prompt, int n_gen, int 
 
   // Decode: one-token layout resident on the device; greedy_advance feeds each argmax back as the next input.
   batch.assign(1, BatchToken{first, seq, n_prompt, true});
-  build_layout(batch.data(), 1);
-  max_keys_ = n_prompt + n_gen;  // attention LDS sized for the last step
-  upload_layout(1);
-  max_keys_ = n_prompt + n_gen;
-  const int32_t zero = 0;
+  layout_batch(batch.data(), 1);
+  lay_.max_keys = n_prompt + n_gen;  // attention sized for the last step
+  upload_layout();
   const int steps = n_gen - 1;
   std::vector<int32_t> toks(steps);
   const auto t1 = Clock::now();
   for (int done = 0; done < steps;) {
     const int seg = std::min(B, steps - done);  // d_tokens holds B ids
-    ck(mk_upload(ctx_, d_counter, &zero, sizeof zero));
+    ck(mk_fill(ctx_, d_counter, 0, sizeof(int32_t)));
     auto step = [&] {
-      run(1);
+      run();
       ck(mk_argmax_top2(ctx_, logits_.as<float>(), 1, cfg_.n_vocab, d_top1, nullptr));
       ck(mk_greedy_advance(ctx_, d_top1, d_ids_, d_rpos_, d_kv_row_, d_n_keys_, d_tokens, d_counter));
     };
@@ -597,7 +664,7 @@ void Model::generate_greedy(const int32_t* prompt, int n_prompt, int n_gen, int 
       hck(hipStreamEndCapture(s, &g), "hipStreamEndCapture");
       hck(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0), "hipGraphInstantiate");
       for (int i = 0; i < seg; ++i) hck(hipGraphLaunch(ge, s), "hipGraphLaunch");
-      hck(hipStreamSynchronize(s), "hipStreamSynchronize");
+      ck(mk_synchronize(ctx_));
       (void)hipGraphExecDestroy(ge);
       (void)hipGraphDestroy(g);
     } else {

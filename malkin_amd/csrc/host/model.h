@@ -2,6 +2,10 @@
 // Same public API and semantics (BatchToken batches, plain / tree forwards, move_kv, the reference's error texts);
 // weights, KV cache, activations and the per-token layout live in HBM and every op is a gfx950 kernel behind the
 // C ABI of include/malkin_hip.h.
+//
+// Host waits: a forward that returns logits or picks to the host waits once for them; enqueue() and move_kv() only
+// queue work on the context's stream. Per-forward layouts travel from a ring of pinned host blocks by asynchronous
+// copies, so several forwards can be queued back to back (the engine's draft rounds).
 #pragma once
 
 #include <cstdint>
@@ -21,7 +25,8 @@ struct ModelConfig {  // model.h:11-16
   float rope_base = 10000.0f, rms_eps = 1e-6f;
 };
 
-ModelConfig read_config(const GgufFile& f);  // model.cpp:78-101
+// Hyperparameters from the GGUF metadata (the keys of model.cpp:78-101, same defaults and error texts).
+ModelConfig read_config(const GgufFile& f);
 
 // model.h:25-30
 struct BatchToken {
@@ -47,6 +52,21 @@ struct DevBuf {
   }
 };
 
+// What every kernel of one forward needs to know about its tokens. Built on the host from either forward form,
+// then copied to the device as one block.
+struct TokenLayout {
+  int n = 0;
+  std::vector<int32_t> id, rope_pos, seq, kv_row, n_keys;  // per token
+  std::vector<int32_t> id_from;  // per token: index into a device id array the token's id is read from, or -1
+  std::vector<int32_t> logit_rows;  // tokens whose logits are produced, in batch order
+  // Tree batches: token t attends to its n_keys[t] contiguous rows, then to rows extra[extra_at[t] .. extra_at[t+1]).
+  bool tree = false;
+  std::vector<int32_t> extra_at, extra;
+  // Derived: the longest key list, and whether no two tokens share a sequence.
+  int max_keys = 0;
+  bool distinct_seqs = false;
+};
+
 class Model {
  public:
   static constexpr int kMaxBatch = 256;  // model.h:35
@@ -58,20 +78,26 @@ class Model {
   const ModelConfig& cfg() const { return cfg_; }
   int n_ctx() const { return n_ctx_; }
   int n_seq() const { return n_seq_; }
+  mk_ctx* ctx() const { return ctx_; }
 
   // model.h:52 — logits: n_vocab floats per token with .logits set, in batch order (host memory).
   void forward(const BatchToken* batch, int n, float* logits);
   // model.h:58-59
   void forward(const int32_t* tokens, int n, int pos, float* logits, bool all_logits, const int* parent = nullptr,
                int seq = 0);
-  // model.h:61
+  // model.h:61. Queued on the stream (no wait): later forwards see the moved rows.
   void move_kv(int from, int to, int seq = 0);
 
   // Same forward, logits left in device memory; top1/top2 (host, may be null): per logits row, the first maximum
-  // and the reference's runner-up (sampler.cpp:27-30, engine.cpp:309-318).
+  // and the reference's runner-up (sampler.cpp:27-30, engine.cpp:309-318). Waits once.
   void forward_top2(const BatchToken* batch, int n, int32_t* top1, int32_t* top2);
+  // Queues the forward of `batch` without waiting. id_from (host, n entries, may be null): token t takes its id from
+  // dev_ids[id_from[t]] at run time when id_from[t] >= 0 (an id another queued kernel produces), else batch[t].id.
+  // The picks of the logits rows (in batch order) go to dev_top1 / dev_top2 (device; either may be null).
+  void enqueue(const BatchToken* batch, int n, const int32_t* id_from, const int32_t* dev_ids, int32_t* dev_top1,
+               int32_t* dev_top2);
   const float* dev_logits() const { return logits_.as<float>(); }
-  int n_out() const { return static_cast<int>(out_.size()); }
+  int n_out() const { return static_cast<int>(lay_.logit_rows.size()); }
 
   // Greedy generation of one sequence (the reference's `malkin bench` protocol, main.cpp:126-143): the prompt in
   // kMaxBatch-token forwards, then n_gen tokens, each from the argmax of the previous forward. The decode steps are
@@ -113,6 +139,11 @@ class Model {
     Group qkv, gateup;
     Weight wo, down;
   };
+  // One pinned host block per in-flight layout copy, reusable once its event has passed.
+  struct Staging {
+    int32_t* host = nullptr;
+    void* done = nullptr;  // event recorded after the copy that reads `host`
+  };
 
   void load_weight(const GgufFile& f, const std::vector<std::string>& names, Weight& w, bool interleave4 = false);
   void load_gateup(const GgufFile& f, const std::string& gate, const std::string& up, Group& g);
@@ -121,10 +152,14 @@ class Model {
   // The group from fp32 rows x (token stride xs) with rmsnorm (norm_w) / quantization inside each matmul; false when
   // a part has no fused kernel for n tokens (nothing launched then).
   bool matmul_group_f32(const Group& g, const float* x, int64_t xs, const float* norm_w, int n, float* y);
-  void build_layout(const BatchToken* batch, int n);
-  void upload_layout(int n);
-  void run(int n);  // device forward over the uploaded layout
-  void check_ids(const int32_t* ids, int n);
+
+  // Layout builders (validation with the reference's error texts), the asynchronous upload, and the layer loop.
+  void layout_batch(const BatchToken* batch, int n);
+  void layout_tokens(const int32_t* tokens, int n, int pos, bool all_logits, const int* parent, int seq);
+  void finish_layout();
+  void upload_layout(const int32_t* dev_ids = nullptr);
+  void run();
+  void check_ids();
 
   mk_ctx* ctx_;
   ModelConfig cfg_;
@@ -132,6 +167,7 @@ class Model {
   bool wide_;
   size_t weight_bytes_ = 0;
   int embd_type_ = 0;
+  int64_t embd_count_ = 0;  // token_embd rows (valid token ids)
   size_t embd_row_bytes_ = 0;
   DevBuf embd_rows_;  // token_embd in GGUF rows (lookup)
   Weight output_;     // LM head (packed token_embd when tied)
@@ -139,16 +175,16 @@ class Model {
   std::vector<Layer> layers_;
   DevBuf rope_cos_, rope_sin_;  // [n_ctx][D/2]
   DevBuf kc_, vc_, ks_, vs_;    // KV cache: [layer][seq][kv_head][n_ctx] rows of D int8 / one float
+  mk_kv_cache kv_{};
 
-  // Per-token layout (host copies + one device block).
-  std::vector<int32_t> ids_, rpos_, seq_, kv_row_, n_keys_, anc_off_, anc_, out_;
-  std::vector<int> depth_;
-  bool tree_ = false;
-  bool distinct_seqs_ = false;  // no two tokens of the batch share a sequence
-  int max_keys_ = 0;
-  std::vector<int32_t> host_block_;
+  TokenLayout lay_;
+  // Device layout block: ids rope_pos seq kv_row n_keys logit_rows id_from [B each], extra_at [B + 1],
+  // extra [B (B + 1) / 2].
   DevBuf layout_;
-  int32_t *d_ids_, *d_rpos_, *d_seq_, *d_kv_row_, *d_n_keys_, *d_anc_off_, *d_anc_, *d_out_;
+  size_t layout_words_ = 0;
+  int32_t *d_ids_, *d_rpos_, *d_seq_, *d_kv_row_, *d_n_keys_, *d_out_, *d_id_from_, *d_extra_at_, *d_extra_;
+  std::vector<Staging> staging_;
+  size_t next_staging_ = 0;
 
   // Activations for kMaxBatch tokens.
   DevBuf x_, qkv_, att_, gu_, xq_, logits_, top_;

@@ -1205,7 +1205,23 @@ __global__ void k_greedy_advance(const int32_t* top1, int32_t* ids, int32_t* rpo
   n_keys[0] += 1;
 }
 
+// dst[dst_idx[i]] = src[src_idx[i]] for i < n (identity where an index array is null; a negative index skips i).
+__global__ void k_move_ids(int32_t* __restrict__ dst, const int32_t* __restrict__ dst_idx,
+                           const int32_t* __restrict__ src, const int32_t* __restrict__ src_idx, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int d = dst_idx ? dst_idx[i] : i, s = src_idx ? src_idx[i] : i;
+  if (d >= 0 && s >= 0) dst[d] = src[s];
+}
+
 }  // namespace
+
+void move_ids(hipStream_t s, int32_t* dst, const int32_t* dst_idx, const int32_t* src, const int32_t* src_idx,
+              int n) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_move_ids, dim3((n + 255) / 256), dim3(256), 0, s, dst, dst_idx, src, src_idx, n);
+  check_launch("move_ids");
+}
 
 void greedy_advance(hipStream_t s, const int32_t* top1, int32_t* ids, int32_t* rpos, int32_t* kv_row, int32_t* n_keys,
                     int32_t* out_tokens, int32_t* counter) {

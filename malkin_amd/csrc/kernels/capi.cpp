@@ -1,6 +1,7 @@
 // extern "C" layer of include/malkin_hip.h over the internal launchers.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -14,7 +15,10 @@ namespace mk {
 
 namespace {
 thread_local char g_err[512] = "";
+std::atomic<uint64_t> g_host_waits{0};
 }
+
+void count_host_wait() { g_host_waits.fetch_add(1, std::memory_order_relaxed); }
 
 void set_error(const char* fmt, ...) {
   va_list ap;
@@ -78,8 +82,13 @@ int mk_destroy(mk_ctx* c) {
 const char* mk_device_name(const mk_ctx* c) { return c ? c->name : ""; }
 
 int mk_synchronize(mk_ctx* c) {
-  return guard([&] { check(hipStreamSynchronize(c->stream), "hipStreamSynchronize"); });
+  return guard([&] {
+    mk::count_host_wait();
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  });
 }
+
+uint64_t mk_host_waits(void) { return mk::g_host_waits.load(std::memory_order_relaxed); }
 
 void* mk_stream(mk_ctx* c) { return c ? c->stream : nullptr; }
 
@@ -95,6 +104,7 @@ int mk_free(mk_ctx* c, void* dev) {
   return guard([&] {
     if (!dev) return;
     check(hipSetDevice(c->device), "hipSetDevice");
+    mk::count_host_wait();
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     check(hipFree(dev), "hipFree");
   });
@@ -104,6 +114,7 @@ int mk_upload(mk_ctx* c, void* dst, const void* src, size_t bytes) {
   return guard([&] {
     if (!bytes) return;
     check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream), "hipMemcpy H2D");
+    mk::count_host_wait();
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
   });
 }
@@ -112,7 +123,64 @@ int mk_download(mk_ctx* c, void* dst, const void* src, size_t bytes) {
   return guard([&] {
     if (!bytes) return;
     check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream), "hipMemcpy D2H");
+    mk::count_host_wait();
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  });
+}
+
+int mk_host_alloc(mk_ctx* c, size_t bytes, void** host) {
+  return guard([&] {
+    require(host != nullptr, "mk_host_alloc: null output");
+    check(hipSetDevice(c->device), "hipSetDevice");
+    check(hipHostMalloc(host, bytes ? bytes : 1, hipHostMallocDefault), "hipHostMalloc");
+  });
+}
+
+int mk_host_free(mk_ctx* c, void* host) {
+  return guard([&] {
+    if (!host) return;
+    check(hipSetDevice(c->device), "hipSetDevice");
+    mk::count_host_wait();
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    check(hipHostFree(host), "hipHostFree");
+  });
+}
+
+int mk_copy_async(mk_ctx* c, void* dst, const void* src, size_t bytes) {
+  return guard([&] {
+    if (!bytes) return;
+    check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, c->stream), "hipMemcpyAsync");
+  });
+}
+
+int mk_event_record(mk_ctx* c, void** event) {
+  return guard([&] {
+    require(event != nullptr, "mk_event_record: null event");
+    if (!*event) {
+      hipEvent_t e = nullptr;
+      check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate");
+      *event = e;
+    }
+    check(hipEventRecord(static_cast<hipEvent_t>(*event), c->stream), "hipEventRecord");
+  });
+}
+
+int mk_event_done(void* event) {
+  if (!event) return 1;
+  return hipEventQuery(static_cast<hipEvent_t>(event)) == hipSuccess ? 1 : 0;
+}
+
+int mk_event_wait(mk_ctx*, void* event) {
+  return guard([&] {
+    if (!event) return;
+    mk::count_host_wait();
+    check(hipEventSynchronize(static_cast<hipEvent_t>(event)), "hipEventSynchronize");
+  });
+}
+
+int mk_event_free(void* event) {
+  return guard([&] {
+    if (event) check(hipEventDestroy(static_cast<hipEvent_t>(event)), "hipEventDestroy");
   });
 }
 
@@ -127,6 +195,7 @@ int mk_timer_start(mk_ctx* c) {
 int mk_timer_stop(mk_ctx* c, float* ms) {
   return guard([&] {
     check(hipEventRecord(c->ev1, c->stream), "hipEventRecord");
+    mk::count_host_wait();
     check(hipEventSynchronize(c->ev1), "hipEventSynchronize");
     check(hipEventElapsedTime(ms, c->ev0, c->ev1), "hipEventElapsedTime");
   });
@@ -269,6 +338,11 @@ int mk_move_kv(mk_ctx* c, const mk_kv_cache* kv, int seq, int from, int to) {
     mk::move_kv_rows(c->stream, kv->k, kv->v, kv->k_scale, kv->v_scale, kv->n_layer, kv->n_seq, kv->n_head_kv,
                      kv->head_dim, kv->n_ctx, seq, from, to);
   });
+}
+
+int mk_move_ids(mk_ctx* c, int32_t* dst, const int32_t* dst_index, const int32_t* src, const int32_t* src_index,
+                int n) {
+  return guard([&] { mk::move_ids(c->stream, dst, dst_index, src, src_index, n); });
 }
 
 int mk_greedy_advance(mk_ctx* c, const int32_t* top1, int32_t* ids, int32_t* rpos, int32_t* kv_row, int32_t* n_keys,

@@ -24,6 +24,8 @@ struct mk_ctx {
 namespace mk {
 
 void set_error(const char* fmt, ...);
+// Counts one host wait on the device (a stream or event synchronization), for mk_host_waits().
+void count_host_wait();
 // Records the HIP error and returns MK_ERR_HIP.
 int hip_fail(hipError_t e, const char* what);
 

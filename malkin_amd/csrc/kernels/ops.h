@@ -134,6 +134,9 @@ void argmax_top2_noalloc(hipStream_t s, const float* logits, int rows, int n_voc
 void argmax_top2(hipStream_t s, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2,
                  void* scratch, size_t scratch_bytes);
 
+// dst[dst_idx[i]] = src[src_idx[i]], i < n; null index arrays are the identity, negative indices skip.
+void move_ids(hipStream_t s, int32_t* dst, const int32_t* dst_idx, const int32_t* src, const int32_t* src_idx,
+              int n);
 void greedy_advance(hipStream_t s, const int32_t* top1, int32_t* ids, int32_t* rpos, int32_t* kv_row, int32_t* n_keys,
                     int32_t* out_tokens, int32_t* counter);
 

@@ -101,3 +101,29 @@ def test_engine_eog_and_errors(mk, model_files):
     assert info["finish"] == 0 and info["completion_tokens"] == 64 - 60
     eng.close()
     target.close()
+
+
+@pytest.mark.parametrize("draft_name", [None, "tiny", "tiny-q4km"])
+def test_engine_one_host_wait_per_step(mk, model_files, draft_name):
+    """The step's draft rounds, tree layout, acceptance moves and next prompt chunks run without the host waiting in
+    between: the library's host waits (stream / event synchronizations) equal the engine's steps."""
+    path = model_files["tiny"]
+    target = mk_.Model(mk, path, 160, 3)
+    draft = mk_.Model(mk, model_files[draft_name], 160, 3) if draft_name else None
+    V = target.cfg["n_vocab"]
+    ps = prompts(np.random.default_rng(13), V, [9, 50, 21])
+    eng = mk_.Engine(target, draft, n_draft=8)
+    ids = [eng.submit(p, max_tokens=24) for p in ps]
+    mk.sync()
+    w0, s0 = mk_.host_waits(), eng.steps
+    eng.run()
+    waits, steps = mk_.host_waits() - w0, eng.steps - s0
+    print("draft", draft_name, "steps", steps, "host waits", waits, flush=True)
+    assert steps > 0 and waits == steps
+    for rid, p in zip(ids, ps):
+        toks, _ = eng.result(rid)
+        assert list(toks) == plain(mk, path, p, 24), (draft_name, rid)
+    eng.close()
+    if draft:
+        draft.close()
+    target.close()
