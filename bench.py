@@ -247,6 +247,28 @@ def traffic_probe():
     ctx.close()
 
 
+def gemm_probe():
+    """Launch sequence for the prefill GEMM's counters (rocprofv3 --pmc): config 1 (Q8_0 9728x2560, n = 512) 8 times,
+    then the Qwen3-8B prompt-chunk shapes of pp512 at n = 256 (q|k|v 6144x4096, attn_output 4096x4096, gate|up
+    24576x4096, down 4096x12288) 4 times each, from BlockQ8 activations."""
+    import malkin_amd as mk
+    ctx = mk.Context(0)
+    rng = np.random.default_rng(5)
+    for rows, cols, n, reps in ((9728, 2560, 512, 8), (6144, 4096, 256, 4), (4096, 4096, 256, 4),
+                                (24576, 4096, 256, 4), (4096, 12288, 256, 4)):
+        ws = pack_copies(ctx, mk.Q8_0, random_weight(rng, mk.Q8_0, rows, cols), rows, cols, 1)
+        xq, y = random_acts(ctx, rng, n, cols), ctx.alloc(n * rows * 4)
+        ctx.sync()
+        sec = time_matmuls(ctx, ws, xq, n, y, reps)
+        log(f"[probe] k_gemm_q8_0 {rows}x{cols} n={n}: {reps} launches, {sec * 1e6:.2f} us each, "
+            f"{2.0 * n * rows * cols / sec / 1e12:.1f} TOPS")
+        for b, _w in ws:
+            b.free()
+        xq.free()
+        y.free()
+    ctx.close()
+
+
 def roofline_traffic():
     """HBM bytes per launch of the roofline kernel, from the committed counter summary (profiles/), or None."""
     f = os.path.join(ROOT, "profiles", "k_gemv_q8_0_decode_n1_hbm_traffic.md")
@@ -453,11 +475,15 @@ def main():
     ap.add_argument("--no-engine-configs", action="store_true",
                     help="skip BASELINE configs 3 (Qwen3-4B pp512 + tg128), 4 (continuous batching) and 5 "
                          "(speculative tree verification)")
-    ap.add_argument("--probe", choices=["traffic"],
-                    help="only run the launch sequence for the roofline kernel's HBM counters")
+    ap.add_argument("--probe", choices=["traffic", "gemm"],
+                    help="only run a launch sequence for counter profiles: the roofline kernel's HBM traffic, or "
+                         "the prefill GEMM (config 1 and the pp512 chunk shapes)")
     args = ap.parse_args()
     if args.probe == "traffic":
         traffic_probe()
+        return
+    if args.probe == "gemm":
+        gemm_probe()
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus})",

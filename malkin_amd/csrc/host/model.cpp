@@ -269,14 +269,14 @@ Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide)
   ck(mk_fill(ctx_, ks_.p, 0, ks_.bytes));
   ck(mk_fill(ctx_, vs_.p, 0, vs_.bytes));
 
-  const size_t B = kMaxBatch;
+  const size_t B = kMaxBatch, T = kDevBatch;
   const size_t qkv_rows = static_cast<size_t>(H + 2 * KV) * D;
   const size_t kmax = std::max({static_cast<size_t>(E), static_cast<size_t>(H) * D, static_cast<size_t>(F)});
-  x_ = DevBuf(ctx_, B * E * sizeof(float));
-  qkv_ = DevBuf(ctx_, B * qkv_rows * sizeof(float));
-  att_ = DevBuf(ctx_, B * H * D * sizeof(float));
-  gu_ = DevBuf(ctx_, B * 2 * F * sizeof(float));
-  xq_ = DevBuf(ctx_, B * (kmax / 32) * 40);
+  x_ = DevBuf(ctx_, T * E * sizeof(float));
+  qkv_ = DevBuf(ctx_, T * qkv_rows * sizeof(float));
+  att_ = DevBuf(ctx_, T * H * D * sizeof(float));
+  gu_ = DevBuf(ctx_, T * 2 * F * sizeof(float));
+  xq_ = DevBuf(ctx_, T * (kmax / 32) * 40);
   logits_ = DevBuf(ctx_, B * static_cast<size_t>(c.n_vocab) * sizeof(float));
   top_ = DevBuf(ctx_, 2 * B * sizeof(int32_t) + 2 * sizeof(int32_t));
 
@@ -284,18 +284,18 @@ Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide)
                     n_ctx_};
 
   // Layout block (see model.h) and its pinned staging ring.
-  layout_words_ = 7 * B + (B + 1) + B * (B + 1) / 2;
+  layout_words_ = 7 * T + (B + 1) + B * (B + 1) / 2;
   layout_ = DevBuf(ctx_, layout_words_ * sizeof(int32_t));
   int32_t* d = layout_.as<int32_t>();
   d_ids_ = d;
-  d_rpos_ = d + B;
-  d_seq_ = d + 2 * B;
-  d_kv_row_ = d + 3 * B;
-  d_n_keys_ = d + 4 * B;
-  d_out_ = d + 5 * B;
-  d_id_from_ = d + 6 * B;
-  d_extra_at_ = d + 7 * B;
-  d_extra_ = d + 8 * B + 1;
+  d_rpos_ = d + T;
+  d_seq_ = d + 2 * T;
+  d_kv_row_ = d + 3 * T;
+  d_n_keys_ = d + 4 * T;
+  d_out_ = d + 5 * T;
+  d_id_from_ = d + 6 * T;
+  d_extra_at_ = d + 7 * T;
+  d_extra_ = d + 7 * T + B + 1;
   staging_.resize(kStagingBlocks);
   for (Staging& st : staging_) {
     void* h = nullptr;
@@ -347,8 +347,8 @@ void reset_layout(TokenLayout& L, int n) {
 // writes KV row pos of its sequence and attends to rows 0..pos. A tree token writes row kv and attends to what its
 // parent attends to, then to its own row. Unrolled: follow the parent links up to the plain token the chain starts
 // from; the keys are that token's rows 0..pos, then the rows of the chain's tokens from just below it down to t.
-void Model::layout_batch(const BatchToken* batch, int n) {
-  if (n <= 0 || n > kMaxBatch) throw std::runtime_error("forward: batch size out of range");
+void Model::layout_batch(const BatchToken* batch, int n, int limit) {
+  if (n <= 0 || n > limit) throw std::runtime_error("forward: batch size out of range");
   TokenLayout& L = lay_;
   reset_layout(L, n);
   for (int t = 0; t < n; ++t) {
@@ -380,6 +380,7 @@ void Model::layout_batch(const BatchToken* batch, int n) {
     }
   }
   if (L.tree) L.extra_at.push_back(static_cast<int32_t>(L.extra.size()));
+  if (L.tree && n > kMaxBatch) throw std::runtime_error("forward: tree too deep");
   finish_layout();
 }
 
@@ -442,23 +443,24 @@ void Model::check_ids() {
 void Model::upload_layout(const int32_t* dev_ids) {
   check_ids();
   const TokenLayout& L = lay_;
-  const size_t B = kMaxBatch;
+  const size_t T = kDevBatch, B = kMaxBatch;
+  if (L.logit_rows.size() > B) throw std::runtime_error("forward: more than 256 logits rows");
   Staging& st = staging_[next_staging_];
   next_staging_ = (next_staging_ + 1) % staging_.size();
   if (!mk_event_done(st.done)) ck(mk_event_wait(ctx_, st.done));
   int32_t* h = st.host;
   std::copy(L.id.begin(), L.id.end(), h);
-  std::copy(L.rope_pos.begin(), L.rope_pos.end(), h + B);
-  std::copy(L.seq.begin(), L.seq.end(), h + 2 * B);
-  std::copy(L.kv_row.begin(), L.kv_row.end(), h + 3 * B);
-  std::copy(L.n_keys.begin(), L.n_keys.end(), h + 4 * B);
-  std::copy(L.logit_rows.begin(), L.logit_rows.end(), h + 5 * B);
-  std::copy(L.id_from.begin(), L.id_from.end(), h + 6 * B);
-  size_t words = 7 * B;
+  std::copy(L.rope_pos.begin(), L.rope_pos.end(), h + T);
+  std::copy(L.seq.begin(), L.seq.end(), h + 2 * T);
+  std::copy(L.kv_row.begin(), L.kv_row.end(), h + 3 * T);
+  std::copy(L.n_keys.begin(), L.n_keys.end(), h + 4 * T);
+  std::copy(L.logit_rows.begin(), L.logit_rows.end(), h + 5 * T);
+  std::copy(L.id_from.begin(), L.id_from.end(), h + 6 * T);
+  size_t words = 7 * T;
   if (L.tree) {
-    std::copy(L.extra_at.begin(), L.extra_at.end(), h + 7 * B);
-    std::copy(L.extra.begin(), L.extra.end(), h + 8 * B + 1);
-    words = 8 * B + 1 + L.extra.size();
+    std::copy(L.extra_at.begin(), L.extra_at.end(), h + 7 * T);
+    std::copy(L.extra.begin(), L.extra.end(), h + 7 * T + B + 1);
+    words = 7 * T + B + 1 + L.extra.size();
   }
   ck(mk_copy_async(ctx_, layout_.p, h, words * sizeof(int32_t)));
   ck(mk_event_record(ctx_, &st.done));
@@ -617,13 +619,14 @@ void Model::generate_greedy(const int32_t* prompt, int n_prompt, int n_gen, int 
   std::vector<BatchToken> batch;
   hipStream_t s = static_cast<hipStream_t>(mk_stream(ctx_));
 
-  // Prefill: the reference's engine evaluates prompts in kMaxBatch-token forwards (engine.cpp:381-393).
+  // Prefill in kDevBatch-token forwards (the reference's engine takes 256 per forward, engine.cpp:381-393; the
+  // per-token results are the same either way).
   const auto t0 = Clock::now();
-  for (int pos = 0; pos < n_prompt; pos += B) {
-    const int m = std::min(B, n_prompt - pos);
+  for (int pos = 0; pos < n_prompt; pos += kDevBatch) {
+    const int m = std::min(kDevBatch, n_prompt - pos);
     batch.clear();
     for (int i = 0; i < m; ++i) batch.push_back({prompt[pos + i], seq, pos + i, pos + i + 1 == n_prompt});
-    layout_batch(batch.data(), m);
+    layout_batch(batch.data(), m, kDevBatch);
     upload_layout();
     run();
   }

@@ -69,7 +69,10 @@ struct TokenLayout {
 
 class Model {
  public:
-  static constexpr int kMaxBatch = 256;  // model.h:35
+  static constexpr int kMaxBatch = 256;  // model.h:35: tokens per forward through the public API
+  // Tokens per device forward of a prompt inside generate_greedy: per-token results do not depend on how the
+  // prompt is split, and 512-token forwards give the prefill GEMMs twice the workgroups of 256-token ones.
+  static constexpr int kDevBatch = 512;
 
   // wide: the reference's wide Q6_K prefill panels are packed (Engine packs them when RAM allows,
   // engine.cpp:130-145); MALKIN_NO_WIDE turns them off there.
@@ -154,7 +157,7 @@ class Model {
   bool matmul_group_f32(const Group& g, const float* x, int64_t xs, const float* norm_w, int n, float* y);
 
   // Layout builders (validation with the reference's error texts), the asynchronous upload, and the layer loop.
-  void layout_batch(const BatchToken* batch, int n);
+  void layout_batch(const BatchToken* batch, int n, int limit = kMaxBatch);
   void layout_tokens(const int32_t* tokens, int n, int pos, bool all_logits, const int* parent, int seq);
   void finish_layout();
   void upload_layout(const int32_t* dev_ids = nullptr);
@@ -178,8 +181,8 @@ class Model {
   mk_kv_cache kv_{};
 
   TokenLayout lay_;
-  // Device layout block: ids rope_pos seq kv_row n_keys logit_rows id_from [B each], extra_at [B + 1],
-  // extra [B (B + 1) / 2].
+  // Device layout block: ids rope_pos seq kv_row n_keys logit_rows id_from [kDevBatch each], extra_at [B + 1],
+  // extra [B (B + 1) / 2] with B = kMaxBatch (tree batches come through the public API only).
   DevBuf layout_;
   size_t layout_words_ = 0;
   int32_t *d_ids_, *d_rpos_, *d_seq_, *d_kv_row_, *d_n_keys_, *d_out_, *d_id_from_, *d_extra_at_, *d_extra_;
