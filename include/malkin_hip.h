@@ -30,8 +30,9 @@ enum {
   MK_ERR_NO_DEVICE = 4
 };
 
-/* ggml tensor types (gguf.h:12-29) accepted by the kernels. */
-enum { MK_F32 = 0, MK_Q8_0 = 8, MK_Q4_K = 12, MK_Q6_K = 14 };
+/* ggml tensor types (gguf.h:12-29) accepted by the kernels. F16 / BF16 / Q5_K: row path (mk_matmul_rows) and
+   embedding lookup. */
+enum { MK_F32 = 0, MK_F16 = 1, MK_Q8_0 = 8, MK_Q4_K = 12, MK_Q5_K = 13, MK_Q6_K = 14, MK_BF16 = 30 };
 
 typedef struct mk_ctx mk_ctx;
 
@@ -79,6 +80,11 @@ size_t mk_packed_bytes(int type, int64_t rows, int64_t cols);
 /* src_dev: rows of GGUF blocks, src_row_bytes apart. dst_dev: mk_packed_bytes bytes. */
 int mk_pack_weight(mk_ctx* ctx, int type, const void* src_dev, size_t src_row_bytes, int64_t rows, int64_t cols,
                    void* dst_dev);
+/* mk_pack_weight for rows row0 .. row0 + n_rows of a rows x cols weight, src_dev holding only those rows (a chunk of a
+   weight streamed from the file): row0 a multiple of 8, n_rows too unless the chunk ends the weight. Chunks packed in
+   any order fill the same buffer mk_pack_weight fills. */
+int mk_pack_weight_rows(mk_ctx* ctx, int type, const void* src_dev, size_t src_row_bytes, int64_t row0, int64_t n_rows,
+                        int64_t rows, int64_t cols, void* dst_dev);
 /* Inverse of mk_pack_weight: GGUF rows, ggml_row_size(type, cols) bytes apart (pack round-trip tests). */
 int mk_unpack_weight(mk_ctx* ctx, int type, const void* packed_dev, int64_t rows, int64_t cols, void* dst_dev);
 
@@ -114,12 +120,25 @@ int mk_matmul(mk_ctx* ctx, const mk_weight* w, const void* xq, int n, float* y, 
 int mk_matmul_f32(mk_ctx* ctx, const mk_weight* w, const float* x, int64_t x_stride, const float* norm_w, float eps,
                   int n, float* y, int64_t y_stride, int accumulate, int silu_pairs);
 
+/* matmul's row path (quant.cpp:171-191 vec_dot, 330-351 matmul; kernels_avx512.cpp:82-171): y[t * y_stride + r]
+   (+)= vec_dot(row r, token t) over a weight kept as GGUF rows (row_bytes apart, not repacked). The reference takes
+   this path for F32 / F16 / BF16 weights and, under MALKIN_NO_PACK, for Q8_0 / Q4_K / Q5_K / Q6_K; its arithmetic
+   differs from the panel kernels', and the results here are bit-identical to it. x: fp32 activations (x_stride
+   apart), read by F32 / F16 / BF16; xq: their BlockQ8 rows, read by the quantized types. */
+int mk_matmul_rows(mk_ctx* ctx, int type, const void* w, size_t row_bytes, int64_t rows, int64_t cols, const float* x,
+                   int64_t x_stride, const void* xq, int n, float* y, int64_t y_stride, int accumulate);
+
 /* ---- elementwise (model.cpp:46-49, kernels.h:39) ---- */
 /* y = rmsnorm(x) * w per row of n floats (model.cpp:46-49). */
 int mk_rmsnorm(mk_ctx* ctx, const float* x, const float* w, int rows, int n, float eps, float* y);
 /* rmsnorm of rows x[rows_idx[i]] (all rows when rows_idx is NULL) quantized straight to BlockQ8 [rows][n/32]. */
 int mk_rmsnorm_q8(mk_ctx* ctx, const float* x, const int32_t* rows_idx, const float* w, int rows, int n, float eps,
                   void* xq);
+/* y[i] = rmsnorm(x[rows_idx[i]]) * w (all rows in order when rows_idx is NULL), fp32 (model.cpp:46-49, 419-421). */
+int mk_rmsnorm_rows(mk_ctx* ctx, const float* x, const int32_t* rows_idx, const float* w, int rows, int n, float eps,
+                    float* y);
+/* Rows [gate | up] (2n floats apart): gate = silu(gate) * up in place (kern::silu_mul per token, model.cpp:409). */
+int mk_silu_mul_rows(mk_ctx* ctx, float* gu, int rows, int64_t n);
 /* g = g / (1 + e^-g) * u (kern::silu_mul, kernels.h:39). */
 int mk_silu_mul(mk_ctx* ctx, int64_t n, float* g, const float* u);
 /* silu_mul of rows of gu (2n floats per row) quantized to BlockQ8 [rows][n/32] (model.cpp:409-411). gu rows are

@@ -44,10 +44,14 @@ typedef struct {
 } mk_model_config;
 
 enum {
-  MK_MODEL_NO_WIDE = 1 /* no wide Q6_K prefill panels (the reference's MALKIN_NO_WIDE, model.cpp:181) */
+  MK_MODEL_NO_WIDE = 1, /* no wide Q6_K prefill panels (the reference's MALKIN_NO_WIDE, model.cpp:181) */
+  MK_MODEL_NO_PACK = 2  /* no packed weights: every matmul on the row path over GGUF rows (MALKIN_NO_PACK,
+                           model.cpp:136; quant.cpp:330-351). F32 / F16 / BF16 weights take that path anyway. */
 };
 
-/* Model::Model(GgufFile, n_ctx, n_seq) (model.h:38) + Model::pack_wide (model.h:43) unless MK_MODEL_NO_WIDE. */
+/* Model::Model(GgufFile, n_ctx, n_seq) (model.h:38) + Model::pack_wide (model.h:43) unless MK_MODEL_NO_WIDE. Weights
+   stream from the file to HBM in chunks through pinned staging, each chunk packed on the device while the next is
+   copied (the reference packs its panels on the host, quant.cpp:212-235, model.cpp:163-178). */
 int mk_model_open(mk_ctx* ctx, const char* gguf_path, int n_ctx, int n_seq, int flags, mk_model** out);
 int mk_model_free(mk_model* m);
 int mk_model_get_config(const mk_model* m, mk_model_config* out);

@@ -12,8 +12,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmalkin_hip.so")
 
 MK_OK, MK_ERR_INVALID, MK_ERR_HIP, MK_ERR_UNSUPPORTED, MK_ERR_NO_DEVICE = 0, 1, 2, 3, 4
-F32, Q8_0, Q4_K, Q6_K = 0, 8, 12, 14
-MODEL_NO_WIDE = 1
+F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 8, 12, 13, 14, 30
+MODEL_NO_WIDE, MODEL_NO_PACK = 1, 2
 
 BLOCK_Q8 = np.dtype([("d", "<f4"), ("s", "<i2", (2,)), ("qs", "i1", (32,))])
 BATCH_TOKEN = np.dtype([("id", "<i4"), ("seq", "<i4"), ("pos", "<i4"), ("logits", "<i4"), ("kv", "<i4"),
@@ -42,6 +42,7 @@ SIGNATURES = {
     "mk_timer_stop": (_I, [_P, ctypes.POINTER(_F)]),
     "mk_packed_bytes": (_SZ, [_I, _I64, _I64]),
     "mk_pack_weight": (_I, [_P, _I, _P, _SZ, _I64, _I64, _P]),
+    "mk_pack_weight_rows": (_I, [_P, _I, _P, _SZ, _I64, _I64, _I64, _I64, _P]),
     "mk_unpack_weight": (_I, [_P, _I, _P, _I64, _I64, _P]),
     "mk_quantize_q8": (_I, [_P, _P, _I, _I64, _P]),
     "mk_quantize_i8": (_I, [_P, _P, _I, _I, _P, _P]),
@@ -51,6 +52,9 @@ SIGNATURES = {
     "mk_rmsnorm": (_I, [_P, _P, _P, _I, _I, _F, _P]),
     "mk_rmsnorm_q8": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),
     "mk_silu_mul": (_I, [_P, _I64, _P, _P]),
+    "mk_rmsnorm_rows": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),
+    "mk_silu_mul_rows": (_I, [_P, _P, _I, _I64]),
+    "mk_matmul_rows": (_I, [_P, _I, _P, _SZ, _I64, _I64, _P, _I64, _P, _I, _P, _I64, _I]),
     "mk_silu_mul_q8": (_I, [_P, _P, _I, _I64, _I, _P]),
     "mk_add": (_I, [_P, _I64, _P, _P]),
     "mk_attend_gqa": (_I, [_P, _P, _I, _I, _P, _P, _SZ, ctypes.c_ssize_t, _I, _F, _P, _P, _I]),
@@ -239,11 +243,11 @@ def gguf_inspect(path):
 class Model:
     """mk_model_* wrapper: the device counterpart of the reference's Model (model.h)."""
 
-    def __init__(self, ctx, path, n_ctx, n_seq=1, wide=True):
+    def __init__(self, ctx, path, n_ctx, n_seq=1, wide=True, no_pack=False):
         self.ctx = ctx
         p = _P()
-        check(load().mk_model_open(ctx.h, path.encode(), n_ctx, n_seq, 0 if wide else MODEL_NO_WIDE,
-                                   ctypes.byref(p)))
+        flags = (0 if wide else MODEL_NO_WIDE) | (MODEL_NO_PACK if no_pack else 0)
+        check(load().mk_model_open(ctx.h, path.encode(), n_ctx, n_seq, flags, ctypes.byref(p)))
         self.h = p.value
         c = MkModelConfig()
         check(load().mk_model_get_config(self.h, ctypes.byref(c)))

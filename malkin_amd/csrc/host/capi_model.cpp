@@ -66,7 +66,8 @@ int mk_model_open(mk_ctx* ctx, const char* path, int n_ctx, int n_seq, int flags
     if (!ctx || !path || !out) throw std::invalid_argument("mk_model_open: null argument");
     auto m = std::make_unique<mk_model>();
     m->file = std::make_unique<malkin_hip::GgufFile>(path);
-    m->model = std::make_unique<malkin_hip::Model>(ctx, *m->file, n_ctx, n_seq, (flags & MK_MODEL_NO_WIDE) == 0);
+    m->model = std::make_unique<malkin_hip::Model>(ctx, *m->file, n_ctx, n_seq, (flags & MK_MODEL_NO_WIDE) == 0,
+                                                    (flags & MK_MODEL_NO_PACK) != 0);
     *out = m.release();
   });
 }

@@ -22,7 +22,14 @@ void hck(hipError_t e, const char* what) {
   if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
 }
 
+// Types with packed (CDNA layout) kernels; types the row path takes; types only the row path takes.
 bool device_type(uint32_t t) { return t == MK_Q8_0 || t == MK_Q4_K || t == MK_Q6_K; }
+bool row_type(uint32_t t) {
+  return t == MK_F32 || t == MK_F16 || t == MK_BF16 || t == MK_Q8_0 || t == MK_Q4_K || t == MK_Q5_K || t == MK_Q6_K;
+}
+bool raw_only_type(uint32_t t) { return t == MK_F32 || t == MK_F16 || t == MK_BF16; }
+
+constexpr size_t kLoadChunkBytes = 32u << 20;  // rows per streamed chunk: about 32 MiB
 
 using Clock = std::chrono::steady_clock;
 double ms_since(Clock::time_point t) { return std::chrono::duration<double, std::milli>(Clock::now() - t).count(); }
@@ -82,16 +89,20 @@ ModelConfig read_config(const GgufFile& f) {
   return c;
 }
 
-// Packs the named GGUF matrices (same type and column count) as one row-concatenated weight.
-// interleave4 (two matrices of equal shape): rows 4k..4k+3 of the first, then rows 4k..4k+3 of the second.
+// Loads the named GGUF matrices (same type and column count) as one row-concatenated weight: CDNA-packed for the
+// panel types, or kept as GGUF rows for the row path (F32 / F16 / BF16, and every type when the model was opened
+// with no_pack: the reference's MALKIN_NO_PACK, model.cpp:136). interleave4 (two matrices of equal shape, packed):
+// rows 4k..4k+3 of the first, then rows 4k..4k+3 of the second.
 void Model::load_weight(const GgufFile& f, const std::vector<std::string>& names, Weight& w, bool interleave4) {
   std::vector<const GgufTensor*> ts;
   for (const auto& nm : names) {
     const GgufTensor* t = f.tensor(nm);
     if (!t) throw std::runtime_error("model: tensor " + nm + " missing");
-    if (!device_type(t->type))
+    const bool packable = device_type(t->type), rowable = row_type(t->type);
+    if (!rowable || (!packable && !no_pack_ && !raw_only_type(t->type)))
       throw std::runtime_error("model: tensor " + nm + " has type " + ggml_type_name(t->type) +
-                               ", supported on the device: Q8_0 Q4_K Q6_K");
+                               ", supported on the device: Q8_0 Q4_K Q6_K (packed), F32 F16 BF16 (row path), Q5_K "
+                               "(row path, with no_pack)");
     ts.push_back(t);
   }
   w.type = static_cast<int>(ts[0]->type);
@@ -101,38 +112,82 @@ void Model::load_weight(const GgufFile& f, const std::vector<std::string>& names
     if (t->type != ts[0]->type || t->ne[0] != w.cols) throw std::runtime_error("model: fused weights differ in type");
     w.rows += t->rows();
   }
-  const size_t rb = ggml_row_size(w.type, w.cols);
-  const size_t pb = mk_packed_bytes(w.type, w.rows, w.cols);
-  if (!pb) throw std::runtime_error("model: weight " + names[0] + " has no device layout (rows % 8)");
-  DevBuf staging(ctx_, rb * static_cast<size_t>(w.rows));
-  if (interleave4) {
-    if (ts.size() != 2 || ts[0]->rows() != ts[1]->rows() || ts[0]->rows() % 4)
-      throw std::runtime_error("model: interleaved weights need two matrices of equal rows, a multiple of 4");
-    std::vector<uint8_t> host(rb * static_cast<size_t>(w.rows));
-    const int64_t half = ts[0]->rows();
-    for (int64_t k = 0; k < half / 4; ++k)
-      for (int m = 0; m < 2; ++m)
-        std::memcpy(host.data() + (8 * k + 4 * m) * rb, static_cast<const uint8_t*>(ts[m]->data) + 4 * k * rb, 4 * rb);
-    ck(mk_upload(ctx_, staging.p, host.data(), host.size()));
-  } else {
-    size_t off = 0;
-    for (const GgufTensor* t : ts) {
-      ck(mk_upload(ctx_, staging.as<uint8_t>() + off, t->data, t->nbytes));
-      off += t->nbytes;
-    }
+  w.raw = no_pack_ || raw_only_type(w.type);
+  w.row_bytes = ggml_row_size(w.type, w.cols);
+  if (interleave4 && (w.raw || ts.size() != 2 || ts[0]->rows() != ts[1]->rows() || ts[0]->rows() % 4))
+    throw std::runtime_error("model: interleaved weights need two packed matrices of equal rows, a multiple of 4");
+  size_t bytes = w.row_bytes * static_cast<size_t>(w.rows);
+  if (!w.raw) {
+    bytes = mk_packed_bytes(w.type, w.rows, w.cols);
+    if (!bytes) throw std::runtime_error("model: weight " + names[0] + " has no device layout (rows % 8)");
   }
-  w.packed = DevBuf(ctx_, pb);
-  ck(mk_pack_weight(ctx_, w.type, staging.p, rb, w.rows, w.cols, w.packed.p));
-  ck(mk_synchronize(ctx_));
-  weight_bytes_ += pb;
+  w.packed = DevBuf(ctx_, bytes);
+  // Logical row r of the weight -> its bytes in the mapped file, and how many rows follow it there contiguously.
+  auto src_row = [&](int64_t r) -> std::pair<const uint8_t*, int64_t> {
+    if (interleave4) {
+      const int64_t k = r / 8, j = r % 8;
+      const GgufTensor* t = ts[j < 4 ? 0 : 1];
+      return {t->data + static_cast<size_t>(4 * k + j % 4) * w.row_bytes, 4 - j % 4};
+    }
+    for (const GgufTensor* t : ts) {
+      if (r < t->rows()) return {t->data + static_cast<size_t>(r) * w.row_bytes, t->rows() - r};
+      r -= t->rows();
+    }
+    throw std::logic_error("stream_rows: row past the weight");
+  };
+  stream_rows(w.rows, w.row_bytes, src_row, [&](const void* dev_rows, int64_t r0, int64_t n) {
+    if (!w.raw) ck(mk_pack_weight_rows(ctx_, w.type, dev_rows, w.row_bytes, r0, n, w.rows, w.cols, w.packed.p));
+  }, w.raw ? w.packed.p : nullptr);
+  weight_bytes_ += bytes;
+}
+
+// Moves rows 0..rows-1 (row_bytes each; src(r): row r's bytes in the mapped file and the count of rows that follow
+// it contiguously there) to the device in chunks through the pinned staging ring: the host copies chunk i + 1 from the mapped file
+// while the device receives and consumes chunk i. With dest, chunk rows land at dest + r0 * row_bytes; without, in a
+// device staging block, and consume(dev_rows, r0, n) is queued after each chunk's copy (the pack).
+void Model::stream_rows(int64_t rows, size_t row_bytes,
+                        const std::function<std::pair<const uint8_t*, int64_t>(int64_t)>& src,
+                        const std::function<void(const void*, int64_t, int64_t)>& consume, void* dest) {
+  if (rows <= 0) return;
+  int64_t chunk = std::max<int64_t>(8, static_cast<int64_t>(kLoadChunkBytes / row_bytes) / 8 * 8);
+  chunk = std::min(chunk, rows);
+  const size_t need = static_cast<size_t>(chunk) * row_bytes;
+  if (need > load_block_bytes_) {
+    if (load_block_bytes_) ck(mk_synchronize(ctx_));
+    for (LoadBlock& b : load_) {
+      b.release();
+      void* h = nullptr;
+      ck(mk_host_alloc(ctx_, need, &h));
+      b.ctx = ctx_;
+      b.host = static_cast<uint8_t*>(h);
+      b.dev = DevBuf(ctx_, need);
+    }
+    load_block_bytes_ = need;
+  }
+  for (int64_t r0 = 0, i = 0; r0 < rows; r0 += chunk, ++i) {
+    const int64_t n = std::min(chunk, rows - r0);
+    LoadBlock& b = load_[static_cast<size_t>(i) % 2];
+    if (!mk_event_done(b.done)) ck(mk_event_wait(ctx_, b.done));
+    for (int64_t r = r0; r < r0 + n;) {  // contiguous runs of the file
+      const auto [p, avail] = src(r);
+      const int64_t take = std::min(r0 + n - r, avail);
+      std::memcpy(b.host + static_cast<size_t>(r - r0) * row_bytes, p, static_cast<size_t>(take) * row_bytes);
+      r += take;
+    }
+    void* to = dest ? static_cast<uint8_t*>(dest) + static_cast<size_t>(r0) * row_bytes : b.dev.p;
+    ck(mk_copy_async(ctx_, to, b.host, static_cast<size_t>(n) * row_bytes));
+    ck(mk_event_record(ctx_, &b.done));
+    if (!dest) consume(b.dev.p, r0, n);
+  }
 }
 
 // ffn_gate | ffn_up: interleaved (silu fused into the decode matmul) when both have one type and the row count
 // allows; otherwise the plain group.
-void Model::load_gateup(const GgufFile& f, const std::string& gate, const std::string& up, Group& g) {
+void Model::load_gateup(const GgufFile& f, const std::string& gate, const std::string& up, Group& g, bool interleave) {
   const GgufTensor* a = f.tensor(gate);
   const GgufTensor* b = f.tensor(up);
-  if (a && b && a->type == b->type && a->ne[0] == b->ne[0] && a->rows() == b->rows() && a->rows() % 4 == 0) {
+  if (interleave && a && b && a->type == b->type && device_type(a->type) && a->ne[0] == b->ne[0] &&
+      a->rows() == b->rows() && a->rows() % 4 == 0) {
     Weight w;
     load_weight(f, {gate, up}, w, true);
     g.rows = w.rows;
@@ -195,8 +250,8 @@ bool Model::matmul_group_f32(const Group& g, const float* x, int64_t xs, const f
   return true;
 }
 
-Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide)
-    : ctx_(ctx), cfg_(read_config(f)), n_ctx_(n_ctx), n_seq_(n_seq), wide_(wide) {
+Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide, bool no_pack)
+    : ctx_(ctx), cfg_(read_config(f)), n_ctx_(n_ctx), n_seq_(n_seq), wide_(wide), no_pack_(no_pack) {
   auto& c = cfg_;
   if (c.n_head <= 0 || c.n_head_kv <= 0 || c.head_dim <= 0 || c.head_dim % 32 || c.n_head % c.n_head_kv)
     throw std::runtime_error("model: unsupported head layout");
@@ -206,13 +261,14 @@ Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide)
   const GgufTensor* te = f.tensor("token_embd.weight");
   if (!te) throw std::runtime_error("model: tensor token_embd.weight missing");
   embd_type_ = static_cast<int>(te->type);
-  if (!device_type(te->type) && te->type != 0)
-    throw std::runtime_error("model: tensor token_embd.weight has unsupported type");
+  if (!row_type(te->type)) throw std::runtime_error("model: tensor token_embd.weight has unsupported type");
   embd_row_bytes_ = ggml_row_size(te->type, te->ne[0]);
   if (te->ne[0] != c.n_embd) throw std::runtime_error("model: token_embd.weight has the wrong row length");
   embd_count_ = te->rows();
   embd_rows_ = DevBuf(ctx_, te->nbytes);
-  ck(mk_upload(ctx_, embd_rows_.p, te->data, te->nbytes));
+  stream_rows(embd_count_, embd_row_bytes_,
+              [&](int64_t r) { return std::make_pair(te->data + static_cast<size_t>(r) * embd_row_bytes_, embd_count_ - r); },
+              {}, embd_rows_.p);
   if (f.tensor("output.weight"))
     load_weight(f, {"output.weight"}, output_);
   else
@@ -237,9 +293,16 @@ Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide)
     upload_norm(p + "ffn_norm.weight", E, L.norms.as<float>() + E);
     upload_norm(p + "attn_q_norm.weight", D, L.norms.as<float>() + 2 * E);
     upload_norm(p + "attn_k_norm.weight", D, L.norms.as<float>() + 2 * E + D);
+    // A layer with any weight on the row path runs the reference's unfused sequence (fp32 activations kept for
+    // the row dots); its gate|up stays [gate | up].
+    L.row_flow = no_pack_;
+    for (const char* nm : {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"}) {
+      const GgufTensor* t = f.tensor(p + nm + ".weight");
+      if (t && raw_only_type(t->type)) L.row_flow = true;
+    }
     load_group(f, {p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"}, L.qkv);
     load_weight(f, {p + "attn_output.weight"}, L.wo);
-    load_gateup(f, p + "ffn_gate.weight", p + "ffn_up.weight", L.gateup);
+    load_gateup(f, p + "ffn_gate.weight", p + "ffn_up.weight", L.gateup, !L.row_flow);
     load_weight(f, {p + "ffn_down.weight"}, L.down);
     if (L.qkv.rows != (int64_t)(H + 2 * KV) * D || L.wo.rows != E || L.gateup.rows != 2 * F || L.down.rows != E)
       throw std::runtime_error("model: layer " + std::to_string(i) + " has unexpected shapes");
@@ -277,6 +340,7 @@ Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide)
   att_ = DevBuf(ctx_, T * H * D * sizeof(float));
   gu_ = DevBuf(ctx_, T * 2 * F * sizeof(float));
   xq_ = DevBuf(ctx_, T * (kmax / 32) * 40);
+  h_ = DevBuf(ctx_, T * E * sizeof(float));
   logits_ = DevBuf(ctx_, B * static_cast<size_t>(c.n_vocab) * sizeof(float));
   top_ = DevBuf(ctx_, 2 * B * sizeof(int32_t) + 2 * sizeof(int32_t));
 
@@ -303,6 +367,16 @@ Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide)
     st.host = static_cast<int32_t*>(h);
   }
   ck(mk_synchronize(ctx_));
+  for (LoadBlock& b : load_) b.release();  // loading is done: the staging ring goes
+  load_block_bytes_ = 0;
+}
+
+void Model::LoadBlock::release() {
+  if (done) (void)mk_event_free(done);
+  if (host) (void)mk_host_free(ctx, host);
+  done = nullptr;
+  host = nullptr;
+  dev = DevBuf();
 }
 
 Model::~Model() {
@@ -483,6 +557,10 @@ void Model::run() {
   for (int il = 0; il < c.n_layer; ++il) {
     const Layer& L = layers_[il];
     const float* norms = L.norms.as<float>();
+    if (L.row_flow) {
+      run_row_layer(L, il);
+      continue;
+    }
     // Decode steps (n <= 2) fuse rmsnorm / quantization into the matmuls (mk_matmul_f32); same results.
     if (!matmul_group_f32(L.qkv, x, E, norms, n, qkv)) {
       ck(mk_rmsnorm_q8(ctx_, x, nullptr, norms, n, E, c.rms_eps, xq));
@@ -531,12 +609,74 @@ void Model::run() {
   }
   const int m = n_out();
   if (m == 0) return;
+  if (output_.raw) {  // model.cpp:419-425 on the row path: fp32 normalized rows and their BlockQ8 rows
+    float* h = h_.as<float>();
+    ck(mk_rmsnorm_rows(ctx_, x, d_out_, output_norm_.as<float>(), m, E, c.rms_eps, h));
+    if (!raw_only_type(output_.type)) ck(mk_quantize_q8(ctx_, h, m, E, xq));
+    ck(mk_matmul_rows(ctx_, output_.type, output_.packed.p, output_.row_bytes, output_.rows, output_.cols, h, E, xq, m,
+                      logits_.as<float>(), c.n_vocab, 0));
+    return;
+  }
   ck(mk_rmsnorm_q8(ctx_, x, d_out_, output_norm_.as<float>(), m, E, c.rms_eps, xq));
   mk_weight wout = output_.w();
   wout.wide = wide_ ? 1 : 0;
   ck(mk_matmul(ctx_, &wout, xq, m, logits_.as<float>(), c.n_vocab, 0));
 }
 
+
+void Model::matmul_any(const Group& g, const float* xf, int64_t xfs, const void* xq, int n, float* y) {
+  for (const Weight& p : g.parts) {
+    if (p.raw) {
+      ck(mk_matmul_rows(ctx_, p.type, p.packed.p, p.row_bytes, p.rows, p.cols, xf, xfs, xq, n, y + p.out_off, g.rows,
+                        0));
+    } else {
+      mk_weight w = p.w();
+      w.wide = wide_ ? 1 : 0;
+      ck(mk_matmul(ctx_, &w, xq, n, y + p.out_off, g.rows, 0));
+    }
+  }
+}
+
+// One layer with weights on the row path, as model.cpp:360-416 runs it: every matmul sees the fp32 activations and
+// their BlockQ8 rows, gate|up gives [gate | up] per token, and the residual adds go into x.
+void Model::run_row_layer(const Layer& L, int il) {
+  const int n = lay_.n;
+  const auto& c = cfg_;
+  const int E = c.n_embd, D = c.head_dim, H = c.n_head, KV = c.n_head_kv, F = c.n_ff;
+  const int64_t QKV = static_cast<int64_t>(H + 2 * KV) * D, HD = static_cast<int64_t>(H) * D;
+  float* x = x_.as<float>();
+  float* h = h_.as<float>();
+  float* qkv = qkv_.as<float>();
+  float* att = att_.as<float>();
+  float* gu = gu_.as<float>();
+  void* xq = xq_.p;
+  const float* norms = L.norms.as<float>();
+  auto single = [&](const Weight& w, const float* xf, int64_t xfs, float* y, int64_t ys) {
+    if (w.raw) {
+      ck(mk_matmul_rows(ctx_, w.type, w.packed.p, w.row_bytes, w.rows, w.cols, xf, xfs, xq, n, y, ys, 1));
+    } else {
+      mk_weight mw = w.w();
+      mw.wide = wide_ ? 1 : 0;
+      ck(mk_matmul(ctx_, &mw, xq, n, y, ys, 1));
+    }
+  };
+  ck(mk_rmsnorm_rows(ctx_, x, nullptr, norms, n, E, c.rms_eps, h));
+  ck(mk_quantize_q8(ctx_, h, n, E, xq));
+  matmul_any(L.qkv, h, E, xq, n, qkv);
+  ck(mk_qk_norm_rope_kv(ctx_, qkv, qkv + HD, qkv + HD + static_cast<int64_t>(KV) * D, QKV, n, H, norms + 2 * E,
+                        norms + 2 * E + D, c.rms_eps, rope_cos_.as<float>(), rope_sin_.as<float>(), d_rpos_, d_seq_,
+                        d_kv_row_, &kv_, il));
+  ck(mk_attention(ctx_, qkv, QKV, att, HD, n, H, &kv_, il, d_seq_, d_n_keys_, lay_.tree ? d_extra_at_ : nullptr,
+                  d_extra_, lay_.max_keys));
+  ck(mk_quantize_q8(ctx_, att, n, HD, xq));
+  single(L.wo, att, HD, x, E);  // x += attn_output(att)
+  ck(mk_rmsnorm_rows(ctx_, x, nullptr, norms + E, n, E, c.rms_eps, h));
+  ck(mk_quantize_q8(ctx_, h, n, E, xq));
+  matmul_any(L.gateup, h, E, xq, n, gu);
+  ck(mk_silu_mul_q8(ctx_, gu, n, F, 0, xq));  // BlockQ8 rows of silu(gate) * up ...
+  ck(mk_silu_mul_rows(ctx_, gu, n, F));       // ... and the fp32 rows themselves, in place of gate
+  single(L.down, gu, 2 * static_cast<int64_t>(F), x, E);  // x += ffn_down(...)
+}
 
 void Model::forward(const BatchToken* batch, int n, float* logits) {
   layout_batch(batch, n);

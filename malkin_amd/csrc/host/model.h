@@ -9,8 +9,10 @@
 #pragma once
 
 #include <cstdint>
+#include <functional>
 #include <memory>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../../../include/malkin_hip.h"
@@ -76,7 +78,8 @@ class Model {
 
   // wide: the reference's wide Q6_K prefill panels are packed (Engine packs them when RAM allows,
   // engine.cpp:130-145); MALKIN_NO_WIDE turns them off there.
-  Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq = 1, bool wide = true);
+  // no_pack: every matmul on the reference's row path over GGUF rows (its MALKIN_NO_PACK, model.cpp:136).
+  Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq = 1, bool wide = true, bool no_pack = false);
   ~Model();
   const ModelConfig& cfg() const { return cfg_; }
   int n_ctx() const { return n_ctx_; }
@@ -125,6 +128,8 @@ class Model {
     int type = 0;
     int64_t rows = 0, cols = 0;
     int64_t out_off = 0;  // first output row within its group (q|k|v, gate|up)
+    bool raw = false;     // GGUF rows for the row path (mk_matmul_rows) instead of the CDNA layout
+    size_t row_bytes = 0;
     DevBuf packed;
     mk_weight w() const;
   };
@@ -141,6 +146,19 @@ class Model {
     DevBuf norms;  // attn_norm[E], ffn_norm[E], q_norm[D], k_norm[D]
     Group qkv, gateup;
     Weight wo, down;
+    bool row_flow = false;  // some weight is on the row path: unfused rmsnorm / quantize / silu steps
+  };
+  // A pinned staging block of the weight loader and its device twin (freed once loading is done, or on unwinding).
+  struct LoadBlock {
+    mk_ctx* ctx = nullptr;
+    uint8_t* host = nullptr;
+    void* done = nullptr;  // event after the copy that reads `host`
+    DevBuf dev;
+    LoadBlock() = default;
+    LoadBlock(const LoadBlock&) = delete;
+    LoadBlock& operator=(const LoadBlock&) = delete;
+    void release();
+    ~LoadBlock() { release(); }
   };
   // One pinned host block per in-flight layout copy, reusable once its event has passed.
   struct Staging {
@@ -149,7 +167,12 @@ class Model {
   };
 
   void load_weight(const GgufFile& f, const std::vector<std::string>& names, Weight& w, bool interleave4 = false);
-  void load_gateup(const GgufFile& f, const std::string& gate, const std::string& up, Group& g);
+  void load_gateup(const GgufFile& f, const std::string& gate, const std::string& up, Group& g, bool interleave);
+  void stream_rows(int64_t rows, size_t row_bytes,
+                   const std::function<std::pair<const uint8_t*, int64_t>(int64_t)>& src,
+                   const std::function<void(const void*, int64_t, int64_t)>& consume, void* dest);
+  // One group's matmul, every part on its own path: packed parts read xq (BlockQ8 rows), row-path parts xf too.
+  void matmul_any(const Group& g, const float* xf, int64_t xfs, const void* xq, int n, float* y);
   void load_group(const GgufFile& f, const std::vector<std::string>& names, Group& g);
   void matmul_group(const Group& g, const void* xq, int n, float* y);
   // The group from fp32 rows x (token stride xs) with rmsnorm (norm_w) / quantization inside each matmul; false when
@@ -162,13 +185,16 @@ class Model {
   void finish_layout();
   void upload_layout(const int32_t* dev_ids = nullptr);
   void run();
+  void run_row_layer(const Layer& L, int il);
   void check_ids();
 
   mk_ctx* ctx_;
   ModelConfig cfg_;
   int n_ctx_, n_seq_;
-  bool wide_;
+  bool wide_, no_pack_;
   size_t weight_bytes_ = 0;
+  LoadBlock load_[2];
+  size_t load_block_bytes_ = 0;
   int embd_type_ = 0;
   int64_t embd_count_ = 0;  // token_embd rows (valid token ids)
   size_t embd_row_bytes_ = 0;
@@ -191,6 +217,7 @@ class Model {
 
   // Activations for kMaxBatch tokens.
   DevBuf x_, qkv_, att_, gu_, xq_, logits_, top_;
+  DevBuf h_;  // fp32 normalized rows of the row-path layers (kDevBatch x n_embd)
 };
 
 }  // namespace malkin_hip

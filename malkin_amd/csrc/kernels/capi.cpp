@@ -207,6 +207,11 @@ int mk_pack_weight(mk_ctx* c, int type, const void* src, size_t srb, int64_t row
   return guard([&] { mk::pack_weight(c->stream, type, src, srb, rows, cols, dst); });
 }
 
+int mk_pack_weight_rows(mk_ctx* c, int type, const void* src, size_t srb, int64_t row0, int64_t n_rows, int64_t rows,
+                        int64_t cols, void* dst) {
+  return guard([&] { mk::pack_weight_rows(c->stream, type, src, srb, row0, n_rows, rows, cols, dst); });
+}
+
 int mk_unpack_weight(mk_ctx* c, int type, const void* packed, int64_t rows, int64_t cols, void* dst) {
   return guard([&] { mk::unpack_weight(c->stream, type, packed, rows, cols, dst); });
 }
@@ -251,6 +256,24 @@ int mk_rmsnorm(mk_ctx* c, const float* x, const float* w, int rows, int n, float
 int mk_rmsnorm_q8(mk_ctx* c, const float* x, const int32_t* rows_idx, const float* w, int rows, int n, float eps,
                   void* xq) {
   return guard([&] { mk::rmsnorm_q8(c->stream, x, rows_idx, w, rows, n, eps, static_cast<mk::BlockQ8*>(xq)); });
+}
+
+int mk_rmsnorm_rows(mk_ctx* c, const float* x, const int32_t* rows_idx, const float* w, int rows, int n, float eps,
+                    float* y) {
+  return guard([&] { mk::rmsnorm(c->stream, x, w, rows, n, eps, y, rows_idx); });
+}
+
+int mk_silu_mul_rows(mk_ctx* c, float* gu, int rows, int64_t n) {
+  return guard([&] { mk::silu_mul_rows(c->stream, gu, rows, n); });
+}
+
+int mk_matmul_rows(mk_ctx* c, int type, const void* w, size_t row_bytes, int64_t rows, int64_t cols, const float* x,
+                   int64_t x_stride, const void* xq, int n, float* y, int64_t y_stride, int accumulate) {
+  return guard([&] {
+    require(w != nullptr && y != nullptr && rows >= 0 && n >= 0, "matmul_rows: bad arguments");
+    mk::matmul_rows(c->stream, type, w, row_bytes, rows, cols, x, x_stride, static_cast<const mk::BlockQ8*>(xq), n, y,
+                    y_stride, accumulate != 0);
+  });
 }
 
 int mk_silu_mul(mk_ctx* c, int64_t n, float* g, const float* u) {

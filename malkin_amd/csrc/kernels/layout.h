@@ -24,7 +24,7 @@
 
 namespace mk {
 
-enum : int { kF32 = 0, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14 };
+enum : int { kF32 = 0, kF16 = 1, kQ8_0 = 8, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14, kBF16 = 30 };
 constexpr int kRowGroup = 8;
 
 struct PackedQ8_0 {

@@ -31,6 +31,10 @@ struct KvLayer {
 };
 
 size_t packed_bytes(int type, int64_t rows, int64_t cols);
+// Rows r0 .. r0 + nrows of a rows x cols weight (src holds just those rows, srb bytes apart) into its packed buffer;
+// r0 on an 8-row group, nrows too unless the range ends the weight.
+void pack_weight_rows(hipStream_t s, int type, const void* src, size_t srb, int64_t r0, int64_t nrows, int64_t rows,
+                      int64_t cols, void* dst);
 void pack_weight(hipStream_t s, int type, const void* src, size_t src_row_bytes, int64_t rows, int64_t cols, void* dst);
 void unpack_weight(hipStream_t s, int type, const void* packed, int64_t rows, int64_t cols, void* dst);
 
@@ -38,10 +42,17 @@ void quantize_q8(hipStream_t s, const float* x, int n, int64_t k, BlockQ8* xq);
 void quantize_i8_rows(hipStream_t s, const float* x, int rows, int n, int8_t* q, float* d);
 void dequantize_rows(hipStream_t s, int type, const void* src, size_t row_bytes, const int32_t* ids, int n, int64_t k,
                      float* dst);
-void rmsnorm(hipStream_t s, const float* x, const float* w, int rows, int n, float eps, float* y);
+void rmsnorm(hipStream_t s, const float* x, const float* w, int rows, int n, float eps, float* y,
+             const int32_t* rows_idx = nullptr);
 void rmsnorm_q8(hipStream_t s, const float* x, const int32_t* rows_idx, const float* w, int rows, int n, float eps,
                 BlockQ8* xq);
 void silu_mul(hipStream_t s, int64_t n, float* g, const float* u);
+// Per row of gu ([gate | up], 2n floats at stride 2n): gate = silu(gate) * up in place.
+void silu_mul_rows(hipStream_t s, float* gu, int rows, int64_t n);
+// matmul's row path (quant.cpp:171-191, 330-351) over GGUF rows: fp32 x for F32/F16/BF16, BlockQ8 xq otherwise.
+bool rows_supported(int type, int64_t cols);
+void matmul_rows(hipStream_t s, int type, const void* w, size_t row_bytes, int64_t rows, int64_t cols, const float* x,
+                 int64_t xs, const BlockQ8* xq, int n, float* y, int64_t ys, bool accumulate);
 // gu rows of 2n floats: [gate | up], or (interleave4) gate/up interleaved by 4 as matmul_f32's silu_pairs rows.
 void silu_mul_q8(hipStream_t s, const float* gu, int rows, int64_t n, BlockQ8* xq, bool interleave4 = false);
 void add(hipStream_t s, int64_t n, float* x, const float* h);

@@ -21,13 +21,13 @@ __device__ __forceinline__ int q6_value(const uint8_t* s, int k) {
 }
 
 template <bool kPack>
-__global__ void k_q8_0(uint8_t* gguf, size_t srb, uint8_t* dst, int64_t rows, int64_t nb) {
+__global__ void k_q8_0(uint8_t* gguf, size_t srb, uint8_t* dst, int64_t rows, int64_t nb, int64_t r0, int64_t nrows) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= rows * nb) return;
-  const int64_t r = i / nb, b = i % nb, g = r / 8;
+  if (i >= nrows * nb) return;
+  const int64_t lr = i / nb, r = r0 + lr, b = i % nb, g = r / 8;
   const int rr = (int)(r % 8);
   const PackedQ8_0 L{rows, nb};
-  uint8_t* row = gguf + r * srb + b * 34;  // GGUF block (source when packing, destination when unpacking)
+  uint8_t* row = gguf + lr * srb + b * 34;  // GGUF block (source when packing, destination when unpacking)
   uint8_t* lo = dst + L.quants(g, b) + rr * 16;
   uint8_t* sc = dst + L.scales(g, b) + rr * 2;
   if (kPack) {
@@ -42,13 +42,13 @@ __global__ void k_q8_0(uint8_t* gguf, size_t srb, uint8_t* dst, int64_t rows, in
 }
 
 template <bool kPack>
-__global__ void k_q4_k(uint8_t* gguf, size_t srb, uint8_t* dst, int64_t rows, int64_t nsb) {
+__global__ void k_q4_k(uint8_t* gguf, size_t srb, uint8_t* dst, int64_t rows, int64_t nsb, int64_t r0, int64_t nrows) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= rows * nsb) return;
-  const int64_t r = i / nsb, sb = i % nsb, g = r / 8;
+  if (i >= nrows * nsb) return;
+  const int64_t lr = i / nsb, r = r0 + lr, sb = i % nsb, g = r / 8;
   const int rr = (int)(r % 8);
   const PackedQ4_K L{rows, nsb};
-  uint8_t* blk = gguf + r * srb + sb * 144;
+  uint8_t* blk = gguf + lr * srb + sb * 144;
   uint8_t* hdr = dst + L.headers(g, sb) + rr * 16;
   if (kPack)
     copy_bytes(hdr, blk, 16);
@@ -67,13 +67,13 @@ __global__ void k_q4_k(uint8_t* gguf, size_t srb, uint8_t* dst, int64_t rows, in
 }
 
 __global__ void k_pack_q6_k(const uint8_t* __restrict__ src, size_t srb, uint8_t* __restrict__ dst, int64_t rows,
-                            int64_t nsb) {
+                            int64_t nsb, int64_t r0, int64_t nrows) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= rows * nsb) return;
-  const int64_t r = i / nsb, sb = i % nsb, g = r / 8;
+  if (i >= nrows * nsb) return;
+  const int64_t lr = i / nsb, r = r0 + lr, sb = i % nsb, g = r / 8;
   const int rr = (int)(r % 8);
   const PackedQ6_K L{rows, nsb};
-  const uint8_t* s = src + r * srb + sb * 210;
+  const uint8_t* s = src + lr * srb + sb * 210;
   for (int b8 = 0; b8 < 8; ++b8) {
     uint8_t* nib = dst + L.quants(g, sb, b8) + rr * 16;
     uint8_t* hb = dst + L.quants(g, sb, b8) + 128 + rr * 8;
@@ -152,26 +152,35 @@ static size_t gguf_row_bytes(int type, int64_t cols) {
   }
 }
 
-void pack_weight(hipStream_t s, int type, const void* src, size_t srb, int64_t rows, int64_t cols, void* dst) {
+void pack_weight_rows(hipStream_t s, int type, const void* src, size_t srb, int64_t r0, int64_t nrows, int64_t rows,
+                      int64_t cols, void* dst) {
   if (!packed_bytes(type, rows, cols)) throw Error(MK_ERR_UNSUPPORTED, "pack_weight: no CDNA layout for this type/shape");
+  require(r0 >= 0 && nrows >= 0 && r0 % kRowGroup == 0 && (nrows % kRowGroup == 0 || r0 + nrows == rows) &&
+              r0 + nrows <= rows,
+          "pack_weight: row range outside the weight or not on 8-row groups");
+  if (nrows == 0) return;
   auto* in = const_cast<uint8_t*>(static_cast<const uint8_t*>(src));
   auto* out = static_cast<uint8_t*>(dst);
   const int T = 256;
   switch (type) {
     case kQ8_0:
-      hipLaunchKernelGGL(k_q8_0<true>, dim3(blocks_for(rows * (cols / 32), T)), dim3(T), 0, s, in, srb, out, rows,
-                         cols / 32);
+      hipLaunchKernelGGL(k_q8_0<true>, dim3(blocks_for(nrows * (cols / 32), T)), dim3(T), 0, s, in, srb, out, rows,
+                         cols / 32, r0, nrows);
       break;
     case kQ4_K:
-      hipLaunchKernelGGL(k_q4_k<true>, dim3(blocks_for(rows * (cols / 256), T)), dim3(T), 0, s, in, srb, out, rows,
-                         cols / 256);
+      hipLaunchKernelGGL(k_q4_k<true>, dim3(blocks_for(nrows * (cols / 256), T)), dim3(T), 0, s, in, srb, out, rows,
+                         cols / 256, r0, nrows);
       break;
     case kQ6_K:
-      hipLaunchKernelGGL(k_pack_q6_k, dim3(blocks_for(rows * (cols / 256), T)), dim3(T), 0, s, in, srb, out, rows,
-                         cols / 256);
+      hipLaunchKernelGGL(k_pack_q6_k, dim3(blocks_for(nrows * (cols / 256), T)), dim3(T), 0, s, in, srb, out, rows,
+                         cols / 256, r0, nrows);
       break;
   }
   check_launch("pack_weight");
+}
+
+void pack_weight(hipStream_t s, int type, const void* src, size_t srb, int64_t rows, int64_t cols, void* dst) {
+  pack_weight_rows(s, type, src, srb, 0, rows, rows, cols, dst);
 }
 
 void unpack_weight(hipStream_t s, int type, const void* packed, int64_t rows, int64_t cols, void* dst) {
@@ -183,12 +192,12 @@ void unpack_weight(hipStream_t s, int type, const void* packed, int64_t rows, in
     case kQ8_0:
       hipLaunchKernelGGL(k_q8_0<false>, dim3(blocks_for(rows * (cols / 32), T)), dim3(T), 0, s,
                          static_cast<uint8_t*>(dst), drb, const_cast<uint8_t*>(static_cast<const uint8_t*>(packed)),
-                         rows, cols / 32);
+                         rows, cols / 32, (int64_t)0, rows);
       break;
     case kQ4_K:
       hipLaunchKernelGGL(k_q4_k<false>, dim3(blocks_for(rows * (cols / 256), T)), dim3(T), 0, s,
                          static_cast<uint8_t*>(dst), drb, const_cast<uint8_t*>(static_cast<const uint8_t*>(packed)),
-                         rows, cols / 256);
+                         rows, cols / 256, (int64_t)0, rows);
       break;
     case kQ6_K:
       hipLaunchKernelGGL(k_unpack_q6_k, dim3(blocks_for(rows * (cols / 256), T)), dim3(T), 0, s,

@@ -136,6 +136,16 @@ __global__ void k_silu_mul(int64_t n, float* __restrict__ g, const float* __rest
   g[i] = (x / (1.0f + e)) * u[i];
 }
 
+// Rows [gate(n) | up(n)] at stride 2n: gate = silu(gate) * up in place (kern::silu_mul per token).
+__global__ void k_silu_mul_rows(float* __restrict__ gu, int64_t n, int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  float* g = gu + (i / n) * 2 * n + i % n;
+  const float x = *g;
+  const float e = exp512(0.0f - x);
+  *g = (x / (1.0f + e)) * g[n];
+}
+
 // gu row: [gate(n) | up(n)], or gate/up interleaved by 4 (row 8k + j: gate 4k + j for j < 4, else up 4k + j - 4)
 // -> silu(gate) * up, quantized; one element per thread, n % 32 == 0.
 __global__ void k_silu_mul_q8(const float* __restrict__ gu, int64_t n, int64_t total, int interleave4,
@@ -184,6 +194,19 @@ __global__ void k_dequant(int type, const uint8_t* __restrict__ src, size_t row_
   float v = 0.0f;
   if (type == kF32) {
     v = reinterpret_cast<const float*>(row)[e];
+  } else if (type == kF16) {
+    v = half_to_float(reinterpret_cast<const uint16_t*>(row)[e]);
+  } else if (type == kBF16) {
+    v = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(row)[e] << 16);
+  } else if (type == kQ5_K) {
+    const uint8_t* b = row + (e / 256) * 176;
+    const int within = (int)(e % 256), j = within / 32, l = within % 32;
+    const float d = half_to_float((uint16_t)(b[0] | (b[1] << 8))), dmin = half_to_float((uint16_t)(b[2] | (b[3] << 8)));
+    int sc, m;
+    scale_min_k4(j, b + 4, sc, m);
+    const uint8_t qb = b[48 + 32 * (j / 2) + l];
+    const int q = ((j & 1) ? qb >> 4 : qb & 0xF) | (((b[16 + l] >> j) & 1) << 4);
+    v = d * (float)sc * (float)q - dmin * (float)m;
   } else if (type == kQ8_0) {
     const uint8_t* b = row + (e / 32) * 34;
     v = half_to_float((uint16_t)(b[0] | (b[1] << 8))) * (float)(int8_t)b[2 + e % 32];
@@ -229,7 +252,9 @@ void quantize_i8_rows(hipStream_t s, const float* x, int rows, int n, int8_t* q,
 
 void dequantize_rows(hipStream_t s, int type, const void* src, size_t row_bytes, const int32_t* ids, int n, int64_t k,
                      float* dst) {
-  require(type == kF32 || type == kQ8_0 || type == kQ4_K || type == kQ6_K, "dequantize: unsupported type");
+  require(type == kF32 || type == kF16 || type == kBF16 || type == kQ8_0 || type == kQ4_K || type == kQ5_K ||
+              type == kQ6_K,
+          "dequantize: unsupported type");
   const int64_t total = (int64_t)n * k;
   if (total == 0) return;
   hipLaunchKernelGGL(k_dequant, dim3(grid_for(total, kT)), dim3(kT), 0, s, type, static_cast<const uint8_t*>(src),
@@ -239,10 +264,11 @@ void dequantize_rows(hipStream_t s, int type, const void* src, size_t row_bytes,
 
 static size_t rmsnorm_lds(int n) { return 16 * (size_t)sumsq_tstride(n / 16) * sizeof(float); }
 
-void rmsnorm(hipStream_t s, const float* x, const float* w, int rows, int n, float eps, float* y) {
+void rmsnorm(hipStream_t s, const float* x, const float* w, int rows, int n, float eps, float* y,
+             const int32_t* rows_idx) {
   if (rows <= 0) return;
   require(n % 16 == 0 && n <= 8192, "rmsnorm: n must be a multiple of 16, <= 8192");
-  hipLaunchKernelGGL(k_rmsnorm<false>, dim3(rows), dim3(kT), rmsnorm_lds(n), s, x, nullptr, w, n, eps, y, nullptr);
+  hipLaunchKernelGGL(k_rmsnorm<false>, dim3(rows), dim3(kT), rmsnorm_lds(n), s, x, rows_idx, w, n, eps, y, nullptr);
   check_launch("rmsnorm");
 }
 
@@ -252,6 +278,14 @@ void rmsnorm_q8(hipStream_t s, const float* x, const int32_t* rows_idx, const fl
   require(n % 32 == 0 && n <= 8192, "rmsnorm_q8: n must be a multiple of 32, <= 8192");
   hipLaunchKernelGGL(k_rmsnorm<true>, dim3(rows), dim3(kT), rmsnorm_lds(n), s, x, rows_idx, w, n, eps, nullptr, xq);
   check_launch("rmsnorm_q8");
+}
+
+void silu_mul_rows(hipStream_t s, float* gu, int rows, int64_t n) {
+  if (rows <= 0 || n <= 0) return;
+  if (n % 16) throw Error(MK_ERR_UNSUPPORTED, "silu_mul: n must be a multiple of 16");
+  const int64_t total = (int64_t)rows * n;
+  hipLaunchKernelGGL(k_silu_mul_rows, dim3(grid_for(total, kT)), dim3(kT), 0, s, gu, n, total);
+  check_launch("silu_mul_rows");
 }
 
 void silu_mul(hipStream_t s, int64_t n, float* g, const float* u) {

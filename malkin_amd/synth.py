@@ -9,7 +9,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmalkin_synth.so")
 
-Q8_0, Q4_K, Q6_K = 8, 12, 14
+F16, Q8_0, Q4_K, Q6_K, BF16 = 1, 8, 12, 14, 30
 MIX_UNIFORM, MIX_Q4_K_M = 0, 1
 
 

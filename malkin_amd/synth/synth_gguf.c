@@ -19,7 +19,7 @@
 #include <sys/mman.h>
 #include <unistd.h>
 
-enum { T_F32 = 0, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
+enum { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14, T_BF16 = 30 };
 
 static uint64_t splitmix(uint64_t x) {
   x += 0x9E3779B97F4A7C15ull;
@@ -171,10 +171,20 @@ static void quant_q6_k(const float* x, uint8_t* out, int64_t k) {
   }
 }
 
+/* float -> bfloat16, round to nearest even (finite values). */
+static uint16_t to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
 static size_t row_bytes(int type, int64_t k) {
   switch (type) {
     case T_F32:
       return (size_t)k * 4;
+    case T_F16:
+    case T_BF16:
+      return (size_t)k * 2;
     case T_Q8_0:
       return (size_t)(k / 32) * 34;
     case T_Q4_K:
@@ -268,6 +278,12 @@ static void gen_row(const job* j, const tinfo* t, int ti, int64_t r, float* buf)
   switch (t->type) {
     case T_F32:
       memcpy(dst, buf, (size_t)t->ne0 * 4);
+      break;
+    case T_F16:
+      for (int64_t i = 0; i < t->ne0; ++i) put16(dst + 2 * i, to_half(buf[i]));
+      break;
+    case T_BF16:
+      for (int64_t i = 0; i < t->ne0; ++i) put16(dst + 2 * i, to_bf16(buf[i]));
       break;
     case T_Q8_0:
       quant_q8_0(buf, dst, t->ne0);
@@ -369,7 +385,7 @@ static size_t header(wbuf* w, const mks_config* c, const tinfo* t, int nt) {
 
 int mks_quantize_rows(int type, const float* x, int64_t rows, int64_t k, uint8_t* out) {
   const size_t rb = row_bytes(type, k);
-  if (!rb || type == T_F32 || k % (type == T_Q8_0 ? 32 : 256)) return -2;
+  if (!rb || (type != T_Q8_0 && type != T_Q4_K && type != T_Q6_K) || k % (type == T_Q8_0 ? 32 : 256)) return -2;
   for (int64_t r = 0; r < rows; ++r, x += k, out += rb) {
     if (type == T_Q8_0)
       quant_q8_0(x, out, k);

@@ -72,6 +72,15 @@ class _Common:
         self._f("silu_mul")(ctypes.c_int64(g.size), ptr(g), ptr(u))
         return g
 
+    def vec_dot(self, t, k, w, x=None, xq=None):
+        """vec_dot (quant.cpp:171-191): one weight row (GGUF bytes) . one activation row (fp32 x or BlockQ8 xq)."""
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        x = None if x is None else np.ascontiguousarray(x, dtype=np.float32)
+        xq = None if xq is None else np.ascontiguousarray(xq, dtype=BLOCK_Q8)
+        f = self._f("vec_dot")
+        f.restype = ctypes.c_float
+        return np.float32(f(ctypes.c_int(t), ctypes.c_int64(k), ptr(w), ptr(x), ptr(xq)))
+
     def attend_gqa(self, q, G, D, k, v, stride, soff, n, scale, extra=None):
         q = np.ascontiguousarray(q, dtype=np.float32)
         out = np.zeros(G * D, dtype=np.float32)
@@ -151,8 +160,21 @@ class Oracle(_Common):
         self.lib.or_top2(ptr(l), ctypes.c_int(l.size), ctypes.byref(a), ctypes.byref(b))
         return a.value, b.value
 
-    def model(self, path, n_ctx, n_seq=1, wide=True):
-        return OracleModel(self, path, n_ctx, n_seq, wide)
+    def matmul_rows(self, t, w, rows, cols, x=None, xq=None, n=1):
+        """matmul's row path (quant.cpp:330-351)."""
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        x = None if x is None else np.ascontiguousarray(x, dtype=np.float32)
+        xq = None if xq is None else np.ascontiguousarray(xq, dtype=BLOCK_Q8)
+        y = np.zeros((n, rows), dtype=np.float32)
+        rc = self.lib.or_matmul_rows(ctypes.c_int(t), ptr(w), ctypes.c_size_t(row_size(t, cols)), ctypes.c_int64(rows),
+                                     ctypes.c_int64(cols), ptr(x), ptr(xq), ctypes.c_int(n), ptr(y),
+                                     ctypes.c_int64(rows))
+        if rc != 0:
+            raise RuntimeError("unsupported type")
+        return y
+
+    def model(self, path, n_ctx, n_seq=1, wide=True, no_pack=False):
+        return OracleModel(self, path, n_ctx, n_seq, wide | (2 if no_pack else 0))
 
 
 class _ModelBase:
@@ -167,7 +189,7 @@ class OracleModel(_ModelBase):
     def __init__(self, o, path, n_ctx, n_seq, wide):
         self.L = o.lib
         self.errbuf = ctypes.create_string_buffer(512)
-        self.h = self.L.or_model_open(path.encode(), n_ctx, n_seq, 1 if wide else 0, self.errbuf, 512)
+        self.h = self.L.or_model_open(path.encode(), n_ctx, n_seq, int(wide), self.errbuf, 512)
         if not self.h:
             raise RuntimeError(self._err())
         c = (ctypes.c_int * 9)()
@@ -251,6 +273,17 @@ class Ref(_Common):
     def set_threads(self, n):
         self.lib.ref_set_threads(ctypes.c_int(n))
 
+    def matmul_rows(self, t, w, rows, cols, x=None, xq=None, n=1):
+        """The reference's matmul over an unpacked weight: its row path (quant.cpp:330-351)."""
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        x = np.zeros((n, cols), np.float32) if x is None else np.ascontiguousarray(x, dtype=np.float32)
+        xq = np.zeros(n * (cols // 32), BLOCK_Q8) if xq is None else np.ascontiguousarray(xq, dtype=BLOCK_Q8)
+        h = self.lib.ref_weight_new(t, ptr(w), rows, cols, 0)
+        y = np.zeros((n, rows), dtype=np.float32)
+        self.lib.ref_weight_matmul(_P(h), ptr(x), ptr(xq), ctypes.c_int(n), ptr(y))
+        self.lib.ref_weight_free(_P(h))
+        return y
+
     def matmul(self, t, w, rows, cols, xq, mode=1):
         """mode 1: compact panels; 2: compact + wide (as the engine packs them, engine.cpp:130-145)."""
         w = np.ascontiguousarray(w, dtype=np.uint8)
@@ -263,15 +296,16 @@ class Ref(_Common):
         self.lib.ref_weight_free(_P(h))
         return y
 
-    def model(self, path, n_ctx, n_seq=1, wide=True):
-        return RefModel(self, path, n_ctx, n_seq, wide)
+    def model(self, path, n_ctx, n_seq=1, wide=True, no_pack=False):
+        """no_pack: the reference's MALKIN_NO_PACK (model.cpp:136): no panels, every matmul on the row path."""
+        return RefModel(self, path, n_ctx, n_seq, (1 if wide else 0) | (2 if no_pack else 0))
 
 
 class RefModel(_ModelBase):
     def __init__(self, r, path, n_ctx, n_seq, wide):
         self.L = r.lib
         self.errbuf = ctypes.create_string_buffer(512)
-        self.h = self.L.ref_model_open(path.encode(), n_ctx, n_seq, 1 if wide else 0, self.errbuf, 512)
+        self.h = self.L.ref_model_open(path.encode(), n_ctx, n_seq, int(wide), self.errbuf, 512)
         if not self.h:
             raise RuntimeError(self._err())
         c = (ctypes.c_int * 8)()

@@ -239,6 +239,168 @@ float or_dot_f32(int64_t k, const float* w, const float* x) {
   return s;
 }
 
+/* ------------------------------------------------------------ row path
+ * vec_dot (quant.cpp:171-191): one weight row . one activation row, used by matmul's row path (quant.cpp:330-351)
+ * for F32/F16/BF16 weights and, under MALKIN_NO_PACK, for the quantized types. Each restates the register layout of
+ * its AVX-512 kernel: lane l of the 16-float accumulator, then the halving tree. Scalar expressions follow clang's
+ * default contraction (-ffp-contract=on: a*b + c in one expression becomes one fma, the left product first). */
+
+static float bf16_to_fp32(uint16_t h) {
+  const uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* kernels_avx512.cpp:91-107: dot_f16 / dot_bf16, the dot_f32 lanes over converted weights. */
+static float dot_half(int bf, int64_t k, const uint8_t* w, const float* x) {
+  float acc[16] = {0};
+  int64_t i = 0;
+  for (; i + 16 <= k; i += 16)
+    for (int l = 0; l < 16; ++l) {
+      const uint16_t h = ld16(w + 2 * (i + l));
+      acc[l] = fmaf(bf ? bf16_to_fp32(h) : or_fp16_to_fp32(h), x[i + l], acc[l]);
+    }
+  float s = or_reduce16(acc);
+  for (; i < k; ++i) {
+    const uint16_t h = ld16(w + 2 * i);
+    s = fmaf(bf ? bf16_to_fp32(h) : or_fp16_to_fp32(h), x[i], s);
+  }
+  return s;
+}
+
+/* Exact int dot of n int8 weights with n int8 activations. */
+static int32_t idot8(const int8_t* w, const int8_t* x, int n) {
+  int32_t s = 0;
+  for (int e = 0; e < n; ++e) s += (int32_t)w[e] * x[e];
+  return s;
+}
+
+/* kernels_avx512.cpp:110-137: blocks in pairs, lanes 0-7 the first block's 4-byte groups, lanes 8-15 the second's;
+   an odd last block is added after the tree, s += float(dot) * dw * dx. */
+static float dot_q8_0_rows(int64_t k, const uint8_t* w, const or_block_q8* x) {
+  const int64_t nb = k / 32;
+  float acc[16] = {0};
+  int64_t i = 0;
+  for (; i + 2 <= nb; i += 2)
+    for (int l = 0; l < 16; ++l) {
+      const int64_t b = i + l / 8;
+      const uint8_t* blk = w + b * 34;
+      const int32_t dp = idot8((const int8_t*)blk + 2 + 4 * (l % 8), x[b].qs + 4 * (l % 8), 4);
+      acc[l] = fmaf((float)dp, or_fp16_to_fp32(ld16(blk)) * x[b].d, acc[l]);
+    }
+  float s = or_reduce16(acc);
+  for (; i < nb; ++i) {
+    const uint8_t* blk = w + i * 34;
+    const int32_t dp = idot8((const int8_t*)blk + 2, x[i].qs, 32);
+    s = fmaf((float)dp * or_fp16_to_fp32(ld16(blk)), x[i].d, s);
+  }
+  return s;
+}
+
+/* kernels_avx512.cpp:31-64 (dot_qk_45): per super-block and sub-block pair j, lanes 0-7 the 4-value groups of
+   sub-block 2j (low nibbles), lanes 8-15 those of 2j + 1 (high nibbles); Q5_K adds the high bit of each value.
+   mins is one scalar chain: mins = fma(dmin, fma(m0 * dx0, S0, (m1 * dx1) * S1), mins). */
+static float dot_qk_45_rows(int high, int64_t k, const uint8_t* w, const or_block_q8* x) {
+  const size_t bytes = high ? 176 : 144;
+  float acc[16] = {0};
+  float mins = 0.0f;
+  for (int64_t i = 0; i < k / 256; ++i, w += bytes, x += 8) {
+    const float d = or_fp16_to_fp32(ld16(w)), dmin = or_fp16_to_fp32(ld16(w + 2));
+    const uint8_t* qh = w + 16;
+    const uint8_t* q = w + (high ? 48 : 16);
+    for (int j = 0; j < 4; ++j, q += 32) {
+      int s0, m0, s1, m1;
+      scale_min_k4(2 * j, w + 4, &s0, &m0);
+      scale_min_k4(2 * j + 1, w + 4, &s1, &m1);
+      const or_block_q8* x0 = x + 2 * j;
+      const or_block_q8* x1 = x + 2 * j + 1;
+      const float sc0 = d * (float)s0 * x0->d, sc1 = d * (float)s1 * x1->d;
+      for (int l = 0; l < 16; ++l) {
+        const int hi = l >= 8, g = l % 8;
+        int32_t dp = 0;
+        for (int e = 0; e < 4; ++e) {
+          const int idx = 4 * g + e;
+          int v = hi ? q[idx] >> 4 : q[idx] & 0xF;
+          if (high) v |= ((qh[idx] >> (2 * j + hi)) & 1) << 4;
+          dp += v * (hi ? x1 : x0)->qs[idx];
+        }
+        acc[l] = fmaf((float)dp, hi ? sc1 : sc0, acc[l]);
+      }
+      const float in = fmaf((float)m0 * x0->d, (float)(x0->s[0] + x0->s[1]), ((float)m1 * x1->d) * (float)(x1->s[0] + x1->s[1]));
+      mins = fmaf(dmin, in, mins);
+    }
+  }
+  return or_reduce16(acc) - mins;
+}
+
+/* kernels_avx512.cpp:142-171 (dot_q6_k): per 128-value half, lanes 0-7 / 8-15 the 4-value groups of its first /
+   second 32 values (unsigned q, 0..63) times the 16-value sub-block scale, then the third / fourth 32 values; the
+   q - 32 offset comes back through bias = fma(d * dx * 32, sc0 * s0 + sc1 * s1, bias). */
+static float dot_q6_k_rows(int64_t k, const uint8_t* w, const or_block_q8* x) {
+  float acc[16] = {0};
+  float bias = 0.0f;
+  for (int64_t i = 0; i < k / 256; ++i, w += 210) {
+    const uint8_t* ql = w;
+    const uint8_t* qh = w + 128;
+    const int8_t* sc = (const int8_t*)(w + 192);
+    const float d = or_fp16_to_fp32(ld16(w + 208));
+    for (int n = 0; n < 2; ++n, ql += 64, qh += 32, sc += 8, x += 4) {
+      /* q of value v (0..127) of this half: groups of 32 per (low/high nibble, first/second 32 bytes) */
+      int q[128];
+      for (int l = 0; l < 32; ++l) {
+        q[l] = (ql[l] & 0xF) | ((qh[l] & 3) << 4);
+        q[32 + l] = (ql[32 + l] & 0xF) | (((qh[l] >> 2) & 3) << 4);
+        q[64 + l] = (ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4);
+        q[96 + l] = (ql[32 + l] >> 4) | (((qh[l] >> 6) & 3) << 4);
+      }
+      for (int pass = 0; pass < 2; ++pass)
+        for (int l = 0; l < 16; ++l) {
+          const int grp = 2 * pass + l / 8;  /* 32-value group: x block grp of this half */
+          int32_t dp = 0;
+          for (int e = 0; e < 4; ++e) dp += q[32 * grp + 4 * (l % 8) + e] * x[grp].qs[4 * (l % 8) + e];
+          const int32_t scl = sc[4 * pass + l / 4];
+          acc[l] = fmaf((float)(dp * scl), d * x[grp].d, acc[l]);
+        }
+      for (int g = 0; g < 4; ++g)
+        bias = fmaf(d * x[g].d * 32.0f, (float)(sc[2 * g] * x[g].s[0] + sc[2 * g + 1] * x[g].s[1]), bias);
+    }
+  }
+  return or_reduce16(acc) - bias;
+}
+
+float or_vec_dot(int type, int64_t k, const uint8_t* w, const float* x, const or_block_q8* xq) {
+  switch (type) {
+    case OR_F32:
+      return or_dot_f32(k, (const float*)w, x);
+    case OR_F16:
+      return dot_half(0, k, w, x);
+    case OR_BF16:
+      return dot_half(1, k, w, x);
+    case OR_Q8_0:
+      return dot_q8_0_rows(k, w, xq);
+    case OR_Q4_K:
+      return dot_qk_45_rows(0, k, w, xq);
+    case OR_Q5_K:
+      return dot_qk_45_rows(1, k, w, xq);
+    case OR_Q6_K:
+      return dot_q6_k_rows(k, w, xq);
+    default:
+      return NAN;
+  }
+}
+
+/* quant.cpp:330-351: y[t][r] = vec_dot(row r, token t). */
+int or_matmul_rows(int type, const uint8_t* w, size_t row_bytes, int64_t rows, int64_t cols, const float* x,
+                   const or_block_q8* xq, int n, float* y, int64_t y_stride) {
+  if (or_row_size(type, cols) == 0) return -1;
+  for (int t = 0; t < n; ++t)
+    for (int64_t r = 0; r < rows; ++r)
+      y[(int64_t)t * y_stride + r] = or_vec_dot(type, cols, w + (size_t)r * row_bytes, x + (int64_t)t * cols,
+                                                xq ? xq + (int64_t)t * (cols / 32) : NULL);
+  return 0;
+}
+
 /* kernels_avx512.cpp:186-202: max(x, -87), Cody-Waite reduction, degree-6 Taylor, scalef. */
 float or_exp(float x) {
   x = fmaxf(x, -87.0f); /* _mm512_max_ps(x, -87): NaN x gives -87, as fmaxf */
@@ -746,7 +908,7 @@ enum { kMaxBatch = 256 }; /* model.h:35 */
 struct or_model {
   or_gguf g;
   or_config c;
-  int n_ctx, n_seq, wide;
+  int n_ctx, n_seq, wide, no_pack;
   or_weight tok_embd, output;
   const float* output_norm;
   or_layer* layers;
@@ -869,7 +1031,8 @@ or_model* or_model_open(const char* path, int n_ctx, int n_seq, int wide, char* 
 #undef NORM
 #undef W
   }
-  m->wide = wide;
+  m->wide = wide & 1;
+  m->no_pack = (wide & 2) != 0; /* MALKIN_NO_PACK (model.cpp:136): every matmul on the row path */
   m->inv_freq = (float*)malloc(sizeof(float) * c->head_dim / 2);
   for (int i = 0; i < c->head_dim / 2; ++i)
     m->inv_freq[i] = powf(c->rope_base, -2.0f * (float)i / (float)c->head_dim); /* model.cpp:137 */
@@ -920,8 +1083,13 @@ static void quantize_acts(const float* x, int n, int64_t k, or_block_q8* out) {
   for (int t = 0; t < n; ++t) or_quantize_row_q8(x + (int64_t)t * k, out + (int64_t)t * (k / 32), k);
 }
 
-static void matmul(const or_model* m, const or_weight* w, const or_block_q8* xq, int n, float* y) {
-  or_matmul(w->type, w->data, w->row_bytes, w->rows, w->cols, xq, n, y, w->rows, m->wide);
+/* quant.cpp:320-351: panels for the quantized types unless MALKIN_NO_PACK; F32/F16/BF16 have no panels (row path). */
+static void matmul(const or_model* m, const or_weight* w, const float* x, const or_block_q8* xq, int n, float* y) {
+  const int rows_path = m->no_pack || w->type == OR_F32 || w->type == OR_F16 || w->type == OR_BF16;
+  if (rows_path)
+    or_matmul_rows(w->type, w->data, w->row_bytes, w->rows, w->cols, x, xq, n, y, w->rows);
+  else
+    or_matmul(w->type, w->data, w->row_bytes, w->rows, w->cols, xq, n, y, w->rows, m->wide);
 }
 
 /* model.cpp:204-247 (AVX-512 attends one token per call, attend_block_tokens = 1) */
@@ -965,9 +1133,9 @@ static int run(or_model* m, const int32_t* tokens, int n, float* logits, char* e
     const or_layer* L = &m->layers[il];
     for (int t = 0; t < n; ++t) or_rmsnorm(m->h + (size_t)t * E, m->x + (size_t)t * E, L->attn_norm, E, c->rms_eps);
     quantize_acts(m->h, n, E, m->xq);
-    matmul(m, &L->wq, m->xq, n, m->q);
-    matmul(m, &L->wk, m->xq, n, m->k);
-    matmul(m, &L->wv, m->xq, n, m->v);
+    matmul(m, &L->wq, m->h, m->xq, n, m->q);
+    matmul(m, &L->wk, m->h, m->xq, n, m->k);
+    matmul(m, &L->wv, m->h, m->xq, n, m->v);
     const size_t layer = (size_t)il * m->n_seq * m->n_ctx;
     for (int t = 0; t < n; ++t) {
       const float* cs = m->cs + t * D / 2;
@@ -995,22 +1163,22 @@ static int run(or_model* m, const int32_t* tokens, int n, float* logits, char* e
     }
     attention(m, il, n);
     quantize_acts(m->att, n, (int64_t)H * D, m->xq);
-    matmul(m, &L->wo, m->xq, n, m->h);
+    matmul(m, &L->wo, m->att, m->xq, n, m->h);
     for (size_t i = 0; i < (size_t)n * E; ++i) m->x[i] += m->h[i];
     for (int t = 0; t < n; ++t) or_rmsnorm(m->h + (size_t)t * E, m->x + (size_t)t * E, L->ffn_norm, E, c->rms_eps);
     quantize_acts(m->h, n, E, m->xq);
-    matmul(m, &L->w_gate, m->xq, n, m->gate);
-    matmul(m, &L->w_up, m->xq, n, m->up);
+    matmul(m, &L->w_gate, m->h, m->xq, n, m->gate);
+    matmul(m, &L->w_up, m->h, m->xq, n, m->up);
     for (int t = 0; t < n; ++t) or_silu_mul(F, m->gate + (size_t)t * F, m->up + (size_t)t * F);
     quantize_acts(m->gate, n, F, m->xq);
-    matmul(m, &L->w_down, m->xq, n, m->h);
+    matmul(m, &L->w_down, m->gate, m->xq, n, m->h);
     for (size_t i = 0; i < (size_t)n * E; ++i) m->x[i] += m->h[i];
   }
   if (m->n_out == 0) return 0;
   for (int i = 0; i < m->n_out; ++i)
     or_rmsnorm(m->h + (size_t)i * E, m->x + (size_t)m->out[i] * E, m->output_norm, E, c->rms_eps);
   quantize_acts(m->h, m->n_out, E, m->xq);
-  matmul(m, &m->output, m->xq, m->n_out, logits);
+  matmul(m, &m->output, m->h, m->xq, m->n_out, logits);
   return 0;
 }
 

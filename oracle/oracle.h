@@ -43,6 +43,12 @@ float or_quantize_i8(const float* x, int n, int8_t* q);
 int or_dequantize_row(int type, const void* src, float* dst, int64_t k);
 /* kernels_avx512.cpp:82-89 */
 float or_dot_f32(int64_t k, const float* w, const float* x);
+/* vec_dot (quant.cpp:171-191; kernels_avx512.cpp:82-171): the row path's dot of one weight row (GGUF bytes of
+   `type`) with one activation row (x: fp32, used by F32/F16/BF16; xq: BlockQ8, used by the quantized types). */
+float or_vec_dot(int type, int64_t k, const uint8_t* w, const float* x, const or_block_q8* xq);
+/* matmul's row path (quant.cpp:330-351): y[t * y_stride + r] = vec_dot(row r, x[t], xq[t]). -1 for unknown types. */
+int or_matmul_rows(int type, const uint8_t* w, size_t row_bytes, int64_t rows, int64_t cols, const float* x,
+                   const or_block_q8* xq, int n, float* y, int64_t y_stride);
 /* _mm512_reduce_add_ps: halving tree (i, i+8), (i, i+4), (i, i+2), (0, 1) */
 float or_reduce16(const float* v);
 /* kernels_avx512.cpp:186-202, one lane */

@@ -5,6 +5,7 @@
 #include <omp.h>
 
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <exception>
 #include <memory>
@@ -98,12 +99,22 @@ void ref_weight_matmul(void* h, const float* x, const void* xq, int n, float* y)
 }
 void ref_weight_free(void* h) { delete static_cast<RefWeight*>(h); }
 
-void* ref_model_open(const char* path, int n_ctx, int n_seq, int wide, char* err, int errlen) {
+// flags: 1 = pack the wide prefill panels (as the engine does when RAM allows); 2 = MALKIN_NO_PACK (model.cpp:136),
+// set in the environment only while the Model is constructed.
+void* ref_model_open(const char* path, int n_ctx, int n_seq, int flags, char* err, int errlen) {
   try {
     auto m = std::make_unique<RefModel>();
     m->file = std::make_unique<GgufFile>(path);
-    m->model = std::make_unique<Model>(*m->file, n_ctx, n_seq);
-    if (wide && m->model->wide_bytes() > 0) m->model->pack_wide();
+    if (flags & 2) setenv("MALKIN_NO_PACK", "1", 1);
+    try {
+      m->model = std::make_unique<Model>(*m->file, n_ctx, n_seq);
+    } catch (...) {
+      if (flags & 2) unsetenv("MALKIN_NO_PACK");
+      throw;
+    }
+    if (flags & 2) unsetenv("MALKIN_NO_PACK");
+    // Model::wide_bytes is 0 under MALKIN_NO_PACK (model.cpp:181): no wide panels then either.
+    if ((flags & 1) && !(flags & 2) && m->model->wide_bytes() > 0) m->model->pack_wide();
     return m.release();
   } catch (const std::exception& e) {
     set_err(err, errlen, e.what());

@@ -137,6 +137,11 @@ MODEL_CFGS = {
     "tiny-tied": dict(preset="tiny-tied", wtype=synth.Q8_0, seed=11),
     "tiny-q6k": dict(preset="tiny", wtype=synth.Q6_K, seed=13),
     "tiny-q4km": dict(preset="tiny", wtype=synth.Q4_K, mix=synth.MIX_Q4_K_M, seed=17),
+    # the row path (quant.cpp:171-191, 330-351): F16 / BF16 weights always, the quantized types under MALKIN_NO_PACK
+    "tiny-f16": dict(preset="tiny", wtype=synth.F16, seed=19),
+    "tiny-bf16": dict(preset="tiny-tied", wtype=synth.BF16, seed=23),
+    "tiny-nopack": dict(preset="tiny", wtype=synth.Q8_0, seed=29, no_pack=True),
+    "tiny-q4km-nopack": dict(preset="tiny", wtype=synth.Q4_K, mix=synth.MIX_Q4_K_M, seed=31, no_pack=True),
 }
 
 
@@ -149,12 +154,13 @@ def model_path(tmp, name):
 
 
 def gen_models(ref, rng):
+    # one generator in MODEL_CFGS order: models appended at the end leave the earlier fixtures unchanged
     out = {}
     with tempfile.TemporaryDirectory() as tmp:
         for name in MODEL_CFGS:
             p = model_path(tmp, name)
             out[f"{name}_sha256"] = np.frombuffer(bytes.fromhex(sha256(p)), dtype=np.uint8)
-            m = ref.model(p, 256, 2)
+            m = ref.model(p, 256, 2, no_pack=MODEL_CFGS[name].get("no_pack", False))
             V = m.cfg["n_vocab"]
             prompt = rng.integers(0, V, size=24).astype(np.int32)
             logits = m.forward(prompt, 0, all_logits=True)

@@ -94,11 +94,12 @@ def test_attention_golden(oracle, golden):
 
 def test_model_golden(oracle, golden, model_files):
     import hashlib
+    import make_golden
     g = golden("models.npz")
     for name, path in model_files.items():
         with open(path, "rb") as f:
             assert hashlib.sha256(f.read()).digest() == bytes(g[f"{name}_sha256"]), f"synthetic {name} drifted"
-        m = oracle.model(path, 256, 2)
+        m = oracle.model(path, 256, 2, no_pack=make_golden.MODEL_CFGS[name].get("no_pack", False))
         logits = m.forward(g[f"{name}_prompt"], 0, all_logits=True)
         assert np.array_equal(bits(logits), bits(g[f"{name}_prompt_logits"])), name
         toks, last = [], logits[-1]
@@ -127,6 +128,54 @@ def test_against_reference_random(oracle, ref):
         k = int(rng.choice([16, 100, 128, 4096]))
         w = rng.standard_normal(k).astype(np.float32)
         assert bits(oracle.dot_f32(w, w)) == bits(ref.dot_f32(w, w))
+
+
+def _row_weights(rng, t, rows, k):
+    import make_golden
+    if t == bind.F32:
+        return rng.standard_normal((rows, k)).astype(np.float32).view(np.uint8).reshape(rows, -1)
+    if t == bind.F16:
+        return rng.standard_normal((rows, k)).astype(np.float16).view(np.uint8).reshape(rows, -1)
+    if t == bind.BF16:
+        h = (rng.standard_normal((rows, k)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        return h.view(np.uint8).reshape(rows, -1)
+    return make_golden.random_rows(rng, t, rows, k)
+
+
+ROW_CASES = [(t, k) for t in (bind.F32, bind.F16, bind.BF16) for k in (40, 512, 4096)] + \
+    [(bind.Q8_0, k) for k in (512, 544, 4096)] + [(t, k) for t in (bind.Q4_K, bind.Q5_K, bind.Q6_K) for k in (512, 4096)]
+
+
+@pytest.mark.parametrize("t,k", ROW_CASES)
+def test_row_path_against_reference(oracle, ref, t, k):
+    """The row path (vec_dot, quant.cpp:171-191): F types with a k % 16 tail, Q8_0 with an odd last block."""
+    rng = np.random.default_rng(t * 10007 + k)
+    w = _row_weights(rng, t, 6, k)
+    x = rng.uniform(-2, 2, (3, k)).astype(np.float32)
+    x[:, ::97] *= 50
+    xq = ref.quantize_row_q8(x) if k % 32 == 0 else None
+    yo = oracle.matmul_rows(t, w, 6, k, x=x, xq=xq, n=3)
+    yr = ref.matmul_rows(t, w, 6, k, x=x, xq=xq, n=3)
+    assert np.array_equal(bits(yo), bits(yr))
+
+
+@pytest.mark.parametrize("t,k", [(t, k) for t, k in ROW_CASES if k >= 512])
+def test_row_path_vs_float64(oracle, t, k):
+    """Independent of the reference: every row-path output is the dot of the dequantized operands (float64) within
+    the reference's own |d|/rms < 1e-5 (test_quant.cpp:250-256); the F types against the fp32 activations."""
+    rng = np.random.default_rng(t + k)
+    w = _row_weights(rng, t, 8, k)
+    x = rng.uniform(-2, 2, (2, k)).astype(np.float32)
+    xq = oracle.quantize_row_q8(x)
+    y = oracle.matmul_rows(t, w, 8, k, x=x, xq=xq, n=2)
+    wd = np.stack([oracle.dequantize_row(t, w[r], k) for r in range(8)]).astype(np.float64)
+    if t in (bind.F32, bind.F16, bind.BF16):
+        xd = x.astype(np.float64)
+    else:  # the BlockQ8 values d * q, exactly
+        xd = (xq["d"].astype(np.float64)[..., None] * xq["qs"].astype(np.float64)).reshape(2, k)
+    exp = xd @ wd.T
+    err = np.abs(y - exp).max() / np.sqrt((exp ** 2).mean())
+    assert err < 1e-5, err
 
 
 def test_model_against_reference(oracle, ref, model_files):
