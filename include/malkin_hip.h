@@ -128,6 +128,13 @@ int mk_matmul_f32(mk_ctx* ctx, const mk_weight* w, const float* x, int64_t x_str
 int mk_matmul_rows(mk_ctx* ctx, int type, const void* w, size_t row_bytes, int64_t rows, int64_t cols, const float* x,
                    int64_t x_stride, const void* xq, int n, float* y, int64_t y_stride, int accumulate);
 
+/* The reference's Q4_K / Q5_K panel arithmetic (gemm_avx512.cpp:104-155 compact, 217-266 wide: one sequence per output
+   over its 32-value sub-blocks, acc = fma(float(int dot), (d*sc)*dx, acc), acc = fma(-(dmin*m), dx*(s0+s1), acc)) read
+   straight from GGUF rows: the device path of Q5_K weights, which have no CDNA layout. Same results as mk_matmul's
+   packed Q4_K kernels for Q4_K. */
+int mk_matmul_gguf(mk_ctx* ctx, int type, const void* w, size_t row_bytes, int64_t rows, int64_t cols, const void* xq,
+                   int n, float* y, int64_t y_stride, int accumulate);
+
 /* ---- elementwise (model.cpp:46-49, kernels.h:39) ---- */
 /* y = rmsnorm(x) * w per row of n floats (model.cpp:46-49). */
 int mk_rmsnorm(mk_ctx* ctx, const float* x, const float* w, int rows, int n, float eps, float* y);

@@ -54,6 +54,7 @@ SIGNATURES = {
     "mk_silu_mul": (_I, [_P, _I64, _P, _P]),
     "mk_rmsnorm_rows": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),
     "mk_silu_mul_rows": (_I, [_P, _P, _I, _I64]),
+    "mk_matmul_gguf": (_I, [_P, _I, _P, _SZ, _I64, _I64, _P, _I, _P, _I64, _I]),
     "mk_matmul_rows": (_I, [_P, _I, _P, _SZ, _I64, _I64, _P, _I64, _P, _I, _P, _I64, _I]),
     "mk_silu_mul_q8": (_I, [_P, _P, _I, _I64, _I, _P]),
     "mk_add": (_I, [_P, _I64, _P, _P]),

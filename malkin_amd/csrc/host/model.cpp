@@ -98,11 +98,9 @@ void Model::load_weight(const GgufFile& f, const std::vector<std::string>& names
   for (const auto& nm : names) {
     const GgufTensor* t = f.tensor(nm);
     if (!t) throw std::runtime_error("model: tensor " + nm + " missing");
-    const bool packable = device_type(t->type), rowable = row_type(t->type);
-    if (!rowable || (!packable && !no_pack_ && !raw_only_type(t->type)))
+    if (!row_type(t->type))
       throw std::runtime_error("model: tensor " + nm + " has type " + ggml_type_name(t->type) +
-                               ", supported on the device: Q8_0 Q4_K Q6_K (packed), F32 F16 BF16 (row path), Q5_K "
-                               "(row path, with no_pack)");
+                               ", supported on the device: Q8_0 Q4_K Q5_K Q6_K F32 F16 BF16");
     ts.push_back(t);
   }
   w.type = static_cast<int>(ts[0]->type);
@@ -112,7 +110,8 @@ void Model::load_weight(const GgufFile& f, const std::vector<std::string>& names
     if (t->type != ts[0]->type || t->ne[0] != w.cols) throw std::runtime_error("model: fused weights differ in type");
     w.rows += t->rows();
   }
-  w.raw = no_pack_ || raw_only_type(w.type);
+  w.raw = no_pack_ || !device_type(w.type);
+  w.rowdot = no_pack_ || raw_only_type(w.type);
   w.row_bytes = ggml_row_size(w.type, w.cols);
   if (interleave4 && (w.raw || ts.size() != 2 || ts[0]->rows() != ts[1]->rows() || ts[0]->rows() % 4))
     throw std::runtime_error("model: interleaved weights need two packed matrices of equal rows, a multiple of 4");
@@ -293,12 +292,12 @@ Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide, bo
     upload_norm(p + "ffn_norm.weight", E, L.norms.as<float>() + E);
     upload_norm(p + "attn_q_norm.weight", D, L.norms.as<float>() + 2 * E);
     upload_norm(p + "attn_k_norm.weight", D, L.norms.as<float>() + 2 * E + D);
-    // A layer with any weight on the row path runs the reference's unfused sequence (fp32 activations kept for
+    // A layer with any weight kept as GGUF rows runs the reference's unfused sequence (fp32 activations kept for
     // the row dots); its gate|up stays [gate | up].
     L.row_flow = no_pack_;
     for (const char* nm : {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"}) {
       const GgufTensor* t = f.tensor(p + nm + ".weight");
-      if (t && raw_only_type(t->type)) L.row_flow = true;
+      if (t && !device_type(t->type)) L.row_flow = true;
     }
     load_group(f, {p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"}, L.qkv);
     load_weight(f, {p + "attn_output.weight"}, L.wo);
@@ -609,12 +608,16 @@ void Model::run() {
   }
   const int m = n_out();
   if (m == 0) return;
-  if (output_.raw) {  // model.cpp:419-425 on the row path: fp32 normalized rows and their BlockQ8 rows
+  if (output_.raw) {  // model.cpp:419-425 over GGUF rows: fp32 normalized rows and their BlockQ8 rows
     float* h = h_.as<float>();
     ck(mk_rmsnorm_rows(ctx_, x, d_out_, output_norm_.as<float>(), m, E, c.rms_eps, h));
     if (!raw_only_type(output_.type)) ck(mk_quantize_q8(ctx_, h, m, E, xq));
-    ck(mk_matmul_rows(ctx_, output_.type, output_.packed.p, output_.row_bytes, output_.rows, output_.cols, h, E, xq, m,
-                      logits_.as<float>(), c.n_vocab, 0));
+    if (output_.rowdot)
+      ck(mk_matmul_rows(ctx_, output_.type, output_.packed.p, output_.row_bytes, output_.rows, output_.cols, h, E, xq,
+                        m, logits_.as<float>(), c.n_vocab, 0));
+    else
+      ck(mk_matmul_gguf(ctx_, output_.type, output_.packed.p, output_.row_bytes, output_.rows, output_.cols, xq, m,
+                        logits_.as<float>(), c.n_vocab, 0));
     return;
   }
   ck(mk_rmsnorm_q8(ctx_, x, d_out_, output_norm_.as<float>(), m, E, c.rms_eps, xq));
@@ -626,9 +629,11 @@ void Model::run() {
 
 void Model::matmul_any(const Group& g, const float* xf, int64_t xfs, const void* xq, int n, float* y) {
   for (const Weight& p : g.parts) {
-    if (p.raw) {
+    if (p.raw && p.rowdot) {
       ck(mk_matmul_rows(ctx_, p.type, p.packed.p, p.row_bytes, p.rows, p.cols, xf, xfs, xq, n, y + p.out_off, g.rows,
                         0));
+    } else if (p.raw) {
+      ck(mk_matmul_gguf(ctx_, p.type, p.packed.p, p.row_bytes, p.rows, p.cols, xq, n, y + p.out_off, g.rows, 0));
     } else {
       mk_weight w = p.w();
       w.wide = wide_ ? 1 : 0;
@@ -652,8 +657,10 @@ void Model::run_row_layer(const Layer& L, int il) {
   void* xq = xq_.p;
   const float* norms = L.norms.as<float>();
   auto single = [&](const Weight& w, const float* xf, int64_t xfs, float* y, int64_t ys) {
-    if (w.raw) {
+    if (w.raw && w.rowdot) {
       ck(mk_matmul_rows(ctx_, w.type, w.packed.p, w.row_bytes, w.rows, w.cols, xf, xfs, xq, n, y, ys, 1));
+    } else if (w.raw) {
+      ck(mk_matmul_gguf(ctx_, w.type, w.packed.p, w.row_bytes, w.rows, w.cols, xq, n, y, ys, 1));
     } else {
       mk_weight mw = w.w();
       mw.wide = wide_ ? 1 : 0;

@@ -128,7 +128,9 @@ class Model {
     int type = 0;
     int64_t rows = 0, cols = 0;
     int64_t out_off = 0;  // first output row within its group (q|k|v, gate|up)
-    bool raw = false;     // GGUF rows for the row path (mk_matmul_rows) instead of the CDNA layout
+    bool raw = false;     // kept as GGUF rows (no CDNA layout)
+    bool rowdot = false;  // raw: the row path's arithmetic (mk_matmul_rows); else the panel arithmetic on GGUF rows
+                          // (mk_matmul_gguf, Q5_K)
     size_t row_bytes = 0;
     DevBuf packed;
     mk_weight w() const;

@@ -276,6 +276,15 @@ int mk_matmul_rows(mk_ctx* c, int type, const void* w, size_t row_bytes, int64_t
   });
 }
 
+int mk_matmul_gguf(mk_ctx* c, int type, const void* w, size_t row_bytes, int64_t rows, int64_t cols, const void* xq,
+                   int n, float* y, int64_t y_stride, int accumulate) {
+  return guard([&] {
+    require(w != nullptr && y != nullptr && rows >= 0 && n >= 0, "matmul_gguf: bad arguments");
+    mk::matmul_gguf(c->stream, type, w, row_bytes, rows, cols, static_cast<const mk::BlockQ8*>(xq), n, y, y_stride,
+                    accumulate != 0);
+  });
+}
+
 int mk_silu_mul(mk_ctx* c, int64_t n, float* g, const float* u) {
   return guard([&] { mk::silu_mul(c->stream, n, g, u); });
 }

@@ -51,6 +51,9 @@ void silu_mul(hipStream_t s, int64_t n, float* g, const float* u);
 void silu_mul_rows(hipStream_t s, float* gu, int rows, int64_t n);
 // matmul's row path (quant.cpp:171-191, 330-351) over GGUF rows: fp32 x for F32/F16/BF16, BlockQ8 xq otherwise.
 bool rows_supported(int type, int64_t cols);
+// The Q4_K / Q5_K panel arithmetic (gemm_avx512.cpp:104-155, 217-266) over GGUF rows: Q5_K's device path.
+void matmul_gguf(hipStream_t s, int type, const void* w, size_t row_bytes, int64_t rows, int64_t cols,
+                 const BlockQ8* xq, int n, float* y, int64_t ys, bool accumulate);
 void matmul_rows(hipStream_t s, int type, const void* w, size_t row_bytes, int64_t rows, int64_t cols, const float* x,
                  int64_t xs, const BlockQ8* xq, int n, float* y, int64_t ys, bool accumulate);
 // gu rows of 2n floats: [gate | up], or (interleave4) gate/up interleaved by 4 as matmul_f32's silu_pairs rows.

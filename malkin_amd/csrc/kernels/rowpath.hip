@@ -208,6 +208,60 @@ __global__ __launch_bounds__(kRowsThreads) void k_rows(const uint8_t* __restrict
       }
 }
 
+// The panel kernels' arithmetic for Q4_K / Q5_K (gemm_avx512.cpp:104-155 compact, 217-266 wide: the same sequence)
+// read straight from GGUF rows: per output, per 32-value sub-block j in order, acc = fma(float(int dot), (d * sc) * dx,
+// acc), then acc = fma(-(dmin * m), dx * (s0 + s1), acc). An 8-lane group owns one row: lane g takes the 4-value
+// group g of each sub-block, the exact int dot is summed over the group (butterfly), and every lane keeps the same
+// chain. This is the device path for Q5_K weights, which have no CDNA layout.
+template <bool kHigh>
+__global__ __launch_bounds__(kRowsThreads) void k_gguf45(const uint8_t* __restrict__ W, size_t row_bytes, int64_t rows,
+                                                         int64_t cols, const BlockQ8* __restrict__ xq, int n,
+                                                         float* __restrict__ y, int64_t ys, int accumulate) {
+  constexpr int kBytes = kHigh ? 176 : 144;
+  const int g = threadIdx.x & 7;
+  const int64_t r = (int64_t)blockIdx.x * (kRowsThreads / 8) + threadIdx.x / 8;
+  const int t0 = blockIdx.y * kRowsNT;
+  if (r >= rows) return;  // whole 8-lane groups leave together
+  const int nt = min(kRowsNT, n - t0);
+  const uint8_t* w = W + (size_t)r * row_bytes;
+  const int64_t nb = cols / 32;
+  float acc[kRowsNT];
+#pragma unroll
+  for (int t = 0; t < kRowsNT; ++t) acc[t] = 0.0f;
+  for (int64_t sb = 0; sb < cols / 256; ++sb) {
+    const uint8_t* s = w + sb * kBytes;
+    const float d = half_to_float(ld_u16(s)), dmin = half_to_float(ld_u16(s + 2));
+    const uint32_t qh = kHigh ? (uint32_t)ld_i8x4(s + 16 + 4 * g) : 0u;
+    for (int j = 0; j < 8; ++j) {
+      int sc, m;
+      scale_min_k4(j, s + 4, sc, m);
+      const float fsc = d * (float)sc, fmn = dmin * (float)m;
+      const uint32_t qw = (uint32_t)ld_i8x4(s + (kHigh ? 48 : 16) + 32 * (j / 2) + 4 * g);
+      uint32_t v = (j & 1) ? (qw >> 4) & 0x0F0F0F0Fu : qw & 0x0F0F0F0Fu;
+      if constexpr (kHigh) v |= ((qh >> j) & 0x01010101u) << 4;
+#pragma unroll
+      for (int t = 0; t < kRowsNT; ++t)
+        if (t < nt) {
+          const BlockQ8& xb = xq[(int64_t)(t0 + t) * nb + sb * 8 + j];
+          int ai = dot4((int)v, xq_word(xb, g), 0);
+          ai += __shfl_xor(ai, 1, 8);
+          ai += __shfl_xor(ai, 2, 8);
+          ai += __shfl_xor(ai, 4, 8);
+          const float dsx = xb.d * (float)(xb.s[0] + xb.s[1]);
+          acc[t] = fma_((float)ai, fsc * xb.d, acc[t]);
+          acc[t] = fma_(-fmn, dsx, acc[t]);
+        }
+    }
+  }
+  if (g == 0)
+#pragma unroll
+    for (int t = 0; t < kRowsNT; ++t)
+      if (t < nt) {
+        float* o = y + (int64_t)(t0 + t) * ys + r;
+        *o = accumulate ? *o + acc[t] : acc[t];
+      }
+}
+
 }  // namespace
 
 bool rows_supported(int type, int64_t cols) {
@@ -248,6 +302,24 @@ void matmul_rows(hipStream_t s, int type, const void* w, size_t row_bytes, int64
     default: go(k_rows<kQ6_K>); break;
   }
   check_launch("matmul_rows");
+}
+
+void matmul_gguf(hipStream_t s, int type, const void* w, size_t row_bytes, int64_t rows, int64_t cols,
+                 const BlockQ8* xq, int n, float* y, int64_t ys, bool accumulate) {
+  require((type == kQ4_K || type == kQ5_K) && cols > 0 && cols % 256 == 0,
+          "matmul_gguf: Q4_K / Q5_K rows of a multiple of 256 values");
+  require(xq != nullptr, "matmul_gguf: missing activations");
+  if (rows <= 0 || n <= 0) return;
+  const dim3 grid((unsigned)((rows + kRowsThreads / 8 - 1) / (kRowsThreads / 8)), (unsigned)((n + kRowsNT - 1) / kRowsNT));
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(kRowsThreads), 0, s, static_cast<const uint8_t*>(w), row_bytes, rows, cols, xq,
+                       n, y, ys, accumulate ? 1 : 0);
+  };
+  if (type == kQ5_K)
+    go(k_gguf45<true>);
+  else
+    go(k_gguf45<false>);
+  check_launch("matmul_gguf");
 }
 
 }  // namespace mk

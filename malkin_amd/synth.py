@@ -9,7 +9,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmalkin_synth.so")
 
-F16, Q8_0, Q4_K, Q6_K, BF16 = 1, 8, 12, 14, 30
+F16, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 1, 8, 12, 13, 14, 30
 MIX_UNIFORM, MIX_Q4_K_M = 0, 1
 
 
@@ -80,7 +80,7 @@ def file_bytes(cfg):
     return int(lib().mks_file_bytes(ctypes.byref(cfg)))
 
 
-_BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+_BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
 
 
 def quantize_rows(wtype, x):

@@ -19,7 +19,7 @@
 #include <sys/mman.h>
 #include <unistd.h>
 
-enum { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14, T_BF16 = 30 };
+enum { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_BF16 = 30 };
 
 static uint64_t splitmix(uint64_t x) {
   x += 0x9E3779B97F4A7C15ull;
@@ -138,6 +138,53 @@ static void quant_q4_k(const float* x, uint8_t* out, int64_t k) {
   }
 }
 
+/* Q5_K: Q4_K's asymmetric sub-block ranges with 5-bit values: low nibbles in qs (Q4_K layout), the fifth bit of value l
+   of sub-block j in bit j of qh[l]. */
+static void quant_q5_k(const float* x, uint8_t* out, int64_t k) {
+  for (int64_t sb = 0; sb < k / 256; ++sb, x += 256, out += 176) {
+    float scale[8], mins[8], maxs = 0.0f, maxm = 0.0f;
+    for (int j = 0; j < 8; ++j) {
+      float lo = 0.0f, hi = x[32 * j];
+      for (int l = 0; l < 32; ++l) {
+        const float v = x[32 * j + l];
+        lo = v < lo ? v : lo;
+        hi = v > hi ? v : hi;
+      }
+      scale[j] = (hi - lo) / 31.0f;
+      mins[j] = -lo;
+      maxs = scale[j] > maxs ? scale[j] : maxs;
+      maxm = mins[j] > maxm ? mins[j] : maxm;
+    }
+    const uint16_t hd = to_half(maxs / 63.0f), hm = to_half(maxm / 63.0f);
+    const float d = from_half(hd), dmin = from_half(hm);
+    int sc[8], m[8];
+    for (int j = 0; j < 8; ++j) {
+      sc[j] = d > 0.0f ? clampi(round_(scale[j] / d), 0, 63) : 0;
+      m[j] = dmin > 0.0f ? clampi(round_(mins[j] / dmin), 0, 63) : 0;
+    }
+    put16(out, hd);
+    put16(out + 2, hm);
+    uint8_t* s = out + 4;
+    for (int j = 0; j < 4; ++j) {
+      s[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+      s[j + 4] = (uint8_t)((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+      s[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((m[j + 4] & 0xF) << 4));
+    }
+    uint8_t* qh = out + 16;
+    uint8_t* qs = out + 48;
+    memset(qh, 0, 32);
+    memset(qs, 0, 128);
+    for (int j = 0; j < 8; ++j) {
+      const float step = d * (float)sc[j], off = dmin * (float)m[j];
+      for (int l = 0; l < 32; ++l) {
+        const int q = step > 0.0f ? clampi(round_((x[32 * j + l] + off) / step), 0, 31) : 0;
+        qs[32 * (j / 2) + l] |= (uint8_t)((q & 0xF) << (4 * (j & 1)));
+        qh[l] |= (uint8_t)(((q >> 4) & 1) << j);
+      }
+    }
+  }
+}
+
 /* Q6_K: per 16-value sub-block an int8 scale under half d, q in [-32, 31] stored + 32. */
 static void quant_q6_k(const float* x, uint8_t* out, int64_t k) {
   for (int64_t sb = 0; sb < k / 256; ++sb, x += 256, out += 210) {
@@ -189,6 +236,8 @@ static size_t row_bytes(int type, int64_t k) {
       return (size_t)(k / 32) * 34;
     case T_Q4_K:
       return (size_t)(k / 256) * 144;
+    case T_Q5_K:
+      return (size_t)(k / 256) * 176;
     case T_Q6_K:
       return (size_t)(k / 256) * 210;
     default:
@@ -291,6 +340,9 @@ static void gen_row(const job* j, const tinfo* t, int ti, int64_t r, float* buf)
     case T_Q4_K:
       quant_q4_k(buf, dst, t->ne0);
       break;
+    case T_Q5_K:
+      quant_q5_k(buf, dst, t->ne0);
+      break;
     case T_Q6_K:
       quant_q6_k(buf, dst, t->ne0);
       break;
@@ -385,12 +437,15 @@ static size_t header(wbuf* w, const mks_config* c, const tinfo* t, int nt) {
 
 int mks_quantize_rows(int type, const float* x, int64_t rows, int64_t k, uint8_t* out) {
   const size_t rb = row_bytes(type, k);
-  if (!rb || (type != T_Q8_0 && type != T_Q4_K && type != T_Q6_K) || k % (type == T_Q8_0 ? 32 : 256)) return -2;
+  if (!rb || (type != T_Q8_0 && type != T_Q4_K && type != T_Q5_K && type != T_Q6_K) || k % (type == T_Q8_0 ? 32 : 256))
+    return -2;
   for (int64_t r = 0; r < rows; ++r, x += k, out += rb) {
     if (type == T_Q8_0)
       quant_q8_0(x, out, k);
     else if (type == T_Q4_K)
       quant_q4_k(x, out, k);
+    else if (type == T_Q5_K)
+      quant_q5_k(x, out, k);
     else
       quant_q6_k(x, out, k);
   }

@@ -14,8 +14,8 @@ typedef struct {
   int n_layer, n_embd, n_ff, n_head, n_head_kv, head_dim, n_vocab, n_ctx_train;
   float rope_base, rms_eps;
   int tied;     /* 1: no output.weight (LM head = token_embd, model.cpp:116-118) */
-  int type;     /* ggml type of every matmul weight and token_embd under MKS_MIX_UNIFORM: 8 Q8_0, 12 Q4_K, 14 Q6_K,
-                   1 F16, 30 BF16 */
+  int type;     /* ggml type of every matmul weight and token_embd under MKS_MIX_UNIFORM: 8 Q8_0, 12 Q4_K, 13 Q5_K,
+                   14 Q6_K, 1 F16, 30 BF16 */
   int mix;      /* MKS_MIX_* */
   float std;    /* weight standard deviation (0.02) */
   uint64_t seed;

@@ -142,6 +142,8 @@ MODEL_CFGS = {
     "tiny-bf16": dict(preset="tiny-tied", wtype=synth.BF16, seed=23),
     "tiny-nopack": dict(preset="tiny", wtype=synth.Q8_0, seed=29, no_pack=True),
     "tiny-q4km-nopack": dict(preset="tiny", wtype=synth.Q4_K, mix=synth.MIX_Q4_K_M, seed=31, no_pack=True),
+    # Q5_K: the panel arithmetic (gemm_avx512.cpp:104-155, kHigh)
+    "tiny-q5k": dict(preset="tiny", wtype=synth.Q5_K, seed=37),
 }
 
 

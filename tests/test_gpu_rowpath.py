@@ -102,3 +102,66 @@ def test_row_path_model_golden(row_models, golden, name):
     assert list(out) == list(g[f"{name}_greedy"])
     batch = g[f"{name}_tree_batch"].astype(np.int32).view(mk_.BATCH_TOKEN).reshape(-1)
     assert np.array_equal(bits(m.forward_batch(batch)), bits(g[f"{name}_tree_logits"])), name
+
+
+@pytest.mark.parametrize("t", [bind.Q4_K, bind.Q5_K])
+@pytest.mark.parametrize("n", [1, 5, 17, 40])
+def test_matmul_gguf_panel_arithmetic(mk, oracle, t, n):
+    """mk_matmul_gguf: the Q4_K / Q5_K panel arithmetic over GGUF rows, against the oracle's panel restatement (and,
+    for Q4_K, against the packed kernels of mk_matmul)."""
+    import make_golden
+    rng = np.random.default_rng(t * 31 + n)
+    rows, k = 72, 1024
+    w = make_golden.random_rows(rng, t, rows, k)
+    x = rng.uniform(-2, 2, (n, k)).astype(np.float32)
+    xq = oracle.quantize_row_q8(x)
+    exp = oracle.matmul(t, w, rows, k, xq.reshape(-1))
+    dw, dq, dy = mk.to_device(w), mk.to_device(xq), mk.alloc(n * rows * 4)
+    print("gguf panel", t, n, flush=True)
+    mk_.check(mk_.load().mk_matmul_gguf(mk.h, t, dw.ptr, w.shape[1], rows, k, dq.ptr, n, dy.ptr, rows, 0))
+    got = dy.download(np.float32).reshape(n, rows)
+    assert np.array_equal(bits(got), bits(exp)), np.abs(got - exp).max()
+    if t == bind.Q4_K:
+        pk = mk.alloc(mk_.load().mk_packed_bytes(t, rows, k))
+        mk_.check(mk_.load().mk_pack_weight(mk.h, t, dw.ptr, w.shape[1], rows, k, pk.ptr))
+        wt = mk_.MkWeight(t, 1, rows, k, pk.p)
+        mk_.check(mk_.load().mk_matmul(mk.h, ctypes.byref(wt), dq.ptr, n, dy.ptr, rows, 0))
+        assert np.array_equal(bits(dy.download(np.float32).reshape(n, rows)), bits(exp))
+
+
+def test_matmul_gguf_q5k_golden(mk, golden):
+    """The reference's own Q5_K panel outputs (gemm.npz, written by oracle/_ref, compact and wide panels)."""
+    g = golden("gemm.npz")
+    ci = next(i for i in range(8) if f"c{i}_type" in g.files and int(g[f"c{i}_type"]) == bind.Q5_K)
+    w = g[f"c{ci}_w"]
+    rows, k = w.shape[0], w.shape[1] // 176 * 256
+    for key in g.files:
+        if not (key.startswith(f"c{ci}_n") and key.endswith("_xq")):
+            continue
+        n = int(key[len(f"c{ci}_n"):-3])
+        xq = g[key]
+        dw, dq, dy = mk.to_device(w), mk.to_device(xq), mk.alloc(n * rows * 4)
+        mk_.check(mk_.load().mk_matmul_gguf(mk.h, bind.Q5_K, dw.ptr, w.shape[1], rows, k, dq.ptr, n, dy.ptr, rows, 0))
+        got = dy.download(np.float32).reshape(n, rows)
+        for ref_key in (f"c{ci}_n{n}_y", f"c{ci}_n{n}_y_compact"):
+            assert np.array_equal(bits(got), bits(g[ref_key])), ref_key
+
+
+def test_q5k_model_golden(mk, model_files, golden):
+    g = golden("models.npz")
+    name = "tiny-q5k"
+    m = mk_.Model(mk, model_files[name], 256, 2)
+    try:
+        logits = m.forward(g[f"{name}_prompt"], 0, all_logits=True)
+        assert np.array_equal(bits(logits), bits(g[f"{name}_prompt_logits"]))
+        last = logits[-1]
+        for step in range(16):  # the stream on sequence 0 (the tree batch below continues it)
+            t = int(np.argmax(last))
+            assert t == g[f"{name}_greedy"][step]
+            last = m.forward(np.array([t], np.int32), 24 + step)[0]
+        out, _ = m.generate(g[f"{name}_prompt"], 16, seq=1)
+        assert list(out) == list(g[f"{name}_greedy"])
+        batch = g[f"{name}_tree_batch"].astype(np.int32).view(mk_.BATCH_TOKEN).reshape(-1)
+        assert np.array_equal(bits(m.forward_batch(batch)), bits(g[f"{name}_tree_logits"]))
+    finally:
+        m.close()

@@ -16,7 +16,7 @@ def digest(path):
         return hashlib.sha256(f.read()).hexdigest()
 
 
-@pytest.mark.parametrize("wtype,mix", [(8, 0), (12, 0), (14, 0), (12, 1)])
+@pytest.mark.parametrize("wtype,mix", [(8, 0), (12, 0), (13, 0), (14, 0), (12, 1), (1, 0), (30, 0)])
 def test_weights_have_the_drawn_spread(tmp_path, synth_lib, oracle, wtype, mix):
     synth = synth_lib
     path = str(tmp_path / "m.gguf")
