@@ -1,13 +1,15 @@
 /*
- * malkin-mi355x: C ABI of the device token loop (libmalkin_hip.so): continuous batching and greedy speculative
- * decoding over mk_model, the greedy part of the reference's malkin::Engine (engine.h:51-141, engine.cpp:242-479)
- * without tokenizer or text: requests are token ids in, token ids out.
+ * malkin-mi355x: C ABI of the device token loop (libmalkin_hip.so): continuous batching and speculative decoding
+ * over mk_model, the reference's malkin::Engine (engine.h:51-141, engine.cpp:242-501) without tokenizer or text:
+ * requests are token ids in, token ids out, greedy (mk_engine_submit) or with SamplingParams
+ * (mk_engine_submit_sampled).
  *
  * A request is admitted into the idle slot (model sequence) whose cached tokens share the longest prefix with its
  * prompt (that prefix's KV is reused); each step is one target forward over all busy slots: decoding slots put their
  * next token, with a draft model also the draft's greedy tree [next, chain0, alt0, chain1, alt1, ...], then prompt
  * chunks fill the batch up to 256 tokens. Accepted tree nodes move their KV rows (Model::move_kv). Greedy picks run
- * on the device (first maximum, strict-> runner-up for the draft alternative). Status codes and mk_last_error() as
+ * on the device (first maximum, strict-> runner-up for the draft alternative). Sampled requests draft a chain with
+ * the draft's sampler and verify it with Sampler::verify (engine.cpp:481-501). Status codes and mk_last_error() as
  * in malkin_hip.h.
  */
 #ifndef MALKIN_ENGINE_H
@@ -16,6 +18,7 @@
 #include <stdint.h>
 
 #include "malkin_model.h"
+#include "malkin_sampler.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -39,6 +42,10 @@ int mk_engine_free(mk_engine* e);
    ids (may be NULL). Errors as the reference: empty prompt, prompt not shorter than the context. */
 int mk_engine_submit(mk_engine* e, const int32_t* prompt, int n_prompt, int max_tokens, const int32_t* eog, int n_eog,
                      int32_t* request_id);
+/* The same request with the reference's SamplingParams (GenRequest::sampling, engine.h:29-34): temperature > 0 samples
+   (speculative chains verified exactly), penalties count the request's generated tokens, seed 0 is random. */
+int mk_engine_submit_sampled(mk_engine* e, const int32_t* prompt, int n_prompt, int max_tokens, const int32_t* eog,
+                             int n_eog, const mk_sampling_params* sampling, int32_t* request_id);
 /* The worker loop's iteration (engine.cpp:193-224): pending requests into idle slots, then one step. busy (may be
    NULL): slots still in flight. */
 int mk_engine_step(mk_engine* e, int32_t* busy);

@@ -210,6 +210,19 @@ int mk_argmax_top2(mk_ctx* ctx, const float* logits, int rows, int n_vocab, int3
    call on one GPU shares that array, so calls that overlap on one GPU (two streams) race; calls in one stream's
    order do not. Results are identical to mk_argmax_top2's. */
 int mk_argmax_top2_noalloc(void* stream, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2);
+/* ---- stochastic sampling: candidate selection (sampler.cpp:22-36) ---- */
+/* Row r of a call is logits row rows[r] (rows NULL: row r), `stride` floats apart; rows, pen_* are device arrays.
+   mk_penalize: the repetition penalties in place (sampler.cpp:24-26), l[pen_id[i]] -= pen_amt[i] for i in
+   pen_off[r] .. pen_off[r + 1] (pen_off has n_rows + 1 entries; ids outside 0..n_vocab-1 are skipped). */
+int mk_penalize(mk_ctx* ctx, float* logits, int64_t stride, const int32_t* rows, int n_rows, int n_vocab,
+                const int32_t* pen_off, const int32_t* pen_id, const float* pen_amt);
+/* The top-k cut of Sampler::distribution (sampler.cpp:32-36, std::partial_sort by value): per row the k largest
+   logits, highest first, into values / ids [n_rows][k]. k = 1..1024 and at most n_vocab. Equal logits are ordered
+   by lower id (the reference leaves their order unspecified). One workgroup per row: radix select of the k-th
+   largest value, then a sort of the k candidates in LDS. */
+int mk_topk(mk_ctx* ctx, const float* logits, int64_t stride, const int32_t* rows, int n_rows, int n_vocab, int k,
+            float* values, int32_t* ids);
+
 /* dst[dst_index[i]] = src[src_index[i]] for i < n, in stream order (a NULL index array is the identity; a negative
    index skips i). Moves token ids between device arrays without a host round trip: draft picks into a proposal tree,
    tree ids into a forward's token slots (no reference counterpart: the CPU engine keeps ids in host vectors). */

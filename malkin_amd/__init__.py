@@ -94,6 +94,17 @@ SIGNATURES = {
     "mk_engine_run": (_I, [_P]),
     "mk_engine_steps": (_I, [_P, ctypes.POINTER(ctypes.c_uint64)]),
     "mk_engine_result": (_I, [_P, _I, _P, _I, _P]),
+    "mk_engine_submit_sampled": (_I, [_P, _P, _I, _I, _P, _I, _P, _P]),
+    "mk_penalize": (_I, [_P, _P, _I64, _P, _I, _I, _P, _P, _P]),
+    "mk_topk": (_I, [_P, _P, _I64, _P, _I, _I, _I, _P, _P]),
+    "mk_sampler_create": (_I, [_P, _I, ctypes.POINTER(_P)]),
+    "mk_sampler_free": (_I, [_P]),
+    "mk_sampler_accept": (_I, [_P, ctypes.c_int32]),
+    "mk_sampler_distribution": (_I, [_P, _P, _P, _I, _P, _P, _I, ctypes.POINTER(_I)]),
+    "mk_sampler_sample": (_I, [_P, _P, _P, _I, ctypes.POINTER(ctypes.c_int32)]),
+    "mk_sampler_draw": (_I, [_P, _P, _P, _I, ctypes.POINTER(ctypes.c_int32)]),
+    "mk_sampler_verify": (_I, [_P, _P, _P, _I, _P, _P, _I, ctypes.c_int32, ctypes.POINTER(_I),
+                               ctypes.POINTER(ctypes.c_int32)]),
 }
 
 _lib = None
@@ -342,12 +353,19 @@ class Engine:
         except Exception:
             pass
 
-    def submit(self, prompt, max_tokens=0, eog=()):
+    def submit(self, prompt, max_tokens=0, eog=(), sampling=None):
+        """sampling: None (greedy) or SamplingParams fields as keywords of sampling_params()."""
         prompt = np.ascontiguousarray(prompt, dtype=np.int32)
         eog = np.ascontiguousarray(list(eog), dtype=np.int32)
         rid = ctypes.c_int32()
-        check(load().mk_engine_submit(self.h, _ptr(prompt), len(prompt), max_tokens, _ptr(eog) if len(eog) else None,
-                                      len(eog), ctypes.byref(rid)))
+        if sampling is None:
+            check(load().mk_engine_submit(self.h, _ptr(prompt), len(prompt), max_tokens,
+                                          _ptr(eog) if len(eog) else None, len(eog), ctypes.byref(rid)))
+        else:
+            sp = sampling_params(**sampling)
+            check(load().mk_engine_submit_sampled(self.h, _ptr(prompt), len(prompt), max_tokens,
+                                                  _ptr(eog) if len(eog) else None, len(eog), ctypes.byref(sp),
+                                                  ctypes.byref(rid)))
         return rid.value
 
     def step(self):
@@ -370,6 +388,75 @@ class Engine:
         toks = np.zeros(max(info.completion_tokens, 1), dtype=np.int32)
         check(load().mk_engine_result(self.h, rid, _ptr(toks), len(toks), ctypes.byref(info)))
         return toks[:info.completion_tokens], {f: getattr(info, f) for f, _ in MkRequestInfo._fields_}
+
+
+class MkSamplingParams(ctypes.Structure):
+    _fields_ = [("temperature", _F), ("top_p", _F), ("top_k", ctypes.c_int32), ("min_p", _F),
+                ("presence_penalty", _F), ("frequency_penalty", _F), ("seed", ctypes.c_uint64)]
+
+
+def sampling_params(temperature=0.8, top_p=0.95, top_k=40, min_p=0.05, presence=0.0, frequency=0.0, seed=0):
+    """mk_sampling_params with the reference's defaults (sampler.h:10-18)."""
+    return MkSamplingParams(temperature, top_p, top_k, min_p, presence, frequency, seed)
+
+
+class Sampler:
+    """mk_sampler_*: the reference's Sampler (sampler.h:23-42) with its distribution over device logits rows.
+    Distributions are [(p, id), ...] lists, highest first."""
+
+    def __init__(self, seed, penalties=True, **params):
+        sp = sampling_params(seed=seed, **params)
+        p = _P()
+        check(load().mk_sampler_create(ctypes.byref(sp), 1 if penalties else 0, ctypes.byref(p)))
+        self.h = p.value
+
+    def close(self):
+        if self.h:
+            load().mk_sampler_free(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def accept(self, tok):
+        check(load().mk_sampler_accept(self.h, int(tok)))
+
+    def distribution(self, ctx, dev_logits, n_vocab):
+        """dev_logits: DeviceBuffer (or device pointer) of one row; penalized in place."""
+        ptr = dev_logits.ptr if hasattr(dev_logits, "ptr") else dev_logits
+        cap = n_vocab
+        probs = np.zeros(cap, np.float32)
+        ids = np.zeros(cap, np.int32)
+        n = ctypes.c_int()
+        check(load().mk_sampler_distribution(ctx.h, self.h, ptr, n_vocab, _ptr(probs), _ptr(ids), cap,
+                                             ctypes.byref(n)))
+        return [(float(probs[i]), int(ids[i])) for i in range(n.value)]
+
+    def sample(self, ctx, dev_logits, n_vocab):
+        ptr = dev_logits.ptr if hasattr(dev_logits, "ptr") else dev_logits
+        t = ctypes.c_int32()
+        check(load().mk_sampler_sample(ctx.h, self.h, ptr, n_vocab, ctypes.byref(t)))
+        return t.value
+
+    def draw(self, d):
+        pp = np.ascontiguousarray([e[0] for e in d], np.float32)
+        pi = np.ascontiguousarray([e[1] for e in d], np.int32)
+        t = ctypes.c_int32()
+        check(load().mk_sampler_draw(self.h, _ptr(pp), _ptr(pi), len(pp), ctypes.byref(t)))
+        return t.value
+
+    def verify(self, p, q, draft):
+        pp = np.ascontiguousarray([e[0] for e in p], np.float32)
+        pi = np.ascontiguousarray([e[1] for e in p], np.int32)
+        qp = np.ascontiguousarray([e[0] for e in q] or [0.0], np.float32)
+        qi = np.ascontiguousarray([e[1] for e in q] or [0], np.int32)
+        a, t = ctypes.c_int(), ctypes.c_int32()
+        check(load().mk_sampler_verify(self.h, _ptr(pp), _ptr(pi), len(pp), _ptr(qp), _ptr(qi), len(q), int(draft),
+                                       ctypes.byref(a), ctypes.byref(t)))
+        return t.value, bool(a.value)
 
 
 def host_waits():

@@ -26,9 +26,11 @@ HIP_SOURCES = [
     "csrc/kernels/quant.hip",
     "csrc/kernels/attn.hip",
     "csrc/kernels/rowpath.hip",
+    "csrc/kernels/sample.hip",
     "csrc/kernels/capi.cpp",
     "csrc/host/gguf.cpp",
     "csrc/host/model.cpp",
+    "csrc/host/sampler.cpp",
     "csrc/host/engine.cpp",
     "csrc/host/capi_model.cpp",
 ]

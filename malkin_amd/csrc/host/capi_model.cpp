@@ -8,6 +8,7 @@
 
 #include "../../../include/malkin_engine.h"
 #include "../../../include/malkin_model.h"
+#include "../../../include/malkin_sampler.h"
 #include "../kernels/ctx.h"
 #include "engine.h"
 #include "model.h"
@@ -19,6 +20,16 @@ struct mk_model {
 
 struct mk_engine {
   std::unique_ptr<malkin_hip::Engine> engine;
+};
+
+struct mk_sampler {
+  std::unique_ptr<malkin_hip::Sampler> sampler;
+  // Candidate selection for device rows, made for the first (context, vocabulary) it is used with.
+  std::unique_ptr<malkin_hip::Selector> select;
+  mk_ctx* ctx = nullptr;
+  int n_vocab = 0;
+  std::vector<int32_t> pen_ids;
+  std::vector<float> pen_amts;
 };
 
 namespace {
@@ -35,6 +46,44 @@ int run(F&& f) {
     mk::set_error("%s", e.what());
     return MK_ERR_INVALID;
   }
+}
+
+malkin_hip::SamplingParams to_params(const mk_sampling_params& p) {
+  malkin_hip::SamplingParams s;
+  s.temperature = p.temperature;
+  s.top_p = p.top_p;
+  s.top_k = p.top_k;
+  s.min_p = p.min_p;
+  s.presence_penalty = p.presence_penalty;
+  s.frequency_penalty = p.frequency_penalty;
+  s.seed = p.seed;
+  return s;
+}
+
+malkin_hip::Distribution to_dist(const float* probs, const int32_t* ids, int n) {
+  if (n <= 0 || !probs || !ids) throw std::invalid_argument("sampler: empty distribution");
+  malkin_hip::Distribution d(static_cast<size_t>(n));
+  for (int i = 0; i < n; ++i) d[static_cast<size_t>(i)] = malkin_hip::Candidate{probs[i], ids[i]};
+  return d;
+}
+
+// Sampler::distribution of one device row: penalties and top-k on the device, one wait, the rest on the host.
+void device_distribution(mk_ctx* ctx, mk_sampler* s, float* dev_logits, int n_vocab, malkin_hip::Distribution& out) {
+  if (!ctx || !s || !dev_logits || n_vocab <= 0) throw std::invalid_argument("sampler: bad arguments");
+  if (!s->select || s->ctx != ctx || s->n_vocab != n_vocab) {
+    s->select = std::make_unique<malkin_hip::Selector>(ctx, n_vocab);
+    s->ctx = ctx;
+    s->n_vocab = n_vocab;
+  }
+  s->pen_ids.clear();
+  s->pen_amts.clear();
+  s->sampler->penalties(nullptr, 0, s->pen_ids, s->pen_amts);
+  s->select->clear();
+  s->select->add(0, s->sampler->candidates(n_vocab), s->pen_ids, s->pen_amts);
+  s->select->enqueue(dev_logits);
+  if (mk_synchronize(ctx) != MK_OK) throw std::runtime_error(mk_last_error());
+  s->select->collect();
+  s->sampler->finish(s->select->values(0), s->select->ids(0), s->select->count(0), out);
 }
 
 std::vector<malkin_hip::BatchToken> to_batch(const mk_batch_token* b, int n) {
@@ -165,6 +214,21 @@ int mk_engine_submit(mk_engine* e, const int32_t* prompt, int n_prompt, int max_
   });
 }
 
+int mk_engine_submit_sampled(mk_engine* e, const int32_t* prompt, int n_prompt, int max_tokens, const int32_t* eog,
+                             int n_eog, const mk_sampling_params* sampling, int32_t* request_id) {
+  return run([&] {
+    if (!e || (n_prompt > 0 && !prompt) || (n_eog > 0 && !eog) || !sampling)
+      throw std::invalid_argument("mk_engine_submit_sampled: null argument");
+    malkin_hip::EngineRequest r;
+    if (n_prompt > 0) r.prompt.assign(prompt, prompt + n_prompt);
+    if (n_eog > 0) r.eog.assign(eog, eog + n_eog);
+    r.max_tokens = max_tokens;
+    r.sampling = to_params(*sampling);
+    const int id = e->engine->submit(r);
+    if (request_id) *request_id = id;
+  });
+}
+
 int mk_engine_step(mk_engine* e, int32_t* busy) {
   return run([&] {
     if (!e) throw std::invalid_argument("mk_engine_step: null engine");
@@ -196,6 +260,68 @@ int mk_engine_result(mk_engine* e, int32_t request_id, int32_t* tokens, int32_t 
     if (info)
       *info = mk_request_info{r.prompt_tokens, r.cached_tokens, r.completion_tokens, r.drafted, r.accepted,
                                r.finish_reason == "stop" ? 1 : 0, r.done ? 1 : 0, r.prefill_ms, r.decode_ms};
+  });
+}
+
+int mk_sampler_create(const mk_sampling_params* params, int penalties, mk_sampler** out) {
+  return run([&] {
+    if (!params || !out) throw std::invalid_argument("mk_sampler_create: null argument");
+    auto s = std::make_unique<mk_sampler>();
+    s->sampler = std::make_unique<malkin_hip::Sampler>(to_params(*params), penalties != 0);
+    *out = s.release();
+  });
+}
+
+int mk_sampler_free(mk_sampler* s) {
+  return run([&] { delete s; });
+}
+
+int mk_sampler_accept(mk_sampler* s, int32_t id) {
+  return run([&] {
+    if (!s) throw std::invalid_argument("mk_sampler_accept: null sampler");
+    s->sampler->accept(id);
+  });
+}
+
+int mk_sampler_distribution(mk_ctx* ctx, mk_sampler* s, float* dev_logits, int n_vocab, float* probs, int32_t* ids,
+                            int cap, int* n_out) {
+  return run([&] {
+    if (cap > 0 && (!probs || !ids)) throw std::invalid_argument("mk_sampler_distribution: null output");
+    malkin_hip::Distribution d;
+    device_distribution(ctx, s, dev_logits, n_vocab, d);
+    for (int i = 0; i < cap && i < static_cast<int>(d.size()); ++i) {
+      probs[i] = d[static_cast<size_t>(i)].p;
+      ids[i] = d[static_cast<size_t>(i)].id;
+    }
+    if (n_out) *n_out = static_cast<int>(d.size());
+  });
+}
+
+int mk_sampler_sample(mk_ctx* ctx, mk_sampler* s, float* dev_logits, int n_vocab, int32_t* id_out) {
+  return run([&] {
+    if (!id_out) throw std::invalid_argument("mk_sampler_sample: null output");
+    malkin_hip::Distribution d;
+    device_distribution(ctx, s, dev_logits, n_vocab, d);
+    *id_out = s->sampler->draw(d);
+  });
+}
+
+int mk_sampler_draw(mk_sampler* s, const float* probs, const int32_t* ids, int n, int32_t* id_out) {
+  return run([&] {
+    if (!s || !id_out) throw std::invalid_argument("mk_sampler_draw: null argument");
+    *id_out = s->sampler->draw(to_dist(probs, ids, n));
+  });
+}
+
+int mk_sampler_verify(mk_sampler* s, const float* p_probs, const int32_t* p_ids, int n_p, const float* q_probs,
+                      const int32_t* q_ids, int n_q, int32_t draft, int* accepted, int32_t* id_out) {
+  return run([&] {
+    if (!s || !accepted || !id_out) throw std::invalid_argument("mk_sampler_verify: null argument");
+    const malkin_hip::Distribution p = to_dist(p_probs, p_ids, n_p);
+    const malkin_hip::Distribution q = n_q > 0 ? to_dist(q_probs, q_ids, n_q) : malkin_hip::Distribution{};
+    bool ok = false;
+    *id_out = s->sampler->verify(p, q, draft, ok);
+    *accepted = ok ? 1 : 0;
   });
 }
 

@@ -26,12 +26,20 @@ size_t common_prefix(const std::vector<int32_t>& a, const std::vector<int32_t>& 
 struct DraftPass {
   std::vector<BatchToken> batch;
   std::vector<int32_t> id_from;              // per token: tree slot its id comes from, or -1
-  std::vector<int32_t> chain_dst, alt_dst;   // per logits row: tree slots of its first / second pick
+  std::vector<int32_t> chain_dst, alt_dst;   // per logits row: tree slots of its first / second pick (-1: none)
+  int depth = -1;                            // round passes: the depth whose chain tokens are fed
+  std::vector<std::pair<int, int>> fed;      // (batch index, spec) of sampled lanes' chain tokens, set at launch
+  std::vector<std::pair<int, int>> drawn;    // (logits row, spec) whose row the host draws the next draft from
 };
 
 }  // namespace
 
-Engine::Engine(Model* target, Model* draft, int n_draft) : target_(target), draft_(draft) {
+Engine::Engine(Model* target, Model* draft, int n_draft)
+    : target_(target),
+      draft_(draft),
+      sel_(target->ctx(), target->cfg().n_vocab),
+      tree_sel_(target->ctx(), target->cfg().n_vocab),
+      draft_sel_(target->ctx(), target->cfg().n_vocab) {
   if (!target_) throw std::invalid_argument("engine: no target model");
   if (draft_) {
     if (draft_->cfg().n_vocab != target_->cfg().n_vocab)
@@ -82,6 +90,13 @@ int Engine::submit(const EngineRequest& req) {
   job->res = results_.back().get();
   job->budget = req.max_tokens > 0 ? req.max_tokens : n_ctx;
   job->admitted = Clock::now();
+  // The request's sampler counts its tokens for the penalties; the draft's draws with seed + 1 and no penalties
+  // (engine.cpp:40-44).
+  job->sampler = std::make_unique<Sampler>(req.sampling, true);
+  SamplingParams dp = req.sampling;
+  dp.seed = dp.seed ? dp.seed + 1 : 0;
+  job->draft_sampler = std::make_unique<Sampler>(dp, false);
+  job->plain = job->sampler->greedy() && !job->sampler->penalizes();
   waiting_.push_back(std::move(job));
   return static_cast<int>(results_.size()) - 1;
 }
@@ -130,7 +145,11 @@ void Engine::admit(std::unique_ptr<Job> job) {
 void Engine::plan_specs() {
   specs_.clear();
   for (size_t i = 0; i < lanes_.size(); ++i)
-    if (lanes_[i].job && lanes_[i].job->decoding) specs_.push_back(Spec{static_cast<int>(i), 0, 0});
+    if (lanes_[i].job && lanes_[i].job->decoding) {
+      specs_.emplace_back();
+      specs_.back().lane = static_cast<int>(i);
+      specs_.back().sampled = !lanes_[i].job->sampler->greedy();
+    }
   if (!draft_ || specs_.empty()) return;
   const int share = Model::kMaxBatch / static_cast<int>(specs_.size()) - 1;  // tokens per lane after its pending one
   for (Spec& sp : specs_) {
@@ -138,14 +157,16 @@ void Engine::plan_specs() {
     const Job& job = *lane.job;
     const int left = job.budget - job.res->completion_tokens;
     const int room = target_->n_ctx() - static_cast<int>(lane.kv.size()) - 2;
-    // two tree tokens (chain and alt) per depth
-    sp.depth = std::max(0, std::min({job.k, left, room / 2, share / 2}));
+    const int per_depth = sp.sampled ? 1 : 2;  // a greedy tree holds chain and alt tokens
+    sp.depth = std::max(0, std::min({job.k, left, room / per_depth, share / per_depth}));
   }
 }
 
-// The draft's part of a step, all queued before the host waits: catch-up forwards that bring each drafting lane's
-// draft KV to its target tokens plus the pending token (prefix rows reused), then one forward per depth that feeds
-// every lane's chain token of that depth. Each forward's picks go to the next depth's tree slots.
+// The draft's part of a step: catch-up forwards that bring each drafting lane's draft KV to its target tokens plus
+// the pending token (prefix rows reused), then one forward per depth that feeds every lane's chain token of that
+// depth. Greedy lanes: each forward's picks go to the next depth's tree slots on the device, nothing waits.
+// Sampled lanes: after a forward that produced a row they draw from, the host waits, draws, and feeds the draw to
+// the next forward.
 void Engine::draft_trees() {
   std::vector<DraftPass> passes(1);
   std::vector<int> fed_from(lanes_.size(), -1);  // draft_kv index of each lane's first chain token fed
@@ -154,7 +175,8 @@ void Engine::draft_trees() {
     passes.emplace_back();
     return passes.back();
   };
-  for (const Spec& sp : specs_) {
+  for (size_t si = 0; si < specs_.size(); ++si) {
+    const Spec& sp = specs_[si];
     if (sp.depth == 0) continue;
     Lane& lane = lanes_[static_cast<size_t>(sp.lane)];
     const size_t n_tok = lane.kv.size() + 1;  // target tokens plus the pending one
@@ -169,23 +191,35 @@ void Engine::draft_trees() {
       p.batch.push_back(BatchToken{id, sp.lane, static_cast<int>(pos), last});
       p.id_from.push_back(-1);
       if (last) {
-        p.chain_dst.push_back(tree_slot(sp.lane, 0, false));
-        p.alt_dst.push_back(tree_slot(sp.lane, 0, true));
+        if (sp.sampled) p.drawn.emplace_back(static_cast<int>(p.chain_dst.size()), static_cast<int>(si));
+        p.chain_dst.push_back(sp.sampled ? -1 : tree_slot(sp.lane, 0, false));
+        p.alt_dst.push_back(sp.sampled ? -1 : tree_slot(sp.lane, 0, true));
       }
       lane.draft_kv.push_back(id);
     }
   }
-  for (int d = 0;; ++d) {  // depth d's chain tokens fed, their picks are depth d + 1
+  for (int d = 0;; ++d) {  // depth d's chain tokens fed, their picks (draws) are depth d + 1
     DraftPass p;
-    for (const Spec& sp : specs_) {
+    p.depth = d;
+    for (size_t si = 0; si < specs_.size(); ++si) {
+      const Spec& sp = specs_[si];
       if (d + 1 >= sp.depth) continue;
       Lane& lane = lanes_[static_cast<size_t>(sp.lane)];
       if (d == 0) fed_from[static_cast<size_t>(sp.lane)] = static_cast<int>(lane.draft_kv.size());
+      const int row = static_cast<int>(p.batch.size());
       p.batch.push_back(BatchToken{0, sp.lane, static_cast<int>(lane.draft_kv.size()), true});
-      p.id_from.push_back(tree_slot(sp.lane, d, false));
-      p.chain_dst.push_back(tree_slot(sp.lane, d + 1, false));
-      p.alt_dst.push_back(tree_slot(sp.lane, d + 1, true));
-      lane.draft_kv.push_back(-1);  // the chain id, known on the host after the step's wait
+      if (sp.sampled) {
+        p.id_from.push_back(-1);
+        p.fed.emplace_back(row, static_cast<int>(si));
+        p.drawn.emplace_back(row, static_cast<int>(si));
+        p.chain_dst.push_back(-1);
+        p.alt_dst.push_back(-1);
+      } else {
+        p.id_from.push_back(tree_slot(sp.lane, d, false));
+        p.chain_dst.push_back(tree_slot(sp.lane, d + 1, false));
+        p.alt_dst.push_back(tree_slot(sp.lane, d + 1, true));
+      }
+      lane.draft_kv.push_back(-1);  // the chain id, filled in once the host knows it
     }
     if (p.batch.empty()) break;
     passes.push_back(std::move(p));
@@ -204,21 +238,46 @@ void Engine::draft_trees() {
   mk_ctx* c = target_->ctx();
   ck(mk_copy_async(c, plan_.p, plan_h_, off * sizeof(int32_t)));
   int32_t* tree = tree_.as<int32_t>();
+  const int n_vocab = target_->cfg().n_vocab;
   for (size_t i = 0; i < passes.size(); ++i) {
-    const DraftPass& p = passes[i];
+    DraftPass& p = passes[i];
     if (p.batch.empty()) continue;
+    for (const auto& [b, si] : p.fed) p.batch[static_cast<size_t>(b)].id = specs_[static_cast<size_t>(si)].chain[static_cast<size_t>(p.depth)];
     const int m = static_cast<int>(p.chain_dst.size());
     draft_->enqueue(p.batch.data(), static_cast<int>(p.batch.size()), p.id_from.data(), tree, draft_top1_.as<int32_t>(),
                     draft_top2_.as<int32_t>());
     int32_t* dst = plan_.as<int32_t>() + at[i];
     ck(mk_move_ids(c, tree, dst, draft_top1_.as<int32_t>(), nullptr, m));
     ck(mk_move_ids(c, tree, dst + m, draft_top2_.as<int32_t>(), nullptr, m));
+    if (p.drawn.empty()) continue;
+    // Sampled lanes: the draft sampler's distribution of each row, one wait, then the draws (engine.cpp:319-323).
+    draft_sel_.clear();
+    for (const auto& [row, si] : p.drawn) {
+      const Job& job = *lanes_[static_cast<size_t>(specs_[static_cast<size_t>(si)].lane)].job;
+      draft_sel_.add(row, job.draft_sampler->candidates(n_vocab), pen_ids_, pen_amts_);
+    }
+    draft_sel_.enqueue(draft_->dev_logits());
+    ck(mk_synchronize(c));
+    draft_sel_.collect();
+    for (size_t j = 0; j < p.drawn.size(); ++j) {
+      Spec& sp = specs_[static_cast<size_t>(p.drawn[j].second)];
+      Sampler& ds = *lanes_[static_cast<size_t>(sp.lane)].job->draft_sampler;
+      const int r = static_cast<int>(j);
+      sp.q.emplace_back();
+      ds.finish(draft_sel_.values(r), draft_sel_.ids(r), draft_sel_.count(r), sp.q.back());
+      sp.chain.push_back(ds.draw(sp.q.back()));
+    }
   }
-  // Remember where each lane's chain tokens sit in draft_kv (filled in after the wait).
-  for (Spec& sp : specs_) sp.root = fed_from[static_cast<size_t>(sp.lane)];
+  // Remember where each lane's chain tokens sit in draft_kv (greedy ones filled in after the step's wait).
+  for (Spec& sp : specs_) {
+    sp.root = fed_from[static_cast<size_t>(sp.lane)];
+    if (!sp.sampled || sp.root < 0) continue;
+    Lane& lane = lanes_[static_cast<size_t>(sp.lane)];
+    for (int d = 0; d + 1 < sp.depth; ++d) lane.draft_kv[static_cast<size_t>(sp.root + d)] = sp.chain[static_cast<size_t>(d)];
+  }
 }
 
-// Decoding lanes' pending tokens and trees, then prompt tokens; returns the number of decode rows.
+// Decoding lanes' pending tokens and drafts, then prompt tokens; returns the number of decode rows.
 int Engine::build_target_batch() {
   batch_.clear();
   id_from_.clear();
@@ -230,6 +289,11 @@ int Engine::build_target_batch() {
     batch_.push_back(BatchToken{lane.job->pending, sp.lane, P, true});
     id_from_.push_back(-1);
     for (int d = 0; d < sp.depth; ++d) {
+      if (sp.sampled) {  // a chain in a row: ordinary causal tokens
+        batch_.push_back(BatchToken{sp.chain[static_cast<size_t>(d)], sp.lane, P + 1 + d, true});
+        id_from_.push_back(-1);
+        continue;
+      }
       const int parent = d == 0 ? root : root + 2 * d - 1;  // chain_{d-1}
       batch_.push_back(BatchToken{0, sp.lane, P + 1 + d, true, P + 1 + 2 * d, parent});
       id_from_.push_back(tree_slot(sp.lane, d, false));
@@ -255,6 +319,70 @@ int Engine::build_target_batch() {
   return decode_rows;
 }
 
+// Candidates of the target rows whose penalties the host knows before the step's wait: sampled lanes' rows (the
+// path to row i is the chain before it), penalized greedy lanes without a tree, and finished prompts of non-plain
+// requests.
+void Engine::select_known_rows(int decode_rows) {
+  const int n_vocab = target_->cfg().n_vocab;
+  sel_.clear();
+  for (Spec& sp : specs_) {
+    const Job& job = *lanes_[static_cast<size_t>(sp.lane)].job;
+    if (job.plain || (!sp.sampled && sp.depth > 0)) continue;
+    sp.cand = &sel_;
+    const int rows = sp.sampled ? sp.depth + 1 : 1;
+    for (int i = 0; i < rows; ++i) {
+      pen_ids_.clear();
+      pen_amts_.clear();
+      job.sampler->penalties(sp.chain.data(), i, pen_ids_, pen_amts_);
+      const int at = sel_.add(sp.root + i, job.sampler->candidates(n_vocab), pen_ids_, pen_amts_);
+      if (i == 0) sp.sel = at;
+    }
+  }
+  finishing_sel_.assign(finishing_lanes_.size(), -1);
+  for (size_t j = 0; j < finishing_lanes_.size(); ++j) {
+    const Job& job = *lanes_[static_cast<size_t>(finishing_lanes_[j])].job;
+    if (job.plain) continue;
+    pen_ids_.clear();
+    pen_amts_.clear();
+    job.sampler->penalties(nullptr, 0, pen_ids_, pen_amts_);
+    finishing_sel_[j] = sel_.add(decode_rows + static_cast<int>(j), job.sampler->candidates(n_vocab), pen_ids_, pen_amts_);
+  }
+  pen_ids_.clear();
+  pen_amts_.clear();
+}
+
+// Penalized greedy trees: every node's row with the penalties of its path (chain tokens above it, then itself),
+// known once the tree is on the host. One more wait.
+void Engine::select_tree_rows() {
+  tree_sel_.clear();
+  for (Spec& sp : specs_) {
+    const Job& job = *lanes_[static_cast<size_t>(sp.lane)].job;
+    if (job.plain || sp.sampled || sp.depth == 0) continue;
+    sp.cand = &tree_sel_;
+    const int32_t* tree = tree_host(sp.lane);
+    std::vector<int32_t> path;
+    for (int node = 0; node < 1 + 2 * sp.depth; ++node) {
+      path.clear();
+      if (node > 0) {
+        const int d = (node - 1) / 2;  // depth of the node; chain nodes are odd
+        for (int e = 0; e < d; ++e) path.push_back(tree[2 * e]);
+        path.push_back(tree[2 * d + (node % 2 == 1 ? 0 : 1)]);
+      }
+      pen_ids_.clear();
+      pen_amts_.clear();
+      job.sampler->penalties(path.data(), static_cast<int>(path.size()), pen_ids_, pen_amts_);
+      const int at = tree_sel_.add(sp.root + node, 1, pen_ids_, pen_amts_);
+      if (node == 0) sp.sel = at;
+    }
+  }
+  pen_ids_.clear();
+  pen_amts_.clear();
+  if (tree_sel_.empty()) return;
+  tree_sel_.enqueue(target_->dev_logits());
+  ck(mk_synchronize(target_->ctx()));
+  tree_sel_.collect();
+}
+
 void Engine::step() {
   plan_specs();
   std::vector<int> chain_at;
@@ -268,20 +396,24 @@ void Engine::step() {
   if (n == 0) return;
   mk_ctx* c = target_->ctx();
   target_->enqueue(batch_.data(), n, id_from_.data(), tree_.as<int32_t>(), target_top_.as<int32_t>(), nullptr);
+  select_known_rows(decode_rows);
+  sel_.enqueue(target_->dev_logits());
   const int rows = target_->n_out();
   ck(mk_copy_async(c, picks_h_, target_top_.p, static_cast<size_t>(rows) * sizeof(int32_t)));
   if (drafting) ck(mk_copy_async(c, tree_h_, tree_.p, lanes_.size() * 2 * max_depth_ * sizeof(int32_t)));
   ck(mk_synchronize(c));  // the step's one host wait
   ++steps_;
+  sel_.collect();
 
-  if (drafting)  // the chain ids fed to the draft, now known on the host
+  if (drafting)  // the greedy chain ids fed to the draft, now known on the host
     for (size_t i = 0; i < specs_.size(); ++i) {
       const Spec& sp = specs_[i];
-      if (chain_at[i] < 0) continue;
+      if (chain_at[i] < 0 || sp.sampled) continue;
       Lane& lane = lanes_[static_cast<size_t>(sp.lane)];
       for (int d = 0; d + 1 < sp.depth; ++d)
         lane.draft_kv[static_cast<size_t>(chain_at[i] + d)] = tree_host(sp.lane)[2 * d];
     }
+  select_tree_rows();
   for (int t = decode_rows; t < n; ++t) lanes_[static_cast<size_t>(batch_[t].seq)].kv.push_back(batch_[t].id);
   for (size_t j = 0; j < finishing_lanes_.size(); ++j) {  // prompts that finished: their first token
     Lane& lane = lanes_[static_cast<size_t>(finishing_lanes_[j])];
@@ -289,14 +421,40 @@ void Engine::step() {
     job.first_token = Clock::now();
     job.res->prefill_ms = ms_between(job.admitted, job.first_token);
     job.decoding = true;
-    job.pending = picks_h_[decode_rows + static_cast<int>(j)];
+    if (job.plain) {
+      job.pending = picks_h_[decode_rows + static_cast<int>(j)];
+    } else {
+      const int r = finishing_sel_[j];
+      job.sampler->finish(sel_.values(r), sel_.ids(r), sel_.count(r), dist_);
+      job.pending = job.sampler->draw(dist_);
+    }
     if (!emit(job, job.pending, lane.kv.size())) finish(lane);
   }
-  for (const Spec& sp : specs_) settle(sp, picks_h_);
+  for (const Spec& sp : specs_) {
+    if (sp.sampled)
+      settle_sampled(sp);
+    else
+      settle(sp);
+  }
 }
 
-// The acceptance walk of one decoding lane over the target's picks (rows root.. of this step).
-void Engine::settle(const Spec& sp, const int32_t* picks) {
+// The target's greedy pick at tree node `node` of a lane: the device's first maximum, or for a penalized request
+// the first maximum of the penalized row.
+int32_t Engine::target_pick(const Spec& sp, int node) const {
+  if (!sp.cand) return picks_h_[sp.root + node];
+  return sp.cand->ids(sp.sel + node)[0];
+}
+
+// The request sampler's distribution of target row `row` (0 = the pending token's) of a non-plain lane.
+Distribution& Engine::target_dist(const Spec& sp, int row) {
+  const Sampler& s = *lanes_[static_cast<size_t>(sp.lane)].job->sampler;
+  const int r = sp.sel + row;
+  s.finish(sp.cand->values(r), sp.cand->ids(r), sp.cand->count(r), dist_);
+  return dist_;
+}
+
+// The acceptance walk of one greedy lane over the target's picks (rows root.. of this step).
+void Engine::settle(const Spec& sp) {
   Lane& lane = lanes_[static_cast<size_t>(sp.lane)];
   Job& job = *lane.job;
   const int P = static_cast<int>(lane.kv.size());
@@ -306,7 +464,7 @@ void Engine::settle(const Spec& sp, const int32_t* picks) {
   int node = 0, held = 0;  // tree node the walk stands on (0 = the pending token), draft depths accepted
   const int32_t* tree = tree_host(sp.lane);
   for (int d = 0; d < sp.depth; ++d) {
-    const int32_t want = picks[sp.root + node];
+    const int32_t want = target_pick(sp, node);
     int next = -1;
     if (want == tree[2 * d])
       next = 1 + 2 * d;
@@ -326,9 +484,44 @@ void Engine::settle(const Spec& sp, const int32_t* picks) {
     held = d + 1;
     if (next == 2 + 2 * d) break;  // an alt token has no children
   }
-  if (alive && !missed) job.pending = picks[sp.root + node];
+  if (alive && !missed) job.pending = target_pick(sp, node);
   if (sp.depth > 0) {
     if (held == sp.depth && sp.depth == job.k && node == 2 * sp.depth - 1)
+      job.k = std::min(job.k + 1, max_depth_);
+    else if (2 * held < sp.depth)
+      job.k = std::max(1, job.k - 1);
+  }
+  if (alive) alive = emit(job, job.pending, lane.kv.size());
+  if (!alive) finish(lane);
+}
+
+// A sampled lane: each draft d_i verified against the target's distribution at its row (the rows sit at KV rows
+// P + 1 + i already, so nothing moves); a rejection's replacement, or a draw from the row after a fully accepted
+// chain, is the next pending token.
+void Engine::settle_sampled(const Spec& sp) {
+  Lane& lane = lanes_[static_cast<size_t>(sp.lane)];
+  Job& job = *lane.job;
+  Sampler& s = *job.sampler;
+  lane.kv.push_back(job.pending);
+  job.res->drafted += sp.depth;
+  bool alive = true;
+  int held = 0;  // drafts accepted
+  while (held < sp.depth) {
+    bool ok = false;
+    const int32_t t = s.verify(target_dist(sp, held), sp.q[static_cast<size_t>(held)], sp.chain[static_cast<size_t>(held)], ok);
+    if (!ok) {
+      job.pending = t;
+      break;
+    }
+    ++job.res->accepted;
+    lane.kv.push_back(t);
+    alive = emit(job, t, lane.kv.size());
+    if (!alive) break;
+    ++held;
+  }
+  if (alive && held == sp.depth) job.pending = s.draw(target_dist(sp, sp.depth));
+  if (sp.depth > 0) {
+    if (held == sp.depth && sp.depth == job.k)
       job.k = std::min(job.k + 1, max_depth_);
     else if (2 * held < sp.depth)
       job.k = std::max(1, job.k - 1);
@@ -342,6 +535,7 @@ bool Engine::emit(Job& job, int32_t id, size_t cached) {
     job.res->finish_reason = "stop";
     return false;
   }
+  job.sampler->accept(id);
   job.res->tokens.push_back(id);
   ++job.res->completion_tokens;
   if (job.res->completion_tokens >= job.budget) return false;

@@ -1,28 +1,39 @@
-// Continuous batching and greedy speculative decoding over the device Model: the token loop of the reference's
-// malkin::Engine (engine.h:51-141, engine.cpp:242-479) for greedy requests, without text, tokenizer or threads.
-// Requests are token ids in, token ids out.
+// Continuous batching and speculative decoding over the device Model: the token loop of the reference's
+// malkin::Engine (engine.h:51-141, engine.cpp:242-501), without text, tokenizer or threads. Requests are token ids
+// in, token ids out; each carries the reference's SamplingParams (greedy by default here).
 //
 // Contract (what the reference engine does, and therefore what the streams, KV rows and counters must equal):
 //   * A request waits in FIFO order for an idle lane (one model sequence). It takes the idle lane whose cached
 //     tokens share the longest prefix with its prompt (ties: the lane admitted least recently), keeps that prefix's
 //     KV, and always re-evaluates at least its last prompt token.
 //   * One step = one target forward. Its batch holds, lane by lane, every decoding lane's pending token followed by
-//     its draft tree, then prompt tokens of prefilling lanes in lane order until the batch has 256 tokens.
-//   * Draft depth per decoding lane: its adaptive k (4 to start, at most n_draft), limited by its remaining budget,
-//     half its context room and half its share of the batch. The tree after the pending token at KV row P is
-//     chain_0, alt_0, chain_1, alt_1, ...: chain_i and alt_i are the draft's first and second greedy picks at depth
-//     i, at RoPE position P + 1 + i, KV rows P + 1 + 2i and P + 2 + 2i, both children of chain_{i-1} (of the pending
-//     token for i = 0).
-//   * Acceptance walks down from the pending token: while the target's pick at the current node equals that depth's
-//     chain (or alt) token, that token is accepted, its KV row moves to the next cache position, and the walk goes
-//     on below it (an alt is a leaf); the first pick that matches neither becomes the next pending token. k grows
-//     by one after a fully accepted chain at full depth and shrinks by one when fewer than half the drafts held.
+//     its drafts, then prompt tokens of prefilling lanes in lane order until the batch has 256 tokens.
+//   * Draft depth per decoding lane: its adaptive k (4 to start, at most n_draft), limited by its remaining budget
+//     and by its context room and its share of the batch (both halved for greedy lanes, whose trees hold two tokens
+//     per depth).
+//   * Greedy lanes (temperature <= 0): the tree after the pending token at KV row P is chain_0, alt_0, chain_1,
+//     alt_1, ...: chain_i and alt_i are the draft's first and second greedy picks at depth i, at RoPE position
+//     P + 1 + i, KV rows P + 1 + 2i and P + 2 + 2i, both children of chain_{i-1} (of the pending token for i = 0).
+//     Acceptance walks down from the pending token: while the target's pick at the current node (the first maximum
+//     of its penalized logits) equals that depth's chain (or alt) token, that token is accepted, its KV row moves to
+//     the next cache position, and the walk goes on below it (an alt is a leaf); the first pick that matches neither
+//     becomes the next pending token. k grows by one after a fully accepted chain at full depth and shrinks by one
+//     when fewer than half the drafts held.
+//   * Sampled lanes (temperature > 0): the draft's sampler (the request's parameters, seed + 1, no penalties) draws
+//     a chain d_0 .. d_{k-1}, fed back one token per draft forward; the target sees [pending, d_0, ..] in a row. Each
+//     d_i is verified against the target's distribution at its position (Sampler::verify); the first rejection's
+//     replacement becomes the pending token, a fully accepted chain draws the pending token from the last row. k
+//     grows after a fully accepted chain at full depth and shrinks when fewer than half held.
+//   * Every emitted token counts towards the request sampler's repetition penalties; the distribution of a row
+//     sees the tokens accepted before it.
 //   * A generated token ends its request when it is an end-of-generation id (not emitted, finish "stop"), when the
 //     budget is reached, or when the context has no room for another row (finish "length").
 //
-// Device residency: the draft's rounds run back to back on the stream. Each round's tokens are the previous
-// round's picks, read from a device array (Model::enqueue id redirects); picks are scattered into a per-lane tree
-// array on the device; accepted rows move on the device. The host waits once per step, for the target's picks.
+// Device residency: greedy drafting runs back to back on the stream. Each round's tokens are the previous round's
+// picks, read from a device array (Model::enqueue id redirects); picks are scattered into a per-lane tree array on
+// the device; accepted rows move on the device. The host waits once per step, for the target's picks. Sampled
+// lanes add one wait per draft round (the draw happens on the host); penalized greedy trees add one after the
+// step's wait (the penalties of a tree row depend on its path, which the host learns at that wait).
 #pragma once
 
 #include <chrono>
@@ -33,6 +44,7 @@
 #include <vector>
 
 #include "model.h"
+#include "sampler.h"
 
 namespace malkin_hip {
 
@@ -40,6 +52,7 @@ struct EngineRequest {
   std::vector<int32_t> prompt;
   int max_tokens = 0;          // 0: until the context ends
   std::vector<int32_t> eog;    // end-of-generation ids
+  SamplingParams sampling{0.0f};  // greedy unless set
 };
 
 struct EngineResult {
@@ -77,6 +90,8 @@ class Engine {
     bool decoding = false;
     int32_t pending = 0;  // generated and emitted, not yet in the KV cache
     Clock::time_point admitted, first_token;
+    std::unique_ptr<Sampler> sampler, draft_sampler;
+    bool plain = true;  // greedy without penalties: the device's picks are the tokens
   };
   struct Lane {
     std::vector<int32_t> kv;        // tokens whose target KV rows are valid
@@ -86,6 +101,11 @@ class Engine {
   };
   struct Spec {  // a decoding lane's share of one step
     int lane = 0, depth = 0, root = 0;  // root: batch index of the lane's pending token
+    bool sampled = false;
+    std::vector<int32_t> chain;         // sampled lanes: the drawn drafts
+    std::vector<Distribution> q;        // ... and the draft distributions they were drawn from
+    const Selector* cand = nullptr;     // non-plain lanes: candidates of the target rows root.. (index sel..)
+    int sel = -1;
   };
 
   void admit(std::unique_ptr<Job> job);
@@ -95,7 +115,12 @@ class Engine {
   void draft_forward(const std::vector<BatchToken>& batch, const std::vector<int32_t>& id_from,
                      const std::vector<int32_t>& chain_slot);
   int build_target_batch();
-  void settle(const Spec& sp, const int32_t* picks);
+  void select_known_rows(int decode_rows);
+  void select_tree_rows();
+  int32_t target_pick(const Spec& sp, int node) const;
+  Distribution& target_dist(const Spec& sp, int row);
+  void settle(const Spec& sp);
+  void settle_sampled(const Spec& sp);
   bool emit(Job& job, int32_t id, size_t cached);
   void finish(Lane& lane);
   int32_t* tree_host(int lane) { return tree_h_ + static_cast<size_t>(lane) * 2 * max_depth_; }
@@ -115,6 +140,13 @@ class Engine {
   std::vector<BatchToken> batch_;
   std::vector<int32_t> id_from_;
   std::vector<int> finishing_lanes_;  // prefilling lanes whose last prompt token is in this step's batch
+  std::vector<int> finishing_sel_;    // their candidate rows in sel_ (non-plain jobs), else -1
+
+  // Candidate selection: target rows known before the step's wait, penalized greedy tree rows after it, draft rows.
+  Selector sel_, tree_sel_, draft_sel_;
+  Distribution dist_;
+  std::vector<int32_t> pen_ids_;
+  std::vector<float> pen_amts_;
 
   // Device state: the per-lane draft trees (chain / alt ids by depth), the latest draft picks, the target's picks,
   // and the step's scatter plan (destination slots of each draft forward's picks).

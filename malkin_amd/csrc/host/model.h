@@ -102,7 +102,8 @@ class Model {
   // The picks of the logits rows (in batch order) go to dev_top1 / dev_top2 (device; either may be null).
   void enqueue(const BatchToken* batch, int n, const int32_t* id_from, const int32_t* dev_ids, int32_t* dev_top1,
                int32_t* dev_top2);
-  const float* dev_logits() const { return logits_.as<float>(); }
+  // The last forward's logits rows (device, n_vocab floats each, in batch order); samplers penalize them in place.
+  float* dev_logits() const { return logits_.as<float>(); }
   int n_out() const { return static_cast<int>(lay_.logit_rows.size()); }
 
   // Greedy generation of one sequence (the reference's `malkin bench` protocol, main.cpp:126-143): the prompt in

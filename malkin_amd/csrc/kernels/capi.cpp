@@ -390,4 +390,20 @@ int mk_argmax_top2_noalloc(void* stream, const float* logits, int rows, int n_vo
   return guard([&] { mk::argmax_top2_noalloc(static_cast<hipStream_t>(stream), logits, rows, n_vocab, top1, top2); });
 }
 
+int mk_penalize(mk_ctx* c, float* logits, int64_t stride, const int32_t* rows, int n_rows, int n_vocab,
+                const int32_t* pen_off, const int32_t* pen_id, const float* pen_amt) {
+  return guard([&] {
+    require(logits && n_rows >= 0 && n_vocab > 0 && stride >= n_vocab, "penalize: bad logits");
+    mk::penalize(c->stream, logits, stride, rows, n_rows, n_vocab, pen_off, pen_id, pen_amt);
+  });
+}
+
+int mk_topk(mk_ctx* c, const float* logits, int64_t stride, const int32_t* rows, int n_rows, int n_vocab, int k,
+            float* values, int32_t* ids) {
+  return guard([&] {
+    require(logits && values && ids && n_rows >= 0 && n_vocab > 0 && stride >= n_vocab, "topk: bad arguments");
+    mk::topk(c->stream, logits, stride, rows, n_rows, n_vocab, k, values, ids);
+  });
+}
+
 }  // extern "C"

@@ -148,6 +148,15 @@ void argmax_top2_noalloc(hipStream_t s, const float* logits, int rows, int n_voc
 void argmax_top2(hipStream_t s, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2,
                  void* scratch, size_t scratch_bytes);
 
+// Stochastic sampling's candidate selection (sampler.cpp:24-36). Row r of a launch is logits row rows[r] (rows null:
+// row r) of `stride` floats. penalize: l[pen_id[i]] -= pen_amt[i] for i in pen_off[r] .. pen_off[r + 1] (ids outside
+// the vocabulary skipped). topk: the k (1..1024) largest logits of each row, highest first, ties by lower id, into
+// values / ids [n_rows][k].
+void penalize(hipStream_t s, float* logits, int64_t stride, const int32_t* rows, int n_rows, int n_vocab,
+              const int32_t* pen_off, const int32_t* pen_id, const float* pen_amt);
+void topk(hipStream_t s, const float* logits, int64_t stride, const int32_t* rows, int n_rows, int n_vocab, int k,
+          float* values, int32_t* ids);
+
 // dst[dst_idx[i]] = src[src_idx[i]], i < n; null index arrays are the identity, negative indices skip.
 void move_ids(hipStream_t s, int32_t* dst, const int32_t* dst_idx, const int32_t* src, const int32_t* src_idx,
               int n);

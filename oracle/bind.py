@@ -117,9 +117,20 @@ class Oracle(_Common):
                                     ctypes.c_int]
         L.or_model_kv_row.restype = _P
         L.or_model_kv_row_bytes.restype = ctypes.c_size_t
-        for f in ("or_model_free", "or_model_config", "or_model_forward_batch", "or_model_forward",
-                  "or_model_move_kv", "or_model_kv_row", "or_model_kv_row_bytes"):
-            pass
+        L.or_mt64_seed.argtypes = [_P, ctypes.c_uint64]
+        L.or_mt64_next.restype = ctypes.c_uint64
+        L.or_mt64_next.argtypes = [_P]
+        L.or_mt64_uniform.restype = ctypes.c_double
+        L.or_mt64_uniform.argtypes = [_P]
+        L.or_penalize.argtypes = [_P, _P, _P, ctypes.c_int, ctypes.c_float, ctypes.c_float]
+        L.or_distribution.argtypes = [_P, _P, ctypes.c_int, _P, _P]
+        L.or_draw.restype = ctypes.c_int32
+        L.or_draw.argtypes = [_P, _P, _P, ctypes.c_int]
+        L.or_verify.restype = ctypes.c_int32
+        L.or_verify.argtypes = [_P, _P, _P, ctypes.c_int, _P, _P, ctypes.c_int, ctypes.c_int32, _P]
+        L.or_verify_experiment.restype = ctypes.c_long
+        L.or_verify_experiment.argtypes = [_P, _P, ctypes.c_int, _P, _P, ctypes.c_int, ctypes.c_uint64,
+                                           ctypes.c_uint64, ctypes.c_long, _P, ctypes.c_int]
 
     def exp(self, x):
         return np.float32(self.lib.or_exp(ctypes.c_float(x)))
@@ -175,6 +186,90 @@ class Oracle(_Common):
 
     def model(self, path, n_ctx, n_seq=1, wide=True, no_pack=False):
         return OracleModel(self, path, n_ctx, n_seq, wide | (2 if no_pack else 0))
+
+    def mt64(self, seed):
+        return Mt64(self, seed)
+
+    def sampler(self, seed, penalties=True, **params):
+        return OracleSampler(self, seed, penalties, **params)
+
+    def verify_experiment(self, p, q, target_seed, draft_seed, n_trials, V):
+        """The reference's test_sampler.cpp experiment: (histogram of verified tokens, accepted count)."""
+        pp, pi = _dist_arrays(p)
+        qp, qi = _dist_arrays(q)
+        hist = np.zeros(V, np.int64)
+        acc = self.lib.or_verify_experiment(ptr(pp), ptr(pi), len(pp), ptr(qp), ptr(qi), len(qp), target_seed,
+                                            draft_seed, n_trials, ptr(hist), V)
+        return hist, int(acc)
+
+
+SAMPLING_DEFAULTS = dict(temperature=0.8, top_p=0.95, top_k=40, min_p=0.05, presence=0.0, frequency=0.0)
+
+
+def _dist_arrays(d):
+    """[(p, id), ...] -> float32 probabilities, int32 ids."""
+    return (np.ascontiguousarray([e[0] for e in d], np.float32), np.ascontiguousarray([e[1] for e in d], np.int32))
+
+
+class _OrSampling(ctypes.Structure):
+    _fields_ = [("temperature", ctypes.c_float), ("top_p", ctypes.c_float), ("top_k", ctypes.c_int),
+                ("min_p", ctypes.c_float)]
+
+
+class Mt64:
+    """or_mt64: std::mt19937_64 and libstdc++'s uniform_real_distribution<double> on it."""
+
+    def __init__(self, o, seed):
+        self.o = o
+        self.state = ctypes.create_string_buffer(312 * 8 + 8)
+        o.lib.or_mt64_seed(self.state, seed)
+
+    def next(self):
+        return int(self.o.lib.or_mt64_next(self.state))
+
+    def uniform(self):
+        return float(self.o.lib.or_mt64_uniform(self.state))
+
+
+class OracleSampler:
+    """The reference's Sampler (sampler.h:23-42) over the oracle's C restatement: same methods, distributions as
+    [(p, id), ...] lists, logits modified in place by the penalties."""
+
+    def __init__(self, o, seed, penalties=True, **params):
+        self.o, self.penalties = o, penalties
+        self.p = dict(SAMPLING_DEFAULTS, **params)
+        self.rng = Mt64(o, seed)
+        self.counts = {}
+
+    def accept(self, tok):
+        self.counts[int(tok)] = self.counts.get(int(tok), 0) + 1
+
+    def distribution(self, logits):
+        assert logits.dtype == np.float32 and logits.flags.c_contiguous
+        if self.penalties and self.counts:
+            ids = np.array(list(self.counts.keys()), np.int32)
+            cnt = np.array(list(self.counts.values()), np.int32)
+            self.o.lib.or_penalize(ptr(logits), ptr(ids), ptr(cnt), len(ids), self.p["presence"], self.p["frequency"])
+        sp = _OrSampling(self.p["temperature"], self.p["top_p"], self.p["top_k"], self.p["min_p"])
+        probs = np.zeros(logits.size, np.float32)
+        ids = np.zeros(logits.size, np.int32)
+        n = self.o.lib.or_distribution(ctypes.byref(sp), ptr(logits), logits.size, ptr(probs), ptr(ids))
+        return [(float(probs[i]), int(ids[i])) for i in range(n)]
+
+    def draw(self, d):
+        pp, pi = _dist_arrays(d)
+        return int(self.o.lib.or_draw(self.rng.state, ptr(pp), ptr(pi), len(pp)))
+
+    def sample(self, logits):
+        return self.draw(self.distribution(logits))
+
+    def verify(self, p, q, draft):
+        pp, pi = _dist_arrays(p)
+        qp, qi = _dist_arrays(q) if q else (np.zeros(1, np.float32), np.zeros(1, np.int32))
+        a = ctypes.c_int()
+        t = self.o.lib.or_verify(self.rng.state, ptr(pp), ptr(pi), len(pp), ptr(qp), ptr(qi), len(q), draft,
+                                 ctypes.byref(a))
+        return int(t), bool(a.value)
 
 
 class _ModelBase:
@@ -258,6 +353,18 @@ class Ref(_Common):
         L.ref_model_open.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_char_p,
                                      ctypes.c_int]
         L.ref_isa.restype = ctypes.c_char_p
+        if hasattr(L, "ref_sampler_new"):
+            L.ref_sampler_new.restype = _P
+            L.ref_sampler_new.argtypes = [_P, ctypes.c_int, ctypes.c_uint64, ctypes.c_int]
+            L.ref_sampler_free.argtypes = [_P]
+            L.ref_sampler_accept.argtypes = [_P, ctypes.c_int32]
+            L.ref_sampler_distribution.argtypes = [_P, _P, ctypes.c_int, _P, _P, ctypes.c_int]
+            L.ref_sampler_sample.restype = ctypes.c_int32
+            L.ref_sampler_sample.argtypes = [_P, _P, ctypes.c_int]
+            L.ref_sampler_draw.restype = ctypes.c_int32
+            L.ref_sampler_draw.argtypes = [_P, _P, _P, ctypes.c_int]
+            L.ref_sampler_verify.restype = ctypes.c_int32
+            L.ref_sampler_verify.argtypes = [_P, _P, _P, ctypes.c_int, _P, _P, ctypes.c_int, ctypes.c_int32, _P]
 
     def cpu_ok(self):
         return bool(self.lib.ref_cpu_ok())
@@ -295,6 +402,9 @@ class Ref(_Common):
         self.lib.ref_weight_matmul(_P(h), ptr(x), ptr(xq), ctypes.c_int(n), ptr(y))
         self.lib.ref_weight_free(_P(h))
         return y
+
+    def sampler(self, seed, penalties=True, **params):
+        return RefSampler(self, seed, penalties, **params)
 
     def model(self, path, n_ctx, n_seq=1, wide=True, no_pack=False):
         """no_pack: the reference's MALKIN_NO_PACK (model.cpp:136): no panels, every matmul on the row path."""
@@ -344,3 +454,49 @@ class RefModel(_ModelBase):
 
     def move_kv(self, frm, to, seq=0):
         self.L.ref_model_move_kv(_P(self.h), ctypes.c_int(frm), ctypes.c_int(to), ctypes.c_int(seq))
+
+
+class RefSampler:
+    """The reference's own Sampler (sampler.cpp, compiled into oracle/_ref) behind OracleSampler's methods."""
+
+    def __init__(self, r, seed, penalties=True, **params):
+        self.r = r
+        p = dict(SAMPLING_DEFAULTS, **params)
+        pf = np.array([p["temperature"], p["top_p"], p["min_p"], p["presence"], p["frequency"]], np.float32)
+        self.h = r.lib.ref_sampler_new(ptr(pf), p["top_k"], seed, 1 if penalties else 0)
+
+    def close(self):
+        if self.h:
+            self.r.lib.ref_sampler_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def accept(self, tok):
+        self.r.lib.ref_sampler_accept(self.h, int(tok))
+
+    def distribution(self, logits):
+        assert logits.dtype == np.float32 and logits.flags.c_contiguous
+        probs = np.zeros(logits.size, np.float32)
+        ids = np.zeros(logits.size, np.int32)
+        n = self.r.lib.ref_sampler_distribution(self.h, ptr(logits), logits.size, ptr(probs), ptr(ids), logits.size)
+        return [(float(probs[i]), int(ids[i])) for i in range(n)]
+
+    def draw(self, d):
+        pp, pi = _dist_arrays(d)
+        return int(self.r.lib.ref_sampler_draw(self.h, ptr(pp), ptr(pi), len(pp)))
+
+    def sample(self, logits):
+        return int(self.r.lib.ref_sampler_sample(self.h, ptr(logits), logits.size))
+
+    def verify(self, p, q, draft):
+        pp, pi = _dist_arrays(p)
+        qp, qi = _dist_arrays(q) if q else (np.zeros(1, np.float32), np.zeros(1, np.int32))
+        a = ctypes.c_int()
+        t = self.r.lib.ref_sampler_verify(self.h, ptr(pp), ptr(pi), len(pp), ptr(qp), ptr(qi), len(q), draft,
+                                          ctypes.byref(a))
+        return int(t), bool(a.value)

@@ -1259,3 +1259,159 @@ void or_model_move_kv(or_model* m, int from, int to, int seq) {
     memcpy(m->vcache + (base + to) * m->kv_row, m->vcache + (base + from) * m->kv_row, m->kv_row);
   }
 }
+
+/* ---------------------------------------------------------------- sampling (sampler.cpp:22-141) */
+
+#define MT_N 312
+#define MT_M 156
+
+void or_mt64_seed(or_mt64* g, uint64_t seed) {
+  g->mt[0] = seed;
+  for (int i = 1; i < MT_N; ++i) g->mt[i] = 6364136223846793005ULL * (g->mt[i - 1] ^ (g->mt[i - 1] >> 62)) + (uint64_t)i;
+  g->i = MT_N;
+}
+
+uint64_t or_mt64_next(or_mt64* g) {
+  const uint64_t upper = 0xFFFFFFFF80000000ULL, lower = 0x7FFFFFFFULL, a = 0xB5026F5AA96619E9ULL;
+  if (g->i >= MT_N) { /* regenerate the whole state */
+    for (int k = 0; k < MT_N; ++k) {
+      const uint64_t y = (g->mt[k] & upper) | (g->mt[(k + 1) % MT_N] & lower);
+      g->mt[k] = g->mt[(k + MT_M) % MT_N] ^ (y >> 1) ^ ((y & 1) ? a : 0);
+    }
+    g->i = 0;
+  }
+  uint64_t z = g->mt[g->i++];
+  z ^= (z >> 29) & 0x5555555555555555ULL;
+  z ^= (z << 17) & 0x71D67FFFEDA60000ULL;
+  z ^= (z << 37) & 0xFFF7EEE000000000ULL;
+  z ^= z >> 43;
+  return z;
+}
+
+double or_mt64_uniform(or_mt64* g) {
+  const double u = (double)or_mt64_next(g) / 18446744073709551616.0;
+  return u >= 1.0 ? nextafter(1.0, 0.0) : u;
+}
+
+void or_penalize(float* l, const int32_t* ids, const int* counts, int n, float presence, float frequency) {
+  for (int i = 0; i < n; ++i) l[ids[i]] -= fmaf(frequency, (float)counts[i], presence);
+}
+
+typedef struct {
+  float v;
+  int32_t id;
+} or_cand;
+
+static int cand_before(const void* pa, const void* pb) {
+  const or_cand *a = (const or_cand*)pa, *b = (const or_cand*)pb;
+  if (a->v > b->v) return -1;
+  if (b->v > a->v) return 1;
+  return a->id < b->id ? -1 : a->id > b->id;
+}
+
+int or_distribution(const or_sampling* p, const float* l, int n_vocab, float* probs, int32_t* ids) {
+  if (n_vocab < 1) return 0;
+  if (p->temperature <= 0.0f) { /* the first maximum */
+    probs[0] = 1.0f;
+    ids[0] = or_argmax(l, n_vocab);
+    return 1;
+  }
+  or_cand* c = (or_cand*)malloc(sizeof(or_cand) * (size_t)n_vocab);
+  double* w = (double*)malloc(sizeof(double) * (size_t)n_vocab);
+  for (int i = 0; i < n_vocab; ++i) {
+    c[i].v = l[i];
+    c[i].id = i;
+  }
+  qsort(c, (size_t)n_vocab, sizeof(or_cand), cand_before);
+  const int k = p->top_k > 0 && p->top_k < n_vocab ? p->top_k : n_vocab;
+  for (int i = k; i < n_vocab; ++i) w[i] = 0.0;
+  double sum = 0.0;
+  for (int i = 0; i < k; ++i) {
+    const float e = expf((c[i].v - c[0].v) / p->temperature); /* float weight, as the reference stores it */
+    w[i] = e;
+    sum += e;
+  }
+  const double floor_w = (double)p->min_p * w[0];
+  double kept = 0.0;
+  int n = 0;
+  for (; n < k; ++n) {
+    if (n > 0 && w[n] < floor_w) break;
+    kept += w[n];
+    if (kept >= (double)p->top_p * sum) {
+      ++n;
+      break;
+    }
+  }
+  if (n < 1) n = 1;
+  double total = 0.0;
+  for (int i = 0; i < n; ++i) total += w[i];
+  for (int i = 0; i < n; ++i) {
+    probs[i] = (float)(w[i] / total);
+    ids[i] = c[i].id;
+  }
+  free(c);
+  free(w);
+  return n;
+}
+
+int32_t or_draw(or_mt64* g, const float* probs, const int32_t* ids, int n) {
+  if (n == 1) return ids[0];
+  double r = or_mt64_uniform(g);
+  for (int i = 0; i < n; ++i) {
+    r -= probs[i];
+    if (r <= 0.0) return ids[i];
+  }
+  return ids[n - 1];
+}
+
+static float prob_of(const float* probs, const int32_t* ids, int n, int32_t id) {
+  for (int i = 0; i < n; ++i)
+    if (ids[i] == id) return probs[i];
+  return 0.0f;
+}
+
+int32_t or_verify(or_mt64* g, const float* pp, const int32_t* pi, int np, const float* qp, const int32_t* qi, int nq,
+                  int32_t draft, int* accepted) {
+  const float pd = prob_of(pp, pi, np, draft), qd = prob_of(qp, qi, nq, draft);
+  const double u = or_mt64_uniform(g);
+  *accepted = qd > 0.0f && u * (double)qd < (double)pd;
+  if (*accepted) return draft;
+  float* rp = (float*)malloc(sizeof(float) * (size_t)np);
+  int32_t* ri = (int32_t*)malloc(sizeof(int32_t) * (size_t)np);
+  int m = 0;
+  double total = 0.0;
+  for (int i = 0; i < np; ++i) {
+    const float r = pp[i] - prob_of(qp, qi, nq, pi[i]);
+    if (r > 0.0f) {
+      rp[m] = r;
+      ri[m++] = pi[i];
+      total += r;
+    }
+  }
+  int32_t t;
+  if (m == 0) {
+    t = or_draw(g, pp, pi, np);
+  } else {
+    for (int i = 0; i < m; ++i) rp[i] = (float)(rp[i] / total);
+    t = or_draw(g, rp, ri, m);
+  }
+  free(rp);
+  free(ri);
+  return t;
+}
+
+long or_verify_experiment(const float* pp, const int32_t* pi, int np, const float* qp, const int32_t* qi, int nq,
+                          uint64_t target_seed, uint64_t draft_seed, long n_trials, long* hist, int V) {
+  or_mt64 target, draft;
+  or_mt64_seed(&target, target_seed);
+  or_mt64_seed(&draft, draft_seed);
+  long acc = 0;
+  for (long n = 0; n < n_trials; ++n) {
+    const int32_t d = or_draw(&draft, qp, qi, nq);
+    int a = 0;
+    const int32_t t = or_verify(&target, pp, pi, np, qp, qi, nq, d, &a);
+    if (t >= 0 && t < V) ++hist[t];
+    acc += a;
+  }
+  return acc;
+}

@@ -105,6 +105,44 @@ void or_model_move_kv(or_model* m, int from, int to, int seq);
 const int8_t* or_model_kv_row(const or_model* m, int il, int seq, int pos, int k);
 size_t or_model_kv_row_bytes(const or_model* m);
 
+/* ---- Sampling (sampler.h:10-43, sampler.cpp:22-141) ---- */
+
+/* std::mt19937_64: the 64-bit Mersenne Twister of Matsumoto & Nishimura (2004) with the parameters the C++ standard
+   fixes for it ([rand.predef]: n 312, m 156, r 31, a 0xB5026F5AA96619E9, tempering u 29 / d 0x5555555555555555,
+   s 17 / b 0x71D67FFFEDA60000, t 37 / c 0xFFF7EEE000000000, l 43, initialisation multiplier 6364136223846793005). */
+typedef struct {
+  uint64_t mt[312];
+  int i;
+} or_mt64;
+void or_mt64_seed(or_mt64* g, uint64_t seed);
+uint64_t or_mt64_next(or_mt64* g);
+/* std::uniform_real_distribution<double>(0, 1) on it as libstdc++'s generate_canonical computes it for a 64-bit
+   generator: one output x, (double)x / 2^64, a result that rounds to 1 replaced by the largest double below 1. */
+double or_mt64_uniform(or_mt64* g);
+
+typedef struct {
+  float temperature, top_p;
+  int top_k;
+  float min_p;
+} or_sampling;
+/* The penalty step of Sampler::distribution (sampler.cpp:68-70): l[ids[i]] -= presence + frequency * counts[i], the
+   amount one fused multiply-add (the reference is built with contraction on). */
+void or_penalize(float* l, const int32_t* ids, const int* counts, int n, float presence, float frequency);
+/* The rest of Sampler::distribution (sampler.cpp:71-105) over penalized logits l[n_vocab]: greedy -> the first
+   maximum; else the top_k candidates (value descending, equal values by lower id), temperature weights, min-p and
+   top-p cut, normalisation. Writes the distribution (at most n_vocab entries) and returns its size. */
+int or_distribution(const or_sampling* p, const float* l, int n_vocab, float* probs, int32_t* ids);
+/* Sampler::draw (sampler.cpp:108-116). */
+int32_t or_draw(or_mt64* g, const float* probs, const int32_t* ids, int n);
+/* Sampler::verify (sampler.cpp:124-141). */
+int32_t or_verify(or_mt64* g, const float* pp, const int32_t* pi, int np, const float* qp, const int32_t* qi, int nq,
+                  int32_t draft, int* accepted);
+/* The experiment of the reference's test_sampler.cpp:20-51: n_trials drafts d ~ q drawn by a generator seeded
+   draft_seed, each verified against p by one seeded target_seed; hist[id] counts the verified tokens (ids < V).
+   Returns the number of accepted drafts. */
+long or_verify_experiment(const float* pp, const int32_t* pi, int np, const float* qp, const int32_t* qi, int nq,
+                          uint64_t target_seed, uint64_t draft_seed, long n_trials, long* hist, int V);
+
 #ifdef __cplusplus
 }
 #endif

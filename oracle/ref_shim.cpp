@@ -17,6 +17,7 @@
 #include "kernels.h"
 #include "model.h"
 #include "quant.h"
+#include "sampler.h"
 
 using namespace malkin;
 
@@ -162,5 +163,47 @@ int ref_model_forward(void* h, const int32_t* tokens, int n, int pos, float* log
   }
 }
 void ref_model_move_kv(void* h, int from, int to, int seq) { static_cast<RefModel*>(h)->model->move_kv(from, to, seq); }
+
+// The reference's Sampler (sampler.h:24-43) on caller logits: params as {temperature, top_p, min_p, presence,
+// frequency} floats plus top_k and seed. A handle keeps the sampler (its RNG and penalty counts) across calls.
+void* ref_sampler_new(const float* pf, int top_k, uint64_t seed, int penalties) {
+  SamplingParams p;
+  p.temperature = pf[0];
+  p.top_p = pf[1];
+  p.min_p = pf[2];
+  p.presence_penalty = pf[3];
+  p.frequency_penalty = pf[4];
+  p.top_k = top_k;
+  p.seed = seed;
+  return new Sampler(p, penalties != 0);
+}
+void ref_sampler_free(void* h) { delete static_cast<Sampler*>(h); }
+void ref_sampler_accept(void* h, int32_t id) { static_cast<Sampler*>(h)->accept(id); }
+// distribution() over logits (modified in place, as the reference does); up to cap entries out; returns the size.
+int ref_sampler_distribution(void* h, float* logits, int n_vocab, float* probs, int32_t* ids, int cap) {
+  Dist d;
+  static_cast<Sampler*>(h)->distribution(logits, n_vocab, d);
+  for (int i = 0; i < static_cast<int>(d.size()) && i < cap; ++i) {
+    probs[i] = d[i].first;
+    ids[i] = d[i].second;
+  }
+  return static_cast<int>(d.size());
+}
+int32_t ref_sampler_sample(void* h, float* logits, int n_vocab) { return static_cast<Sampler*>(h)->sample(logits, n_vocab); }
+int32_t ref_sampler_draw(void* h, const float* probs, const int32_t* ids, int n) {
+  Dist d;
+  for (int i = 0; i < n; ++i) d.emplace_back(probs[i], ids[i]);
+  return static_cast<Sampler*>(h)->draw(d);
+}
+int32_t ref_sampler_verify(void* h, const float* pp, const int32_t* pi, int np, const float* qp, const int32_t* qi,
+                           int nq, int32_t draft, int* accepted) {
+  Dist p, q;
+  for (int i = 0; i < np; ++i) p.emplace_back(pp[i], pi[i]);
+  for (int i = 0; i < nq; ++i) q.emplace_back(qp[i], qi[i]);
+  bool a = false;
+  const int32_t t = static_cast<Sampler*>(h)->verify(p, q, draft, a);
+  *accepted = a ? 1 : 0;
+  return t;
+}
 
 }  // extern "C"

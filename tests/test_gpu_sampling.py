@@ -1,0 +1,165 @@
+"""Stochastic sampling on the device: mk_penalize / mk_topk against numpy (ties, infinities, row subsets, k up to
+1024, vocabularies from 5 to 151936), mk_sampler_distribution / mk_sampler_sample over device rows against the
+oracle's Sampler (itself pinned to the compiled reference's in test_sampler.py) with the same seeds and accepted
+tokens, and the engine's sampled and penalized requests, with and without a draft model, against the reference
+Engine's token loop restated over the oracle's model and sampler (tests/engine_ref.py)."""
+import numpy as np
+import pytest
+
+import engine_ref
+import malkin_amd as mk_
+
+pytestmark = pytest.mark.gpu
+
+
+def order_key(x):
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return np.where(u & 0x80000000, (~u) & 0xFFFFFFFF, u | 0x80000000)
+
+
+def expected_topk(row, k):
+    key = order_key(row)
+    idx = np.lexsort((np.arange(len(row)), -key.astype(np.int64)))[:k]
+    return row[idx], idx
+
+
+@pytest.mark.parametrize("V", [5, 1024, 151936])
+@pytest.mark.parametrize("k", [1, 40, 256, 1024])
+def test_topk_vs_numpy(mk, V, k):
+    if k > V:
+        k = V
+    rng = np.random.default_rng(V + k)
+    n_rows = 6
+    x = (rng.standard_normal((n_rows, V)) * 3).astype(np.float32)
+    x[1] = np.round(x[1] * 4) / 4  # many ties: the lower id first
+    x[2, ::7] = -np.inf
+    x[3, :] = 0.0
+    x[3, ::3] = -0.0
+    x[4, rng.integers(V)] = np.inf
+    rows = np.array([5, 0, 3, 1, 2, 4], np.int32)
+    dx, dr = mk.to_device(x), mk.to_device(rows)
+    dv, di = mk.alloc(n_rows * k * 4), mk.alloc(n_rows * k * 4)
+    print("topk", V, k, flush=True)
+    mk_.check(mk_.load().mk_topk(mk.h, dx.ptr, V, dr.ptr, n_rows, V, k, dv.ptr, di.ptr))
+    gv = dv.download(np.float32).reshape(n_rows, k)
+    gi = di.download(np.int32).reshape(n_rows, k)
+    for r in range(n_rows):
+        ev, ei = expected_topk(x[rows[r]], k)
+        assert np.array_equal(gi[r], ei), (V, k, r)
+        assert np.array_equal(gv[r].view(np.uint32), ev.view(np.uint32)), (V, k, r)
+
+
+def test_penalize_vs_numpy(mk):
+    rng = np.random.default_rng(3)
+    V, n_rows = 2000, 4
+    x = rng.standard_normal((n_rows, V)).astype(np.float32)
+    rows = np.array([2, 0, 3, 1], np.int32)
+    lists = [[(5, 0.5), (7, 1.25)], [], [(1999, -0.3), (0, 2.0), (5000, 1.0)], [(3, 0.125)]]
+    off = np.zeros(n_rows + 1, np.int32)
+    ids, amts = [], []
+    for r, l in enumerate(lists):
+        ids += [i for i, _ in l]
+        amts += [a for _, a in l]
+        off[r + 1] = len(ids)
+    ids, amts = np.array(ids, np.int32), np.array(amts, np.float32)
+    dx, dr, do, di, da = mk.to_device(x), mk.to_device(rows), mk.to_device(off), mk.to_device(ids), mk.to_device(amts)
+    mk_.check(mk_.load().mk_penalize(mk.h, dx.ptr, V, dr.ptr, n_rows, V, do.ptr, di.ptr, da.ptr))
+    got = dx.download(np.float32).reshape(n_rows, V)
+    want = x.copy()
+    for r, l in enumerate(lists):
+        for i, a in l:
+            if 0 <= i < V:
+                want[rows[r], i] -= np.float32(a)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+GRID = [
+    dict(),
+    dict(temperature=0.0),
+    dict(temperature=0.0, presence=0.7, frequency=0.2),
+    dict(top_k=0),
+    dict(top_k=1),
+    dict(top_k=1024, top_p=0.98, min_p=0.0),
+    dict(top_k=2000, top_p=0.8),
+    dict(temperature=1.7, top_p=1.0, min_p=0.0),
+    dict(temperature=0.3, top_p=0.5, min_p=0.2),
+    dict(presence=0.5, frequency=0.3),
+]
+
+
+@pytest.mark.parametrize("V", [1024, 151936])
+@pytest.mark.parametrize("params", GRID, ids=[str(g) for g in GRID])
+def test_device_distribution_matches_oracle(mk, oracle, V, params):
+    """20 steps: each a fresh row, its distribution on the device (penalized in place) and in the oracle, then the
+    sampled token accepted by both."""
+    rng = np.random.default_rng(V)
+    s, a = mk_.Sampler(42, **params), oracle.sampler(42, **params)
+    buf = mk.alloc(V * 4)
+    print("distribution", V, params, flush=True)
+    for step in range(20):
+        l = (rng.standard_normal(V) * rng.uniform(0.5, 4)).astype(np.float32)
+        buf.upload(l)
+        d = s.distribution(mk, buf, V)
+        la = l.copy()
+        e = a.distribution(la)
+        assert d == e, (step, d[:4], e[:4])
+        assert np.array_equal(buf.download(np.float32).view(np.uint32), la.view(np.uint32)), step
+        t1, t2 = s.draw(d), a.draw(e)
+        assert t1 == t2, step
+        s.accept(t1)
+        a.accept(t2)
+        buf.upload(l)
+        assert s.sample(mk, buf, V) == a.sample(l.copy()), step
+    s.close()
+    buf.free()
+
+
+REQUESTS = [
+    dict(seed=5),
+    dict(seed=6, temperature=1.1, top_k=0, top_p=0.9, presence=0.4, frequency=0.2),
+    dict(seed=12, temperature=0.7, top_k=1500, min_p=0.01),
+    dict(seed=8, temperature=0.0, frequency=0.6),
+    None,  # greedy, no penalties
+]
+
+
+def check_engine(mk, oracle, model_files, draft_name, requests, budget=40, n_ctx=160):
+    target = mk_.Model(mk, model_files["tiny"], n_ctx, len(requests))
+    draft = mk_.Model(mk, model_files[draft_name], n_ctx, len(requests)) if draft_name else None
+    eng = mk_.Engine(target, draft, n_draft=8)
+    rng = np.random.default_rng(99)
+    prompts = [rng.integers(0, 1024, int(n)).astype(np.int32) for n in rng.integers(3, 40, len(requests))]
+    ids = [eng.submit(p, max_tokens=budget, sampling=r) for p, r in zip(prompts, requests)]
+    eng.run()
+    for rid, p, r in zip(ids, prompts, requests):
+        toks, info = eng.result(rid)
+        t = oracle.model(model_files["tiny"], n_ctx, 1)
+        d = oracle.model(model_files[draft_name], n_ctx, 1) if draft_name else None
+        params = dict(r) if r is not None else dict(seed=1, temperature=0.0)
+        want, winfo = engine_ref.run_request(oracle, t, d, p, budget, n_ctx, **params)
+        t.close()
+        if d:
+            d.close()
+        print("request", rid, draft_name, r, info, winfo, flush=True)
+        assert list(toks) == want, (rid, r)
+        assert info["drafted"] == winfo["drafted"] and info["accepted"] == winfo["accepted"], (rid, r)
+        assert info["finish"] == (1 if winfo["finish"] == "stop" else 0)
+    eng.close()
+    if draft:
+        draft.close()
+    target.close()
+
+
+def test_engine_sampled_requests(mk, oracle, model_files):
+    """Sampled, penalized-greedy and plain requests batched together: each stream is the reference loop's for its
+    seed."""
+    check_engine(mk, oracle, model_files, None, REQUESTS)
+
+
+@pytest.mark.parametrize("draft_name", ["tiny", "tiny-q4km"])
+def test_engine_sampled_speculative(mk, oracle, model_files, draft_name):
+    """With a draft: sampled chains verified by Sampler::verify (the draft = the target itself accepts nearly all,
+    penalties make the target's distribution differ from the draft's), penalized greedy trees."""
+    reqs = [dict(seed=7), dict(seed=11, temperature=0.9, presence=1.5), dict(seed=10, temperature=0.0, frequency=0.6),
+            dict(seed=9, temperature=0.6, top_k=300)]
+    check_engine(mk, oracle, model_files, draft_name, reqs)
