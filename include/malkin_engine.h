@@ -27,7 +27,8 @@ extern "C" {
 typedef struct mk_engine mk_engine;
 
 /* GenResult (engine.h:36-42) without text. finish: 0 = "length" (budget or context end), 1 = "stop" (an
-   end-of-generation id, which is not part of the tokens). */
+   end-of-generation id, which is not part of the tokens), 2 = "cancelled" (an HTTP client went away or the server
+   stopped). */
 typedef struct {
   int32_t prompt_tokens, cached_tokens, completion_tokens, drafted, accepted, finish, done;
   double prefill_ms, decode_ms;

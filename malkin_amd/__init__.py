@@ -97,6 +97,8 @@ SIGNATURES = {
     "mk_engine_submit_sampled": (_I, [_P, _P, _I, _I, _P, _I, _P, _P]),
     "mk_penalize": (_I, [_P, _P, _I64, _P, _I, _I, _P, _P, _P]),
     "mk_topk": (_I, [_P, _P, _I64, _P, _I, _I, _I, _P, _P]),
+    "mk_server_start": (_I, [_P, ctypes.c_char_p, ctypes.c_char_p, _I, ctypes.POINTER(_P), ctypes.POINTER(_I)]),
+    "mk_server_stop": (_I, [_P]),
     "mk_sampler_create": (_I, [_P, _I, ctypes.POINTER(_P)]),
     "mk_sampler_free": (_I, [_P]),
     "mk_sampler_accept": (_I, [_P, ctypes.c_int32]),
@@ -388,6 +390,29 @@ class Engine:
         toks = np.zeros(max(info.completion_tokens, 1), dtype=np.int32)
         check(load().mk_engine_result(self.h, rid, _ptr(toks), len(toks), ctypes.byref(info)))
         return toks[:info.completion_tokens], {f: getattr(info, f) for f, _ in MkRequestInfo._fields_}
+
+
+class Server:
+    """mk_server_*: the HTTP API (include/malkin_server.h) over an Engine (None: health and models only), on
+    host:port (0: a free port, then .port)."""
+
+    def __init__(self, engine=None, model_id="malkin", host="127.0.0.1", port=0):
+        self.engine = engine
+        p, bound = _P(), _I()
+        check(load().mk_server_start(engine.h if engine is not None else None, model_id.encode(), host.encode(), port,
+                                     ctypes.byref(p), ctypes.byref(bound)))
+        self.h, self.port = p.value, bound.value
+
+    def close(self):
+        if self.h:
+            load().mk_server_stop(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class MkSamplingParams(ctypes.Structure):

@@ -33,6 +33,9 @@ HIP_SOURCES = [
     "csrc/host/sampler.cpp",
     "csrc/host/engine.cpp",
     "csrc/host/capi_model.cpp",
+    "csrc/server/json.cpp",
+    "csrc/server/http.cpp",
+    "csrc/server/server.cpp",
 ]
 
 HIP_FLAGS = [
@@ -84,7 +87,7 @@ def build_hip(jobs=None, verbose=False):
     with cf.ThreadPoolExecutor(max_workers=jobs or min(8, os.cpu_count() or 1)) as ex:
         list(ex.map(compile_one, srcs))
     tmp = LIB + ".tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + [_obj(s) for s in srcs])
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", "-o", tmp] + [_obj(s) for s in srcs])
     os.replace(tmp, LIB)
     return LIB
 

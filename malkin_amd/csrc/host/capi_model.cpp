@@ -13,14 +13,7 @@
 #include "engine.h"
 #include "model.h"
 
-struct mk_model {
-  std::unique_ptr<malkin_hip::GgufFile> file;
-  std::unique_ptr<malkin_hip::Model> model;
-};
-
-struct mk_engine {
-  std::unique_ptr<malkin_hip::Engine> engine;
-};
+#include "capi_internal.h"
 
 struct mk_sampler {
   std::unique_ptr<malkin_hip::Sampler> sampler;
@@ -46,6 +39,11 @@ int run(F&& f) {
     mk::set_error("%s", e.what());
     return MK_ERR_INVALID;
   }
+}
+
+// The engine's loop belongs to an HTTP server between mk_server_start and mk_server_stop.
+void not_serving(const mk_engine* e) {
+  if (e->serving) throw std::invalid_argument("engine is serving HTTP (mk_server_stop first)");
 }
 
 malkin_hip::SamplingParams to_params(const mk_sampling_params& p) {
@@ -198,13 +196,17 @@ int mk_engine_create(mk_model* target, mk_model* draft, int n_draft, mk_engine**
 }
 
 int mk_engine_free(mk_engine* e) {
-  return run([&] { delete e; });
+  return run([&] {
+    if (e) not_serving(e);
+    delete e;
+  });
 }
 
 int mk_engine_submit(mk_engine* e, const int32_t* prompt, int n_prompt, int max_tokens, const int32_t* eog, int n_eog,
                      int32_t* request_id) {
   return run([&] {
     if (!e || (n_prompt > 0 && !prompt) || (n_eog > 0 && !eog)) throw std::invalid_argument("mk_engine_submit: null argument");
+    not_serving(e);
     malkin_hip::EngineRequest r;
     if (n_prompt > 0) r.prompt.assign(prompt, prompt + n_prompt);
     if (n_eog > 0) r.eog.assign(eog, eog + n_eog);
@@ -219,6 +221,7 @@ int mk_engine_submit_sampled(mk_engine* e, const int32_t* prompt, int n_prompt, 
   return run([&] {
     if (!e || (n_prompt > 0 && !prompt) || (n_eog > 0 && !eog) || !sampling)
       throw std::invalid_argument("mk_engine_submit_sampled: null argument");
+    not_serving(e);
     malkin_hip::EngineRequest r;
     if (n_prompt > 0) r.prompt.assign(prompt, prompt + n_prompt);
     if (n_eog > 0) r.eog.assign(eog, eog + n_eog);
@@ -232,6 +235,7 @@ int mk_engine_submit_sampled(mk_engine* e, const int32_t* prompt, int n_prompt, 
 int mk_engine_step(mk_engine* e, int32_t* busy) {
   return run([&] {
     if (!e) throw std::invalid_argument("mk_engine_step: null engine");
+    not_serving(e);
     const int b = e->engine->step_once();
     if (busy) *busy = b;
   });
@@ -240,6 +244,7 @@ int mk_engine_step(mk_engine* e, int32_t* busy) {
 int mk_engine_run(mk_engine* e) {
   return run([&] {
     if (!e) throw std::invalid_argument("mk_engine_run: null engine");
+    not_serving(e);
     e->engine->run();
   });
 }
@@ -254,12 +259,14 @@ int mk_engine_steps(mk_engine* e, uint64_t* steps) {
 int mk_engine_result(mk_engine* e, int32_t request_id, int32_t* tokens, int32_t cap, mk_request_info* info) {
   return run([&] {
     if (!e) throw std::invalid_argument("mk_engine_result: null engine");
+    not_serving(e);
     const malkin_hip::EngineResult& r = e->engine->result(request_id);
     if (tokens)
       for (size_t i = 0; i < r.tokens.size() && static_cast<int32_t>(i) < cap; ++i) tokens[i] = r.tokens[i];
     if (info)
       *info = mk_request_info{r.prompt_tokens, r.cached_tokens, r.completion_tokens, r.drafted, r.accepted,
-                               r.finish_reason == "stop" ? 1 : 0, r.done ? 1 : 0, r.prefill_ms, r.decode_ms};
+                               r.finish_reason == "stop" ? 1 : r.finish_reason == "cancelled" ? 2 : 0, r.done ? 1 : 0,
+                               r.prefill_ms, r.decode_ms};
   });
 }
 

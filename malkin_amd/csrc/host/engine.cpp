@@ -106,6 +106,23 @@ const EngineResult& Engine::result(int id) const {
   return *results_[static_cast<size_t>(id)];
 }
 
+void Engine::cancel(int id) {
+  EngineResult* r = results_.at(static_cast<size_t>(id)).get();
+  if (r->done) return;
+  r->finish_reason = "cancelled";
+  for (auto it = waiting_.begin(); it != waiting_.end(); ++it)
+    if ((*it)->res == r) {
+      r->done = true;
+      waiting_.erase(it);
+      return;
+    }
+  for (Lane& lane : lanes_)
+    if (lane.job && lane.job->res == r) {
+      finish(lane);
+      return;
+    }
+}
+
 int Engine::step_once() {
   while (!waiting_.empty() && busy_ < static_cast<int>(lanes_.size())) {
     admit(std::move(waiting_.front()));
@@ -544,7 +561,7 @@ bool Engine::emit(Job& job, int32_t id, size_t cached) {
 
 void Engine::finish(Lane& lane) {
   Job& job = *lane.job;
-  job.res->decode_ms = ms_between(job.first_token, Clock::now());
+  job.res->decode_ms = job.decoding ? ms_between(job.first_token, Clock::now()) : 0.0;
   job.res->done = true;
   lane.job.reset();
   --busy_;

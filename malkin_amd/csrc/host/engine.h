@@ -57,7 +57,7 @@ struct EngineRequest {
 
 struct EngineResult {
   std::vector<int32_t> tokens;          // generated ids (an end-of-generation id is not included)
-  std::string finish_reason = "length";  // "stop" (end-of-generation id) | "length" (budget or context)
+  std::string finish_reason = "length";  // "stop" (end-of-generation id) | "length" (budget or context) | "cancelled"
   int prompt_tokens = 0, cached_tokens = 0, completion_tokens = 0;
   int drafted = 0, accepted = 0;
   double prefill_ms = 0, decode_ms = 0;
@@ -78,7 +78,12 @@ class Engine {
   int step_once();
   void run();  // steps until no request waits or runs
   const EngineResult& result(int id) const;
+  // Ends a waiting or running request now, finish "cancelled" (the reference's cancelled generation,
+  // engine.cpp:509-512); a finished request is left as it is.
+  void cancel(int id);
   int busy() const { return busy_; }
+  int n_ctx() const { return target_->n_ctx(); }
+  int n_vocab() const { return target_->cfg().n_vocab; }
   uint64_t steps() const { return steps_; }
 
  private:
