@@ -43,6 +43,14 @@ int mk_destroy(mk_ctx* ctx);
 const char* mk_device_name(const mk_ctx* ctx);
 const char* mk_last_error(void);
 int mk_synchronize(mk_ctx* ctx);
+/* Grows the context's device scratch buffer to at least `bytes` (never shrinks; waits for the stream first). Calls
+   that use the scratch (mk_attention on rows longer than one workgroup's LDS, mk_argmax_top2) then run without
+   allocating, also under graph capture. No reference counterpart (the CPU engine's scratch is host memory). */
+int mk_reserve_scratch(mk_ctx* ctx, size_t bytes);
+/* Scratch mk_attention needs for `pairs` (token, query head) pairs over up to max_keys keys: 0 while a row fits in
+   one workgroup's LDS (about 7600 keys at head_dim 128); beyond that, global slots of 2 floats per key per pair
+   (up to 1024 pairs at once). */
+size_t mk_attention_scratch_bytes(int head_dim, int max_keys, int pairs);
 /* Host waits on the device made by this library so far (stream and event synchronizations, including those inside
    mk_upload / mk_download / mk_free), for tests that bound the waits of a token loop. */
 uint64_t mk_host_waits(void);
@@ -192,7 +200,8 @@ int mk_attention_decode(mk_ctx* ctx, const float* qkv, int64_t stride, int n, in
                         int layer, float* out, int64_t out_stride, int max_keys);
 /* Model::attention (model.cpp:204-247) over the device cache: token t attends with its n_head query heads to rows
    0..n_keys[t]-1 of sequence seq[t], then (tree verification) rows anc[anc_off[t] .. anc_off[t+1]) when anc_off is
-   not NULL. max_keys bounds n_keys[t] + ancestors for every t. */
+   not NULL. max_keys bounds n_keys[t] + ancestors for every t. Rows longer than one workgroup's LDS holds use the
+   context's scratch (mk_reserve_scratch, mk_attention_scratch_bytes); with none reserved they fail. */
 int mk_attention(mk_ctx* ctx, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int n_head,
                  const mk_kv_cache* kv, int layer, const int32_t* seq, const int32_t* n_keys, const int32_t* anc_off,
                  const int32_t* anc, int max_keys);

@@ -32,6 +32,8 @@ SIGNATURES = {
     "mk_device_name": (ctypes.c_char_p, [_P]),
     "mk_last_error": (ctypes.c_char_p, []),
     "mk_synchronize": (_I, [_P]),
+    "mk_reserve_scratch": (_I, [_P, _SZ]),
+    "mk_attention_scratch_bytes": (_SZ, [_I, _I, _I]),
     "mk_stream": (_P, [_P]),
     "mk_malloc": (_I, [_P, _SZ, ctypes.POINTER(_P)]),
     "mk_free": (_I, [_P, _P]),

@@ -345,6 +345,9 @@ Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide, bo
 
   kv_ = mk_kv_cache{kc_.as<int8_t>(), vc_.as<int8_t>(), ks_.as<float>(), vs_.as<float>(), c.n_layer, n_seq_, KV, D,
                     n_ctx_};
+  // Rows longer than one workgroup's LDS keep their attention scores in the context's scratch (global slots, one
+  // per workgroup in flight): reserved now, so that no forward allocates (graphs capture them).
+  ck(mk_reserve_scratch(ctx_, mk_attention_scratch_bytes(D, n_ctx_, std::min(static_cast<int>(T) * H, 256))));
 
   // Layout block (see model.h) and its pinned staging ring.
   layout_words_ = 7 * T + (B + 1) + B * (B + 1) / 2;

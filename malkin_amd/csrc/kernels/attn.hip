@@ -150,29 +150,18 @@ struct KLane<16> {
   __device__ static int8_t at(T w, int c) { return (int8_t)((&w.x)[c >> 2] >> (8 * (c & 3))); }
 };
 
-template <int D, bool PERM>
-__global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restrict__ q, int64_t q_stride,
-                                                            float* __restrict__ out, int64_t out_stride, int G,
-                                                            float scale, AttnAddr a, const int32_t* __restrict__ seqs,
-                                                            const int32_t* __restrict__ n_keys,
-                                                            const int32_t* __restrict__ anc_off,
-                                                            const int32_t* __restrict__ anc, int n, int H) {
+// One (token, query head) of k_attention / k_attention_long. LONG: the scores and P.V coefficients live in the
+// global slot gsc [2][gcap] instead of LDS (any key count); the V tiles start after the softmax, and each chunk's
+// coefficients and e values are staged into LDS with its V tile (the chains and the lane sums read LDS only).
+template <int D, bool PERM, bool LONG>
+__device__ __forceinline__ void attend_pair(int t, int h, const float* __restrict__ q, int64_t q_stride,
+                                            float* __restrict__ out, int64_t out_stride, int G, float scale,
+                                            const AttnAddr& a, const int32_t* __restrict__ seqs,
+                                            const int32_t* __restrict__ n_keys, const int32_t* __restrict__ anc_off,
+                                            const int32_t* __restrict__ anc, float* __restrict__ gsc, int gcap) {
   constexpr int DC = D / 16;
   using T = AttnTile<D>;
-  // Workgroups are dealt to the 8 XCDs in turn (workgroup w on XCD w % 8). (token, head) pairs are numbered
-  // KV-group-major (group, token, head in group) and XCD x takes a contiguous run of them: a KV group's K/V rows are
-  // read into one XCD's L2, and in prefill every XCD gets tokens of all lengths.
   const int tid = threadIdx.x;
-  int t, h;
-  if ((n * H) % 8 == 0) {
-    const int pair = (int)(blockIdx.x % 8) * (n * H / 8) + (int)(blockIdx.x / 8);
-    const int grp = pair / (n * G), rem = pair % (n * G);
-    t = rem / G;
-    h = grp * G + rem % G;
-  } else {
-    t = (int)blockIdx.x / H;
-    h = (int)blockIdx.x % H;
-  }
   const int g = h / G;
   const int n0 = n_keys[t];
   const int e0 = anc_off ? anc_off[t] : 0, ne = anc_off ? anc_off[t + 1] - e0 : 0;
@@ -181,9 +170,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
   extern __shared__ int4 smem4[];
   float* tiles = reinterpret_cast<float*>(smem4);                 // 2 x [D][stride] fp32
   float* qs = tiles + 2 * T::tile / 4;                           // D
-  float* sc = qs + D;                                            // nk_pad: scores, then e^(s - max)
-  float* pv = sc + nk_pad;                                       // nk_pad: e * v-scale, zero past nk
-  int* anc_s = reinterpret_cast<int*>(pv + nk_pad);              // ne: KV rows of keys n0 .. nk - 1
+  // LONG: per chunk (double-buffered) its P.V coefficients and e values, then the ancestors; the full arrays are
+  // global.
+  float* sc = LONG ? gsc : qs + D;                               // nk_pad: scores, then e^(s - max)
+  float* pv = LONG ? gsc + gcap : sc + nk_pad;                   // nk_pad: e * v-scale, zero past nk
+  float* pch = qs + D;                                           // LONG: [2][chunk] coefficients
+  float* ech = pch + 2 * T::chunk;                               // LONG: [2][chunk] e values
+  int* anc_s = reinterpret_cast<int*>(pv + nk_pad);              // !LONG, ne: KV rows of keys n0 .. nk - 1
   __shared__ float red[kAttnThreads / 64];
   __shared__ float inv_s;
   const int64_t sq = seqs[t];
@@ -193,11 +186,12 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
   const char* vsb = a.vs + sq * a.s_seq + g * a.s_head;
   // Tree ancestors go to LDS first: a key row read from global memory would make every later load wait for all
   // earlier ones (the compiler's wait counts are per wave and in order), serialising the K and V prefetches.
-  if (ne > 0) {
+  // LONG: ancestors are read from global memory (their count is not bounded by the LDS reservation).
+  if (!LONG && ne > 0) {
     for (int i = tid; i < ne; i += kAttnThreads) anc_s[i] = anc[e0 + i];
     lds_barrier();
   }
-  auto key_row = [&](int j) -> int64_t { return j < n0 ? j : anc_s[j - n0]; };
+  auto key_row = [&](int j) -> int64_t { return j < n0 ? j : LONG ? anc[e0 + j - n0] : anc_s[j - n0]; };
 
   // V staging: task = 4 consecutive keys x 16 consecutive values, written as 16 float4 of the transposed tile.
   constexpr int NG = T::groups;
@@ -205,6 +199,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
   const int grp = (tid - D) / T::tasks, task = (tid - D) % T::tasks;
   auto mine = [&](int c) { return stager && grp == c % NG; };
   uint4 vreg[4];
+  // LONG: the chunk's coefficients and e values ride with its V rows (2 chunk floats over the group's tasks).
+  constexpr int PE = (2 * T::chunk + T::tasks - 1) / T::tasks;
+  float pe[LONG ? PE : 1];
   auto load_chunk = [&](int c) {
     if (!mine(c)) return;
     const int kq = task % (T::chunk / 4), db = task / (T::chunk / 4);
@@ -212,6 +209,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
     for (int i = 0; i < 4; ++i) {
       const int j = c * T::chunk + 4 * kq + i;
       vreg[i] = j < nk ? *reinterpret_cast<const uint4*>(vb + key_row(j) * a.k_row + 16 * db) : make_uint4(0, 0, 0, 0);
+    }
+    if constexpr (LONG) {
+#pragma unroll
+      for (int u = 0; u < PE; ++u) {
+        const int idx = task + u * T::tasks, j = c * T::chunk + idx % T::chunk;
+        pe[u] = idx < 2 * T::chunk && j < nk_pad ? (idx < T::chunk ? pv : sc)[j] : 0.0f;
+      }
     }
   };
   auto store_chunk = [&](int c) {
@@ -225,12 +229,19 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
       for (int i = 0; i < 4; ++i) f[i] = (float)(int8_t)((&vreg[i].x)[v >> 2] >> (8 * (v & 3)));
       *reinterpret_cast<float4*>(tile + (16 * db + v) * T::stride + 4 * kq) = make_float4(f[0], f[1], f[2], f[3]);
     }
+    if constexpr (LONG) {
+#pragma unroll
+      for (int u = 0; u < PE; ++u) {
+        const int idx = task + u * T::tasks;
+        if (idx < 2 * T::chunk) (idx < T::chunk ? pch : ech)[(c & 1) * T::chunk + idx % T::chunk] = pe[u];
+      }
+    }
   };
   const int chunks = (nk + T::chunk - 1) / T::chunk;
   // q first (its wait then covers it alone), then each staging group's first tile: in flight during the scores.
   const float* qh = q + t * q_stride + (int64_t)h * D;
   const float qv = tid < D ? qh[tid] : 0.0f;
-  if (stager && grp < chunks) load_chunk(grp);
+  if (!LONG && stager && grp < chunks) load_chunk(grp);  // LONG: the V pipeline starts after the softmax
 
   if constexpr (PERM) {
     // 16 lanes per key: group grp of the workgroup takes keys grp, grp + 64, ...; KB keys per group in flight.
@@ -319,9 +330,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
       pv[j] = vscale;
     }
   }
-  store_chunk(0);
-  if (NG < chunks) load_chunk(NG);
-  lds_barrier();
+  if constexpr (LONG) {
+    __syncthreads();  // the scores are in global memory
+  } else {
+    store_chunk(0);
+    if (NG < chunks) load_chunk(NG);
+    lds_barrier();
+  }
 
   // softmax_inplace (kernels_avx512.cpp:205-226).
   float m = -INFINITY;
@@ -336,20 +351,29 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
     sc[j] = e;
     pv[j] = e * pv[j];
   }
-  for (int j = nk + tid; j < nk_pad; j += kAttnThreads) pv[j] = 0.0f;
+  for (int j = nk + tid; j < nk_pad; j += kAttnThreads) {
+    pv[j] = 0.0f;
+    if constexpr (LONG) sc[j] = 0.0f;
+  }
+  if constexpr (LONG) {
+    __syncthreads();  // e and the coefficients are in global memory; now the V pipeline
+    if (stager && grp < chunks) load_chunk(grp);
+    store_chunk(0);
+    if (NG < chunks) load_chunk(NG);
+  }
   lds_barrier();
 
   // P.V (kernels_avx512.cpp:247-265): chunk c from tile c & 1 while chunk c + 1 is stored and c + 1 + NG loaded.
   // The chain waves are latency-bound: at raised priority they issue as soon as their operands are ready instead of
   // queueing behind the staging waves of their SIMD.
   if (tid < D) __builtin_amdgcn_s_setprio(3);
-  float acc = 0.0f;
+  float acc = 0.0f, lane_sum = 0.0f;
   for (int c = 0; c < chunks; ++c) {
     if (tid < D) {
       const int j0 = c * T::chunk;
       const int len = min(T::chunk, nk_pad - j0);  // a multiple of 16
       const float4* vr = reinterpret_cast<const float4*>(tiles + (c & 1) * (T::tile / 4) + tid * T::stride);
-      const float* pc = pv + j0 + (tid & 15);
+      const float* pc = (LONG ? pch + (c & 1) * T::chunk : pv + j0) + (tid & 15);
       // Two register sets alternate: a 16-key group's LDS reads are issued while the previous group's chain runs
       // (past the last group they re-read it). The scheduling barriers keep the reads ahead of the chain.
       float4 a[4], b[4];
@@ -389,8 +413,15 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
         chain(b, pb);
       }
     } else if (tid >= kSumThread) {
-      if (c == 0) {
-        const int l = tid - kSumThread;
+      const int l = tid - kSumThread;
+      if constexpr (LONG) {  // this chunk's part of lane l's sequential sum (chunks are whole 16-key groups)
+        const int j0 = c * T::chunk;
+        for (int j = l; j < T::chunk && j0 + j < nk; j += 16) lane_sum = lane_sum + ech[(c & 1) * T::chunk + j];
+        if (c + 1 == chunks) {
+          const float s = reduce16_lanes(lane_sum);
+          if (l == 0) inv_s = 1.0f / s;
+        }
+      } else if (c == 0) {
         float s = 0.0f;
 #pragma unroll 8
         for (int j = l; j < nk; j += 16) s = s + sc[j];
@@ -404,6 +435,48 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
     lds_barrier();
   }
   if (tid < D) out[t * out_stride + (int64_t)h * D + tid] = acc * inv_s;
+}
+
+template <int D, bool PERM>
+__global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restrict__ q, int64_t q_stride,
+                                                            float* __restrict__ out, int64_t out_stride, int G,
+                                                            float scale, AttnAddr a, const int32_t* __restrict__ seqs,
+                                                            const int32_t* __restrict__ n_keys,
+                                                            const int32_t* __restrict__ anc_off,
+                                                            const int32_t* __restrict__ anc, int n, int H) {
+  // Workgroups are dealt to the 8 XCDs in turn (workgroup w on XCD w % 8). (token, head) pairs are numbered
+  // KV-group-major (group, token, head in group) and XCD x takes a contiguous run of them: a KV group's K/V rows are
+  // read into one XCD's L2, and in prefill every XCD gets tokens of all lengths.
+  int t, h;
+  if ((n * H) % 8 == 0) {
+    const int pair = (int)(blockIdx.x % 8) * (n * H / 8) + (int)(blockIdx.x / 8);
+    const int grp = pair / (n * G), rem = pair % (n * G);
+    t = rem / G;
+    h = grp * G + rem % G;
+  } else {
+    t = (int)blockIdx.x / H;
+    h = (int)blockIdx.x % H;
+  }
+  attend_pair<D, PERM, false>(t, h, q, q_stride, out, out_stride, G, scale, a, seqs, n_keys, anc_off, anc, nullptr, 0);
+}
+
+// Rows with more keys than LDS holds: workgroup w owns the global slot w (2 gcap floats) and takes the (token,
+// head) pairs w, w + grid, ... in turn.
+template <int D, bool PERM>
+__global__ __launch_bounds__(kAttnThreads) void k_attention_long(const float* __restrict__ q, int64_t q_stride,
+                                                                 float* __restrict__ out, int64_t out_stride, int G,
+                                                                 float scale, AttnAddr a,
+                                                                 const int32_t* __restrict__ seqs,
+                                                                 const int32_t* __restrict__ n_keys,
+                                                                 const int32_t* __restrict__ anc_off,
+                                                                 const int32_t* __restrict__ anc, int n, int H,
+                                                                 float* __restrict__ gsc, int gcap) {
+  float* slot = gsc + (size_t)blockIdx.x * 2 * (size_t)gcap;
+  for (int pair = (int)blockIdx.x; pair < n * H; pair += (int)gridDim.x) {
+    __syncthreads();  // the previous pair's LDS and slot are no longer read
+    attend_pair<D, PERM, true>(pair / H, pair % H, q, q_stride, out, out_stride, G, scale, a, seqs, n_keys, anc_off,
+                               anc, slot, gcap);
+  }
 }
 
 // Attention of one query head of one token per workgroup for plain tokens (decode steps and other short plain
@@ -1288,9 +1361,16 @@ bool attention_decode_fused(hipStream_t s, const float* qkv, int64_t stride, flo
   return true;
 }
 
+size_t attention_scratch_bytes(int D, int max_keys, int pairs) {
+  const int tile = D == 64 ? AttnTile<64>::tile : D == 128 ? AttnTile<128>::tile : AttnTile<256>::tile;
+  const int nk_pad = attn_keys_pad(max_keys);
+  if (attn_lds_bytes(tile, D, nk_pad) <= 160 * 1024 - 1024) return 0;
+  return (size_t)std::min(pairs, 1024) * 2 * (size_t)nk_pad * sizeof(float);
+}
+
 void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int H, int KV,
                int D, float scale, const AttnAddr& a, const int32_t* seq, const int32_t* n_keys,
-               const int32_t* anc_off, const int32_t* anc, int max_keys) {
+               const int32_t* anc_off, const int32_t* anc, int max_keys, void* scratch, size_t scratch_bytes) {
   if (n <= 0) return;
   require(D % 16 == 0 && D <= 256 && H % KV == 0 && max_keys > 0, "attention: unsupported head layout");
   const int G = H / KV;
@@ -1319,25 +1399,49 @@ void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int6
     launch_dec<false>(s, q, q_stride, out, out_stride, n, H, D, G, scale, a, seq, n_keys, max_keys, DecFuse{});
   } else if (G <= 16 && (D == 64 || D == 128 || D == 256) && aligned) {
     const int tile = D == 64 ? AttnTile<64>::tile : D == 128 ? AttnTile<128>::tile : AttnTile<256>::tile;
-    const size_t lds = attn_lds_bytes(tile, D, attn_keys_pad(max_keys));
-    require(lds <= 160 * 1024 - 1024, "attention: too many keys for one workgroup");
-    auto go = [&](auto kernel) {
-      static bool attr = false;
-      if (!attr) {
+    const int nk_pad = attn_keys_pad(max_keys);
+    const size_t lds = attn_lds_bytes(tile, D, nk_pad);
+    auto attr = [&](auto kernel, bool& done) {
+      if (!done) {
         check(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                                   160 * 1024 - 1024),
               "hipFuncSetAttribute");
-        attr = true;
+        done = true;
       }
-      hipLaunchKernelGGL(kernel, dim3(n * H), dim3(kAttnThreads), lds, s, q, q_stride, out, out_stride, G, scale, a,
-                         seq, n_keys, anc_off, anc, n, H);
     };
-    if (D == 64)
-      a.k_perm ? go(k_attention<64, true>) : go(k_attention<64, false>);
-    else if (D == 128)
-      a.k_perm ? go(k_attention<128, true>) : go(k_attention<128, false>);
-    else
-      a.k_perm ? go(k_attention<256, true>) : go(k_attention<256, false>);
+    if (lds <= 160 * 1024 - 1024) {
+      auto go = [&](auto kernel) {
+        static bool done = false;
+        attr(kernel, done);
+        hipLaunchKernelGGL(kernel, dim3(n * H), dim3(kAttnThreads), lds, s, q, q_stride, out, out_stride, G, scale, a,
+                           seq, n_keys, anc_off, anc, n, H);
+      };
+      if (D == 64)
+        a.k_perm ? go(k_attention<64, true>) : go(k_attention<64, false>);
+      else if (D == 128)
+        a.k_perm ? go(k_attention<128, true>) : go(k_attention<128, false>);
+      else
+        a.k_perm ? go(k_attention<256, true>) : go(k_attention<256, false>);
+    } else {
+      // More keys than LDS holds: scores and coefficients in global slots of the caller's scratch.
+      const size_t slot = 2 * (size_t)nk_pad * sizeof(float);
+      const int slots = (int)std::min<size_t>({(size_t)n * H, scratch_bytes / slot, (size_t)1024});
+      require(scratch && slots >= 1, "attention: too many keys for the scratch buffer (mk_reserve_scratch)");
+      const int chunk = D == 64 ? AttnTile<64>::chunk : D == 128 ? AttnTile<128>::chunk : AttnTile<256>::chunk;
+      const size_t lds_long = 2 * (size_t)tile + 4 * ((size_t)D + 4 * (size_t)chunk);
+      auto go = [&](auto kernel) {
+        static bool done = false;
+        attr(kernel, done);
+        hipLaunchKernelGGL(kernel, dim3(slots), dim3(kAttnThreads), lds_long, s, q, q_stride, out, out_stride, G,
+                           scale, a, seq, n_keys, anc_off, anc, n, H, static_cast<float*>(scratch), nk_pad);
+      };
+      if (D == 64)
+        a.k_perm ? go(k_attention_long<64, true>) : go(k_attention_long<64, false>);
+      else if (D == 128)
+        a.k_perm ? go(k_attention_long<128, true>) : go(k_attention_long<128, false>);
+      else
+        a.k_perm ? go(k_attention_long<256, true>) : go(k_attention_long<256, false>);
+    }
   } else {
     const size_t lds = (size_t)(D + 2 * (size_t)max_keys) * sizeof(float);
     require(lds <= 60 * 1024, "attention: too many keys for one workgroup");

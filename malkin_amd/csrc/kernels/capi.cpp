@@ -81,6 +81,24 @@ int mk_destroy(mk_ctx* c) {
 
 const char* mk_device_name(const mk_ctx* c) { return c ? c->name : ""; }
 
+int mk_reserve_scratch(mk_ctx* c, size_t bytes) {
+  return guard([&] {
+    if (bytes <= c->scratch_bytes) return;
+    check(hipSetDevice(c->device), "hipSetDevice");
+    mk::count_host_wait();
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    void* p = nullptr;
+    check(hipMalloc(&p, bytes), "hipMalloc");
+    (void)hipFree(c->scratch);
+    c->scratch = p;
+    c->scratch_bytes = bytes;
+  });
+}
+
+size_t mk_attention_scratch_bytes(int head_dim, int max_keys, int pairs) {
+  return head_dim > 0 && max_keys > 0 && pairs > 0 ? mk::attention_scratch_bytes(head_dim, max_keys, pairs) : 0;
+}
+
 int mk_synchronize(mk_ctx* c) {
   return guard([&] {
     mk::count_host_wait();
@@ -308,7 +326,7 @@ int mk_attend_gqa(mk_ctx* c, const float* q, int G, int D, const int8_t* k, cons
     mk::AttnAddr a{k, v, reinterpret_cast<const char*>(k) + soff, reinterpret_cast<const char*>(v) + soff,
                    0, 0, (int64_t)stride, 0, 0, (int64_t)stride, 0};
     mk::attention(c->stream, q, (int64_t)G * D, out, (int64_t)G * D, 1, G, 1, D, scale, a, dm, dm + 1,
-                  ne > 0 ? dm + 2 : nullptr, extra, n + ne);
+                  ne > 0 ? dm + 2 : nullptr, extra, n + ne, c->scratch, c->scratch_bytes);
   });
 }
 
@@ -341,7 +359,7 @@ int mk_attention(mk_ctx* c, const float* q, int64_t q_stride, float* out, int64_
                    (int64_t)kv->n_head_kv * rows * 4, rows * 4, 4, 1};
     const float scale = 1.0f / std::sqrt(static_cast<float>(D));  // model.cpp:208
     mk::attention(c->stream, q, q_stride, out, out_stride, n, n_head, kv->n_head_kv, D, scale, a, seq, n_keys, anc_off,
-                  anc, max_keys);
+                  anc, max_keys, c->scratch, c->scratch_bytes);
   });
 }
 

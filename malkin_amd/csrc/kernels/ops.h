@@ -118,11 +118,15 @@ struct AttnAddr {
 // (kernels_avx512.cpp:234-244) multiplies, e = 16 c + l for c < DC, are contiguous at DC * l.
 __host__ __device__ constexpr int kv_perm(int e, int DC) { return DC * (e & 15) + (e >> 4); }
 // q [n][H*D] (token stride q_stride floats), out [n][H*D] (stride out_stride). Per token t: keys rows
-// 0..n_keys[t]-1 of sequence seq[t], then anc[anc_off[t] .. anc_off[t+1]) when anc_off is non-null.
+// 0..n_keys[t]-1 of sequence seq[t], then anc[anc_off[t] .. anc_off[t+1]) when anc_off is non-null. Rows with more
+// keys than one workgroup's LDS holds keep their scores in `scratch` (attention_scratch_bytes of it for full speed;
+// a smaller scratch runs fewer workgroups at a time; one without room for a single row fails).
 void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int H, int KV,
                int D, float scale,
                const AttnAddr& a, const int32_t* seq, const int32_t* n_keys, const int32_t* anc_off,
-               const int32_t* anc, int max_keys);
+               const int32_t* anc, int max_keys, void* scratch, size_t scratch_bytes);
+// Scratch the attention of `pairs` (token, head) pairs over max_keys keys uses (0: none).
+size_t attention_scratch_bytes(int D, int max_keys, int pairs);
 
 // qk_norm_rope_kv followed by attention in one launch, for batches whose tokens are plain (no tree) and belong to
 // distinct sequences, so that no token reads another's new KV row. qkv rows: H query heads, KV key heads, KV value

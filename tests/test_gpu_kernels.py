@@ -533,3 +533,82 @@ def test_attention_decode_fused(mk, case):
     for x, y in zip(ba, bb):
         assert np.array_equal(x.download(np.uint8), y.download(np.uint8))
     assert np.array_equal(dqb.download(np.float32), qkv.reshape(-1))  # raw projections untouched
+
+
+# Rows longer than one workgroup's LDS (about 7600 keys at D = 128): scores in global slots of the context's scratch.
+# (D, H, KV, token seqs, n_keys, n_ctx, ancestors per token)
+LONG_CASES = [
+    (128, 8, 2, [0], [8200], 8200, None),                                     # a decode step, G = 4
+    (128, 4, 4, [0, 1, 0], [12000, 9000, 11000], 12100, None),               # G = 1, two sequences
+    (64, 4, 2, [0, 0], [16500, 16400], 16500, None),                         # D = 64
+    (128, 8, 2, [0, 0, 0], [8000, 8000, 8000], 8100, [[], [8001], [8001, 8003]]),  # a tree: ancestors past the prefix
+]
+
+
+@pytest.mark.parametrize("case", range(len(LONG_CASES)))
+def test_attention_long_rows_vs_oracle(mk, oracle, case):
+    D, H, KV, seqs, nks, n_ctx, ancs = LONG_CASES[case]
+    G, n, n_seq = H // KV, len(seqs), max(seqs) + 1
+    print("long attention case", case, dict(D=D, H=H, KV=KV, n=n, keys=max(nks)), flush=True)
+    rng = np.random.default_rng(700 + case)
+    k8 = rng.integers(-127, 128, (n_seq, KV, n_ctx, D), dtype=np.int8)
+    v8 = rng.integers(-127, 128, (n_seq, KV, n_ctx, D), dtype=np.int8)
+    ks = rng.uniform(0.001, 0.05, (n_seq, KV, n_ctx)).astype(np.float32)
+    vs = rng.uniform(0.001, 0.05, (n_seq, KV, n_ctx)).astype(np.float32)
+    q = (rng.standard_normal((n, H * D)) * 3).astype(np.float32)
+    dk = mk.to_device(np.ascontiguousarray(k8[..., np.argsort(_kv_perm(D))]))
+    dv, dks, dvs, dq = mk.to_device(v8), mk.to_device(ks), mk.to_device(vs), mk.to_device(q)
+    dseq, dnk = mk.to_device(np.array(seqs, np.int32)), mk.to_device(np.array(nks, np.int32))
+    anc_off = anc = None
+    max_keys = max(nks)
+    if ancs is not None:
+        off = np.cumsum([0] + [len(a) for a in ancs]).astype(np.int32)
+        flat = np.array([r for a in ancs for r in a] or [0], np.int32)
+        anc_off, anc = mk.to_device(off), mk.to_device(flat)
+        max_keys = max(nk + len(a) for nk, a in zip(nks, ancs))
+    out = mk.alloc(n * H * D * 4)
+    kv = mk_.MkKvCache(dk.ptr, dv.ptr, dks.ptr, dvs.ptr, 1, n_seq, KV, D, n_ctx)
+    need = L().mk_attention_scratch_bytes(D, max_keys, n * H)
+    assert need > 0
+    mk_.check(L().mk_reserve_scratch(mk.h, need))
+    mk_.check(L().mk_attention(mk.h, dq.ptr, H * D, out.ptr, H * D, n, H, ctypes.byref(kv), 0, dseq.ptr, dnk.ptr,
+                               anc_off.ptr if anc_off is not None else None, anc.ptr if anc is not None else None,
+                               max_keys))
+    got = out.download(np.float32).reshape(n, H * D)
+    row = KV * D + 4 * KV
+    scale = np.float32(1.0) / np.sqrt(np.float32(D))
+    for s in sorted(set(seqs)):
+        kb = np.zeros((n_ctx, row), np.uint8)
+        vb = np.zeros((n_ctx, row), np.uint8)
+        kb[:, :KV * D] = k8[s].transpose(1, 0, 2).reshape(n_ctx, KV * D).view(np.uint8)
+        vb[:, :KV * D] = v8[s].transpose(1, 0, 2).reshape(n_ctx, KV * D).view(np.uint8)
+        kb[:, KV * D:] = ks[s].T.copy().view(np.uint8).reshape(n_ctx, 4 * KV)
+        vb[:, KV * D:] = vs[s].T.copy().view(np.uint8).reshape(n_ctx, 4 * KV)
+        kf, vf = kb.reshape(-1), vb.reshape(-1)
+        for t in (t for t in range(n) if seqs[t] == s):
+            extra = np.array(ancs[t], np.int32) if ancs is not None and ancs[t] else None
+            for g in range(KV):
+                exp = oracle.attend_gqa(q[t, g * G * D:(g + 1) * G * D], G, D, kf[g * D:], vf[g * D:], row,
+                                        (KV - g) * D + 4 * g, nks[t], scale, extra=extra)
+                assert np.array_equal(bits(got[t, g * G * D:(g + 1) * G * D]), bits(exp)), (case, t, g)
+
+
+def test_attention_long_rows_need_scratch():
+    """Rows whose global slot does not fit the context's scratch (a fresh context holds 1 MiB: 131072 keys' slot)
+    fail with a status, nothing launched."""
+    c = mk_.Context(0)
+    try:
+        D, KV, n_ctx = 128, 1, 140000
+        buf = mk_.load()
+        dk = c.alloc(KV * n_ctx * D)
+        ds = c.alloc(KV * n_ctx * 4)
+        dq = c.alloc(D * 4)
+        dseq = c.to_device(np.zeros(1, np.int32))
+        dnk = c.to_device(np.array([n_ctx], np.int32))
+        out = c.alloc(D * 4)
+        kv = mk_.MkKvCache(dk.ptr, dk.ptr, ds.ptr, ds.ptr, 1, 1, KV, D, n_ctx)
+        rc = buf.mk_attention(c.h, dq.ptr, D, out.ptr, D, 1, 1, ctypes.byref(kv), 0, dseq.ptr, dnk.ptr, None, None,
+                              n_ctx)
+        assert rc == mk_.MK_ERR_INVALID and b"scratch" in buf.mk_last_error()
+    finally:
+        c.close()

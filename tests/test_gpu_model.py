@@ -156,3 +156,30 @@ def test_fused_decode_only_for_distinct_sequences(mk, oracle, model_files):
     assert np.array_equal(bits(dm.forward_batch(b2)), bits(om.forward_batch(b2)))
     dm.close()
     om.close()
+
+
+def test_long_context_against_reference(mk, ref, model_files):
+    """A context past one workgroup's LDS (head_dim 128: about 7600 keys): a 16000-token prompt in 256-token forwards,
+    a 3-token tree over it and two decode steps, logits bit-identical to the compiled reference's Model."""
+    name = "tiny"
+    n_ctx = 16400
+    dm = mk_.Model(mk, model_files[name], n_ctx, 1)
+    rm = ref.model(model_files[name], n_ctx, 1)
+    try:
+        V = dm.cfg["n_vocab"]
+        rng = np.random.default_rng(40)
+        p = rng.integers(0, V, 16000).astype(np.int32)
+        print("long prompt", len(p), "head_dim", dm.cfg["head_dim"], flush=True)
+        for at in range(0, len(p), 256):
+            c = p[at:at + 256]
+            got, want = dm.forward(c, at), rm.forward(c, at)
+            assert np.array_equal(bits(got), bits(want)), at
+        par = np.array([-1, 0, 0], np.int32)
+        tl = rng.integers(0, V, 3).astype(np.int32)
+        assert np.array_equal(bits(dm.forward(tl, 16000, True, par)), bits(rm.forward(tl, 16000, True, par)))
+        for step, t in enumerate(rng.integers(0, V, 2)):
+            x = np.array([t], np.int32)
+            assert np.array_equal(bits(dm.forward(x, 16000 + step)), bits(rm.forward(x, 16000 + step))), step
+    finally:
+        dm.close()
+        rm.close()
