@@ -502,10 +502,15 @@ __host__ __device__ constexpr int dec_vstride(int nk_pad) { return ((nk_pad + 12
 __host__ __device__ constexpr size_t dec_lds_bytes(int D, int nk_pad) {
   return (size_t)D * (size_t)dec_vstride(nk_pad) + 4 * (2 * (size_t)nk_pad + (size_t)D);
 }
-__host__ __device__ constexpr int dec_slots(int D, int nk) { return (((nk + 3) / 4) * (D / 16) + kDecThreads - 1) / kDecThreads; }
+// V staging threads: with the fused QK-norm / RoPE / KV-write step its three waves stage nothing (the others
+// transpose V while they run).
+__host__ __device__ constexpr int dec_stagers(bool fuse) { return fuse ? kDecThreads - 3 * 64 : kDecThreads; }
+__host__ __device__ constexpr int dec_slots(int D, int nk, bool fuse) {
+  return (((nk + 3) / 4) * (D / 16) + dec_stagers(fuse) - 1) / dec_stagers(fuse);
+}
 __host__ __device__ constexpr bool dec_fits(int D, int nk) {
   return dec_lds_bytes(D, attn_keys_pad(nk)) <= 160 * 1024 - 1024 &&
-         ((nk + 3) / 4) * (D / 16) <= kDecMaxTasks * kDecThreads;
+         ((nk + 3) / 4) * (D / 16) <= kDecMaxTasks * dec_stagers(true);
 }
 
 // The fused QK-norm / RoPE / KV-write step of k_attention_dec (model.cpp:370-392, the arithmetic of
@@ -680,27 +685,35 @@ __global__ __launch_bounds__(kDecThreads) void k_attention_dec(const float* __re
     R.sv = *reinterpret_cast<const float*>((gl < KB ? ksb : vsb) + (int64_t)js * a.s_row);
   };
   const int rounds = (nk + NGR * KB - 1) / (NGR * KB);
+  // The first two rounds' K rows are issued here, before anything waits: a load issued later would be waited for
+  // together with everything issued before it (the wait counts are in order).
   Round RA, RB;
   fetch(RA, 0);
+  fetch(RB, min(1, rounds - 1));
 
   // V staging: task k = (quad kq = k / (D/16) of 4 keys, segment sg = k % (D/16) of 16 values), NSLOT tasks per
-  // thread. Past the last task the loads re-read it (the same rows: no extra lines), unused.
-  constexpr int SEG = D / 16;
+  // staging thread (st = tid less the fuse roles' waves). Past the last task the loads re-read it (the same rows:
+  // no extra lines), unused.
+  constexpr int SEG = D / 16, NST = dec_stagers(FUSE);
   const int ntask = ((nk + 3) / 4) * SEG;
+  const int st = tid - (kDecThreads - NST);
   v4i vr[NSLOT][4];
+  if (st >= 0) {
 #pragma unroll
-  for (int i = 0; i < NSLOT; ++i) {
-    const int tk = min(tid + kDecThreads * i, ntask - 1);
-    const int sg = tk % SEG, kq = tk / SEG;
+    for (int i = 0; i < NSLOT; ++i) {
+      const int tk = min(st + NST * i, ntask - 1);
+      const int sg = tk % SEG, kq = tk / SEG;
 #pragma unroll
-    for (int x = 0; x < 4; ++x)
-      vr[i][x] = *reinterpret_cast<const v4i*>(vb + (int64_t)min(4 * kq + x, nk - 1) * a.k_row + 16 * sg);
+      for (int x = 0; x < 4; ++x)
+        vr[i][x] = *reinterpret_cast<const v4i*>(vb + (int64_t)min(4 * kq + x, nk - 1) * a.k_row + 16 * sg);
+    }
   }
 
+  __shared__ float kscr[FUSE ? D : 1];  // the key role's rmsnorm scratch
   if constexpr (FUSE) {
-    // One wave per role; the key role's scratch is the V rows' LDS, written only after the scores.
+    // One wave per role; the staging waves transpose V meanwhile (below).
     const int wv = tid >> 6;
-    float* ksc = reinterpret_cast<float*>(vt);
+    float* ksc = kscr;
     if (wv == 0)
       fuse_qkv<D, 0>(f, t, h, g, tid & 63, H, (int64_t)seqs[t], jo, h % G == 0, qs, ksc, own_k, own_v, own_sc);
     else if (wv == 1)
@@ -710,7 +723,36 @@ __global__ __launch_bounds__(kDecThreads) void k_attention_dec(const float* __re
   } else {
     if (tid < D) qs[tid] = qv;
   }
+
+  // V: 4 x 4 byte transposes into the [value][key] rows; rows of segment sg hold their 16-key blocks XOR sg % 8.
+  // The token's own key (FUSE) is written over after the barrier, once its row exists.
+  if (st >= 0) {
+#pragma unroll
+    for (int i = 0; i < NSLOT; ++i) {
+      const int tk = st + NST * i;
+      const int sg = tk % SEG, kq = tk / SEG;
+      if (tk < ntask) {
+        const int col = 16 * ((kq >> 2) ^ (sg & 7)) + 4 * (kq & 3);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t A = (uint32_t)vr[i][0][u], B = (uint32_t)vr[i][1][u];
+          const uint32_t C = (uint32_t)vr[i][2][u], E = (uint32_t)vr[i][3][u];
+          const uint32_t t0 = __builtin_amdgcn_perm(B, A, 0x05010400u), t1 = __builtin_amdgcn_perm(B, A, 0x07030602u);
+          const uint32_t t2 = __builtin_amdgcn_perm(E, C, 0x05010400u), t3 = __builtin_amdgcn_perm(E, C, 0x07030602u);
+          uint8_t* row = vt + (16 * sg + 4 * u) * vstride + col;
+          *reinterpret_cast<uint32_t*>(row) = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+          *reinterpret_cast<uint32_t*>(row + vstride) = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+          *reinterpret_cast<uint32_t*>(row + 2 * vstride) = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+          *reinterpret_cast<uint32_t*>(row + 3 * vstride) = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+        }
+      }
+    }
+  }
   lds_barrier();
+  if (FUSE && tid < D) {  // value tid of the token's own key jo
+    const int kq = jo >> 2;
+    vt[tid * vstride + 16 * ((kq >> 2) ^ ((tid >> 4) & 7)) + 4 * (kq & 3) + (jo & 3)] = (uint8_t)own_v[tid];
+  }
   float qr[CPL][DC];  // qr[k][c] = q[16 c + CPL gl + k]
 #pragma unroll
   for (int k = 0; k < CPL; ++k)
@@ -756,40 +798,11 @@ __global__ __launch_bounds__(kDecThreads) void k_attention_dec(const float* __re
       }
     }
   };
-  for (int r = 0; r < rounds; r += 2) {
-    fetch(RB, min(r + 1, rounds - 1));
+  score(RA, 0);
+  if (rounds > 1) score(RB, 1);
+  for (int r = 2; r < rounds; ++r) {  // more than 1024 keys (D = 128)
+    fetch(RA, r);
     score(RA, r);
-    if (r + 1 >= rounds) break;
-    fetch(RA, min(r + 2, rounds - 1));
-    score(RB, r + 1);
-  }
-
-  // V: 4 x 4 byte transposes into the [value][key] rows; rows of segment sg hold their 16-key blocks XOR sg % 8.
-#pragma unroll
-  for (int i = 0; i < NSLOT; ++i) {
-    const int tk = tid + kDecThreads * i;
-    const int sg = tk % SEG, kq = tk / SEG;
-    if (tk < ntask) {
-      if (FUSE && (jo >> 2) == kq) {
-        const v4i ov = *reinterpret_cast<const v4i*>(own_v + 16 * sg);
-#pragma unroll
-        for (int x = 0; x < 4; ++x)
-          if ((jo & 3) == x) vr[i][x] = ov;
-      }
-      const int col = 16 * ((kq >> 2) ^ (sg & 7)) + 4 * (kq & 3);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint32_t A = (uint32_t)vr[i][0][u], B = (uint32_t)vr[i][1][u];
-        const uint32_t C = (uint32_t)vr[i][2][u], E = (uint32_t)vr[i][3][u];
-        const uint32_t t0 = __builtin_amdgcn_perm(B, A, 0x05010400u), t1 = __builtin_amdgcn_perm(B, A, 0x07030602u);
-        const uint32_t t2 = __builtin_amdgcn_perm(E, C, 0x05010400u), t3 = __builtin_amdgcn_perm(E, C, 0x07030602u);
-        uint8_t* row = vt + (16 * sg + 4 * u) * vstride + col;
-        *reinterpret_cast<uint32_t*>(row) = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
-        *reinterpret_cast<uint32_t*>(row + vstride) = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
-        *reinterpret_cast<uint32_t*>(row + 2 * vstride) = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
-        *reinterpret_cast<uint32_t*>(row + 3 * vstride) = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
-      }
-    }
   }
   lds_barrier();
 
@@ -827,23 +840,8 @@ __global__ __launch_bounds__(kDecThreads) void k_attention_dec(const float* __re
     // One 16-key group: the chain over the group's converted values fc (coefficients p), with the converts of the
     // next group's raw bytes w into fn issued in the fmas' latency, one per step.
     auto group = [&](const float (&fc)[16], float p, const v4i& w, float (&fn)[16]) {
-      const uint32_t w0 = (uint32_t)w[0], w1 = (uint32_t)w[1], w2 = (uint32_t)w[2], w3 = (uint32_t)w[3];
-      acc = fma_bcast16_cvt<0, 0>(p, fc[0], acc, w0, fn[0]);
-      acc = fma_bcast16_cvt<1, 1>(p, fc[1], acc, w0, fn[1]);
-      acc = fma_bcast16_cvt<2, 2>(p, fc[2], acc, w0, fn[2]);
-      acc = fma_bcast16_cvt<3, 3>(p, fc[3], acc, w0, fn[3]);
-      acc = fma_bcast16_cvt<4, 0>(p, fc[4], acc, w1, fn[4]);
-      acc = fma_bcast16_cvt<5, 1>(p, fc[5], acc, w1, fn[5]);
-      acc = fma_bcast16_cvt<6, 2>(p, fc[6], acc, w1, fn[6]);
-      acc = fma_bcast16_cvt<7, 3>(p, fc[7], acc, w1, fn[7]);
-      acc = fma_bcast16_cvt<8, 0>(p, fc[8], acc, w2, fn[8]);
-      acc = fma_bcast16_cvt<9, 1>(p, fc[9], acc, w2, fn[9]);
-      acc = fma_bcast16_cvt<10, 2>(p, fc[10], acc, w2, fn[10]);
-      acc = fma_bcast16_cvt<11, 3>(p, fc[11], acc, w2, fn[11]);
-      acc = fma_bcast16_cvt<12, 0>(p, fc[12], acc, w3, fn[12]);
-      acc = fma_bcast16_cvt<13, 1>(p, fc[13], acc, w3, fn[13]);
-      acc = fma_bcast16_cvt<14, 2>(p, fc[14], acc, w3, fn[14]);
-      acc = fma_bcast16_cvt<15, 3>(p, fc[15], acc, w3, fn[15]);
+      acc = fma8_bcast16_cvt<0>(p, fc, acc, (uint32_t)w[0], (uint32_t)w[1], fn);
+      acc = fma8_bcast16_cvt<8>(p, fc, acc, (uint32_t)w[2], (uint32_t)w[3], fn);
     };
     // Group g's values are converted during group g - 1's chain; its raw bytes are read during group g - 2's.
     v4i ra, rb;
@@ -1334,7 +1332,7 @@ void launch_dec(hipStream_t s, const float* q, int64_t q_stride, float* out, int
     hipLaunchKernelGGL(kernel, dim3(n * H), dim3(kDecThreads), lds, s, q, q_stride, out, out_stride, G, scale, a, seq,
                        n_keys, n, H, f);
   };
-  const int slots = dec_slots(D, max_keys);
+  const int slots = dec_slots(D, max_keys, FUSE);
   if (D == 64) {
     slots == 1   ? go(k_attention_dec<64, 1, FUSE>)
     : slots == 2 ? go(k_attention_dec<64, 2, FUSE>)

@@ -178,6 +178,60 @@ __device__ __forceinline__ float fma_bcast16_cvt(float x, float v, float acc, ui
   return acc;
 }
 
+// Eight consecutive fma_bcast16_cvt steps (keys K0 .. K0 + 7 of a 16-key group: converts of the bytes of w0, then
+// w1) in one asm statement, so that no wait states are placed between the steps: inside the statement only the DPP
+// source x is read through DPP, and nothing in it writes x. K0 = 0 starts with the two wait states a DPP read of x
+// needs after x is written.
+template <int K0>
+__device__ __forceinline__ float fma8_bcast16_cvt(float x, const float (&v)[16], float acc, uint32_t w0, uint32_t w1,
+                                                  float (&cvt)[16]) {
+  static_assert(K0 == 0 || K0 == 8, "two halves of a 16-key group");
+  if constexpr (K0 == 0)
+    asm("s_nop 1\n\t"
+        "v_fmac_f32_dpp %0, %17, %9 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+        "v_cvt_f32_i32_sdwa %1, sext(%18) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_fmac_f32_dpp %0, %17, %10 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+        "v_cvt_f32_i32_sdwa %2, sext(%18) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+        "v_fmac_f32_dpp %0, %17, %11 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+        "v_cvt_f32_i32_sdwa %3, sext(%18) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+        "v_fmac_f32_dpp %0, %17, %12 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+        "v_cvt_f32_i32_sdwa %4, sext(%18) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3\n\t"
+        "v_fmac_f32_dpp %0, %17, %13 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_cvt_f32_i32_sdwa %5, sext(%19) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_fmac_f32_dpp %0, %17, %14 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+        "v_cvt_f32_i32_sdwa %6, sext(%19) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+        "v_fmac_f32_dpp %0, %17, %15 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_cvt_f32_i32_sdwa %7, sext(%19) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+        "v_fmac_f32_dpp %0, %17, %16 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_cvt_f32_i32_sdwa %8, sext(%19) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3\n\t"
+        : "+v"(acc), "=&v"(cvt[0]), "=&v"(cvt[1]), "=&v"(cvt[2]), "=&v"(cvt[3]), "=&v"(cvt[4]), "=&v"(cvt[5]),
+          "=&v"(cvt[6]), "=&v"(cvt[7])
+        : "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]), "v"(x), "v"(w0),
+          "v"(w1));
+  else
+    asm("v_fmac_f32_dpp %0, %17, %9 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_cvt_f32_i32_sdwa %1, sext(%18) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_fmac_f32_dpp %0, %17, %10 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_cvt_f32_i32_sdwa %2, sext(%18) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+        "v_fmac_f32_dpp %0, %17, %11 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_cvt_f32_i32_sdwa %3, sext(%18) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+        "v_fmac_f32_dpp %0, %17, %12 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+        "v_cvt_f32_i32_sdwa %4, sext(%18) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3\n\t"
+        "v_fmac_f32_dpp %0, %17, %13 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+        "v_cvt_f32_i32_sdwa %5, sext(%19) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_fmac_f32_dpp %0, %17, %14 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+        "v_cvt_f32_i32_sdwa %6, sext(%19) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+        "v_fmac_f32_dpp %0, %17, %15 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+        "v_cvt_f32_i32_sdwa %7, sext(%19) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+        "v_fmac_f32_dpp %0, %17, %16 row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"
+        "v_cvt_f32_i32_sdwa %8, sext(%19) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3\n\t"
+        : "+v"(acc), "=&v"(cvt[8]), "=&v"(cvt[9]), "=&v"(cvt[10]), "=&v"(cvt[11]), "=&v"(cvt[12]), "=&v"(cvt[13]),
+          "=&v"(cvt[14]), "=&v"(cvt[15])
+        : "v"(v[8]), "v"(v[9]), "v"(v[10]), "v"(v[11]), "v"(v[12]), "v"(v[13]), "v"(v[14]), "v"(v[15]), "v"(x),
+          "v"(w0), "v"(w1));
+  return acc;
+}
+
 // (float)(int8_t)(w >> 8 K): one SDWA convert of byte K (the compiler otherwise emits shift, extract and convert
 // where the source word is live across a scheduling barrier).
 template <int K>
