@@ -13,6 +13,8 @@ reference's own AVX-512 path timed on this host's cores on a bounded sample of t
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-kernel-configs]
     python bench.py --probe traffic     # launch sequence for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+    python bench.py --probe gemm        # the prefill GEMM shapes, for counter passes
+    python bench.py --probe kquant      # config 2's Q4_K shapes at n = 1, 4, 8, for counter passes
 """
 import argparse
 import json
@@ -269,6 +271,31 @@ def gemm_probe():
     ctx.close()
 
 
+def kquant_probe():
+    """Launch sequence for the short-batch K-quant counters (rocprofv3 --pmc / --kernel-trace): config 2's Q4_K shapes
+    (gate/up 17408x5120, down 5120x17408) at n = 1, 4, 8, each 8 launches over 4 packed copies, from BlockQ8
+    activations."""
+    import ctypes
+    import malkin_amd as mk
+    L = mk.load()
+    ctx = mk.Context(0)
+    rng = np.random.default_rng(0)
+    y = ctx.alloc(8 * 17408 * 4)
+    for rows, cols in ((17408, 5120), (5120, 17408)):
+        ws = pack_copies(ctx, mk.Q4_K, random_weight(rng, mk.Q4_K, rows, cols), rows, cols, 4)
+        for n in (1, 4, 8):
+            xq = random_acts(ctx, rng, n, cols)
+            for i in range(8):
+                mk.check(L.mk_matmul(ctx.h, ctypes.byref(ws[i % 4][1]), xq.ptr, n, y.ptr, rows, 0))
+            ctx.sync()
+            log(f"[probe] Q4_K {rows}x{cols} n={n}: 8 launches")
+            xq.free()
+        for b, _w in ws:
+            b.free()
+    y.free()
+    ctx.close()
+
+
 def roofline_traffic():
     """HBM bytes per launch of the roofline kernel, from the committed counter summary (profiles/), or None."""
     f = os.path.join(ROOT, "profiles", "k_gemv_q8_0_decode_n1_hbm_traffic.md")
@@ -475,15 +502,18 @@ def main():
     ap.add_argument("--no-engine-configs", action="store_true",
                     help="skip BASELINE configs 3 (Qwen3-4B pp512 + tg128), 4 (continuous batching) and 5 "
                          "(speculative tree verification)")
-    ap.add_argument("--probe", choices=["traffic", "gemm"],
-                    help="only run a launch sequence for counter profiles: the roofline kernel's HBM traffic, or "
-                         "the prefill GEMM (config 1 and the pp512 chunk shapes)")
+    ap.add_argument("--probe", choices=["traffic", "gemm", "kquant"],
+                    help="only run a launch sequence for counter profiles: the roofline kernel's HBM traffic, "
+                         "the prefill GEMM (config 1 and the pp512 chunk shapes), or config 2's short K-quant batches")
     args = ap.parse_args()
     if args.probe == "traffic":
         traffic_probe()
         return
     if args.probe == "gemm":
         gemm_probe()
+        return
+    if args.probe == "kquant":
+        kquant_probe()
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus})",

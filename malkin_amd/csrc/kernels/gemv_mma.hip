@@ -178,6 +178,8 @@ __global__ __launch_bounds__(kThreads) void k_mmv(const uint8_t* W, int64_t rows
   // This lane: row r = lane % 16 of the wave's 16 (group gi = r / 8, row rr = r % 8), weight quarter c = lane / 16;
   // accumulator elements i: tokens 4 c + i (+ 16 m for tile m).
   const int r = lane & 15, c = lane >> 4, gi = r >> 3, rr = r & 7;
+  __shared__ __align__(16) float xsum_tab[TYPE == kQ4_K ? kWaves * kUnits * 16 * NTT : 4];
+  float* xsum_w = xsum_tab + (TYPE == kQ4_K ? wu * kUnits * 16 * NTT : 0);
   float acc[NTT][4];
 #pragma unroll
   for (int m = 0; m < NTT; ++m)
@@ -244,6 +246,18 @@ __global__ __launch_bounds__(kThreads) void k_mmv(const uint8_t* W, int64_t rows
         }
       }
     } else {  // Q4_K: unit u = sub-block j = u of the stage's super-block; chunk j2 = u / 2, nibble u % 2
+      // dx (s0 + s1) of the stage's (unit, token) pairs (the reference's dsx, gemm_avx512.cpp:143), computed once per
+      // stage and wave into the wave's table instead of once per row lane, read back as each lane's four tokens.
+#pragma unroll
+      for (int k = 0; k < kUnits * 16 * NTT / 64; ++k) {
+        const int idx = lane + 64 * k;
+        const uint32_t sx = *reinterpret_cast<const uint32_t*>(st + S::xs + idx * 4);
+        const float dxv = *reinterpret_cast<const float*>(st + S::dx + idx * 4);
+        xsum_w[idx] = dxv * (float)((int)(int16_t)(sx & 0xFFFF) + (int)(int16_t)(sx >> 16));
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
       const uint4 hd = *reinterpret_cast<const uint4*>(wv + S::s_off + gi * 128 + rr * 16);
       const float d = half_to_float((uint16_t)(hd.x & 0xFFFF)), dmin = half_to_float((uint16_t)(hd.x >> 16));
 #pragma unroll
@@ -261,15 +275,14 @@ __global__ __launch_bounds__(kThreads) void k_mmv(const uint8_t* W, int64_t rows
           for (int m = 0; m < NTT; ++m) {
             const long a = *reinterpret_cast<const long*>(st + S::x + ((u * NTT + m) * 16 + r) * 32 + 8 * c);
             const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + ((u * NTT + m) * 16 + 4 * c) * 4);
-            const uint4 sx4 = *reinterpret_cast<const uint4*>(st + S::xs + ((u * NTT + m) * 16 + 4 * c) * 4);
+            const float4 xs4 = *reinterpret_cast<const float4*>(xsum_w + ((u * NTT + m) * 16 + 4 * c));
             const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
-            const uint32_t sx[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
+            const float xsum[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
             const v4i dq = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq, zero4, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const float xsum = dx[i] * (float)((int)(int16_t)(sx[i] & 0xFFFF) + (int)(int16_t)(sx[i] >> 16));
               acc[m][i] = fma_((float)dq[i], fsc * dx[i], acc[m][i]);
-              acc[m][i] = fma_(nmn, xsum, acc[m][i]);
+              acc[m][i] = fma_(nmn, xsum[i], acc[m][i]);
             }
           }
         }
@@ -304,11 +317,12 @@ __global__ __launch_bounds__(kThreads) void k_mmv(const uint8_t* W, int64_t rows
 // (the operands of the reference's fmas, rounded as the reference rounds them) into LDS; after a barrier every
 // lane runs the sequential chains of NTT (row, token) outputs over the stage's 8 units in order. Terms per unit and
 // output, E floats: Q8_0 {float(ai), dw dx}; Q6_K compact {float(ai_0), (d sc_0) dx, float(ai_1), (d sc_1) dx};
-// Q6_K wide {fma(float(ai_1), d sc_1, float(ai_0) (d sc_0)), dx}; Q4_K {float(ai), (d sc) dx, -(dmin m),
-// dx (s0 + s1)}; the chain applies acc = fma(e0, e1, acc) (and acc = fma(e2, e3, acc)).
+// Q6_K wide {fma(float(ai_1), d sc_1, float(ai_0) (d sc_0)), dx}; Q4_K {float(ai), (d sc) dx}; the chain applies
+// acc = fma(e0, e1, acc) (and acc = fma(e2, e3, acc)). Q4_K's second fma, acc = fma(-(dmin m), dx (s0 + s1), acc),
+// takes its operands from two small per-stage tables (per row and unit, per token and unit) instead.
 template <int TYPE, bool WIDE>
 struct Ks {
-  static constexpr int E = (TYPE == kQ8_0 || (TYPE == kQ6_K && WIDE)) ? 2 : 4;
+  static constexpr int E = (TYPE == kQ8_0 || TYPE == kQ4_K || (TYPE == kQ6_K && WIDE)) ? 2 : 4;
 };
 template <int TYPE, bool WIDE, int NTT>
 struct KsLds {
@@ -318,7 +332,10 @@ struct KsLds {
   static constexpr int dx = x + kUnits * 16 * NTT * 32;
   static constexpr int xs = dx + kUnits * 16 * NTT * 4;
   static constexpr int bytes = xs + (TYPE == kQ4_K ? kUnits * 16 * NTT * 4 : 0);  // one ring stage
-  static constexpr int terms = kUnits * 16 * NTT * 16 * Ks<TYPE, WIDE>::E * 4;    // the term buffer
+  static constexpr int terms1 = kUnits * 16 * NTT * 16 * Ks<TYPE, WIDE>::E * 4;   // one stage's terms
+  // Double-buffered where it leaves room for the ring: stage s's terms are written while stage s - 1's chains run.
+  static constexpr bool db = terms1 <= 32 * 1024;
+  static constexpr int terms = (db ? 2 : 1) * terms1;
   // loads per wave per stage: W, S, (D), X, DX, (XS); pieces past a wave's share repeat another wave's copy
   static constexpr int loads = 1 + 1 + (TYPE == kQ6_K ? 1 : 0) + NTT + 1 + (TYPE == kQ4_K ? 1 : 0);
 };
@@ -330,7 +347,7 @@ __global__ __launch_bounds__(256) void k_mmv_ks(const uint8_t* W, int64_t rows, 
   constexpr int E = Ks<TYPE, WIDE>::E;
   static_assert((NS - 1) * S::loads < 64, "the ring's loads must fit the vmcnt counter");
   extern __shared__ __align__(16) uint8_t smem[];
-  float* terms = reinterpret_cast<float*>(smem + NS * S::bytes);  // [unit][token][row][E]
+  float* terms_base = reinterpret_cast<float*>(smem + NS * S::bytes);  // [2][unit][token][row][E]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wu = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int rt = blockIdx.x;                        // 16-row tile
@@ -417,6 +434,20 @@ __global__ __launch_bounds__(256) void k_mmv_ks(const uint8_t* W, int64_t rows, 
 #pragma unroll
   for (int m = 0; m < NTT; ++m) acc[m] = 0.0f;
   const v4i zero4 = {0, 0, 0, 0};
+  // Q4_K per stage (double-buffered like the terms): -(dmin m) per (row, unit) and dx (s0 + s1) per (token, unit)
+  __shared__ __align__(16) float nmn_tab[TYPE == kQ4_K ? 2 * 16 * kUnits : 4];
+  __shared__ __align__(16) float xs_tab[TYPE == kQ4_K ? 2 * 16 * NTT * kUnits : 4];
+  float* terms = terms_base;
+  float* nmn_t = nmn_tab;
+  float* xs_t = xs_tab;
+  auto select = [&](int sn) __attribute__((always_inline)) {  // stage sn's buffers
+    const int b = S::db ? (sn & 1) : 0;
+    terms = terms_base + b * (S::terms1 / 4);
+    if constexpr (TYPE == kQ4_K) {
+      nmn_t = nmn_tab + b * 16 * kUnits;
+      xs_t = xs_tab + b * 16 * NTT * kUnits;
+    }
+  };
   auto put = [&](int u, int tok, const float (&e)[E]) __attribute__((always_inline)) {
     float* p = terms + (((u * 16 * NTT) + tok) * 16 + r) * E;
     if constexpr (E == 2)
@@ -425,12 +456,52 @@ __global__ __launch_bounds__(256) void k_mmv_ks(const uint8_t* W, int64_t rows, 
       *reinterpret_cast<float4*>(p) = make_float4(e[0], e[1], e[2], e[3]);
   };
 
+  // Every lane runs its chains over stage sn's units in order.
+  auto chain = [&](int sn) __attribute__((always_inline)) {
+    select(sn);
+    float nm[kUnits];
+    if constexpr (TYPE == kQ4_K) {
+#pragma unroll
+      for (int h = 0; h < kUnits / 4; ++h) {
+        const float4 v = *reinterpret_cast<const float4*>(nmn_t + cr * kUnits + 4 * h);
+        nm[4 * h] = v.x, nm[4 * h + 1] = v.y, nm[4 * h + 2] = v.z, nm[4 * h + 3] = v.w;
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < NTT; ++m) {
+      float xsv[kUnits];
+      if constexpr (TYPE == kQ4_K) {
+#pragma unroll
+        for (int h = 0; h < kUnits / 4; ++h) {
+          const float4 v = *reinterpret_cast<const float4*>(xs_t + (ct + 16 * m) * kUnits + 4 * h);
+          xsv[4 * h] = v.x, xsv[4 * h + 1] = v.y, xsv[4 * h + 2] = v.z, xsv[4 * h + 3] = v.w;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnits; ++u) {
+        const float* p = terms + (((u * 16 * NTT) + ct + 16 * m) * 16 + cr) * E;
+        if constexpr (E == 2) {
+          const float2 e = *reinterpret_cast<const float2*>(p);
+          acc[m] = fma_(e.x, e.y, acc[m]);
+          if constexpr (TYPE == kQ4_K) acc[m] = fma_(nm[u], xsv[u], acc[m]);
+        } else {
+          const float4 e = *reinterpret_cast<const float4*>(p);
+          acc[m] = fma_(e.x, e.y, acc[m]);
+          acc[m] = fma_(e.z, e.w, acc[m]);
+        }
+      }
+    }
+  };
+
   auto stage = [&]<int BUF>(int s) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(0xC07F);
     wait_vm_stages<S::loads, NS - 2>(min(NS - 2, nst - 1 - s));
-    ring_barrier();  // stage s landed everywhere; every chain of stage s - 1 is done with the term buffer
+    // stage s landed everywhere; double-buffered terms: stage s - 1's are written and the chains of stage s - 2
+    // (which read the buffer stage s writes) are done; single: the chains of stage s - 1 are done
+    ring_barrier();
     if (s + NS - 1 < nst) issue.template operator()<(BUF + NS - 1) % NS>(s + NS - 1);
     const uint8_t* st = smem + BUF * S::bytes;
+    select(s);
     if constexpr (TYPE == kQ8_0) {
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
@@ -480,6 +551,20 @@ __global__ __launch_bounds__(256) void k_mmv_ks(const uint8_t* W, int64_t rows, 
         }
       }
     } else {  // Q4_K: wave w takes chunk j2 = w: units 2 w (low nibbles) and 2 w + 1 (high nibbles)
+      {  // dx (s0 + s1) of the wave's two units' tokens, once per (unit, token)
+        constexpr int TOKS = 16 * NTT;
+#pragma unroll
+        for (int k = 0; k < (2 * TOKS + 63) / 64; ++k) {
+          const int idx = lane + 64 * k;
+          if (idx < 2 * TOKS) {
+            const int u = 2 * wu + idx / TOKS, tok = idx % TOKS;
+            const int at = (u * NTT + tok / 16) * 16 + tok % 16;
+            const uint32_t sx = *reinterpret_cast<const uint32_t*>(st + S::xs + at * 4);
+            const float dxv = *reinterpret_cast<const float*>(st + S::dx + at * 4);
+            xs_t[tok * kUnits + u] = dxv * (float)((int)(int16_t)(sx & 0xFFFF) + (int)(int16_t)(sx >> 16));
+          }
+        }
+      }
       const uint4 hd = *reinterpret_cast<const uint4*>(st + S::s_off + gi * 128 + rr * 16);
       const float d = half_to_float((uint16_t)(hd.x & 0xFFFF)), dmin = half_to_float((uint16_t)(hd.x >> 16));
       const uint2 raw =
@@ -490,41 +575,29 @@ __global__ __launch_bounds__(256) void k_mmv_ks(const uint8_t* W, int64_t rows, 
         const long bq = (long)(((uint64_t)((raw.y >> (4 * e)) & 0x0F0F0F0Fu) << 32) | ((raw.x >> (4 * e)) & 0x0F0F0F0Fu));
         int sc, mn;
         scale_min(u, hd.y, hd.z, hd.w, sc, mn);
-        const float fsc = d * (float)sc, nmn = -(dmin * (float)mn);
+        const float fsc = d * (float)sc;
+        if (c == 0) nmn_t[r * kUnits + u] = -(dmin * (float)mn);
 #pragma unroll
         for (int m = 0; m < NTT; ++m) {
           const long a = *reinterpret_cast<const long*>(st + S::x + ((u * NTT + m) * 16 + r) * 32 + 8 * c);
           const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + ((u * NTT + m) * 16 + 4 * c) * 4);
-          const uint4 sx4 = *reinterpret_cast<const uint4*>(st + S::xs + ((u * NTT + m) * 16 + 4 * c) * 4);
           const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
-          const uint32_t sx[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
           const v4i dq = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq, zero4, 0, 0, 0);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float xsum = dx[i] * (float)((int)(int16_t)(sx[i] & 0xFFFF) + (int)(int16_t)(sx[i] >> 16));
-            put(u, 16 * m + 4 * c + i, {(float)dq[i], fsc * dx[i], nmn, xsum});
-          }
+          for (int i = 0; i < 4; ++i) put(u, 16 * m + 4 * c + i, {(float)dq[i], fsc * dx[i]});
         }
       }
     }
-    // Terms written (LDS only): then every lane runs its chains over the stage's units in order.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-#pragma unroll
-    for (int m = 0; m < NTT; ++m) {
-#pragma unroll
-      for (int u = 0; u < kUnits; ++u) {
-        const float* p = terms + (((u * 16 * NTT) + ct + 16 * m) * 16 + cr) * E;
-        if constexpr (E == 2) {
-          const float2 e = *reinterpret_cast<const float2*>(p);
-          acc[m] = fma_(e.x, e.y, acc[m]);
-        } else {
-          const float4 e = *reinterpret_cast<const float4*>(p);
-          acc[m] = fma_(e.x, e.y, acc[m]);
-          acc[m] = fma_(e.z, e.w, acc[m]);
-        }
-      }
+    if constexpr (S::db) {
+      // The previous stage's terms were written before this stage's barrier: its chains run now, alongside this
+      // stage's term work (the last stage's chains run after the loop).
+      if (s > 0) chain(s - 1);
+    } else {
+      // Terms written (LDS only): then every lane runs its chains over the stage's units in order.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+      chain(s);
     }
   };
 
@@ -535,6 +608,12 @@ __global__ __launch_bounds__(256) void k_mmv_ks(const uint8_t* W, int64_t rows, 
     [&]<int... B>(std::integer_sequence<int, B...>) __attribute__((always_inline)) {
       ((s + B < nst ? stage.template operator()<B>(s + B) : void()), ...);
     }(std::make_integer_sequence<int, NS>{});
+  }
+  if constexpr (S::db) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();  // the last stage's terms are written
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    chain(nst - 1);
   }
 
   const int64_t row = (int64_t)rt * 16 + cr;
@@ -574,6 +653,7 @@ void launch_ks_ntt(hipStream_t s, const void* w, int64_t rows, int64_t cols, con
   const int64_t wgs = rows / 16 * ((n + 16 * NTT - 1) / (16 * NTT)), cus = device_cus();
   constexpr int kDeep = (150 * 1024 - S::terms) / S::bytes >= 8 ? 8 : (150 * 1024 - S::terms) / S::bytes;
   constexpr int kTwo = (80 * 1024 - S::terms) / S::bytes;
+  static_assert(kDeep >= 3, "the K-split ring needs three stages");
   if constexpr (kTwo >= 3) {
     if (wgs > cus) {
       launch_ks_ns<TYPE, WIDE, NTT, (kTwo > 6 ? 6 : kTwo)>(s, w, rows, cols, x, n, y, ys, accumulate);
