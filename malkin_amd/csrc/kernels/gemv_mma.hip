@@ -333,8 +333,9 @@ struct KsLds {
   static constexpr int xs = dx + kUnits * 16 * NTT * 4;
   static constexpr int bytes = xs + (TYPE == kQ4_K ? kUnits * 16 * NTT * 4 : 0);  // one ring stage
   static constexpr int terms1 = kUnits * 16 * NTT * 16 * Ks<TYPE, WIDE>::E * 4;   // one stage's terms
-  // Double-buffered where it leaves room for the ring: stage s's terms are written while stage s - 1's chains run.
-  static constexpr bool db = terms1 <= 32 * 1024;
+  // Double-buffered (stage s's terms written while stage s - 1's chains run) where two workgroups per CU still get
+  // a three-stage ring in 80 KB each.
+  static constexpr bool db = (80 * 1024 - 2 * terms1) / bytes >= 3;
   static constexpr int terms = (db ? 2 : 1) * terms1;
   // loads per wave per stage: W, S, (D), X, DX, (XS); pieces past a wave's share repeat another wave's copy
   static constexpr int loads = 1 + 1 + (TYPE == kQ6_K ? 1 : 0) + NTT + 1 + (TYPE == kQ4_K ? 1 : 0);
