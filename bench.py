@@ -350,7 +350,7 @@ def cpu_baseline(path, prompt, gpu_tokens, budget_s=30.0):
             "tokens_compared": len(ids), "tokens_match": match}
 
 
-def config3(ctx, reps=3, with_cpu=True):
+def config3(ctx, reps=3, with_cpu=True, use_graph=True):
     """random-init Qwen3-4B architecture in Q8_0 (36 layers, hidden 2560, 32/8 heads, head_dim 128,
     FFN 9728 SwiGLU, vocab 151936, tied embeddings; synthetic seed 31), a prompt of 512 uniform-random ids (numpy
     seed 303), 128 greedy tokens, ctx 4096: pp512 + tg128 on the device with the same protocol as the main line, its
@@ -361,12 +361,12 @@ def config3(ctx, reps=3, with_cpu=True):
         m = mk.Model(ctx, path, N_CTX, 1)
         cfg = m.cfg
         prompt = np.random.default_rng(303).integers(0, cfg["n_vocab"], N_PROMPT).astype(np.int32)
-        m.generate(prompt, N_GEN)
+        m.generate(prompt, N_GEN, use_graph=use_graph)
         ctx.sync()
         pre, dec = [], []
         t0 = time.perf_counter()
         for _ in range(reps):
-            toks, st = m.generate(prompt, N_GEN)
+            toks, st = m.generate(prompt, N_GEN, use_graph=use_graph)
             pre.append(st["prefill_ms"])
             dec.append(st["decode_ms"])
         ctx.sync()
@@ -425,6 +425,43 @@ def config4(ctx, path):
             "mean_decode_ms": round(float(np.mean([i["decode_ms"] for i in infos])), 1)}
 
 
+def tree_nodes(ids, P):
+    """The engine's 17-node tree over a P-token prefix: next token, then per depth k a chain draft and its runner-up
+    (both children of the previous chain node)."""
+    nodes = [(int(ids[0]), 0, P, 1)]
+    for k in range(8):
+        par = 0 if k == 0 else 2 * k - 1
+        nodes.append((int(ids[1 + 2 * k]), 0, P + 1 + k, 1, P + 1 + 2 * k, par))
+        nodes.append((int(ids[2 + 2 * k]), 0, P + 1 + k, 1, P + 2 + 2 * k, par))
+    return nodes
+
+
+def tree_probe():
+    """Launch sequence for the tree-verification kernel trace: config 5's target (Qwen3-14B shape, Q6_K), the
+    2048-token prefix in 256-token forwards, then 4 verifications of the 17-node tree."""
+    import malkin_amd as mk
+    from malkin_amd import synth
+    rng = np.random.default_rng(5)
+    tpath, _ = model_file("qwen3-14b", seed=5, wtype=synth.Q6_K)
+    try:
+        ctx = mk.Context(0)
+        t = mk.Model(ctx, tpath, N_CTX, 1)
+        P = 2048
+        prompt = rng.integers(0, t.cfg["n_vocab"], size=P).astype(np.int32)
+        for i in range(0, P, 256):
+            t.forward(prompt[i:i + 256], i)
+        tree = mk.batch(tree_nodes(rng.integers(0, t.cfg["n_vocab"], size=17), P))
+        for i in range(4):
+            t.forward_top2(tree)
+            ctx.sync()
+            log(f"[probe] verification {i}")
+        t.close()
+        ctx.close()
+    finally:
+        if os.path.exists(tpath):
+            os.remove(tpath)
+
+
 def config5(ctx):
     """target Qwen3-14B in Q6_K, draft Qwen3-0.6B in Q4_K_M, 2048-token prefix. (a) One tree
     verification: the target forward of 17 nodes (next token + a chain of 8 drafts + one runner-up per depth, the
@@ -447,13 +484,7 @@ def config5(ctx):
             t.forward(prompt[i:i + 256], i)
         ctx.sync()
         prefill_s = time.perf_counter() - t0
-        ids = rng.integers(0, V, size=17)
-        nodes = [(int(ids[0]), 0, P, 1)]
-        for k in range(8):
-            par = 0 if k == 0 else 2 * k - 1
-            nodes.append((int(ids[1 + 2 * k]), 0, P + 1 + k, 1, P + 1 + 2 * k, par))
-            nodes.append((int(ids[2 + 2 * k]), 0, P + 1 + k, 1, P + 2 + 2 * k, par))
-        tree = mk.batch(nodes)
+        tree = mk.batch(tree_nodes(rng.integers(0, V, size=17), P))
         t.forward_top2(tree)
         ctx.sync()
         reps = 10
@@ -502,9 +533,10 @@ def main():
     ap.add_argument("--no-engine-configs", action="store_true",
                     help="skip BASELINE configs 3 (Qwen3-4B pp512 + tg128), 4 (continuous batching) and 5 "
                          "(speculative tree verification)")
-    ap.add_argument("--probe", choices=["traffic", "gemm", "kquant"],
+    ap.add_argument("--probe", choices=["traffic", "gemm", "kquant", "tree"],
                     help="only run a launch sequence for counter profiles: the roofline kernel's HBM traffic, "
-                         "the prefill GEMM (config 1 and the pp512 chunk shapes), or config 2's short K-quant batches")
+                         "the prefill GEMM (config 1 and the pp512 chunk shapes), config 2's short K-quant batches, "
+                         "or config 5's tree verification")
     args = ap.parse_args()
     if args.probe == "traffic":
         traffic_probe()
@@ -514,6 +546,9 @@ def main():
         return
     if args.probe == "kquant":
         kquant_probe()
+        return
+    if args.probe == "tree":
+        tree_probe()
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -553,7 +588,7 @@ def main():
             log("[bench] kernel configs: " + json.dumps(kern))
         engine = None
         if not args.no_engine_configs:
-            engine = {"config3": config3(ctx, with_cpu=not args.no_cpu_baseline)}
+            engine = {"config3": config3(ctx, with_cpu=not args.no_cpu_baseline, use_graph=not args.no_graph)}
             log("[bench] config 3: " + json.dumps(engine["config3"]))
             engine["config4"] = config4(ctx, path)
             log("[bench] config 4: " + json.dumps(engine["config4"]))
