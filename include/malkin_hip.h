@@ -200,7 +200,8 @@ int mk_attention_decode(mk_ctx* ctx, const float* qkv, int64_t stride, int n, in
                         int layer, float* out, int64_t out_stride, int max_keys);
 /* Model::attention (model.cpp:204-247) over the device cache: token t attends with its n_head query heads to rows
    0..n_keys[t]-1 of sequence seq[t], then (tree verification) rows anc[anc_off[t] .. anc_off[t+1]) when anc_off is
-   not NULL. max_keys bounds n_keys[t] + ancestors for every t. Rows longer than one workgroup's LDS holds use the
+   not NULL: the KV rows of its ancestors in the batch (model.h:83), so at most n of them. max_keys bounds
+   n_keys[t] + ancestors for every t. Rows longer than one workgroup's LDS holds use the
    context's scratch (mk_reserve_scratch, mk_attention_scratch_bytes); with none reserved they fail. */
 int mk_attention(mk_ctx* ctx, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int n_head,
                  const mk_kv_cache* kv, int layer, const int32_t* seq, const int32_t* n_keys, const int32_t* anc_off,

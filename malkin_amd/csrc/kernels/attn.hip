@@ -5,6 +5,7 @@
 //   move_kv_rows     model.cpp:432-440
 //   argmax_top2      sampler.cpp:27-30 (first maximum), engine.cpp:309-318 (runner-up scan)
 #include <mutex>
+#include <utility>
 
 #include "ctx.h"
 #include "ops.h"
@@ -414,18 +415,19 @@ __device__ __forceinline__ void attend_pair(int t, int h, const float* __restric
       }
     } else if (tid >= kSumThread) {
       const int l = tid - kSumThread;
-      if constexpr (LONG) {  // this chunk's part of lane l's sequential sum (chunks are whole 16-key groups)
-        const int j0 = c * T::chunk;
-        for (int j = l; j < T::chunk && j0 + j < nk; j += 16) lane_sum = lane_sum + ech[(c & 1) * T::chunk + j];
-        if (c + 1 == chunks) {
-          const float s = reduce16_lanes(lane_sum);
-          if (l == 0) inv_s = 1.0f / s;
-        }
-      } else if (c == 0) {
-        float s = 0.0f;
-#pragma unroll 8
-        for (int j = l; j < nk; j += 16) s = s + sc[j];
-        s = reduce16_lanes(s);
+      // This chunk's part of lane l's sequential sum (chunks are whole 16-key groups): the reads are issued first;
+      // keys past the end add +0, which leaves a sum of e >= 0 unchanged.
+      const int j0 = c * T::chunk;
+      float e[T::chunk / 16];
+#pragma unroll
+      for (int i = 0; i < T::chunk / 16; ++i) {
+        const int j = j0 + l + 16 * i;
+        e[i] = j < nk ? (LONG ? ech[(c & 1) * T::chunk + l + 16 * i] : sc[j]) : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < T::chunk / 16; ++i) lane_sum = lane_sum + e[i];
+      if (c + 1 == chunks) {
+        const float s = reduce16_lanes(lane_sum);
         if (l == 0) inv_s = 1.0f / s;
       }
     } else if (c + 1 < chunks) {
@@ -476,6 +478,313 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_long(const float* __
     __syncthreads();  // the previous pair's LDS and slot are no longer read
     attend_pair<D, PERM, true>(pair / H, pair % H, q, q_stride, out, out_stride, G, scale, a, seqs, n_keys, anc_off,
                                anc, slot, gcap);
+  }
+}
+
+// All G query heads of one KV group for one token per workgroup (G = 2..5, D = 128, permuted K rows, the keys in
+// LDS): verification trees and contexts past the decode kernel's LDS, where one workgroup per (token, head) would
+// read, convert and stage every K and V row G times. Same arithmetic as attend_pair, head by head:
+//   scores  16 lanes per key as in attend_pair; each lane holds the D/16 q values of its chain for every head and
+//           runs G dot products on the K bytes it loaded once;
+//   softmax per head, one pass over the keys for all heads (G maxima, one barrier);
+//   P.V     V tiles staged once for the G heads. A chain lane owns one value d and the chains of up to three heads
+//           (GH > 3: two head sets on four waves), so one LDS read of V feeds several independent chains;
+//   sums    the 16 sequential lane sums per head advance chunk by chunk on the last 16 threads.
+constexpr int kGrpMaxHeads = 5;
+
+template <int GH>
+struct GrpCfg {
+  static constexpr int D = 128, DC = 8;
+  static constexpr int sets = GH <= 3 ? 1 : 2;           // head sets of the chain lanes
+  static constexpr int h0 = (GH + sets - 1) / sets;      // heads of set 0 (set 1: GH - h0)
+  static constexpr int chain = sets * D;                 // chain threads
+  using T = AttnTile<D>;
+  static constexpr int groups = (kSumThread - chain) / T::tasks;  // V staging groups
+  static_assert(groups >= 2, "too few staging threads");
+};
+
+// LDS: two V tiles, q of the GH heads, per head scores then e values and P.V coefficients, the token's ancestors.
+__host__ __device__ constexpr size_t grp_lds_bytes(int GH, int nk_pad, int anc_cap) {
+  return 2 * (size_t)AttnTile<128>::tile + 4 * ((size_t)GH * 128 + 2 * (size_t)GH * nk_pad + (size_t)anc_cap);
+}
+
+template <int GH>
+__global__ __launch_bounds__(kAttnThreads) void k_attention_grp(const float* __restrict__ q, int64_t q_stride,
+                                                                float* __restrict__ out, int64_t out_stride,
+                                                                float scale, AttnAddr a,
+                                                                const int32_t* __restrict__ seqs,
+                                                                const int32_t* __restrict__ n_keys,
+                                                                const int32_t* __restrict__ anc_off,
+                                                                const int32_t* __restrict__ anc, int n, int KV,
+                                                                int nk_pad, int anc_cap) {
+  using C = GrpCfg<GH>;
+  using T = typename C::T;
+  constexpr int D = C::D, DC = C::DC;
+  const int tid = threadIdx.x;
+  // (token, group) pairs numbered group-major; XCD x (workgroups x, x + 8, ...) takes a contiguous run, so a group's
+  // K/V rows are read into one XCD's L2.
+  int t, g;
+  {
+    const int total = n * KV, w = (int)blockIdx.x;
+    const int pair = total % 8 == 0 ? (w % 8) * (total / 8) + w / 8 : w;
+    g = pair / n;
+    t = pair % n;
+  }
+  const int n0 = n_keys[t];
+  const int e0 = anc_off ? anc_off[t] : 0, ne = anc_off ? anc_off[t + 1] - e0 : 0;
+  const int nk = n0 + ne;
+  extern __shared__ int4 smem4[];
+  float* tiles = reinterpret_cast<float*>(smem4);                 // 2 x [D][stride] fp32
+  float* qs = tiles + 2 * T::tile / 4;                           // [GH][D]
+  float* sc = qs + GH * D;                                       // [GH][nk_pad]: scores, then e^(s - max)
+  float* pv = sc + GH * nk_pad;                                  // [GH][nk_pad]: v-scale, then e * v-scale
+  int* anc_s = reinterpret_cast<int*>(pv + GH * nk_pad);         // anc_cap: KV rows of keys n0 .. nk - 1
+  __shared__ float red[GH][kAttnThreads / 64];
+  __shared__ float inv_s[GH];
+  const int64_t sq = seqs[t];
+  const int8_t* kb = a.k + sq * a.k_seq + g * a.k_head;
+  const int8_t* vb = a.v + sq * a.k_seq + g * a.k_head;
+  const char* ksb = a.ks + sq * a.s_seq + g * a.s_head;
+  const char* vsb = a.vs + sq * a.s_seq + g * a.s_head;
+  // Ancestors to LDS (see attend_pair). They are rows of tokens of this batch, so at most anc_cap = n of them; the
+  // index is clamped so that a longer list cannot read past the reservation.
+  if (ne > 0) {
+    for (int i = tid; i < min(ne, anc_cap); i += kAttnThreads) anc_s[i] = anc[e0 + i];
+    lds_barrier();
+  }
+  auto key_row = [&](int j) -> int64_t { return j < n0 ? j : anc_s[min(j - n0, anc_cap - 1)]; };
+
+  // V staging (as attend_pair): task = 4 consecutive keys x 16 consecutive values.
+  constexpr int NG = C::groups;
+  const bool stager = tid >= C::chain && tid < C::chain + NG * T::tasks;
+  const int sgrp = (tid - C::chain) / T::tasks, task = (tid - C::chain) % T::tasks;
+  auto mine = [&](int c) { return stager && sgrp == c % NG; };
+  uint4 vreg[4];
+  auto load_chunk = [&](int c) {
+    if (!mine(c)) return;
+    const int kq = task % (T::chunk / 4), db = task / (T::chunk / 4);
+    // Loads are never predicated (past the last key they re-read it; store_chunk writes zeros there), so the
+    // compiler's wait counts stay exact and the NG chunks of loads in flight are not waited for early.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = min(c * T::chunk + 4 * kq + i, nk - 1);
+      vreg[i] = *reinterpret_cast<const uint4*>(vb + key_row(j) * a.k_row + 16 * db);
+    }
+  };
+  auto store_chunk = [&](int c) {
+    if (!mine(c)) return;
+    const int kq = task % (T::chunk / 4), db = task / (T::chunk / 4);
+    float* tile = tiles + (c & 1) * (T::tile / 4);
+    const int jq = c * T::chunk + 4 * kq;  // keys jq .. jq + 3; past nk the values are zero
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      float f[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        f[i] = jq + i < nk ? (float)(int8_t)((&vreg[i].x)[v >> 2] >> (8 * (v & 3))) : 0.0f;
+      *reinterpret_cast<float4*>(tile + (16 * db + v) * T::stride + 4 * kq) = make_float4(f[0], f[1], f[2], f[3]);
+    }
+  };
+  const int chunks = (nk + T::chunk - 1) / T::chunk;
+  const float* qg = q + t * q_stride + (int64_t)g * GH * D;  // the group's GH heads are contiguous
+  float qv[(GH * D + kAttnThreads - 1) / kAttnThreads];
+#pragma unroll
+  for (int i = 0; i < (GH * D + kAttnThreads - 1) / kAttnThreads; ++i) {
+    const int e = tid + i * kAttnThreads;
+    qv[i] = e < GH * D ? qg[e] : 0.0f;
+  }
+  if (stager && sgrp < chunks) load_chunk(sgrp);
+
+  {
+    // Scores (kernels_avx512.cpp:234-244): 16 lanes per key, group grp takes keys grp, grp + 64, ...; KB keys per
+    // group in flight. Loads are never predicated (past the last key they re-read it, unused).
+    using KL = KLane<DC>;
+    constexpr int NGR = kAttnThreads / 16, KB = 8;
+    const int gl = tid & 15, grp = tid >> 4;
+    struct Round {
+      typename KL::T k[KB];
+      float sv;
+    };
+    auto fetch = [&](Round& R, int r) {
+#pragma unroll
+      for (int b = 0; b < KB; ++b) {
+        const int j = min((r * KB + b) * NGR + grp, nk - 1);
+        R.k[b] = *reinterpret_cast<const typename KL::T*>(kb + key_row(j) * a.k_row + DC * gl);
+      }
+      const int js = min((r * KB + (gl & 7) % KB) * NGR + grp, nk - 1);
+      R.sv = *reinterpret_cast<const float*>((gl < 8 ? ksb : vsb) + key_row(js) * a.s_row);
+    };
+    const int rounds = (nk + NGR * KB - 1) / (NGR * KB);
+    Round RA, RB;
+    fetch(RA, 0);
+#pragma unroll
+    for (int i = 0; i < (GH * D + kAttnThreads - 1) / kAttnThreads; ++i) {
+      const int e = tid + i * kAttnThreads;
+      if (e < GH * D) qs[e] = qv[i];
+    }
+    lds_barrier();
+    float qr[GH][DC];  // q of chain gl for each head: q_h[16 c + gl]
+#pragma unroll
+    for (int h = 0; h < GH; ++h)
+#pragma unroll
+      for (int c = 0; c < DC; ++c) qr[h][c] = qs[h * D + 16 * c + gl];
+    auto score = [&](const Round& R, int r) {
+#pragma unroll
+      for (int b = 0; b < KB; ++b) {
+        const int j = (r * KB + b) * NGR + grp;
+        if (j < nk) {  // uniform over the 16 lanes of the key
+          float kf[DC];
+#pragma unroll
+          for (int c = 0; c < DC; ++c) kf[c] = (float)KL::at(R.k[b], c);
+          const float ksv = bcast16(R.sv, b), vsv = bcast16(R.sv, 8 + b);
+#pragma unroll
+          for (int h = 0; h < GH; ++h) {
+            float acc = qr[h][0] * kf[0];
+#pragma unroll
+            for (int c = 1; c < DC; ++c) acc = fma_(qr[h][c], kf[c], acc);
+            acc = reduce16_lanes(acc);
+            if (gl == 0) {
+              sc[h * nk_pad + j] = acc * (ksv * scale);
+              pv[h * nk_pad + j] = vsv;
+            }
+          }
+        }
+      }
+    };
+    for (int r = 0; r < rounds; r += 2) {
+      fetch(RB, min(r + 1, rounds - 1));
+      score(RA, r);
+      if (r + 1 >= rounds) break;
+      fetch(RA, min(r + 2, rounds - 1));
+      score(RB, r + 1);
+    }
+  }
+  store_chunk(0);
+  if (NG < chunks) load_chunk(NG);
+  lds_barrier();
+
+  // softmax_inplace (kernels_avx512.cpp:205-226), every head in one pass.
+  {
+    float m[GH];
+#pragma unroll
+    for (int h = 0; h < GH; ++h) m[h] = -INFINITY;
+    for (int j = tid; j < nk; j += kAttnThreads)
+#pragma unroll
+      for (int h = 0; h < GH; ++h) m[h] = fmaxf(m[h], sc[h * nk_pad + j]);
+#pragma unroll
+    for (int h = 0; h < GH; ++h) {
+      for (int off = 32; off > 0; off >>= 1) m[h] = fmaxf(m[h], __shfl_xor(m[h], off));
+      if ((tid & 63) == 0) red[h][tid >> 6] = m[h];
+    }
+    lds_barrier();
+#pragma unroll
+    for (int h = 0; h < GH; ++h) {
+      float mx = red[h][0];
+      for (int i = 1; i < kAttnThreads / 64; ++i) mx = fmaxf(mx, red[h][i]);
+      m[h] = mx;
+    }
+    for (int j = tid; j < nk; j += kAttnThreads)
+#pragma unroll
+      for (int h = 0; h < GH; ++h) {
+        const float e = exp512(sc[h * nk_pad + j] - m[h]);
+        sc[h * nk_pad + j] = e;
+        pv[h * nk_pad + j] = e * pv[h * nk_pad + j];
+      }
+    for (int j = nk + tid; j < attn_keys_pad(nk); j += kAttnThreads)
+#pragma unroll
+      for (int h = 0; h < GH; ++h) pv[h * nk_pad + j] = 0.0f;
+  }
+  lds_barrier();
+
+  // P.V (kernels_avx512.cpp:247-265): chunk c from tile c & 1 while chunk c + 1 is stored and c + 1 + NG loaded.
+  const int nk16 = attn_keys_pad(nk);
+  const int set = tid / D, d = tid % D;
+  const int hb = set * C::h0;  // first head of this chain lane's set
+  float acc[C::h0];
+#pragma unroll
+  for (int k = 0; k < C::h0; ++k) acc[k] = 0.0f;
+  float lane_sum[GH];
+#pragma unroll
+  for (int h = 0; h < GH; ++h) lane_sum[h] = 0.0f;
+  if (tid < C::chain) __builtin_amdgcn_s_setprio(3);
+  for (int c = 0; c < chunks; ++c) {
+    if (tid < C::chain) {
+      const int j0 = c * T::chunk;
+      const int len = min(T::chunk, nk16 - j0);  // a multiple of 16
+      const float4* vr = reinterpret_cast<const float4*>(tiles + (c & 1) * (T::tile / 4) + d * T::stride);
+      auto run = [&]<int NH>() __attribute__((always_inline)) {
+        const float* pc = pv + hb * nk_pad + j0 + (tid & 15);
+        float4 va[4], vb2[4];
+        float pa[NH], pb[NH];
+        auto ld = [&](float4(&v)[4], float(&p)[NH], int jj) {
+          const int j = min(jj, len - 16);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = vr[j / 4 + i];
+#pragma unroll
+          for (int k = 0; k < NH; ++k) p[k] = pc[k * nk_pad + j];
+        };
+        auto chain = [&](const float4(&v)[4], const float(&p)[NH]) {
+          [&]<int... I>(std::integer_sequence<int, I...>) __attribute__((always_inline)) {
+            ((
+                 [&] {
+                   const float vi = (&v[I / 4].x)[I % 4];
+#pragma unroll
+                   for (int k = 0; k < NH; ++k) acc[k] = fma_bcast16<I>(p[k], vi, acc[k]);
+                 }()),
+             ...);
+          }(std::make_integer_sequence<int, 16>{});
+        };
+        ld(va, pa, 0);
+        for (int jj = 0; jj < len; jj += 32) {
+          ld(vb2, pb, jj + 16);
+          __builtin_amdgcn_sched_barrier(0);
+          chain(va, pa);
+          if (jj + 16 >= len) break;
+          ld(va, pa, jj + 32);
+          __builtin_amdgcn_sched_barrier(0);
+          chain(vb2, pb);
+        }
+      };
+      if constexpr (C::sets == 1)
+        run.template operator()<GH>();
+      else if (set == 0)
+        run.template operator()<C::h0>();
+      else
+        run.template operator()<GH - C::h0>();
+    } else if (tid >= kSumThread) {
+      // this chunk's part of lane l's sequential sum, per head (chunks are whole 16-key groups). All the chunk's
+      // reads are issued first; keys past the end add +0, which leaves a sum of e >= 0 unchanged.
+      const int l = tid - kSumThread, j0 = c * T::chunk;
+      float e[GH][T::chunk / 16];
+#pragma unroll
+      for (int i = 0; i < T::chunk / 16; ++i) {
+        const int j = j0 + l + 16 * i;
+#pragma unroll
+        for (int h = 0; h < GH; ++h) e[h][i] = j < nk ? sc[h * nk_pad + j] : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < T::chunk / 16; ++i)
+#pragma unroll
+        for (int h = 0; h < GH; ++h) lane_sum[h] = lane_sum[h] + e[h][i];
+      if (c + 1 == chunks) {
+#pragma unroll
+        for (int h = 0; h < GH; ++h) {
+          const float sm = reduce16_lanes(lane_sum[h]);
+          if (l == 0) inv_s[h] = 1.0f / sm;
+        }
+      }
+    } else if (c + 1 < chunks) {
+      store_chunk(c + 1);
+      if (c + 1 + NG < chunks) load_chunk(c + 1 + NG);
+    }
+    lds_barrier();
+  }
+  if (tid < C::chain) {
+    const int nh = set == 0 ? C::h0 : GH - C::h0;
+    float* o = out + t * out_stride + (int64_t)(g * GH + hb) * D + d;
+#pragma unroll
+    for (int k = 0; k < C::h0; ++k)
+      if (k < nh) o[k * D] = acc[k] * inv_s[hb + k];
   }
 }
 
@@ -1395,6 +1704,31 @@ void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int6
       a.k_perm ? go(k_attention_rows<128, true>) : go(k_attention_rows<128, false>);
   } else if (!anc_off && dec_ok(G, D, a, max_keys)) {
     launch_dec<false>(s, q, q_stride, out, out_stride, n, H, D, G, scale, a, seq, n_keys, max_keys, DecFuse{});
+  } else if (D == 128 && a.k_perm && aligned && G >= 2 && G <= kGrpMaxHeads && (int64_t)n * H > device_cus() &&
+             grp_lds_bytes(G, attn_keys_pad(max_keys), anc_off ? std::min(n, attn_keys_pad(max_keys)) : 0) <=
+                 160 * 1024 - 1024) {
+    // All heads of a KV group per workgroup (trees, keys past the decode kernel's LDS) where one workgroup per
+    // (token, head) would take more than one round of the CUs. A grouped workgroup costs about 1.6 times a per-head
+    // one (2048 keys, G = 5: 70 vs 44 us), so with fewer pairs than CUs the per-head form is faster (measured).
+    const int nk_pad = attn_keys_pad(max_keys), anc_cap = anc_off ? std::min(n, nk_pad) : 0;
+    const size_t lds = grp_lds_bytes(G, nk_pad, anc_cap);
+    auto go = [&](auto kernel) {
+      static bool done = false;
+      if (!done) {
+        check(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  160 * 1024 - 1024),
+              "hipFuncSetAttribute");
+        done = true;
+      }
+      hipLaunchKernelGGL(kernel, dim3(n * KV), dim3(kAttnThreads), lds, s, q, q_stride, out, out_stride, scale, a, seq,
+                         n_keys, anc_off, anc, n, KV, nk_pad, anc_cap);
+    };
+    switch (G) {
+      case 2: go(k_attention_grp<2>); break;
+      case 3: go(k_attention_grp<3>); break;
+      case 4: go(k_attention_grp<4>); break;
+      default: go(k_attention_grp<5>); break;
+    }
   } else if (G <= 16 && (D == 64 || D == 128 || D == 256) && aligned) {
     const int tile = D == 64 ? AttnTile<64>::tile : D == 128 ? AttnTile<128>::tile : AttnTile<256>::tile;
     const int nk_pad = attn_keys_pad(max_keys);

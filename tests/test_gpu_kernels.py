@@ -546,12 +546,49 @@ LONG_CASES = [
 ]
 
 
+def _tree(P, depth):
+    """Ancestor rows of the engine's tree after a P-token prefix: node 0 at row P, chain / alternative of depth k at
+    rows P + 1 + 2k and P + 2 + 2k, both children of the chain node of depth k - 1 (of node 0 for k = 0); a node's
+    list runs from node 0 down to itself."""
+    par = [-1] + [0 if k == 0 else 2 * k - 1 for k in range(depth) for _ in range(2)]
+    out = []
+    for t in range(len(par)):
+        chain, u = [], t
+        while u >= 0:
+            chain.append(P + u)
+            u = par[u]
+        out.append(chain[::-1])
+    return out
+
+
+# The grouped kernel (all G query heads of a KV group per workgroup, G = 2..5, D = 128): trees, and keys past the
+# decode and multi-row kernels' LDS, where one workgroup per (token, head) would take more than one round of the
+# 256 CUs. (D, H, KV, token seqs, n_keys, n_ctx, ancestors per token)
+GRP_CASES = [
+    (128, 40, 8, [0] * 17, [2048] * 17, 2100, _tree(2048, 8)),              # config 5's verification tree, G = 5
+    (128, 16, 8, [0] * 17, [2000] * 17, 2048, _tree(2000, 8)),              # the same tree at G = 2
+    (128, 12, 4, [0] * 11 + [1] * 11, [1500] * 11 + [1300] * 11, 1600,
+     _tree(1500, 5) + _tree(1300, 5)),                                      # G = 3, two sequences' trees
+    (128, 32, 8, [0] * 9, [1200] * 9, 1300, _tree(1200, 4)),                # G = 4
+    (128, 40, 8, [0] * 20, [2000 - t for t in range(20)], 2048, None),     # 20 plain tokens past the multi-row LDS
+]
+
+
 @pytest.mark.parametrize("case", range(len(LONG_CASES)))
 def test_attention_long_rows_vs_oracle(mk, oracle, case):
-    D, H, KV, seqs, nks, n_ctx, ancs = LONG_CASES[case]
+    _attention_vs_oracle(mk, oracle, LONG_CASES[case], 700 + case, "long attention case %d" % case, True)
+
+
+@pytest.mark.parametrize("case", range(len(GRP_CASES)))
+def test_attention_grouped_vs_oracle(mk, oracle, case):
+    _attention_vs_oracle(mk, oracle, GRP_CASES[case], 800 + case, "grouped attention case %d" % case, False)
+
+
+def _attention_vs_oracle(mk, oracle, spec, seed, name, long_rows):
+    D, H, KV, seqs, nks, n_ctx, ancs = spec
     G, n, n_seq = H // KV, len(seqs), max(seqs) + 1
-    print("long attention case", case, dict(D=D, H=H, KV=KV, n=n, keys=max(nks)), flush=True)
-    rng = np.random.default_rng(700 + case)
+    print(name, dict(D=D, H=H, KV=KV, n=n, keys=max(nks)), flush=True)
+    rng = np.random.default_rng(seed)
     k8 = rng.integers(-127, 128, (n_seq, KV, n_ctx, D), dtype=np.int8)
     v8 = rng.integers(-127, 128, (n_seq, KV, n_ctx, D), dtype=np.int8)
     ks = rng.uniform(0.001, 0.05, (n_seq, KV, n_ctx)).astype(np.float32)
@@ -570,8 +607,9 @@ def test_attention_long_rows_vs_oracle(mk, oracle, case):
     out = mk.alloc(n * H * D * 4)
     kv = mk_.MkKvCache(dk.ptr, dv.ptr, dks.ptr, dvs.ptr, 1, n_seq, KV, D, n_ctx)
     need = L().mk_attention_scratch_bytes(D, max_keys, n * H)
-    assert need > 0
-    mk_.check(L().mk_reserve_scratch(mk.h, need))
+    assert (need > 0) == long_rows  # global slots only past one workgroup's LDS
+    if need:
+        mk_.check(L().mk_reserve_scratch(mk.h, need))
     mk_.check(L().mk_attention(mk.h, dq.ptr, H * D, out.ptr, H * D, n, H, ctypes.byref(kv), 0, dseq.ptr, dnk.ptr,
                                anc_off.ptr if anc_off is not None else None, anc.ptr if anc is not None else None,
                                max_keys))
@@ -591,7 +629,7 @@ def test_attention_long_rows_vs_oracle(mk, oracle, case):
             for g in range(KV):
                 exp = oracle.attend_gqa(q[t, g * G * D:(g + 1) * G * D], G, D, kf[g * D:], vf[g * D:], row,
                                         (KV - g) * D + 4 * g, nks[t], scale, extra=extra)
-                assert np.array_equal(bits(got[t, g * G * D:(g + 1) * G * D]), bits(exp)), (case, t, g)
+                assert np.array_equal(bits(got[t, g * G * D:(g + 1) * G * D]), bits(exp)), (name, t, g)
 
 
 def test_attention_long_rows_need_scratch():
