@@ -312,10 +312,10 @@ __global__ __launch_bounds__(kThreads) void k_mmv(const uint8_t* W, int64_t rows
     }
 }
 
-// K-split form for matrices with few rows (down and attn_output projections): four waves share one 16-row tile.
-// Per stage of 8 units, wave w computes the MFMA dots of units 2 w and 2 w + 1 and their per-unit float terms
-// (the operands of the reference's fmas, rounded as the reference rounds them) into LDS; after a barrier every
-// lane runs the sequential chains of NTT (row, token) outputs over the stage's 8 units in order. Terms per unit and
+// K-split form for matrices with few rows (down and attn_output projections): KW = 4 or 8 waves share one 16-row
+// tile. Per stage of 8 units, wave w computes the MFMA dots of units (8 / KW) w .. and their per-unit float terms
+// (the operands of the reference's fmas, rounded as the reference rounds them) into LDS; after a barrier the lanes
+// run the sequential chains of the tile's (row, token) outputs over the stage's 8 units in order. Terms per unit and
 // output, E floats: Q8_0 {float(ai), dw dx}; Q6_K compact {float(ai_0), (d sc_0) dx, float(ai_1), (d sc_1) dx};
 // Q6_K wide {fma(float(ai_1), d sc_1, float(ai_0) (d sc_0)), dx}; Q4_K {float(ai), (d sc) dx}; the chain applies
 // acc = fma(e0, e1, acc) (and acc = fma(e2, e3, acc)). Q4_K's second fma, acc = fma(-(dmin m), dx (s0 + s1), acc),
@@ -324,7 +324,7 @@ template <int TYPE, bool WIDE>
 struct Ks {
   static constexpr int E = (TYPE == kQ8_0 || TYPE == kQ4_K || (TYPE == kQ6_K && WIDE)) ? 2 : 4;
 };
-template <int TYPE, bool WIDE, int NTT>
+template <int TYPE, bool WIDE, int NTT, int KW>
 struct KsLds {
   static constexpr int w_bytes = TYPE == kQ8_0 ? 2 * 8 * 256 : TYPE == kQ6_K ? 2 * 1536 : 2 * 1024;
   static constexpr int s_off = w_bytes, d_off = w_bytes + 256;
@@ -337,15 +337,21 @@ struct KsLds {
   // a three-stage ring in 80 KB each.
   static constexpr bool db = (80 * 1024 - 2 * terms1) / bytes >= 3;
   static constexpr int terms = (db ? 2 : 1) * terms1;
+  // X: 4 NTT pieces of 1 KB per stage, xp per wave (KW waves)
+  static constexpr int xp = (4 * NTT + KW - 1) / KW;
   // loads per wave per stage: W, S, (D), X, DX, (XS); pieces past a wave's share repeat another wave's copy
-  static constexpr int loads = 1 + 1 + (TYPE == kQ6_K ? 1 : 0) + NTT + 1 + (TYPE == kQ4_K ? 1 : 0);
+  static constexpr int loads = 1 + 1 + (TYPE == kQ6_K ? 1 : 0) + xp + 1 + (TYPE == kQ4_K ? 1 : 0);
 };
 
-template <int TYPE, bool WIDE, int NTT, int NS>
-__global__ __launch_bounds__(256) void k_mmv_ks(const uint8_t* W, int64_t rows, int64_t cols, const BlockQ8* x,
-                                                 int n, float* __restrict__ y, int64_t ys, int accumulate) {
-  using S = KsLds<TYPE, WIDE, NTT>;
+// KW waves per workgroup (4 or 8): each wave computes the dots and terms of 8 / KW of a stage's 8 units.
+template <int TYPE, bool WIDE, int NTT, int NS, int KW>
+__global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t rows, int64_t cols, const BlockQ8* x,
+                                                     int n, float* __restrict__ y, int64_t ys, int accumulate) {
+  using S = KsLds<TYPE, WIDE, NTT, KW>;
   constexpr int E = Ks<TYPE, WIDE>::E;
+  constexpr int UPW = kUnits / KW;                  // units per wave and stage
+  constexpr int CT = 4 * KW;                        // token rows of the chain threads (16 rows x CT tokens)
+  constexpr int CPT = (16 * NTT + CT - 1) / CT;     // chains per thread
   static_assert((NS - 1) * S::loads < 64, "the ring's loads must fit the vmcnt counter");
   extern __shared__ __align__(16) uint8_t smem[];
   float* terms_base = reinterpret_cast<float*>(smem + NS * S::bytes);  // [2][unit][token][row][E]
@@ -358,14 +364,16 @@ __global__ __launch_bounds__(256) void k_mmv_ks(const uint8_t* W, int64_t rows, 
   const int nst = nq8 / kUnits;
   const int64_t g0 = (int64_t)rt * 2;               // first 8-row group
 
-  // Copies. W: 1 KB pieces, wave w takes piece min(w, pieces - 1); S, D: one 256-byte piece, every wave; X: NTT
-  // 1 KB pieces per wave; DX, XS: 256-byte pieces, wave w takes piece w % (2 NTT).
+  // Copies. W: 1 KB pieces, wave w takes piece min(w, pieces - 1); S, D: one 256-byte piece, every wave; X: xp
+  // 1 KB pieces per wave (piece min(xp w + k, 4 NTT - 1)); DX, XS: 256-byte pieces, wave w takes piece w % (2 NTT).
   constexpr int WP = S::w_bytes / 1024;
   const uint8_t* xb = reinterpret_cast<const uint8_t*>(x + (int64_t)t0 * nq8);
-  uint32_t x_off[NTT], dx_off;
+  uint32_t x_off[S::xp], dx_off;
+  int x_pc[S::xp];
 #pragma unroll
-  for (int k = 0; k < NTT; ++k) {
-    const int p = 1024 * (NTT * wu + k) + 16 * lane;
+  for (int k = 0; k < S::xp; ++k) {
+    x_pc[k] = min(S::xp * wu + k, 4 * NTT - 1);
+    const int p = 1024 * x_pc[k] + 16 * lane;
     const int unit = p / (512 * NTT), rem = p % (512 * NTT);
     const int tok = min(rem / 32, ntok - 1), half = (rem % 32) / 16;
     x_off[k] = (uint32_t)((tok * nq8 + unit) * 40 + 8 + 16 * half);
@@ -422,18 +430,18 @@ __global__ __launch_bounds__(256) void k_mmv_ks(const uint8_t* W, int64_t rows, 
     if constexpr (TYPE == kQ6_K) ld4(wd + (size_t)sn * 16 + d_off, st + S::d_off);
     const uint8_t* xs = xb + (size_t)sn * kUnits * 40;
 #pragma unroll
-    for (int k = 0; k < NTT; ++k) ld16(xs + x_off[k], st + S::x + 1024 * (NTT * wu + k));
+    for (int k = 0; k < S::xp; ++k) ld16(xs + x_off[k], st + S::x + 1024 * x_pc[k]);
     ld4(xs + dx_off, st + S::dx + 256 * dxp);
     if constexpr (TYPE == kQ4_K) ld4(xs + dx_off + 4, st + S::xs + 256 * dxp);
   };
 
   // MFMA lane roles: row r = lane % 16 (group gi = r / 8, row rr = r % 8), weight quarter c = lane / 16, result
-  // elements i: tokens 4 c + i (+ 16 m). Chain role: row cr = tid % 16, token ct = tid / 16 (+ 16 m).
+  // elements i: tokens 4 c + i (+ 16 m). Chain role: row cr = tid % 16, tokens ct + CT m (those below 16 NTT).
   const int r = lane & 15, c = lane >> 4, gi = r >> 3, rr = r & 7;
   const int cr = tid & 15, ct = tid >> 4;
-  float acc[NTT];
+  float acc[CPT];
 #pragma unroll
-  for (int m = 0; m < NTT; ++m) acc[m] = 0.0f;
+  for (int m = 0; m < CPT; ++m) acc[m] = 0.0f;
   const v4i zero4 = {0, 0, 0, 0};
   // Q4_K per stage (double-buffered like the terms): -(dmin m) per (row, unit) and dx (s0 + s1) per (token, unit)
   __shared__ __align__(16) float nmn_tab[TYPE == kQ4_K ? 2 * 16 * kUnits : 4];
@@ -469,18 +477,20 @@ __global__ __launch_bounds__(256) void k_mmv_ks(const uint8_t* W, int64_t rows, 
       }
     }
 #pragma unroll
-    for (int m = 0; m < NTT; ++m) {
+    for (int m = 0; m < CPT; ++m) {
+      const int tk = ct + CT * m;
+      if (CT * CPT > 16 * NTT && tk >= 16 * NTT) break;  // wave-uniform: threads past the tile's tokens
       float xsv[kUnits];
       if constexpr (TYPE == kQ4_K) {
 #pragma unroll
         for (int h = 0; h < kUnits / 4; ++h) {
-          const float4 v = *reinterpret_cast<const float4*>(xs_t + (ct + 16 * m) * kUnits + 4 * h);
+          const float4 v = *reinterpret_cast<const float4*>(xs_t + tk * kUnits + 4 * h);
           xsv[4 * h] = v.x, xsv[4 * h + 1] = v.y, xsv[4 * h + 2] = v.z, xsv[4 * h + 3] = v.w;
         }
       }
 #pragma unroll
       for (int u = 0; u < kUnits; ++u) {
-        const float* p = terms + (((u * 16 * NTT) + ct + 16 * m) * 16 + cr) * E;
+        const float* p = terms + (((u * 16 * NTT) + tk) * 16 + cr) * E;
         if constexpr (E == 2) {
           const float2 e = *reinterpret_cast<const float2*>(p);
           acc[m] = fma_(e.x, e.y, acc[m]);
@@ -505,8 +515,8 @@ __global__ __launch_bounds__(256) void k_mmv_ks(const uint8_t* W, int64_t rows, 
     select(s);
     if constexpr (TYPE == kQ8_0) {
 #pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int u = 2 * wu + k;
+      for (int k = 0; k < UPW; ++k) {
+        const int u = UPW * wu + k;
         const long b = *reinterpret_cast<const long*>(st + gi * 2048 + u * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
         const float dw = half_to_float(*reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + u * 16 + rr * 2));
 #pragma unroll
@@ -523,8 +533,8 @@ __global__ __launch_bounds__(256) void k_mmv_ks(const uint8_t* W, int64_t rows, 
       const float dd = half_to_float(*reinterpret_cast<const uint16_t*>(st + S::d_off + gi * 16 + rr * 2));
       const int hw = c >> 1, h = c & 1;
 #pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int u = 2 * wu + k;
+      for (int k = 0; k < UPW; ++k) {
+        const int u = UPW * wu + k;
         const uint8_t* au = st + gi * 1536 + u * 192;
         const uint2 nib = *reinterpret_cast<const uint2*>(au + rr * 16 + 8 * h);
         const uint2 hb = *reinterpret_cast<const uint2*>(au + 128 + rr * 8);
@@ -551,14 +561,14 @@ __global__ __launch_bounds__(256) void k_mmv_ks(const uint8_t* W, int64_t rows, 
           }
         }
       }
-    } else {  // Q4_K: wave w takes chunk j2 = w: units 2 w (low nibbles) and 2 w + 1 (high nibbles)
-      {  // dx (s0 + s1) of the wave's two units' tokens, once per (unit, token)
+    } else {  // Q4_K: the wave's units UPW w .. (64-weight chunk u / 2: even units low nibbles, odd high)
+      {  // dx (s0 + s1) of the wave's units' tokens, once per (unit, token)
         constexpr int TOKS = 16 * NTT;
 #pragma unroll
-        for (int k = 0; k < (2 * TOKS + 63) / 64; ++k) {
+        for (int k = 0; k < (UPW * TOKS + 63) / 64; ++k) {
           const int idx = lane + 64 * k;
-          if (idx < 2 * TOKS) {
-            const int u = 2 * wu + idx / TOKS, tok = idx % TOKS;
+          if (idx < UPW * TOKS) {
+            const int u = UPW * wu + idx / TOKS, tok = idx % TOKS;
             const int at = (u * NTT + tok / 16) * 16 + tok % 16;
             const uint32_t sx = *reinterpret_cast<const uint32_t*>(st + S::xs + at * 4);
             const float dxv = *reinterpret_cast<const float*>(st + S::dx + at * 4);
@@ -568,11 +578,12 @@ __global__ __launch_bounds__(256) void k_mmv_ks(const uint8_t* W, int64_t rows, 
       }
       const uint4 hd = *reinterpret_cast<const uint4*>(st + S::s_off + gi * 128 + rr * 16);
       const float d = half_to_float((uint16_t)(hd.x & 0xFFFF)), dmin = half_to_float((uint16_t)(hd.x >> 16));
+      const int j2 = UPW * wu / 2;  // the wave's 64-weight chunk
       const uint2 raw =
-          *reinterpret_cast<const uint2*>(st + gi * 1024 + wu * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
+          *reinterpret_cast<const uint2*>(st + gi * 1024 + j2 * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int u = 2 * wu + e;
+      for (int k = 0; k < UPW; ++k) {
+        const int u = UPW * wu + k, e = u & 1;
         const long bq = (long)(((uint64_t)((raw.y >> (4 * e)) & 0x0F0F0F0Fu) << 32) | ((raw.x >> (4 * e)) & 0x0F0F0F0Fu));
         int sc, mn;
         scale_min(u, hd.y, hd.z, hd.w, sc, mn);
@@ -619,8 +630,8 @@ __global__ __launch_bounds__(256) void k_mmv_ks(const uint8_t* W, int64_t rows, 
 
   const int64_t row = (int64_t)rt * 16 + cr;
 #pragma unroll
-  for (int m = 0; m < NTT; ++m) {
-    const int t = ct + 16 * m;
+  for (int m = 0; m < CPT; ++m) {
+    const int t = ct + CT * m;
     if (t < ntok) {
       float* o = y + (int64_t)(t0 + t) * ys + row;
       *o = accumulate ? *o + acc[m] : acc[m];
@@ -628,40 +639,48 @@ __global__ __launch_bounds__(256) void k_mmv_ks(const uint8_t* W, int64_t rows, 
   }
 }
 
-template <int TYPE, bool WIDE, int NTT, int NS>
+template <int TYPE, bool WIDE, int NTT, int NS, int KW>
 void launch_ks_ns(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
                   int64_t ys, bool accumulate) {
-  using S = KsLds<TYPE, WIDE, NTT>;
+  using S = KsLds<TYPE, WIDE, NTT, KW>;
   const size_t lds = NS * (size_t)S::bytes + S::terms;
   static bool attr = false;
   if (!attr) {
-    check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_mmv_ks<TYPE, WIDE, NTT, NS>),
+    check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_mmv_ks<TYPE, WIDE, NTT, NS, KW>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
           "hipFuncSetAttribute");
     attr = true;
   }
   const int tiles = (n + 16 * NTT - 1) / (16 * NTT);
-  hipLaunchKernelGGL((k_mmv_ks<TYPE, WIDE, NTT, NS>), dim3((unsigned)(rows / 16), (unsigned)tiles), dim3(256), lds, s,
-                     static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0);
+  hipLaunchKernelGGL((k_mmv_ks<TYPE, WIDE, NTT, NS, KW>), dim3((unsigned)(rows / 16), (unsigned)tiles), dim3(64 * KW),
+                     lds, s, static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0);
 }
+
+// Waves per 16-row tile of the K-split kernel, measured on MI355X: eight (one unit per wave and stage) for two token
+// tiles (17-32 tokens: Qwen3-14B Q6_K at 17 tokens, 5120 x 17408 95.4 -> 86.3 us, 5120 x 5120 30.1 -> 27.4 us) and
+// for Q8_0 (4096 x 12288 at 8 tokens 26.4 -> 24.5 us); four for one K-quant token tile (Q4_K 5120 x 17408 at 8
+// tokens: 63.6 vs 74.4 us with eight).
+template <int TYPE, int NTT>
+constexpr int ks_waves() { return NTT == 2 || TYPE == kQ8_0 ? 8 : 4; }
 
 // Ring depth: the deepest ring that fits one workgroup per CU when the grid fits the GPU once, else one that lets
 // two workgroups share a CU (80 KB each).
 template <int TYPE, bool WIDE, int NTT>
 void launch_ks_ntt(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
                    int64_t ys, bool accumulate) {
-  using S = KsLds<TYPE, WIDE, NTT>;
+  constexpr int KW = ks_waves<TYPE, NTT>();
+  using S = KsLds<TYPE, WIDE, NTT, KW>;
   const int64_t wgs = rows / 16 * ((n + 16 * NTT - 1) / (16 * NTT)), cus = device_cus();
   constexpr int kDeep = (150 * 1024 - S::terms) / S::bytes >= 8 ? 8 : (150 * 1024 - S::terms) / S::bytes;
   constexpr int kTwo = (80 * 1024 - S::terms) / S::bytes;
   static_assert(kDeep >= 3, "the K-split ring needs three stages");
   if constexpr (kTwo >= 3) {
     if (wgs > cus) {
-      launch_ks_ns<TYPE, WIDE, NTT, (kTwo > 6 ? 6 : kTwo)>(s, w, rows, cols, x, n, y, ys, accumulate);
+      launch_ks_ns<TYPE, WIDE, NTT, (kTwo > 6 ? 6 : kTwo), KW>(s, w, rows, cols, x, n, y, ys, accumulate);
       return;
     }
   }
-  launch_ks_ns<TYPE, WIDE, NTT, kDeep>(s, w, rows, cols, x, n, y, ys, accumulate);
+  launch_ks_ns<TYPE, WIDE, NTT, kDeep, KW>(s, w, rows, cols, x, n, y, ys, accumulate);
 }
 
 template <int TYPE, bool WIDE>
