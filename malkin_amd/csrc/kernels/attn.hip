@@ -492,20 +492,24 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_long(const float* __
 //   sums    the 16 sequential lane sums per head advance chunk by chunk on the last 16 threads.
 constexpr int kGrpMaxHeads = 5;
 
+// V tiles of CK keys as int8, transposed to [value][key] (rows of CK + 16 bytes; a value row's 16-key blocks are
+// stored XOR (value / 16) % 8 so that the staging writes spread over the banks), converted to fp32 by the chain lanes
+// one 16-key group ahead of the fmas that use them.
 template <int GH>
 struct GrpCfg {
   static constexpr int D = 128, DC = 8;
   static constexpr int sets = GH <= 3 ? 1 : 2;           // head sets of the chain lanes
   static constexpr int h0 = (GH + sets - 1) / sets;      // heads of set 0 (set 1: GH - h0)
   static constexpr int chain = sets * D;                 // chain threads
-  using T = AttnTile<D>;
-  static constexpr int groups = (kSumThread - chain) / T::tasks;  // V staging groups
-  static_assert(groups >= 2, "too few staging threads");
+  static constexpr int CK = 256, VS = CK + 16;           // keys per V tile, bytes per value row
+  static constexpr int tile = D * VS;                    // bytes per tile
+  static constexpr int tasks = (CK / 4) * (D / 16);      // staging task: 4 keys x 16 values
+  static_assert(chain + tasks <= kSumThread, "too few staging threads");
 };
 
 // LDS: two V tiles, q of the GH heads, per head scores then e values and P.V coefficients, the token's ancestors.
 __host__ __device__ constexpr size_t grp_lds_bytes(int GH, int nk_pad, int anc_cap) {
-  return 2 * (size_t)AttnTile<128>::tile + 4 * ((size_t)GH * 128 + 2 * (size_t)GH * nk_pad + (size_t)anc_cap);
+  return 2 * (size_t)GrpCfg<2>::tile + 4 * ((size_t)GH * 128 + 2 * (size_t)GH * nk_pad + (size_t)anc_cap);
 }
 
 template <int GH>
@@ -518,8 +522,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_grp(const float* __r
                                                                 const int32_t* __restrict__ anc, int n, int KV,
                                                                 int nk_pad, int anc_cap) {
   using C = GrpCfg<GH>;
-  using T = typename C::T;
-  constexpr int D = C::D, DC = C::DC;
+  constexpr int D = C::D, DC = C::DC, CK = C::CK, VS = C::VS;
   const int tid = threadIdx.x;
   // (token, group) pairs numbered group-major; XCD x (workgroups x, x + 8, ...) takes a contiguous run, so a group's
   // K/V rows are read into one XCD's L2.
@@ -534,8 +537,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_grp(const float* __r
   const int e0 = anc_off ? anc_off[t] : 0, ne = anc_off ? anc_off[t + 1] - e0 : 0;
   const int nk = n0 + ne;
   extern __shared__ int4 smem4[];
-  float* tiles = reinterpret_cast<float*>(smem4);                 // 2 x [D][stride] fp32
-  float* qs = tiles + 2 * T::tile / 4;                           // [GH][D]
+  uint8_t* tiles = reinterpret_cast<uint8_t*>(smem4);             // 2 x [D][VS] int8
+  float* qs = reinterpret_cast<float*>(tiles + 2 * C::tile);     // [GH][D]
   float* sc = qs + GH * D;                                       // [GH][nk_pad]: scores, then e^(s - max)
   float* pv = sc + GH * nk_pad;                                  // [GH][nk_pad]: v-scale, then e * v-scale
   int* anc_s = reinterpret_cast<int*>(pv + GH * nk_pad);         // anc_cap: KV rows of keys n0 .. nk - 1
@@ -554,38 +557,39 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_grp(const float* __r
   }
   auto key_row = [&](int j) -> int64_t { return j < n0 ? j : anc_s[min(j - n0, anc_cap - 1)]; };
 
-  // V staging (as attend_pair): task = 4 consecutive keys x 16 consecutive values.
-  constexpr int NG = C::groups;
-  const bool stager = tid >= C::chain && tid < C::chain + NG * T::tasks;
-  const int sgrp = (tid - C::chain) / T::tasks, task = (tid - C::chain) % T::tasks;
-  auto mine = [&](int c) { return stager && sgrp == c % NG; };
-  uint4 vreg[4];
+  // V staging: task = (quad kq of 4 keys, segment sg of 16 values); every chunk's tasks go to the same threads,
+  // which hold one chunk's rows in registers: chunk c + 2 is loaded right after chunk c + 1 is stored, a chunk's
+  // chain time ahead of its use. Past the last key the loads re-read it: those keys have coefficient 0 and a finite
+  // value, and fma(0, v, acc) == acc (the chain never holds -0).
+  const int si = tid - C::chain;
+  const bool stager = si >= 0 && si < C::tasks;
+  const int ssg = si % (D / 16), skq = si / (D / 16);
+  v4i vr[4];
   auto load_chunk = [&](int c) {
-    if (!mine(c)) return;
-    const int kq = task % (T::chunk / 4), db = task / (T::chunk / 4);
-    // Loads are never predicated (past the last key they re-read it; store_chunk writes zeros there), so the
-    // compiler's wait counts stay exact and the NG chunks of loads in flight are not waited for early.
+    if (!stager) return;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int j = min(c * T::chunk + 4 * kq + i, nk - 1);
-      vreg[i] = *reinterpret_cast<const uint4*>(vb + key_row(j) * a.k_row + 16 * db);
+    for (int x = 0; x < 4; ++x) {
+      const int j = min(c * CK + 4 * skq + x, nk - 1);
+      vr[x] = *reinterpret_cast<const v4i*>(vb + key_row(j) * a.k_row + 16 * ssg);
     }
   };
-  auto store_chunk = [&](int c) {
-    if (!mine(c)) return;
-    const int kq = task % (T::chunk / 4), db = task / (T::chunk / 4);
-    float* tile = tiles + (c & 1) * (T::tile / 4);
-    const int jq = c * T::chunk + 4 * kq;  // keys jq .. jq + 3; past nk the values are zero
+  auto store_chunk = [&](int c) {  // 4 x 4 byte transposes into the [value][key] rows
+    if (!stager) return;
+    const int col = 16 * ((skq >> 2) ^ (ssg & 7)) + 4 * (skq & 3);
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      float f[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        f[i] = jq + i < nk ? (float)(int8_t)((&vreg[i].x)[v >> 2] >> (8 * (v & 3))) : 0.0f;
-      *reinterpret_cast<float4*>(tile + (16 * db + v) * T::stride + 4 * kq) = make_float4(f[0], f[1], f[2], f[3]);
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t A = (uint32_t)vr[0][u], B = (uint32_t)vr[1][u];
+      const uint32_t Cw = (uint32_t)vr[2][u], E = (uint32_t)vr[3][u];
+      const uint32_t t0 = __builtin_amdgcn_perm(B, A, 0x05010400u), t1 = __builtin_amdgcn_perm(B, A, 0x07030602u);
+      const uint32_t t2 = __builtin_amdgcn_perm(E, Cw, 0x05010400u), t3 = __builtin_amdgcn_perm(E, Cw, 0x07030602u);
+      uint8_t* row = tiles + (c & 1) * C::tile + (16 * ssg + 4 * u) * VS + col;
+      *reinterpret_cast<uint32_t*>(row) = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+      *reinterpret_cast<uint32_t*>(row + VS) = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+      *reinterpret_cast<uint32_t*>(row + 2 * VS) = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+      *reinterpret_cast<uint32_t*>(row + 3 * VS) = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
     }
   };
-  const int chunks = (nk + T::chunk - 1) / T::chunk;
+  const int chunks = (nk + CK - 1) / CK;
   const float* qg = q + t * q_stride + (int64_t)g * GH * D;  // the group's GH heads are contiguous
   float qv[(GH * D + kAttnThreads - 1) / kAttnThreads];
 #pragma unroll
@@ -593,7 +597,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_grp(const float* __r
     const int e = tid + i * kAttnThreads;
     qv[i] = e < GH * D ? qg[e] : 0.0f;
   }
-  if (stager && sgrp < chunks) load_chunk(sgrp);
+  load_chunk(0);
 
   {
     // Scores (kernels_avx512.cpp:234-244): 16 lanes per key, group grp takes keys grp, grp + 64, ...; KB keys per
@@ -605,18 +609,30 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_grp(const float* __r
       typename KL::T k[KB];
       float sv;
     };
-    auto fetch = [&](Round& R, int r) {
+    // A key's row: its position below n0; a tree ancestor's KV row from LDS past it (TREE: the batch has ancestors,
+    // a uniform choice, so the plain form has no per-key branch). Offsets in 32 bits: a head's rows span
+    // n_ctx * (D + 4) bytes.
+    auto row_of = [&]<bool TREE>(int j) __attribute__((always_inline)) -> uint32_t {
+      if constexpr (TREE) return (uint32_t)(j < n0 ? j : anc_s[min(j - n0, anc_cap - 1)]);
+      return (uint32_t)j;
+    };
+    auto fetch = [&]<bool TREE>(Round& R, int r) __attribute__((always_inline)) {
 #pragma unroll
       for (int b = 0; b < KB; ++b) {
         const int j = min((r * KB + b) * NGR + grp, nk - 1);
-        R.k[b] = *reinterpret_cast<const typename KL::T*>(kb + key_row(j) * a.k_row + DC * gl);
+        R.k[b] = *reinterpret_cast<const typename KL::T*>(kb + row_of.template operator()<TREE>(j) *
+                                                                   (uint32_t)a.k_row + DC * gl);
       }
       const int js = min((r * KB + (gl & 7) % KB) * NGR + grp, nk - 1);
-      R.sv = *reinterpret_cast<const float*>((gl < 8 ? ksb : vsb) + key_row(js) * a.s_row);
+      R.sv = *reinterpret_cast<const float*>((gl < 8 ? ksb : vsb) +
+                                             row_of.template operator()<TREE>(js) * (uint32_t)a.s_row);
     };
     const int rounds = (nk + NGR * KB - 1) / (NGR * KB);
     Round RA, RB;
-    fetch(RA, 0);
+    if (ne > 0)
+      fetch.template operator()<true>(RA, 0);
+    else
+      fetch.template operator()<false>(RA, 0);
 #pragma unroll
     for (int i = 0; i < (GH * D + kAttnThreads - 1) / kAttnThreads; ++i) {
       const int e = tid + i * kAttnThreads;
@@ -628,7 +644,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_grp(const float* __r
     for (int h = 0; h < GH; ++h)
 #pragma unroll
       for (int c = 0; c < DC; ++c) qr[h][c] = qs[h * D + 16 * c + gl];
-    auto score = [&](const Round& R, int r) {
+    // One key: the GH dot products of the lane's chain (mul, then fma over the D/16 values), the halving trees of
+    // all heads interleaved; lane 0 of the key stores the scores and (head 0's slot) the value scale.
+    auto score = [&](const Round& R, int r) __attribute__((always_inline)) {
 #pragma unroll
       for (int b = 0; b < KB; ++b) {
         const int j = (r * KB + b) * NGR + grp;
@@ -636,31 +654,39 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_grp(const float* __r
           float kf[DC];
 #pragma unroll
           for (int c = 0; c < DC; ++c) kf[c] = (float)KL::at(R.k[b], c);
-          const float ksv = bcast16(R.sv, b), vsv = bcast16(R.sv, 8 + b);
+          float acc[GH];
 #pragma unroll
           for (int h = 0; h < GH; ++h) {
-            float acc = qr[h][0] * kf[0];
+            acc[h] = qr[h][0] * kf[0];
 #pragma unroll
-            for (int c = 1; c < DC; ++c) acc = fma_(qr[h][c], kf[c], acc);
-            acc = reduce16_lanes(acc);
-            if (gl == 0) {
-              sc[h * nk_pad + j] = acc * (ksv * scale);
-              pv[h * nk_pad + j] = vsv;
-            }
+            for (int c = 1; c < DC; ++c) acc[h] = fma_(qr[h][c], kf[c], acc[h]);
+          }
+          reduce16_lanes_n(acc);
+          const float ks2 = bcast16(R.sv, b) * scale, vsv = bcast16(R.sv, 8 + b);
+          if (gl == 0) {
+#pragma unroll
+            for (int h = 0; h < GH; ++h) sc[h * nk_pad + j] = acc[h] * ks2;
+            pv[j] = vsv;
           }
         }
       }
     };
-    for (int r = 0; r < rounds; r += 2) {
-      fetch(RB, min(r + 1, rounds - 1));
-      score(RA, r);
-      if (r + 1 >= rounds) break;
-      fetch(RA, min(r + 2, rounds - 1));
-      score(RB, r + 1);
-    }
+    auto loop = [&]<bool TREE>() __attribute__((always_inline)) {
+      for (int r = 0; r < rounds; r += 2) {
+        fetch.template operator()<TREE>(RB, min(r + 1, rounds - 1));
+        score(RA, r);
+        if (r + 1 >= rounds) break;
+        fetch.template operator()<TREE>(RA, min(r + 2, rounds - 1));
+        score(RB, r + 1);
+      }
+    };
+    if (ne > 0)
+      loop.template operator()<true>();
+    else
+      loop.template operator()<false>();
   }
   store_chunk(0);
-  if (NG < chunks) load_chunk(NG);
+  if (1 < chunks) load_chunk(1);
   lds_barrier();
 
   // softmax_inplace (kernels_avx512.cpp:205-226), every head in one pass.
@@ -683,20 +709,22 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_grp(const float* __r
       for (int i = 1; i < kAttnThreads / 64; ++i) mx = fmaxf(mx, red[h][i]);
       m[h] = mx;
     }
-    for (int j = tid; j < nk; j += kAttnThreads)
+    for (int j = tid; j < nk; j += kAttnThreads) {
+      const float vs = pv[j];  // the key's value scale (head 0's slot)
 #pragma unroll
       for (int h = 0; h < GH; ++h) {
         const float e = exp512(sc[h * nk_pad + j] - m[h]);
         sc[h * nk_pad + j] = e;
-        pv[h * nk_pad + j] = e * pv[h * nk_pad + j];
+        pv[h * nk_pad + j] = e * vs;
       }
+    }
     for (int j = nk + tid; j < attn_keys_pad(nk); j += kAttnThreads)
 #pragma unroll
       for (int h = 0; h < GH; ++h) pv[h * nk_pad + j] = 0.0f;
   }
   lds_barrier();
 
-  // P.V (kernels_avx512.cpp:247-265): chunk c from tile c & 1 while chunk c + 1 is stored and c + 1 + NG loaded.
+  // P.V (kernels_avx512.cpp:247-265): chunk c from tile c & 1 while chunk c + 1 is stored and c + 2 loaded.
   const int nk16 = attn_keys_pad(nk);
   const int set = tid / D, d = tid % D;
   const int hb = set * C::h0;  // first head of this chain lane's set
@@ -709,40 +737,49 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_grp(const float* __r
   if (tid < C::chain) __builtin_amdgcn_s_setprio(3);
   for (int c = 0; c < chunks; ++c) {
     if (tid < C::chain) {
-      const int j0 = c * T::chunk;
-      const int len = min(T::chunk, nk16 - j0);  // a multiple of 16
-      const float4* vr = reinterpret_cast<const float4*>(tiles + (c & 1) * (T::tile / 4) + d * T::stride);
+      const int j0 = c * CK;
+      const int len = min(CK, nk16 - j0);  // a multiple of 16
+      const uint8_t* vrow = tiles + (c & 1) * C::tile + d * VS;
+      const int swz = (d >> 4) & 7;
       auto run = [&]<int NH>() __attribute__((always_inline)) {
         const float* pc = pv + hb * nk_pad + j0 + (tid & 15);
-        float4 va[4], vb2[4];
+        // A 16-key group: its raw bytes and coefficients are read one group ahead; its values are converted before
+        // its fmas (one convert feeds NH chains).
+        v4i wa, wb;
         float pa[NH], pb[NH];
-        auto ld = [&](float4(&v)[4], float(&p)[NH], int jj) {
+        auto ld = [&](v4i& w, float(&p)[NH], int jj) {
           const int j = min(jj, len - 16);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) v[i] = vr[j / 4 + i];
+          w = *reinterpret_cast<const v4i*>(vrow + 16 * ((j >> 4) ^ swz));
 #pragma unroll
           for (int k = 0; k < NH; ++k) p[k] = pc[k * nk_pad + j];
         };
-        auto chain = [&](const float4(&v)[4], const float(&p)[NH]) {
+        auto chain = [&](const v4i& w, const float(&p)[NH]) {
+          float f[16];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            f[4 * q] = i8_to_f32<0>((uint32_t)w[q]);
+            f[4 * q + 1] = i8_to_f32<1>((uint32_t)w[q]);
+            f[4 * q + 2] = i8_to_f32<2>((uint32_t)w[q]);
+            f[4 * q + 3] = i8_to_f32<3>((uint32_t)w[q]);
+          }
           [&]<int... I>(std::integer_sequence<int, I...>) __attribute__((always_inline)) {
             ((
                  [&] {
-                   const float vi = (&v[I / 4].x)[I % 4];
 #pragma unroll
-                   for (int k = 0; k < NH; ++k) acc[k] = fma_bcast16<I>(p[k], vi, acc[k]);
+                   for (int k = 0; k < NH; ++k) acc[k] = fma_bcast16<I>(p[k], f[I], acc[k]);
                  }()),
              ...);
           }(std::make_integer_sequence<int, 16>{});
         };
-        ld(va, pa, 0);
+        ld(wa, pa, 0);
         for (int jj = 0; jj < len; jj += 32) {
-          ld(vb2, pb, jj + 16);
+          ld(wb, pb, jj + 16);
           __builtin_amdgcn_sched_barrier(0);
-          chain(va, pa);
+          chain(wa, pa);
           if (jj + 16 >= len) break;
-          ld(va, pa, jj + 32);
+          ld(wa, pa, jj + 32);
           __builtin_amdgcn_sched_barrier(0);
-          chain(vb2, pb);
+          chain(wb, pb);
         }
       };
       if constexpr (C::sets == 1)
@@ -752,20 +789,20 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_grp(const float* __r
       else
         run.template operator()<GH - C::h0>();
     } else if (tid >= kSumThread) {
-      // this chunk's part of lane l's sequential sum, per head (chunks are whole 16-key groups). All the chunk's
-      // reads are issued first; keys past the end add +0, which leaves a sum of e >= 0 unchanged.
-      const int l = tid - kSumThread, j0 = c * T::chunk;
-      float e[GH][T::chunk / 16];
+      // this chunk's part of lane l's sequential sum, per head (chunks are whole 16-key groups): a head's reads are
+      // issued first; keys past the end add +0, which leaves a sum of e >= 0 unchanged.
+      const int l = tid - kSumThread, j0 = c * CK;
 #pragma unroll
-      for (int i = 0; i < T::chunk / 16; ++i) {
-        const int j = j0 + l + 16 * i;
+      for (int h = 0; h < GH; ++h) {
+        float e[CK / 16];
 #pragma unroll
-        for (int h = 0; h < GH; ++h) e[h][i] = j < nk ? sc[h * nk_pad + j] : 0.0f;
+        for (int i = 0; i < CK / 16; ++i) {
+          const int j = j0 + l + 16 * i;
+          e[i] = j < nk ? sc[h * nk_pad + j] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < CK / 16; ++i) lane_sum[h] = lane_sum[h] + e[i];
       }
-#pragma unroll
-      for (int i = 0; i < T::chunk / 16; ++i)
-#pragma unroll
-        for (int h = 0; h < GH; ++h) lane_sum[h] = lane_sum[h] + e[h][i];
       if (c + 1 == chunks) {
 #pragma unroll
         for (int h = 0; h < GH; ++h) {
@@ -775,7 +812,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_grp(const float* __r
       }
     } else if (c + 1 < chunks) {
       store_chunk(c + 1);
-      if (c + 1 + NG < chunks) load_chunk(c + 1 + NG);
+      if (c + 2 < chunks) load_chunk(c + 2);
     }
     lds_barrier();
   }

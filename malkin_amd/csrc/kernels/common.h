@@ -72,6 +72,43 @@ __device__ __forceinline__ float reduce16_lanes(float v) {
   return v;
 }
 
+// reduce16_lanes of N values at once (N = 2..5), the halving steps interleaved across the values: one v_add_f32_dpp
+// per value and step (lane l adds lane l + S's value: the same pairs as reduce16_lanes; a + b == b + a). A DPP read
+// of a VGPR needs two wait states after a VALU write of it: before the first step, and between steps when fewer than
+// three other instructions separate them (N < 3), an s_nop provides them.
+template <int S, int N>
+__device__ __forceinline__ void add_shl16_step(float (&v)[N]) {
+  static_assert(N >= 2 && N <= 5, "2 to 5 values");
+#define MK_ADD(I) "v_add_f32_dpp %" #I ", %" #I ", %" #I " row_shl:%" MK_NS " row_mask:0xf bank_mask:0xf\n\t"
+  if constexpr (N == 2) {
+#define MK_NS "2"
+    asm("s_nop 1\n\t" MK_ADD(0) MK_ADD(1) : "+v"(v[0]), "+v"(v[1]) : "i"(S));
+#undef MK_NS
+  } else if constexpr (N == 3) {
+#define MK_NS "3"
+    asm("s_nop 1\n\t" MK_ADD(0) MK_ADD(1) MK_ADD(2) : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]) : "i"(S));
+#undef MK_NS
+  } else if constexpr (N == 4) {
+#define MK_NS "4"
+    asm("s_nop 1\n\t" MK_ADD(0) MK_ADD(1) MK_ADD(2) MK_ADD(3)
+        : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]) : "i"(S));
+#undef MK_NS
+  } else {
+#define MK_NS "5"
+    asm("s_nop 1\n\t" MK_ADD(0) MK_ADD(1) MK_ADD(2) MK_ADD(3) MK_ADD(4)
+        : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]) : "i"(S));
+#undef MK_NS
+  }
+#undef MK_ADD
+}
+template <int N>
+__device__ __forceinline__ void reduce16_lanes_n(float (&v)[N]) {
+  add_shl16_step<8>(v);
+  add_shl16_step<4>(v);
+  add_shl16_step<2>(v);
+  add_shl16_step<1>(v);
+}
+
 // Direct global -> LDS copies: lane i writes its 16 (or 4) bytes at the wave-uniform LDS address + 16 i (4 i). They
 // are issued as inline assembly so that the compiler does not track them as LDS stores: it cannot tell a copy into a
 // later pipeline stage from the stage being read and would wait for every copy in flight (vmcnt(0)) before each LDS
