@@ -481,9 +481,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_long(const float* __
   }
 }
 
-// All G query heads of one KV group for one token per workgroup (G = 2..5, D = 128, permuted K rows, the keys in
-// LDS): verification trees and contexts past the decode kernel's LDS, where one workgroup per (token, head) would
-// read, convert and stage every K and V row G times. Same arithmetic as attend_pair, head by head:
+// GH query heads of one KV group for one token per workgroup (GH = G = 2..5, or GH = 1; D = 128, permuted K rows,
+// the keys in LDS): verification trees and contexts past the decode kernel's LDS. With GH = G every K and V row is
+// read, converted and staged once for the G heads instead of G times. Same arithmetic as attend_pair, head by head:
 //   scores  16 lanes per key as in attend_pair; each lane holds the D/16 q values of its chain for every head and
 //           runs G dot products on the K bytes it loaded once;
 //   softmax per head, one pass over the keys for all heads (G maxima, one barrier);
@@ -514,7 +514,7 @@ __host__ __device__ constexpr size_t grp_lds_bytes(int GH, int nk_pad, int anc_c
 
 template <int GH>
 __global__ __launch_bounds__(kAttnThreads) void k_attention_grp(const float* __restrict__ q, int64_t q_stride,
-                                                                float* __restrict__ out, int64_t out_stride,
+                                                                float* __restrict__ out, int64_t out_stride, int G,
                                                                 float scale, AttnAddr a,
                                                                 const int32_t* __restrict__ seqs,
                                                                 const int32_t* __restrict__ n_keys,
@@ -524,15 +524,18 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_grp(const float* __r
   using C = GrpCfg<GH>;
   constexpr int D = C::D, DC = C::DC, CK = C::CK, VS = C::VS;
   const int tid = threadIdx.x;
-  // (token, group) pairs numbered group-major; XCD x (workgroups x, x + 8, ...) takes a contiguous run, so a group's
-  // K/V rows are read into one XCD's L2.
-  int t, g;
+  // (group, token, head subset) numbered group-major; XCD x (workgroups x, x + 8, ...) takes a contiguous run, so a
+  // group's K/V rows are read into one XCD's L2.
+  const int hs = G / GH;  // head subsets per group
+  int t, g, hsub;
   {
-    const int total = n * KV, w = (int)blockIdx.x;
+    const int total = n * KV * hs, w = (int)blockIdx.x;
     const int pair = total % 8 == 0 ? (w % 8) * (total / 8) + w / 8 : w;
-    g = pair / n;
-    t = pair % n;
+    g = pair / (n * hs);
+    t = (pair / hs) % n;
+    hsub = pair % hs;
   }
+  const int hfirst = g * G + hsub * GH;  // the workgroup's first query head
   const int n0 = n_keys[t];
   const int e0 = anc_off ? anc_off[t] : 0, ne = anc_off ? anc_off[t + 1] - e0 : 0;
   const int nk = n0 + ne;
@@ -590,7 +593,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_grp(const float* __r
     }
   };
   const int chunks = (nk + CK - 1) / CK;
-  const float* qg = q + t * q_stride + (int64_t)g * GH * D;  // the group's GH heads are contiguous
+  const float* qg = q + t * q_stride + (int64_t)hfirst * D;  // the workgroup's GH heads are contiguous
   float qv[(GH * D + kAttnThreads - 1) / kAttnThreads];
 #pragma unroll
   for (int i = 0; i < (GH * D + kAttnThreads - 1) / kAttnThreads; ++i) {
@@ -818,7 +821,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_grp(const float* __r
   }
   if (tid < C::chain) {
     const int nh = set == 0 ? C::h0 : GH - C::h0;
-    float* o = out + t * out_stride + (int64_t)(g * GH + hb) * D + d;
+    float* o = out + t * out_stride + (int64_t)(hfirst + hb) * D + d;
 #pragma unroll
     for (int k = 0; k < C::h0; ++k)
       if (k < nh) o[k * D] = acc[k] * inv_s[hb + k];
@@ -1709,7 +1712,21 @@ size_t attention_scratch_bytes(int D, int max_keys, int pairs) {
   const int tile = D == 64 ? AttnTile<64>::tile : D == 128 ? AttnTile<128>::tile : AttnTile<256>::tile;
   const int nk_pad = attn_keys_pad(max_keys);
   if (attn_lds_bytes(tile, D, nk_pad) <= 160 * 1024 - 1024) return 0;
+  // D = 128 over the device cache: the grouped kernel with one head per workgroup holds more keys in LDS
+  if (D == 128 && grp_lds_bytes(1, nk_pad, std::min(pairs, nk_pad)) <= 160 * 1024 - 1024) return 0;
   return (size_t)std::min(pairs, 1024) * 2 * (size_t)nk_pad * sizeof(float);
+}
+
+// Heads per workgroup of the grouped kernel for this batch (0: not used). All G heads of a KV group (G = 2..5) when one
+// workgroup per (token, head) would take more than one round of the CUs: a grouped workgroup costs about twice a
+// single-head one (2057 keys, G = 5: 62 vs 31 us), so with fewer pairs than CUs one head per workgroup is faster.
+int grp_heads(int n, int H, int G, int D, const AttnAddr& a, const int32_t* anc_off, int max_keys) {
+  if (D != 128 || !a.k_perm || !attn_aligned(a) || G > 16) return 0;
+  const int nk_pad = attn_keys_pad(max_keys), anc_cap = anc_off ? std::min(n, nk_pad) : 0;
+  const size_t limit = 160 * 1024 - 1024;
+  if (G >= 2 && G <= kGrpMaxHeads && (int64_t)n * H > device_cus() && grp_lds_bytes(G, nk_pad, anc_cap) <= limit)
+    return G;
+  return grp_lds_bytes(1, nk_pad, anc_cap) <= limit ? 1 : 0;
 }
 
 void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int H, int KV,
@@ -1741,14 +1758,12 @@ void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int6
       a.k_perm ? go(k_attention_rows<128, true>) : go(k_attention_rows<128, false>);
   } else if (!anc_off && dec_ok(G, D, a, max_keys)) {
     launch_dec<false>(s, q, q_stride, out, out_stride, n, H, D, G, scale, a, seq, n_keys, max_keys, DecFuse{});
-  } else if (D == 128 && a.k_perm && aligned && G >= 2 && G <= kGrpMaxHeads && (int64_t)n * H > device_cus() &&
-             grp_lds_bytes(G, attn_keys_pad(max_keys), anc_off ? std::min(n, attn_keys_pad(max_keys)) : 0) <=
-                 160 * 1024 - 1024) {
-    // All heads of a KV group per workgroup (trees, keys past the decode kernel's LDS) where one workgroup per
-    // (token, head) would take more than one round of the CUs. A grouped workgroup costs about 1.6 times a per-head
-    // one (2048 keys, G = 5: 70 vs 44 us), so with fewer pairs than CUs the per-head form is faster (measured).
+  } else if (grp_heads(n, H, G, D, a, anc_off, max_keys) > 0) {
+    // Grouped workgroups (trees, keys past the decode kernel's LDS): all heads of a KV group per workgroup where one
+    // workgroup per (token, head) would take more than one round of the CUs, else one head per workgroup.
+    const int GH = grp_heads(n, H, G, D, a, anc_off, max_keys);
     const int nk_pad = attn_keys_pad(max_keys), anc_cap = anc_off ? std::min(n, nk_pad) : 0;
-    const size_t lds = grp_lds_bytes(G, nk_pad, anc_cap);
+    const size_t lds = grp_lds_bytes(GH, nk_pad, anc_cap);
     auto go = [&](auto kernel) {
       static bool done = false;
       if (!done) {
@@ -1757,10 +1772,11 @@ void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int6
               "hipFuncSetAttribute");
         done = true;
       }
-      hipLaunchKernelGGL(kernel, dim3(n * KV), dim3(kAttnThreads), lds, s, q, q_stride, out, out_stride, scale, a, seq,
-                         n_keys, anc_off, anc, n, KV, nk_pad, anc_cap);
+      hipLaunchKernelGGL(kernel, dim3(n * KV * (G / GH)), dim3(kAttnThreads), lds, s, q, q_stride, out, out_stride, G,
+                         scale, a, seq, n_keys, anc_off, anc, n, KV, nk_pad, anc_cap);
     };
-    switch (G) {
+    switch (GH) {
+      case 1: go(k_attention_grp<1>); break;
       case 2: go(k_attention_grp<2>); break;
       case 3: go(k_attention_grp<3>); break;
       case 4: go(k_attention_grp<4>); break;

@@ -536,13 +536,13 @@ def test_attention_decode_fused(mk, case):
     assert np.array_equal(dqb.download(np.float32), qkv.reshape(-1))  # raw projections untouched
 
 
-# Rows longer than one workgroup's LDS (about 7600 keys at D = 128): scores in global slots of the context's scratch.
-# (D, H, KV, token seqs, n_keys, n_ctx, ancestors per token)
+# Rows longer than one workgroup's LDS (about 11600 keys at D = 128, 7600 at D = 64): scores in global slots of the
+# context's scratch. (D, H, KV, token seqs, n_keys, n_ctx, ancestors per token)
 LONG_CASES = [
-    (128, 8, 2, [0], [8200], 8200, None),                                     # a decode step, G = 4
+    (128, 8, 2, [0], [12200], 12200, None),                                   # a decode step, G = 4
     (128, 4, 4, [0, 1, 0], [12000, 9000, 11000], 12100, None),               # G = 1, two sequences
     (64, 4, 2, [0, 0], [16500, 16400], 16500, None),                         # D = 64
-    (128, 8, 2, [0, 0, 0], [8000, 8000, 8000], 8100, [[], [8001], [8001, 8003]]),  # a tree: ancestors past the prefix
+    (128, 8, 2, [0, 0, 0], [12000, 12000, 12000], 12100, [[], [12001], [12001, 12003]]),  # a tree past the prefix
 ]
 
 
@@ -571,6 +571,8 @@ GRP_CASES = [
      _tree(1500, 5) + _tree(1300, 5)),                                      # G = 3, two sequences' trees
     (128, 32, 8, [0] * 9, [1200] * 9, 1300, _tree(1200, 4)),                # G = 4
     (128, 40, 8, [0] * 20, [2000 - t for t in range(20)], 2048, None),     # 20 plain tokens past the multi-row LDS
+    (128, 40, 8, [0], [2048], 2048, None),                                  # one head per workgroup: a long decode
+    (128, 16, 8, [0, 0, 0], [9000] * 3, 9100, [[9000], [9000, 9001], [9000, 9002]]),  # past the per-head fp32 tiles
 ]
 
 
