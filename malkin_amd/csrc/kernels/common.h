@@ -72,7 +72,7 @@ __device__ __forceinline__ float reduce16_lanes(float v) {
   return v;
 }
 
-// reduce16_lanes of N values at once (N = 2..5), the halving steps interleaved across the values: one v_add_f32_dpp
+// reduce16_lanes of N values at once (N = 1..5), the halving steps interleaved across the values: one v_add_f32_dpp
 // per value and step (lane l adds lane l + S's value: the same pairs as reduce16_lanes; a + b == b + a). A DPP read
 // of a VGPR needs two wait states after a VALU write of it: before the first step, and between steps when fewer than
 // three other instructions separate them (N < 3), an s_nop provides them.
@@ -103,10 +103,14 @@ __device__ __forceinline__ void add_shl16_step(float (&v)[N]) {
 }
 template <int N>
 __device__ __forceinline__ void reduce16_lanes_n(float (&v)[N]) {
-  add_shl16_step<8>(v);
-  add_shl16_step<4>(v);
-  add_shl16_step<2>(v);
-  add_shl16_step<1>(v);
+  if constexpr (N == 1) {
+    v[0] = reduce16_lanes(v[0]);
+  } else {
+    add_shl16_step<8>(v);
+    add_shl16_step<4>(v);
+    add_shl16_step<2>(v);
+    add_shl16_step<1>(v);
+  }
 }
 
 // Direct global -> LDS copies: lane i writes its 16 (or 4) bytes at the wave-uniform LDS address + 16 i (4 i). They
