@@ -62,6 +62,15 @@ __device__ __forceinline__ float shl16_k(float v, int k) {
   return __builtin_bit_cast(float, r);
 }
 
+// Workgroups are dealt to the 8 XCDs in turn (workgroup w runs on XCD w % 8, each XCD with its own L2). xcd_run
+// numbers them so that XCD x takes one contiguous run of the items 0 .. total - 1, for any total (a bijection: XCD x
+// holds total / 8 + (x < total % 8) workgroups, and its run starts after those of XCDs 0 .. x - 1). Items that share
+// operands and are numbered next to each other then share an XCD and read those operands into its L2 once.
+__device__ __forceinline__ int xcd_run(int w, int total) {
+  const int x = w & 7, j = w >> 3;
+  return x * (total >> 3) + min(x, total & 7) + j;
+}
+
 // The same tree over 16 consecutive lanes of a wavefront: lane l (l % 16 == 0 after the call holds the sum of lanes
 // l..l+15). Valid in lanes whose 16-lane group is fully active.
 __device__ __forceinline__ float reduce16_lanes(float v) {

@@ -81,30 +81,25 @@ __device__ __forceinline__ void load_lds16(const void* g, uint8_t* l) { lds_copy
 
 __device__ __forceinline__ void load_lds4(const void* g, uint8_t* l) { lds_copy4(g, l); }
 
-// waves_per_eu(1): the register budget of one wave per SIMD, so the two pipeline register sets never spill (the
-// kernel needs about 230 VGPRs, so two waves per SIMD still fit when the grid has them).
+// Waves per SIMD: the 3-stage TOK = 64 ring (78 KB) lets two workgroups share a CU, and a wave's MFMAs overlap the
+// VALU work of the other wave on its SIMD far better than its own (the step below: about 185 cycles per step and SIMD
+// with two waves, 334 with one), so that form keeps within 256 registers; the others run one workgroup per CU and
+// keep the register budget of one wave.
+// RA: how many steps ahead the operands are read from LDS (two where two waves share a SIMD: each wave then runs
+// about half as fast and the other wave's reads queue in front of its own).
 template <int TOK, int NS>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm_q8_0(
+constexpr int gemm_waves() { return TOK == 64 && NS == 3 ? 2 : 1; }
+template <int TOK, int NS, int RA>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(gemm_waves<TOK, NS>(), gemm_waves<TOK, NS>()))) void k_gemm_q8_0(
     const uint8_t* W, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* __restrict__ y, int64_t ys,
     int accumulate, int n_rt, int n_tt, int vec) {
   using S = StageLds<TOK>;
   constexpr int KB = S::KB;
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;  // wave w: rows 32 w .. 32 w + 31 of the tile
-  // Workgroup -> (row tile, token tile). Consecutive workgroups go to consecutive XCDs; the token tiles of a row tile
-  // are placed 8 apart so they share an XCD and its L2 holds the rows once.
-  int rt, tt;
-  {
-    const int wg = blockIdx.x;
-    if (n_rt % 8 == 0) {
-      const int xcd = wg % 8, j = wg / 8;
-      rt = (j / n_tt) * 8 + xcd;
-      tt = j % n_tt;
-    } else {
-      rt = wg / n_tt;
-      tt = wg % n_tt;
-    }
-  }
+  // Workgroup -> (row tile, token tile): tiles numbered row-major, each XCD a contiguous run of them, so the token
+  // tiles of a row tile share an XCD and its L2 holds the rows once.
+  const int tile = xcd_run((int)blockIdx.x, n_rt * n_tt), rt = tile / n_tt, tt = tile % n_tt;
   const int nb = (int)(cols / 32);
   const PackedQ8_0 L{rows, nb};
   const int64_t g0 = (int64_t)rt * (kRowsT / 8);                  // first 8-row group of the tile
@@ -178,9 +173,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
             off_dw = S::dw + 2 * arow + (TOK == 64 ? 0 : h * kRowsT * 2),
             off_dx = S::dx + (TOK == 64 ? 4 * lane : 4 * li + h * TOK * 4);
 
-  // Software pipeline over blocks j = 0, 1, ..., two register sets (X = even j, Y = odd j). Step j:
-  //   read the operands of block j + 1 (the first block of a stage: entered between the steps),
-  //   MFMAs of block j (scale products, int8 dots, their conversions; operands read in step j - 1),
+  // Software pipeline over blocks j = 0, 1, ..., RA + 1 operand register sets and two result sets. Step j:
+  //   read the operands of block j + RA (RA steps of LDS latency hidden),
+  //   MFMAs of block j (scale products, int8 dots, their conversions; operands read in step j - RA),
   //   fmas of block j - 1, interleaved with those MFMAs.
   // A wave issues one instruction every few cycles, in order, and one wave per SIMD is the common case here, so the
   // overlap of matrix and vector work has to be in the instruction stream itself, and the stream has to be short:
@@ -215,64 +210,74 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     for (int i = i0; i < i1; ++i) acc[i] = fma_(f[i], pp[16 * t + i], acc[i]);
     asm volatile("" : "+v"(acc));
   };
-  // One step: the MFMAs of a block (TOK = 32: two blocks; operands o*, results r*) and the fmas of the previous step
-  // (pf*, pp), in five regions of one MFMA each; the VALU work of a region covers its MFMA's time in the matrix pipe
-  // (64 or 32 cycles). `next` reads the following step's operands at the start. bl: the step's first block; a
-  // lane's scales are zeroed past the matrix (TOK = 32: the lane's block is bl + h).
+  // One step: the MFMAs of a block (TOK = 32: two blocks) and the fmas of the previous step, in five regions of one
+  // MFMA each; the VALU work of a region covers its MFMA's time in the matrix pipe. I: the step's index in a ring
+  // cycle, which picks the register sets: operands op[I % (RA + 1)] (read RA steps earlier), results rs[I % 2], the
+  // previous step's results rs[1 - I % 2]; the step first reads the operands of step I + RA (buffer RB, step RBL of
+  // that stage) into op[(I + RA) % (RA + 1)]. bl: the step's first block; a lane's scales are zeroed past the matrix (TOK =
+  // 32: the lane's block is bl + h).
+  struct Ops {
+    v4i a0, a1, b0, b1;
+    uint16_t dw;  // f16 weight scale as read
+    float dx;
+  };
+  struct Res {
+    v16f f0, f1;
+    v32f p;
+  };
+  Ops op[RA + 1];
+  Res rs[2];
+  rs[1].f0 = {};
+  rs[1].f1 = {};
+  rs[1].p = {};
   v16f& acc_b = TOK == 64 ? acc1 : acc0;  // the second MFMA's accumulator
-  auto step = [&](const v4i& oa0, const v4i& oa1, const v4i& ob0, const v4i& ob1, uint16_t odw, float odx, int bl,
-                  v16f& rf0, v16f& rf1, v32f& rp, const v16f& pf0, const v16f& pf1, const v32f& pp, auto&& next)
-      __attribute__((always_inline)) {
+  auto step = [&]<int I, int RB, int RBL>(int bl) __attribute__((always_inline)) {
+    const Ops& o = op[I % (RA + 1)];
+    Res& r = rs[I % 2];
+    const Res& pr = rs[1 - I % 2];
+    Ops& nx = op[(I + RA) % (RA + 1)];
     const bool live = (TOK == 64 ? bl : bl + h) < nb;
-    const float dw = live ? half_to_float(odw) : 0.0f, dx = live ? odx : 0.0f;
-    next();
-    rp = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, dx, zero, 0, 0, 0);
-    fold(acc0, pf0, pp, 0, 0, 16);
+    const float dw = live ? half_to_float(o.dw) : 0.0f, dx = live ? o.dx : 0.0f;
+    read.template operator()<RB, RBL>(nx.a0, nx.a1, nx.b0, nx.b1, nx.dw, nx.dx);
+    r.p = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, dx, zero, 0, 0, 0);
+    fold(acc0, pr.f0, pr.p, 0, 0, 16);
     __builtin_amdgcn_sched_barrier(0);
-    rf0 = __builtin_bit_cast(v16f, __builtin_amdgcn_mfma_i32_32x32x32_i8(oa0, ob0, magic, 0, 0, 0));
-    fold(acc_b, pf1, pp, 1, 0, 8);
+    r.f0 = __builtin_bit_cast(v16f, __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a0, o.b0, magic, 0, 0, 0));
+    fold(acc_b, pr.f1, pr.p, 1, 0, 8);
     __builtin_amdgcn_sched_barrier(0);
-    rf1 = __builtin_bit_cast(v16f, __builtin_amdgcn_mfma_i32_32x32x32_i8(TOK == 64 ? oa0 : oa1, ob1, magic, 0, 0, 0));
-    fold(acc_b, pf1, pp, 1, 8, 16);
+    r.f1 = __builtin_bit_cast(v16f, __builtin_amdgcn_mfma_i32_32x32x32_i8(TOK == 64 ? o.a0 : o.a1, o.b1, magic, 0, 0, 0));
+    fold(acc_b, pr.f1, pr.p, 1, 8, 16);
     __builtin_amdgcn_sched_barrier(0);
-    rf0 = __builtin_amdgcn_mfma_f32_16x16x1f32(-kMagicF, 1.0f, rf0, 0, 0, 0);
+    r.f0 = __builtin_amdgcn_mfma_f32_16x16x1f32(-kMagicF, 1.0f, r.f0, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    rf1 = __builtin_amdgcn_mfma_f32_16x16x1f32(-kMagicF, 1.0f, rf1, 0, 0, 0);
+    r.f1 = __builtin_amdgcn_mfma_f32_16x16x1f32(-kMagicF, 1.0f, r.f1, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
-  v4i xa, xa1, xb0, xb1, ya, ya1, yb0, yb1;
-  uint16_t xdw, ydw;  // f16 weight scales as read
-  float xdx, ydx;
-  v16f xf0, xf1, yf0 = {}, yf1 = {};
-  v32f xp, yp = {};
 
-  // Stage s (blocks 4 s .. 4 s + 3) from buffer BUF; on entry X holds block 4 s's operands, Y block 4 s - 1's results.
-  // Between its third and fourth step the next stage is entered: it has landed (at most the NS - 2 after it are
-  // outstanding), every wave is done reading the buffer that stage s + NS will overwrite (this one: its reads were
-  // issued before and are waited for here), and stage s + NS is issued into it.
-  auto stage = [&]<int BUF>(int s) __attribute__((always_inline)) {
-    constexpr int NBUF = (BUF + 1) % NS;
-    constexpr int BPS = KB / 4;  // blocks per step
-    const int j = s * KB;
-    step(xa, xa1, xb0, xb1, xdw, xdx, j, xf0, xf1, xp, yf0, yf1, yp, [&]() __attribute__((always_inline)) {
-      read.template operator()<BUF, 1>(ya, ya1, yb0, yb1, ydw, ydx);
-    });
-    step(ya, ya1, yb0, yb1, ydw, ydx, j + BPS, yf0, yf1, yp, xf0, xf1, xp, [&]() __attribute__((always_inline)) {
-      read.template operator()<BUF, 2>(xa, xa1, xb0, xb1, xdw, xdx);
-    });
-    step(xa, xa1, xb0, xb1, xdw, xdx, j + 2 * BPS, xf0, xf1, xp, yf0, yf1, yp, [&]() __attribute__((always_inline)) {
-      read.template operator()<BUF, 3>(ya, ya1, yb0, yb1, ydw, ydx);
-    });
+  // Stage s (steps of blocks KB s ..) from buffer BUF, the BUF-th stage of a ring cycle. Its step k reads the
+  // operands of step k + RA, which from step 4 - RA on belong to the next stage, so the next stage is entered before
+  // step 4 - RA: it has landed (at most the NS - 2 after it are outstanding), every wave is done reading this buffer
+  // (its last reads were issued in the step before and are waited for here), and stage s + NS is issued into it.
+  auto enter = [&]<int BUF>(int s) __attribute__((always_inline)) {
     if (s + 1 < nstages) {
       __builtin_amdgcn_s_waitcnt(0xC07F);                         // lgkmcnt(0)
       wait_vm_stages<S::loads, NS - 2>(nstages - 2 - s);  // stages s + 2 .. s + NS - 1 may be in flight
       ring_barrier();
       if (s + NS < nstages) issue.template operator()<BUF>(s + NS);
     }
-    step(ya, ya1, yb0, yb1, ydw, ydx, j + 3 * BPS, yf0, yf1, yp, xf0, xf1, xp, [&]() __attribute__((always_inline)) {
-      read.template operator()<NBUF, 0>(xa, xa1, xb0, xb1, xdw, xdx);
-    });
   };
+  auto stage = [&]<int BUF>(int s) __attribute__((always_inline)) {
+    constexpr int NBUF = (BUF + 1) % NS;
+    constexpr int BPS = KB / 4;  // blocks per step
+    const int j = s * KB;
+    [&]<int... K>(std::integer_sequence<int, K...>) __attribute__((always_inline)) {
+      ((K == 4 - RA ? enter.template operator()<BUF>(s) : void(),
+        step.template operator()<4 * BUF + K, (K + RA < 4 ? BUF : NBUF), (K + RA) % 4>(j + K * BPS)),
+       ...);
+    }(std::make_integer_sequence<int, 4>{});
+  };
+  static_assert(RA == 1 || RA == 2, "read-ahead of one or two steps");
+  static_assert((4 * NS) % (RA + 1) == 0, "a ring cycle of 4 NS steps keeps the operand sets (mod RA + 1) and result sets (mod 2) in place");
 
   // Stages 0 .. NS - 2 into buffers 0 .. NS - 2; once stage 0 has landed, stage NS - 1.
   [&]<int... I>(std::integer_sequence<int, I...>) __attribute__((always_inline)) {
@@ -281,15 +286,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   wait_vm_stages<S::loads, NS - 2>(nstages - 1);
   ring_barrier();
   if (NS - 1 < nstages) issue.template operator()<NS - 1>(NS - 1);
-  read.template operator()<0, 0>(xa, xa1, xb0, xb1, xdw, xdx);
-  // Ring cycles, left after the last stage: every stage is four steps, so X and Y are in place at any stage boundary.
+  read.template operator()<0, 0>(op[0].a0, op[0].a1, op[0].b0, op[0].b1, op[0].dw, op[0].dx);
+  if constexpr (RA == 2) read.template operator()<0, 1>(op[1].a0, op[1].a1, op[1].b0, op[1].b1, op[1].dw, op[1].dx);
+  // Ring cycles, left after the last stage: every stage is four steps, so the register sets are in place at any stage
+  // boundary and the last step's results are in rs[1].
   for (int s = 0; s < nstages; s += NS) {
     [&]<int... I>(std::integer_sequence<int, I...>) __attribute__((always_inline)) {
       (void)((s + I < nstages ? (stage.template operator()<I>(s + I), true) : false) && ...);
     }(std::make_integer_sequence<int, NS>{});
   }
-  fold(acc0, yf0, yp, 0, 0, 16);
-  fold(acc_b, yf1, yp, 1, 0, 16);
+  fold(acc0, rs[1].f0, rs[1].p, 0, 0, 16);
+  fold(acc_b, rs[1].f1, rs[1].p, 1, 0, 16);
   // The last stage's loads were waited for (vmcnt(0)) when it was entered; nothing is in flight past the loop.
 
   // Element i of tile j: row 32 w + 8 (i / 4) + 4 h + i % 4, token 32 j + li.
@@ -330,26 +337,26 @@ void gemm_q8_0(hipStream_t s, const void* w, int64_t rows, int64_t cols, const B
   require(gemm_q8_0_supported(rows, cols, n), "gemm_q8_0: rows must be a multiple of 32, n > 8");
   const int n_rt = (int)((rows + kRowsT - 1) / kRowsT);
   const int vec = (reinterpret_cast<uintptr_t>(y) % 16 == 0 && ys % 4 == 0) ? 1 : 0;
-  auto go = [&]<int TOK, int NS>() {
+  auto go = [&]<int TOK, int NS, int RA>() {
     const int n_tt = (n + TOK - 1) / TOK;
     const size_t lds = NS * (size_t)StageLds<TOK>::bytes;
     static bool attr = false;
     if (!attr) {
-      check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_q8_0<TOK, NS>),
+      check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_q8_0<TOK, NS, RA>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
             "hipFuncSetAttribute");
       attr = true;
     }
-    hipLaunchKernelGGL((k_gemm_q8_0<TOK, NS>), dim3((unsigned)((int64_t)n_rt * n_tt)), dim3(kThreads), lds, s,
+    hipLaunchKernelGGL((k_gemm_q8_0<TOK, NS, RA>), dim3((unsigned)((int64_t)n_rt * n_tt)), dim3(kThreads), lds, s,
                        static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0, n_rt, n_tt, vec);
   };
   const int64_t cus = device_cus();
   if ((int64_t)n_rt * ((n + 31) / 32) <= cus)
-    go.template operator()<32, 3>();
+    go.template operator()<32, 3, 1>();
   else if ((int64_t)n_rt * ((n + 63) / 64) <= cus)
-    go.template operator()<64, 6>();
+    go.template operator()<64, 6, 1>();
   else
-    go.template operator()<64, 3>();
+    go.template operator()<64, 3, 2>();
   check_launch("gemm_q8_0");
 }
 

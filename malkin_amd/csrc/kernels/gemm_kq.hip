@@ -104,19 +104,9 @@ __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t 
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wu = __builtin_amdgcn_readfirstlane(w);
-  // Workgroup -> (row tile, token tile), token tiles of a row tile 8 apart (same XCD, rows read once into its L2).
-  int rt, tt;
-  {
-    const int wg = blockIdx.x;
-    if (n_rt % 8 == 0) {
-      const int xcd = wg % 8, j = wg / 8;
-      rt = (j / n_tt) * 8 + xcd;
-      tt = j % n_tt;
-    } else {
-      rt = wg / n_tt;
-      tt = wg % n_tt;
-    }
-  }
+  // Workgroup -> (row tile, token tile): tiles numbered row-major, each XCD a contiguous run of them (token tiles of a
+  // row tile on one XCD, rows read once into its L2).
+  const int tile = xcd_run((int)blockIdx.x, n_rt * n_tt), rt = tile / n_tt, tt = tile % n_tt;
   const int nb = (int)(cols / 32), nsb = (int)(cols / 256);
   const int64_t g0 = (int64_t)rt * (kRowsT / 8);
   const int ngroups = (int)min<int64_t>(kRowsT / 8, rows / 8 - g0);  // 4 .. 16 (rows % 32 == 0)
