@@ -1,9 +1,10 @@
 """Benchmark: the north-star workload of BASELINE.json on one MI355X.
 
 Workload (one "step"): a random-init Qwen3-8B-architecture model in Q8_0 (36 layers, hidden 4096, 32/8 heads,
-head_dim 128, FFN 12288, vocab 151936, untied LM head), ctx 4096, batch 1 — a 512-token prompt evaluated in two
-256-token forwards (the reference engine's kMaxBatch chunks), then greedy decoding to 128 generated tokens (the first
-from the prompt's logits, 127 decode forwards), as `malkin bench` does (main.cpp:126-143).
+head_dim 128, FFN 12288, vocab 151936, untied LM head), ctx 4096, batch 1 — a 512-token prompt evaluated in one
+512-token forward (the reference's engine takes 256 per forward, engine.cpp:381-393; every token's results are the
+same either way), then greedy decoding to 128 generated tokens (the first from the prompt's logits, 127 decode
+forwards), as `malkin bench` does (main.cpp:126-143).
 
 value = (512 + 128) tokens / wall time of the step, inputs (weights, prompt) resident in HBM before the timed region.
 The JSON line also carries pp512 and tg128 rates, the prefill's fraction of the int8 MFMA peak, the live roofline of
@@ -251,13 +252,13 @@ def traffic_probe():
 
 def gemm_probe():
     """Launch sequence for the prefill GEMM's counters (rocprofv3 --pmc): config 1 (Q8_0 9728x2560, n = 512) 8 times,
-    then the Qwen3-8B prompt-chunk shapes of pp512 at n = 256 (q|k|v 6144x4096, attn_output 4096x4096, gate|up
-    24576x4096, down 4096x12288) 4 times each, from BlockQ8 activations."""
+    then the Qwen3-8B shapes of the pp512 forward (q|k|v 6144x4096, attn_output 4096x4096, gate|up 24576x4096, down
+    4096x12288, n = 512) 4 times each, from BlockQ8 activations."""
     import malkin_amd as mk
     ctx = mk.Context(0)
     rng = np.random.default_rng(5)
-    for rows, cols, n, reps in ((9728, 2560, 512, 8), (6144, 4096, 256, 4), (4096, 4096, 256, 4),
-                                (24576, 4096, 256, 4), (4096, 12288, 256, 4)):
+    for rows, cols, n, reps in ((9728, 2560, 512, 8), (6144, 4096, 512, 4), (4096, 4096, 512, 4),
+                                (24576, 4096, 512, 4), (4096, 12288, 512, 4)):
         ws = pack_copies(ctx, mk.Q8_0, random_weight(rng, mk.Q8_0, rows, cols), rows, cols, 1)
         xq, y = random_acts(ctx, rng, n, cols), ctx.alloc(n * rows * 4)
         ctx.sync()
@@ -535,7 +536,7 @@ def main():
                          "(speculative tree verification)")
     ap.add_argument("--probe", choices=["traffic", "gemm", "kquant", "tree"],
                     help="only run a launch sequence for counter profiles: the roofline kernel's HBM traffic, "
-                         "the prefill GEMM (config 1 and the pp512 chunk shapes), config 2's short K-quant batches, "
+                         "the prefill GEMM (config 1 and the pp512 forward's shapes), config 2's short K-quant batches, "
                          "or config 5's tree verification")
     args = ap.parse_args()
     if args.probe == "traffic":

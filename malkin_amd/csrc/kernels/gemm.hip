@@ -16,12 +16,15 @@
 //     +0 and an exact cancellation rounds to +0).
 // That leaves one VALU fma per output and block.
 //
-// A workgroup (4 waves) owns a 128-row x TOK-token tile, 32 rows x TOK tokens per wave, and walks the K dimension
-// in stages of KB blocks held in a ring of NS LDS buffers. TOK = 64: KB = 4 (26 KB per stage); a step is one block,
-// its two int8 MFMAs the two 32-token halves. TOK = 32: KB = 8 (43 KB per stage); a step is two blocks, its two int8
-// MFMAs one block each, and both fold into the one accumulator in block order; the scale-product MFMA's two halves
-// are then the two blocks. TOK = 32 doubles the waves of a grid: it runs where the grid fits the CUs once (the
-// attn_output and down shapes of a 256-token prompt chunk fill half the SIMDs at TOK = 64). A stage holds:
+// A workgroup owns a 128-row x TOK-token tile and walks the K dimension in stages of KB blocks held in a ring of NS
+// LDS buffers; its wave w computes rows 32 (w % 4) .. + 31 and WT tokens of the tile. Three forms:
+//   TOK = WT = 64, 4 waves, KB = 4 (26 KB per stage, 3 stages: two workgroups per CU): a step is one block, its two
+//     int8 MFMAs the two 32-token halves;
+//   TOK = 64, WT = 32, 8 waves, KB = 8 (52 KB per stage, 3 stages: one workgroup per CU, two waves per SIMD): waves
+//     w and w + 4 take the two 32-token halves of the same rows;
+//   TOK = WT = 32, 4 waves, KB = 8 (43 KB per stage, 3 stages): for grids that fit the CUs once at 32 tokens.
+// With WT = 32 a step is two blocks, its two int8 MFMAs one block each, both folding into the one accumulator in
+// block order, and the scale-product MFMA's two halves are then the two blocks. A stage holds:
 //   A  [KB][128 rows][32 B]  the rows' quants (from the CDNA planes of layout.h),
 //   B  [KB][TOK tok][32 B]   the tokens' BlockQ8 quants,
 //   dx [KB][TOK tok]  f32    activation scales,
@@ -30,9 +33,7 @@
 // operand reads (lane l: row l % 32, half l / 32) hit distinct banks. All copies are direct global -> LDS loads
 // (global_load_lds_dwordx4 / _dword: lane i of a wave instruction writes bytes [size * i, size * (i + 1)) after the
 // instruction's LDS base), issued NS - 1 stages ahead, so the data of NS - 1 stages is in flight while a stage is
-// computed and no register holds it on the way. NS by grid size: a TOK = 64 grid that fits the CUs once takes a
-// 6-stage ring (156 KB: one wave per SIMD, nothing else hides the copies' latency); larger grids keep 3 stages and
-// two workgroups per CU; TOK = 32 takes 3 stages (132 KB).
+// computed and no register holds it on the way.
 //
 // Accumulator layout of v_mfma_i32_32x32x32_i8 (checked on gfx950): lane l, element i holds
 //   row 8 * (i / 4) + 4 * (l / 32) + i % 4, column l % 32.
@@ -58,19 +59,27 @@ constexpr int kRowsT = 128;  // workgroup tile rows
 constexpr int kMagic = 0x4B400000;       // bits of 12582912.0f
 constexpr float kMagicF = 12582912.0f;
 
-template <int TOK>
+// Forms: TOK tokens per workgroup tile, WT tokens per wave (64: a step is one block, its two int8 MFMAs the two
+// 32-token halves; 32: a step is two blocks), NW = 4 TOK / WT waves (wave w: rows 32 (w % 4), tokens WT (w / 4) of
+// the tile), KB blocks per stage (four steps).
+template <int TOK, int WT>
 struct StageLds {
-  static constexpr int KB = TOK == 64 ? 4 : 8;         // blocks per stage: four steps either way
+  static constexpr int NW = 4 * TOK / WT;              // waves
+  static constexpr int KB = WT == 64 ? 4 : 8;          // blocks per stage
   static constexpr int a = 0;                          // KB * 128 * 32 bytes
   static constexpr int b = a + KB * kRowsT * 32;       // KB * TOK * 32
   static constexpr int dx = b + KB * TOK * 32;         // KB * TOK floats
   static constexpr int dw = dx + KB * TOK * 4;         // KB * 128 halves
   static constexpr int bytes = dw + KB * kRowsT * 2;
-  // copies per wave and stage: KB A pieces; TOK = 64: B halves 2, dx 1, dw 1 (block w); TOK = 32: B 2, dx 1 (both
+  // A pieces per wave and stage: its row group's 32 rows of blocks w / 4, w / 4 + NW / 4, ...
+  static constexpr int apw = KB * 4 / NW;
+  // copies per wave and stage: apw A pieces; TOK = 64: B halves 2, dx 1, dw 1 (block w); TOK = 32: B 2, dx 1 (both
   // blocks), dw 2 (blocks 2 w, 2 w + 1)
-  static constexpr int loads = TOK == 64 ? KB + 4 : KB + 5;
+  static constexpr int loads = TOK == 64 ? apw + 4 : apw + 5;
 };
-static_assert(StageLds<64>::KB == 4 && StageLds<32>::KB == 8, "one wave copies the B, dx and dw parts of KB / 4 blocks");
+static_assert(StageLds<64, 64>::KB == StageLds<64, 64>::NW && StageLds<64, 32>::KB == StageLds<64, 32>::NW &&
+                  StageLds<32, 32>::KB == 2 * StageLds<32, 32>::NW,
+              "one wave copies the B, dx and dw parts of KB / NW blocks");
 
 // Byte offset of half h (0/1) of row r within a [rows][32 B] operand slab.
 __device__ __forceinline__ int slab_off(int r, int h) { return r * 32 + ((h ^ ((r >> 3) & 1)) << 4); }
@@ -81,22 +90,25 @@ __device__ __forceinline__ void load_lds16(const void* g, uint8_t* l) { lds_copy
 
 __device__ __forceinline__ void load_lds4(const void* g, uint8_t* l) { lds_copy4(g, l); }
 
-// Waves per SIMD: the 3-stage TOK = 64 ring (78 KB) lets two workgroups share a CU, and a wave's MFMAs overlap the
-// VALU work of the other wave on its SIMD far better than its own (the step below: about 185 cycles per step and SIMD
-// with two waves, 334 with one), so that form keeps within 256 registers; the others run one workgroup per CU and
-// keep the register budget of one wave.
+// Waves per SIMD: a wave's MFMAs overlap the VALU work of another wave on its SIMD far better than its own (the step
+// below, alone on a SIMD: 334 cycles; two waves: about 185 cycles per step and SIMD), so the TOK = 64 forms (two
+// four-wave workgroups per CU, or one of eight waves) keep within 256 registers; TOK = 32 runs one wave per SIMD and
+// keeps that wave's register budget.
 // RA: how many steps ahead the operands are read from LDS (two where two waves share a SIMD: each wave then runs
 // about half as fast and the other wave's reads queue in front of its own).
-template <int TOK, int NS>
-constexpr int gemm_waves() { return TOK == 64 && NS == 3 ? 2 : 1; }
-template <int TOK, int NS, int RA>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(gemm_waves<TOK, NS>(), gemm_waves<TOK, NS>()))) void k_gemm_q8_0(
-    const uint8_t* W, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* __restrict__ y, int64_t ys,
-    int accumulate, int n_rt, int n_tt, int vec) {
-  using S = StageLds<TOK>;
+template <int TOK, int WT, int NS>
+constexpr int gemm_waves() { return TOK == 64 ? 2 : 1; }
+template <int TOK, int WT, int NS, int RA>
+__global__ __launch_bounds__((64 * StageLds<TOK, WT>::NW)) __attribute__((amdgpu_waves_per_eu(
+    gemm_waves<TOK, WT, NS>(), gemm_waves<TOK, WT, NS>()))) void k_gemm_q8_0(const uint8_t* W, int64_t rows, int64_t cols,
+                                                                       const BlockQ8* x, int n, float* __restrict__ y,
+                                                                       int64_t ys, int accumulate, int n_rt, int n_tt,
+                                                                       int vec) {
+  using S = StageLds<TOK, WT>;
   constexpr int KB = S::KB;
   extern __shared__ __align__(16) uint8_t smem[];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;  // wave w: rows 32 w .. 32 w + 31 of the tile
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int rg = w & 3, tw = WT * (w >> 2);  // wave w: rows 32 rg .. 32 rg + 31, tokens tw .. tw + WT - 1 of the tile
   // Workgroup -> (row tile, token tile): tiles numbered row-major, each XCD a contiguous run of them, so the token
   // tiles of a row tile share an XCD and its L2 holds the rows once.
   const int tile = xcd_run((int)blockIdx.x, n_rt * n_tt), rt = tile / n_tt, tt = tile % n_tt;
@@ -108,8 +120,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(gemm_w
   const int nstages = (nb + KB - 1) / KB;
 
   // Copy mapping. Loads are never predicated: past the matrix they re-read valid data, unused.
-  //   A: wave w copies its own 32 rows, one 1 KB instruction per block: lane -> row 32 w + lane / 2, physical half
-  //      lane % 2 (logical half (lane % 2) ^ ((lane / 16) & 1)), 16 bytes of plane h of the row's group unit.
+  //   A: wave w copies the 32 rows of its row group rg, one 1 KB instruction per block (blocks w / 4 + k NW / 4):
+  //      lane -> row 32 rg + lane / 2, physical half lane % 2 (logical half (lane % 2) ^ ((lane / 16) & 1)), 16 bytes
+  //      of plane h of the row's group unit.
   //   B: TOK = 64: wave w copies block w, tokens 32 c + lane / 2 for c = 0, 1; TOK = 32: blocks 2 w and 2 w + 1,
   //      tokens lane / 2; the same half mapping, 16 qs bytes.
   //   dx: TOK = 64: block w, lane -> token lane; TOK = 32: lane -> block 2 w + lane / 32, token lane % 32.
@@ -117,7 +130,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(gemm_w
   //       group's 16-byte entry).
   // Addresses are a wave-uniform base that moves with the block plus a fixed 32-bit per-lane offset (the TOK = 32 dx
   // copy: its block, too, is per lane).
-  const int a_row = 32 * w + (lane >> 1);
+  const int a_row = 32 * rg + (lane >> 1);
   const int a_gi = min(a_row >> 3, ngroups - 1);
   const int half_sw = (lane & 1) ^ ((lane >> 4) & 1);
   const uint32_t a_off = (uint32_t)(a_gi * nb * 256 + (half_sw << 7) + (a_row & 7) * 16);
@@ -129,66 +142,80 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(gemm_w
   const uint8_t* x_base = reinterpret_cast<const uint8_t*>(x + (int64_t)t0 * nb);
   const uint8_t* dw_base = W + L.scales(g0, 0);
   const int wu = __builtin_amdgcn_readfirstlane(w);
-  // Stage sn into LDS buffer BUF.
-  auto issue = [&]<int BUF>(int sn) __attribute__((always_inline)) {
+  // Copy I of stage sn into LDS buffer BUF; a stage is S::loads copies per wave: apw A pieces, then TOK = 64: B
+  // halves 0 and 1, dx, dw; TOK = 32: B of blocks 2 w and 2 w + 1, dx, dw of blocks 2 w and 2 w + 1.
+  const int wblk = wu >> 2, wrg = wu & 3;
+  auto copy = [&]<int BUF, int I>(int sn) __attribute__((always_inline)) {
     uint8_t* st = smem + BUF * S::bytes;
     const int b0 = sn * KB;
-#pragma unroll
-    for (int k = 0; k < KB; ++k)
-      load_lds16(a_base + (size_t)min(b0 + k, nb - 1) * 256 + a_off, st + S::a + k * kRowsT * 32 + wu * 1024);
-    if constexpr (TOK == 64) {
+    if constexpr (I < S::apw) {
+      const int blk = wblk + I * (S::NW / 4);
+      load_lds16(a_base + (size_t)min(b0 + blk, nb - 1) * 256 + a_off, st + S::a + blk * kRowsT * 32 + wrg * 1024);
+    } else if constexpr (TOK == 64) {
+      constexpr int J = I - S::apw;
       const int b = min(b0 + wu, nb - 1);
-      load_lds16(x_base + (size_t)b * 40 + b_off0, st + S::b + wu * TOK * 32);
-      load_lds16(x_base + (size_t)b * 40 + b_off1, st + S::b + wu * TOK * 32 + 32 * 32);
-      load_lds4(x_base + (size_t)b * 40 + dx_off, st + S::dx + wu * TOK * 4);
-      load_lds4(dw_base + (size_t)b * 16 + dw_off, st + S::dw + wu * kRowsT * 2);
+      if constexpr (J == 0)
+        load_lds16(x_base + (size_t)b * 40 + b_off0, st + S::b + wu * TOK * 32);
+      else if constexpr (J == 1)
+        load_lds16(x_base + (size_t)b * 40 + b_off1, st + S::b + wu * TOK * 32 + 32 * 32);
+      else if constexpr (J == 2)
+        load_lds4(x_base + (size_t)b * 40 + dx_off, st + S::dx + wu * TOK * 4);
+      else
+        load_lds4(dw_base + (size_t)b * 16 + dw_off, st + S::dw + wu * kRowsT * 2);
     } else {
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int b = min(b0 + 2 * wu + e, nb - 1);
-        load_lds16(x_base + (size_t)b * 40 + b_off0, st + S::b + (2 * wu + e) * TOK * 32);
-      }
-      const int bl = min(b0 + 2 * wu + (lane >> 5), nb - 1);  // per lane
-      load_lds4(x_base + (size_t)bl * 40 + dx_off, st + S::dx + 2 * wu * TOK * 4);
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int b = min(b0 + 2 * wu + e, nb - 1);
-        load_lds4(dw_base + (size_t)b * 16 + dw_off, st + S::dw + (2 * wu + e) * kRowsT * 2);
+      constexpr int J = I - S::apw;
+      if constexpr (J < 2) {
+        const int b = min(b0 + 2 * wu + J, nb - 1);
+        load_lds16(x_base + (size_t)b * 40 + b_off0, st + S::b + (2 * wu + J) * TOK * 32);
+      } else if constexpr (J == 2) {
+        const int bl = min(b0 + 2 * wu + (lane >> 5), nb - 1);  // per lane
+        load_lds4(x_base + (size_t)bl * 40 + dx_off, st + S::dx + 2 * wu * TOK * 4);
+      } else {
+        const int b = min(b0 + 2 * wu + J - 3, nb - 1);
+        load_lds4(dw_base + (size_t)b * 16 + dw_off, st + S::dw + (2 * wu + J - 3) * kRowsT * 2);
       }
     }
   };
+  // Copies I0 .. I1 - 1 of stage sn into buffer BUF.
+  auto copies = [&]<int BUF, int I0, int I1>(int sn) __attribute__((always_inline)) {
+    [&]<int... I>(std::integer_sequence<int, I...>) __attribute__((always_inline)) {
+      (copy.template operator()<BUF, I0 + I>(sn), ...);
+    }(std::make_integer_sequence<int, I1 - I0>{});
+  };
+  static_assert(S::loads == (TOK == 64 ? S::apw + 4 : S::apw + 5), "copies per wave and stage");
+  // A whole stage (the ring's first fills).
+  auto issue = [&]<int BUF>(int sn) __attribute__((always_inline)) { copies.template operator()<BUF, 0, S::loads>(sn); };
 
-  v16f acc0 = {}, acc1 = {};  // TOK = 64: tokens 0..31, 32..63; TOK = 32: acc0 only
+  v16f acc0 = {}, acc1 = {};  // WT = 64: tokens 0..31, 32..63; WT = 32: acc0 only
   v16i magic;
 #pragma unroll
   for (int i = 0; i < 16; ++i) magic[i] = kMagic;
   asm volatile("" : "+v"(magic));  // keep it in VGPRs: as a uniform value it would be copied from SGPRs per MFMA
   const v32f zero = {};
   const int li = lane & 31, h = lane >> 5;
-  const int arow = 32 * w + li;
-  // LDS byte offsets of this lane's operands within a stage buffer, block 0. The scale product's operands: TOK = 64,
-  // lane l: dw of row arow, dx of token l; TOK = 32, lane l: block h (of the step's two): dw of row arow, dx of token
-  // li.
-  const int off_a = S::a + slab_off(arow, h), off_b0 = S::b + slab_off(li, h), off_b1 = S::b + slab_off(32 + li, h),
-            off_dw = S::dw + 2 * arow + (TOK == 64 ? 0 : h * kRowsT * 2),
-            off_dx = S::dx + (TOK == 64 ? 4 * lane : 4 * li + h * TOK * 4);
+  const int arow = 32 * rg + li;
+  // LDS byte offsets of this lane's operands within a stage buffer, block 0. The scale product's operands: WT = 64,
+  // lane l: dw of row arow, dx of token l; WT = 32, lane l: block h (of the step's two): dw of row arow, dx of token
+  // tw + li.
+  const int off_a = S::a + slab_off(arow, h), off_b0 = S::b + slab_off(tw + li, h),
+            off_b1 = S::b + slab_off(tw + 32 + li, h), off_dw = S::dw + 2 * arow + (WT == 64 ? 0 : h * kRowsT * 2),
+            off_dx = S::dx + (WT == 64 ? 4 * lane : 4 * (tw + li) + h * TOK * 4);
 
   // Software pipeline over blocks j = 0, 1, ..., RA + 1 operand register sets and two result sets. Step j:
   //   read the operands of block j + RA (RA steps of LDS latency hidden),
   //   MFMAs of block j (scale products, int8 dots, their conversions; operands read in step j - RA),
   //   fmas of block j - 1, interleaved with those MFMAs.
-  // A wave issues one instruction every few cycles, in order, and one wave per SIMD is the common case here, so the
-  // overlap of matrix and vector work has to be in the instruction stream itself, and the stream has to be short:
-  // each MFMA is followed by about as many VALU instructions as cover its time in the matrix pipe, and the loop is
-  // unrolled over the whole LDS ring (NS stages of KB blocks) so every LDS offset is an immediate. Blocks past the
+  // A wave issues its instructions in order, so each MFMA is followed by about as many VALU instructions as cover its
+  // time in the matrix pipe (the other wave on the SIMD fills what is left), and the loop is unrolled over the whole
+  // LDS ring (NS stages of KB blocks) so every LDS offset is an immediate. Blocks past the
   // end (nb % KB != 0) read a copy of the last block with dw = dx = 0: their products are 0 and fma(f, 0, acc) ==
   // acc (the chain never holds -0), so they add nothing. The results of "block -1" start at zero for the same reason.
-  // Operands of step BL of a stage: TOK = 64, block BL (ra1 unused); TOK = 32, blocks 2 BL (ra0, rb0) and 2 BL + 1
+  // Operands of step BL of a stage: WT = 64, block BL (ra1 unused); WT = 32, blocks 2 BL (ra0, rb0) and 2 BL + 1
   // (ra1, rb1).
   auto read = [&]<int BUF, int BL>(v4i& ra0, v4i& ra1, v4i& rb0, v4i& rb1, uint16_t& rdw, float& rdx)
       __attribute__((always_inline)) {
     const uint8_t* st = smem + BUF * S::bytes;
-    if constexpr (TOK == 64) {
+    if constexpr (WT == 64) {
       ra0 = *reinterpret_cast<const v4i*>(st + off_a + BL * kRowsT * 32);
       rb0 = *reinterpret_cast<const v4i*>(st + off_b0 + BL * TOK * 32);
       rb1 = *reinterpret_cast<const v4i*>(st + off_b1 + BL * TOK * 32);
@@ -230,13 +257,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(gemm_w
   rs[1].f0 = {};
   rs[1].f1 = {};
   rs[1].p = {};
-  v16f& acc_b = TOK == 64 ? acc1 : acc0;  // the second MFMA's accumulator
+  v16f& acc_b = WT == 64 ? acc1 : acc0;  // the second MFMA's accumulator
   auto step = [&]<int I, int RB, int RBL>(int bl) __attribute__((always_inline)) {
     const Ops& o = op[I % (RA + 1)];
     Res& r = rs[I % 2];
     const Res& pr = rs[1 - I % 2];
     Ops& nx = op[(I + RA) % (RA + 1)];
-    const bool live = (TOK == 64 ? bl : bl + h) < nb;
+    const bool live = (WT == 64 ? bl : bl + h) < nb;
     const float dw = live ? half_to_float(o.dw) : 0.0f, dx = live ? o.dx : 0.0f;
     read.template operator()<RB, RBL>(nx.a0, nx.a1, nx.b0, nx.b1, nx.dw, nx.dx);
     r.p = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, dx, zero, 0, 0, 0);
@@ -245,7 +272,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(gemm_w
     r.f0 = __builtin_bit_cast(v16f, __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a0, o.b0, magic, 0, 0, 0));
     fold(acc_b, pr.f1, pr.p, 1, 0, 8);
     __builtin_amdgcn_sched_barrier(0);
-    r.f1 = __builtin_bit_cast(v16f, __builtin_amdgcn_mfma_i32_32x32x32_i8(TOK == 64 ? o.a0 : o.a1, o.b1, magic, 0, 0, 0));
+    r.f1 = __builtin_bit_cast(v16f, __builtin_amdgcn_mfma_i32_32x32x32_i8(WT == 64 ? o.a0 : o.a1, o.b1, magic, 0, 0, 0));
     fold(acc_b, pr.f1, pr.p, 1, 8, 16);
     __builtin_amdgcn_sched_barrier(0);
     r.f0 = __builtin_amdgcn_mfma_f32_16x16x1f32(-kMagicF, 1.0f, r.f0, 0, 0, 0);
@@ -256,22 +283,30 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(gemm_w
 
   // Stage s (steps of blocks KB s ..) from buffer BUF, the BUF-th stage of a ring cycle. Its step k reads the
   // operands of step k + RA, which from step 4 - RA on belong to the next stage, so the next stage is entered before
-  // step 4 - RA: it has landed (at most the NS - 2 after it are outstanding), every wave is done reading this buffer
-  // (its last reads were issued in the step before and are waited for here), and stage s + NS is issued into it.
-  auto enter = [&]<int BUF>(int s) __attribute__((always_inline)) {
+  // step 4 - RA: it has landed (at most the NS - 2 after it are outstanding) and every wave is done reading this buffer
+  // (its last reads were issued in the step before and are waited for here). Stage s + NS then goes into this buffer,
+  // a quarter of its copies at the start of each of the four steps that follow: a CU's texture unit takes a 1 KB copy
+  // in about 16 cycles, and all of them issued at the entry queued each wave behind the others' (about 80 cycles per
+  // copy and wave). All of stage s + NS is issued before the next entry, which counts it as in flight.
+  auto enter = [&](int s) __attribute__((always_inline)) {
     if (s + 1 < nstages) {
       __builtin_amdgcn_s_waitcnt(0xC07F);                         // lgkmcnt(0)
       wait_vm_stages<S::loads, NS - 2>(nstages - 2 - s);  // stages s + 2 .. s + NS - 1 may be in flight
       ring_barrier();
-      if (s + NS < nstages) issue.template operator()<BUF>(s + NS);
     }
   };
+  // Quarter P of stage t's copies into buffer BUF.
+  auto quarter = [&]<int BUF, int P>(int t) __attribute__((always_inline)) {
+    if (t < nstages) copies.template operator()<BUF, P * S::loads / 4, (P + 1) * S::loads / 4>(t);
+  };
   auto stage = [&]<int BUF>(int s) __attribute__((always_inline)) {
-    constexpr int NBUF = (BUF + 1) % NS;
+    constexpr int NBUF = (BUF + 1) % NS, PBUF = (BUF + NS - 1) % NS;
     constexpr int BPS = KB / 4;  // blocks per step
     const int j = s * KB;
     [&]<int... K>(std::integer_sequence<int, K...>) __attribute__((always_inline)) {
-      ((K == 4 - RA ? enter.template operator()<BUF>(s) : void(),
+      (((K == 4 - RA) ? enter(s) : void(),
+        (K >= 4 - RA) ? quarter.template operator()<BUF, (K + RA) % 4>(s + NS)
+                      : (s >= 1 ? quarter.template operator()<PBUF, (K + RA) % 4>(s - 1 + NS) : void()),
         step.template operator()<4 * BUF + K, (K + RA < 4 ? BUF : NBUF), (K + RA) % 4>(j + K * BPS)),
        ...);
     }(std::make_integer_sequence<int, 4>{});
@@ -299,12 +334,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(gemm_w
   fold(acc_b, rs[1].f1, rs[1].p, 1, 0, 16);
   // The last stage's loads were waited for (vmcnt(0)) when it was entered; nothing is in flight past the loop.
 
-  // Element i of tile j: row 32 w + 8 (i / 4) + 4 h + i % 4, token 32 j + li.
-  if (32 * w < 8 * ngroups) {
-    float* yr = y + (int64_t)rt * kRowsT + 32 * w + 4 * h;
+  // Element i of tile j: row 32 rg + 8 (i / 4) + 4 h + i % 4, token tw + 32 j + li.
+  if (32 * rg < 8 * ngroups) {
+    float* yr = y + (int64_t)rt * kRowsT + 32 * rg + 4 * h;
 #pragma unroll
-    for (int j = 0; j < TOK / 32; ++j) {
-      const int t = t0 + 32 * j + li;
+    for (int j = 0; j < WT / 32; ++j) {
+      const int t = t0 + tw + 32 * j + li;
       if (t >= n) continue;
       float* yt = yr + (int64_t)t * ys;
 #pragma unroll
@@ -337,26 +372,33 @@ void gemm_q8_0(hipStream_t s, const void* w, int64_t rows, int64_t cols, const B
   require(gemm_q8_0_supported(rows, cols, n), "gemm_q8_0: rows must be a multiple of 32, n > 8");
   const int n_rt = (int)((rows + kRowsT - 1) / kRowsT);
   const int vec = (reinterpret_cast<uintptr_t>(y) % 16 == 0 && ys % 4 == 0) ? 1 : 0;
-  auto go = [&]<int TOK, int NS, int RA>() {
+  auto go = [&]<int TOK, int WT, int NS, int RA>() {
+    using S = StageLds<TOK, WT>;
     const int n_tt = (n + TOK - 1) / TOK;
-    const size_t lds = NS * (size_t)StageLds<TOK>::bytes;
+    const size_t lds = NS * (size_t)S::bytes;
     static bool attr = false;
     if (!attr) {
-      check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_q8_0<TOK, NS, RA>),
+      check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_q8_0<TOK, WT, NS, RA>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
             "hipFuncSetAttribute");
       attr = true;
     }
-    hipLaunchKernelGGL((k_gemm_q8_0<TOK, NS, RA>), dim3((unsigned)((int64_t)n_rt * n_tt)), dim3(kThreads), lds, s,
-                       static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0, n_rt, n_tt, vec);
+    hipLaunchKernelGGL((k_gemm_q8_0<TOK, WT, NS, RA>), dim3((unsigned)((int64_t)n_rt * n_tt)), dim3(64 * S::NW), lds,
+                       s, static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0, n_rt, n_tt, vec);
   };
+  // Forms by grid size, measured on MI355X (bench.py --probe gemm shapes; every form bit-identical): a grid that fits
+  // the CUs once at 32-token tiles takes them (4096 x 4096 at 256 tokens: 23.8 us against 29.7 with eight waves); one
+  // that fits once at 64-token tiles takes the eight-wave form, two waves per SIMD in one workgroup (4096 x 4096 at 512
+  // tokens 40.5 -> 34.0 us, 4096 x 12288 103.1 -> 85.2, 6144 x 4096 at 256 tokens 38.8 -> 32.0, against the
+  // four-wave 6-stage ring); larger grids take two four-wave workgroups per CU (config 1: 60.0 us against 63.1 with
+  // eight waves, gate|up 24576 x 4096 at 512 tokens 170.6 against 187.6).
   const int64_t cus = device_cus();
   if ((int64_t)n_rt * ((n + 31) / 32) <= cus)
-    go.template operator()<32, 3, 1>();
+    go.template operator()<32, 32, 3, 1>();
   else if ((int64_t)n_rt * ((n + 63) / 64) <= cus)
-    go.template operator()<64, 6, 1>();
+    go.template operator()<64, 32, 3, 2>();
   else
-    go.template operator()<64, 3, 2>();
+    go.template operator()<64, 64, 3, 2>();
   check_launch("gemm_q8_0");
 }
 
