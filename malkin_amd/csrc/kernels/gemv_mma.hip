@@ -439,6 +439,9 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
   // elements i: tokens 4 c + i (+ 16 m). Chain role: row cr = tid % 16, tokens ct + CT m (those below 16 NTT).
   const int r = lane & 15, c = lane >> 4, gi = r >> 3, rr = r & 7;
   const int cr = tid & 15, ct = tid >> 4;
+  // Result element i of the second token tile holds tokens 16 + 4 c + i: elements i >= ntok - 16 are padding in every
+  // lane, and their terms are neither formed nor read (17 tokens, the tree verification batch: only i = 0).
+  const int lim1 = min(4, ntok - 16);
   float acc[CPT];
 #pragma unroll
   for (int m = 0; m < CPT; ++m) acc[m] = 0.0f;
@@ -480,6 +483,7 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
     for (int m = 0; m < CPT; ++m) {
       const int tk = ct + CT * m;
       if (CT * CPT > 16 * NTT && tk >= 16 * NTT) break;  // wave-uniform: threads past the tile's tokens
+      if (tk >= ntok) break;                              // padding token: its output is never stored
       float xsv[kUnits];
       if constexpr (TYPE == kQ4_K) {
 #pragma unroll
@@ -526,7 +530,8 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
           const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
           const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero4, 0, 0, 0);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) put(u, 16 * m + 4 * c + i, {(float)d[i], dw * dx[i]});
+          for (int i = 0; i < 4; ++i)
+            if (m == 0 || i < lim1) put(u, 16 * m + 4 * c + i, {(float)d[i], dw * dx[i]});
         }
       }
     } else if constexpr (TYPE == kQ6_K) {
@@ -554,6 +559,7 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
           const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, zero4, 0, 0, 0);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
+            if (m > 0 && i >= lim1) continue;
             if constexpr (WIDE)
               put(u, 16 * m + 4 * c + i, {fma_((float)d1[i], dsc1, (float)d0[i] * dsc0), dx[i]});
             else
@@ -596,7 +602,8 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
           const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
           const v4i dq = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq, zero4, 0, 0, 0);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) put(u, 16 * m + 4 * c + i, {(float)dq[i], fsc * dx[i]});
+          for (int i = 0; i < 4; ++i)
+            if (m == 0 || i < lim1) put(u, 16 * m + 4 * c + i, {(float)dq[i], fsc * dx[i]});
         }
       }
     }
