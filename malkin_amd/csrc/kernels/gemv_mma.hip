@@ -344,10 +344,16 @@ struct KsLds {
 };
 
 // KW waves per workgroup (4 or 8): each wave computes the dots and terms of 8 / KW of a stage's 8 units.
-template <int TYPE, bool WIDE, int NTT, int NS, int KW>
+// PAIR (at most 8 tokens, one token tile): a wave takes its units two at a time in one 16 x 16 MFMA tile, unit u's
+// tokens in the tile's token rows 0..7 and unit u + 1's in rows 8..15. The first MFMA has unit u's activations in rows
+// 0..7 (zero elsewhere) against unit u's weights, the second accumulates unit u + 1's activations in rows 8..15
+// against unit u + 1's weights, so result element i of lane quarter c is (unit u + c / 2, token 4 (c % 2) + i):
+// exact int dots of both units, and no epilogue work for padding token columns.
+template <int TYPE, bool WIDE, int NTT, int NS, int KW, bool PAIR>
 __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t rows, int64_t cols, const BlockQ8* x,
                                                      int n, float* __restrict__ y, int64_t ys, int accumulate) {
   using S = KsLds<TYPE, WIDE, NTT, KW>;
+  static_assert(!PAIR || (NTT == 1 && kUnits / KW % 2 == 0), "pairs: one token tile, an even number of units per wave");
   constexpr int E = Ks<TYPE, WIDE>::E;
   constexpr int UPW = kUnits / KW;                  // units per wave and stage
   constexpr int CT = 4 * KW;                        // token rows of the chain threads (16 rows x CT tokens)
@@ -517,7 +523,113 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
     if (s + NS - 1 < nst) issue.template operator()<(BUF + NS - 1) % NS>(s + NS - 1);
     const uint8_t* st = smem + BUF * S::bytes;
     select(s);
-    if constexpr (TYPE == kQ8_0) {
+    if constexpr (PAIR) {
+      // Lane (r, c): MFMA operand rows r (token r % 8 of unit u, or of u + 1), result unit u + ph, tokens 4 pt + i.
+      const int ph = c >> 1, pt = c & 1;
+      const bool lo = r < 8;
+      auto xa = [&](int u) __attribute__((always_inline)) {  // operand bytes of token r % 8 of unit u
+        return *reinterpret_cast<const long*>(st + S::x + (u * 16 + (r & 7)) * 32 + 8 * c);
+      };
+      auto dxs = [&](int u0) __attribute__((always_inline)) {  // dx of this lane's result tokens
+        return *reinterpret_cast<const float4*>(st + S::dx + ((u0 + ph) * 16 + 4 * pt) * 4);
+      };
+      if constexpr (TYPE == kQ8_0) {
+#pragma unroll
+        for (int k = 0; k < UPW; k += 2) {
+          const int u0 = UPW * wu + k;
+          long bw[2];
+          float dw[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            bw[e] = *reinterpret_cast<const long*>(st + gi * 2048 + (u0 + e) * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
+            dw[e] = half_to_float(*reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + (u0 + e) * 16 + rr * 2));
+          }
+          const long a0 = lo ? xa(u0) : 0, a1 = lo ? 0 : xa(u0 + 1);
+          const float4 dx4 = dxs(u0);
+          const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+          const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bw[1], __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bw[0], zero4, 0, 0, 0), 0, 0, 0);
+          const float dwl = ph ? dw[1] : dw[0];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) put(u0 + ph, 4 * pt + i, {(float)d[i], dwl * dx[i]});
+        }
+      } else if constexpr (TYPE == kQ6_K) {
+        const float dd = half_to_float(*reinterpret_cast<const uint16_t*>(st + S::d_off + gi * 16 + rr * 2));
+        const int hw = c >> 1, h = c & 1;
+#pragma unroll
+        for (int k = 0; k < UPW; k += 2) {
+          const int u0 = UPW * wu + k;
+          long bl[2], bh[2];
+          float s0[2], s1[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const uint8_t* au = st + gi * 1536 + (u0 + e) * 192;
+            const uint2 nib = *reinterpret_cast<const uint2*>(au + rr * 16 + 8 * h);
+            const uint2 hb = *reinterpret_cast<const uint2*>(au + 128 + rr * 8);
+            const uint32_t hv = (hw ? hb.y : hb.x) >> (4 * h);
+            const uint32_t q0 = ((nib.x >> (4 * hw)) & 0x0F0F0F0Fu) | ((hv & 0x03030303u) << 4);
+            const uint32_t q1 = ((nib.y >> (4 * hw)) & 0x0F0F0F0Fu) | (((hv >> 2) & 0x03030303u) << 4);
+            const long bq = (long)(((uint64_t)minus32(q1) << 32) | minus32(q0));
+            bl[e] = hw ? 0 : bq;
+            bh[e] = hw ? bq : 0;
+            const uint32_t scw = *reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + rr * 16 + 2 * (u0 + e));
+            s0[e] = dd * (float)(int8_t)(scw & 0xFF);
+            s1[e] = dd * (float)(int8_t)(scw >> 8);
+          }
+          const long a0 = lo ? xa(u0) : 0, a1 = lo ? 0 : xa(u0 + 1);
+          const float4 dx4 = dxs(u0);
+          const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+          const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bl[1], __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bl[0], zero4, 0, 0, 0), 0, 0, 0);
+          const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bh[1], __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bh[0], zero4, 0, 0, 0), 0, 0, 0);
+          const float dsc0 = ph ? s0[1] : s0[0], dsc1 = ph ? s1[1] : s1[0];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if constexpr (WIDE)
+              put(u0 + ph, 4 * pt + i, {fma_((float)d1[i], dsc1, (float)d0[i] * dsc0), dx[i]});
+            else
+              put(u0 + ph, 4 * pt + i, {(float)d0[i], dsc0 * dx[i], (float)d1[i], dsc1 * dx[i]});
+          }
+        }
+      } else {  // Q4_K: the wave's pairs are whole 64-weight chunks (even unit: low nibbles, odd: high)
+        {  // dx (s0 + s1) of the wave's units' tokens, once per (unit, token)
+#pragma unroll
+          for (int k = 0; k < (UPW * 16 + 63) / 64; ++k) {
+            const int idx = lane + 64 * k;
+            if (idx < UPW * 16) {
+              const int u = UPW * wu + idx / 16, tok = idx % 16;
+              const int at = u * 16 + tok;
+              const uint32_t sx = *reinterpret_cast<const uint32_t*>(st + S::xs + at * 4);
+              const float dxv = *reinterpret_cast<const float*>(st + S::dx + at * 4);
+              xs_t[tok * kUnits + u] = dxv * (float)((int)(int16_t)(sx & 0xFFFF) + (int)(int16_t)(sx >> 16));
+            }
+          }
+        }
+        const uint4 hd = *reinterpret_cast<const uint4*>(st + S::s_off + gi * 128 + rr * 16);
+        const float d = half_to_float((uint16_t)(hd.x & 0xFFFF)), dmin = half_to_float((uint16_t)(hd.x >> 16));
+#pragma unroll
+        for (int k = 0; k < UPW; k += 2) {
+          const int u0 = UPW * wu + k, j2 = u0 / 2;
+          const uint2 raw =
+              *reinterpret_cast<const uint2*>(st + gi * 1024 + j2 * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
+          long bq[2];
+          float fsc[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            bq[e] = (long)(((uint64_t)((raw.y >> (4 * e)) & 0x0F0F0F0Fu) << 32) | ((raw.x >> (4 * e)) & 0x0F0F0F0Fu));
+            int sc, mn;
+            scale_min(u0 + e, hd.y, hd.z, hd.w, sc, mn);
+            fsc[e] = d * (float)sc;
+            if (c == 0) nmn_t[r * kUnits + u0 + e] = -(dmin * (float)mn);
+          }
+          const long a0 = lo ? xa(u0) : 0, a1 = lo ? 0 : xa(u0 + 1);
+          const float4 dx4 = dxs(u0);
+          const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+          const v4i dq = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bq[1], __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bq[0], zero4, 0, 0, 0), 0, 0, 0);
+          const float fs = ph ? fsc[1] : fsc[0];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) put(u0 + ph, 4 * pt + i, {(float)dq[i], fs * dx[i]});
+        }
+      }
+    } else if constexpr (TYPE == kQ8_0) {
 #pragma unroll
       for (int k = 0; k < UPW; ++k) {
         const int u = UPW * wu + k;
@@ -646,20 +758,20 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
   }
 }
 
-template <int TYPE, bool WIDE, int NTT, int NS, int KW>
+template <int TYPE, bool WIDE, int NTT, int NS, int KW, bool PAIR>
 void launch_ks_ns(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
                   int64_t ys, bool accumulate) {
   using S = KsLds<TYPE, WIDE, NTT, KW>;
   const size_t lds = NS * (size_t)S::bytes + S::terms;
   static bool attr = false;
   if (!attr) {
-    check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_mmv_ks<TYPE, WIDE, NTT, NS, KW>),
+    check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_mmv_ks<TYPE, WIDE, NTT, NS, KW, PAIR>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
           "hipFuncSetAttribute");
     attr = true;
   }
   const int tiles = (n + 16 * NTT - 1) / (16 * NTT);
-  hipLaunchKernelGGL((k_mmv_ks<TYPE, WIDE, NTT, NS, KW>), dim3((unsigned)(rows / 16), (unsigned)tiles), dim3(64 * KW),
+  hipLaunchKernelGGL((k_mmv_ks<TYPE, WIDE, NTT, NS, KW, PAIR>), dim3((unsigned)(rows / 16), (unsigned)tiles), dim3(64 * KW),
                      lds, s, static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0);
 }
 
@@ -667,15 +779,15 @@ void launch_ks_ns(hipStream_t s, const void* w, int64_t rows, int64_t cols, cons
 // tiles (17-32 tokens: Qwen3-14B Q6_K at 17 tokens, 5120 x 17408 95.4 -> 86.3 us, 5120 x 5120 30.1 -> 27.4 us) and
 // for Q8_0 (4096 x 12288 at 8 tokens 26.4 -> 24.5 us); four for one K-quant token tile (Q4_K 5120 x 17408 at 8
 // tokens: 63.6 vs 74.4 us with eight).
-template <int TYPE, int NTT>
-constexpr int ks_waves() { return NTT == 2 || TYPE == kQ8_0 ? 8 : 4; }
+template <int TYPE, int NTT, bool PAIR>
+constexpr int ks_waves() { return PAIR ? 4 : NTT == 2 || TYPE == kQ8_0 ? 8 : 4; }
 
 // Ring depth: the deepest ring that fits one workgroup per CU when the grid fits the GPU once, else one that lets
 // two workgroups share a CU (80 KB each).
-template <int TYPE, bool WIDE, int NTT>
+template <int TYPE, bool WIDE, int NTT, bool PAIR>
 void launch_ks_ntt(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
                    int64_t ys, bool accumulate) {
-  constexpr int KW = ks_waves<TYPE, NTT>();
+  constexpr int KW = ks_waves<TYPE, NTT, PAIR>();
   using S = KsLds<TYPE, WIDE, NTT, KW>;
   const int64_t wgs = rows / 16 * ((n + 16 * NTT - 1) / (16 * NTT)), cus = device_cus();
   constexpr int kDeep = (150 * 1024 - S::terms) / S::bytes >= 8 ? 8 : (150 * 1024 - S::terms) / S::bytes;
@@ -683,20 +795,22 @@ void launch_ks_ntt(hipStream_t s, const void* w, int64_t rows, int64_t cols, con
   static_assert(kDeep >= 3, "the K-split ring needs three stages");
   if constexpr (kTwo >= 3) {
     if (wgs > cus) {
-      launch_ks_ns<TYPE, WIDE, NTT, (kTwo > 6 ? 6 : kTwo), KW>(s, w, rows, cols, x, n, y, ys, accumulate);
+      launch_ks_ns<TYPE, WIDE, NTT, (kTwo > 6 ? 6 : kTwo), KW, PAIR>(s, w, rows, cols, x, n, y, ys, accumulate);
       return;
     }
   }
-  launch_ks_ns<TYPE, WIDE, NTT, kDeep, KW>(s, w, rows, cols, x, n, y, ys, accumulate);
+  launch_ks_ns<TYPE, WIDE, NTT, kDeep, KW, PAIR>(s, w, rows, cols, x, n, y, ys, accumulate);
 }
 
 template <int TYPE, bool WIDE>
 void launch_ks(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
                int64_t ys, bool accumulate) {
-  if (n <= 16)
-    launch_ks_ntt<TYPE, WIDE, 1>(s, w, rows, cols, x, n, y, ys, accumulate);
+  if (n <= 8)
+    launch_ks_ntt<TYPE, WIDE, 1, true>(s, w, rows, cols, x, n, y, ys, accumulate);
+  else if (n <= 16)
+    launch_ks_ntt<TYPE, WIDE, 1, false>(s, w, rows, cols, x, n, y, ys, accumulate);
   else
-    launch_ks_ntt<TYPE, WIDE, 2>(s, w, rows, cols, x, n, y, ys, accumulate);
+    launch_ks_ntt<TYPE, WIDE, 2, false>(s, w, rows, cols, x, n, y, ys, accumulate);
 }
 
 template <int TYPE, bool WIDE, int NTT, int NS>
