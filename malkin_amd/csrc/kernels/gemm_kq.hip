@@ -96,7 +96,10 @@ __device__ __forceinline__ void scale_min(int j, uint32_t q0, uint32_t q1, uint3
 
 // NS: stages in the LDS ring, NS - 1 of them in flight. 3 when the grid takes several workgroups per CU (prefill);
 // deeper rings when few row tiles cover the matrix (short batches), where the stream is latency-bound otherwise.
-template <int TYPE, bool WIDE, int NS>
+// NE: accumulator elements with a live token. Element i holds tokens 8 (i / 4) + i % 4 and 8 (i / 4) + 4 + i % 4 of
+// the tile, so for a batch of at most 17 tokens (config 5's tree verification) elements 9..15 hold only padding
+// tokens in every lane: NE = 9 skips their epilogue (their MFMA results are computed and dropped).
+template <int TYPE, bool WIDE, int NS, int NE>
 __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t rows, int64_t cols,
                                                       const BlockQ8* x, int n, float* __restrict__ y, int64_t ys,
                                                       int accumulate, int n_rt, int n_tt) {
@@ -253,7 +256,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t 
         if constexpr (WIDE) {
           const v16f dx = tok16(st + S::dx + u * 128);
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
+          for (int i = 0; i < NE; ++i) {
             const float sm = fma_(f1[i], d1, f0[i] * d0);
             acc[i] = fma_(sm, dx[i], acc[i]);
           }
@@ -262,7 +265,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t 
           const float dxl = *reinterpret_cast<const float*>(st + S::dx + u * 128 + li * 4);
           const v32f p = __builtin_amdgcn_mfma_f32_32x32x1f32(dxl, h ? d1 : d0, zero, 0, 0, 0);
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
+          for (int i = 0; i < NE; ++i) {
             acc[i] = fma_(f0[i], p[i], acc[i]);
             acc[i] = fma_(f1[i], p[16 + i], acc[i]);
           }
@@ -306,7 +309,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t 
           const v16f dsx = tok16(st + S::dsx + w * 512 + u * 128);
           const float nm = -fmn[u];
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
+          for (int i = 0; i < NE; ++i) {
             acc[i] = fma_(f[i], p[16 * e + i], acc[i]);
             acc[i] = fma_(nm, dsx[i], acc[i]);
           }
@@ -338,18 +341,18 @@ __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t 
   }
 }
 
-template <int TYPE, bool WIDE, int NS>
+template <int TYPE, bool WIDE, int NS, int NE>
 void launch_kq_ns(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
                   int64_t ys, bool accumulate, int n_rt, int n_tt) {
   const size_t lds = NS * (size_t)KqLds<TYPE>::bytes;
   static bool attr = false;  // per instantiation: rings past 64 KB of dynamic LDS
   if (!attr) {
-    check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_kq<TYPE, WIDE, NS>),
+    check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_kq<TYPE, WIDE, NS, NE>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
           "hipFuncSetAttribute");
     attr = true;
   }
-  hipLaunchKernelGGL((k_gemm_kq<TYPE, WIDE, NS>), dim3((unsigned)((int64_t)n_rt * n_tt)), dim3(kThreads), lds, s,
+  hipLaunchKernelGGL((k_gemm_kq<TYPE, WIDE, NS, NE>), dim3((unsigned)((int64_t)n_rt * n_tt)), dim3(kThreads), lds, s,
                      static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0, n_rt, n_tt);
 }
 
@@ -362,11 +365,13 @@ void launch_kq(hipStream_t s, const void* w, int64_t rows, int64_t cols, const B
   const int n_tt = (n + kTokT - 1) / kTokT;
   const int64_t wgs = (int64_t)n_rt * n_tt, cus = device_cus();
   if (wgs <= cus)
-    launch_kq_ns<TYPE, WIDE, 8>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt);
+    n <= 17 ? launch_kq_ns<TYPE, WIDE, 8, 9>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt)
+            : launch_kq_ns<TYPE, WIDE, 8, 16>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt);
   else if (wgs <= 2 * cus)
-    launch_kq_ns<TYPE, WIDE, 4>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt);
+    n <= 17 ? launch_kq_ns<TYPE, WIDE, 4, 9>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt)
+            : launch_kq_ns<TYPE, WIDE, 4, 16>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt);
   else
-    launch_kq_ns<TYPE, WIDE, 3>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt);
+    launch_kq_ns<TYPE, WIDE, 3, 16>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt);
 }
 
 }  // namespace

@@ -258,6 +258,7 @@ SHORT = [
     (mk_.Q6_K, 13, 96, 1024), (mk_.Q6_K, 25, 64, 512), (mk_.Q6_K, 32, 4096, 256),
     (mk_.Q4_K, 3, 8224, 512), (mk_.Q4_K, 4, 8224, 256), (mk_.Q8_0, 3, 24576, 256),  # 3-4 tokens on many rows
     (mk_.Q6_K, 5, 96, 512), (mk_.Q8_0, 8, 4096, 1024), (mk_.Q4_K, 6, 2048, 2048),  # up to 8 tokens: two units a tile
+    (mk_.Q6_K, 17, 16384, 512), (mk_.Q4_K, 17, 16384, 256),   # K-quant GEMM at 17 tokens: padding elements skipped
 ]
 
 
