@@ -206,6 +206,17 @@ int mk_attention_decode(mk_ctx* ctx, const float* qkv, int64_t stride, int n, in
 int mk_attention(mk_ctx* ctx, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int n_head,
                  const mk_kv_cache* kv, int layer, const int32_t* seq, const int32_t* n_keys, const int32_t* anc_off,
                  const int32_t* anc, int max_keys);
+/* mk_attention and mk_attention_decode that also write the BlockQ8 rows of `out` into xq: token t's
+   n_head * head_dim / 32 blocks at xq + t * n_head * head_dim / 32 blocks, byte-identical to mk_quantize_q8(out) (the
+   reference quantizes the attention output right after attention, model.cpp:398-401; this fuses that launch away).
+   head_dim % 32 == 0. Same outputs, errors and MK_ERR_UNSUPPORTED cases as the calls they extend. */
+int mk_attention_q8(mk_ctx* ctx, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int n_head,
+                    const mk_kv_cache* kv, int layer, const int32_t* seq, const int32_t* n_keys,
+                    const int32_t* anc_off, const int32_t* anc, int max_keys, void* xq);
+int mk_attention_decode_q8(mk_ctx* ctx, const float* qkv, int64_t stride, int n, int n_head, const float* q_norm,
+                           const float* k_norm, float eps, const float* cos_t, const float* sin_t,
+                           const int32_t* rpos, const int32_t* seq, const int32_t* kv_row, const int32_t* n_keys,
+                           const mk_kv_cache* kv, int layer, float* out, int64_t out_stride, int max_keys, void* xq);
 /* Model::move_kv (model.cpp:432-440): row `from` -> row `to` of sequence seq, K and V of every layer. */
 int mk_move_kv(mk_ctx* ctx, const mk_kv_cache* kv, int seq, int from, int to);
 

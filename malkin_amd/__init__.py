@@ -64,6 +64,9 @@ SIGNATURES = {
     "mk_qk_norm_rope_kv": (_I, [_P, _P, _P, _P, _I64, _I, _I, _P, _P, _F, _P, _P, _P, _P, _P, _P, _I]),
     "mk_attention": (_I, [_P, _P, _I64, _P, _I64, _I, _I, _P, _I, _P, _P, _P, _P, _I]),
     "mk_attention_decode": (_I, [_P, _P, _I64, _I, _I, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I64, _I]),
+    "mk_attention_q8": (_I, [_P, _P, _I64, _P, _I64, _I, _I, _P, _I, _P, _P, _P, _P, _I, _P]),
+    "mk_attention_decode_q8": (_I, [_P, _P, _I64, _I, _I, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I64, _I,
+                                    _P]),
     "mk_move_kv": (_I, [_P, _P, _I, _I, _I]),
     "mk_argmax_top2": (_I, [_P, _P, _I, _I, _P, _P]),
     "mk_greedy_advance": (_I, [_P, _P, _P, _P, _P, _P, _P, _P]),

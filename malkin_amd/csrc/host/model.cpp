@@ -570,28 +570,37 @@ void Model::run() {
     }
     // Short plain batches of distinct sequences (decode steps): QK-norm, RoPE, the KV write and attention in one
     // launch; otherwise (prompt chunks, trees, shared sequences) the KV rows are written before any token attends.
+    // Where attn_output takes BlockQ8 activations, the attention kernels write them beside att (the reference's
+    // quantize_acts of att, model.cpp:398-401).
+    mk_weight wo = L.wo.w();
+    wo.wide = wide_ ? 1 : 0;
+    const bool wo_f32 = matmul_f32_ok(wo, n, false);
     int rc = MK_ERR_UNSUPPORTED;
-    if (!lay_.tree && lay_.distinct_seqs && n < 16)
-      rc = mk_attention_decode(ctx_, qkv, QKV, n, H, norms + 2 * E, norms + 2 * E + D, c.rms_eps,
-                               rope_cos_.as<float>(), rope_sin_.as<float>(), d_rpos_, d_seq_, d_kv_row_, d_n_keys_,
-                               &kv, il, att, static_cast<int64_t>(H) * D, lay_.max_keys);
+    if (!lay_.tree && lay_.distinct_seqs && n < 16) {
+      rc = wo_f32 ? mk_attention_decode(ctx_, qkv, QKV, n, H, norms + 2 * E, norms + 2 * E + D, c.rms_eps,
+                                        rope_cos_.as<float>(), rope_sin_.as<float>(), d_rpos_, d_seq_, d_kv_row_,
+                                        d_n_keys_, &kv, il, att, static_cast<int64_t>(H) * D, lay_.max_keys)
+                  : mk_attention_decode_q8(ctx_, qkv, QKV, n, H, norms + 2 * E, norms + 2 * E + D, c.rms_eps,
+                                           rope_cos_.as<float>(), rope_sin_.as<float>(), d_rpos_, d_seq_, d_kv_row_,
+                                           d_n_keys_, &kv, il, att, static_cast<int64_t>(H) * D, lay_.max_keys, xq);
+    }
     if (rc == MK_ERR_UNSUPPORTED) {
       ck(mk_qk_norm_rope_kv(ctx_, qkv, qkv + static_cast<int64_t>(H) * D, qkv + static_cast<int64_t>(H + KV) * D, QKV,
                             n, H, norms + 2 * E, norms + 2 * E + D, c.rms_eps, rope_cos_.as<float>(),
                             rope_sin_.as<float>(), d_rpos_, d_seq_, d_kv_row_, &kv, il));
-      ck(mk_attention(ctx_, qkv, QKV, att, static_cast<int64_t>(H) * D, n, H, &kv, il, d_seq_, d_n_keys_,
-                      lay_.tree ? d_extra_at_ : nullptr, d_extra_, lay_.max_keys));
+      if (wo_f32)
+        ck(mk_attention(ctx_, qkv, QKV, att, static_cast<int64_t>(H) * D, n, H, &kv, il, d_seq_, d_n_keys_,
+                        lay_.tree ? d_extra_at_ : nullptr, d_extra_, lay_.max_keys));
+      else
+        ck(mk_attention_q8(ctx_, qkv, QKV, att, static_cast<int64_t>(H) * D, n, H, &kv, il, d_seq_, d_n_keys_,
+                           lay_.tree ? d_extra_at_ : nullptr, d_extra_, lay_.max_keys, xq));
     } else {
       ck(rc);
     }
-    mk_weight wo = L.wo.w();
-    wo.wide = wide_ ? 1 : 0;
-    if (matmul_f32_ok(wo, n, false)) {
+    if (wo_f32)
       ck(mk_matmul_f32(ctx_, &wo, att, static_cast<int64_t>(H) * D, nullptr, 0.0f, n, x, E, 1, 0));
-    } else {
-      ck(mk_quantize_q8(ctx_, att, n, static_cast<int64_t>(H) * D, xq));
+    else
       ck(mk_matmul(ctx_, &wo, xq, n, x, E, 1));  // x += attn_output(att) (model.cpp:398-401)
-    }
     mk_weight wd = L.down.w();
     wd.wide = wide_ ? 1 : 0;
     if (L.gateup.silu_pairs && matmul_f32_ok(L.gateup.parts[0].w(), n, true) && matmul_f32_ok(wd, n, false)) {
@@ -676,9 +685,8 @@ void Model::run_row_layer(const Layer& L, int il) {
   ck(mk_qk_norm_rope_kv(ctx_, qkv, qkv + HD, qkv + HD + static_cast<int64_t>(KV) * D, QKV, n, H, norms + 2 * E,
                         norms + 2 * E + D, c.rms_eps, rope_cos_.as<float>(), rope_sin_.as<float>(), d_rpos_, d_seq_,
                         d_kv_row_, &kv_, il));
-  ck(mk_attention(ctx_, qkv, QKV, att, HD, n, H, &kv_, il, d_seq_, d_n_keys_, lay_.tree ? d_extra_at_ : nullptr,
-                  d_extra_, lay_.max_keys));
-  ck(mk_quantize_q8(ctx_, att, n, HD, xq));
+  ck(mk_attention_q8(ctx_, qkv, QKV, att, HD, n, H, &kv_, il, d_seq_, d_n_keys_,
+                     lay_.tree ? d_extra_at_ : nullptr, d_extra_, lay_.max_keys, xq));  // att and its BlockQ8 rows
   single(L.wo, att, HD, x, E);  // x += attn_output(att)
   ck(mk_rmsnorm_rows(ctx_, x, nullptr, norms + E, n, E, c.rms_eps, h));
   ck(mk_quantize_q8(ctx_, h, n, E, xq));

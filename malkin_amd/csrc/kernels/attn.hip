@@ -159,7 +159,8 @@ __device__ __forceinline__ void attend_pair(int t, int h, const float* __restric
                                             float* __restrict__ out, int64_t out_stride, int G, float scale,
                                             const AttnAddr& a, const int32_t* __restrict__ seqs,
                                             const int32_t* __restrict__ n_keys, const int32_t* __restrict__ anc_off,
-                                            const int32_t* __restrict__ anc, float* __restrict__ gsc, int gcap) {
+                                            const int32_t* __restrict__ anc, float* __restrict__ gsc, int gcap,
+                                            BlockQ8* __restrict__ xq, int64_t xq_stride) {
   constexpr int DC = D / 16;
   using T = AttnTile<D>;
   const int tid = threadIdx.x;
@@ -436,7 +437,7 @@ __device__ __forceinline__ void attend_pair(int t, int h, const float* __restric
     }
     lds_barrier();
   }
-  if (tid < D) out[t * out_stride + (int64_t)h * D + tid] = acc * inv_s;
+  if (tid < D) put_out(out + t * out_stride + (int64_t)h * D, xq, t * xq_stride, h * D, tid, acc * inv_s);
 }
 
 template <int D, bool PERM>
@@ -445,7 +446,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
                                                             float scale, AttnAddr a, const int32_t* __restrict__ seqs,
                                                             const int32_t* __restrict__ n_keys,
                                                             const int32_t* __restrict__ anc_off,
-                                                            const int32_t* __restrict__ anc, int n, int H) {
+                                                            const int32_t* __restrict__ anc, int n, int H,
+                                                            BlockQ8* __restrict__ xq, int64_t xq_stride) {
   // Workgroups are dealt to the 8 XCDs in turn (workgroup w on XCD w % 8). (token, head) pairs are numbered
   // KV-group-major (group, token, head in group) and XCD x takes a contiguous run of them: a KV group's K/V rows are
   // read into one XCD's L2, and in prefill every XCD gets tokens of all lengths.
@@ -459,7 +461,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(const float* __restr
     t = (int)blockIdx.x / H;
     h = (int)blockIdx.x % H;
   }
-  attend_pair<D, PERM, false>(t, h, q, q_stride, out, out_stride, G, scale, a, seqs, n_keys, anc_off, anc, nullptr, 0);
+  attend_pair<D, PERM, false>(t, h, q, q_stride, out, out_stride, G, scale, a, seqs, n_keys, anc_off, anc, nullptr, 0,
+                              xq, xq_stride);
 }
 
 // Rows with more keys than LDS holds: workgroup w owns the global slot w (2 gcap floats) and takes the (token,
@@ -472,12 +475,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_long(const float* __
                                                                  const int32_t* __restrict__ n_keys,
                                                                  const int32_t* __restrict__ anc_off,
                                                                  const int32_t* __restrict__ anc, int n, int H,
-                                                                 float* __restrict__ gsc, int gcap) {
+                                                                 float* __restrict__ gsc, int gcap,
+                                                                 BlockQ8* __restrict__ xq, int64_t xq_stride) {
   float* slot = gsc + (size_t)blockIdx.x * 2 * (size_t)gcap;
   for (int pair = (int)blockIdx.x; pair < n * H; pair += (int)gridDim.x) {
     __syncthreads();  // the previous pair's LDS and slot are no longer read
     attend_pair<D, PERM, true>(pair / H, pair % H, q, q_stride, out, out_stride, G, scale, a, seqs, n_keys, anc_off,
-                               anc, slot, gcap);
+                               anc, slot, gcap, xq, xq_stride);
   }
 }
 
@@ -520,7 +524,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_grp(const float* __r
                                                                 const int32_t* __restrict__ n_keys,
                                                                 const int32_t* __restrict__ anc_off,
                                                                 const int32_t* __restrict__ anc, int n, int KV,
-                                                                int nk_pad, int anc_cap) {
+                                                                int nk_pad, int anc_cap, BlockQ8* __restrict__ xq,
+                                                                int64_t xq_stride) {
   using C = GrpCfg<GH>;
   constexpr int D = C::D, DC = C::DC, CK = C::CK, VS = C::VS;
   const int tid = threadIdx.x;
@@ -824,7 +829,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_grp(const float* __r
     float* o = out + t * out_stride + (int64_t)(hfirst + hb) * D + d;
 #pragma unroll
     for (int k = 0; k < C::h0; ++k)
-      if (k < nh) o[k * D] = acc[k] * inv_s[hb + k];
+      if (k < nh) put_out(o + k * D - d, xq, t * xq_stride, (hfirst + hb + k) * D, d, acc[k] * inv_s[hb + k]);
   }
 }
 
@@ -978,7 +983,8 @@ __global__ __launch_bounds__(kDecThreads) void k_attention_dec(const float* __re
                                                                float scale, AttnAddr a,
                                                                const int32_t* __restrict__ seqs,
                                                                const int32_t* __restrict__ n_keys, int n, int H,
-                                                               DecFuse f) {
+                                                               DecFuse f, BlockQ8* __restrict__ xq,
+                                                               int64_t xq_stride) {
   constexpr int DC = D / 16;
   const int tid = threadIdx.x;
   int t, h;
@@ -1227,7 +1233,7 @@ __global__ __launch_bounds__(kDecThreads) void k_attention_dec(const float* __re
     if (l == 0) inv_s = 1.0f / s;
   }
   lds_barrier();
-  if (tid < D) out[t * out_stride + (int64_t)h * D + tid] = acc * inv_s;
+  if (tid < D) put_out(out + t * out_stride + (int64_t)h * D, xq, t * xq_stride, h * D, tid, acc * inv_s);
 }
 
 // Attention of many query rows at once (prefill and other long plain batches), attend_t semantics for D in {64, 128}
@@ -1270,7 +1276,8 @@ __global__ __launch_bounds__(kRowsThreads) void k_attention_rows(const float* __
                                                                  float scale, AttnAddr a,
                                                                  const int32_t* __restrict__ seqs,
                                                                  const int32_t* __restrict__ n_keys, int n, int KV,
-                                                                 int nk_pad) {
+                                                                 int nk_pad, BlockQ8* __restrict__ xq,
+                                                                 int64_t xq_stride) {
   using C = RowsCfg<D>;
   constexpr int DC = C::DC;
   const int tid = threadIdx.x;
@@ -1436,10 +1443,15 @@ __global__ __launch_bounds__(kRowsThreads) void k_attention_rows(const float* __
     }
     auto put = [&](int r, const float* acc) {
       if (r < R && ((act >> r) & 1)) {
-        float* o = out + (int64_t)(t0 + r / G) * out_stride + (int64_t)(g * G + r % G) * D + d0;
+        const int64_t tr = t0 + r / G;
+        const int hd = (g * G + r % G) * D;
+        float* o = out + tr * out_stride + hd + d0;
         const float inv = inv_s[r];
+        float v[C::dl];
 #pragma unroll
-        for (int k = 0; k < C::dl; ++k) o[k] = acc[k] * inv;
+        for (int k = 0; k < C::dl; ++k) o[k] = v[k] = acc[k] * inv;
+        // A Q8 block of the row is 32 / dl consecutive lanes of this lane's 16-lane group (same row).
+        if (xq) quantize_block_lanes_n<C::dl>(v, (d0 & 31) / C::dl, xq + tr * xq_stride + (hd + d0) / 32);
       }
     };
     put(ra, acc0);
@@ -1457,7 +1469,8 @@ __global__ __launch_bounds__(256) void k_attention_generic(const float* __restri
                                                            const int32_t* __restrict__ seqs,
                                                            const int32_t* __restrict__ n_keys,
                                                            const int32_t* __restrict__ anc_off,
-                                                           const int32_t* __restrict__ anc) {
+                                                           const int32_t* __restrict__ anc, BlockQ8* __restrict__ xq,
+                                                           int64_t xq_stride) {
   const int t = blockIdx.x, h = blockIdx.y, g = h / G, tid = threadIdx.x;
   extern __shared__ float sm[];
   float* qs = sm;
@@ -1519,7 +1532,8 @@ __global__ __launch_bounds__(256) void k_attention_generic(const float* __restri
       const int64_t r = j < n0 ? j : anc[e0 + j - n0];
       acc = fma_(pv[j], (float)vb[r * a.k_row + d], acc);
     }
-    out[t * out_stride + (int64_t)h * D + d] = acc;
+    // With xq, D % 32 == 0: a Q8 block is 32 consecutive threads, all in the loop or all past it.
+    put_out(out + t * out_stride + (int64_t)h * D, xq, t * xq_stride, h * D, d, acc);
   }
 }
 
@@ -1668,7 +1682,7 @@ bool dec_ok(int G, int D, const AttnAddr& a, int max_keys) {
 template <bool FUSE>
 void launch_dec(hipStream_t s, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int H, int D,
                 int G, float scale, const AttnAddr& a, const int32_t* seq, const int32_t* n_keys, int max_keys,
-                const DecFuse& f) {
+                const DecFuse& f, BlockQ8* xq, int64_t xq_stride) {
   const size_t lds = dec_lds_bytes(D, attn_keys_pad(max_keys));
   auto go = [&](auto kernel) {
     static bool attr = false;
@@ -1679,7 +1693,7 @@ void launch_dec(hipStream_t s, const float* q, int64_t q_stride, float* out, int
       attr = true;
     }
     hipLaunchKernelGGL(kernel, dim3(n * H), dim3(kDecThreads), lds, s, q, q_stride, out, out_stride, G, scale, a, seq,
-                       n_keys, n, H, f);
+                       n_keys, n, H, f, xq, xq_stride);
   };
   const int slots = dec_slots(D, max_keys, FUSE);
   if (D == 64) {
@@ -1699,11 +1713,13 @@ bool attention_decode_fused(hipStream_t s, const float* qkv, int64_t stride, flo
                             int H, int KV, int D, float scale, const AttnAddr& a, const float* q_norm,
                             const float* k_norm, float eps, const float* cos_t, const float* sin_t,
                             const int32_t* rpos, const int32_t* seq, const int32_t* kv_row, const int32_t* n_keys,
-                            const KvLayer& kv, int n_ctx, int max_keys) {
+                            const KvLayer& kv, int n_ctx, int max_keys, BlockQ8* xq, int64_t xq_stride) {
   if (n <= 0) return true;
+  require(!xq || D % 32 == 0, "attention_decode_fused: Q8 rows need head_dim % 32 == 0");
   if (H % KV != 0 || !dec_ok(H / KV, D, a, max_keys)) return false;
   const DecFuse f{qkv, stride, q_norm, k_norm, eps, cos_t, sin_t, rpos, kv_row, kv, n_ctx, KV};
-  launch_dec<true>(s, nullptr, 0, out, out_stride, n, H, D, H / KV, scale, a, seq, n_keys, max_keys, f);
+  launch_dec<true>(s, nullptr, 0, out, out_stride, n, H, D, H / KV, scale, a, seq, n_keys, max_keys, f, xq,
+                   xq_stride);
   check_launch("attention_decode_fused");
   return true;
 }
@@ -1731,9 +1747,11 @@ int grp_heads(int n, int H, int G, int D, const AttnAddr& a, const int32_t* anc_
 
 void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int H, int KV,
                int D, float scale, const AttnAddr& a, const int32_t* seq, const int32_t* n_keys,
-               const int32_t* anc_off, const int32_t* anc, int max_keys, void* scratch, size_t scratch_bytes) {
+               const int32_t* anc_off, const int32_t* anc, int max_keys, void* scratch, size_t scratch_bytes,
+               BlockQ8* xq, int64_t xq_stride) {
   if (n <= 0) return;
   require(D % 16 == 0 && D <= 256 && H % KV == 0 && max_keys > 0, "attention: unsupported head layout");
+  require(!xq || D % 32 == 0, "attention: Q8 rows need head_dim % 32 == 0");
   const int G = H / KV;
   const bool aligned = attn_aligned(a);
   if (!anc_off && n >= kRowsMinTokens && G <= 16 && (D == 64 || D == 128) && aligned &&
@@ -1750,14 +1768,15 @@ void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int6
       }
       const int TQ = kRowsMax / G;
       hipLaunchKernelGGL(kernel, dim3(((n + TQ - 1) / TQ) * KV), dim3(kRowsThreads), lds, s, q, q_stride, out,
-                         out_stride, G, scale, a, seq, n_keys, n, KV, nk_pad);
+                         out_stride, G, scale, a, seq, n_keys, n, KV, nk_pad, xq, xq_stride);
     };
     if (D == 64)
       a.k_perm ? go(k_attention_rows<64, true>) : go(k_attention_rows<64, false>);
     else
       a.k_perm ? go(k_attention_rows<128, true>) : go(k_attention_rows<128, false>);
   } else if (!anc_off && dec_ok(G, D, a, max_keys)) {
-    launch_dec<false>(s, q, q_stride, out, out_stride, n, H, D, G, scale, a, seq, n_keys, max_keys, DecFuse{});
+    launch_dec<false>(s, q, q_stride, out, out_stride, n, H, D, G, scale, a, seq, n_keys, max_keys, DecFuse{}, xq,
+                      xq_stride);
   } else if (grp_heads(n, H, G, D, a, anc_off, max_keys) > 0) {
     // Grouped workgroups (trees, keys past the decode kernel's LDS): all heads of a KV group per workgroup where one
     // workgroup per (token, head) would take more than one round of the CUs, else one head per workgroup.
@@ -1773,7 +1792,7 @@ void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int6
         done = true;
       }
       hipLaunchKernelGGL(kernel, dim3(n * KV * (G / GH)), dim3(kAttnThreads), lds, s, q, q_stride, out, out_stride, G,
-                         scale, a, seq, n_keys, anc_off, anc, n, KV, nk_pad, anc_cap);
+                         scale, a, seq, n_keys, anc_off, anc, n, KV, nk_pad, anc_cap, xq, xq_stride);
     };
     switch (GH) {
       case 1: go(k_attention_grp<1>); break;
@@ -1799,7 +1818,7 @@ void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int6
         static bool done = false;
         attr(kernel, done);
         hipLaunchKernelGGL(kernel, dim3(n * H), dim3(kAttnThreads), lds, s, q, q_stride, out, out_stride, G, scale, a,
-                           seq, n_keys, anc_off, anc, n, H);
+                           seq, n_keys, anc_off, anc, n, H, xq, xq_stride);
       };
       if (D == 64)
         a.k_perm ? go(k_attention<64, true>) : go(k_attention<64, false>);
@@ -1818,7 +1837,8 @@ void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int6
         static bool done = false;
         attr(kernel, done);
         hipLaunchKernelGGL(kernel, dim3(slots), dim3(kAttnThreads), lds_long, s, q, q_stride, out, out_stride, G,
-                           scale, a, seq, n_keys, anc_off, anc, n, H, static_cast<float*>(scratch), nk_pad);
+                           scale, a, seq, n_keys, anc_off, anc, n, H, static_cast<float*>(scratch), nk_pad, xq,
+                           xq_stride);
       };
       if (D == 64)
         a.k_perm ? go(k_attention_long<64, true>) : go(k_attention_long<64, false>);
@@ -1833,7 +1853,7 @@ void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int6
     const bool ref_order = G <= 16 && (D == 64 || D == 128 || D == 256);
     require(!ref_order, "attention: K/V rows must be 16-byte aligned");
     hipLaunchKernelGGL(k_attention_generic, dim3(n, H), dim3(256), lds, s, q, q_stride, out, out_stride, G, D, scale,
-                       a, seq, n_keys, anc_off, anc);
+                       a, seq, n_keys, anc_off, anc, xq, xq_stride);
   }
   check_launch("attention");
 }

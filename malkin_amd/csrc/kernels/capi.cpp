@@ -347,19 +347,67 @@ int mk_qk_norm_rope_kv(mk_ctx* c, float* q, float* k, const float* v, int64_t st
   });
 }
 
+namespace {
+
+void attention_rows(mk_ctx* c, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int n_head,
+                    const mk_kv_cache* kv, int layer, const int32_t* seq, const int32_t* n_keys,
+                    const int32_t* anc_off, const int32_t* anc, int max_keys, void* xq) {
+  const mk::KvLayer L = kv_layer(kv, layer);
+  const int D = kv->head_dim;
+  const int64_t rows = (int64_t)kv->n_ctx;
+  mk::AttnAddr a{L.k, L.v, reinterpret_cast<const char*>(L.ks), reinterpret_cast<const char*>(L.vs),
+                 (int64_t)kv->n_head_kv * rows * D, rows * D, D,
+                 (int64_t)kv->n_head_kv * rows * 4, rows * 4, 4, 1};
+  const float scale = 1.0f / std::sqrt(static_cast<float>(D));  // model.cpp:208
+  mk::attention(c->stream, q, q_stride, out, out_stride, n, n_head, kv->n_head_kv, D, scale, a, seq, n_keys, anc_off,
+                anc, max_keys, c->scratch, c->scratch_bytes, static_cast<mk::BlockQ8*>(xq), (int64_t)n_head * D / 32);
+}
+
+void attention_decode(mk_ctx* c, const float* qkv, int64_t stride, int n, int n_head, const float* q_norm,
+                      const float* k_norm, float eps, const float* cos_t, const float* sin_t, const int32_t* rpos,
+                      const int32_t* seq, const int32_t* kv_row, const int32_t* n_keys, const mk_kv_cache* kv,
+                      int layer, float* out, int64_t out_stride, int max_keys, void* xq) {
+  const mk::KvLayer L = kv_layer(kv, layer);
+  const int D = kv->head_dim, KV = kv->n_head_kv;
+  require(n_head > 0 && n_head % KV == 0 && max_keys > 0, "mk_attention_decode: bad head layout");
+  const int64_t rows = (int64_t)kv->n_ctx;
+  mk::AttnAddr a{L.k, L.v, reinterpret_cast<const char*>(L.ks), reinterpret_cast<const char*>(L.vs),
+                 (int64_t)KV * rows * D, rows * D, D, (int64_t)KV * rows * 4, rows * 4, 4, 1};
+  const float scale = 1.0f / std::sqrt(static_cast<float>(D));  // model.cpp:208
+  if (!mk::attention_decode_fused(c->stream, qkv, stride, out, out_stride, n, n_head, KV, D, scale, a, q_norm,
+                                  k_norm, eps, cos_t, sin_t, rpos, seq, kv_row, n_keys, L, kv->n_ctx, max_keys,
+                                  static_cast<mk::BlockQ8*>(xq), (int64_t)n_head * D / 32))
+    throw mk::Error(MK_ERR_UNSUPPORTED, "mk_attention_decode: no fused kernel for this head layout / key count");
+}
+
+}  // namespace
+
+int mk_attention_q8(mk_ctx* c, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int n_head,
+                    const mk_kv_cache* kv, int layer, const int32_t* seq, const int32_t* n_keys,
+                    const int32_t* anc_off, const int32_t* anc, int max_keys, void* xq) {
+  return guard([&] {
+    require(xq != nullptr, "mk_attention_q8: xq is NULL");
+    attention_rows(c, q, q_stride, out, out_stride, n, n_head, kv, layer, seq, n_keys, anc_off, anc, max_keys, xq);
+  });
+}
+
+int mk_attention_decode_q8(mk_ctx* c, const float* qkv, int64_t stride, int n, int n_head, const float* q_norm,
+                           const float* k_norm, float eps, const float* cos_t, const float* sin_t,
+                           const int32_t* rpos, const int32_t* seq, const int32_t* kv_row, const int32_t* n_keys,
+                           const mk_kv_cache* kv, int layer, float* out, int64_t out_stride, int max_keys, void* xq) {
+  return guard([&] {
+    require(xq != nullptr, "mk_attention_decode_q8: xq is NULL");
+    attention_decode(c, qkv, stride, n, n_head, q_norm, k_norm, eps, cos_t, sin_t, rpos, seq, kv_row, n_keys, kv,
+                     layer, out, out_stride, max_keys, xq);
+  });
+}
+
 int mk_attention(mk_ctx* c, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int n_head,
                  const mk_kv_cache* kv, int layer, const int32_t* seq, const int32_t* n_keys, const int32_t* anc_off,
                  const int32_t* anc, int max_keys) {
   return guard([&] {
-    const mk::KvLayer L = kv_layer(kv, layer);
-    const int D = kv->head_dim;
-    const int64_t rows = (int64_t)kv->n_ctx;
-    mk::AttnAddr a{L.k, L.v, reinterpret_cast<const char*>(L.ks), reinterpret_cast<const char*>(L.vs),
-                   (int64_t)kv->n_head_kv * rows * D, rows * D, D,
-                   (int64_t)kv->n_head_kv * rows * 4, rows * 4, 4, 1};
-    const float scale = 1.0f / std::sqrt(static_cast<float>(D));  // model.cpp:208
-    mk::attention(c->stream, q, q_stride, out, out_stride, n, n_head, kv->n_head_kv, D, scale, a, seq, n_keys, anc_off,
-                  anc, max_keys, c->scratch, c->scratch_bytes);
+    attention_rows(c, q, q_stride, out, out_stride, n, n_head, kv, layer, seq, n_keys, anc_off, anc, max_keys,
+                   nullptr);
   });
 }
 
@@ -368,16 +416,8 @@ int mk_attention_decode(mk_ctx* c, const float* qkv, int64_t stride, int n, int 
                         const int32_t* seq, const int32_t* kv_row, const int32_t* n_keys, const mk_kv_cache* kv,
                         int layer, float* out, int64_t out_stride, int max_keys) {
   return guard([&] {
-    const mk::KvLayer L = kv_layer(kv, layer);
-    const int D = kv->head_dim, KV = kv->n_head_kv;
-    require(n_head > 0 && n_head % KV == 0 && max_keys > 0, "mk_attention_decode: bad head layout");
-    const int64_t rows = (int64_t)kv->n_ctx;
-    mk::AttnAddr a{L.k, L.v, reinterpret_cast<const char*>(L.ks), reinterpret_cast<const char*>(L.vs),
-                   (int64_t)KV * rows * D, rows * D, D, (int64_t)KV * rows * 4, rows * 4, 4, 1};
-    const float scale = 1.0f / std::sqrt(static_cast<float>(D));  // model.cpp:208
-    if (!mk::attention_decode_fused(c->stream, qkv, stride, out, out_stride, n, n_head, KV, D, scale, a, q_norm,
-                                    k_norm, eps, cos_t, sin_t, rpos, seq, kv_row, n_keys, L, kv->n_ctx, max_keys))
-      throw mk::Error(MK_ERR_UNSUPPORTED, "mk_attention_decode: no fused kernel for this head layout / key count");
+    attention_decode(c, qkv, stride, n, n_head, q_norm, k_norm, eps, cos_t, sin_t, rpos, seq, kv_row, n_keys, kv,
+                     layer, out, out_stride, max_keys, nullptr);
   });
 }
 

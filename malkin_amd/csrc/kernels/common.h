@@ -326,6 +326,53 @@ __device__ __forceinline__ int cvt_rne(float x) {
 
 __device__ __forceinline__ int sat8(int v) { return v > 127 ? 127 : (v < -128 ? -128 : v); }
 
+// One 32-value block of f32 activations -> BlockQ8 (kernels_avx512.cpp:66-80), held by 32 / N consecutive lanes
+// (aligned to 32 / N): lane l of the block holds values N l .. N l + N - 1. Every lane of the block calls this. amax is
+// an exact max and the half sums are exact integer sums, so the lane order of the reductions does not matter.
+template <int N>
+__device__ __forceinline__ void quantize_block_lanes_n(const float (&v)[N], int l, BlockQ8* out) {
+  constexpr int LB = 32 / N;  // lanes per block
+  static_assert(N == 1 || N == 2 || N == 4, "1, 2 or 4 values per lane");
+  float amax = fabsf(v[0]);
+#pragma unroll
+  for (int k = 1; k < N; ++k) amax = fmaxf(amax, fabsf(v[k]));
+#pragma unroll
+  for (int off = LB / 2; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, LB));
+  const float d = amax / 127.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  int s = 0;
+  uint32_t packed = 0;
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    const int q = cvt_rne(v[k] * id);
+    s += q;
+    packed |= (uint32_t)(uint8_t)(int8_t)sat8(q) << (8 * k);
+  }
+#pragma unroll
+  for (int off = LB / 4; off > 0; off >>= 1) s += __shfl_xor(s, off, LB / 2);
+  int8_t* o = reinterpret_cast<int8_t*>(out);
+  if constexpr (N == 1) o[8 + l] = (int8_t)packed;
+  else if constexpr (N == 2) *reinterpret_cast<uint16_t*>(o + 8 + 2 * l) = (uint16_t)packed;
+  else *reinterpret_cast<uint32_t*>(o + 8 + 4 * l) = packed;
+  if (l == 0) {
+    *reinterpret_cast<float*>(o) = d;
+    *reinterpret_cast<int16_t*>(o + 4) = (int16_t)s;
+  } else if (l == LB / 2) {
+    *reinterpret_cast<int16_t*>(o + 6) = (int16_t)s;
+  }
+}
+
+// Value d of an attention output row (row[d] = v) and, with xq, its BlockQ8 row as quantize_acts writes it
+// (model.cpp:398-401): column hd + d of the token's blocks at xq + xq_row (hd % 32 == 0). The 32 lanes that hold
+// d = 32 b .. 32 b + 31 must call this together.
+__device__ __forceinline__ void put_out(float* row, BlockQ8* xq, int64_t xq_row, int hd, int d, float v) {
+  row[d] = v;
+  if (xq) {
+    const float one[1] = {v};
+    quantize_block_lanes_n<1>(one, d & 31, xq + xq_row + (hd + d) / 32);
+  }
+}
+
 // Half of one Q8 block (16 consecutive values, h = which half) -> its BlockQ8 bytes (kernels_avx512.cpp:66-80). The
 // two halves sit on neighbouring lanes (h = lane & 1); every lane must call this, as the block max is exchanged between
 // the pair. amax is an exact max and the half sums are exact integer sums, so their order does not matter.

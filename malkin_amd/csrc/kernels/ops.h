@@ -117,6 +117,8 @@ struct AttnAddr {
 // Byte position of element e in a permuted K row of D = 16 * DC values: the DC values a reference lane l
 // (kernels_avx512.cpp:234-244) multiplies, e = 16 c + l for c < DC, are contiguous at DC * l.
 __host__ __device__ constexpr int kv_perm(int e, int DC) { return DC * (e & 15) + (e >> 4); }
+// With xq (D % 32 == 0) both also write the BlockQ8 rows of out (token t's H*D/32 blocks at xq + t * xq_stride), as
+// quantize_q8 of out would, so the attn_output matmul needs no separate quantization launch.
 // q [n][H*D] (token stride q_stride floats), out [n][H*D] (stride out_stride). Per token t: keys rows
 // 0..n_keys[t]-1 of sequence seq[t], then anc[anc_off[t] .. anc_off[t+1]) when anc_off is non-null. Rows with more
 // keys than one workgroup's LDS holds keep their scores in `scratch` (attention_scratch_bytes of it for full speed;
@@ -124,7 +126,8 @@ __host__ __device__ constexpr int kv_perm(int e, int DC) { return DC * (e & 15) 
 void attention(hipStream_t s, const float* q, int64_t q_stride, float* out, int64_t out_stride, int n, int H, int KV,
                int D, float scale,
                const AttnAddr& a, const int32_t* seq, const int32_t* n_keys, const int32_t* anc_off,
-               const int32_t* anc, int max_keys, void* scratch, size_t scratch_bytes);
+               const int32_t* anc, int max_keys, void* scratch, size_t scratch_bytes, BlockQ8* xq = nullptr,
+               int64_t xq_stride = 0);
 // Scratch the attention of `pairs` (token, head) pairs over max_keys keys uses (0: none).
 size_t attention_scratch_bytes(int D, int max_keys, int pairs);
 
@@ -135,7 +138,8 @@ bool attention_decode_fused(hipStream_t s, const float* qkv, int64_t stride, flo
                             int H, int KV, int D, float scale, const AttnAddr& a, const float* q_norm,
                             const float* k_norm, float eps, const float* cos_t, const float* sin_t,
                             const int32_t* rpos, const int32_t* seq, const int32_t* kv_row, const int32_t* n_keys,
-                            const KvLayer& kv, int n_ctx, int max_keys);
+                            const KvLayer& kv, int n_ctx, int max_keys, BlockQ8* xq = nullptr,
+                            int64_t xq_stride = 0);
 
 // QK-norm + RoPE on q [n][H*D] and k [n][KV*D] (in place), then k, v quantized into the KV cache (model.cpp:370-392).
 // cos/sin tables [n_pos][D/2].

@@ -13,33 +13,12 @@ namespace {
 
 constexpr int kT = 256;
 
-// One 32-value block of f32 activations -> BlockQ8 (kernels_avx512.cpp:66-80), one block per 32 lanes (a half
-// wavefront): lane l holds value l of the block. amax is an exact max and the half sums are exact integer sums, so the lane order of the reductions does not matter.
-__device__ __forceinline__ void quantize_block_lanes(float v, int l, BlockQ8* out) {
-  float amax = fabsf(v);
-#pragma unroll
-  for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
-  const float d = amax / 127.0f;
-  const float id = d != 0.0f ? 1.0f / d : 0.0f;
-  const int q = cvt_rne(v * id);
-  int s = q;
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) s += __shfl_xor(s, off, 16);
-  int8_t* o = reinterpret_cast<int8_t*>(out);
-  o[8 + l] = (int8_t)sat8(q);
-  if (l == 0) {
-    *reinterpret_cast<float*>(o) = d;
-    *reinterpret_cast<int16_t*>(o + 4) = (int16_t)s;
-  } else if (l == 16) {
-    *reinterpret_cast<int16_t*>(o + 6) = (int16_t)s;
-  }
-}
-
 // One element per thread; x has n * k elements, k % 32 == 0.
 __global__ void k_quantize_q8(const float* __restrict__ x, int64_t total, BlockQ8* __restrict__ y) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
-  quantize_block_lanes(x[i], (int)(i & 31), y + i / 32);
+  const float v[1] = {x[i]};
+  quantize_block_lanes_n<1>(v, (int)(i & 31), y + i / 32);
 }
 
 __global__ void k_quantize_i8(const float* __restrict__ x, int n, int8_t* __restrict__ q, float* __restrict__ d) {
@@ -156,7 +135,8 @@ __global__ void k_silu_mul_q8(const float* __restrict__ gu, int64_t n, int64_t t
   const int64_t gi = interleave4 ? 8 * (c / 4) + c % 4 : c, ui = interleave4 ? gi + 4 : n + c;
   const float x = gu[r * 2 * n + gi];
   const float e = exp512(0.0f - x);
-  quantize_block_lanes((x / (1.0f + e)) * gu[r * 2 * n + ui], (int)(c & 31), xq + i / 32);
+  const float v[1] = {(x / (1.0f + e)) * gu[r * 2 * n + ui]};
+  quantize_block_lanes_n<1>(v, (int)(c & 31), xq + i / 32);
 }
 
 __global__ void k_add(int64_t n, float* __restrict__ x, const float* __restrict__ h) {

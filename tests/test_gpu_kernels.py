@@ -439,7 +439,19 @@ ROWS_CASES = [
     (64, 4, 4, [t % 3 for t in range(40)], [1 + t for t in range(40)], 48),          # G = 1, 3 sequences per block
     (128, 8, 4, [0] * 16, [1840 - t for t in range(16)], 1840),                       # longest rows in LDS
     (128, 8, 4, [0] * 16, [1900 - t for t in range(16)], 1900),                       # per-token kernel
+    (96, 4, 2, [0, 1, 0], [33, 17, 50], 64),                                          # other head size: generic
+    (64, 20, 1, [0, 0], [10, 30], 32),                                                # G = 20: generic
 ]
+
+
+def _check_q8_variant(mk, oracle, call, got):
+    """call(out, xq) runs the _q8 variant of the attention call that produced got ([n][H*D] fp32): its out must equal
+    got bit for bit and its xq the oracle's quantize_acts of got (quant.h:11-16 blocks) byte for byte."""
+    n, k = got.shape
+    out2, xq = mk.alloc(n * k * 4), mk.alloc(n * k // 32 * 40)
+    call(out2.ptr, xq.ptr)
+    assert np.array_equal(bits(out2.download(np.float32).reshape(n, k)), bits(got))
+    assert np.array_equal(xq.download(np.uint8), oracle.quantize_row_q8(got).view(np.uint8).reshape(-1))
 
 
 @pytest.mark.parametrize("case", range(len(ROWS_CASES)))
@@ -461,6 +473,8 @@ def test_attention_batch_vs_oracle(mk, oracle, case):
     mk_.check(L().mk_attention(mk.h, dq.ptr, H * D, out.ptr, H * D, n, H, ctypes.byref(kv), 0, dseq.ptr, dnk.ptr,
                                None, None, max(nks)))
     got = out.download(np.float32).reshape(n, H * D)
+    _check_q8_variant(mk, oracle, lambda o, x: mk_.check(L().mk_attention_q8(
+        mk.h, dq.ptr, H * D, o, H * D, n, H, ctypes.byref(kv), 0, dseq.ptr, dnk.ptr, None, None, max(nks), x)), got)
     # The reference's KV rows: KV heads x D int8, then KV float scales (model.cpp:105-110).
     row = KV * D + 4 * KV
     scale = np.float32(1.0) / np.sqrt(np.float32(D))
@@ -490,7 +504,7 @@ DECODE_CASES = [
 
 
 @pytest.mark.parametrize("case", range(len(DECODE_CASES)))
-def test_attention_decode_fused(mk, case):
+def test_attention_decode_fused(mk, oracle, case):
     """mk_attention_decode == mk_qk_norm_rope_kv + mk_attention: outputs bit for bit, every cache byte identical."""
     D, H, KV, seqs, pos, n_ctx, max_keys = DECODE_CASES[case]
     n, n_seq = len(seqs), max(seqs) + 1
@@ -536,6 +550,14 @@ def test_attention_decode_fused(mk, case):
     for x, y in zip(ba, bb):
         assert np.array_equal(x.download(np.uint8), y.download(np.uint8))
     assert np.array_equal(dqb.download(np.float32), qkv.reshape(-1))  # raw projections untouched
+    # the _q8 variant on a third copy of the cache: same out, same cache bytes, and the BlockQ8 rows of out
+    bc, kvc = cache()
+    _check_q8_variant(mk, oracle, lambda o, x: mk_.check(L().mk_attention_decode_q8(
+        mk.h, dqb.ptr, QKV, n, H, dnorm.ptr, dnorm.offset(D * 4), eps, dcos.ptr, dsin.ptr, meta["rpos"].ptr,
+        meta["seq"].ptr, meta["kv_row"].ptr, meta["n_keys"].ptr, ctypes.byref(kvc), 0, o, H * D, max_keys, x)),
+        outb.download(np.float32).reshape(n, H * D))
+    for x, y in zip(ba, bc):
+        assert np.array_equal(x.download(np.uint8), y.download(np.uint8))
 
 
 # Rows longer than one workgroup's LDS (about 11600 keys at D = 128, 7600 at D = 64): scores in global slots of the
@@ -618,6 +640,9 @@ def _attention_vs_oracle(mk, oracle, spec, seed, name, long_rows):
                                anc_off.ptr if anc_off is not None else None, anc.ptr if anc is not None else None,
                                max_keys))
     got = out.download(np.float32).reshape(n, H * D)
+    _check_q8_variant(mk, oracle, lambda o, x: mk_.check(L().mk_attention_q8(
+        mk.h, dq.ptr, H * D, o, H * D, n, H, ctypes.byref(kv), 0, dseq.ptr, dnk.ptr,
+        anc_off.ptr if anc_off is not None else None, anc.ptr if anc is not None else None, max_keys, x)), got)
     row = KV * D + 4 * KV
     scale = np.float32(1.0) / np.sqrt(np.float32(D))
     for s in sorted(set(seqs)):
