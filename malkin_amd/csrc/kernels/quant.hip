@@ -127,16 +127,24 @@ __global__ void k_silu_mul_rows(float* __restrict__ gu, int64_t n, int64_t total
 
 // gu row: [gate(n) | up(n)], or gate/up interleaved by 4 (row 8k + j: gate 4k + j for j < 4, else up 4k + j - 4)
 // -> silu(gate) * up, quantized; one element per thread, n % 32 == 0.
-__global__ void k_silu_mul_q8(const float* __restrict__ gu, int64_t n, int64_t total, int interleave4,
-                              BlockQ8* __restrict__ xq) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= total) return;
-  const int64_t r = i / n, c = i % n;
-  const int64_t gi = interleave4 ? 8 * (c / 4) + c % 4 : c, ui = interleave4 ? gi + 4 : n + c;
-  const float x = gu[r * 2 * n + gi];
-  const float e = exp512(0.0f - x);
-  const float v[1] = {(x / (1.0f + e)) * gu[r * 2 * n + ui]};
-  quantize_block_lanes_n<1>(v, (int)(c & 31), xq + i / 32);
+// Row r (blockIdx.y), four consecutive outputs c .. c + 3 per thread (16-byte loads of gate and up), so that a Q8
+// block is 8 consecutive lanes. Per element the arithmetic of kernels_avx512.cpp:271-280.
+__global__ void k_silu_mul_q8(const float* __restrict__ gu, int64_t n, int interleave4, BlockQ8* __restrict__ xq) {
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // outputs 4q .. 4q + 3 of the row
+  if (q >= n / 4) return;  // n % 32 == 0: whole 8-lane blocks leave together
+  const int64_t r = blockIdx.y;
+  const float* row = gu + r * 2 * n;
+  // gate values 4q .. 4q + 3 and their up values: [gate | up] rows, or rows interleaved by 4 (8q: gate, 8q + 4: up)
+  const float4 g4 = *reinterpret_cast<const float4*>(row + (interleave4 ? 8 * q : 4 * q));
+  const float4 u4 = *reinterpret_cast<const float4*>(row + (interleave4 ? 8 * q + 4 : n + 4 * q));
+  const float g[4] = {g4.x, g4.y, g4.z, g4.w}, u[4] = {u4.x, u4.y, u4.z, u4.w};
+  float v[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float e = exp512(0.0f - g[k]);
+    v[k] = (g[k] / (1.0f + e)) * u[k];
+  }
+  quantize_block_lanes_n<4>(v, (int)(q & 7), xq + r * (n / 32) + q / 8);
 }
 
 __global__ void k_add(int64_t n, float* __restrict__ x, const float* __restrict__ h) {
@@ -278,9 +286,9 @@ void silu_mul(hipStream_t s, int64_t n, float* g, const float* u) {
 
 void silu_mul_q8(hipStream_t s, const float* gu, int rows, int64_t n, BlockQ8* xq, bool interleave4) {
   require(n % 32 == 0, "silu_mul_q8: n must be a multiple of 32");
-  const int64_t total = (int64_t)rows * n;
-  if (total == 0) return;
-  hipLaunchKernelGGL(k_silu_mul_q8, dim3(grid_for(total, kT)), dim3(kT), 0, s, gu, n, total, interleave4 ? 1 : 0, xq);
+  require(rows <= 65535, "silu_mul_q8: at most 65535 rows per call");
+  if (rows <= 0 || n == 0) return;
+  hipLaunchKernelGGL(k_silu_mul_q8, dim3(grid_for(n / 4, kT), rows), dim3(kT), 0, s, gu, n, interleave4 ? 1 : 0, xq);
   check_launch("silu_mul_q8");
 }
 

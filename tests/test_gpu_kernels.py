@@ -71,14 +71,18 @@ def test_quantize_i8(mk, golden):
     assert np.array_equal(bits(d.download(np.float32)), bits(g["di"]))
 
 
-def test_silu(mk, golden, oracle):
+def test_silu(mk, golden):
     g = golden("quant.npz")
     dg, du = mk.to_device(g["g"]), mk.to_device(g["u"])
     mk_.check(L().mk_silu_mul(mk.h, g["g"].size, dg.ptr, du.ptr))
     assert np.array_equal(bits(dg.download(np.float32)), bits(g["silu"]))
-    # fused silu_mul + quantize of [gate | up] rows
-    rng = np.random.default_rng(2)
-    rows, F = 5, 512
+
+
+# (rows, F): part of one workgroup per row, a row ending in a partial workgroup, a Qwen3-14B-wide row
+@pytest.mark.parametrize("rows,F", [(5, 512), (3, 1056), (2, 17408)])
+def test_silu_mul_q8(mk, oracle, rows, F):
+    """Fused silu_mul + quantize of [gate | up] rows against the oracle, and of the same rows interleaved by 4."""
+    rng = np.random.default_rng(2 + F)
     gu = rng.uniform(-20, 20, (rows, 2 * F)).astype(np.float32)
     dgu = mk.to_device(gu)
     out = mk.alloc(rows * F // 32 * 40)
