@@ -1432,26 +1432,23 @@ __global__ __launch_bounds__(kRowsThreads) void k_attention_rows(const float* __
       const int len = min(C::ck, nkb_pad - j0);  // a multiple of 16
       for (int jj = 0; jj < len; jj += 16) {
         const float pa = sc[ra * nk_pad + j0 + jj + dl], pb = sc[rb * nk_pad + j0 + jj + dl];
-        // key jj + I: its coefficients (lane I of pa / pb's 16-lane row) broadcast by DPP inside each fma
-        [&]<int... I>(std::integer_sequence<int, I...>) __attribute__((always_inline)) {
-          (
-              [&] {
-                float v[C::dl];
-                if constexpr (C::dl == 4) {
-                  const float4 t = *reinterpret_cast<const float4*>(tile + (jj + I) * C::stride);
-                  v[0] = t.x, v[1] = t.y, v[2] = t.z, v[3] = t.w;
-                } else {
-                  const float2 t = *reinterpret_cast<const float2*>(tile + (jj + I) * C::stride);
-                  v[0] = t.x, v[1] = t.y;
-                }
 #pragma unroll
-                for (int k = 0; k < C::dl; ++k) {
-                  acc0[k] = fma_bcast16<I>(pa, v[k], acc0[k]);
-                  acc1[k] = fma_bcast16<I>(pb, v[k], acc1[k]);
-                }
-              }(),
-              ...);
-        }(std::make_integer_sequence<int, 16>{});
+        for (int i = 0; i < 16; ++i) {
+          const float p0 = bcast16(pa, i), p1 = bcast16(pb, i);
+          float v[C::dl];
+          if constexpr (C::dl == 4) {
+            const float4 t = *reinterpret_cast<const float4*>(tile + (jj + i) * C::stride);
+            v[0] = t.x, v[1] = t.y, v[2] = t.z, v[3] = t.w;
+          } else {
+            const float2 t = *reinterpret_cast<const float2*>(tile + (jj + i) * C::stride);
+            v[0] = t.x, v[1] = t.y;
+          }
+#pragma unroll
+          for (int k = 0; k < C::dl; ++k) {
+            acc0[k] = fma_(p0, v[k], acc0[k]);
+            acc1[k] = fma_(p1, v[k], acc1[k]);
+          }
+        }
       }
       if (c + 1 < nch) vstore(c + 1);
       lds_barrier();
