@@ -1342,39 +1342,26 @@ __global__ __launch_bounds__(kRowsThreads) void k_attention_rows(const float* __
       for (int u = 0; u < D / 16; ++u) kw[u] = *reinterpret_cast<const v4i*>(kb + (int64_t)j * a.k_row + 16 * u);
       const float ksv = *reinterpret_cast<const float*>(ksb + (int64_t)j * a.s_row);
       const float vsv = *reinterpret_cast<const float*>(vsb + (int64_t)j * a.s_row);
-      float kf[DC][16];  // kf[c][l] = k[16 c + l]
+      float kf[16][DC];  // kf[l][c] = k[16 c + l]
 #pragma unroll
       for (int l = 0; l < 16; ++l)
 #pragma unroll
         for (int c = 0; c < DC; ++c) {
           const int e = PERM ? DC * l + c : 16 * c + l;  // byte of element 16 c + l
-          kf[c][l] = (float)(int8_t)(kw[e >> 4][(e >> 2) & 3] >> (8 * (e & 3)));
+          kf[l][c] = (float)(int8_t)(kw[e >> 4][(e >> 2) & 3] >> (8 * (e & 3)));
         }
       if (live) vsc[j] = vsv;
       const float kss = ksv * scale;
-      // Row r's q: lane l of every 16-lane row holds q[16 c + l] (c < DC), broadcast to the row's lanes by DPP inside
-      // the chain steps, and the next row's values are loaded while this row's chains run.
-      auto qload = [&](float(&v)[DC], int r) {
-        const float* qr = q + (int64_t)(t0 + r / G) * q_stride + (int64_t)(g * G + r % G) * D + (tid & 15);
-#pragma unroll
-        for (int c = 0; c < DC; ++c) v[c] = qr[16 * c];
-      };
-      float qn[DC];
-      qload(qn, 0);
       for (int r = 0; r < R; ++r) {
-        float qc[DC];
-#pragma unroll
-        for (int c = 0; c < DC; ++c) qc[c] = qn[c];
-        qload(qn, min(r + 1, R - 1));
         if (!((act >> r) & 1)) continue;
+        const float* qr = q + (int64_t)(t0 + r / G) * q_stride + (int64_t)(g * G + r % G) * D;
         float lanes[16];
-        chains8_bcast16<0, true>(qc[0], kf[0], lanes);
-        chains8_bcast16<8, true>(qc[0], kf[0], lanes);
 #pragma unroll
-        for (int c = 1; c < DC; ++c) {
-          chains8_bcast16<0, false>(qc[c], kf[c], lanes);
-          chains8_bcast16<8, false>(qc[c], kf[c], lanes);
-        }
+        for (int l = 0; l < 16; ++l) lanes[l] = qr[l] * kf[l][0];
+#pragma unroll
+        for (int c = 1; c < DC; ++c)
+#pragma unroll
+          for (int l = 0; l < 16; ++l) lanes[l] = fma_(qr[16 * c + l], kf[l][c], lanes[l]);
         const float sres = reduce16(lanes) * kss;
         if (live) sc[r * nk_pad + j] = sres;
       }

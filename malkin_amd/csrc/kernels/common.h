@@ -210,43 +210,6 @@ __device__ __forceinline__ float fma_bcast16(float x, float v, float acc) {
   return acc;
 }
 
-// One step of chains L0 .. L0 + 7 of the 16 lane chains of a dot product (kernels_avx512.cpp:234-244), where every
-// lane holds all 16 chains of its own key: lanes[L0 + i] = fma(q_i, k[L0 + i], lanes[L0 + i]) (MUL: q_i * k[L0 + i]),
-// q_i = lane L0 + i of x's 16-lane row (row_newbcast). One asm statement; it starts with the two wait states a DPP read
-// of x needs after a VALU write of it, and nothing in it writes x.
-#define MK_DPP_STEP(OP, D, S, B) OP " %" #D ", %16, %" #S " row_newbcast:" #B " row_mask:0xf bank_mask:0xf\n\t"
-#define MK_DPP_8(OP, B0, B1, B2, B3, B4, B5, B6, B7)                                                              \
-  "s_nop 1\n\t" MK_DPP_STEP(OP, 0, 8, B0) MK_DPP_STEP(OP, 1, 9, B1) MK_DPP_STEP(OP, 2, 10, B2)                  \
-      MK_DPP_STEP(OP, 3, 11, B3) MK_DPP_STEP(OP, 4, 12, B4) MK_DPP_STEP(OP, 5, 13, B5) MK_DPP_STEP(OP, 6, 14, B6) \
-          MK_DPP_STEP(OP, 7, 15, B7)
-template <int L0, bool MUL>
-__device__ __forceinline__ void chains8_bcast16(float x, const float (&k)[16], float (&lanes)[16]) {
-  static_assert(L0 == 0 || L0 == 8, "two halves of the 16 chains");
-// The products write their outputs only (early-clobber: the statement still reads its inputs after the first write).
-#define MK_DPP_IN                                                                                                    \
-  "v"(k[L0]), "v"(k[L0 + 1]), "v"(k[L0 + 2]), "v"(k[L0 + 3]), "v"(k[L0 + 4]), "v"(k[L0 + 5]), "v"(k[L0 + 6]),       \
-      "v"(k[L0 + 7]), "v"(x)
-#define MK_DPP_OUT(C)                                                                                                \
-  C(lanes[L0]), C(lanes[L0 + 1]), C(lanes[L0 + 2]), C(lanes[L0 + 3]), C(lanes[L0 + 4]), C(lanes[L0 + 5]),            \
-      C(lanes[L0 + 6]), C(lanes[L0 + 7])
-#define MK_RW(v) "+v"(v)
-#define MK_WO(v) "=&v"(v)
-  if constexpr (MUL && L0 == 0)
-    asm volatile(MK_DPP_8("v_mul_f32_dpp", 0, 1, 2, 3, 4, 5, 6, 7) : MK_DPP_OUT(MK_WO) : MK_DPP_IN);
-  else if constexpr (MUL)
-    asm volatile(MK_DPP_8("v_mul_f32_dpp", 8, 9, 10, 11, 12, 13, 14, 15) : MK_DPP_OUT(MK_WO) : MK_DPP_IN);
-  else if constexpr (L0 == 0)
-    asm volatile(MK_DPP_8("v_fmac_f32_dpp", 0, 1, 2, 3, 4, 5, 6, 7) : MK_DPP_OUT(MK_RW) : MK_DPP_IN);
-  else
-    asm volatile(MK_DPP_8("v_fmac_f32_dpp", 8, 9, 10, 11, 12, 13, 14, 15) : MK_DPP_OUT(MK_RW) : MK_DPP_IN);
-#undef MK_WO
-#undef MK_RW
-#undef MK_DPP_OUT
-#undef MK_DPP_IN
-}
-#undef MK_DPP_8
-#undef MK_DPP_STEP
-
 // fma_bcast16<K>, then the SDWA convert of byte B of w into cvt (as i8_to_f32<B>), as one pair of instructions: a
 // chain that converts the next group of values while it runs the current one puts each convert, which does not
 // depend on the chain, in the dependent fma's latency instead of in front of the fma that consumes it.
