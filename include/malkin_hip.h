@@ -220,6 +220,42 @@ int mk_attention_decode_q8(mk_ctx* ctx, const float* qkv, int64_t stride, int n,
 /* Model::move_kv (model.cpp:432-440): row `from` -> row `to` of sequence seq, K and V of every layer. */
 int mk_move_kv(mk_ctx* ctx, const mk_kv_cache* kv, int seq, int from, int to);
 
+/* ---- persistent decode step: the layer loop of Model::run for one token (model.cpp:355-417 at n = 1) ----
+ * Per layer: rmsnorm + q|k|v, QK-norm + RoPE + KV write + attention, attn_output + residual, rmsnorm + gate|up,
+ * silu * up, down + residual; all layers of a step in one launch, one workgroup per CU handing off between the steps
+ * through device counters. Results are bit-identical to the per-step calls (mk_matmul_f32 with norm_w, silu_pairs
+ * and accumulate; mk_attention_decode_q8). */
+typedef struct {
+  mk_weight qkv;     /* MK_Q8_0: q|k|v rows, (n_head + 2 n_head_kv) head_dim x n_embd */
+  mk_weight wo;      /* MK_Q8_0: n_embd x n_head head_dim */
+  mk_weight gate_up; /* MK_Q8_0: 2 n_ff x n_embd, gate/up rows interleaved by 4 (mk_matmul_f32's silu_pairs rows) */
+  mk_weight down;    /* MK_Q8_0: n_embd x n_ff */
+  const float* attn_norm;
+  const float* ffn_norm;
+  const float* q_norm;
+  const float* k_norm;
+} mk_decode_layer;
+typedef struct mk_decode_plan mk_decode_plan;
+/* A plan for one model: device copies of the layer table and of the kernel's argument block, and its hand-off
+   counters (allocated here, once). Device buffers: x [n_embd] (the residual stream, updated in place), qkv
+   [(n_head + 2 n_head_kv) head_dim], att (BlockQ8 rows of n_head head_dim / 32 blocks), h [n_ff]; the token's layout
+   rpos, seq, kv_row, n_keys (one entry each); cos_t / sin_t as for mk_qk_norm_rope_kv. MK_ERR_UNSUPPORTED (no plan)
+   where the kernel does not apply: other weight types, head_dim other than 128, rows of 48 blocks or fewer, more
+   than 16 query heads per KV head, no more CUs than query heads. */
+int mk_decode_plan_create(mk_ctx* ctx, const mk_decode_layer* layers, int n_layer, int n_head, float eps,
+                          const mk_kv_cache* kv, float* x, float* qkv, void* att, float* h, const float* cos_t,
+                          const float* sin_t, const int32_t* rpos, const int32_t* seq, const int32_t* kv_row,
+                          const int32_t* n_keys, mk_decode_plan** plan);
+int mk_decode_plan_destroy(mk_decode_plan* plan);
+/* 1 if mk_decode_layers runs for a token with up to max_keys keys (its LDS holds them), else 0. */
+int mk_decode_supported(const mk_decode_plan* plan, int max_keys);
+/* Queues layers [l0, l1) of one decode step on the context's stream; allocates nothing (graph-capturable). Every
+   cross-workgroup wait inside is bounded; a wait that runs out marks the plan's error word (mk_decode_check). */
+int mk_decode_layers(mk_ctx* ctx, mk_decode_plan* plan, int l0, int l1, int max_keys);
+/* After the stream has been synchronized: MK_OK, or MK_ERR_HIP if a launch since the last check timed out in a
+   hand-off wait (its results are invalid); the error word and the counters are then cleared. */
+int mk_decode_check(mk_ctx* ctx, mk_decode_plan* plan);
+
 /* ---- greedy selection (sampler.cpp:27-30 argmax; engine.cpp:309-318 draft top-2) ---- */
 /* Per row of n_vocab logits: top1 = first maximum, top2 = the reference's runner-up scan. top2 may be NULL. */
 int mk_argmax_top2(mk_ctx* ctx, const float* logits, int rows, int n_vocab, int32_t* top1, int32_t* top2);

@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(HERE, "libmalkin_hip.so")
 
 MK_OK, MK_ERR_INVALID, MK_ERR_HIP, MK_ERR_UNSUPPORTED, MK_ERR_NO_DEVICE = 0, 1, 2, 3, 4
 F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 8, 12, 13, 14, 30
-MODEL_NO_WIDE, MODEL_NO_PACK = 1, 2
+MODEL_NO_WIDE, MODEL_NO_PACK, MODEL_PERSISTENT = 1, 2, 4
 
 BLOCK_Q8 = np.dtype([("d", "<f4"), ("s", "<i2", (2,)), ("qs", "i1", (32,))])
 BATCH_TOKEN = np.dtype([("id", "<i4"), ("seq", "<i4"), ("pos", "<i4"), ("logits", "<i4"), ("kv", "<i4"),
@@ -68,6 +68,12 @@ SIGNATURES = {
     "mk_attention_decode_q8": (_I, [_P, _P, _I64, _I, _I, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I64, _I,
                                     _P]),
     "mk_move_kv": (_I, [_P, _P, _I, _I, _I]),
+    "mk_decode_plan_create": (_I, [_P, _P, _I, _I, _F, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, ctypes.POINTER(_P)]),
+    "mk_decode_plan_destroy": (_I, [_P]),
+    "mk_decode_supported": (_I, [_P, _I]),
+    "mk_decode_layers": (_I, [_P, _P, _I, _I, _I]),
+    "mk_decode_check": (_I, [_P, _P]),
+    "mk_model_persistent": (_I, [_P]),
     "mk_argmax_top2": (_I, [_P, _P, _I, _I, _P, _P]),
     "mk_greedy_advance": (_I, [_P, _P, _P, _P, _P, _P, _P, _P]),
     "mk_argmax_top2_noalloc": (_I, [_P, _P, _I, _I, _P, _P]),
@@ -230,6 +236,12 @@ class MkWeight(ctypes.Structure):
                 ("cols", ctypes.c_int64), ("data", ctypes.c_void_p)]
 
 
+class MkDecodeLayer(ctypes.Structure):
+    _fields_ = [("qkv", MkWeight), ("wo", MkWeight), ("gate_up", MkWeight), ("down", MkWeight),
+                ("attn_norm", ctypes.c_void_p), ("ffn_norm", ctypes.c_void_p), ("q_norm", ctypes.c_void_p),
+                ("k_norm", ctypes.c_void_p)]
+
+
 class MkKvCache(ctypes.Structure):
     _fields_ = [("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("k_scale", ctypes.c_void_p),
                 ("v_scale", ctypes.c_void_p), ("n_layer", ctypes.c_int32), ("n_seq", ctypes.c_int32),
@@ -262,10 +274,11 @@ def gguf_inspect(path):
 class Model:
     """mk_model_* wrapper: the device counterpart of the reference's Model (model.h)."""
 
-    def __init__(self, ctx, path, n_ctx, n_seq=1, wide=True, no_pack=False):
+    def __init__(self, ctx, path, n_ctx, n_seq=1, wide=True, no_pack=False, persistent=False):
         self.ctx = ctx
         p = _P()
-        flags = (0 if wide else MODEL_NO_WIDE) | (MODEL_NO_PACK if no_pack else 0)
+        flags = ((0 if wide else MODEL_NO_WIDE) | (MODEL_NO_PACK if no_pack else 0) |
+                 (MODEL_PERSISTENT if persistent else 0))
         check(load().mk_model_open(ctx.h, path.encode(), n_ctx, n_seq, flags, ctypes.byref(p)))
         self.h = p.value
         c = MkModelConfig()
@@ -282,6 +295,10 @@ class Model:
             self.close()
         except Exception:
             pass
+
+    @property
+    def persistent(self):
+        return bool(load().mk_model_persistent(self.h))
 
     @property
     def weight_bytes(self):

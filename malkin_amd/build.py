@@ -25,6 +25,7 @@ HIP_SOURCES = [
     "csrc/kernels/gemm_kq.hip",
     "csrc/kernels/quant.hip",
     "csrc/kernels/attn.hip",
+    "csrc/kernels/decode.hip",
     "csrc/kernels/rowpath.hip",
     "csrc/kernels/sample.hip",
     "csrc/kernels/capi.cpp",

@@ -114,10 +114,13 @@ int mk_model_open(mk_ctx* ctx, const char* path, int n_ctx, int n_seq, int flags
     auto m = std::make_unique<mk_model>();
     m->file = std::make_unique<malkin_hip::GgufFile>(path);
     m->model = std::make_unique<malkin_hip::Model>(ctx, *m->file, n_ctx, n_seq, (flags & MK_MODEL_NO_WIDE) == 0,
-                                                    (flags & MK_MODEL_NO_PACK) != 0);
+                                                    (flags & MK_MODEL_NO_PACK) != 0,
+                                                    (flags & MK_MODEL_PERSISTENT) != 0);
     *out = m.release();
   });
 }
+
+int mk_model_persistent(const mk_model* m) { return m && m->model && m->model->persistent() ? 1 : 0; }
 
 int mk_model_free(mk_model* m) {
   return run([&] { delete m; });

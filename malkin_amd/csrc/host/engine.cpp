@@ -275,6 +275,7 @@ void Engine::draft_trees() {
     }
     draft_sel_.enqueue(draft_->dev_logits());
     ck(mk_synchronize(c));
+    draft_->check_device();
     draft_sel_.collect();
     for (size_t j = 0; j < p.drawn.size(); ++j) {
       Spec& sp = specs_[static_cast<size_t>(p.drawn[j].second)];
@@ -397,6 +398,7 @@ void Engine::select_tree_rows() {
   if (tree_sel_.empty()) return;
   tree_sel_.enqueue(target_->dev_logits());
   ck(mk_synchronize(target_->ctx()));
+  target_->check_device();
   tree_sel_.collect();
 }
 
@@ -419,6 +421,8 @@ void Engine::step() {
   ck(mk_copy_async(c, picks_h_, target_top_.p, static_cast<size_t>(rows) * sizeof(int32_t)));
   if (drafting) ck(mk_copy_async(c, tree_h_, tree_.p, lanes_.size() * 2 * max_depth_ * sizeof(int32_t)));
   ck(mk_synchronize(c));  // the step's one host wait
+  target_->check_device();
+  if (draft_) draft_->check_device();
   ++steps_;
   sel_.collect();
 

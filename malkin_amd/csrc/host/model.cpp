@@ -249,7 +249,7 @@ bool Model::matmul_group_f32(const Group& g, const float* x, int64_t xs, const f
   return true;
 }
 
-Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide, bool no_pack)
+Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide, bool no_pack, bool persistent)
     : ctx_(ctx), cfg_(read_config(f)), n_ctx_(n_ctx), n_seq_(n_seq), wide_(wide), no_pack_(no_pack) {
   auto& c = cfg_;
   if (c.n_head <= 0 || c.n_head_kv <= 0 || c.head_dim <= 0 || c.head_dim % 32 || c.n_head % c.n_head_kv)
@@ -368,9 +368,37 @@ Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide, bo
     ck(mk_host_alloc(ctx_, layout_words_ * sizeof(int32_t), &h));
     st.host = static_cast<int32_t*>(h);
   }
+  if (persistent) make_decode_plan();
   ck(mk_synchronize(ctx_));
   for (LoadBlock& b : load_) b.release();  // loading is done: the staging ring goes
   load_block_bytes_ = 0;
+}
+
+// The persistent decode kernel takes the layer loop of one-token forwards where every layer has fused Q8_0 groups
+// (q|k|v one buffer, gate|up one interleaved buffer) and the library has a kernel for the shape.
+void Model::make_decode_plan() {
+  const auto& c = cfg_;
+  std::vector<mk_decode_layer> dl(c.n_layer);
+  for (int i = 0; i < c.n_layer; ++i) {
+    const Layer& L = layers_[i];
+    if (L.row_flow || L.qkv.parts.size() != 1 || L.gateup.parts.size() != 1 || !L.gateup.silu_pairs) return;
+    const float* nw = L.norms.as<float>();
+    dl[i] = mk_decode_layer{L.qkv.parts[0].w(), L.wo.w(), L.gateup.parts[0].w(), L.down.w(),
+                            nw,                 nw + c.n_embd, nw + 2 * c.n_embd, nw + 2 * c.n_embd + c.head_dim};
+  }
+  mk_decode_plan* p = nullptr;
+  const int rc = mk_decode_plan_create(ctx_, dl.data(), c.n_layer, c.n_head, c.rms_eps, &kv_, x_.as<float>(),
+                                       qkv_.as<float>(), xq_.p, gu_.as<float>(), rope_cos_.as<float>(),
+                                       rope_sin_.as<float>(), d_rpos_, d_seq_, d_kv_row_, d_n_keys_, &p);
+  if (rc == MK_ERR_UNSUPPORTED) return;
+  ck(rc);
+  dplan_ = p;
+}
+
+void Model::check_device() {
+  if (!dplan_pending_) return;
+  dplan_pending_ = false;
+  ck(mk_decode_check(ctx_, dplan_));
 }
 
 void Model::LoadBlock::release() {
@@ -383,6 +411,7 @@ void Model::LoadBlock::release() {
 
 Model::~Model() {
   if (!staging_.empty()) (void)mk_synchronize(ctx_);
+  if (dplan_) (void)mk_decode_plan_destroy(dplan_);
   for (Staging& st : staging_) {
     (void)mk_event_free(st.done);
     (void)mk_host_free(ctx_, st.host);
@@ -556,7 +585,13 @@ void Model::run() {
   void* xq = xq_.p;
   const mk_kv_cache& kv = kv_;
   ck(mk_dequantize_rows(ctx_, embd_type_, embd_rows_.p, embd_row_bytes_, d_ids_, n, E, x));
-  for (int il = 0; il < c.n_layer; ++il) {
+  // One token: every layer in one persistent launch (same results as the per-step launches below).
+  const bool persistent = dplan_ && n == 1 && !lay_.tree && mk_decode_supported(dplan_, lay_.max_keys);
+  if (persistent) {
+    ck(mk_decode_layers(ctx_, dplan_, 0, c.n_layer, lay_.max_keys));
+    dplan_pending_ = true;
+  }
+  for (int il = 0; il < (persistent ? 0 : c.n_layer); ++il) {
     const Layer& L = layers_[il];
     const float* norms = L.norms.as<float>();
     if (L.row_flow) {
@@ -704,6 +739,7 @@ void Model::forward(const BatchToken* batch, int n, float* logits) {
     ck(mk_download(ctx_, logits, logits_.p, lay_.logit_rows.size() * static_cast<size_t>(cfg_.n_vocab) * sizeof(float)));
   else
     ck(mk_synchronize(ctx_));
+  check_device();
 }
 
 void Model::enqueue(const BatchToken* batch, int n, const int32_t* id_from, const int32_t* dev_ids, int32_t* dev_top1,
@@ -733,6 +769,7 @@ void Model::forward_top2(const BatchToken* batch, int n, int32_t* top1, int32_t*
   if (m > 0 && top1) ck(mk_download(ctx_, top1, d1, m * sizeof(int32_t)));
   if (m > 0 && top2) ck(mk_download(ctx_, top2, d2, m * sizeof(int32_t)));
   if (m == 0 || (!top1 && !top2)) ck(mk_synchronize(ctx_));
+  check_device();
 }
 
 void Model::forward(const int32_t* tokens, int n, int pos, float* logits, bool all_logits, const int* parent,
@@ -744,6 +781,7 @@ void Model::forward(const int32_t* tokens, int n, int pos, float* logits, bool a
     ck(mk_download(ctx_, logits, logits_.p, lay_.logit_rows.size() * static_cast<size_t>(cfg_.n_vocab) * sizeof(float)));
   else
     ck(mk_synchronize(ctx_));
+  check_device();
 }
 
 void Model::move_kv(int from, int to, int seq) {
@@ -791,6 +829,7 @@ void Model::generate_greedy(const int32_t* prompt, int n_prompt, int n_gen, int 
   ck(mk_argmax_top2(ctx_, logits_.as<float>(), 1, cfg_.n_vocab, d_top1, nullptr));
   int32_t first = 0;
   ck(mk_download(ctx_, &first, d_top1, sizeof first));
+  check_device();
   if (st) st->prefill_ms = ms_since(t0);
   out[0] = first;
   if (n_gen == 1) return;
@@ -832,6 +871,7 @@ void Model::generate_greedy(const int32_t* prompt, int n_prompt, int n_gen, int 
       for (int i = 0; i < seg; ++i) step();
     }
     ck(mk_download(ctx_, toks.data() + done, d_tokens, seg * sizeof(int32_t)));
+    check_device();
     done += seg;
   }
   if (st) {

@@ -79,7 +79,8 @@ class Model {
   // wide: the reference's wide Q6_K prefill panels are packed (Engine packs them when RAM allows,
   // engine.cpp:130-145); MALKIN_NO_WIDE turns them off there.
   // no_pack: every matmul on the reference's row path over GGUF rows (its MALKIN_NO_PACK, model.cpp:136).
-  Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq = 1, bool wide = true, bool no_pack = false);
+  Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq = 1, bool wide = true, bool no_pack = false,
+        bool persistent = false);
   ~Model();
   const ModelConfig& cfg() const { return cfg_; }
   int n_ctx() const { return n_ctx_; }
@@ -121,6 +122,10 @@ class Model {
 
   // Bytes of packed weights resident in HBM, and the GGUF bytes of the matmul weights one decode token reads.
   size_t weight_bytes() const { return weight_bytes_; }
+  // Whether one-token forwards run the persistent decode kernel (mk_decode_layers); after a host wait on the model's
+  // stream, check_device() raises if one of its launches since the last check timed out in a hand-off wait.
+  bool persistent() const { return dplan_ != nullptr; }
+  void check_device();
   // Packed matmul weight: which = 0 qkv, 1 wo, 2 gate|up, 3 down of `layer`; 4 the LM head.
   mk_weight weight(int layer, int which) const;
 
@@ -189,6 +194,7 @@ class Model {
   void upload_layout(const int32_t* dev_ids = nullptr);
   void run();
   void run_row_layer(const Layer& L, int il);
+  void make_decode_plan();
   void check_ids();
 
   mk_ctx* ctx_;
@@ -220,6 +226,8 @@ class Model {
 
   // Activations for kMaxBatch tokens.
   DevBuf x_, qkv_, att_, gu_, xq_, logits_, top_;
+  mk_decode_plan* dplan_ = nullptr;  // the persistent decode kernel's plan (all layers Q8_0, fused groups)
+  bool dplan_pending_ = false;       // launched since the last check_device()
   DevBuf h_;  // fp32 normalized rows of the row-path layers (kDevBatch x n_embd)
 };
 

@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <memory>
 #include <vector>
 
 #include "ctx.h"
@@ -465,3 +466,113 @@ int mk_topk(mk_ctx* c, const float* logits, int64_t stride, const int32_t* rows,
 }
 
 }  // extern "C"
+
+struct mk_decode_plan {
+  mk::DecodeDims d{};
+  int n_layer = 0;
+  void* layers = nullptr;  // device mk::DecodeLayer[n_layer]
+  void* args = nullptr;    // device argument block
+  unsigned* sync = nullptr;
+  size_t sync_bytes = 0;
+};
+
+namespace {
+
+void decode_plan_free(mk_decode_plan* p) {
+  if (!p) return;
+  if (p->layers) (void)hipFree(p->layers);
+  if (p->args) (void)hipFree(p->args);
+  if (p->sync) (void)hipFree(p->sync);
+  delete p;
+}
+
+}  // namespace
+
+int mk_decode_plan_create(mk_ctx* c, const mk_decode_layer* layers, int n_layer, int n_head, float eps,
+                          const mk_kv_cache* kv, float* x, float* qkv, void* att, float* h, const float* cos_t,
+                          const float* sin_t, const int32_t* rpos, const int32_t* seq, const int32_t* kv_row,
+                          const int32_t* n_keys, mk_decode_plan** out) {
+  return guard([&] {
+    require(c && layers && n_layer > 0 && kv && out && n_layer <= kv->n_layer, "mk_decode_plan_create: bad arguments");
+    *out = nullptr;
+    mk::DecodeDims d{};
+    d.E = (int)layers[0].wo.rows;
+    d.H = n_head;
+    d.KV = kv->n_head_kv;
+    d.D = kv->head_dim;
+    d.F = (int)layers[0].down.cols;
+    d.n_ctx = kv->n_ctx;
+    d.n_seq = kv->n_seq;
+    d.eps = eps;
+    const int64_t QKV = (int64_t)(d.H + 2 * d.KV) * d.D;
+    std::vector<mk::DecodeLayer> dl(n_layer);
+    for (int i = 0; i < n_layer; ++i) {
+      const mk_decode_layer& L = layers[i];
+      const bool shapes = L.qkv.type == MK_Q8_0 && L.wo.type == MK_Q8_0 && L.gate_up.type == MK_Q8_0 &&
+                          L.down.type == MK_Q8_0 && L.qkv.rows == QKV && L.qkv.cols == d.E && L.wo.rows == d.E &&
+                          L.wo.cols == (int64_t)d.H * d.D && L.gate_up.rows == 2 * (int64_t)d.F &&
+                          L.gate_up.cols == d.E && L.down.rows == d.E && L.down.cols == d.F;
+      if (!shapes) throw mk::Error(MK_ERR_UNSUPPORTED, "mk_decode_plan_create: weights other than Q8_0 / bad shapes");
+      require(L.attn_norm && L.ffn_norm && L.q_norm && L.k_norm, "mk_decode_plan_create: missing norm weights");
+      dl[i] = mk::DecodeLayer{L.qkv.data,   L.wo.data,     L.gate_up.data, L.down.data,
+                              L.attn_norm,  L.ffn_norm,    L.q_norm,       L.k_norm};
+    }
+    // Keys are bounded by the context; the smallest row (one key) must fit for the plan to be of any use.
+    if (!mk::decode_layers_supported(d, 1))
+      throw mk::Error(MK_ERR_UNSUPPORTED, "mk_decode_plan_create: no persistent decode kernel for this model shape");
+    std::unique_ptr<mk_decode_plan, void (*)(mk_decode_plan*)> p(new mk_decode_plan, decode_plan_free);
+    p->d = d;
+    p->n_layer = n_layer;
+    p->sync_bytes = mk::decode_sync_bytes(n_layer);
+    check(hipMalloc(&p->layers, sizeof(mk::DecodeLayer) * n_layer), "hipMalloc");
+    check(hipMalloc(&p->args, mk::decode_args_bytes()), "hipMalloc");
+    check(hipMalloc(reinterpret_cast<void**>(&p->sync), p->sync_bytes), "hipMalloc");
+    check(hipMemcpy(p->layers, dl.data(), sizeof(mk::DecodeLayer) * n_layer, hipMemcpyHostToDevice), "hipMemcpy");
+    check(hipMemset(p->sync, 0, p->sync_bytes), "hipMemset");
+    mk::DecodeBufs b{};
+    b.layers = static_cast<const mk::DecodeLayer*>(p->layers);
+    b.kv0 = mk::KvLayer{kv->k, kv->v, kv->k_scale, kv->v_scale};
+    b.x = x, b.qkv = qkv, b.att = att, b.h = h;
+    b.cos_t = cos_t, b.sin_t = sin_t, b.rpos = rpos, b.seq = seq, b.kv_row = kv_row, b.n_keys = n_keys;
+    b.sync = p->sync;
+    // About one poll per microsecond: a wait gives up after about half a second.
+    b.spin_max = 1u << 19;
+    mk::decode_set_args(p->args, d, b);
+    *out = p.release();
+  });
+}
+
+int mk_decode_plan_destroy(mk_decode_plan* p) {
+  return guard([&] {
+    if (p) check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    decode_plan_free(p);
+  });
+}
+
+int mk_decode_supported(const mk_decode_plan* p, int max_keys) {
+  if (!p) return 0;
+  int ok = 0;
+  (void)guard([&] { ok = mk::decode_layers_supported(p->d, max_keys) ? 1 : 0; });
+  return ok;
+}
+
+int mk_decode_layers(mk_ctx* c, mk_decode_plan* p, int l0, int l1, int max_keys) {
+  return guard([&] {
+    require(c && p && l0 >= 0 && l1 > l0 && l1 <= p->n_layer, "mk_decode_layers: bad layer range");
+    mk::decode_layers(c->stream, p->args, p->d, l0, l1, max_keys);
+  });
+}
+
+int mk_decode_check(mk_ctx* c, mk_decode_plan* p) {
+  return guard([&] {
+    require(c && p, "mk_decode_check: no plan");
+    unsigned err = 0;
+    const unsigned* word = p->sync + mk::decode_error_word(p->n_layer);
+    check(hipMemcpy(&err, word, sizeof err, hipMemcpyDeviceToHost), "hipMemcpy");
+    if (err != 0) {
+      // Some workgroup may have left without resetting the counters: clear them and the error word.
+      check(hipMemset(p->sync, 0, p->sync_bytes), "hipMemset");
+      throw mk::Error(MK_ERR_HIP, "mk_decode_layers: a hand-off wait timed out (results of the step are invalid)");
+    }
+  });
+}

@@ -318,6 +318,23 @@ __device__ __forceinline__ float half_to_float(uint16_t h) {
 // Signed 8-bit dot of 4-byte groups: exact int32.
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// A BlockQ8 held in LDS as 10 words {d, s0 | s1 << 16, qs[32]}: the exact int dot of its 32 quants with 32 int8
+// weights given as two 16-byte planes (lo = weights 0..15, hi = 16..31), and its fields.
+__device__ __forceinline__ int dot8(const uint4& lo, const uint4& hi, const int* xq) {
+  int ai = dot4((int)lo.x, xq[2], 0);
+  ai = dot4((int)lo.y, xq[3], ai);
+  ai = dot4((int)lo.z, xq[4], ai);
+  ai = dot4((int)lo.w, xq[5], ai);
+  ai = dot4((int)hi.x, xq[6], ai);
+  ai = dot4((int)hi.y, xq[7], ai);
+  ai = dot4((int)hi.z, xq[8], ai);
+  ai = dot4((int)hi.w, xq[9], ai);
+  return ai;
+}
+__device__ __forceinline__ float xd(const int* xq) { return __int_as_float(xq[0]); }
+__device__ __forceinline__ int xs0(const int* xq) { return (int)(int16_t)(xq[1] & 0xFFFF); }
+__device__ __forceinline__ int xs1(const int* xq) { return (int)(int16_t)((uint32_t)xq[1] >> 16); }
+
 // _mm512_cvtps_epi32 under the default MXCSR (round to nearest even), then saturation to int8.
 __device__ __forceinline__ int cvt_rne(float x) {
   if (!(x >= -2147483648.0f && x < 2147483648.0f)) return INT32_MIN;
@@ -360,6 +377,47 @@ __device__ __forceinline__ void quantize_block_lanes_n(const float (&v)[N], int 
   } else if (l == LB / 2) {
     *reinterpret_cast<int16_t*>(o + 6) = (int16_t)s;
   }
+}
+
+// Device-coherent 4-byte accesses (relaxed atomics at agent scope: global loads and stores with sc1, which bypass the
+// per-XCD caches). Data that one workgroup stores this way is read correctly by a workgroup on another XCD once the
+// writer's stores have completed (s_waitcnt) before it signals, and the reader reads after seeing the signal.
+__device__ __forceinline__ uint32_t ld_coh_u32(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coh(const float* p) {
+  return __builtin_bit_cast(float, ld_coh_u32(reinterpret_cast<const uint32_t*>(p)));
+}
+__device__ __forceinline__ void st_coh_u32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh(float* p, float v) {
+  st_coh_u32(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v));
+}
+
+// quantize_block_lanes_n<1> (one value per lane, 32 lanes per block, l = d % 32) writing the block at blk0 + d / 32
+// with coherent word stores: lane 0 the scale, lane 1 the two half sums, lanes 2..9 the quants of lanes 4 (l - 2) ..
+// 4 (l - 2) + 3. The 32 lanes of a block must call this together.
+__device__ __forceinline__ void put_q8_coh(BlockQ8* blk0, int d, float v) {
+  const int l = d & 31;
+  float amax = fabsf(v);
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+  const float dq = amax / 127.0f;
+  const float id = dq != 0.0f ? 1.0f / dq : 0.0f;
+  const int q = cvt_rne(v * id);
+  int s = q;
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) s += __shfl_xor(s, off, 16);
+  const int b = (int)(uint32_t)(uint8_t)(int8_t)sat8(q);
+  const int src = 4 * (l >= 2 && l < 10 ? l - 2 : 0);
+  const uint32_t quad = (uint32_t)__shfl(b, src, 32) | (uint32_t)__shfl(b, src + 1, 32) << 8 |
+                        (uint32_t)__shfl(b, src + 2, 32) << 16 | (uint32_t)__shfl(b, src + 3, 32) << 24;
+  const int s_hi = __shfl(s, 16, 32);
+  const uint32_t word = l == 0 ? __builtin_bit_cast(uint32_t, dq)
+                        : l == 1 ? ((uint32_t)(uint16_t)(int16_t)s | (uint32_t)(uint16_t)(int16_t)s_hi << 16)
+                                 : quad;
+  if (l < 10) st_coh_u32(reinterpret_cast<uint32_t*>(blk0 + d / 32) + l, word);
 }
 
 // Value d of an attention output row (row[d] = v) and, with xq, its BlockQ8 row as quantize_acts writes it

@@ -99,23 +99,6 @@ __device__ __forceinline__ Raw load_unit(const uint8_t* W, int64_t rows, int64_t
   return w;
 }
 
-// x block in LDS: 10 dwords = BlockQ8 {d, s0|s1, qs[32]}.
-__device__ __forceinline__ int dot8(const uint4& lo, const uint4& hi, const int* xq) {
-  int ai = dot4((int)lo.x, xq[2], 0);
-  ai = dot4((int)lo.y, xq[3], ai);
-  ai = dot4((int)lo.z, xq[4], ai);
-  ai = dot4((int)lo.w, xq[5], ai);
-  ai = dot4((int)hi.x, xq[6], ai);
-  ai = dot4((int)hi.y, xq[7], ai);
-  ai = dot4((int)hi.z, xq[8], ai);
-  ai = dot4((int)hi.w, xq[9], ai);
-  return ai;
-}
-
-__device__ __forceinline__ float xd(const int* xq) { return __int_as_float(xq[0]); }
-__device__ __forceinline__ int xs0(const int* xq) { return (int)(int16_t)(xq[1] & 0xFFFF); }
-__device__ __forceinline__ int xs1(const int* xq) { return (int)(int16_t)((uint32_t)xq[1] >> 16); }
-
 enum : int { kProQ8 = 0, kProF32 = 1, kProNorm = 2 };
 enum : int { kEpiStore = 0, kEpiSilu = 1 };
 constexpr int kProPass = 2;  // fp32 prologues: 2 x 256 threads x 16 values = up to 8192 columns

@@ -141,6 +141,57 @@ bool attention_decode_fused(hipStream_t s, const float* qkv, int64_t stride, flo
                             const KvLayer& kv, int n_ctx, int max_keys, BlockQ8* xq = nullptr,
                             int64_t xq_stride = 0);
 
+// The weights of one decoder layer for the persistent decode kernel: Q8_0 packed q|k|v rows (H + 2 KV heads of D), the
+// attn_output rows, gate|up rows interleaved by 4 (matmul_f32's silu_pairs layout) and the down rows; the layer's
+// norm weights.
+struct DecodeLayer {
+  const void* qkv;
+  const void* wo;
+  const void* gate_up;
+  const void* down;
+  const float* attn_norm;
+  const float* ffn_norm;
+  const float* q_norm;
+  const float* k_norm;
+};
+// Layers [l0, l1) of a one-token decode step (model.cpp:355-417 at n = 1) in one persistent launch, one workgroup
+// per CU: x += every layer's attention and FFN, with the same results as the per-step launches (matmul_f32 with the
+// rmsnorm / silu / residual forms, attention_decode_fused with BlockQ8 output). The kernel's argument block lives in
+// device memory (decode_args_bytes), written once by decode_set_args:
+//   layers   device array of the model's layers;
+//   kv0      layer 0 of the cache (KV heads, n_ctx rows per head, n_seq sequences);
+//   qkv [(H + 2 KV) D], att (BlockQ8 [H D / 32]), h [F]: the step's scratch rows;
+//   rpos, seq, kv_row, n_keys: the token's layout on the device (one entry each);
+//   sync     decode_sync_bytes(layers per launch) bytes, zero before the first launch (each launch leaves them zero).
+// A wait longer than spin_max polls sets the error word (word decode_error_word(layers per launch) of sync): the
+// launch's results are then invalid.
+struct DecodeDims {
+  int E, H, KV, D, F, n_ctx, n_seq;
+  float eps;
+};
+struct DecodeBufs {
+  const DecodeLayer* layers;
+  KvLayer kv0;
+  float* x;
+  float* qkv;
+  void* att;
+  float* h;
+  const float* cos_t;
+  const float* sin_t;
+  const int32_t* rpos;
+  const int32_t* seq;
+  const int32_t* kv_row;
+  const int32_t* n_keys;
+  unsigned* sync;
+  unsigned spin_max;
+};
+bool decode_layers_supported(const DecodeDims& d, int max_keys);
+size_t decode_sync_bytes(int n_layer);
+size_t decode_error_word(int n_layer);
+size_t decode_args_bytes();
+void decode_set_args(void* dev_args, const DecodeDims& d, const DecodeBufs& b);
+void decode_layers(hipStream_t s, const void* dev_args, const DecodeDims& d, int l0, int l1, int max_keys);
+
 // QK-norm + RoPE on q [n][H*D] and k [n][KV*D] (in place), then k, v quantized into the KV cache (model.cpp:370-392).
 // cos/sin tables [n_pos][D/2].
 void qk_norm_rope_kv(hipStream_t s, float* q, float* k, const float* v, int64_t stride, int n, int H, int KV, int D,
