@@ -37,20 +37,19 @@ constexpr int kDT = 512;                  // threads per workgroup (two waves pe
 constexpr int kSubs = kDT / 256;          // GEMV sub-units per workgroup
 constexpr int kR = 8;                     // rows per packed group
 constexpr int kChunk = 48;                // blocks per chunk (k_gemv's measured best at one token)
-constexpr int kWk = 192;                  // worker lanes per sub-unit
-constexpr int kP = kChunk * kR / kWk;     // (row, block) pairs per worker lane and chunk
 constexpr int kG = 8;                     // blocks per chain step group
 constexpr int kLane = (kChunk + kG) * 2 + 4;  // term floats per row: the chunk's (dot, scale) pairs + read-ahead + pad
 constexpr int kSlot = kR * kLane;
 constexpr int kSteps = 5;                 // per layer
 constexpr int kCtr = 32;                  // words per counter (128 bytes)
 constexpr int kMaxSlots = 8;              // V staging tasks per attention thread (keys up to LDS capacity)
-static_assert(kChunk * kR % kWk == 0 && kChunk % kG == 0, "chunk shape");
-
-struct Raw8 {
-  uint4 a, b;
-  uint32_t s;
-};
+constexpr int kMaxRing = 4;               // weight chunk slots per sub-unit (3 where LDS is short), filled by direct
+                                          // global -> LDS copies
+constexpr int kStaticLds = 8 * 1024;      // bound on the kernel's static LDS (checked against the build in the tests)
+constexpr int kChunkQ = kChunk * 256;     // quant bytes of a chunk (one 8-row group, 48 blocks)
+constexpr int kChunkBytes = kChunkQ + kChunk * 16;  // + its scales
+constexpr int kCopies = 5;                // copies per worker wave and chunk: 4 x 1 KB of quants, 256 B of scales
+static_assert(kChunk == 3 * 16 && kChunk % kG == 0, "three worker waves take 16 blocks of a chunk each");
 
 // A pointer read from the argument block points to global memory: saying so lets loads and stores through it (and
 // through pointers derived from it) use global instructions with a scalar base instead of flat ones.
@@ -58,7 +57,6 @@ template <typename T>
 __device__ __forceinline__ T* glob(T* p) {
   return (T*)((__attribute__((address_space(1))) T*)p);
 }
-
 
 // A GEMV step over one packed Q8_0 weight (rows x nu blocks), taken by workgroups [wlo, wlo + nw).
 struct Gs {
@@ -83,36 +81,45 @@ __device__ __forceinline__ Gs make_gs(const void* W, int rows, int cols, int wlo
   return g;
 }
 
-// Chunk p of sub-unit su's share of step S: its pairs (row f % 8, block f / 8 of the chunk) for f = wi + 192 k.
-// Blocks past the row's end re-read its last block (unused).
-// Offsets as in PackedQ8_0 (layout.h), in 32 bits: a packed weight here is far below 4 GB.
-__device__ __forceinline__ void load_chunk(Raw8 (&r)[kP], const Gs& S, int su, int p, int wi) {
-  const uint32_t g = (uint32_t)(su + (p / S.nc) * (kSubs * S.nw));
-  const int cc = p % S.nc;
-  const uint8_t* W = glob(S.W);
-  const uint32_t scales0 = (uint32_t)S.ng * (uint32_t)S.nu * 256u;
-#pragma unroll
-  for (int k = 0; k < kP; ++k) {
-    const int f = wi + k * kWk;
-    const uint32_t gu = g * (uint32_t)S.nu + (uint32_t)min(cc * kChunk + f / kR, S.nu - 1);
-    const uint32_t q = gu * 256u + (uint32_t)(f % kR) * 16u;
-    r[k].a = *reinterpret_cast<const uint4*>(W + q);
-    r[k].b = *reinterpret_cast<const uint4*>(W + q + 128u);
-    r[k].s = *reinterpret_cast<const uint16_t*>(W + scales0 + gu * 16u + (uint32_t)(f % kR) * 2u);
-  }
+// Direct global -> LDS copies (as lds_copy16 / lds_copy4 in common.h) from a scalar base and a 32-bit lane offset:
+// lane i reads sbase + voff_i and writes LDS l + 16 i (4 i). sbase and l are wave-uniform here but derived from the
+// thread index, so they are taken from the first lane.
+template <typename T>
+__device__ __forceinline__ const T* uniform_ptr(const T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<const T*>((uint64_t)hi << 32 | lo);
 }
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void copy16s(const void* sbase, uint32_t voff, void* l) {
+  const uint32_t a = __builtin_amdgcn_readfirstlane(lds_addr(l));
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(uniform_ptr(sbase)),
+               "s"(a) : "m0");
+}
+__device__ __forceinline__ void copy4s(const void* sbase, uint32_t voff, void* l) {
+  const uint32_t a = __builtin_amdgcn_readfirstlane(lds_addr(l));
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(uniform_ptr(sbase)),
+               "s"(a) : "m0");
+}
+#pragma clang diagnostic pop
 
-// Position p of a sub-unit's load stream in step S (nq chunks): chunk p of S, then the first two chunks of the next
-// GEMV step N (nn chunks there, as sub-unit sun), or where there are none a re-read of S's last chunk. Every path
-// issues the same loads, so the compiler's wait counts stay exact.
-__device__ __forceinline__ void load_pos(Raw8 (&r)[kP], const Gs& S, int su, int nq, const Gs& N, int sun, int nn,
-                                         int p, int wi) {
-  if (p < nq)
-    load_chunk(r, S, su, p, wi);
-  else if (nn > 0)
-    load_chunk(r, N, sun, p - nq, wi);
-  else
-    load_chunk(r, S, su, nq - 1, wi);
+// Worker wave ww (0..2) of sub-unit su copies its share of chunk p of step S into the LDS slot: quants 1 KB pieces
+// 4 ww .. 4 ww + 3 (piece k = blocks 4k .. 4k + 3 of the chunk, 256 bytes each, in the packed order: lo plane, hi
+// plane), and scales 256-byte piece ww (blocks 16 ww .. 16 ww + 15). The quants of a row's last chunk run on into
+// the next group's blocks, or for the last group into the scales stream (at least a chunk long: decode_ring checks
+// it), never used; scale reads past the row's end re-read its last block. Offsets as in PackedQ8_0 (layout.h), in 32
+// bits: a packed weight here is far below 4 GB.
+__device__ __forceinline__ void copy_chunk(const Gs& S, int su, int p, int ww, int lane, uint8_t* slot) {
+  const uint32_t g = (uint32_t)(su + (p / S.nc) * (kSubs * S.nw));
+  const int u0 = (p % S.nc) * kChunk;
+  const uint8_t* W = glob(S.W);
+  const uint8_t* q = W + (g * (uint32_t)S.nu + (uint32_t)u0) * 256u;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) copy16s(q, (uint32_t)((4 * ww + j) * 1024 + lane * 16), slot + (4 * ww + j) * 1024);
+  const uint8_t* sc = W + (uint32_t)S.ng * (uint32_t)S.nu * 256u + g * (uint32_t)S.nu * 16u;
+  const uint32_t u = (uint32_t)min(u0 + 16 * ww + lane / 4, S.nu - 1);
+  copy4s(sc, u * 16u + (uint32_t)(lane % 4) * 4u, slot + kChunkQ + ww * 256);
 }
 
 // The per-model constants of the kernel, in device memory (written once per model): they are read where used through
@@ -205,41 +212,49 @@ __device__ __forceinline__ void signal_step(const DecodeArgs* P, int sid) {
 enum : int { kInNorm = 0, kInQ8 = 1, kInF32 = 2 };
 enum : int { kOutStore = 0, kOutAcc = 1, kOutSilu = 2 };
 
-// LDS of a GEMV step: the input's BlockQ8 row (xs), four sub-units' double-buffered term slots, and an fp32 staging
-// area (the rmsnorm's transposed row, or an fp32 input row read with coalesced loads before it is quantized).
+// LDS of a GEMV step: the input's BlockQ8 row (xs), the two sub-units' double-buffered term slots, an fp32 staging
+// area (the rmsnorm's transposed row, or a batch of an fp32 input row read with coalesced loads before it is
+// quantized), and the sub-units' weight rings (RING chunk slots each). Only the rings stay live across steps.
 struct GemvLds {
   int* xs;
   float* res;
   float* tr;
+  uint8_t* ring;
 };
-__host__ __device__ constexpr size_t gemv_stage_floats(int max_cols, int E) {
-  return (size_t)16 * sumsq_tstride(E / 16) > (size_t)max_cols ? (size_t)16 * sumsq_tstride(E / 16) : (size_t)max_cols;
-}
+constexpr int kLB = 8;                          // 16-byte pieces per loader thread and batch
+constexpr int kLoaders = kSubs * 64;            // the chain waves
+constexpr int kStageF = kLB * kLoaders * 4;     // fp32 values per input batch
 __host__ __device__ constexpr size_t gemv_xs_bytes(int max_cols) { return ((size_t)(max_cols / 32) * 40 + 15) & ~15; }
-__host__ __device__ constexpr size_t gemv_lds_bytes(int max_cols, int E) {
-  return gemv_xs_bytes(max_cols) + (size_t)kSubs * 2 * kSlot * 4 + gemv_stage_floats(max_cols, E) * 4;
+__host__ __device__ constexpr size_t gemv_stage_floats(int E) { return (size_t)E > (size_t)kStageF ? E : kStageF; }
+__host__ __device__ constexpr size_t gemv_ring_offset(int max_cols, int E) {
+  return gemv_xs_bytes(max_cols) + (size_t)kSubs * 2 * kSlot * 4 + gemv_stage_floats(E) * 4;
 }
-__device__ __forceinline__ GemvLds gemv_lds(int max_cols) {
+__host__ __device__ constexpr size_t gemv_lds_bytes(int max_cols, int E, int ring) {
+  return gemv_ring_offset(max_cols, E) + (size_t)kSubs * ring * kChunkBytes;
+}
+__device__ __forceinline__ GemvLds gemv_lds(int max_cols, int E) {
   extern __shared__ int smem[];
   GemvLds l;
   l.xs = smem;
   l.res = reinterpret_cast<float*>(smem + gemv_xs_bytes(max_cols) / 4);
   l.tr = l.res + kSubs * 2 * kSlot;
+  l.ring = reinterpret_cast<uint8_t*>(smem) + gemv_ring_offset(max_cols, E);
   return l;
 }
 
-// The loader threads' share of n4 16-byte pieces of the coherent array in: batches of kLB pieces per thread, all of a
-// batch's loads issued before the first is used (one memory round trip per batch), then use(i4, piece).
-constexpr int kLB = 8;
+// The loader threads' share of n4 16-byte pieces of the coherent array in (from piece p0): batches of kLB pieces per
+// thread, all of a batch's loads issued before the first is used (one memory round trip per batch), then
+// use(i4, piece) with i4 counted from p0.
 template <typename F>
-__device__ __forceinline__ void load_pieces(const void* in, int n4, int li, int loaders, F&& use) {
-  for (int base = 0; base < n4; base += kLB * loaders) {
+__device__ __forceinline__ void load_pieces(const void* in, int p0, int n4, int li, F&& use) {
+  for (int base = 0; base < n4; base += kLB * kLoaders) {
     float4 v[kLB];
 #pragma unroll
-    for (int k = 0; k < kLB; ++k) v[k] = ld_coh16(in, 16u * (uint32_t)min(base + li + k * loaders, n4 - 1));
+    for (int k = 0; k < kLB; ++k)
+      v[k] = ld_coh16(in, 16u * (uint32_t)(p0 + min(base + li + k * kLoaders, n4 - 1)));
 #pragma unroll
     for (int k = 0; k < kLB; ++k)
-      if (base + li + k * loaders < n4) use(base + li + k * loaders, v[k]);
+      if (base + li + k * kLoaders < n4) use(base + li + k * kLoaders, v[k]);
   }
 }
 
@@ -254,122 +269,172 @@ __device__ __forceinline__ void gemv_input(const GemvLds& l, const void* in, con
   const int tid = threadIdx.x, wv = tid >> 6;
   const bool loader = (wv & 3) == 0;
   const int li = (wv >> 2) * 64 + (tid & 63);  // loader index
-  constexpr int kLoaders = kSubs * 64;
   const int nq8 = cols / 32;
   BlockQ8* xb = reinterpret_cast<BlockQ8*>(l.xs);
   if constexpr (IN == kInNorm) {
+    // rmsnorm (model.cpp:46-49): the 16 lane chains of kern::dot_f32 (lane c: x[c], x[16 + c], ... in order) over a
+    // transposed copy tt[c][j] = x[16 j + c] (sumsq_lane_chain's layout: four values per LDS read), then the halving
+    // tree. The row is loaded in order into tr, transposed into tt (the xs and term-slot area, unused until the
+    // quantization below), and tr is read again for the scaling. The norm weights are loaded first: they are ready
+    // by the time the scaling needs them.
     const int per = cols / 16, tstride = sumsq_tstride(per), padded = sumsq_padded(per);
-    // tr[c][j] = x[16 j + c] (the 16 lane chains' values in order), zero past the row.
-    if (loader)
-      load_pieces(in, cols / 4, li, kLoaders, [&](int i4, const float4& v) {
-        const int i = 4 * i4, j = i >> 4, c = i & 15;
-        l.tr[c * tstride + j] = v.x;
-        l.tr[(c + 1) * tstride + j] = v.y;
-        l.tr[(c + 2) * tstride + j] = v.z;
-        l.tr[(c + 3) * tstride + j] = v.w;
-      });
-    for (int i = cols + tid; i < 16 * padded; i += kDT) l.tr[(i & 15) * tstride + (i >> 4)] = 0.0f;
-    __shared__ float scale_s;
-    lds_barrier();
-    if (tid < 16) {
-      float acc = sumsq_lane_chain(l.tr + tid * tstride, per);
-      acc = reduce16_lanes(acc);
-      if (tid == 0) scale_s = 1.0f / sqrtf(acc / (float)cols + eps);
-    }
-    lds_barrier();
-    const float sc = scale_s;
-    for (int c16 = tid; c16 < per; c16 += kDT) {
-      float wv[16], yv[16];
+    float wv[16];
+    const int c16 = tid;  // per <= kDT: one half-block per thread
+    if (c16 < per) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const float4 w4 = reinterpret_cast<const float4*>(nw + 16 * c16)[k];
         wv[4 * k] = w4.x, wv[4 * k + 1] = w4.y, wv[4 * k + 2] = w4.z, wv[4 * k + 3] = w4.w;
       }
+    }
+    if (loader)
+      load_pieces(in, 0, cols / 4, li, [&](int i4, const float4& v) { reinterpret_cast<float4*>(l.tr)[i4] = v; });
+    float* tt = reinterpret_cast<float*>(l.xs);
+    lds_barrier();
+    for (int i = tid; i < 16 * padded; i += kDT) tt[(i & 15) * tstride + (i >> 4)] = i < cols ? l.tr[i] : 0.0f;
+    __shared__ float scale_s;
+    lds_barrier();
+    if (tid < 16) {
+      float acc = sumsq_lane_chain(tt + tid * tstride, per);
+      acc = reduce16_lanes(acc);
+      if (tid == 0) scale_s = 1.0f / sqrtf(acc / (float)cols + eps);
+    }
+    lds_barrier();
+    const float sc = scale_s;
+    if (c16 < per) {
+      float yv[16];
 #pragma unroll
-      for (int c = 0; c < 16; ++c) yv[c] = l.tr[c * tstride + c16] * sc * wv[c];
+      for (int k = 0; k < 4; ++k) {
+        const float4 x4 = reinterpret_cast<const float4*>(l.tr + 16 * c16)[k];
+        yv[4 * k] = x4.x, yv[4 * k + 1] = x4.y, yv[4 * k + 2] = x4.z, yv[4 * k + 3] = x4.w;
+      }
+#pragma unroll
+      for (int c = 0; c < 16; ++c) yv[c] = yv[c] * sc * wv[c];
       quantize_half_block(yv, c16 & 1, true, xb + c16 / 2);
     }
   } else if constexpr (IN == kInQ8) {
     // nq8 * 40 bytes: whole 16-byte pieces (nq8 even), and the odd one's last 8 bytes by a 4-byte pair.
     if (loader) {
-      load_pieces(in, nq8 * 10 / 4, li, kLoaders,
-                  [&](int i4, const float4& v) { reinterpret_cast<float4*>(l.xs)[i4] = v; });
+      load_pieces(in, 0, nq8 * 10 / 4, li, [&](int i4, const float4& v) { reinterpret_cast<float4*>(l.xs)[i4] = v; });
       for (int i = (nq8 * 10 / 4) * 4 + li; i < nq8 * 10; i += kLoaders)
         l.xs[i] = (int)ld_coh_u32(static_cast<const uint32_t*>(in) + i);
     }
   } else {
-    // Coalesced coherent loads into the staging area, then 16 consecutive values per lane from LDS.
-    if (loader)
-      load_pieces(in, cols / 4, li, kLoaders,
-                  [&](int i4, const float4& v) { reinterpret_cast<float4*>(l.tr)[i4] = v; });
-    lds_barrier();
-    for (int c16 = tid; c16 < 2 * nq8; c16 += kDT) {
-      float v[16];
-      const float4* p4 = reinterpret_cast<const float4*>(l.tr + 16 * c16);
+    // Batches of kStageF values: coalesced coherent loads into the staging area, then 16 consecutive values per lane.
+    for (int b0 = 0; b0 < cols; b0 += kStageF) {
+      const int nb = min(kStageF, cols - b0);
+      if (loader)
+        load_pieces(in, b0 / 4, nb / 4, li, [&](int i4, const float4& v) { reinterpret_cast<float4*>(l.tr)[i4] = v; });
+      lds_barrier();
+      for (int c16 = tid; c16 < nb / 16; c16 += kDT) {
+        float v[16];
+        const float4* p4 = reinterpret_cast<const float4*>(l.tr + 16 * c16);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float4 a = p4[k];
-        v[4 * k] = a.x, v[4 * k + 1] = a.y, v[4 * k + 2] = a.z, v[4 * k + 3] = a.w;
+        for (int k = 0; k < 4; ++k) {
+          const float4 a = p4[k];
+          v[4 * k] = a.x, v[4 * k + 1] = a.y, v[4 * k + 2] = a.z, v[4 * k + 3] = a.w;
+        }
+        quantize_half_block(v, c16 & 1, true, xb + (b0 / 16 + c16) / 2);
       }
-      quantize_half_block(v, c16 & 1, true, xb + c16 / 2);
+      lds_barrier();
     }
+    return;
   }
   lds_barrier();
 }
 
-// Worker terms of chunk c (blocks c * 48 ...): per pair the exact int dot and dw * dx, zero past the row.
-__device__ __forceinline__ void gemv_dots(const Raw8 (&raw)[kP], float* slot, const int* xs, int c, int nu, int wi) {
+// Worker terms of chunk c (blocks c * 48 ...) from its ring slot: per (block, row) the exact int dot and dw * dx, zero
+// past the row. Worker wave ww takes blocks 16 ww .. 16 ww + 15, four per step; lane l reads the 16 bytes at 16 l of
+// the step's four blocks (block l / 16, plane (l / 8) % 2, row l % 8: whole 1 KB, no bank conflicts) and computes the
+// int dot of its plane with its half of the block's Q8 activations; the lo-plane lane adds the hi lane's partial
+// (lane + 8 of its 16-lane row) and writes the terms. Int sums are exact in any order.
+__device__ __forceinline__ void gemv_dots(const uint8_t* slot, float* terms, const int* xs, int c, int nu, int ww,
+                                          int lane) {
+  const int r = lane & 7, h = (lane >> 3) & 1;
 #pragma unroll
-  for (int k = 0; k < kP; ++k) {
-    const int f = wi + k * kWk;
-    const int ul = f / kR, r = f % kR;
+  for (int k = 0; k < 4; ++k) {
+    const int ul = 16 * ww + 4 * k + (lane >> 4);
     const int u = c * kChunk + ul;
     const bool live = u < nu;
-    const float dw = half_to_float((uint16_t)raw[k].s);
+    const uint4 w = *reinterpret_cast<const uint4*>(slot + ul * 256 + (lane & 15) * 16);
     const int* xq = xs + (live ? u : 0) * 10;
-    *reinterpret_cast<float2*>(slot + r * kLane + ul * 2) =
-        live ? make_float2((float)dot8(raw[k].a, raw[k].b, xq), dw * xd(xq)) : make_float2(0.0f, 0.0f);
+    const uint2 x0 = *reinterpret_cast<const uint2*>(xq + 2 + 4 * h);
+    const uint2 x1 = *reinterpret_cast<const uint2*>(xq + 4 + 4 * h);
+    int part = dot4((int)w.x, (int)x0.x, 0);
+    part = dot4((int)w.y, (int)x0.y, part);
+    part = dot4((int)w.z, (int)x1.x, part);
+    part = dot4((int)w.w, (int)x1.y, part);
+    const int hi = __builtin_amdgcn_update_dpp(0, part, 0x108, 0xF, 0xF, false);  // row_shl:8
+    if (h == 0) {
+      const float dw = half_to_float(*reinterpret_cast<const uint16_t*>(slot + kChunkQ + ul * 16 + r * 2));
+      *reinterpret_cast<float2*>(terms + r * kLane + ul * 2) =
+          live ? make_float2((float)(part + hi), dw * xd(xq)) : make_float2(0.0f, 0.0f);
+    }
   }
 }
 
-// One GEMV step of this workgroup (step id sid, its input step sid - 1). ra / rb are the sub-unit's register sets
-// and pf says which holds chunk 0 of this step (0: ra, 1: rb, -1: not loaded). N: the sub-unit's next GEMV step
-// (n_ok false: none), whose first two chunks the loop loads after this step's last. Returns pf for N.
-template <int IN, int OUT>
-__device__ __forceinline__ int gemv_step(const DecodeArgs* P, int n_steps, int sid, const Gs& S, const Gs& N,
-                                         bool n_ok, Raw8 (&ra)[kP], Raw8 (&rb)[kP], int pf, const void* in,
-                                         const float* nw, int cols, int max_cols, float* y) {
-  const int tid = threadIdx.x, w = blockIdx.x, wv = tid >> 6, sub = wv >> 2;
+// Target of the copies that carry nothing: every worker wave issues kCopies copies per position of its copy stream,
+// so that the explicit wait counts stay exact.
+__shared__ __align__(16) uint8_t g_junk[1024];
+
+// Where a sub-unit's weight ring (RING slots) stands between steps: base = slot of the next step's chunk 0; ready = the
+// copies of that step's first RING - 1 chunks have been issued (by the previous step's last iterations).
+struct Ring {
+  int base;
+  int ready;
+};
+
+// One GEMV step of this workgroup (step id sid; its input is step sid - 1's output). N: the sub-unit's next GEMV step
+// (n_ok false: none), whose first chunks the last iterations copy into the ring. Returns the ring state for N.
+template <int IN, int OUT, int RING>
+__device__ __forceinline__ Ring gemv_step(const DecodeArgs* P, int n_steps, int sid, const Gs& S, const Gs& N,
+                                          bool n_ok, Ring rs, const void* in, const float* nw, int cols,
+                                          int max_cols, int E, float* y) {
+  const int tid = threadIdx.x, w = blockIdx.x, wv = tid >> 6, sub = wv >> 2, lane = tid & 63;
   const bool worker = (wv & 3) != 0;
-  const int wi = (tid & 255) - 64;
+  const int ww = (wv & 3) - 1;
   const int su = S.su_of(w, sub), nq = S.nq_of(su);
   const int nq_wg = S.nq_of(S.su_of(w, 0));
   const int sun = n_ok ? N.su_of(w, sub) : -1, nn = n_ok ? N.nq_of(sun) : 0;
-  const int pf_next = nn > 0 ? (nq > 0 ? (nq & 1) : 0) : -1;
+  const GemvLds l = gemv_lds(max_cols, E);
+  uint8_t* ring = l.ring + sub * RING * kChunkBytes;
+  auto slot = [&](int p) { return ring + ((rs.base + p) % RING) * kChunkBytes; };
+  auto copy_junk = [&](const Gs& G) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) copy16s(glob(G.W), (uint32_t)lane * 16u, g_junk);
+    copy4s(glob(G.W), (uint32_t)lane * 16u, g_junk);
+  };
+  // Position p of the sub-unit's copy stream: chunk p of S, then N's chunks, then nothing.
+  auto issue = [&](int p) {
+    if (p < nq)
+      copy_chunk(S, su, p, ww, lane, slot(p));
+    else if (p - nq < nn)
+      copy_chunk(N, sun, p - nq, ww, lane, slot(p));
+    else
+      copy_junk(S);
+  };
   if (worker) {
     if (nq > 0) {
-      if (pf < 0) {
-        load_pos(ra, S, su, nq, N, sun, nn, 0, wi);
-        load_pos(rb, S, su, nq, N, sun, nn, 1, wi);
-      } else if (pf == 1) {
-        const Raw8 t0 = ra[0], t1 = ra[1];
-        ra[0] = rb[0], ra[1] = rb[1];
-        rb[0] = t0, rb[1] = t1;
-      }
+      if (!rs.ready)
+        for (int p = 0; p < RING - 1; ++p) issue(p);
     } else if (nn > 0) {
-      load_chunk(ra, N, sun, 0, wi);
-      load_chunk(rb, N, sun, 1, wi);
+      for (int p = 0; p < RING - 1; ++p) {
+        if (p < nn)
+          copy_chunk(N, sun, p, ww, lane, slot(p));
+        else
+          copy_junk(N);
+      }
     }
   }
+  const Ring next = nq > 0 ? Ring{(rs.base + nq) % RING, nn > 0} : Ring{rs.base, nn > 0};
   if (nq_wg == 0) {
     signal_step(P, sid);
-    return pf_next;
+    return next;
   }
   wait_step(P, n_steps, sid - 1);
-  const GemvLds l = gemv_lds(max_cols);
   gemv_input<IN>(l, in, nw, opaque(P)->eps, cols);
 
-  float* slots = l.res + sub * 2 * kSlot;
+  float* terms = l.res + sub * 2 * kSlot;
   const int cr = tid & 255;
   const bool chain_lane = !worker && cr < kR && nq > 0;
   float acc = 0.0f, xr = 0.0f;
@@ -380,7 +445,7 @@ __device__ __forceinline__ int gemv_step(const DecodeArgs* P, int n_steps, int s
     const int g = su + (q / S.nc) * (kSubs * S.nw);
     if (OUT == kOutAcc && c == 0) xr = ld_coh(y + g * kR + cr);  // the residual, read early
     const int cn = min(kChunk, S.nu - c * kChunk);
-    const float4* e = reinterpret_cast<const float4*>(slots + (q & 1) * kSlot + cr * kLane);
+    const float4* e = reinterpret_cast<const float4*>(terms + (q & 1) * kSlot + cr * kLane);
     float4 T0[4], T1[4];
     auto fetch = [&](float4(&T)[4], int ul0) {
 #pragma unroll
@@ -421,45 +486,38 @@ __device__ __forceinline__ int gemv_step(const DecodeArgs* P, int n_steps, int s
     }
   };
 
+  // Iteration q: the workers wait for their copies of chunk q (the RING - 2 chunks after it may be in flight), and
+  // after the barrier refill the slot of chunk q - 1 (its dots are done) with position q + RING - 1 and compute
+  // chunk q's terms, while the chain wave runs chunk q - 1's chains.
   if (!worker) __builtin_amdgcn_s_setprio(2);
-  for (int q = 0; q < nq_wg; q += 2) {
+  for (int q = 0; q < nq_wg; ++q) {
+    if (worker && q < nq) wait_vm<kCopies * (RING - 2)>();
+    lds_barrier();
     if (worker) {
       if (q < nq) {
-        gemv_dots(ra, slots + (q & 1) * kSlot, l.xs, q % S.nc, S.nu, wi);
-        load_pos(ra, S, su, nq, N, sun, nn, q + 2, wi);
+        issue(q + RING - 1);
+        gemv_dots(slot(q), terms + (q & 1) * kSlot, l.xs, q % S.nc, S.nu, ww, lane);
       }
     } else if (q > 0 && q - 1 < nq) {
       chain(q - 1);
     }
-    lds_barrier();
-    if (q + 1 < nq_wg) {
-      if (worker) {
-        if (q + 1 < nq) {
-          gemv_dots(rb, slots + ((q + 1) & 1) * kSlot, l.xs, (q + 1) % S.nc, S.nu, wi);
-          load_pos(rb, S, su, nq, N, sun, nn, q + 3, wi);
-        }
-      } else if (q < nq) {
-        chain(q);
-      }
-      lds_barrier();
-    }
   }
+  lds_barrier();
   if (nq == nq_wg) chain(nq - 1);
   if (!worker) {
     __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's output stores have completed
   }
   signal_step(P, sid);
-  return pf_next;
+  return next;
 }
 
-template <int D, int NSLOT>
+template <int D, int NSLOT, int RING>
 __global__ __launch_bounds__(kDT) void k_decode_layers(const DecodeArgs* __restrict__ P, int l0, int l1) {
   const int w = blockIdx.x, tid = threadIdx.x;
   const int G = (int)gridDim.x;
   const int n_steps = (l1 - l0) * kSteps;
-  Raw8 ra[kP], rb[kP];
-  int pf = -1;
+  Ring rs{0, 0};
   for (int il = l0; il < l1; ++il) {
     const int s0 = (il - l0) * kSteps;
     const bool last = il + 1 == l1;
@@ -470,10 +528,9 @@ __global__ __launch_bounds__(kDT) void k_decode_layers(const DecodeArgs* __restr
 
     // q|k|v = W_qkv . rmsnorm(x); the attention workgroups load nothing ahead across their attention step (they load
     // their attn_output chunks right after it).
-    pf = gemv_step<kInNorm, kOutStore>(P, n_steps, s0, make_gs(glob(opaque(L)->qkv), QKV, E, 0, G),
-                                       make_gs(glob(opaque(L)->wo), E, HD, 0, G), !is_att, ra, rb, pf,
-                                       glob(opaque(P)->x), glob(opaque(L)->attn_norm), E, max_cols,
-                                       glob(opaque(P)->qkv));
+    rs = gemv_step<kInNorm, kOutStore, RING>(P, n_steps, s0, make_gs(glob(opaque(L)->qkv), QKV, E, 0, G),
+                                       make_gs(glob(opaque(L)->wo), E, HD, 0, G), !is_att, rs, glob(opaque(P)->x),
+                                       glob(opaque(L)->attn_norm), E, max_cols, E, glob(opaque(P)->qkv));
 
     // Attention: QK-norm, RoPE, the KV row write and attention of one query head; BlockQ8 output rows.
     if (is_att) {
@@ -489,27 +546,23 @@ __global__ __launch_bounds__(kDT) void k_decode_layers(const DecodeArgs* __restr
                                             glob(Q->n_keys), 1, H, f, glob(Q->att), 0,
                                             [&] { poll_step(P, n_steps, s0); });
       __builtin_amdgcn_s_waitcnt(0);
-      // Nothing was loaded ahead for the next GEMV step; clearing the register sets here also ends their lifetime
-      // before the attention code (which needs the registers) on this path.
-      ra[0] = ra[1] = rb[0] = rb[1] = Raw8{};
-      pf = -1;
+      rs.ready = 0;  // the attention's LDS overlaps the rings: nothing was copied ahead
     }
     signal_step(P, s0 + 1);
 
     // x += W_o . att
-    pf = gemv_step<kInQ8, kOutAcc>(P, n_steps, s0 + 2, make_gs(glob(opaque(L)->wo), E, HD, 0, G),
-                                   make_gs(glob(opaque(L)->gate_up), 2 * F, E, 0, G), true, ra, rb, pf,
-                                   glob(opaque(P)->att), nullptr, HD, max_cols, glob(opaque(P)->x));
+    rs = gemv_step<kInQ8, kOutAcc, RING>(P, n_steps, s0 + 2, make_gs(glob(opaque(L)->wo), E, HD, 0, G),
+                                   make_gs(glob(opaque(L)->gate_up), 2 * F, E, 0, G), true, rs, glob(opaque(P)->att),
+                                   nullptr, HD, max_cols, E, glob(opaque(P)->x));
     // h = silu(gate) * up of W_gate|up . rmsnorm(x)
-    pf = gemv_step<kInNorm, kOutSilu>(P, n_steps, s0 + 3, make_gs(glob(opaque(L)->gate_up), 2 * F, E, 0, G),
-                                      make_gs(glob(opaque(L)->down), E, F, 0, G), true, ra, rb, pf,
-                                      glob(opaque(P)->x), glob(opaque(L)->ffn_norm), E, max_cols,
-                                      glob(opaque(P)->h));
+    rs = gemv_step<kInNorm, kOutSilu, RING>(P, n_steps, s0 + 3, make_gs(glob(opaque(L)->gate_up), 2 * F, E, 0, G),
+                                      make_gs(glob(opaque(L)->down), E, F, 0, G), true, rs, glob(opaque(P)->x),
+                                      glob(opaque(L)->ffn_norm), E, max_cols, E, glob(opaque(P)->h));
     // x += W_down . h; then the next layer's q|k|v
     const void* next_qkv = last ? glob(opaque(L)->qkv) : glob(opaque(L + 1)->qkv);
-    pf = gemv_step<kInF32, kOutAcc>(P, n_steps, s0 + 4, make_gs(glob(opaque(L)->down), E, F, 0, G),
-                                    make_gs(next_qkv, QKV, E, 0, G), !last, ra, rb, pf, glob(opaque(P)->h), nullptr,
-                                    F, max_cols, glob(opaque(P)->x));
+    rs = gemv_step<kInF32, kOutAcc, RING>(P, n_steps, s0 + 4, make_gs(glob(opaque(L)->down), E, F, 0, G),
+                                    make_gs(next_qkv, QKV, E, 0, G), !last, rs, glob(opaque(P)->h), nullptr, F,
+                                    max_cols, E, glob(opaque(P)->x));
   }
 
   // The last workgroup to leave resets the counters (every workgroup has finished its waits by then, and its signals
@@ -538,10 +591,28 @@ bool decode_layers_supported(const DecodeDims& d, int max_keys) {
   // two chunks relies on it): more than 48 blocks per row.
   if (d.E / 32 <= kChunk || (d.H * d.D) / 32 <= kChunk || d.F / 32 <= kChunk) return false;
   if (max_keys <= 0 || max_keys > d.n_ctx || !dec_fits(d.D, max_keys, kDT, kMaxSlots)) return false;
-  const int max_cols = std::max(std::max(d.E, d.H * d.D), d.F);
-  const size_t lds = std::max(gemv_lds_bytes(max_cols, d.E), dec_lds_bytes(d.D, attn_keys_pad(max_keys)));
   // The attention step takes H of the workgroups (one per CU).
-  return lds <= 160 * 1024 - 1024 && device_cus() >= d.H;
+  return decode_ring(d, max_keys) >= 3 && device_cus() >= d.H;
+}
+
+// Weight ring depth for a model and key count: 4 slots where LDS allows, else 3 (0: the step does not fit). A step's
+// copy stream runs ring - 1 chunks ahead, into the next GEMV step only: every sub-unit's share of a step (whole rows:
+// at least one row's chunks) has at least ring - 1 chunks.
+int decode_ring(const DecodeDims& d, int max_keys) {
+  const int max_cols = std::max(std::max(d.E, d.H * d.D), d.F);
+  // A row's last chunk of quants may run on into the scales stream (E rows is the smallest weight: at least a chunk)
+  if ((size_t)d.E / 8 * (size_t)(d.E / 32) * 16 < (size_t)kChunkQ) return 0;
+  // rmsnorm: one half-block per thread; the transposed row fits in the xs and term-slot area
+  if (d.E / 16 > kDT ||
+      (size_t)16 * sumsq_tstride(d.E / 16) * 4 > gemv_xs_bytes(max_cols) + (size_t)kSubs * 2 * kSlot * 4)
+    return 0;
+  const int min_cols = std::min(std::min(d.E, d.H * d.D), d.F);
+  const int min_chunks = (min_cols / 32 + kChunk - 1) / kChunk;
+  for (int ring = std::min(kMaxRing, min_chunks + 1); ring >= 3; --ring) {
+    const size_t lds = std::max(gemv_lds_bytes(max_cols, d.E, ring), dec_lds_bytes(d.D, attn_keys_pad(max_keys)));
+    if (lds + kStaticLds <= 160 * 1024) return ring;
+  }
+  return 0;
 }
 
 size_t decode_args_bytes() { return sizeof(DecodeArgs); }
@@ -565,17 +636,21 @@ void decode_layers(hipStream_t s, const void* dev_args, const DecodeDims& d, int
   require(decode_layers_supported(d, max_keys), "decode_layers: unsupported shape");
   require(l0 >= 0 && l1 > l0, "decode_layers: bad layer range");
   const int max_cols = std::max(std::max(d.E, d.H * d.D), d.F);
-  const size_t lds = std::max(gemv_lds_bytes(max_cols, d.E), dec_lds_bytes(d.D, attn_keys_pad(max_keys)));
+  const int ring = decode_ring(d, max_keys);
+  const size_t lds = std::max(gemv_lds_bytes(max_cols, d.E, ring), dec_lds_bytes(d.D, attn_keys_pad(max_keys)));
   const int cus = device_cus();
   const DecodeArgs* P = static_cast<const DecodeArgs*>(dev_args);
   auto go = [&](auto kernel) {
     static bool attr = false;
     if (!attr) {
       check(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                160 * 1024 - 1024),
+                                160 * 1024 - kStaticLds),
             "hipFuncSetAttribute");
       attr = true;
     }
+    hipFuncAttributes fa{};
+    check(hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(kernel)), "hipFuncGetAttributes");
+    require(fa.sharedSizeBytes <= (size_t)kStaticLds, "decode_layers: static LDS above its bound");
     int per_cu = 0;
     check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kDT, lds),
           "hipOccupancyMaxActiveBlocksPerMultiprocessor");
@@ -584,14 +659,15 @@ void decode_layers(hipStream_t s, const void* dev_args, const DecodeDims& d, int
     hipLaunchKernelGGL(kernel, dim3(cus), dim3(kDT), lds, s, P, l0, l1);
   };
   const int slots = dec_slots(d.D, max_keys, true, kDT);
+  auto pick = [&](auto k4, auto k3) { ring == 4 ? go(k4) : go(k3); };
   if (slots <= 2)
-    go(k_decode_layers<128, 2>);
+    pick(k_decode_layers<128, 2, 4>, k_decode_layers<128, 2, 3>);
   else if (slots <= 4)
-    go(k_decode_layers<128, 4>);
+    pick(k_decode_layers<128, 4, 4>, k_decode_layers<128, 4, 3>);
   else if (slots <= 6)
-    go(k_decode_layers<128, 6>);
+    pick(k_decode_layers<128, 6, 4>, k_decode_layers<128, 6, 3>);
   else
-    go(k_decode_layers<128, kMaxSlots>);
+    pick(k_decode_layers<128, kMaxSlots, 4>, k_decode_layers<128, kMaxSlots, 3>);
   check_launch("decode_layers");
 }
 

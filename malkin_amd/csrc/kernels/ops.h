@@ -186,6 +186,7 @@ struct DecodeBufs {
   unsigned spin_max;
 };
 bool decode_layers_supported(const DecodeDims& d, int max_keys);
+int decode_ring(const DecodeDims& d, int max_keys);
 size_t decode_sync_bytes(int n_layer);
 size_t decode_error_word(int n_layer);
 size_t decode_args_bytes();
