@@ -49,6 +49,7 @@ constexpr int kStaticLds = 8 * 1024;      // bound on the kernel's static LDS (c
 constexpr int kChunkQ = kChunk * 256;     // quant bytes of a chunk (one 8-row group, 48 blocks)
 constexpr int kChunkBytes = kChunkQ + kChunk * 16;  // + its scales
 constexpr int kCopies = 5;                // copies per worker wave and chunk: 4 x 1 KB of quants, 256 B of scales
+constexpr int kWarm = 3;                  // chunks after the ring's first brought into L2 while the input is prepared
 static_assert(kChunk == 3 * 16 && kChunk % kG == 0, "three worker waves take 16 blocks of a chunk each");
 
 // A pointer read from the argument block points to global memory: saying so lets loads and stores through it (and
@@ -92,15 +93,13 @@ __device__ __forceinline__ const T* uniform_ptr(const T* p) {
 }
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void copy16s(const void* sbase, uint32_t voff, void* l) {
-  const uint32_t a = __builtin_amdgcn_readfirstlane(lds_addr(l));
+__device__ __forceinline__ void copy16s(const void* sbase, uint32_t voff, uint32_t l) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(uniform_ptr(sbase)),
-               "s"(a) : "m0");
+               "s"(__builtin_amdgcn_readfirstlane(l)) : "m0");
 }
-__device__ __forceinline__ void copy4s(const void* sbase, uint32_t voff, void* l) {
-  const uint32_t a = __builtin_amdgcn_readfirstlane(lds_addr(l));
+__device__ __forceinline__ void copy4s(const void* sbase, uint32_t voff, uint32_t l) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(uniform_ptr(sbase)),
-               "s"(a) : "m0");
+               "s"(__builtin_amdgcn_readfirstlane(l)) : "m0");
 }
 #pragma clang diagnostic pop
 
@@ -109,17 +108,20 @@ __device__ __forceinline__ void copy4s(const void* sbase, uint32_t voff, void* l
 // plane), and scales 256-byte piece ww (blocks 16 ww .. 16 ww + 15). The quants of a row's last chunk run on into
 // the next group's blocks, or for the last group into the scales stream (at least a chunk long: decode_ring checks
 // it), never used; scale reads past the row's end re-read its last block. Offsets as in PackedQ8_0 (layout.h), in 32
-// bits: a packed weight here is far below 4 GB.
-__device__ __forceinline__ void copy_chunk(const Gs& S, int su, int p, int ww, int lane, uint8_t* slot) {
+// bits: a packed weight here is far below 4 GB. slot: the LDS address of the slot. WARM: the same reads, every one
+// into the 1 KB at slot (never read): they only bring the chunk into the L2 cache ahead of its real copies.
+template <bool WARM = false>
+__device__ __forceinline__ void copy_chunk(const Gs& S, int su, int p, int ww, int lane, uint32_t slot) {
   const uint32_t g = (uint32_t)(su + (p / S.nc) * (kSubs * S.nw));
   const int u0 = (p % S.nc) * kChunk;
   const uint8_t* W = glob(S.W);
   const uint8_t* q = W + (g * (uint32_t)S.nu + (uint32_t)u0) * 256u;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) copy16s(q, (uint32_t)((4 * ww + j) * 1024 + lane * 16), slot + (4 * ww + j) * 1024);
+  for (int j = 0; j < 4; ++j)
+    copy16s(q, (uint32_t)((4 * ww + j) * 1024 + lane * 16), WARM ? slot : slot + (4 * ww + j) * 1024);
   const uint8_t* sc = W + (uint32_t)S.ng * (uint32_t)S.nu * 256u + g * (uint32_t)S.nu * 16u;
   const uint32_t u = (uint32_t)min(u0 + 16 * ww + lane / 4, S.nu - 1);
-  copy4s(sc, u * 16u + (uint32_t)(lane % 4) * 4u, slot + kChunkQ + ww * 256);
+  copy4s(sc, u * 16u + (uint32_t)(lane % 4) * 4u, WARM ? slot : slot + kChunkQ + ww * 256);
 }
 
 // The per-model constants of the kernel, in device memory (written once per model): they are read where used through
@@ -348,28 +350,38 @@ __device__ __forceinline__ void gemv_input(const GemvLds& l, const void* in, con
 // the step's four blocks (block l / 16, plane (l / 8) % 2, row l % 8: whole 1 KB, no bank conflicts) and computes the
 // int dot of its plane with its half of the block's Q8 activations; the lo-plane lane adds the hi lane's partial
 // (lane + 8 of its 16-lane row) and writes the terms. Int sums are exact in any order.
+// All of a call's LDS reads (16 per lane: within the 15 the LDS counter can track once the first is consumed) are
+// issued before the first dot, so their latencies overlap.
 __device__ __forceinline__ void gemv_dots(const uint8_t* slot, float* terms, const int* xs, int c, int nu, int ww,
                                           int lane) {
   const int r = lane & 7, h = (lane >> 3) & 1;
+  uint4 w[4];
+  uint2 x0[4], x1[4];
+  uint16_t dh[4];
+  float dx[4];
+  bool live[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int ul = 16 * ww + 4 * k + (lane >> 4);
     const int u = c * kChunk + ul;
-    const bool live = u < nu;
-    const uint4 w = *reinterpret_cast<const uint4*>(slot + ul * 256 + (lane & 15) * 16);
-    const int* xq = xs + (live ? u : 0) * 10;
-    const uint2 x0 = *reinterpret_cast<const uint2*>(xq + 2 + 4 * h);
-    const uint2 x1 = *reinterpret_cast<const uint2*>(xq + 4 + 4 * h);
-    int part = dot4((int)w.x, (int)x0.x, 0);
-    part = dot4((int)w.y, (int)x0.y, part);
-    part = dot4((int)w.z, (int)x1.x, part);
-    part = dot4((int)w.w, (int)x1.y, part);
+    live[k] = u < nu;
+    const int* xq = xs + (live[k] ? u : 0) * 10;
+    w[k] = *reinterpret_cast<const uint4*>(slot + ul * 256 + (lane & 15) * 16);
+    x0[k] = *reinterpret_cast<const uint2*>(xq + 2 + 4 * h);
+    x1[k] = *reinterpret_cast<const uint2*>(xq + 4 + 4 * h);
+    dh[k] = *reinterpret_cast<const uint16_t*>(slot + kChunkQ + ul * 16 + r * 2);
+    dx[k] = xd(xq);
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int ul = 16 * ww + 4 * k + (lane >> 4);
+    int part = dot4((int)w[k].x, (int)x0[k].x, 0);
+    part = dot4((int)w[k].y, (int)x0[k].y, part);
+    part = dot4((int)w[k].z, (int)x1[k].x, part);
+    part = dot4((int)w[k].w, (int)x1[k].y, part);
     const int hi = __builtin_amdgcn_update_dpp(0, part, 0x108, 0xF, 0xF, false);  // row_shl:8
-    if (h == 0) {
-      const float dw = half_to_float(*reinterpret_cast<const uint16_t*>(slot + kChunkQ + ul * 16 + r * 2));
-      *reinterpret_cast<float2*>(terms + r * kLane + ul * 2) =
-          live ? make_float2((float)(part + hi), dw * xd(xq)) : make_float2(0.0f, 0.0f);
-    }
+    const float2 t = live[k] ? make_float2((float)(part + hi), half_to_float(dh[k]) * dx[k]) : make_float2(0.0f, 0.0f);
+    if (h == 0) *reinterpret_cast<float2*>(terms + r * kLane + ul * 2) = t;
   }
 }
 
@@ -390,7 +402,9 @@ template <int IN, int OUT, int RING>
 __device__ __forceinline__ Ring gemv_step(const DecodeArgs* P, int n_steps, int sid, const Gs& S, const Gs& N,
                                           bool n_ok, Ring rs, const void* in, const float* nw, int cols,
                                           int max_cols, int E, float* y) {
-  const int tid = threadIdx.x, w = blockIdx.x, wv = tid >> 6, sub = wv >> 2, lane = tid & 63;
+  // Wave-uniform values are taken from the first lane, so that the copy addresses are scalar arithmetic.
+  const int tid = threadIdx.x, w = blockIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), sub = wv >> 2;
   const bool worker = (wv & 3) != 0;
   const int ww = (wv & 3) - 1;
   const int su = S.su_of(w, sub), nq = S.nq_of(su);
@@ -398,18 +412,21 @@ __device__ __forceinline__ Ring gemv_step(const DecodeArgs* P, int n_steps, int 
   const int sun = n_ok ? N.su_of(w, sub) : -1, nn = n_ok ? N.nq_of(sun) : 0;
   const GemvLds l = gemv_lds(max_cols, E);
   uint8_t* ring = l.ring + sub * RING * kChunkBytes;
+  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));
   auto slot = [&](int p) { return ring + ((rs.base + p) % RING) * kChunkBytes; };
+  auto slot_lds = [&](int p) { return ring_lds + (uint32_t)(((rs.base + p) % RING) * kChunkBytes); };
   auto copy_junk = [&](const Gs& G) {
+    const uint32_t junk = lds_addr(g_junk);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) copy16s(glob(G.W), (uint32_t)lane * 16u, g_junk);
-    copy4s(glob(G.W), (uint32_t)lane * 16u, g_junk);
+    for (int j = 0; j < 4; ++j) copy16s(glob(G.W), (uint32_t)lane * 16u, junk);
+    copy4s(glob(G.W), (uint32_t)lane * 16u, junk);
   };
   // Position p of the sub-unit's copy stream: chunk p of S, then N's chunks, then nothing.
   auto issue = [&](int p) {
     if (p < nq)
-      copy_chunk(S, su, p, ww, lane, slot(p));
+      copy_chunk(S, su, p, ww, lane, slot_lds(p));
     else if (p - nq < nn)
-      copy_chunk(N, sun, p - nq, ww, lane, slot(p));
+      copy_chunk(N, sun, p - nq, ww, lane, slot_lds(p));
     else
       copy_junk(S);
   };
@@ -417,10 +434,19 @@ __device__ __forceinline__ Ring gemv_step(const DecodeArgs* P, int n_steps, int 
     if (nq > 0) {
       if (!rs.ready)
         for (int p = 0; p < RING - 1; ++p) issue(p);
+      // The next kWarm chunks into L2 (or as many as there are; the rest of the kWarm * kCopies reads are junk
+      // copies, which keep the first iteration's wait count exact).
+      const uint32_t junk = lds_addr(g_junk);
+      for (int p = RING - 1; p < RING - 1 + kWarm; ++p) {
+        if (p < nq)
+          copy_chunk<true>(S, su, p, ww, lane, junk);
+        else
+          copy_junk(S);
+      }
     } else if (nn > 0) {
       for (int p = 0; p < RING - 1; ++p) {
         if (p < nn)
-          copy_chunk(N, sun, p, ww, lane, slot(p));
+          copy_chunk(N, sun, p, ww, lane, slot_lds(p));
         else
           copy_junk(N);
       }
@@ -446,28 +472,26 @@ __device__ __forceinline__ Ring gemv_step(const DecodeArgs* P, int n_steps, int 
     if (OUT == kOutAcc && c == 0) xr = ld_coh(y + g * kR + cr);  // the residual, read early
     const int cn = min(kChunk, S.nu - c * kChunk);
     const float4* e = reinterpret_cast<const float4*>(terms + (q & 1) * kSlot + cr * kLane);
-    float4 T0[4], T1[4];
-    auto fetch = [&](float4(&T)[4], int ul0) {
+    // The chunk's kChunk / kG groups of terms (4 float4 reads each, inside the row's slot whatever cn is), read three
+    // groups ahead of the group being summed.
+    constexpr int kNG = kChunk / kG, kAhead = 3;
+    float4 T[kNG][4];
+    auto fetch = [&](int g) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) T[i] = e[ul0 / 2 + i];
+      for (int i = 0; i < 4; ++i) T[g][i] = e[g * kG / 2 + i];
     };
-    auto step = [&](const float4(&T)[4]) {
-      const float* v = reinterpret_cast<const float*>(T);
 #pragma unroll
-      for (int i = 0; i < kG; ++i) acc = fma_(v[2 * i], v[2 * i + 1], acc);
-    };
-    fetch(T0, 0);
-    for (int ul0 = 0;;) {
-      fetch(T1, ul0 + kG);
+    for (int g = 0; g < kAhead; ++g) fetch(g);
+#pragma unroll
+    for (int g = 0; g < kNG; ++g) {
+      if (g + kAhead < kNG) fetch(g + kAhead);
       __builtin_amdgcn_sched_barrier(0);
-      step(T0);
+      if (g * kG < cn) {
+        const float* v = reinterpret_cast<const float*>(T[g]);
+#pragma unroll
+        for (int i = 0; i < kG; ++i) acc = fma_(v[2 * i], v[2 * i + 1], acc);
+      }
       __builtin_amdgcn_sched_barrier(0);
-      if ((ul0 += kG) >= cn) break;
-      fetch(T0, ul0 + kG);
-      __builtin_amdgcn_sched_barrier(0);
-      step(T1);
-      __builtin_amdgcn_sched_barrier(0);
-      if ((ul0 += kG) >= cn) break;
     }
     if (c == S.nc - 1) {
       if constexpr (OUT == kOutSilu) {
@@ -491,7 +515,12 @@ __device__ __forceinline__ Ring gemv_step(const DecodeArgs* P, int n_steps, int 
   // chunk q's terms, while the chain wave runs chunk q - 1's chains.
   if (!worker) __builtin_amdgcn_s_setprio(2);
   for (int q = 0; q < nq_wg; ++q) {
-    if (worker && q < nq) wait_vm<kCopies * (RING - 2)>();
+    if (worker && q < nq) {
+      if (q == 0)
+        wait_vm<kCopies * (RING - 2 + kWarm)>();
+      else
+        wait_vm<kCopies * (RING - 2)>();
+    }
     lds_barrier();
     if (worker) {
       if (q < nq) {
