@@ -56,6 +56,10 @@ int mk_engine_run(mk_engine* e);
 int mk_engine_steps(mk_engine* e, uint64_t* steps);
 /* Generated ids of a request (up to cap) and its counters. */
 int mk_engine_result(mk_engine* e, int32_t request_id, int32_t* tokens, int32_t cap, mk_request_info* info);
+/* Frees a finished request's result (the reference hands each result to its caller and keeps none, engine.cpp:
+   226-240); the id is unknown afterwards. MK_ERR_INVALID for a request still pending or in flight. held (may be
+   NULL): results still held after the call. */
+int mk_engine_release(mk_engine* e, int32_t request_id, int64_t* held);
 
 #ifdef __cplusplus
 }

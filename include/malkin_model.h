@@ -26,6 +26,8 @@ typedef struct {
   int64_t tensor_bytes; /* sum of the tensors' data bytes */
   int32_t n_layer;      /* <arch>.block_count, 0 when absent */
   char arch[32];        /* general.architecture ("" when absent) */
+  int32_t n_eog;        /* end-of-generation ids the metadata names (as mk_model_eog, before the vocabulary bound) */
+  int32_t eog[8];       /* the first min(n_eog, 8) of them, ascending */
 } mk_gguf_info;
 
 /* Opens and validates a GGUF v3 file without a device: header, metadata and tensor directory, every tensor inside
@@ -57,6 +59,10 @@ enum {
 int mk_model_open(mk_ctx* ctx, const char* gguf_path, int n_ctx, int n_seq, int flags, mk_model** out);
 int mk_model_free(mk_model* m);
 int mk_model_get_config(const mk_model* m, mk_model_config* out);
+/* The model's end-of-generation ids (Tokenizer::is_eog's set, tokenizer.cpp:93-102: the eos / eot / eom ids of the
+   GGUF metadata and the control tokens among the reference's end-of-turn names), ascending. Writes at most cap ids to
+   out (out may be null when cap is 0) and returns the count of the whole set, or a negative error code. */
+int mk_model_eog(const mk_model* m, int32_t* out, int cap);
 /* Model::forward(const BatchToken*, int, float*) (model.h:52): logits (host) gets n_vocab floats per token with
    logits set, in batch order. */
 int mk_model_forward_batch(mk_model* m, const mk_batch_token* batch, int n, float* logits);

@@ -74,6 +74,7 @@ SIGNATURES = {
     "mk_decode_layers": (_I, [_P, _P, _I, _I, _I]),
     "mk_decode_check": (_I, [_P, _P]),
     "mk_model_persistent": (_I, [_P]),
+    "mk_model_eog": (_I, [_P, _P, _I]),
     "mk_argmax_top2": (_I, [_P, _P, _I, _I, _P, _P]),
     "mk_greedy_advance": (_I, [_P, _P, _P, _P, _P, _P, _P, _P]),
     "mk_argmax_top2_noalloc": (_I, [_P, _P, _I, _I, _P, _P]),
@@ -105,6 +106,7 @@ SIGNATURES = {
     "mk_engine_run": (_I, [_P]),
     "mk_engine_steps": (_I, [_P, ctypes.POINTER(ctypes.c_uint64)]),
     "mk_engine_result": (_I, [_P, _I, _P, _I, _P]),
+    "mk_engine_release": (_I, [_P, _I, ctypes.POINTER(ctypes.c_int64)]),
     "mk_engine_submit_sampled": (_I, [_P, _P, _I, _I, _P, _I, _P, _P]),
     "mk_penalize": (_I, [_P, _P, _I64, _P, _I, _I, _P, _P, _P]),
     "mk_topk": (_I, [_P, _P, _I64, _P, _I, _I, _I, _P, _P]),
@@ -260,15 +262,18 @@ class MkGenStats(ctypes.Structure):
 
 class MkGgufInfo(ctypes.Structure):
     _fields_ = [("n_tensors", ctypes.c_int64), ("tensor_bytes", ctypes.c_int64), ("n_layer", ctypes.c_int32),
-                ("arch", ctypes.c_char * 32)]
+                ("arch", ctypes.c_char * 32), ("n_eog", ctypes.c_int32), ("eog", ctypes.c_int32 * 8)]
 
 
 def gguf_inspect(path):
     """mk_gguf_inspect: validates a GGUF file on the host (no device needed); raises MkError with the reason."""
     info = MkGgufInfo()
     check(load().mk_gguf_inspect(path.encode(), ctypes.byref(info)))
-    return {"n_tensors": info.n_tensors, "tensor_bytes": info.tensor_bytes, "n_layer": info.n_layer,
-            "arch": info.arch.decode()}
+    out = {"n_tensors": info.n_tensors, "tensor_bytes": info.tensor_bytes, "n_layer": info.n_layer,
+           "arch": info.arch.decode()}
+    if info.n_eog:
+        out["eog"] = list(info.eog[:min(info.n_eog, 8)])
+    return out
 
 
 class Model:
@@ -299,6 +304,16 @@ class Model:
     @property
     def persistent(self):
         return bool(load().mk_model_persistent(self.h))
+
+    @property
+    def eog(self):
+        """The model's end-of-generation ids (the GGUF's eos / eot / eom ids and end-of-turn control tokens)."""
+        n = load().mk_model_eog(self.h, None, 0)
+        if n < 0:
+            check(n)
+        out = np.zeros(max(n, 1), np.int32)
+        check(min(0, load().mk_model_eog(self.h, out.ctypes.data, n)))
+        return [int(v) for v in out[:n]]
 
     @property
     def weight_bytes(self):
@@ -412,6 +427,12 @@ class Engine:
         toks = np.zeros(max(info.completion_tokens, 1), dtype=np.int32)
         check(load().mk_engine_result(self.h, rid, _ptr(toks), len(toks), ctypes.byref(info)))
         return toks[:info.completion_tokens], {f: getattr(info, f) for f, _ in MkRequestInfo._fields_}
+
+    def release(self, rid):
+        """Frees a finished request's result; returns the number of results still held."""
+        held = ctypes.c_int64()
+        check(load().mk_engine_release(self.h, rid, ctypes.byref(held)))
+        return held.value
 
 
 class Server:

@@ -104,6 +104,9 @@ int mk_gguf_inspect(const char* path, mk_gguf_info* out) {
     const std::string arch = f.get_str("general.architecture").value_or("");
     std::snprintf(info.arch, sizeof info.arch, "%s", arch.c_str());
     info.n_layer = static_cast<int32_t>(f.get_int(arch + ".block_count").value_or(0));
+    const std::vector<int32_t> eog = malkin_hip::read_eog(f);
+    info.n_eog = static_cast<int32_t>(eog.size());
+    for (size_t i = 0; i < eog.size() && i < 8; ++i) info.eog[i] = eog[i];
     *out = info;
   });
 }
@@ -121,6 +124,17 @@ int mk_model_open(mk_ctx* ctx, const char* path, int n_ctx, int n_seq, int flags
 }
 
 int mk_model_persistent(const mk_model* m) { return m && m->model && m->model->persistent() ? 1 : 0; }
+
+int mk_model_eog(const mk_model* m, int32_t* out, int cap) {
+  int n = 0;
+  const int rc = run([&] {
+    if (!m || cap < 0 || (cap > 0 && !out)) throw std::invalid_argument("mk_model_eog: bad argument");
+    const auto& eog = m->model->cfg().eog;
+    for (size_t i = 0; i < eog.size() && static_cast<int>(i) < cap; ++i) out[i] = eog[i];
+    n = static_cast<int>(eog.size());
+  });
+  return rc != 0 ? rc : n;
+}
 
 int mk_model_free(mk_model* m) {
   return run([&] { delete m; });
@@ -270,6 +284,15 @@ int mk_engine_result(mk_engine* e, int32_t request_id, int32_t* tokens, int32_t 
       *info = mk_request_info{r.prompt_tokens, r.cached_tokens, r.completion_tokens, r.drafted, r.accepted,
                                r.finish_reason == "stop" ? 1 : r.finish_reason == "cancelled" ? 2 : 0, r.done ? 1 : 0,
                                r.prefill_ms, r.decode_ms};
+  });
+}
+
+int mk_engine_release(mk_engine* e, int32_t request_id, int64_t* held) {
+  return run([&] {
+    if (!e) throw std::invalid_argument("mk_engine_release: null engine");
+    not_serving(e);
+    e->engine->release(request_id);
+    if (held) *held = static_cast<int64_t>(e->engine->results_held());
   });
 }
 

@@ -84,10 +84,10 @@ int Engine::submit(const EngineRequest& req) {
                                 std::to_string(n_ctx));
   for (int32_t id : req.prompt)
     if (id < 0 || id >= target_->cfg().n_vocab) throw std::invalid_argument("prompt token id out of range");
-  results_.push_back(std::make_unique<EngineResult>());
+  const int id = next_id_++;
   auto job = std::make_unique<Job>();
   job->req = req;
-  job->res = results_.back().get();
+  job->res = (results_[id] = std::make_unique<EngineResult>()).get();
   job->budget = req.max_tokens > 0 ? req.max_tokens : n_ctx;
   job->admitted = Clock::now();
   // The request's sampler counts its tokens for the penalties; the draft's draws with seed + 1 and no penalties
@@ -98,16 +98,26 @@ int Engine::submit(const EngineRequest& req) {
   job->draft_sampler = std::make_unique<Sampler>(dp, false);
   job->plain = job->sampler->greedy() && !job->sampler->penalizes();
   waiting_.push_back(std::move(job));
-  return static_cast<int>(results_.size()) - 1;
+  return id;
 }
 
 const EngineResult& Engine::result(int id) const {
-  if (id < 0 || id >= static_cast<int>(results_.size())) throw std::invalid_argument("engine: bad request id");
-  return *results_[static_cast<size_t>(id)];
+  const auto it = results_.find(id);
+  if (it == results_.end()) throw std::invalid_argument("engine: bad request id");
+  return *it->second;
+}
+
+void Engine::release(int id) {
+  const auto it = results_.find(id);
+  if (it == results_.end()) throw std::invalid_argument("engine: bad request id");
+  if (!it->second->done) throw std::invalid_argument("engine: request still in flight");
+  results_.erase(it);
 }
 
 void Engine::cancel(int id) {
-  EngineResult* r = results_.at(static_cast<size_t>(id)).get();
+  const auto it = results_.find(id);
+  if (it == results_.end()) throw std::invalid_argument("engine: bad request id");
+  EngineResult* r = it->second.get();
   if (r->done) return;
   r->finish_reason = "cancelled";
   for (auto it = waiting_.begin(); it != waiting_.end(); ++it)

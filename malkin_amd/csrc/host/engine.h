@@ -39,6 +39,7 @@
 #include <chrono>
 #include <cstdint>
 #include <deque>
+#include <map>
 #include <memory>
 #include <string>
 #include <vector>
@@ -78,12 +79,17 @@ class Engine {
   int step_once();
   void run();  // steps until no request waits or runs
   const EngineResult& result(int id) const;
+  // Frees a finished request's result (its id is then unknown); a request still waiting or running is refused.
+  void release(int id);
+  size_t results_held() const { return results_.size(); }
   // Ends a waiting or running request now, finish "cancelled" (the reference's cancelled generation,
   // engine.cpp:509-512); a finished request is left as it is.
   void cancel(int id);
   int busy() const { return busy_; }
   int n_ctx() const { return target_->n_ctx(); }
   int n_vocab() const { return target_->cfg().n_vocab; }
+  // The target model's end-of-generation ids (the set the reference's Tokenizer::is_eog tests, engine.cpp:60).
+  const std::vector<int32_t>& model_eog() const { return target_->cfg().eog; }
   uint64_t steps() const { return steps_; }
 
  private:
@@ -136,7 +142,8 @@ class Engine {
   int max_depth_ = 8;
   std::vector<Lane> lanes_;
   std::deque<std::unique_ptr<Job>> waiting_;
-  std::vector<std::unique_ptr<EngineResult>> results_;
+  std::map<int, std::unique_ptr<EngineResult>> results_;  // by request id, until released
+  int next_id_ = 0;
   int busy_ = 0;
   uint64_t admissions_ = 0, steps_ = 0;
 

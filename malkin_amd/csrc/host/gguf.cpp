@@ -46,7 +46,8 @@ size_t fixed_width(uint32_t t) {
 // offset arithmetic can wrap.
 class Reader {
  public:
-  Reader(const uint8_t* base, size_t size, const std::string& path) : base_(base), size_(size), path_(path) {}
+  Reader(const uint8_t* base, size_t size, const std::string& path, size_t at = 0)
+      : base_(base), size_(size), at_(at), path_(path) {}
 
   const uint8_t* take(size_t n, const char* what) {
     if (n > size_ - at_) fail(std::string(what) + " runs past the end of the file");
@@ -73,7 +74,7 @@ class Reader {
  private:
   const uint8_t* base_;
   size_t size_;
-  size_t at_ = 0;
+  size_t at_;
   const std::string& path_;
 };
 
@@ -189,6 +190,8 @@ void GgufFile::parse(const std::string& path) {
     } else if (t == kArr) {
       const uint32_t elem = r.get<uint32_t>("metadata array type");
       const uint64_t count = r.get<uint64_t>("metadata array count");
+      v.elem = elem;
+      v.at = r.offset();
       skip_array(r, elem, count, 0);
       v.kind = Meta::kArray;
       v.i = static_cast<int64_t>(count > static_cast<uint64_t>(std::numeric_limits<int64_t>::max())
@@ -288,6 +291,31 @@ size_t GgufFile::str_array_size(const std::string& key) const {
   const auto it = meta_.find(key);
   if (it == meta_.end() || it->second.kind != Meta::kArray) return 0;
   return static_cast<size_t>(it->second.i);
+}
+
+// The array was walked (every element in bounds) when the file was opened, so these re-reads cannot fail.
+std::vector<std::string> GgufFile::str_array(const std::string& key) const {
+  std::vector<std::string> out;
+  const auto it = meta_.find(key);
+  if (it == meta_.end() || it->second.kind != Meta::kArray || it->second.elem != kStr) return out;
+  const std::string path = "(array " + key + ")";
+  Reader r(static_cast<const uint8_t*>(map_), size_, path, it->second.at);
+  out.reserve(static_cast<size_t>(it->second.i));
+  for (int64_t k = 0; k < it->second.i; ++k) out.push_back(r.text("metadata array string"));
+  return out;
+}
+
+std::vector<int64_t> GgufFile::int_array(const std::string& key) const {
+  std::vector<int64_t> out;
+  const auto it = meta_.find(key);
+  if (it == meta_.end() || it->second.kind != Meta::kArray) return out;
+  const uint32_t e = it->second.elem;
+  if (e == kF32 || e == kF64 || !fixed_width(e)) return out;
+  const std::string path = "(array " + key + ")";
+  Reader r(static_cast<const uint8_t*>(map_), size_, path, it->second.at);
+  out.reserve(static_cast<size_t>(it->second.i));
+  for (int64_t k = 0; k < it->second.i; ++k) out.push_back(e == kBool ? r.get<uint8_t>("metadata array") : read_integer(r, e));
+  return out;
 }
 
 const GgufTensor* GgufFile::tensor(const std::string& name) const {

@@ -54,18 +54,25 @@ class GgufFile {
   std::optional<std::string> get_str(const std::string& key) const;
   // Element count of an array value (the tokenizer's vocabulary, tokenizer.ggml.tokens); 0 when absent.
   size_t str_array_size(const std::string& key) const;
+  // The elements of an array of strings / of integers (tokenizer.ggml.tokens, tokenizer.ggml.token_type); empty
+  // when the key is absent or its elements are of another kind.
+  std::vector<std::string> str_array(const std::string& key) const;
+  std::vector<int64_t> int_array(const std::string& key) const;
 
   const GgufTensor* tensor(const std::string& name) const;
   const std::map<std::string, GgufTensor>& tensors() const { return tensors_; }
   size_t size() const { return size_; }
 
  private:
-  // One decoded metadata value. Arrays keep only their element count (the device model reads no array contents).
+  // One decoded metadata value. Arrays keep their element count, element type and the file offset of their first
+  // element (decoded on request).
   struct Meta {
     enum Kind { kInt, kFloat, kBool, kString, kArray } kind = kInt;
     int64_t i = 0;
     double f = 0;
     std::string s;
+    uint32_t elem = 0;
+    size_t at = 0;
   };
   void parse(const std::string& path);
 

@@ -86,7 +86,32 @@ ModelConfig read_config(const GgufFile& f) {
   c.rope_base = float_or("rope.freq_base", 10000.0);
   c.rms_eps = float_or("attention.layer_norm_rms_epsilon", 1e-6);
   c.n_vocab = static_cast<int>(f.str_array_size("tokenizer.ggml.tokens"));
+  c.eog = read_eog(f);  // bounded by the vocabulary once its size is known (Model's constructor)
   return c;
+}
+
+// tokenizer.cpp:93-102: the eos / eot / eom ids the metadata names, and, where the file carries its token list and
+// token types, the control tokens (type 3) among the reference's end-of-turn names.
+std::vector<int32_t> read_eog(const GgufFile& f) {
+  std::vector<int32_t> eog;
+  for (const char* key : {"tokenizer.ggml.eos_token_id", "tokenizer.ggml.eot_token_id", "tokenizer.ggml.eom_token_id"}) {
+    const auto id = f.get_int(key);
+    if (id && *id >= 0 && *id <= INT32_MAX) eog.push_back(static_cast<int32_t>(*id));
+  }
+  const std::vector<std::string> toks = f.str_array("tokenizer.ggml.tokens");
+  const std::vector<int64_t> types = f.int_array("tokenizer.ggml.token_type");
+  if (!toks.empty() && types.size() == toks.size()) {
+    constexpr int64_t kControl = 3;
+    for (const char* name : {"<|im_end|>", "<|endoftext|>", "<|eot_id|>", "<|eom_id|>", "<end_of_turn>", "<|return|>",
+                             "<|call|>", "<|end|>"}) {
+      const auto it = std::find(toks.begin(), toks.end(), name);
+      if (it != toks.end() && types[static_cast<size_t>(it - toks.begin())] == kControl)
+        eog.push_back(static_cast<int32_t>(it - toks.begin()));
+    }
+  }
+  std::sort(eog.begin(), eog.end());
+  eog.erase(std::unique(eog.begin(), eog.end()), eog.end());
+  return eog;
 }
 
 // Loads the named GGUF matrices (same type and column count) as one row-concatenated weight: CDNA-packed for the
@@ -273,6 +298,7 @@ Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide, bo
   else
     load_weight(f, {"token_embd.weight"}, output_);  // tied embeddings (model.cpp:116-118)
   c.n_vocab = static_cast<int>(output_.rows);
+  c.eog.erase(std::remove_if(c.eog.begin(), c.eog.end(), [&](int32_t id) { return id >= c.n_vocab; }), c.eog.end());
 
   auto upload_norm = [&](const std::string& nm, int64_t n, float* dst) {
     const GgufTensor* t = f.tensor(nm);

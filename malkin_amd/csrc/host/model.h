@@ -25,10 +25,15 @@ struct ModelConfig {  // model.h:11-16
   int n_layer = 0, n_embd = 0, n_ff = 0, n_head = 0, n_head_kv = 0, head_dim = 0;
   int n_ctx_train = 0, n_vocab = 0;
   float rope_base = 10000.0f, rms_eps = 1e-6f;
+  // End-of-generation ids (Tokenizer::is_eog's set, tokenizer.cpp:93-102), ascending, each < n_vocab.
+  std::vector<int32_t> eog;
 };
 
 // Hyperparameters from the GGUF metadata (the keys of model.cpp:78-101, same defaults and error texts).
 ModelConfig read_config(const GgufFile& f);
+// End-of-generation ids the metadata names (tokenizer.cpp:93-102), ascending, unique; not yet bounded by the
+// vocabulary size.
+std::vector<int32_t> read_eog(const GgufFile& f);
 
 // model.h:25-30
 struct BatchToken {

@@ -7,6 +7,8 @@
 #include <sys/time.h>
 #include <unistd.h>
 
+#include <chrono>
+#include <thread>
 #include <cctype>
 #include <cerrno>
 #include <cstring>
@@ -161,22 +163,55 @@ int Server::bind(const std::string& host, int port) {
                                         : reinterpret_cast<sockaddr_in*>(&ss)->sin_port);
 }
 
+void Server::refuse(int fd) {
+  timeval tv{1, 0};
+  ::setsockopt(fd, SOL_SOCKET, SO_SNDTIMEO, &tv, sizeof tv);
+  Writer w(fd);
+  w.send(503, "application/json", "{\"error\":{\"message\":\"too many connections\",\"type\":\"server_error\"}}");
+  ::shutdown(fd, SHUT_RDWR);
+  ::close(fd);
+}
+
+// The accept loop. Out of descriptors or memory (EMFILE, ENFILE, ENOBUFS, ENOMEM) it retries after a pause; other
+// errors end it (after stop(), the listener's shutdown is one).
 void Server::serve() {
   while (!stopping_) {
     const int fd = ::accept(listen_fd_, nullptr, nullptr);
     if (fd < 0) {
       if (stopping_) break;
       if (errno == EINTR || errno == ECONNABORTED) continue;
+      if (errno == EMFILE || errno == ENFILE || errno == ENOBUFS || errno == ENOMEM) {
+        std::this_thread::sleep_for(std::chrono::milliseconds(50));
+        continue;
+      }
       break;
     }
     timeval tv{kTimeoutS, 0};
     ::setsockopt(fd, SOL_SOCKET, SO_RCVTIMEO, &tv, sizeof tv);
     ::setsockopt(fd, SOL_SOCKET, SO_SNDTIMEO, &tv, sizeof tv);
+    bool full;
     {
       std::lock_guard<std::mutex> lk(m_);
-      ++live_;
+      full = live_ >= kMaxConnections || stopping_;
+      if (!full) {
+        ++live_;
+        clients_.insert(fd);
+      }
     }
-    std::thread([this, fd] { connection(fd); }).detach();
+    if (full) {
+      refuse(fd);
+      continue;
+    }
+    try {
+      std::thread([this, fd] { connection(fd); }).detach();
+    } catch (const std::exception&) {  // no thread: refused like a connection past the cap
+      {
+        std::lock_guard<std::mutex> lk(m_);
+        clients_.erase(fd);
+        if (--live_ == 0) idle_.notify_all();
+      }
+      refuse(fd);
+    }
   }
 }
 
@@ -196,9 +231,10 @@ void Server::connection(int fd) {
       handler_(rq, w);
   } catch (...) {
   }
+  std::lock_guard<std::mutex> lk(m_);
+  clients_.erase(fd);  // before the close, so that stop() never shuts down a reused descriptor
   ::shutdown(fd, SHUT_RDWR);
   ::close(fd);
-  std::lock_guard<std::mutex> lk(m_);
   if (--live_ == 0) idle_.notify_all();
 }
 
@@ -211,6 +247,7 @@ void Server::stop() {
     listen_fd_ = -1;
   }
   std::unique_lock<std::mutex> lk(m_);
+  for (const int fd : clients_) ::shutdown(fd, SHUT_RDWR);  // a pending recv or send returns at once
   idle_.wait(lk, [this] { return live_ == 0; });
 }
 

@@ -8,6 +8,7 @@
 #include <functional>
 #include <map>
 #include <mutex>
+#include <set>
 #include <string>
 #include <thread>
 
@@ -47,10 +48,13 @@ class Server {
   int bind(const std::string& host, int port);
   void serve();  // the accept loop, until stop()
   void start();  // serve() on a thread of its own
-  void stop();   // closes the listener, waits for the connection threads
+  void stop();   // closes the listener, shuts the open connections down, waits for their threads
+
+  static constexpr int kMaxConnections = 256;  // open connections; beyond it a client gets 503 at once
 
  private:
   void connection(int fd);
+  void refuse(int fd);  // 503 on the accept thread, then close
 
   Handler handler_;
   int listen_fd_ = -1;
@@ -58,7 +62,8 @@ class Server {
   std::thread accept_thread_;
   std::mutex m_;
   std::condition_variable idle_;
-  int live_ = 0;  // connection threads running (detached; stop() waits for none)
+  int live_ = 0;            // connection threads running (detached; stop() waits for none)
+  std::set<int> clients_;   // their sockets, shut down by stop()
 };
 
 }  // namespace malkin_hip::http

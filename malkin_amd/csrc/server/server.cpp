@@ -145,6 +145,10 @@ class EngineLoop {
         for (Active& a : active_) {
           e_.cancel(a.id);
           close_channel(*a.ch, nullptr, std::string("engine: ") + ex.what());
+          try {
+            e_.release(a.id);
+          } catch (const std::exception&) {
+          }
         }
         active_.clear();
         continue;
@@ -162,7 +166,8 @@ class EngineLoop {
           a.ch->cv.notify_all();
         }
         if (r.done) {
-          close_channel(*a.ch, &r, "");
+          close_channel(*a.ch, &r, "");  // copies the result out
+          e_.release(a.id);
           active_.erase(active_.begin() + static_cast<std::ptrdiff_t>(i));
         } else {
           ++i;
@@ -212,6 +217,13 @@ std::vector<int32_t> id_list(const Value& v, const char* what, int n_vocab) {
   return out;
 }
 
+// An integer field that must fit an int: out-of-range values are refused (400) rather than narrowed.
+int int_field(const Value& v, const char* name) {
+  const int64_t x = v.as_int();
+  if (x < INT32_MIN || x > INT32_MAX) throw BadRequest(std::string(name) + " is out of range");
+  return static_cast<int>(x);
+}
+
 // sampling_from (server.cpp:59-69): the reference's defaults, each field optional.
 SamplingParams sampling_from(const Value& b) {
   SamplingParams p;
@@ -223,8 +235,12 @@ SamplingParams sampling_from(const Value& b) {
   num("min_p", p.min_p);
   num("presence_penalty", p.presence_penalty);
   num("frequency_penalty", p.frequency_penalty);
-  if (b.has("top_k") && !b["top_k"].is_null()) p.top_k = static_cast<int>(b["top_k"].as_int());
-  if (b.has("seed") && b["seed"].is_integer()) p.seed = b["seed"].as_uint();
+  if (b.has("top_k") && !b["top_k"].is_null()) p.top_k = int_field(b["top_k"], "top_k");
+  // Any JSON integer, converted as the reference's get<uint64_t>() converts it: a negative value wraps modulo 2^64.
+  if (b.has("seed") && b["seed"].is_integer()) {
+    const Value& s = b["seed"];
+    p.seed = s.kind() == Value::Kind::Uint ? s.as_uint() : static_cast<uint64_t>(s.as_int());
+  }
   return p;
 }
 
@@ -288,11 +304,15 @@ class Api {
     EngineRequest req;
     req.prompt = id_list(ids, "prompt", engine_->n_vocab());
     req.sampling = sampling_from(b);
-    req.max_tokens = b.has("max_tokens") && !b["max_tokens"].is_null() ? static_cast<int>(b["max_tokens"].as_int())
-                                                                       : 16;
+    req.max_tokens = b.has("max_tokens") && !b["max_tokens"].is_null() ? int_field(b["max_tokens"], "max_tokens") : 16;
     if (req.max_tokens < 0) throw BadRequest("max_tokens must not be negative");
-    if (b.has("stop_token_ids") && !b["stop_token_ids"].is_null())
-      req.eog = id_list(b["stop_token_ids"], "stop_token_ids", engine_->n_vocab());
+    // Generation stops at the model's end-of-generation ids, as the reference's engine does for every request
+    // (engine.cpp:60), and at any further ids the client lists.
+    req.eog = engine_->model_eog();
+    if (b.has("stop_token_ids") && !b["stop_token_ids"].is_null()) {
+      const std::vector<int32_t> extra = id_list(b["stop_token_ids"], "stop_token_ids", engine_->n_vocab());
+      req.eog.insert(req.eog.end(), extra.begin(), extra.end());
+    }
     if (b.has("stop") && !b["stop"].is_null() && !(b["stop"].is_array() && b["stop"].items().empty()))
       throw BadRequest("stop strings need a tokenizer: use stop_token_ids");
     const bool stream = b.has("stream") && b["stream"].as_bool();

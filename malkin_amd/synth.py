@@ -19,7 +19,7 @@ class _Config(ctypes.Structure):
         ("n_head_kv", ctypes.c_int), ("head_dim", ctypes.c_int), ("n_vocab", ctypes.c_int),
         ("n_ctx_train", ctypes.c_int), ("rope_base", ctypes.c_float), ("rms_eps", ctypes.c_float),
         ("tied", ctypes.c_int), ("type", ctypes.c_int), ("mix", ctypes.c_int), ("std", ctypes.c_float),
-        ("seed", ctypes.c_uint64), ("name", ctypes.c_char * 32),
+        ("seed", ctypes.c_uint64), ("name", ctypes.c_char * 32), ("eos_id", ctypes.c_int),
     ]
 
 
@@ -58,7 +58,9 @@ def lib():
 
 
 def make_config(preset="tiny", wtype=Q8_0, mix=MIX_UNIFORM, seed=1, std=0.02, rope_base=1e6, rms_eps=1e-6,
-                n_ctx_train=40960, **over):
+                n_ctx_train=40960, eos_id=-1, **over):
+    """eos_id >= 0: the file carries tokenizer.ggml.eos_token_id = eos_id (no token list: the synthetic models have
+    no tokenizer)."""
     p = dict(PRESETS[preset])
     p.update(over)
     c = _Config()
@@ -73,6 +75,7 @@ def make_config(preset="tiny", wtype=Q8_0, mix=MIX_UNIFORM, seed=1, std=0.02, ro
     c.std = std
     c.seed = seed
     c.name = preset.encode()[:31]
+    c.eos_id = eos_id
     return c
 
 

@@ -411,7 +411,7 @@ static size_t header(wbuf* w, const mks_config* c, const tinfo* t, int nt) {
   w_u32(w, 0x46554747);
   w_u32(w, 3);
   w_u64(w, (uint64_t)nt);
-  w_u64(w, 12);
+  w_u64(w, c->eos_id >= 0 ? 13 : 12);
   kv_str(w, "general.architecture", "qwen3");
   kv_str(w, "general.name", c->name[0] ? c->name : "synthetic");
   kv_u32(w, "general.alignment", 32);
@@ -424,6 +424,7 @@ static size_t header(wbuf* w, const mks_config* c, const tinfo* t, int nt) {
   kv_u32(w, "qwen3.context_length", (uint32_t)c->n_ctx_train);
   kv_f32(w, "qwen3.rope.freq_base", c->rope_base);
   kv_f32(w, "qwen3.attention.layer_norm_rms_epsilon", c->rms_eps);
+  if (c->eos_id >= 0) kv_u32(w, "tokenizer.ggml.eos_token_id", (uint32_t)c->eos_id);
   for (int i = 0; i < nt; ++i) {
     w_str(w, t[i].name);
     w_u32(w, (uint32_t)t[i].nd);

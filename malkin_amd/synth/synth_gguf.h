@@ -20,6 +20,7 @@ typedef struct {
   float std;    /* weight standard deviation (0.02) */
   uint64_t seed;
   char name[32];
+  int eos_id;   /* >= 0: written as tokenizer.ggml.eos_token_id (the model's end-of-generation id); < 0: no such key */
 } mks_config;
 
 /* Size of the file mks_write_gguf writes for c. */

@@ -123,3 +123,42 @@ def test_no_descriptor_leak_on_errors(tmp_path):
         with pytest.raises(malkin_amd.MkError):
             inspect(tmp_path, blob)
     assert len(os.listdir("/proc/self/fd")) <= before + 1
+
+
+def str_array(items):
+    return struct.pack("<IQ", 8, len(items)) + b"".join(s(t) for t in items)
+
+
+def i32_array(vals):
+    return struct.pack("<IQ", 5, len(vals)) + b"".join(struct.pack("<i", v) for v in vals)
+
+
+def test_end_of_generation_ids(tmp_path):
+    """The end-of-generation set of tokenizer.cpp:93-102: the eos / eot / eom ids, plus the control tokens (type 3)
+    among the end-of-turn names. A name that is present but not a control token, and ids of other keys, are not in
+    it; repeated ids appear once, ascending."""
+    toks = ["a", "<|im_end|>", "b", "<|endoftext|>", "<|eot_id|>", "<end_of_turn>", "c"]
+    types = [1, 3, 1, 3, 1, 3, 1]  # <|eot_id|> is a normal token here
+    meta = [("general.architecture", 8, s("qwen3")),
+            ("tokenizer.ggml.eos_token_id", 4, struct.pack("<I", 6)),
+            ("tokenizer.ggml.eot_token_id", 4, struct.pack("<I", 3)),
+            ("tokenizer.ggml.bos_token_id", 4, struct.pack("<I", 2)),
+            ("tokenizer.ggml.tokens", 9, str_array(toks)),
+            ("tokenizer.ggml.token_type", 9, i32_array(types))]
+    info = inspect(tmp_path, gguf_bytes(ONE, meta))
+    assert info["eog"] == [1, 3, 5, 6]
+    # Without token types only the metadata ids count; without any of the keys there is no set.
+    info = inspect(tmp_path, gguf_bytes(ONE, meta[:3] + meta[4:5]), name="g.gguf")
+    assert info["eog"] == [3, 6]
+    assert "eog" not in inspect(tmp_path, gguf_bytes(ONE, meta[:1]), name="h.gguf")
+    # eom alone, as a u64.
+    info = inspect(tmp_path, gguf_bytes(ONE, [("tokenizer.ggml.eom_token_id", 10, struct.pack("<Q", 9))]), name="i.gguf")
+    assert info["eog"] == [9]
+
+
+def test_synthetic_eos_id(tmp_path, synth_lib):
+    p = str(tmp_path / "m.gguf")
+    synth_lib.write_gguf(p, synth_lib.make_config("tiny", 8, seed=2, eos_id=77), threads=2)
+    assert malkin_amd.gguf_inspect(p)["eog"] == [77]
+    synth_lib.write_gguf(p, synth_lib.make_config("tiny", 8, seed=2), threads=2)
+    assert "eog" not in malkin_amd.gguf_inspect(p)

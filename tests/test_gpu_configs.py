@@ -4,6 +4,9 @@
   config 2  decode GEMV over the Qwen3-14B FFN shapes (gate/up 5120->17408, down 17408->5120) in Q4_K and Q6_K at
             n = 1, 4, 8.
 
+Weights as BASELINE.json draws them: entries N(0, 0.02), quantized by the GGUF writer's quantizer (synth.quantize_rows,
+the reference's quantize_row_* restated); activations N(0, 1) through the reference's Q8_0 activation quantizer.
+
 Every output is compared with a float64 product of the dequantized operands under the reference's own criterion
 (|y - y64| / rms(y64) < 1e-5, test_quant.cpp:250-256), which catches any misplaced row, token or block; a spread of
 rows (the first and last tiles included) is compared bit for bit with the CPU oracle over the full depth."""
@@ -56,12 +59,16 @@ def check(oracle, t, w, k, xq, y, sel, wide=True):
     assert rel < 1e-5, rel
 
 
-def test_config1_gemm_q8_0_full(mk, oracle):
-    import make_golden
+def normal_rows(synth_lib, rng, t, rows, k):
+    """BASELINE.json's weights: entries N(0, 0.02), quantized to type t by the GGUF writer's quantizer."""
+    return synth_lib.quantize_rows(t, (rng.standard_normal((rows, k), dtype=np.float32) * np.float32(0.02)))
+
+
+def test_config1_gemm_q8_0_full(mk, oracle, synth_lib):
     rows, k, n = 9728, 2560, 512
     print("config 1 GEMM", rows, k, n, flush=True)
     rng = np.random.default_rng(9728)
-    w = make_golden.random_rows(rng, mk_.Q8_0, rows, k)
+    w = normal_rows(synth_lib, rng, mk_.Q8_0, rows, k)
     xq = oracle.quantize_row_q8(rng.standard_normal((n, k)).astype(np.float32))
     y = device_matmul(mk, mk_.Q8_0, w, rows, k, xq.view(np.uint8), n)
     check(oracle, mk_.Q8_0, w, k, xq, y, spread(rows, 97))
@@ -69,10 +76,9 @@ def test_config1_gemm_q8_0_full(mk, oracle):
 
 @pytest.mark.parametrize("t", [mk_.Q4_K, mk_.Q6_K])
 @pytest.mark.parametrize("rows,k", [(17408, 5120), (5120, 17408)])
-def test_config2_gemv_full(mk, oracle, t, rows, k):
-    import make_golden
+def test_config2_gemv_full(mk, oracle, synth_lib, t, rows, k):
     rng = np.random.default_rng(t * 100 + rows)
-    w = make_golden.random_rows(rng, t, rows, k)
+    w = normal_rows(synth_lib, rng, t, rows, k)
     for n in (1, 4, 8):
         print("config 2 GEMV", t, rows, k, n, flush=True)
         xq = oracle.quantize_row_q8(rng.standard_normal((n, k)).astype(np.float32))

@@ -135,3 +135,56 @@ def test_server_completions(mk, oracle, model_files):
     assert list(toks) == want
     eng.close()
     target.close()
+
+
+def test_model_eog_stops_requests(mk, oracle, model_files, tmp_path, synth_lib):
+    """The model's own end-of-generation id (tokenizer.ggml.eos_token_id) ends a request that lists no stop ids,
+    finish "stop", as the reference's engine stops at Tokenizer::is_eog for every request (engine.cpp:60); the server
+    frees each finished result; out-of-range integer fields are refused and negative seeds wrap as get<uint64_t>()
+    makes them."""
+    import make_golden
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(0, 1024, 12).astype(np.int32)
+    want, _ = expected(oracle, model_files, prompt, 24, None)
+    # the first token of the greedy stream, from the fourth on, that has not appeared before it
+    i = next(i for i in range(3, len(want)) if want[i] not in want[:i])
+    eos = want[i]
+    c = make_golden.MODEL_CFGS["tiny"]
+    path = str(tmp_path / "tiny-eos.gguf")
+    synth_lib.write_gguf(path, synth_lib.make_config(c["preset"], c["wtype"], seed=c["seed"], eos_id=eos), threads=4)
+    target = mk_.Model(mk, path, N_CTX, 2)
+    assert target.eog == [eos]
+    eng = mk_.Engine(target)
+    srv = mk_.Server(eng, model_id="tiny-eos")
+    try:
+        st, r = post(srv.port, dict(prompt=[int(x) for x in prompt], max_tokens=24, temperature=0.0))
+        print("eos", eos, "at", i, r["choices"][0], flush=True)
+        assert st == 200 and r["choices"][0]["tokens"] == want[:i] and r["choices"][0]["finish_reason"] == "stop"
+        assert r["usage"]["completion_tokens"] == i
+        # client stop ids are added to the model's
+        st, r = post(srv.port, dict(prompt=[int(x) for x in prompt], max_tokens=24, temperature=0.0,
+                                    stop_token_ids=[want[1]]))
+        assert st == 200 and r["choices"][0]["tokens"] == want[:1] and r["choices"][0]["finish_reason"] == "stop"
+        for body, word in ((dict(prompt=[1, 2], max_tokens=2 ** 32 + 16), "max_tokens"),
+                           (dict(prompt=[1, 2], top_k=2 ** 32 + 1), "top_k"),
+                           (dict(prompt=[1, 2], max_tokens=-1), "max_tokens")):
+            st, r = post(srv.port, body)
+            assert st == 400 and word in r["error"]["message"], (body, r)
+        for seed in (-1, 2 ** 64 - 1):  # the same draws: -1 wraps to 2^64 - 1
+            st, r = post(srv.port, dict(prompt=[int(x) for x in prompt], max_tokens=6, temperature=1.0, seed=seed))
+            assert st == 200
+            if seed == -1:
+                first = r["choices"][0]["tokens"]
+            else:
+                assert r["choices"][0]["tokens"] == first
+    finally:
+        srv.close()
+    # every finished request's result was released by the server: a fresh request gets a fresh id, and releasing it
+    # leaves nothing held
+    rid = eng.submit(prompt, max_tokens=3)
+    eng.run()
+    assert eng.release(rid) == 0
+    with pytest.raises(mk_.MkError):
+        eng.result(rid)
+    eng.close()
+    target.close()
