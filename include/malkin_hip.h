@@ -54,6 +54,9 @@ size_t mk_attention_scratch_bytes(int head_dim, int max_keys, int pairs);
 /* Host waits on the device made by this library so far (stream and event synchronizations, including those inside
    mk_upload / mk_download / mk_free), for tests that bound the waits of a token loop. */
 uint64_t mk_host_waits(void);
+/* Bytes this library has copied from device memory into host memory so far (mk_download, and mk_copy_async into
+   pinned memory), for tests that bound what a token loop downloads. */
+uint64_t mk_host_bytes(void);
 /* The context's hipStream_t. */
 void* mk_stream(mk_ctx* ctx);
 
@@ -279,6 +282,29 @@ int mk_penalize(mk_ctx* ctx, float* logits, int64_t stride, const int32_t* rows,
    largest value, then a sort of the k candidates in LDS. */
 int mk_topk(mk_ctx* ctx, const float* logits, int64_t stride, const int32_t* rows, int n_rows, int n_vocab, int k,
             float* values, int32_t* ids);
+/* Per-row parameters of mk_sample_cut: candidates k (<= 0: the whole vocabulary) and the request's temperature
+   (> 0), min_p and top_p. */
+typedef struct {
+  int32_t k;
+  float temperature, min_p, top_p;
+} mk_cut_params;
+/* The rest of Sampler::distribution for candidate counts above mk_topk's 1024 (top_k <= 0 or > 1024), sampler.cpp:
+   27-56, so that such a row is not downloaded whole: per row the k largest logits sorted (highest first, equal
+   logits by lower id), their weights exp((l - l_max) / T) (float), the total in double in that order, and the kept
+   count (the first candidate, then candidates while the weight is at least min_p times the first, up to the one
+   whose running sum reaches top_p of the total). Writes keep[r], sums[r] and the first min(keep[r] + 1, k, cap)
+   candidates to values / ids [n_rows][cap] (device arrays; params too). The weights are computed as the correctly
+   rounded float of exp (the reference's C library expf agrees except within ~2^-60 of a rounding boundary): the
+   caller recomputes the kept weights itself. workspace: at least mk_sample_cut_workspace(n_rows, n_vocab) device
+   bytes, which also keep the sorted rows for mk_sample_cut_tail until the next call. */
+size_t mk_sample_cut_workspace(int n_rows, int n_vocab);
+int mk_sample_cut(mk_ctx* ctx, const float* logits, int64_t stride, const int32_t* rows, int n_rows, int n_vocab,
+                  const mk_cut_params* params, int cap, float* values, int32_t* ids, int32_t* keep, double* sums,
+                  void* workspace, size_t workspace_bytes);
+/* Candidates [from, from + count) of row `row` of the last mk_sample_cut on this workspace (a kept head longer than
+   its cap), into values / ids (device arrays). */
+int mk_sample_cut_tail(mk_ctx* ctx, void* workspace, int n_rows, int n_vocab, int row, int from, int count,
+                       float* values, int32_t* ids);
 
 /* dst[dst_index[i]] = src[src_index[i]] for i < n, in stream order (a NULL index array is the identity; a negative
    index skips i). Moves token ids between device arrays without a host round trip: draft picks into a proposal tree,

@@ -79,6 +79,7 @@ SIGNATURES = {
     "mk_greedy_advance": (_I, [_P, _P, _P, _P, _P, _P, _P, _P]),
     "mk_argmax_top2_noalloc": (_I, [_P, _P, _I, _I, _P, _P]),
     "mk_host_waits": (ctypes.c_uint64, []),
+    "mk_host_bytes": (ctypes.c_uint64, []),
     "mk_host_alloc": (_I, [_P, _SZ, ctypes.POINTER(_P)]),
     "mk_host_free": (_I, [_P, _P]),
     "mk_copy_async": (_I, [_P, _P, _P, _SZ]),

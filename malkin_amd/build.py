@@ -26,6 +26,7 @@ HIP_SOURCES = [
     "csrc/kernels/quant.hip",
     "csrc/kernels/attn.hip",
     "csrc/kernels/decode.hip",
+    "csrc/kernels/cut.hip",
     "csrc/kernels/rowpath.hip",
     "csrc/kernels/sample.hip",
     "csrc/kernels/capi.cpp",

@@ -77,11 +77,11 @@ void device_distribution(mk_ctx* ctx, mk_sampler* s, float* dev_logits, int n_vo
   s->pen_amts.clear();
   s->sampler->penalties(nullptr, 0, s->pen_ids, s->pen_amts);
   s->select->clear();
-  s->select->add(0, s->sampler->candidates(n_vocab), s->pen_ids, s->pen_amts);
+  s->select->add(0, *s->sampler, s->pen_ids, s->pen_amts);
   s->select->enqueue(dev_logits);
   if (mk_synchronize(ctx) != MK_OK) throw std::runtime_error(mk_last_error());
   s->select->collect();
-  s->sampler->finish(s->select->values(0), s->select->ids(0), s->select->count(0), out);
+  s->sampler->finish(*s->select, 0, out);
 }
 
 std::vector<malkin_hip::BatchToken> to_batch(const mk_batch_token* b, int n) {

@@ -281,7 +281,7 @@ void Engine::draft_trees() {
     draft_sel_.clear();
     for (const auto& [row, si] : p.drawn) {
       const Job& job = *lanes_[static_cast<size_t>(specs_[static_cast<size_t>(si)].lane)].job;
-      draft_sel_.add(row, job.draft_sampler->candidates(n_vocab), pen_ids_, pen_amts_);
+      draft_sel_.add(row, *job.draft_sampler, pen_ids_, pen_amts_);
     }
     draft_sel_.enqueue(draft_->dev_logits());
     ck(mk_synchronize(c));
@@ -292,7 +292,7 @@ void Engine::draft_trees() {
       Sampler& ds = *lanes_[static_cast<size_t>(sp.lane)].job->draft_sampler;
       const int r = static_cast<int>(j);
       sp.q.emplace_back();
-      ds.finish(draft_sel_.values(r), draft_sel_.ids(r), draft_sel_.count(r), sp.q.back());
+      ds.finish(draft_sel_, r, sp.q.back());
       sp.chain.push_back(ds.draw(sp.q.back()));
     }
   }
@@ -362,7 +362,7 @@ void Engine::select_known_rows(int decode_rows) {
       pen_ids_.clear();
       pen_amts_.clear();
       job.sampler->penalties(sp.chain.data(), i, pen_ids_, pen_amts_);
-      const int at = sel_.add(sp.root + i, job.sampler->candidates(n_vocab), pen_ids_, pen_amts_);
+      const int at = sel_.add(sp.root + i, *job.sampler, pen_ids_, pen_amts_);
       if (i == 0) sp.sel = at;
     }
   }
@@ -373,7 +373,7 @@ void Engine::select_known_rows(int decode_rows) {
     pen_ids_.clear();
     pen_amts_.clear();
     job.sampler->penalties(nullptr, 0, pen_ids_, pen_amts_);
-    finishing_sel_[j] = sel_.add(decode_rows + static_cast<int>(j), job.sampler->candidates(n_vocab), pen_ids_, pen_amts_);
+    finishing_sel_[j] = sel_.add(decode_rows + static_cast<int>(j), *job.sampler, pen_ids_, pen_amts_);
   }
   pen_ids_.clear();
   pen_amts_.clear();
@@ -456,7 +456,7 @@ void Engine::step() {
       job.pending = picks_h_[decode_rows + static_cast<int>(j)];
     } else {
       const int r = finishing_sel_[j];
-      job.sampler->finish(sel_.values(r), sel_.ids(r), sel_.count(r), dist_);
+      job.sampler->finish(sel_, r, dist_);
       job.pending = job.sampler->draw(dist_);
     }
     if (!emit(job, job.pending, lane.kv.size())) finish(lane);
@@ -480,7 +480,7 @@ int32_t Engine::target_pick(const Spec& sp, int node) const {
 Distribution& Engine::target_dist(const Spec& sp, int row) {
   const Sampler& s = *lanes_[static_cast<size_t>(sp.lane)].job->sampler;
   const int r = sp.sel + row;
-  s.finish(sp.cand->values(r), sp.cand->ids(r), sp.cand->count(r), dist_);
+  s.finish(*sp.cand, r, dist_);
   return dist_;
 }
 

@@ -13,13 +13,6 @@ void ck(int rc) {
   if (rc != MK_OK) throw std::runtime_error(mk_last_error());
 }
 
-// The device top-k's order on floats: larger key = larger value (+0 above -0).
-uint32_t order_key(float f) {
-  uint32_t u;
-  std::memcpy(&u, &f, sizeof(u));
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
 float prob_in(const Distribution& d, int32_t id) {
   for (const Candidate& c : d)
     if (c.id == id) return c.p;
@@ -97,6 +90,48 @@ void Sampler::finish(const float* values, const int32_t* ids, int n, Distributio
     out.push_back(Candidate{static_cast<float>(weights_[static_cast<size_t>(i)] / kept), ids[i]});
 }
 
+void Sampler::finish(const Selector& sel, int i, Distribution& out) const {
+  const float* values = sel.values(i);
+  const int32_t* ids = sel.ids(i);
+  const int n = sel.count(i);
+  if (!sel.cut(i)) return finish(values, ids, n, out);
+  // The device kept the first keep(i) of the row's candidates against its total of all their weights. The same walk
+  // over the host's weights of the candidates here (the head and one past it) and that total; where the walk stops
+  // inside them, its count is used (the device's otherwise), then the kept weights are normalised as above.
+  out.clear();
+  if (n <= 0) throw std::invalid_argument("sampler: no candidates");
+  if (greedy()) {
+    out.push_back(Candidate{1.0f, ids[0]});
+    return;
+  }
+  const float top = values[0];
+  weights_.resize(static_cast<size_t>(n));
+  for (int j = 0; j < n; ++j) weights_[static_cast<size_t>(j)] = std::exp((values[j] - top) / p_.temperature);
+  const double floor_w = static_cast<double>(p_.min_p) * weights_[0];
+  const double nucleus = static_cast<double>(p_.top_p) * sel.total(i);
+  double run = 0.0;
+  int keep = -1;
+  for (int j = 0; j < n; ++j) {
+    const double w = weights_[static_cast<size_t>(j)];
+    if (j > 0 && w < floor_w) {
+      keep = j;
+      break;
+    }
+    run += w;
+    if (run >= nucleus) {
+      keep = j + 1;
+      break;
+    }
+  }
+  if (keep < 0) keep = sel.keep(i);
+  keep = std::max(1, std::min(keep, n));
+  double kept = 0.0;
+  for (int j = 0; j < keep; ++j) kept += weights_[static_cast<size_t>(j)];
+  out.reserve(static_cast<size_t>(keep));
+  for (int j = 0; j < keep; ++j)
+    out.push_back(Candidate{static_cast<float>(weights_[static_cast<size_t>(j)] / kept), ids[j]});
+}
+
 double Sampler::uniform() { return std::uniform_real_distribution<double>(0.0, 1.0)(rng_); }
 
 int32_t Sampler::draw(const Distribution& d) {
@@ -137,7 +172,11 @@ Selector::~Selector() {
   (void)mk_host_free(ctx_, in_h_);
   (void)mk_host_free(ctx_, out_v_h_);
   (void)mk_host_free(ctx_, out_i_h_);
-  (void)mk_host_free(ctx_, full_h_);
+  (void)mk_host_free(ctx_, cut_par_h_);
+  (void)mk_host_free(ctx_, cut_v_h_);
+  (void)mk_host_free(ctx_, cut_i_h_);
+  (void)mk_host_free(ctx_, cut_keep_h_);
+  (void)mk_host_free(ctx_, cut_sum_h_);
 }
 
 void Selector::clear() {
@@ -146,18 +185,17 @@ void Selector::clear() {
   pen_id_.clear();
   pen_amt_.clear();
   k_max_ = 0;
-  n_full_ = 0;
+  n_cut_ = 0;
 }
 
 int Selector::add(int row, int k, const std::vector<int32_t>& pen_ids, const std::vector<float>& pen_amounts) {
   if (k < 1 || k > n_vocab_) throw std::invalid_argument("selector: bad candidate count");
   if (pen_ids.size() != pen_amounts.size()) throw std::invalid_argument("selector: penalty lists differ in length");
   if (pen_off_.empty()) pen_off_.assign(1, 0);
-  Req r{row, k, -1};
+  Req r{row, k};
   if (k > kMaxDeviceK)
-    r.full = n_full_++;
-  else
-    k_max_ = std::max(k_max_, k);
+    throw std::invalid_argument("selector: more than 1024 candidates need the request's sampler");
+  k_max_ = std::max(k_max_, k);
   reqs_.push_back(r);
   pen_id_.insert(pen_id_.end(), pen_ids.begin(), pen_ids.end());
   pen_amt_.insert(pen_amt_.end(), pen_amounts.begin(), pen_amounts.end());
@@ -195,14 +233,46 @@ void Selector::reserve_out(size_t rows, int k) {
   out_cap_ = want;
 }
 
-void Selector::reserve_full(size_t rows) {
-  if (rows <= full_rows_) return;
-  (void)mk_host_free(ctx_, full_h_);
-  full_h_ = nullptr;
-  void* h = nullptr;
-  ck(mk_host_alloc(ctx_, rows * static_cast<size_t>(n_vocab_) * sizeof(float), &h));
-  full_h_ = static_cast<float*>(h);
-  full_rows_ = rows;
+int Selector::add(int row, const Sampler& s, const std::vector<int32_t>& pen_ids,
+                  const std::vector<float>& pen_amounts) {
+  const int k = s.candidates(n_vocab_);
+  if (k <= kMaxDeviceK) return add(row, k, pen_ids, pen_amounts);
+  if (pen_ids.size() != pen_amounts.size()) throw std::invalid_argument("selector: penalty lists differ in length");
+  if (pen_off_.empty()) pen_off_.assign(1, 0);
+  Req r{row, k, n_cut_++, s.params().temperature, s.params().min_p, s.params().top_p};
+  reqs_.push_back(r);
+  pen_id_.insert(pen_id_.end(), pen_ids.begin(), pen_ids.end());
+  pen_amt_.insert(pen_amt_.end(), pen_amounts.begin(), pen_amounts.end());
+  pen_off_.push_back(static_cast<int32_t>(pen_id_.size()));
+  return static_cast<int>(reqs_.size()) - 1;
+}
+
+void Selector::reserve_cut(size_t rows) {
+  if (rows <= cut_rows_) return;
+  const size_t want = std::max(rows, 2 * cut_rows_);
+  for (void* p : {static_cast<void*>(cut_par_h_), static_cast<void*>(cut_v_h_), static_cast<void*>(cut_i_h_),
+                  static_cast<void*>(cut_keep_h_), static_cast<void*>(cut_sum_h_)})
+    (void)mk_host_free(ctx_, p);
+  cut_par_h_ = nullptr, cut_v_h_ = nullptr, cut_i_h_ = nullptr, cut_keep_h_ = nullptr, cut_sum_h_ = nullptr;
+  auto host = [&](size_t bytes) {
+    void* h = nullptr;
+    ck(mk_host_alloc(ctx_, bytes, &h));
+    return h;
+  };
+  cut_par_h_ = static_cast<mk_cut_params*>(host(want * (sizeof(mk_cut_params) + sizeof(int32_t))));  // + the rows
+  cut_v_h_ = static_cast<float*>(host(want * kCutCap * sizeof(float)));
+  cut_i_h_ = static_cast<int32_t*>(host(want * kCutCap * sizeof(int32_t)));
+  cut_keep_h_ = static_cast<int32_t*>(host(want * sizeof(int32_t)));
+  cut_sum_h_ = static_cast<double*>(host(want * sizeof(double)));
+  cut_par_d_ = DevBuf(ctx_, want * (sizeof(mk_cut_params) + sizeof(int32_t)));  // params, then the rows
+  cut_v_d_ = DevBuf(ctx_, want * kCutCap * sizeof(float));
+  cut_i_d_ = DevBuf(ctx_, want * kCutCap * sizeof(int32_t));
+  cut_keep_d_ = DevBuf(ctx_, want * sizeof(int32_t));
+  cut_sum_d_ = DevBuf(ctx_, want * sizeof(double));
+  cut_ws_bytes_ = mk_sample_cut_workspace(static_cast<int>(want), n_vocab_);
+  if (cut_ws_bytes_ == 0) throw std::runtime_error(mk_last_error());
+  cut_ws_ = DevBuf(ctx_, cut_ws_bytes_);
+  cut_rows_ = want;
 }
 
 void Selector::enqueue(float* dev_logits) {
@@ -230,46 +300,84 @@ void Selector::enqueue(float* dev_logits) {
     ck(mk_copy_async(ctx_, out_v_h_, out_v_d_.p, n * static_cast<size_t>(k_max_) * sizeof(float)));
     ck(mk_copy_async(ctx_, out_i_h_, out_i_d_.p, n * static_cast<size_t>(k_max_) * sizeof(int32_t)));
   }
-  if (n_full_ > 0) {
-    reserve_full(static_cast<size_t>(n_full_));
-    for (const Req& r : reqs_)
-      if (r.full >= 0)
-        ck(mk_copy_async(ctx_, full_h_ + static_cast<size_t>(r.full) * n_vocab_,
-                         dev_logits + static_cast<int64_t>(r.row) * stride, n_vocab_ * sizeof(float)));
+  if (n_cut_ > 0) {
+    const size_t nc = static_cast<size_t>(n_cut_);
+    reserve_cut(nc);
+    cut_rows_h_.assign(nc, 0);
+    for (const Req& r : reqs_) {
+      if (r.cut < 0) continue;
+      cut_par_h_[r.cut] = mk_cut_params{r.k, r.temperature, r.min_p, r.top_p};
+      cut_rows_h_[static_cast<size_t>(r.cut)] = r.row;
+    }
+    std::memcpy(reinterpret_cast<uint8_t*>(cut_par_h_) + nc * sizeof(mk_cut_params), cut_rows_h_.data(),
+                nc * sizeof(int32_t));
+    ck(mk_copy_async(ctx_, cut_par_d_.p, cut_par_h_, nc * (sizeof(mk_cut_params) + sizeof(int32_t))));
+    const auto* par = cut_par_d_.as<mk_cut_params>();
+    const auto* rows = reinterpret_cast<const int32_t*>(cut_par_d_.as<uint8_t>() + nc * sizeof(mk_cut_params));
+    ck(mk_sample_cut(ctx_, dev_logits, stride, rows, n_cut_, n_vocab_, par, kCutCap, cut_v_d_.as<float>(),
+                     cut_i_d_.as<int32_t>(), cut_keep_d_.as<int32_t>(), cut_sum_d_.as<double>(), cut_ws_.p,
+                     cut_ws_bytes_));
+    ck(mk_copy_async(ctx_, cut_keep_h_, cut_keep_d_.p, nc * sizeof(int32_t)));
+    ck(mk_copy_async(ctx_, cut_sum_h_, cut_sum_d_.p, nc * sizeof(double)));
+    ck(mk_copy_async(ctx_, cut_v_h_, cut_v_d_.p, nc * kCutCap * sizeof(float)));
+    ck(mk_copy_async(ctx_, cut_i_h_, cut_i_d_.p, nc * kCutCap * sizeof(int32_t)));
   }
 }
 
+// Device-cut rows: the kept head and one candidate past it (fewer when the head is the whole row); a head longer than
+// kCutCap is fetched from the sorted row left in the workspace, with one more wait.
 void Selector::collect() {
-  full_ids_.resize(static_cast<size_t>(n_full_));
-  full_vals_.resize(static_cast<size_t>(n_full_));
+  cut_vals_.resize(static_cast<size_t>(n_cut_));
+  cut_ids_.resize(static_cast<size_t>(n_cut_));
   for (const Req& r : reqs_) {
-    if (r.full < 0) continue;
-    const float* l = full_h_ + static_cast<size_t>(r.full) * n_vocab_;
-    std::vector<int32_t>& ids = full_ids_[static_cast<size_t>(r.full)];
-    ids.resize(static_cast<size_t>(n_vocab_));
-    for (int i = 0; i < n_vocab_; ++i) ids[static_cast<size_t>(i)] = i;
-    // Highest first, equal values by lower id (the device top-k's order).
-    auto before = [&](int32_t a, int32_t b) {
-      const uint32_t ka = order_key(l[a]), kb = order_key(l[b]);
-      return ka > kb || (ka == kb && a < b);
-    };
-    std::partial_sort(ids.begin(), ids.begin() + r.k, ids.end(), before);
-    ids.resize(static_cast<size_t>(r.k));
-    std::vector<float>& v = full_vals_[static_cast<size_t>(r.full)];
-    v.resize(static_cast<size_t>(r.k));
-    for (int i = 0; i < r.k; ++i) v[static_cast<size_t>(i)] = l[ids[static_cast<size_t>(i)]];
+    if (r.cut < 0) continue;
+    const size_t c = static_cast<size_t>(r.cut);
+    const int keep = cut_keep_h_[c];
+    if (keep < 1 || keep > r.k) throw std::runtime_error("selector: device cut returned a bad keep count");
+    const int m = std::min(keep + 1, r.k);
+    std::vector<float>& v = cut_vals_[c];
+    std::vector<int32_t>& id = cut_ids_[c];
+    v.assign(cut_v_h_ + c * kCutCap, cut_v_h_ + c * kCutCap + std::min(m, kCutCap));
+    id.assign(cut_i_h_ + c * kCutCap, cut_i_h_ + c * kCutCap + std::min(m, kCutCap));
+    if (m > kCutCap) {  // values, then ids, in one device block (room for a whole row) and one download
+      const size_t more = static_cast<size_t>(m - kCutCap);
+      if (!cut_tail_d_.p) cut_tail_d_ = DevBuf(ctx_, static_cast<size_t>(n_vocab_) * 8);
+      float* tv = cut_tail_d_.as<float>();
+      int32_t* ti = reinterpret_cast<int32_t*>(tv + more);
+      ck(mk_sample_cut_tail(ctx_, cut_ws_.p, n_cut_, n_vocab_, r.cut, kCutCap, static_cast<int>(more), tv, ti));
+      tail_h_.resize(2 * more);
+      ck(mk_download(ctx_, tail_h_.data(), tv, 2 * more * sizeof(float)));
+      v.insert(v.end(), tail_h_.begin(), tail_h_.begin() + static_cast<std::ptrdiff_t>(more));
+      const auto* tid = reinterpret_cast<const int32_t*>(tail_h_.data() + more);
+      id.insert(id.end(), tid, tid + more);
+    }
   }
+}
+
+int Selector::count(int i) const {
+  const Req& r = reqs_[static_cast<size_t>(i)];
+  return r.cut >= 0 ? static_cast<int>(cut_ids_[static_cast<size_t>(r.cut)].size()) : r.k;
+}
+
+int Selector::keep(int i) const {
+  const Req& r = reqs_[static_cast<size_t>(i)];
+  return r.cut >= 0 ? cut_keep_h_[r.cut] : r.k;
+}
+
+double Selector::total(int i) const {
+  const Req& r = reqs_[static_cast<size_t>(i)];
+  return r.cut >= 0 ? cut_sum_h_[r.cut] : 0.0;
 }
 
 const float* Selector::values(int i) const {
   const Req& r = reqs_[static_cast<size_t>(i)];
-  if (r.full >= 0) return full_vals_[static_cast<size_t>(r.full)].data();
+  if (r.cut >= 0) return cut_vals_[static_cast<size_t>(r.cut)].data();
   return out_v_h_ + static_cast<size_t>(i) * out_k_;
 }
 
 const int32_t* Selector::ids(int i) const {
   const Req& r = reqs_[static_cast<size_t>(i)];
-  if (r.full >= 0) return full_ids_[static_cast<size_t>(r.full)].data();
+  if (r.cut >= 0) return cut_ids_[static_cast<size_t>(r.cut)].data();
   return out_i_h_ + static_cast<size_t>(i) * out_k_;
 }
 

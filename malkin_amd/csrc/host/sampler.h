@@ -62,6 +62,9 @@ class Sampler {
   // The distribution from a row's candidates: values (penalized logits) and ids, highest first, n of them
   // (candidates(n_vocab), or fewer only for greedy).
   void finish(const float* values, const int32_t* ids, int n, Distribution& out) const;
+  // The same from request i of a collected Selector: its candidates, or for a row cut on the device (more than
+  // Selector::kMaxDeviceK candidates) its kept head and total.
+  void finish(const class Selector& sel, int i, Distribution& out) const;
   int32_t draw(const Distribution& d);
   int32_t verify(const Distribution& p, const Distribution& q, int32_t draft, bool& accepted);
   void accept(int32_t id) { ++counts_[id]; }
@@ -77,12 +80,15 @@ class Sampler {
 };
 
 // Candidate selection for several logits rows with one host wait: per row its penalties and candidate count; the
-// device penalizes the rows in place and cuts the top-k (up to 1024 candidates), a row that needs more (top_k <= 0,
-// or above 1024) is copied whole and sorted on the host. enqueue() queues the work and the copies on the context's
-// stream; after the caller's next mk_synchronize, collect() makes the candidates readable.
+// device penalizes the rows in place and cuts the top-k (up to 1024 candidates); a row that needs more (top_k <= 0,
+// or above 1024) is sorted and cut on the device with its request's temperature, min_p and top_p (mk_sample_cut),
+// and only its kept head and total come back. enqueue() queues the work and the copies on the context's stream;
+// after the caller's next mk_synchronize, collect() makes the candidates readable (a kept head longer than
+// kCutCap takes one more copy and wait there).
 class Selector {
  public:
   static constexpr int kMaxDeviceK = 1024;
+  static constexpr int kCutCap = 4096;  // candidates of a device-cut row copied back with the step's wait
   Selector(mk_ctx* ctx, int n_vocab);
   ~Selector();
   Selector(const Selector&) = delete;
@@ -92,29 +98,36 @@ class Selector {
   // Logits row `row` of the buffer the next enqueue() reads; penalties (may be empty) are applied in place.
   // Returns the request's index.
   int add(int row, int k, const std::vector<int32_t>& pen_ids, const std::vector<float>& pen_amounts);
+  // The same for a request's sampler: its candidate count, and its parameters for a device cut.
+  int add(int row, const Sampler& s, const std::vector<int32_t>& pen_ids, const std::vector<float>& pen_amounts);
   bool empty() const { return reqs_.empty(); }
   void enqueue(float* dev_logits);
   void collect();
   // After collect(): candidates of request i, highest first (count(i) of them).
   const float* values(int i) const;
   const int32_t* ids(int i) const;
-  int count(int i) const { return reqs_[static_cast<size_t>(i)].k; }
+  int count(int i) const;
+  // A row cut on the device: count(i) candidates of which the first keep(i) are kept, the total of all weights.
+  bool cut(int i) const { return reqs_[static_cast<size_t>(i)].cut >= 0; }
+  int keep(int i) const;
+  double total(int i) const;
 
  private:
   struct Req {
     int row, k;
-    int full = -1;  // index among whole-row copies, or -1
+    int cut = -1;  // index among the device-cut rows, or -1
+    float temperature = 1.0f, min_p = 0.0f, top_p = 1.0f;
   };
   void reserve_host(size_t words);
   void reserve_out(size_t rows, int k);
-  void reserve_full(size_t rows);
+  void reserve_cut(size_t rows);
 
   mk_ctx* ctx_;
   int n_vocab_;
   std::vector<Req> reqs_;
   std::vector<int32_t> pen_off_, pen_id_;
   std::vector<float> pen_amt_;
-  int k_max_ = 0, n_full_ = 0;
+  int k_max_ = 0, n_cut_ = 0;
   // Upload block (rows, pen_off, pen_id, pen_amt) in pinned memory and on the device; results likewise.
   int32_t* in_h_ = nullptr;
   size_t in_words_ = 0;
@@ -123,10 +136,21 @@ class Selector {
   int32_t* out_i_h_ = nullptr;
   size_t out_cap_ = 0;  // rows * k entries
   DevBuf out_v_d_, out_i_d_;
-  float* full_h_ = nullptr;
-  size_t full_rows_ = 0;
-  std::vector<std::vector<int32_t>> full_ids_;  // whole-vocabulary rows after collect(): ids and values, sorted
-  std::vector<std::vector<float>> full_vals_;
+  // Device-cut rows: parameters, outputs and workspace on the device; outputs in pinned memory; after collect()
+  // each row's candidates (the kept head and one past it) on the host.
+  size_t cut_rows_ = 0;
+  DevBuf cut_ws_, cut_par_d_, cut_v_d_, cut_i_d_, cut_keep_d_, cut_sum_d_;
+  size_t cut_ws_bytes_ = 0;
+  mk_cut_params* cut_par_h_ = nullptr;
+  float* cut_v_h_ = nullptr;
+  int32_t* cut_i_h_ = nullptr;
+  int32_t* cut_keep_h_ = nullptr;
+  double* cut_sum_h_ = nullptr;
+  std::vector<int32_t> cut_rows_h_;
+  DevBuf cut_tail_d_;          // a kept head past kCutCap: its candidates from the sorted row
+  std::vector<float> tail_h_;
+  std::vector<std::vector<float>> cut_vals_;
+  std::vector<std::vector<int32_t>> cut_ids_;
   int out_k_ = 0;
 };
 

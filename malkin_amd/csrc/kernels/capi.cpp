@@ -6,7 +6,9 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <memory>
+#include <mutex>
 #include <vector>
 
 #include "ctx.h"
@@ -17,6 +19,18 @@ namespace mk {
 namespace {
 thread_local char g_err[512] = "";
 std::atomic<uint64_t> g_host_waits{0};
+std::atomic<uint64_t> g_host_bytes{0};
+// Pinned blocks from mk_host_alloc (start -> bytes): copies into them count as downloads.
+std::mutex g_pinned_m;
+std::map<uintptr_t, size_t> g_pinned;
+bool pinned(const void* p, size_t bytes) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  std::lock_guard<std::mutex> lk(g_pinned_m);
+  auto it = g_pinned.upper_bound(a);
+  if (it == g_pinned.begin()) return false;
+  --it;
+  return a + bytes <= it->first + it->second;
+}
 }
 
 void count_host_wait() { g_host_waits.fetch_add(1, std::memory_order_relaxed); }
@@ -108,6 +122,7 @@ int mk_synchronize(mk_ctx* c) {
 }
 
 uint64_t mk_host_waits(void) { return mk::g_host_waits.load(std::memory_order_relaxed); }
+uint64_t mk_host_bytes(void) { return mk::g_host_bytes.load(std::memory_order_relaxed); }
 
 void* mk_stream(mk_ctx* c) { return c ? c->stream : nullptr; }
 
@@ -142,6 +157,7 @@ int mk_download(mk_ctx* c, void* dst, const void* src, size_t bytes) {
   return guard([&] {
     if (!bytes) return;
     check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream), "hipMemcpy D2H");
+    mk::g_host_bytes.fetch_add(bytes, std::memory_order_relaxed);
     mk::count_host_wait();
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
   });
@@ -152,6 +168,8 @@ int mk_host_alloc(mk_ctx* c, size_t bytes, void** host) {
     require(host != nullptr, "mk_host_alloc: null output");
     check(hipSetDevice(c->device), "hipSetDevice");
     check(hipHostMalloc(host, bytes ? bytes : 1, hipHostMallocDefault), "hipHostMalloc");
+    std::lock_guard<std::mutex> lk(mk::g_pinned_m);
+    mk::g_pinned[reinterpret_cast<uintptr_t>(*host)] = bytes ? bytes : 1;
   });
 }
 
@@ -162,6 +180,8 @@ int mk_host_free(mk_ctx* c, void* host) {
     mk::count_host_wait();
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     check(hipHostFree(host), "hipHostFree");
+    std::lock_guard<std::mutex> lk(mk::g_pinned_m);
+    mk::g_pinned.erase(reinterpret_cast<uintptr_t>(host));
   });
 }
 
@@ -169,6 +189,7 @@ int mk_copy_async(mk_ctx* c, void* dst, const void* src, size_t bytes) {
   return guard([&] {
     if (!bytes) return;
     check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, c->stream), "hipMemcpyAsync");
+    if (mk::pinned(dst, bytes) && !mk::pinned(src, bytes)) mk::g_host_bytes.fetch_add(bytes, std::memory_order_relaxed);
   });
 }
 
@@ -462,6 +483,31 @@ int mk_topk(mk_ctx* c, const float* logits, int64_t stride, const int32_t* rows,
   return guard([&] {
     require(logits && values && ids && n_rows >= 0 && n_vocab > 0 && stride >= n_vocab, "topk: bad arguments");
     mk::topk(c->stream, logits, stride, rows, n_rows, n_vocab, k, values, ids);
+  });
+}
+
+size_t mk_sample_cut_workspace(int n_rows, int n_vocab) {
+  size_t n = 0;
+  return guard([&] { n = mk::sample_cut_workspace(n_rows, n_vocab); }) == MK_OK ? n : 0;
+}
+
+int mk_sample_cut(mk_ctx* c, const float* logits, int64_t stride, const int32_t* rows, int n_rows, int n_vocab,
+                  const mk_cut_params* params, int cap, float* values, int32_t* ids, int32_t* keep, double* sums,
+                  void* workspace, size_t workspace_bytes) {
+  return guard([&] {
+    require(c && logits && params && values && ids && keep && sums && n_rows >= 0 && n_vocab > 0 &&
+                stride >= n_vocab,
+            "sample_cut: bad arguments");
+    mk::sample_cut(c->stream, logits, stride, rows, n_rows, n_vocab, params, cap, values, ids, keep, sums, workspace,
+                   workspace_bytes);
+  });
+}
+
+int mk_sample_cut_tail(mk_ctx* c, void* workspace, int n_rows, int n_vocab, int row, int from, int count,
+                       float* values, int32_t* ids) {
+  return guard([&] {
+    require(c && workspace && values && ids && n_vocab > 0, "sample_cut_tail: bad arguments");
+    mk::sample_cut_tail(c->stream, workspace, n_rows, n_vocab, row, from, count, values, ids);
   });
 }
 

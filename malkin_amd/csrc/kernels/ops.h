@@ -1,6 +1,7 @@
 // Library-internal launchers (throw mk::Error). The extern "C" layer and the host Model call these.
 #pragma once
 
+#include "../../../include/malkin_hip.h"
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -216,6 +217,12 @@ void penalize(hipStream_t s, float* logits, int64_t stride, const int32_t* rows,
               const int32_t* pen_off, const int32_t* pen_id, const float* pen_amt);
 void topk(hipStream_t s, const float* logits, int64_t stride, const int32_t* rows, int n_rows, int n_vocab, int k,
           float* values, int32_t* ids);
+size_t sample_cut_workspace(int n_rows, int n_vocab);
+void sample_cut(hipStream_t s, const float* logits, int64_t stride, const int32_t* rows, int n_rows, int n_vocab,
+                const mk_cut_params* params, int cap, float* values, int32_t* ids, int32_t* keep, double* sums,
+                void* workspace, size_t workspace_bytes);
+void sample_cut_tail(hipStream_t s, void* workspace, int n_rows, int n_vocab, int row, int from, int count,
+                     float* values, int32_t* ids);
 
 // dst[dst_idx[i]] = src[src_idx[i]], i < n; null index arrays are the identity, negative indices skip.
 void move_ids(hipStream_t s, int32_t* dst, const int32_t* dst_idx, const int32_t* src, const int32_t* src_idx,

@@ -39,6 +39,18 @@ def top2(l):
     return a, b
 
 
+def chunked(m, toks, pos):
+    """The last row of tokens fed from position pos in forwards of at most K_MAX_BATCH tokens, as the reference
+    engine feeds a prompt (one chunk per step, engine.cpp:359-381) and a draft's catch-up (passes flushed when full,
+    engine.cpp:283-298): where the arithmetic depends on a forward's size (Q6_K's wide panels past 16 tokens), the
+    chunking decides the row."""
+    toks = np.asarray(toks, np.int32)
+    last = None
+    for i in range(0, len(toks), K_MAX_BATCH):
+        last = m.forward(toks[i:i + K_MAX_BATCH], pos + i)[-1].copy()
+    return last
+
+
 def run_request(cpu, target, draft, prompt, max_tokens, n_ctx, seed, eog=(), n_draft=8, **params):
     """cpu: bind.Oracle() or bind.Ref(); target / draft: its models (draft may be None) with a fresh sequence 0.
     Returns (tokens, info) with the engine's counters."""
@@ -61,7 +73,7 @@ def run_request(cpu, target, draft, prompt, max_tokens, n_ctx, seed, eog=(), n_d
             return False
         return len(cache) + 1 < n_ctx
 
-    last = target.forward(np.asarray(prompt, np.int32), 0)[-1].copy()
+    last = chunked(target, prompt, 0)
     nxt = S.sample(last)
     alive = emit(nxt)
     while alive:
@@ -79,7 +91,7 @@ def run_request(cpu, target, draft, prompt, max_tokens, n_ctx, seed, eog=(), n_d
             common = min(common, L - 1)
             dcache = dcache[:common]
             toks = [cache[q] if q < P else nxt for q in range(common, L)]
-            dl = draft.forward(np.asarray(toks, np.int32), common)[-1].copy()
+            dl = chunked(draft, toks, common)
             dcache += toks
             for i in range(kk):
                 if greedy:

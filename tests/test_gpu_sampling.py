@@ -163,3 +163,47 @@ def test_engine_sampled_speculative(mk, oracle, model_files, draft_name):
     reqs = [dict(seed=7), dict(seed=11, temperature=0.9, presence=1.5), dict(seed=10, temperature=0.0, frequency=0.6),
             dict(seed=9, temperature=0.6, top_k=300)]
     check_engine(mk, oracle, model_files, draft_name, reqs)
+
+
+CUT_CASES = [
+    (dict(top_k=0), 4.0),                                   # peaked rows: a short kept head
+    (dict(top_k=0, temperature=1.3, top_p=0.99, min_p=0.0), 0.5),  # flat rows: a head past the copy's cap
+    (dict(top_k=2000, top_p=0.97, min_p=0.0), 1.0),
+    (dict(top_k=5000, top_p=1.0, min_p=0.0), 2.0),         # every candidate kept: 5000 > the cap
+]
+
+
+@pytest.mark.parametrize("params,scale", CUT_CASES, ids=[str(c[0]) for c in CUT_CASES])
+def test_whole_vocab_cut_on_device(mk, oracle, params, scale):
+    """Rows with more than 1024 candidates (top_k <= 0 or above 1024) at V = 151,936 are sorted and cut on the
+    device (mk_sample_cut): the distributions and draws equal the oracle's, and what a step downloads is the kept
+    head (within the 4096-candidate copy, one wait) instead of the 608 KB row; a head past the copy costs one more
+    wait and only its own candidates."""
+    V = 151936
+    L = mk_.load()
+    rng = np.random.default_rng(17)
+    s, a = mk_.Sampler(7, **params), oracle.sampler(7, **params)
+    buf = mk.alloc(V * 4)
+    print("cut", params, scale, flush=True)
+    for step in range(6):
+        l = (rng.standard_normal(V) * scale).astype(np.float32)
+        buf.upload(l)
+        w0, b0 = L.mk_host_waits(), L.mk_host_bytes()
+        d = s.distribution(mk, buf, V)
+        waits, nbytes = L.mk_host_waits() - w0, L.mk_host_bytes() - b0
+        e = a.distribution(l.copy())
+        assert d == e, (step, len(d), len(e), d[:3], e[:3])
+        kept = len(d)
+        print("step", step, "kept", kept, "waits", waits, "bytes", nbytes, flush=True)
+        head = min(kept + 1, params["top_k"] if params["top_k"] > 0 else V)
+        if step > 0:  # the first call also allocates the selector's buffers
+            assert waits == (1 if head <= 4096 else 2), waits
+        assert nbytes <= 4096 * 8 + 64 + max(0, head - 4096) * 8, nbytes
+        if head <= 4096:
+            assert nbytes < V * 4 // 16, nbytes
+        t1, t2 = s.draw(d), a.draw(e)
+        assert t1 == t2, step
+        s.accept(t1)
+        a.accept(t2)
+    s.close()
+    buf.free()
