@@ -111,6 +111,9 @@ SIGNATURES = {
     "mk_engine_submit_sampled": (_I, [_P, _P, _I, _I, _P, _I, _P, _P]),
     "mk_penalize": (_I, [_P, _P, _I64, _P, _I, _I, _P, _P, _P]),
     "mk_topk": (_I, [_P, _P, _I64, _P, _I, _I, _I, _P, _P]),
+    "mk_sample_cut_workspace": (ctypes.c_size_t, [_I, _I]),
+    "mk_sample_cut": (_I, [_P, _P, _I64, _P, _I, _I, _P, _I, _P, _P, _P, _P, _P, ctypes.c_size_t]),
+    "mk_sample_cut_tail": (_I, [_P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "mk_server_start": (_I, [_P, ctypes.c_char_p, ctypes.c_char_p, _I, ctypes.POINTER(_P), ctypes.POINTER(_I)]),
     "mk_server_stop": (_I, [_P]),
     "mk_sampler_create": (_I, [_P, _I, ctypes.POINTER(_P)]),
