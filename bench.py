@@ -207,6 +207,60 @@ def kernel_configs(ctx):
     return out
 
 
+def decode_probe():
+    """Launch sequence for the instruction / wait / LDS counters of one decode layer's kernels (run under rocprofv3
+    --pmc with one counter group per pass): the fused decode attention of the Qwen3-8B shape (32 query heads over 8
+    KV heads, head_dim 128) at 600 keys with its QK-norm / RoPE / KV write and BlockQ8 output (mk_attention_decode_q8),
+    then the four decode GEMVs as the decode launches them (q|k|v with the norm prologue, attn_output accumulating,
+    gate|up with the norm prologue and SiLU epilogue, down accumulating), each 4 times."""
+    import ctypes
+    import malkin_amd as mk
+    L = mk.load()
+    ctx = mk.Context(0)
+    rng = np.random.default_rng(5)
+    eps = ctypes.c_float(1e-6)
+    D, H, KV, n_ctx, pos = 128, 32, 8, 1024, 599
+    QKV = (H + 2 * KV) * D
+    qkv = ctx.to_device(rng.standard_normal(QKV).astype(np.float32))
+    norms = ctx.to_device(rng.uniform(0.5, 1.5, 2 * D).astype(np.float32))
+    ang = np.arange(n_ctx, dtype=np.float32)[:, None] * np.float32(1e-3) * (np.arange(D // 2, dtype=np.float32) + 1)
+    cos_t, sin_t = ctx.to_device(np.cos(ang).astype(np.float32)), ctx.to_device(np.sin(ang).astype(np.float32))
+    k8 = ctx.to_device(rng.integers(-127, 128, (1, KV, n_ctx, D), dtype=np.int8))
+    v8 = ctx.to_device(rng.integers(-127, 128, (1, KV, n_ctx, D), dtype=np.int8))
+    ks = ctx.to_device(rng.uniform(0.001, 0.05, (1, KV, n_ctx)).astype(np.float32))
+    vs = ctx.to_device(rng.uniform(0.001, 0.05, (1, KV, n_ctx)).astype(np.float32))
+    kv = mk.MkKvCache(k8.ptr, v8.ptr, ks.ptr, vs.ptr, 1, 1, KV, D, n_ctx)
+    meta = {nm: ctx.to_device(np.array([v], np.int32)) for nm, v in (("rpos", pos), ("seq", 0), ("kv_row", pos),
+                                                                       ("n_keys", pos + 1))}
+    out, xq = ctx.alloc(H * D * 4), ctx.alloc(H * D // 32 * 40)
+    ctx.sync()
+    for i in range(4):
+        mk.check(L.mk_attention_decode_q8(ctx.h, qkv.ptr, QKV, 1, H, norms.ptr, norms.offset(D * 4), eps, cos_t.ptr,
+                                          sin_t.ptr, meta["rpos"].ptr, meta["seq"].ptr, meta["kv_row"].ptr,
+                                          meta["n_keys"].ptr, ctypes.byref(kv), 0, out.ptr, H * D, pos + 1, xq.ptr))
+    ctx.sync()
+    log(f"[probe] k_attention_dec: {H} heads over {KV} KV heads, head_dim {D}, {pos + 1} keys: 4 launches")
+    for rows, cols, norm, acc, silu in ((6144, 4096, 1, 0, 0), (4096, 4096, 0, 1, 0), (24576, 4096, 1, 0, 1),
+                                        (4096, 12288, 0, 1, 0)):
+        ws = pack_copies(ctx, mk.Q8_0, random_weight(rng, mk.Q8_0, rows, cols), rows, cols, 2)
+        x = ctx.to_device(rng.standard_normal(cols).astype(np.float32))
+        nw = ctx.to_device(np.ones(cols, np.float32)) if norm else None
+        out_rows = rows // 2 if silu else rows
+        y = ctx.to_device(np.zeros(out_rows, np.float32))
+        ctx.sync()
+        for i in range(4):
+            mk.check(L.mk_matmul_f32(ctx.h, ctypes.byref(ws[i % 2][1]), x.ptr, cols, nw.ptr if nw else None, eps, 1,
+                                     y.ptr, out_rows, acc, silu))
+        ctx.sync()
+        log(f"[probe] k_gemv Q8_0 {rows}x{cols} n=1 (norm {norm}, accumulate {acc}, silu {silu}): 4 launches")
+        for b, _w in ws:
+            b.free()
+        for b in (x, nw, y):
+            if b is not None:
+                b.free()
+    ctx.close()
+
+
 def traffic_probe():
     """Launch sequence for the HBM-traffic counters of the roofline kernel (run under rocprofv3 --pmc FETCH_SIZE, then
     WRITE_SIZE): the four decode GEMV variants of the Qwen3-8B layer as the decode launches them (q|k|v 6144x4096 with
@@ -534,13 +588,17 @@ def main():
     ap.add_argument("--no-engine-configs", action="store_true",
                     help="skip BASELINE configs 3 (Qwen3-4B pp512 + tg128), 4 (continuous batching) and 5 "
                          "(speculative tree verification)")
-    ap.add_argument("--probe", choices=["traffic", "gemm", "kquant", "tree"],
+    ap.add_argument("--probe", choices=["traffic", "decode", "gemm", "kquant", "tree"],
                     help="only run a launch sequence for counter profiles: the roofline kernel's HBM traffic, "
+                         "one decode layer's kernels (attention and the four GEMVs, for instruction and wait counters), "
                          "the prefill GEMM (config 1 and the pp512 forward's shapes), config 2's short K-quant batches, "
                          "or config 5's tree verification")
     args = ap.parse_args()
     if args.probe == "traffic":
         traffic_probe()
+        return
+    if args.probe == "decode":
+        decode_probe()
         return
     if args.probe == "gemm":
         gemm_probe()
