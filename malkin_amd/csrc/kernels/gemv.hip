@@ -118,8 +118,8 @@ struct GemvCfg {
   // Units the chain reads per group; it runs whole groups, over zero terms past the last unit.
   static constexpr int kG = (TYPE == kQ4_K || (TYPE == kQ6_K && !WIDE)) ? 4 : 8;
   static_assert(kChunk % kG == 0, "groups tile the chunk");
-  // Term slot: per chain lane (token t, row r) the chunk's units in order, E floats each, plus one group that the
-  // chain reads ahead past the end, plus 4 floats against bank conflicts (rows stay 16-byte aligned). Q4_K mins:
+  // Term slot: per chain lane (token t, row r) the chunk's units in order, E floats each, plus one group of padding,
+  // plus 4 floats against bank conflicts (rows stay 16-byte aligned). Q4_K mins:
   // per row, 2 floats per unit, laid out the same way.
   static constexpr int kLane = (kChunk + kG) * E + 4;
   static constexpr int kSlot = NT * R * kLane;
@@ -501,22 +501,20 @@ __global__ __launch_bounds__(kThreads) void k_gemv(const uint8_t* W, int64_t row
     if (!chain_lane) return;
     const int c = q % nc;
     const int cn = min(kChunk, nu - c * kChunk);
-    Terms A, B;
-    fetch(A, q, 0);
-    // The fetches are never predicated (the last one reads the padding group): the wait before each group then
-    // counts exactly the reads issued after it.
-    // Scheduling barriers keep each fetch ahead of the previous group's fmas.
-    for (int ul0 = 0;;) {
-      fetch(B, q, ul0 + kG);
+    // The chunk's kChunk / kG groups, each read kAhead groups ahead of its fmas (Q8_0's small groups: two, so that
+    // the LDS latency hides behind the fmas of two groups; the larger K-quant groups: one). The reads stay inside
+    // the chunk's terms whatever cn is (never predicated, so the wait before each group counts exactly the reads
+    // issued after it); groups past cn are skipped (wave-uniform). Scheduling barriers keep the reads ahead.
+    constexpr int kNG = kChunk / kG, kAhead = TYPE == kQ8_0 ? 2 : 1;
+    Terms T[kNG];
+#pragma unroll
+    for (int g = 0; g < kAhead; ++g) fetch(T[g], q, g * kG);
+#pragma unroll
+    for (int g = 0; g < kNG; ++g) {
+      if (g + kAhead < kNG) fetch(T[g + kAhead], q, (g + kAhead) * kG);
       __builtin_amdgcn_sched_barrier(0);
-      step(A);
+      if (g * kG < cn) step(T[g]);
       __builtin_amdgcn_sched_barrier(0);
-      if ((ul0 += kG) >= cn) break;
-      fetch(A, q, ul0 + kG);
-      __builtin_amdgcn_sched_barrier(0);
-      step(B);
-      __builtin_amdgcn_sched_barrier(0);
-      if ((ul0 += kG) >= cn) break;
     }
     if (c == nc - 1) {
       if constexpr (EPI == kEpiSilu) {
