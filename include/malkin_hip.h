@@ -255,6 +255,12 @@ int mk_decode_supported(const mk_decode_plan* plan, int max_keys);
 /* Queues layers [l0, l1) of one decode step on the context's stream; allocates nothing (graph-capturable). Every
    cross-workgroup wait inside is bounded; a wait that runs out marks the plan's error word (mk_decode_check). */
 int mk_decode_layers(mk_ctx* ctx, mk_decode_plan* plan, int l0, int l1, int max_keys);
+/* Model::run's attention and attn_output steps of layer `layer` for one token (model.cpp:370-401 at n = 1) in one
+   launch: after the layer's q|k|v matmul has written qkv, the attention (QK-norm, RoPE, KV write, BlockQ8 output)
+   runs on n_head workgroups while the others load their attn_output weights, then x += W_o . att. Same results as
+   mk_attention_decode_q8 followed by mk_matmul (accumulate); same support rule and error word as
+   mk_decode_layers. */
+int mk_decode_attn_wo(mk_ctx* ctx, mk_decode_plan* plan, int layer, int max_keys);
 /* After the stream has been synchronized: MK_OK, or MK_ERR_HIP if a launch since the last check timed out in a
    hand-off wait (its results are invalid); the error word and the counters are then cleared. */
 int mk_decode_check(mk_ctx* ctx, mk_decode_plan* plan);

@@ -49,8 +49,10 @@ enum {
   MK_MODEL_NO_WIDE = 1, /* no wide Q6_K prefill panels (the reference's MALKIN_NO_WIDE, model.cpp:181) */
   MK_MODEL_NO_PACK = 2, /* no packed weights: every matmul on the row path over GGUF rows (MALKIN_NO_PACK,
                            model.cpp:136; quant.cpp:330-351). F32 / F16 / BF16 weights take that path anyway. */
-  MK_MODEL_PERSISTENT = 4 /* one-token forwards run every layer in the persistent decode kernel (mk_decode_layers)
-                             instead of launching each step of each layer on its own; the results are the same */
+  MK_MODEL_PERSISTENT = 4, /* one-token forwards run every layer in the persistent decode kernel (mk_decode_layers)
+                              instead of launching each step of each layer on its own; the results are the same */
+  MK_MODEL_FUSED_ATTN = 8  /* one-token forwards run each layer's attention and attn_output in one launch
+                              (mk_decode_attn_wo); the results are the same. Ignored with MK_MODEL_PERSISTENT. */
 };
 
 /* Model::Model(GgufFile, n_ctx, n_seq) (model.h:38) + Model::pack_wide (model.h:43) unless MK_MODEL_NO_WIDE. Weights
@@ -89,7 +91,8 @@ int mk_model_generate(mk_model* m, const int32_t* prompt, int n_prompt, int n_ge
                       int32_t* out_tokens, mk_gen_stats* stats);
 
 /* 1 if the model's one-token forwards run the persistent decode kernel (mk_decode_layers: MK_MODEL_PERSISTENT set,
-   and every layer with fused Q8_0 q|k|v and gate|up weights of a supported shape), else 0. */
+   and every layer with fused Q8_0 q|k|v and gate|up weights of a supported shape), 2 if they run the fused attention
+   and attn_output launch (mk_decode_attn_wo: MK_MODEL_FUSED_ATTN, same conditions), else 0. */
 int mk_model_persistent(const mk_model* m);
 /* Bytes of packed weights the model holds in HBM. */
 int64_t mk_model_weight_bytes(const mk_model* m);

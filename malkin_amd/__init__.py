@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(HERE, "libmalkin_hip.so")
 
 MK_OK, MK_ERR_INVALID, MK_ERR_HIP, MK_ERR_UNSUPPORTED, MK_ERR_NO_DEVICE = 0, 1, 2, 3, 4
 F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 8, 12, 13, 14, 30
-MODEL_NO_WIDE, MODEL_NO_PACK, MODEL_PERSISTENT = 1, 2, 4
+MODEL_NO_WIDE, MODEL_NO_PACK, MODEL_PERSISTENT, MODEL_FUSED_ATTN = 1, 2, 4, 8
 
 BLOCK_Q8 = np.dtype([("d", "<f4"), ("s", "<i2", (2,)), ("qs", "i1", (32,))])
 BATCH_TOKEN = np.dtype([("id", "<i4"), ("seq", "<i4"), ("pos", "<i4"), ("logits", "<i4"), ("kv", "<i4"),
@@ -73,6 +73,7 @@ SIGNATURES = {
     "mk_decode_supported": (_I, [_P, _I]),
     "mk_decode_layers": (_I, [_P, _P, _I, _I, _I]),
     "mk_decode_check": (_I, [_P, _P]),
+    "mk_decode_attn_wo": (_I, [_P, _P, _I, _I]),
     "mk_model_persistent": (_I, [_P]),
     "mk_model_eog": (_I, [_P, _P, _I]),
     "mk_argmax_top2": (_I, [_P, _P, _I, _I, _P, _P]),
@@ -283,11 +284,11 @@ def gguf_inspect(path):
 class Model:
     """mk_model_* wrapper: the device counterpart of the reference's Model (model.h)."""
 
-    def __init__(self, ctx, path, n_ctx, n_seq=1, wide=True, no_pack=False, persistent=False):
+    def __init__(self, ctx, path, n_ctx, n_seq=1, wide=True, no_pack=False, persistent=False, fused_attn=False):
         self.ctx = ctx
         p = _P()
         flags = ((0 if wide else MODEL_NO_WIDE) | (MODEL_NO_PACK if no_pack else 0) |
-                 (MODEL_PERSISTENT if persistent else 0))
+                 (MODEL_PERSISTENT if persistent else 0) | (MODEL_FUSED_ATTN if fused_attn else 0))
         check(load().mk_model_open(ctx.h, path.encode(), n_ctx, n_seq, flags, ctypes.byref(p)))
         self.h = p.value
         c = MkModelConfig()
@@ -307,7 +308,13 @@ class Model:
 
     @property
     def persistent(self):
-        return bool(load().mk_model_persistent(self.h))
+        """One-token forwards in the persistent decode kernel (every layer in one launch)."""
+        return load().mk_model_persistent(self.h) == 1
+
+    @property
+    def fused_attn(self):
+        """One-token forwards with each layer's attention and attn_output in one launch."""
+        return load().mk_model_persistent(self.h) == 2
 
     @property
     def eog(self):

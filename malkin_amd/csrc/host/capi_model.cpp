@@ -118,12 +118,17 @@ int mk_model_open(mk_ctx* ctx, const char* path, int n_ctx, int n_seq, int flags
     m->file = std::make_unique<malkin_hip::GgufFile>(path);
     m->model = std::make_unique<malkin_hip::Model>(ctx, *m->file, n_ctx, n_seq, (flags & MK_MODEL_NO_WIDE) == 0,
                                                     (flags & MK_MODEL_NO_PACK) != 0,
-                                                    (flags & MK_MODEL_PERSISTENT) != 0);
+                                                    (flags & MK_MODEL_PERSISTENT)  ? malkin_hip::Model::kDecodePersistent
+                                                    : (flags & MK_MODEL_FUSED_ATTN) ? malkin_hip::Model::kDecodeFusedAttn
+                                                                                    : malkin_hip::Model::kDecodeSteps);
     *out = m.release();
   });
 }
 
-int mk_model_persistent(const mk_model* m) { return m && m->model && m->model->persistent() ? 1 : 0; }
+int mk_model_persistent(const mk_model* m) {
+  if (!m || !m->model) return 0;
+  return m->model->persistent() ? 1 : m->model->fused_attn() ? 2 : 0;
+}
 
 int mk_model_eog(const mk_model* m, int32_t* out, int cap) {
   int n = 0;

@@ -274,8 +274,8 @@ bool Model::matmul_group_f32(const Group& g, const float* x, int64_t xs, const f
   return true;
 }
 
-Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide, bool no_pack, bool persistent)
-    : ctx_(ctx), cfg_(read_config(f)), n_ctx_(n_ctx), n_seq_(n_seq), wide_(wide), no_pack_(no_pack) {
+Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide, bool no_pack, int decode)
+    : ctx_(ctx), cfg_(read_config(f)), n_ctx_(n_ctx), n_seq_(n_seq), wide_(wide), no_pack_(no_pack), decode_(decode) {
   auto& c = cfg_;
   if (c.n_head <= 0 || c.n_head_kv <= 0 || c.head_dim <= 0 || c.head_dim % 32 || c.n_head % c.n_head_kv)
     throw std::runtime_error("model: unsupported head layout");
@@ -394,7 +394,7 @@ Model::Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq, bool wide, bo
     ck(mk_host_alloc(ctx_, layout_words_ * sizeof(int32_t), &h));
     st.host = static_cast<int32_t*>(h);
   }
-  if (persistent) make_decode_plan();
+  if (decode_ != kDecodeSteps) make_decode_plan();
   ck(mk_synchronize(ctx_));
   for (LoadBlock& b : load_) b.release();  // loading is done: the staging ring goes
   load_block_bytes_ = 0;
@@ -612,7 +612,8 @@ void Model::run() {
   const mk_kv_cache& kv = kv_;
   ck(mk_dequantize_rows(ctx_, embd_type_, embd_rows_.p, embd_row_bytes_, d_ids_, n, E, x));
   // One token: every layer in one persistent launch (same results as the per-step launches below).
-  const bool persistent = dplan_ && n == 1 && !lay_.tree && mk_decode_supported(dplan_, lay_.max_keys);
+  const bool one = dplan_ && n == 1 && !lay_.tree && mk_decode_supported(dplan_, lay_.max_keys);
+  const bool persistent = one && decode_ == kDecodePersistent, fused_attn = one && decode_ == kDecodeFusedAttn;
   if (persistent) {
     ck(mk_decode_layers(ctx_, dplan_, 0, c.n_layer, lay_.max_keys));
     dplan_pending_ = true;
@@ -629,6 +630,10 @@ void Model::run() {
       ck(mk_rmsnorm_q8(ctx_, x, nullptr, norms, n, E, c.rms_eps, xq));
       matmul_group(L.qkv, xq, n, qkv);
     }
+    if (fused_attn) {  // attention and x += attn_output(att) in one launch
+      ck(mk_decode_attn_wo(ctx_, dplan_, il, lay_.max_keys));
+      dplan_pending_ = true;
+    }
     // Short plain batches of distinct sequences (decode steps): QK-norm, RoPE, the KV write and attention in one
     // launch; otherwise (prompt chunks, trees, shared sequences) the KV rows are written before any token attends.
     // Where attn_output takes BlockQ8 activations, the attention kernels write them beside att (the reference's
@@ -637,7 +642,9 @@ void Model::run() {
     wo.wide = wide_ ? 1 : 0;
     const bool wo_f32 = matmul_f32_ok(wo, n, false);
     int rc = MK_ERR_UNSUPPORTED;
-    if (!lay_.tree && lay_.distinct_seqs && n < 16) {
+    if (fused_attn) {
+      rc = MK_OK;
+    } else if (!lay_.tree && lay_.distinct_seqs && n < 16) {
       rc = wo_f32 ? mk_attention_decode(ctx_, qkv, QKV, n, H, norms + 2 * E, norms + 2 * E + D, c.rms_eps,
                                         rope_cos_.as<float>(), rope_sin_.as<float>(), d_rpos_, d_seq_, d_kv_row_,
                                         d_n_keys_, &kv, il, att, static_cast<int64_t>(H) * D, lay_.max_keys)
@@ -658,7 +665,9 @@ void Model::run() {
     } else {
       ck(rc);
     }
-    if (wo_f32)
+    if (fused_attn)
+      ;
+    else if (wo_f32)
       ck(mk_matmul_f32(ctx_, &wo, att, static_cast<int64_t>(H) * D, nullptr, 0.0f, n, x, E, 1, 0));
     else
       ck(mk_matmul(ctx_, &wo, xq, n, x, E, 1));  // x += attn_output(att) (model.cpp:398-401)

@@ -84,8 +84,12 @@ class Model {
   // wide: the reference's wide Q6_K prefill panels are packed (Engine packs them when RAM allows,
   // engine.cpp:130-145); MALKIN_NO_WIDE turns them off there.
   // no_pack: every matmul on the reference's row path over GGUF rows (its MALKIN_NO_PACK, model.cpp:136).
+  // decode: how one-token forwards run their layers where the shape allows (kDecodeSteps: one launch per step;
+  // kDecodePersistent: every layer in one launch, mk_decode_layers; kDecodeFusedAttn: each layer's attention and
+  // attn_output in one launch, mk_decode_attn_wo). The results are the same.
+  enum { kDecodeSteps = 0, kDecodePersistent = 1, kDecodeFusedAttn = 2 };
   Model(mk_ctx* ctx, const GgufFile& f, int n_ctx, int n_seq = 1, bool wide = true, bool no_pack = false,
-        bool persistent = false);
+        int decode = kDecodeSteps);
   ~Model();
   const ModelConfig& cfg() const { return cfg_; }
   int n_ctx() const { return n_ctx_; }
@@ -129,7 +133,8 @@ class Model {
   size_t weight_bytes() const { return weight_bytes_; }
   // Whether one-token forwards run the persistent decode kernel (mk_decode_layers); after a host wait on the model's
   // stream, check_device() raises if one of its launches since the last check timed out in a hand-off wait.
-  bool persistent() const { return dplan_ != nullptr; }
+  bool persistent() const { return dplan_ != nullptr && decode_ == kDecodePersistent; }
+  bool fused_attn() const { return dplan_ != nullptr && decode_ == kDecodeFusedAttn; }
   void check_device();
   // Packed matmul weight: which = 0 qkv, 1 wo, 2 gate|up, 3 down of `layer`; 4 the LM head.
   mk_weight weight(int layer, int which) const;
@@ -233,6 +238,7 @@ class Model {
   DevBuf x_, qkv_, att_, gu_, xq_, logits_, top_;
   mk_decode_plan* dplan_ = nullptr;  // the persistent decode kernel's plan (all layers Q8_0, fused groups)
   bool dplan_pending_ = false;       // launched since the last check_device()
+  int decode_ = kDecodeSteps;
   DevBuf h_;  // fp32 normalized rows of the row-path layers (kDevBatch x n_embd)
 };
 

@@ -609,6 +609,13 @@ int mk_decode_layers(mk_ctx* c, mk_decode_plan* p, int l0, int l1, int max_keys)
   });
 }
 
+int mk_decode_attn_wo(mk_ctx* c, mk_decode_plan* p, int layer, int max_keys) {
+  return guard([&] {
+    require(c && p && layer >= 0 && layer < p->n_layer, "mk_decode_attn_wo: bad layer");
+    mk::decode_attn_wo(c->stream, p->args, p->d, layer, p->n_layer, max_keys);
+  });
+}
+
 int mk_decode_check(mk_ctx* c, mk_decode_plan* p) {
   return guard([&] {
     require(c && p, "mk_decode_check: no plan");

@@ -609,6 +609,50 @@ __global__ __launch_bounds__(kDT) void k_decode_layers(const DecodeArgs* __restr
   }
 }
 
+// One layer's attention and attn_output GEMV in one launch, between the per-step q|k|v and gate|up launches: the H
+// attention workgroups run attention (their q|k|v input is complete: the previous launch has ended), while the others
+// already copy their attn_output chunks into their rings; the GEMV step then waits for the attention step through the
+// counters of the layer's steps 1 and 2 (the same counters, exit count and error word as k_decode_layers with all
+// n_layer layers). Results as the attention and attn_output launches it replaces.
+template <int D, int NSLOT, int RING>
+__global__ __launch_bounds__(kDT) void k_decode_attn_wo(const DecodeArgs* __restrict__ P, int il, int n_layer) {
+  const int w = blockIdx.x, tid = threadIdx.x;
+  const int G = (int)gridDim.x;
+  const int n_steps = n_layer * kSteps, s0 = il * kSteps;
+  const int E = opaque(P)->E, H = opaque(P)->H, KV = opaque(P)->KV, F = opaque(P)->F;
+  const int HD = H * D, max_cols = max(max(E, HD), F);
+  const DecodeLayer* L = glob(opaque(P)->layers) + il;
+  if (w < H) {
+    const auto* Q = opaque(P);
+    const size_t lrow = (size_t)il * Q->n_seq * KV * Q->n_ctx;
+    const KvLayer kv{glob(Q->k8) + lrow * D, glob(Q->v8) + lrow * D, glob(Q->ks) + lrow, glob(Q->vs) + lrow};
+    const int64_t rows = Q->n_ctx;
+    const AttnAddr a{kv.k,  kv.v, reinterpret_cast<const char*>(kv.ks), reinterpret_cast<const char*>(kv.vs),
+                     (int64_t)KV * rows * D, rows * D, D, (int64_t)KV * rows * 4, rows * 4, 4, 1};
+    const DecFuse f{glob(Q->qkv), 0, glob(opaque(L)->q_norm), glob(opaque(L)->k_norm), Q->eps, glob(Q->cos_t),
+                    glob(Q->sin_t), glob(Q->rpos), glob(Q->kv_row), kv, Q->n_ctx, KV};
+    attend_dec<D, NSLOT, true, true, kDT>(w, nullptr, 0, nullptr, 0, H / KV, Q->scale, a, glob(Q->seq),
+                                          glob(Q->n_keys), 1, H, f, glob(Q->att), 0, [] {});
+    __builtin_amdgcn_s_waitcnt(0);
+  }
+  signal_step(P, s0 + 1);
+  // x += W_o . att (no next step: the gate|up launch follows)
+  const Gs wo = make_gs(glob(opaque(L)->wo), E, HD, 0, G);
+  gemv_step<kInQ8, kOutAcc, RING>(P, n_steps, s0 + 2, wo, wo, false, Ring{0, 0}, glob(opaque(P)->att), nullptr, HD,
+                                  max_cols, E, glob(opaque(P)->x));
+  __builtin_amdgcn_s_waitcnt(0);
+  if ((tid >> 6) == 0) {
+    unsigned old = 0;
+    if (tid == 0) old = __hip_atomic_fetch_add(exit_ctr(P, n_steps), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __shfl(old, 0);
+    if (old == (unsigned)G - 1) {
+      unsigned* sync = glob(opaque(P)->sync);
+      for (int i = tid; i < 2 * 8; i += 64) st_coh_u32(sync + ((size_t)(s0 + 1) * 8 + i) * kCtr, 0u);
+      if (tid == 0) st_coh_u32(exit_ctr(P, n_steps), 0u);
+    }
+  }
+}
+
 }  // namespace
 
 size_t decode_sync_bytes(int n_layer) { return ((size_t)n_layer * kSteps * 8 + 2) * kCtr * sizeof(unsigned); }
@@ -659,6 +703,45 @@ void decode_set_args(void* dev, const DecodeDims& d, const DecodeBufs& b) {
   A.sync = b.sync;
   A.spin_max = b.spin_max;
   check(hipMemcpy(dev, &A, sizeof A, hipMemcpyHostToDevice), "hipMemcpy");
+}
+
+namespace {
+// Launches a kernel of this file (all layers, or one layer's attention + attn_output) with the plan's LDS and the
+// whole grid resident; select(slots, ring) returns the instantiation.
+template <typename Sel, typename... Args>
+void decode_launch(hipStream_t s, const DecodeDims& d, int max_keys, const char* what, Sel&& select, Args... args) {
+  const int max_cols = std::max(std::max(d.E, d.H * d.D), d.F);
+  const int ring = decode_ring(d, max_keys);
+  const size_t lds = std::max(gemv_lds_bytes(max_cols, d.E, ring), dec_lds_bytes(d.D, attn_keys_pad(max_keys)));
+  const int cus = device_cus();
+  const auto kernel = select(dec_slots(d.D, max_keys, true, kDT), ring);
+  check(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            160 * 1024 - kStaticLds),
+        "hipFuncSetAttribute");
+  hipFuncAttributes fa{};
+  check(hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(kernel)), "hipFuncGetAttributes");
+  require(fa.sharedSizeBytes <= (size_t)kStaticLds, "decode: static LDS above its bound");
+  int per_cu = 0;
+  check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kDT, lds),
+        "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+  // Every workgroup waits for the others: the whole grid (one workgroup per CU) must be resident at once.
+  require(per_cu >= 1, "decode: the kernel does not fit on a CU");
+  hipLaunchKernelGGL(kernel, dim3(cus), dim3(kDT), lds, s, args...);
+  check_launch(what);
+}
+}  // namespace
+
+void decode_attn_wo(hipStream_t s, const void* dev_args, const DecodeDims& d, int layer, int n_layer, int max_keys) {
+  require(decode_layers_supported(d, max_keys), "decode_attn_wo: unsupported shape");
+  require(layer >= 0 && layer < n_layer, "decode_attn_wo: bad layer");
+  using K = void (*)(const DecodeArgs*, int, int);
+  auto select = [](int slots, int ring) -> K {
+    if (slots <= 2) return ring == 4 ? k_decode_attn_wo<128, 2, 4> : k_decode_attn_wo<128, 2, 3>;
+    if (slots <= 4) return ring == 4 ? k_decode_attn_wo<128, 4, 4> : k_decode_attn_wo<128, 4, 3>;
+    if (slots <= 6) return ring == 4 ? k_decode_attn_wo<128, 6, 4> : k_decode_attn_wo<128, 6, 3>;
+    return ring == 4 ? k_decode_attn_wo<128, kMaxSlots, 4> : k_decode_attn_wo<128, kMaxSlots, 3>;
+  };
+  decode_launch(s, d, max_keys, "decode_attn_wo", select, static_cast<const DecodeArgs*>(dev_args), layer, n_layer);
 }
 
 void decode_layers(hipStream_t s, const void* dev_args, const DecodeDims& d, int l0, int l1, int max_keys) {

@@ -193,6 +193,8 @@ size_t decode_error_word(int n_layer);
 size_t decode_args_bytes();
 void decode_set_args(void* dev_args, const DecodeDims& d, const DecodeBufs& b);
 void decode_layers(hipStream_t s, const void* dev_args, const DecodeDims& d, int l0, int l1, int max_keys);
+// Layer `layer`'s attention and attn_output GEMV in one launch (the q|k|v output in place; sync sized for n_layer).
+void decode_attn_wo(hipStream_t s, const void* dev_args, const DecodeDims& d, int layer, int n_layer, int max_keys);
 
 // QK-norm + RoPE on q [n][H*D] and k [n][KV*D] (in place), then k, v quantized into the KV cache (model.cpp:370-392).
 // cos/sin tables [n_pos][D/2].

@@ -1,5 +1,6 @@
-"""The persistent decode kernel (mk_decode_layers: every layer of a one-token forward in one launch) against the
-per-step launches it replaces, on synthetic Q8_0 models at the real widths of Qwen3-4B, -8B and -14B (few layers).
+"""The persistent decode kernel (mk_decode_layers: every layer of a one-token forward in one launch) and the fused
+attention + attn_output launch (mk_decode_attn_wo) against the per-step launches they replace, on synthetic Q8_0
+models at the real widths of Qwen3-4B, -8B and -14B (few layers).
 The per-step path is pinned to the reference elsewhere (test_gpu_model.py, test_gpu_scale.py); here every logit and
 every KV cache byte of the persistent path must equal it bit for bit, over short, medium and long rows (the kernel's
 attention takes 2, 4 or 8 staging slots), eager forwards and replayed graphs."""
@@ -27,7 +28,8 @@ def bits(a):
 
 @pytest.fixture(scope="module")
 def pairs(mk, synth_lib, tmp_path_factory):
-    """Each shape loaded twice: with the persistent kernel (MK_MODEL_PERSISTENT), and without."""
+    """Each shape loaded three times: with the persistent kernel (MK_MODEL_PERSISTENT), with per-step launches, and
+    with the fused attention + attn_output launch (MK_MODEL_FUSED_ATTN)."""
     d = tmp_path_factory.mktemp("decode")
     out = {}
     for i, (name, (preset, over)) in enumerate(SHAPES.items()):
@@ -35,18 +37,20 @@ def pairs(mk, synth_lib, tmp_path_factory):
         path = synth_lib.write_gguf(str(d / f"{name}.gguf"), cfg)
         a = mk_.Model(mk, path, N_CTX, 1, persistent=True)
         b = mk_.Model(mk, path, N_CTX, 1, persistent=False)
-        print("model", name, a.cfg, "persistent", a.persistent, flush=True)
-        out[name] = (a, b)
+        c = mk_.Model(mk, path, N_CTX, 1, fused_attn=True)
+        print("model", name, a.cfg, "persistent", a.persistent, "fused", c.fused_attn, flush=True)
+        out[name] = (a, b, c)
     yield out
-    for a, b in out.values():
-        a.close()
-        b.close()
+    for ms in out.values():
+        for m in ms:
+            m.close()
 
 
 def test_plan_only_where_supported(pairs):
-    for name, (a, b) in pairs.items():
+    for name, (a, b, c) in pairs.items():
         assert a.persistent == (name != "q06b"), name
-        assert not b.persistent
+        assert not b.persistent and not b.fused_attn
+        assert c.fused_attn == (name != "q06b") and not c.persistent, name
 
 
 def prompt_ids(n, vocab, seed):
@@ -56,23 +60,26 @@ def prompt_ids(n, vocab, seed):
 @pytest.mark.parametrize("name", ["q4b", "q8b", "q14b", "q06b"])
 def test_eager_steps_match(pairs, name):
     """Prompt, then 10 one-token forwards fed with their argmax: logits and the KV rows written equal."""
-    a, b = pairs[name]
+    a, b, c = pairs[name]
     v = a.cfg["n_vocab"]
     p = prompt_ids(200, v, 7)
-    la, lb = a.forward(p, 0), b.forward(p, 0)
-    assert np.array_equal(bits(la), bits(lb))
+    la, lb, lc = a.forward(p, 0), b.forward(p, 0), c.forward(p, 0)
+    assert np.array_equal(bits(la), bits(lb)) and np.array_equal(bits(lc), bits(lb))
     tok = int(np.argmax(la[0]))
     for step in range(10):
         pos = len(p) + step
         la = a.forward(np.array([tok], np.int32), pos)
         lb = b.forward(np.array([tok], np.int32), pos)
+        lc = c.forward(np.array([tok], np.int32), pos)
         print(name, "step", step, flush=True)
         assert np.array_equal(bits(la), bits(lb)), step
+        assert np.array_equal(bits(lc), bits(lb)), ("fused", step)
         tok = int(np.argmax(la[0]))
     for layer in range(a.cfg["n_layer"]):
         for pos in range(len(p), len(p) + 10):
             for k in (True, False):
                 assert np.array_equal(a.kv_row(layer, 0, pos, k), b.kv_row(layer, 0, pos, k)), (layer, pos, k)
+                assert np.array_equal(c.kv_row(layer, 0, pos, k), b.kv_row(layer, 0, pos, k)), ("fused", layer, pos)
 
 
 @pytest.mark.parametrize("n_prompt", [9, 600, 1100])
@@ -80,12 +87,13 @@ def test_eager_steps_match(pairs, name):
 def test_generate_matches(pairs, n_prompt, use_graph):
     """Greedy generation (device argmax feeding the next step): identical streams with the key count spanning the
     kernel's short, medium and long attention forms."""
-    a, b = pairs["q4b"]
+    a, b, c = pairs["q4b"]
     p = prompt_ids(n_prompt, a.cfg["n_vocab"], n_prompt)
     print("generate", n_prompt, use_graph, flush=True)
     ta, sa = a.generate(p, 40, use_graph=use_graph)
     tb, sb = b.generate(p, 40, use_graph=use_graph)
-    assert list(ta) == list(tb)
+    tc, sc = c.generate(p, 40, use_graph=use_graph)
+    assert list(ta) == list(tb) and list(tc) == list(tb)
     assert sa["decode_forwards"] == 39
     for layer in (0, a.cfg["n_layer"] - 1):
         for pos in (n_prompt, n_prompt + 38):
@@ -95,8 +103,9 @@ def test_generate_matches(pairs, n_prompt, use_graph):
 
 @pytest.mark.parametrize("name", ["q8b", "q14b"])
 def test_generate_matches_wide(pairs, name):
-    a, b = pairs[name]
+    a, b, c = pairs[name]
     p = prompt_ids(300, a.cfg["n_vocab"], 11)
     ta, _ = a.generate(p, 32)
     tb, _ = b.generate(p, 32)
-    assert list(ta) == list(tb)
+    tc, _ = c.generate(p, 32)
+    assert list(ta) == list(tb) and list(tc) == list(tb)
