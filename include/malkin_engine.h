@@ -54,6 +54,11 @@ int mk_engine_step(mk_engine* e, int32_t* busy);
 int mk_engine_run(mk_engine* e);
 /* Steps (target forwards) run so far; with mk_host_waits() it bounds the host waits per step (one). */
 int mk_engine_steps(mk_engine* e, uint64_t* steps);
+/* Sampled requests' drafts drawn on the device so far (mk_sample_draw, no host wait per draft forward), and how many
+   of them the host's replay of the same draw (the draft sampler's distribution over the same candidates, its own
+   generator) picked differently: 0 unless a device weight differed from the C library's expf in its last bit. No
+   reference counterpart (the reference draws every draft on the host, engine.cpp:319-323). */
+int mk_engine_draws(mk_engine* e, uint64_t* device_draws, uint64_t* mismatches);
 /* Generated ids of a request (up to cap) and its counters. */
 int mk_engine_result(mk_engine* e, int32_t request_id, int32_t* tokens, int32_t cap, mk_request_info* info);
 /* Frees a finished request's result (the reference hands each result to its caller and keeps none, engine.cpp:

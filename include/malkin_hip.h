@@ -312,6 +312,30 @@ int mk_sample_cut(mk_ctx* ctx, const float* logits, int64_t stride, const int32_
 int mk_sample_cut_tail(mk_ctx* ctx, void* workspace, int n_rows, int n_vocab, int row, int from, int count,
                        float* values, int32_t* ids);
 
+/* A std::mt19937_64 generator on the device: its 312 state words, then the index of the next word to temper
+   (312 right after seeding: the next output regenerates the state first). */
+#define MK_MT64_WORDS 313
+/* Per-row parameters of mk_sample_draw. */
+typedef struct {
+  int32_t k;                        /* candidates of the row (1 .. stride), highest first */
+  float temperature, min_p, top_p;  /* temperature > 0 */
+  int32_t state;                    /* the row's generator: states + MK_MT64_WORDS * state, 0 .. n_states - 1 */
+  int32_t dst;                      /* out[dst] receives the drawn id, 0 .. n_out - 1 */
+} mk_draw_params;
+/* Sampler::sample over rows already cut to their top k (mk_topk's values / ids [n_rows][stride], stride 1..1024),
+   sampler.cpp:27-56 and 108-116, as the draft's proposals draw it (engine.cpp:319-323): per row the weights
+   exp((l - l_max) / T) as floats, the total in double in order, the kept head (min_p floor, top_p nucleus), the
+   probabilities weight / (kept total) rounded to float, and, when more than one candidate is kept, one
+   u = uniform(generator) and the first candidate where the running u - p_i reaches zero (the last if none does).
+   The row's generator is advanced in place; a one-candidate head draws nothing. Rows run in parallel: two rows of
+   one call must not share a generator. The weights are the correctly rounded float of exp, which the C library's
+   expf can differ from in the last bit (within ~2^-60 of a rounding boundary): the caller replays the draw on the
+   host to know the distribution and can compare. All arrays are device arrays; a row whose state or dst is out of
+   range is skipped. No reference counterpart as one call: the reference draws on the host after each draft
+   forward. */
+int mk_sample_draw(mk_ctx* ctx, const float* values, const int32_t* ids, int stride, int n_rows,
+                   const mk_draw_params* params, uint64_t* states, int n_states, int32_t* out, int n_out);
+
 /* dst[dst_index[i]] = src[src_index[i]] for i < n, in stream order (a NULL index array is the identity; a negative
    index skips i). Moves token ids between device arrays without a host round trip: draft picks into a proposal tree,
    tree ids into a forward's token slots (no reference counterpart: the CPU engine keeps ids in host vectors). */

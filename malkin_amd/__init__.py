@@ -107,6 +107,7 @@ SIGNATURES = {
     "mk_engine_step": (_I, [_P, _P]),
     "mk_engine_run": (_I, [_P]),
     "mk_engine_steps": (_I, [_P, ctypes.POINTER(ctypes.c_uint64)]),
+    "mk_engine_draws": (_I, [_P, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
     "mk_engine_result": (_I, [_P, _I, _P, _I, _P]),
     "mk_engine_release": (_I, [_P, _I, ctypes.POINTER(ctypes.c_int64)]),
     "mk_engine_submit_sampled": (_I, [_P, _P, _I, _I, _P, _I, _P, _P]),
@@ -115,6 +116,7 @@ SIGNATURES = {
     "mk_sample_cut_workspace": (ctypes.c_size_t, [_I, _I]),
     "mk_sample_cut": (_I, [_P, _P, _I64, _P, _I, _I, _P, _I, _P, _P, _P, _P, _P, ctypes.c_size_t]),
     "mk_sample_cut_tail": (_I, [_P, _P, _I, _I, _I, _I, _I, _P, _P]),
+    "mk_sample_draw": (_I, [_P, _P, _P, _I, _I, _P, _P, _I, _P, _I]),
     "mk_server_start": (_I, [_P, ctypes.c_char_p, ctypes.c_char_p, _I, ctypes.POINTER(_P), ctypes.POINTER(_I)]),
     "mk_server_stop": (_I, [_P]),
     "mk_sampler_create": (_I, [_P, _I, ctypes.POINTER(_P)]),
@@ -431,6 +433,13 @@ class Engine:
         n = ctypes.c_uint64()
         check(load().mk_engine_steps(self.h, ctypes.byref(n)))
         return n.value
+
+    @property
+    def draws(self):
+        """(drafts drawn on the device, of which the host's replay drew differently)."""
+        a, b = ctypes.c_uint64(), ctypes.c_uint64()
+        check(load().mk_engine_draws(self.h, ctypes.byref(a), ctypes.byref(b)))
+        return a.value, b.value
 
     def result(self, rid):
         info = MkRequestInfo()

@@ -278,6 +278,14 @@ int mk_engine_steps(mk_engine* e, uint64_t* steps) {
   });
 }
 
+int mk_engine_draws(mk_engine* e, uint64_t* device_draws, uint64_t* mismatches) {
+  return run([&] {
+    if (!e || !device_draws || !mismatches) throw std::invalid_argument("mk_engine_draws: null argument");
+    *device_draws = e->engine->device_draws();
+    *mismatches = e->engine->draw_mismatches();
+  });
+}
+
 int mk_engine_result(mk_engine* e, int32_t request_id, int32_t* tokens, int32_t cap, mk_request_info* info) {
   return run([&] {
     if (!e) throw std::invalid_argument("mk_engine_result: null engine");

@@ -30,7 +30,15 @@ struct DraftPass {
   int depth = -1;                            // round passes: the depth whose chain tokens are fed
   std::vector<std::pair<int, int>> fed;      // (batch index, spec) of sampled lanes' chain tokens, set at launch
   std::vector<std::pair<int, int>> drawn;    // (logits row, spec) whose row the host draws the next draft from
+  std::vector<std::pair<int, int>> dev_drawn;  // (logits row, spec) whose row the device draws the next draft from
 };
+
+// Upload block of the device draws: generators [lanes][MK_MT64_WORDS], then params [rows], then logits rows [rows].
+static_assert(Mt64::kWords == MK_MT64_WORDS, "the host generator's layout is mk_sample_draw's");
+
+size_t draw_block_bytes(size_t lanes, size_t rows) {
+  return lanes * MK_MT64_WORDS * sizeof(uint64_t) + rows * (sizeof(mk_draw_params) + sizeof(int32_t));
+}
 
 }  // namespace
 
@@ -68,12 +76,27 @@ Engine::Engine(Model* target, Model* draft, int n_draft)
   ck(mk_host_alloc(c, (slots + Model::kMaxBatch) * sizeof(int32_t), &h));
   tree_h_ = static_cast<int32_t*>(h);
   picks_h_ = tree_h_ + slots;
+  if (draft_) {  // at most one draw per lane and depth in a step
+    const size_t rows = S * static_cast<size_t>(max_depth_), cand = rows * Selector::kMaxDeviceK;
+    draw_in_d_ = DevBuf(c, draw_block_bytes(S, rows));
+    ck(mk_host_alloc(c, draw_block_bytes(S, rows), &h));
+    draw_in_h_ = static_cast<uint8_t*>(h);
+    cand_v_d_ = DevBuf(c, cand * sizeof(float));
+    cand_i_d_ = DevBuf(c, cand * sizeof(int32_t));
+    ck(mk_host_alloc(c, cand * sizeof(float), &h));
+    cand_v_h_ = static_cast<float*>(h);
+    ck(mk_host_alloc(c, cand * sizeof(int32_t), &h));
+    cand_i_h_ = static_cast<int32_t*>(h);
+  }
 }
 
 Engine::~Engine() {
   mk_ctx* c = target_->ctx();
   (void)mk_host_free(c, plan_h_);
   (void)mk_host_free(c, tree_h_);
+  (void)mk_host_free(c, draw_in_h_);
+  (void)mk_host_free(c, cand_v_h_);
+  (void)mk_host_free(c, cand_i_h_);
 }
 
 int Engine::submit(const EngineRequest& req) {
@@ -186,14 +209,21 @@ void Engine::plan_specs() {
     const int room = target_->n_ctx() - static_cast<int>(lane.kv.size()) - 2;
     const int per_depth = sp.sampled ? 1 : 2;  // a greedy tree holds chain and alt tokens
     sp.depth = std::max(0, std::min({job.k, left, room / per_depth, share / per_depth}));
+    // The device draws a sampled lane's drafts when its draft sampler's candidates fit mk_topk and the target rows'
+    // penalties do not depend on the drafts (the target's candidates are then selected before the step's wait).
+    sp.on_device = sp.sampled && sp.depth > 0 && !job.sampler->penalizes() &&
+                   job.draft_sampler->candidates(target_->cfg().n_vocab) <= Selector::kMaxDeviceK;
   }
 }
 
 // The draft's part of a step: catch-up forwards that bring each drafting lane's draft KV to its target tokens plus
 // the pending token (prefix rows reused), then one forward per depth that feeds every lane's chain token of that
 // depth. Greedy lanes: each forward's picks go to the next depth's tree slots on the device, nothing waits.
-// Sampled lanes: after a forward that produced a row they draw from, the host waits, draws, and feeds the draw to
-// the next forward.
+// Sampled lanes whose draft candidates fit mk_topk (and whose target rows take no penalties): the device cuts each
+// row they draw from to its top-k and draws from it with the draft sampler's generator (uploaded once per step) into
+// the next depth's chain slot; nothing waits, and the host replays the draws after the step's wait. Other sampled
+// lanes: after a forward that produced a row they draw from, the host waits, draws, and feeds the draw to the next
+// forward.
 void Engine::draft_trees() {
   std::vector<DraftPass> passes(1);
   std::vector<int> fed_from(lanes_.size(), -1);  // draft_kv index of each lane's first chain token fed
@@ -218,7 +248,10 @@ void Engine::draft_trees() {
       p.batch.push_back(BatchToken{id, sp.lane, static_cast<int>(pos), last});
       p.id_from.push_back(-1);
       if (last) {
-        if (sp.sampled) p.drawn.emplace_back(static_cast<int>(p.chain_dst.size()), static_cast<int>(si));
+        if (sp.on_device)
+          p.dev_drawn.emplace_back(static_cast<int>(p.chain_dst.size()), static_cast<int>(si));
+        else if (sp.sampled)
+          p.drawn.emplace_back(static_cast<int>(p.chain_dst.size()), static_cast<int>(si));
         p.chain_dst.push_back(sp.sampled ? -1 : tree_slot(sp.lane, 0, false));
         p.alt_dst.push_back(sp.sampled ? -1 : tree_slot(sp.lane, 0, true));
       }
@@ -235,7 +268,12 @@ void Engine::draft_trees() {
       if (d == 0) fed_from[static_cast<size_t>(sp.lane)] = static_cast<int>(lane.draft_kv.size());
       const int row = static_cast<int>(p.batch.size());
       p.batch.push_back(BatchToken{0, sp.lane, static_cast<int>(lane.draft_kv.size()), true});
-      if (sp.sampled) {
+      if (sp.on_device) {  // the chain token from its tree slot, the next one drawn into the next slot
+        p.id_from.push_back(tree_slot(sp.lane, d, false));
+        p.dev_drawn.emplace_back(row, static_cast<int>(si));
+        p.chain_dst.push_back(-1);
+        p.alt_dst.push_back(-1);
+      } else if (sp.sampled) {
         p.id_from.push_back(-1);
         p.fed.emplace_back(row, static_cast<int>(si));
         p.drawn.emplace_back(row, static_cast<int>(si));
@@ -266,6 +304,39 @@ void Engine::draft_trees() {
   ck(mk_copy_async(c, plan_.p, plan_h_, off * sizeof(int32_t)));
   int32_t* tree = tree_.as<int32_t>();
   const int n_vocab = target_->cfg().n_vocab;
+  // Device draws: each drawing lane's generator, then per drawn row (in pass order) its parameters and logits row.
+  const size_t S = lanes_.size(), max_rows = S * static_cast<size_t>(max_depth_);
+  auto* states_h = reinterpret_cast<uint64_t*>(draw_in_h_);
+  auto* params_h = reinterpret_cast<mk_draw_params*>(states_h + S * MK_MT64_WORDS);
+  auto* rows_h = reinterpret_cast<int32_t*>(params_h + max_rows);
+  size_t n_draws = 0;
+  draw_k_ = 0;
+  for (Spec& sp : specs_) {
+    sp.draws.clear();
+    if (!sp.on_device) continue;
+    const Sampler& ds = *lanes_[static_cast<size_t>(sp.lane)].job->draft_sampler;
+    std::copy(ds.generator().w, ds.generator().w + MK_MT64_WORDS, states_h + static_cast<size_t>(sp.lane) * MK_MT64_WORDS);
+    draw_k_ = std::max(draw_k_, ds.candidates(n_vocab));
+  }
+  std::vector<size_t> first_draw(passes.size());
+  for (size_t i = 0; i < passes.size(); ++i) {
+    first_draw[i] = n_draws;
+    for (const auto& [row, si] : passes[i].dev_drawn) {
+      Spec& sp = specs_[static_cast<size_t>(si)];
+      const SamplingParams& sq = lanes_[static_cast<size_t>(sp.lane)].job->draft_sampler->params();
+      if (n_draws >= max_rows) throw std::runtime_error("engine: device draws exceed their buffer");
+      params_h[n_draws] = mk_draw_params{lanes_[static_cast<size_t>(sp.lane)].job->draft_sampler->candidates(n_vocab),
+                                         sq.temperature, sq.min_p, sq.top_p, sp.lane,
+                                         tree_slot(sp.lane, static_cast<int>(sp.draws.size()), false)};
+      rows_h[n_draws] = row;
+      sp.draws.push_back(static_cast<int>(n_draws));
+      ++n_draws;
+    }
+  }
+  const auto* states_d = draw_in_d_.as<uint64_t>();
+  const auto* params_d = reinterpret_cast<const mk_draw_params*>(states_d + S * MK_MT64_WORDS);
+  const auto* rows_d = reinterpret_cast<const int32_t*>(params_d + max_rows);
+  if (n_draws > 0) ck(mk_copy_async(c, draw_in_d_.p, draw_in_h_, draw_block_bytes(S, max_rows)));
   for (size_t i = 0; i < passes.size(); ++i) {
     DraftPass& p = passes[i];
     if (p.batch.empty()) continue;
@@ -276,6 +347,15 @@ void Engine::draft_trees() {
     int32_t* dst = plan_.as<int32_t>() + at[i];
     ck(mk_move_ids(c, tree, dst, draft_top1_.as<int32_t>(), nullptr, m));
     ck(mk_move_ids(c, tree, dst + m, draft_top2_.as<int32_t>(), nullptr, m));
+    if (!p.dev_drawn.empty()) {  // top-k of the drawing rows, then each row's draw into its lane's next tree slot
+      const size_t j = first_draw[i];
+      const int nr = static_cast<int>(p.dev_drawn.size());
+      float* cv = cand_v_d_.as<float>() + j * static_cast<size_t>(draw_k_);
+      int32_t* ci = cand_i_d_.as<int32_t>() + j * static_cast<size_t>(draw_k_);
+      ck(mk_topk(c, draft_->dev_logits(), n_vocab, rows_d + j, nr, n_vocab, draw_k_, cv, ci));
+      ck(mk_sample_draw(c, cv, ci, draw_k_, nr, params_d + j, const_cast<uint64_t*>(states_d), static_cast<int>(S),
+                        tree, static_cast<int>(tree_.bytes / sizeof(int32_t))));
+    }
     if (p.drawn.empty()) continue;
     // Sampled lanes: the draft sampler's distribution of each row, one wait, then the draws (engine.cpp:319-323).
     draft_sel_.clear();
@@ -296,10 +376,16 @@ void Engine::draft_trees() {
       sp.chain.push_back(ds.draw(sp.q.back()));
     }
   }
-  // Remember where each lane's chain tokens sit in draft_kv (greedy ones filled in after the step's wait).
+  if (n_draws > 0) {  // the candidates of every device draw, for the host's replay after the step's wait
+    const size_t n = n_draws * static_cast<size_t>(draw_k_);
+    ck(mk_copy_async(c, cand_v_h_, cand_v_d_.p, n * sizeof(float)));
+    ck(mk_copy_async(c, cand_i_h_, cand_i_d_.p, n * sizeof(int32_t)));
+  }
+  // Remember where each lane's chain tokens sit in draft_kv (greedy ones and device draws filled in after the step's
+  // wait).
   for (Spec& sp : specs_) {
     sp.root = fed_from[static_cast<size_t>(sp.lane)];
-    if (!sp.sampled || sp.root < 0) continue;
+    if (!sp.sampled || sp.on_device || sp.root < 0) continue;
     Lane& lane = lanes_[static_cast<size_t>(sp.lane)];
     for (int d = 0; d + 1 < sp.depth; ++d) lane.draft_kv[static_cast<size_t>(sp.root + d)] = sp.chain[static_cast<size_t>(d)];
   }
@@ -317,6 +403,11 @@ int Engine::build_target_batch() {
     batch_.push_back(BatchToken{lane.job->pending, sp.lane, P, true});
     id_from_.push_back(-1);
     for (int d = 0; d < sp.depth; ++d) {
+      if (sp.on_device) {  // a chain in a row, its ids in the tree slots the device drew them into
+        batch_.push_back(BatchToken{0, sp.lane, P + 1 + d, true});
+        id_from_.push_back(tree_slot(sp.lane, d, false));
+        continue;
+      }
       if (sp.sampled) {  // a chain in a row: ordinary causal tokens
         batch_.push_back(BatchToken{sp.chain[static_cast<size_t>(d)], sp.lane, P + 1 + d, true});
         id_from_.push_back(-1);
@@ -436,10 +527,11 @@ void Engine::step() {
   ++steps_;
   sel_.collect();
 
-  if (drafting)  // the greedy chain ids fed to the draft, now known on the host
+  if (drafting) replay_draws();
+  if (drafting)  // the greedy chain ids and device-drawn drafts fed to the draft, now known on the host
     for (size_t i = 0; i < specs_.size(); ++i) {
       const Spec& sp = specs_[i];
-      if (chain_at[i] < 0 || sp.sampled) continue;
+      if (chain_at[i] < 0 || (sp.sampled && !sp.on_device)) continue;
       Lane& lane = lanes_[static_cast<size_t>(sp.lane)];
       for (int d = 0; d + 1 < sp.depth; ++d)
         lane.draft_kv[static_cast<size_t>(chain_at[i] + d)] = tree_host(sp.lane)[2 * d];
@@ -466,6 +558,31 @@ void Engine::step() {
       settle_sampled(sp);
     else
       settle(sp);
+  }
+}
+
+// Sampled lanes whose drafts the device drew: the draft sampler's distribution of each draw's candidates and its draw
+// with the host's generator, in depth order (the reference's draws, engine.cpp:319-323), leaving the host generator
+// where the reference's is. The drafts are the device's picks, which the target has verified already; a replay that
+// picks differently (a device weight one ulp off the C library's expf) is counted, and the next step's draws start
+// again from the host generator.
+void Engine::replay_draws() {
+  const int n_vocab = target_->cfg().n_vocab;
+  for (Spec& sp : specs_) {
+    if (!sp.on_device) continue;
+    Sampler& ds = *lanes_[static_cast<size_t>(sp.lane)].job->draft_sampler;
+    const int k = ds.candidates(n_vocab);
+    if (static_cast<int>(sp.draws.size()) != sp.depth) throw std::logic_error("engine: device draws missing");
+    for (int d = 0; d < sp.depth; ++d) {
+      const size_t j = static_cast<size_t>(sp.draws[static_cast<size_t>(d)]) * static_cast<size_t>(draw_k_);
+      sp.q.emplace_back();
+      ds.finish(cand_v_h_ + j, cand_i_h_ + j, k, sp.q.back());
+      const int32_t host = ds.draw(sp.q.back());
+      const int32_t dev = tree_host(sp.lane)[2 * d];
+      ++device_draws_;
+      if (host != dev) ++draw_mismatches_;
+      sp.chain.push_back(dev);
+    }
   }
 }
 

@@ -91,6 +91,9 @@ class Engine {
   // The target model's end-of-generation ids (the set the reference's Tokenizer::is_eog tests, engine.cpp:60).
   const std::vector<int32_t>& model_eog() const { return target_->cfg().eog; }
   uint64_t steps() const { return steps_; }
+  // Drafts drawn on the device so far, and how many of them the host's replay drew differently.
+  uint64_t device_draws() const { return device_draws_; }
+  uint64_t draw_mismatches() const { return draw_mismatches_; }
 
  private:
   using Clock = std::chrono::steady_clock;
@@ -113,8 +116,10 @@ class Engine {
   struct Spec {  // a decoding lane's share of one step
     int lane = 0, depth = 0, root = 0;  // root: batch index of the lane's pending token
     bool sampled = false;
+    bool on_device = false;             // sampled, and its drafts drawn on the device (mk_sample_draw)
     std::vector<int32_t> chain;         // sampled lanes: the drawn drafts
     std::vector<Distribution> q;        // ... and the draft distributions they were drawn from
+    std::vector<int> draws;             // on_device: the step's candidate row of each depth's draw
     const Selector* cand = nullptr;     // non-plain lanes: candidates of the target rows root.. (index sel..)
     int sel = -1;
   };
@@ -132,6 +137,7 @@ class Engine {
   Distribution& target_dist(const Spec& sp, int row);
   void settle(const Spec& sp);
   void settle_sampled(const Spec& sp);
+  void replay_draws();
   bool emit(Job& job, int32_t id, size_t cached);
   void finish(Lane& lane);
   int32_t* tree_host(int lane) { return tree_h_ + static_cast<size_t>(lane) * 2 * max_depth_; }
@@ -168,6 +174,16 @@ class Engine {
   int32_t* tree_h_ = nullptr;  // pinned: trees and target picks read back at the end of a step
   int32_t* picks_h_ = nullptr;
   std::vector<std::pair<size_t, int>> pending_scatters_;  // (plan offset, rows) of each queued draft forward
+
+  // Device draws of sampled lanes' drafts: one upload per step of the draft samplers' generators (one slot per lane),
+  // the draw parameters and the draft logits rows they read; the top-k candidates of every draw, copied back with
+  // the step's wait for the host's replay of each draw.
+  DevBuf draw_in_d_, cand_v_d_, cand_i_d_;
+  uint8_t* draw_in_h_ = nullptr;
+  float* cand_v_h_ = nullptr;
+  int32_t* cand_i_h_ = nullptr;
+  int draw_k_ = 0;                 // candidates per drawn row this step (the largest top_k of the drawing lanes)
+  uint64_t device_draws_ = 0, draw_mismatches_ = 0;
 };
 
 }  // namespace malkin_hip

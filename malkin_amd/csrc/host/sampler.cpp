@@ -3,6 +3,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <random>
 #include <stdexcept>
 
 namespace malkin_hip {
@@ -20,6 +21,38 @@ float prob_in(const Distribution& d, int32_t id) {
 }
 
 }  // namespace
+
+Mt64::Mt64(uint64_t seed) {
+  w[0] = seed;
+  for (int i = 1; i < kN; ++i) w[i] = 6364136223846793005ull * (w[i - 1] ^ (w[i - 1] >> 62)) + static_cast<uint64_t>(i);
+  w[kN] = kN;
+}
+
+uint64_t Mt64::next() {
+  constexpr int kM = 156;
+  if (w[kN] >= static_cast<uint64_t>(kN)) {
+    // The recurrence x[i] = x[i + m] ^ twist(x[i], x[i + 1]) over the words in order: the first n - m read only
+    // words not yet replaced, the rest read replaced words i - m (and the last, replaced word 0).
+    auto mix = [](uint64_t hi, uint64_t lo, uint64_t far) {
+      const uint64_t y = (hi & 0xFFFFFFFF80000000ull) | (lo & 0x7FFFFFFFull);
+      return far ^ (y >> 1) ^ ((y & 1) ? 0xB5026F5AA96619E9ull : 0);
+    };
+    for (int i = 0; i < kN - kM; ++i) w[i] = mix(w[i], w[i + 1], w[i + kM]);
+    for (int i = kN - kM; i < kN - 1; ++i) w[i] = mix(w[i], w[i + 1], w[i - (kN - kM)]);
+    w[kN - 1] = mix(w[kN - 1], w[0], w[kM - 1]);
+    w[kN] = 0;
+  }
+  uint64_t z = w[w[kN]++];
+  z ^= (z >> 29) & 0x5555555555555555ull;
+  z ^= (z << 17) & 0x71D67FFFEDA60000ull;
+  z ^= (z << 37) & 0xFFF7EEE000000000ull;
+  return z ^ (z >> 43);
+}
+
+double Mt64::uniform() {
+  const double u = static_cast<double>(next()) * 0x1p-64;
+  return u < 1.0 ? u : std::nextafter(1.0, 0.0);
+}
 
 Sampler::Sampler(const SamplingParams& params, bool penalties)
     : p_(params), penalties_(penalties), rng_(params.seed ? params.seed : std::random_device{}()) {}
@@ -132,7 +165,7 @@ void Sampler::finish(const Selector& sel, int i, Distribution& out) const {
     out.push_back(Candidate{static_cast<float>(weights_[static_cast<size_t>(j)] / kept), ids[j]});
 }
 
-double Sampler::uniform() { return std::uniform_real_distribution<double>(0.0, 1.0)(rng_); }
+double Sampler::uniform() { return rng_.uniform(); }
 
 int32_t Sampler::draw(const Distribution& d) {
   if (d.empty()) throw std::invalid_argument("sampler: empty distribution");

@@ -13,7 +13,7 @@
 //     while their weight is at least min_p * w_0, up to and including the one whose running sum reaches
 //     top_p * (sum of all candidate weights); probabilities: weight / (sum of kept weights), rounded to float;
 //   * draws: u ~ U[0, 1) from std::mt19937_64 (seeded with the request's seed, or std::random_device for seed 0)
-//     through std::uniform_real_distribution<double>; the first candidate where the running u - p_i <= 0, the last
+//     through std::uniform_real_distribution<double> (Mt64 below: the same generator and the same conversion); the first candidate where the running u - p_i <= 0, the last
 //     if rounding leaves u above zero; a one-entry distribution draws nothing;
 //   * verify (Leviathan et al. 2023, speculative sampling): accept draft d when u * q(d) < p(d) (and q(d) > 0),
 //     else draw from the normalised positive part of p - q over p's candidates (from p itself when that is empty).
@@ -22,7 +22,6 @@
 #pragma once
 
 #include <cstdint>
-#include <random>
 #include <unordered_map>
 #include <vector>
 
@@ -38,6 +37,21 @@ struct SamplingParams {  // sampler.h:10-18 (same fields and defaults)
   float presence_penalty = 0.0f;
   float frequency_penalty = 0.0f;
   uint64_t seed = 0;  // 0: random
+};
+
+// std::mt19937_64 ([rand.predef]: the 64-bit Mersenne Twister of Matsumoto and Nishimura, n 312, m 156, r 31,
+// a 0xB5026F5AA96619E9, tempering (29, 0x5555555555555555), (17, 0x71D67FFFEDA60000), (37, 0xFFF7EEE000000000), 43,
+// seeding multiplier 6364136223846793005) with its state in one plain array, so that the engine can hand a draft
+// sampler's generator to the device's draws (mk_sample_draw, which advances the same layout).
+struct Mt64 {
+  static constexpr int kN = 312;
+  static constexpr int kWords = kN + 1;  // mk_sample_draw's layout: the state words, then the index of the next one
+  uint64_t w[kWords];
+  explicit Mt64(uint64_t seed);
+  uint64_t next();
+  // libstdc++'s std::uniform_real_distribution<double>(0, 1) on a 64-bit generator: generate_canonical with one
+  // output x, (double)x / 2^64, and a result that rounds to 1 replaced by the largest double below 1.
+  double uniform();
 };
 
 struct Candidate {
@@ -68,13 +82,14 @@ class Sampler {
   int32_t draw(const Distribution& d);
   int32_t verify(const Distribution& p, const Distribution& q, int32_t draft, bool& accepted);
   void accept(int32_t id) { ++counts_[id]; }
+  const Mt64& generator() const { return rng_; }
 
  private:
   double uniform();
 
   SamplingParams p_;
   bool penalties_;
-  std::mt19937_64 rng_;
+  Mt64 rng_;
   std::unordered_map<int32_t, int> counts_;
   mutable std::vector<double> weights_;
 };

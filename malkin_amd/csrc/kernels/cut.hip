@@ -5,6 +5,9 @@
 // running sum has not reached top_p of the total). The host downloads the kept candidates and the total instead of
 // the 608 KB row, and normalises the kept weights itself.
 //
+// k_draw finishes a top-k row the same way and draws from it with a std::mt19937_64 held in device memory (the
+// draft's proposals: one row per sequence and draft depth, no host round trip between draft forwards).
+//
 // The sort is rocPRIM's stable device-wide radix sort of (order key, id) pairs, one row at a time (a row is 152k pairs:
 // hundreds of workgroups). The cut is one 1024-thread workgroup per row: the weights in parallel into the workspace,
 // then the sum and the keep scan in the reference's sequential order by one wave, 64 weights per load, each added
@@ -139,6 +142,121 @@ __global__ void k_cut_tail(const uint32_t* __restrict__ key, const int32_t* __re
   out_i[i] = id[i];
 }
 
+// ---- one draw per top-k row from a std::mt19937_64 kept on the device ----
+
+constexpr int kMtN = 312, kMtM = 156;
+constexpr int kDrawMax = 1024;  // candidates per row (mk_topk's limit)
+
+__device__ __forceinline__ uint64_t mt_mix(uint64_t hi, uint64_t lo, uint64_t far) {
+  const uint64_t y = (hi & 0xFFFFFFFF80000000ull) | (lo & 0x7FFFFFFFull);
+  return far ^ (y >> 1) ^ ((y & 1) ? 0xB5026F5AA96619E9ull : 0ull);
+}
+
+// The state regenerated by one wave, in LDS: x[i] = x[i + m] ^ twist(x[i], x[i + 1]) in index order means that words
+// 0..155 read only old words (all read before any is replaced), and words 156..311 read old words i + 1, the new
+// word 0 (for 311) and new words i - 156.
+__device__ void mt_regenerate(uint64_t* x) {
+  const int lane = threadIdx.x;
+  uint64_t v[3];
+  for (int j = 0; j < 3; ++j) {
+    const int i = lane + 64 * j;
+    if (i < kMtM) v[j] = mt_mix(x[i], x[i + 1], x[i + kMtM]);
+  }
+  __syncthreads();
+  for (int j = 0; j < 3; ++j) {
+    const int i = lane + 64 * j;
+    if (i < kMtM) x[i] = v[j];
+  }
+  __syncthreads();
+  for (int j = 0; j < 3; ++j) {
+    const int i = kMtM + lane + 64 * j;
+    if (i < kMtN) v[j] = mt_mix(x[i], x[i + 1 < kMtN ? i + 1 : 0], x[i - kMtM]);
+  }
+  __syncthreads();
+  for (int j = 0; j < 3; ++j) {
+    const int i = kMtM + lane + 64 * j;
+    if (i < kMtN) x[i] = v[j];
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ uint64_t mt_temper(uint64_t z) {
+  z ^= (z >> 29) & 0x5555555555555555ull;
+  z ^= (z << 17) & 0x71D67FFFEDA60000ull;
+  z ^= (z << 37) & 0xFFF7EEE000000000ull;
+  return z ^ (z >> 43);
+}
+
+// One wave per row. The weights go to LDS; every sum and walk below runs in the reference's sequential order in all
+// lanes alike (walk_weights), so each lane holds the same result.
+__global__ __launch_bounds__(64) void k_draw(const float* __restrict__ values, const int32_t* __restrict__ ids,
+                                             int stride, const mk_draw_params* __restrict__ params,
+                                             uint64_t* __restrict__ states, int n_states, int32_t* __restrict__ out,
+                                             int n_out) {
+  __shared__ float w[kDrawMax];
+  __shared__ uint64_t x[kMtN];
+  const int r = blockIdx.x, lane = threadIdx.x;
+  const mk_draw_params p = params[r];
+  if (p.state < 0 || p.state >= n_states || p.dst < 0 || p.dst >= n_out) return;
+  const int k = min(max(p.k, 1), stride);
+  const float* v = values + (int64_t)r * stride;
+  const int32_t* id = ids + (int64_t)r * stride;
+  // sampler.cpp:37-45: weights exp((l - l_max) / T) as floats, their total in double in order.
+  const float top = v[0];
+  for (int i = lane; i < k; i += 64) w[i] = (float)exp((double)((v[i] - top) / p.temperature));
+  __syncthreads();
+  double all = 0.0;
+  walk_weights(w, k, [&](float wi, int) {
+    all += (double)wi;
+    return true;
+  });
+  // sampler.cpp:47-56: the head above min_p of the first weight, up to the candidate whose running sum reaches top_p
+  // of the total; the kept total is that running sum.
+  const double floor_w = (double)p.min_p * (double)w[0], nucleus = (double)p.top_p * all;
+  double run = 0.0;
+  int keep = k;
+  walk_weights(w, k, [&](float wi, int i) {
+    if (i > 0 && (double)wi < floor_w) {
+      keep = i;
+      return false;
+    }
+    run += (double)wi;
+    if (run >= nucleus) {
+      keep = i + 1;
+      return false;
+    }
+    return true;
+  });
+  int32_t pick = id[0];
+  if (keep > 1) {
+    // sampler.cpp:108-116: u from the generator, then the first candidate where the running u - p_i is <= 0.
+    uint64_t* g = states + (int64_t)MK_MT64_WORDS * p.state;
+    for (int i = lane; i < kMtN; i += 64) x[i] = g[i];
+    uint64_t at = g[kMtN];
+    __syncthreads();
+    const bool regen = at >= (uint64_t)kMtN;
+    if (regen) {
+      mt_regenerate(x);
+      at = 0;
+    }
+    double u = (double)mt_temper(x[at]) * 0x1p-64;
+    if (u >= 1.0) u = 0x1.fffffffffffffp-1;
+    pick = id[keep - 1];
+    walk_weights(w, keep, [&](float wi, int i) {
+      u -= (double)(float)((double)wi / run);
+      if (u <= 0.0) {
+        pick = id[i];
+        return false;
+      }
+      return true;
+    });
+    if (regen)
+      for (int i = lane; i < kMtN; i += 64) g[i] = x[i];
+    if (lane == 0) g[kMtN] = at + 1;
+  }
+  if (lane == 0) out[p.dst] = pick;
+}
+
 size_t sort_storage(int n_vocab) {
   size_t bytes = 0;
   check(rocprim::radix_sort_pairs_desc(nullptr, bytes, static_cast<const uint32_t*>(nullptr),
@@ -188,6 +306,14 @@ void sample_cut_tail(hipStream_t s, void* workspace, int n_rows, int n_vocab, in
   hipLaunchKernelGGL(k_cut_tail, dim3((count + 255) / 256), dim3(256), 0, s, ws.key_out + o, ws.id_out + o, count,
                      out_v, out_i);
   check_launch("sample_cut_tail");
+}
+
+void sample_draw(hipStream_t s, const float* values, const int32_t* ids, int stride, int n_rows,
+                 const mk_draw_params* params, uint64_t* states, int n_states, int32_t* out, int n_out) {
+  if (n_rows <= 0) return;
+  require(stride >= 1 && stride <= kDrawMax, "sample_draw: stride outside 1..1024");
+  hipLaunchKernelGGL(k_draw, dim3(n_rows), dim3(64), 0, s, values, ids, stride, params, states, n_states, out, n_out);
+  check_launch("sample_draw");
 }
 
 }  // namespace mk

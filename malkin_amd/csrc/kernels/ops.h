@@ -225,6 +225,9 @@ void sample_cut(hipStream_t s, const float* logits, int64_t stride, const int32_
                 void* workspace, size_t workspace_bytes);
 void sample_cut_tail(hipStream_t s, void* workspace, int n_rows, int n_vocab, int row, int from, int count,
                      float* values, int32_t* ids);
+// One draw per top-k row from its std::mt19937_64 state (MK_MT64_WORDS words each, advanced in place).
+void sample_draw(hipStream_t s, const float* values, const int32_t* ids, int stride, int n_rows,
+                 const mk_draw_params* params, uint64_t* states, int n_states, int32_t* out, int n_out);
 
 // dst[dst_idx[i]] = src[src_idx[i]], i < n; null index arrays are the identity, negative indices skip.
 void move_ids(hipStream_t s, int32_t* dst, const int32_t* dst_idx, const int32_t* src, const int32_t* src_idx,

@@ -165,6 +165,53 @@ def test_engine_sampled_speculative(mk, oracle, model_files, draft_name):
     check_engine(mk, oracle, model_files, draft_name, reqs)
 
 
+@pytest.mark.parametrize("draft_name", ["tiny", "tiny-q4km"])
+def test_engine_sampled_drafts_on_device(mk, oracle, model_files, draft_name):
+    """Sampled requests whose draft candidates fit the device's top-k (and whose target rows take no penalties) draw
+    their drafts on the device (mk_sample_draw): the step has one host wait however many draft forwards it runs,
+    every device draw equals the host's replay of it, and each stream, with its drafted and accepted counts, is the
+    reference loop's for its seed."""
+    n_ctx, budget = 160, 40
+    reqs = [dict(seed=7), dict(seed=9, temperature=0.6, top_k=300), dict(seed=21, temperature=1.3, top_k=1024,
+                                                                        top_p=1.0, min_p=0.0)]
+    target = mk_.Model(mk, model_files["tiny"], n_ctx, len(reqs))
+    draft = mk_.Model(mk, model_files[draft_name], n_ctx, len(reqs))
+    eng = mk_.Engine(target, draft, n_draft=8)
+    rng = np.random.default_rng(31)
+    prompts = [rng.integers(0, 1024, int(n)).astype(np.int32) for n in rng.integers(3, 40, len(reqs))]
+    refs = []
+    for p, r in zip(prompts, reqs):
+        t = oracle.model(model_files["tiny"], n_ctx, 1)
+        d = oracle.model(model_files[draft_name], n_ctx, 1)
+        refs.append(engine_ref.run_request(oracle, t, d, p, budget, n_ctx, **r))
+        t.close()
+        d.close()
+    # Twice: the first run also grows the engine's buffers (frees wait); the second is measured.
+    for run in range(2):
+        ids = [eng.submit(p, max_tokens=budget, sampling=r) for p, r in zip(prompts, reqs)]
+        mk.sync()
+        w0, s0, (dr0, mm0) = mk_.host_waits(), eng.steps, eng.draws
+        eng.run()
+        waits, steps = mk_.host_waits() - w0, eng.steps - s0
+        draws, mismatches = eng.draws[0] - dr0, eng.draws[1] - mm0
+        print("draft", draft_name, "run", run, "steps", steps, "host waits", waits, "device draws", draws,
+              "mismatches", mismatches, flush=True)
+        if run == 1:
+            assert steps > 0 and waits == steps
+        assert draws > 0 and mismatches == 0
+        drafted = 0
+        for rid, r, (want, winfo) in zip(ids, reqs, refs):
+            toks, info = eng.result(rid)
+            print("request", rid, r, info, winfo, flush=True)
+            assert list(toks) == want, (rid, r)
+            assert info["drafted"] == winfo["drafted"] and info["accepted"] == winfo["accepted"], (rid, r)
+            drafted += info["drafted"]
+        assert draws == drafted
+    eng.close()
+    draft.close()
+    target.close()
+
+
 CUT_CASES = [
     (dict(top_k=0), 4.0),                                   # peaked rows: a short kept head
     (dict(top_k=0, temperature=1.3, top_p=0.99, min_p=0.0), 0.5),  # flat rows: a head past the copy's cap
@@ -207,3 +254,69 @@ def test_whole_vocab_cut_on_device(mk, oracle, params, scale):
         a.accept(t2)
     s.close()
     buf.free()
+
+
+DRAW_ROWS = [  # (top_k, temperature, top_p, min_p): per generator
+    (40, 0.8, 0.95, 0.05),   # the defaults
+    (1, 0.8, 0.95, 0.05),    # one candidate: no draw, the generator untouched
+    (1024, 1.5, 1.0, 0.0),   # every candidate kept
+    (12, 0.05, 0.9, 0.1),    # peaked: mostly one kept, some draws
+    (300, 1.1, 0.5, 0.0),    # nucleus cut inside the candidates
+]
+
+
+def mt_words(g):
+    """The oracle generator's state in mk_sample_draw's layout: 312 words, then the index as a word."""
+    raw = np.frombuffer(g.state.raw, np.uint64)
+    return np.concatenate([raw[:312], np.array([int(np.frombuffer(g.state.raw[312 * 8:312 * 8 + 4], np.int32)[0])],
+                                               np.uint64)])
+
+
+def test_sample_draw_matches_oracle(mk, oracle):
+    """mk_sample_draw (the draft's draws on the device) against the oracle's Sampler::distribution + Sampler::draw:
+    rows of 1024 candidates with one generator each, 700 calls in a row (every generator that draws regenerates its
+    state twice), the ids of every call and the final generator states (words and index) bit-equal."""
+    L = mk_.load()
+    rng = np.random.default_rng(23)
+    G, K, R = len(DRAW_ROWS), 1024, 700
+    seeds = [3, 1 << 40, 12345, 0xDEADBEEF, 77]
+    gens = [oracle.mt64(s) for s in seeds]
+    states = np.stack([mt_words(g) for g in gens])
+    dstates = mk.to_device(states)
+    params = np.zeros((R, G, 6), np.int32)
+    pv = params.view(np.float32)
+    vals = np.zeros((R, G, K), np.float32)
+    ids = np.zeros((R, G, K), np.int32)
+    want = np.zeros((R, G), np.int32)
+    for r in range(R):
+        for g, (k, t, tp, mp) in enumerate(DRAW_ROWS):
+            l = (rng.standard_normal(K) * rng.uniform(0.5, 3)).astype(np.float32)
+            e = oracle.sampler(1, top_k=k, temperature=t, top_p=tp, min_p=mp).distribution(l.copy())
+            want[r, g] = oracle_draw(oracle, gens[g], e)
+            order = np.lexsort((np.arange(K), -l.astype(np.float64)))
+            vals[r, g], ids[r, g] = l[order], order
+            params[r, g, 0] = k
+            pv[r, g, 1:4] = (t, mp, tp)
+            params[r, g, 4] = g
+            params[r, g, 5] = r * G + g
+    dv, di, dp = mk.to_device(vals), mk.to_device(ids), mk.to_device(params)
+    dout = mk.alloc(R * G * 4)
+    print("sample_draw", G, K, R, flush=True)
+    for r in range(R):
+        off = r * G
+        mk_.check(L.mk_sample_draw(mk.h, dv.offset(off * K * 4), di.offset(off * K * 4), K, G, dp.offset(off * 24),
+                                   dstates.ptr, G, dout.ptr, R * G))
+    got = dout.download(np.int32).reshape(R, G)
+    for g in range(G):
+        bad = np.nonzero(got[:, g] != want[:, g])[0]
+        assert bad.size == 0, (DRAW_ROWS[g], int(bad[0]), got[bad[0], g], want[bad[0], g])
+    assert np.array_equal(dstates.download(np.uint64).reshape(G, 313), np.stack([mt_words(g) for g in gens]))
+    assert mt_words(gens[1])[312] == 312 and np.array_equal(mt_words(gens[1]), states[1])  # k = 1 drew nothing
+    for b in (dv, di, dp, dout, dstates):
+        b.free()
+
+
+def oracle_draw(oracle, g, d):
+    pp = np.array([p for p, _ in d], np.float32)
+    pi = np.array([i for _, i in d], np.int32)
+    return int(oracle.lib.or_draw(g.state, pp.ctypes.data, pi.ctypes.data, len(pp)))
