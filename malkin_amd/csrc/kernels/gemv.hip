@@ -610,14 +610,29 @@ void launch(hipStream_t s, const void* w, int64_t rows, int64_t cols, const Gemv
                      rows, cols, in, n, y, ys, accumulate ? 1 : 0);
 }
 
-// Tokens per workgroup: up to 8, fewer when the activation rows and term slots would not fit in LDS.
+// Tokens per workgroup: up to 8, fewer when the activation rows and term slots would not fit in LDS. At 3-4 tokens the
+// split into token groups trades the chain wave's width (R x NT chains) against workgroups per CU and the activation
+// staging each group repeats. Measured on MI355X at n = 3 and 4 (every form bit-identical): 2-token groups beat one
+// 4-token group on matrices of up to 8192 rows (Q6_K: up to 2048) and on those of 12288 columns or more (Q4_K
+// 5120 x 5120 at 4 tokens 19.8 -> 14.6 us, 8192 x 4096 22.0 -> 17.3, Q8_0 4096 x 12288 25.4 -> 18.9, Q6_K 1024 x 5120
+// 10.4 -> 8.4); 1-token groups win on Q4_K of 16384 columns or more (5120 x 17408: 51.3 -> 42.3 us); the other
+// matrices keep the 4-token group (Q6_K 17408 x 5120: 36.1 us against 37.4 in 2-token groups, 5120 x 5120 16.5
+// against 17.2).
+template <int TYPE>
+int short_batch_nt(int64_t rows, int64_t cols) {
+  if (TYPE == kQ4_K && rows <= 8192 && cols >= 16384) return 1;
+  if ((rows <= 8192 && TYPE != kQ6_K) || rows <= 2048 || cols >= 12288) return 2;
+  return 4;
+}
+
 template <int TYPE, bool WIDE, int R>
 void launch_nt(hipStream_t s, const void* w, int64_t rows, int64_t cols, const GemvIn& in, int n, float* y, int64_t ys,
                bool acc) {
   auto fits = [&](size_t bytes) { return bytes <= (size_t)kGemvLdsMax; };
-  if (n <= 1 || !fits(GemvCfg<TYPE, WIDE, R, 2>::lds_bytes(cols)))
+  const int nt = n == 3 || n == 4 ? short_batch_nt<TYPE>(rows, cols) : 8;
+  if (n <= 1 || nt == 1 || !fits(GemvCfg<TYPE, WIDE, R, 2>::lds_bytes(cols)))
     launch<TYPE, WIDE, R, 1, kProQ8>(s, w, rows, cols, in, n, y, ys, acc);
-  else if (n <= 2 || !fits(GemvCfg<TYPE, WIDE, R, 4>::lds_bytes(cols)))
+  else if (n <= 2 || nt == 2 || !fits(GemvCfg<TYPE, WIDE, R, 4>::lds_bytes(cols)))
     launch<TYPE, WIDE, R, 2, kProQ8>(s, w, rows, cols, in, n, y, ys, acc);
   else if (n <= 4 || !fits(GemvCfg<TYPE, WIDE, R, 8>::lds_bytes(cols)))
     launch<TYPE, WIDE, R, 4, kProQ8>(s, w, rows, cols, in, n, y, ys, acc);
