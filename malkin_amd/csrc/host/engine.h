@@ -32,8 +32,11 @@
 // Device residency: greedy drafting runs back to back on the stream. Each round's tokens are the previous round's
 // picks, read from a device array (Model::enqueue id redirects); picks are scattered into a per-lane tree array on
 // the device; accepted rows move on the device. The host waits once per step, for the target's picks. Sampled
-// lanes add one wait per draft round (the draw happens on the host); penalized greedy trees add one after the
-// step's wait (the penalties of a tree row depend on its path, which the host learns at that wait).
+// lanes draw their drafts on the device as well (top-k of the draft row, then a draw with the draft sampler's
+// generator, uploaded once per step) and the host replays those draws after the step's wait; sampled lanes whose
+// draft needs more than 1024 candidates, or whose target rows take penalties, add one wait per draft round (the
+// draw happens on the host); penalized greedy trees add one after the step's wait (the penalties of a tree row depend
+// on its path, which the host learns at that wait).
 #pragma once
 
 #include <chrono>
