@@ -7,7 +7,8 @@ same either way), then greedy decoding to 128 generated tokens (the first from t
 forwards), as `malkin bench` does (main.cpp:126-143).
 
 value = (512 + 128) tokens / wall time of the step, inputs (weights, prompt) resident in HBM before the timed region.
-The JSON line also carries pp512 and tg128 rates, the prefill's fraction of the int8 MFMA peak, the live roofline of
+The JSON line also carries pp512 and tg128 rates, pp512 in the reference engine's protocol (two 256-token forwards,
+pp512_2x256_tok_s, the cpu_baseline leg's protocol), the prefill's fraction of the int8 MFMA peak, the live roofline of
 the dominant kernel (the Q8_0 decode GEMV, timed with HIP events on the library's stream; its HBM traffic from the
 committed counter summary), the kernel-level configurations 1 and 2 of BASELINE.json (kernel_configs), and the
 reference's own AVX-512 path timed on this host's cores on a bounded sample of the same workload (cpu_baseline).
@@ -639,6 +640,16 @@ def main():
         ctx.sync()
         wall = time.perf_counter() - t_start
         ms_step = wall * 1e3 / args.steps
+        # The reference engine's prefill protocol (two 256-token forwards, engine.cpp:381-393), outside the timed step.
+        pp2 = []
+        for i in range(3):
+            ctx.sync()
+            t1 = time.perf_counter()
+            for c in range(0, N_PROMPT, 256):
+                model.forward(prompt[c:c + 256], c)
+            ctx.sync()
+            pp2.append(time.perf_counter() - t1)
+        log(f"[bench] pp512 in two 256-token forwards: {min(pp2) * 1e3:.2f} ms (best of 3)")
         roof = gemv_roofline(ctx, model, cfg)
         log(f"[bench] decode GEMV: {roof['achieved']} GB/s ({roof['us_per_launch']} us per launch)")
         model.close()
@@ -678,6 +689,7 @@ def main():
         "config": {"workload": "qwen3-8b-q8_0 pp512+tg128, batch 1, ctx 4096, greedy", "prompt_tokens": N_PROMPT,
                    "gen_tokens": N_GEN, "decode_forwards": N_GEN - 1, "parallelism": "none (1 GPU)"},
         "pp512_tok_s": round(N_PROMPT * 1e3 / pp_ms, 1),
+        "pp512_2x256_tok_s": round(N_PROMPT / float(np.median(pp2)), 1),
         "tg128_tok_s": round((N_GEN - 1) * 1e3 / dec_ms, 2),
         "decode_ms_per_token": round(dec_ms / (N_GEN - 1), 4),
         "decode_hbm_frac": round(model_bytes_per_token(cfg) / (dec_ms / (N_GEN - 1) / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
