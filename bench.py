@@ -17,6 +17,7 @@ reference's own AVX-512 path timed on this host's cores on a bounded sample of t
     python bench.py --probe traffic     # launch sequence for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
     python bench.py --probe gemm        # the prefill GEMM shapes, for counter passes
     python bench.py --probe kquant      # config 2's Q4_K shapes at n = 1, 4, 8, for counter passes
+    python bench.py --probe rows        # the pp512 forward's prefill attention, for counter passes
 """
 import argparse
 import json
@@ -492,6 +493,33 @@ def tree_nodes(ids, P):
     return nodes
 
 
+def rows_probe():
+    """Launch sequence for the prefill attention's counters (rocprofv3 --pmc): k_attention_rows on the pp512 forward's
+    shape (512 causal tokens of one sequence, 32 query heads over 8 KV heads, head_dim 128, keys 1..512 per token) over
+    a random int8 KV cache, 3 untimed launches then 20."""
+    import ctypes
+    import malkin_amd as mk
+    L = mk.load()
+    ctx = mk.Context(0)
+    rng = np.random.default_rng(7)
+    D, H, KV, n_ctx, n = 128, 32, 8, 4096, N_PROMPT
+    k8 = ctx.to_device(rng.integers(-127, 128, (1, KV, n_ctx, D), dtype=np.int8))
+    v8 = ctx.to_device(rng.integers(-127, 128, (1, KV, n_ctx, D), dtype=np.int8))
+    ks = ctx.to_device(rng.uniform(0.001, 0.05, (1, KV, n_ctx)).astype(np.float32))
+    vs = ctx.to_device(rng.uniform(0.001, 0.05, (1, KV, n_ctx)).astype(np.float32))
+    kv = mk.MkKvCache(k8.ptr, v8.ptr, ks.ptr, vs.ptr, 1, 1, KV, D, n_ctx)
+    q = ctx.to_device(rng.standard_normal((n, H * D)).astype(np.float32))
+    seq = ctx.to_device(np.zeros(n, np.int32))
+    nk = ctx.to_device(np.arange(1, n + 1, dtype=np.int32))
+    out = ctx.alloc(n * H * D * 4)
+    for i in range(23):
+        mk.check(L.mk_attention(ctx.h, q.ptr, H * D, out.ptr, H * D, n, H, ctypes.byref(kv), 0, seq.ptr, nk.ptr, None,
+                                None, n))
+    ctx.sync()
+    log(f"[probe] k_attention_rows: {n} causal tokens, {H} heads over {KV} KV heads, head_dim {D}: 23 launches")
+    ctx.close()
+
+
 def tree_probe():
     """Launch sequence for the tree-verification kernel trace: config 5's target (Qwen3-14B shape, Q6_K), the
     2048-token prefix in 256-token forwards, then 4 verifications of the 17-node tree."""
@@ -589,11 +617,11 @@ def main():
     ap.add_argument("--no-engine-configs", action="store_true",
                     help="skip BASELINE configs 3 (Qwen3-4B pp512 + tg128), 4 (continuous batching) and 5 "
                          "(speculative tree verification)")
-    ap.add_argument("--probe", choices=["traffic", "decode", "gemm", "kquant", "tree"],
+    ap.add_argument("--probe", choices=["traffic", "decode", "gemm", "kquant", "tree", "rows"],
                     help="only run a launch sequence for counter profiles: the roofline kernel's HBM traffic, "
                          "one decode layer's kernels (attention and the four GEMVs, for instruction and wait counters), "
                          "the prefill GEMM (config 1 and the pp512 forward's shapes), config 2's short K-quant batches, "
-                         "or config 5's tree verification")
+                         "config 5's tree verification, or the pp512 forward's prefill attention")
     args = ap.parse_args()
     if args.probe == "traffic":
         traffic_probe()
@@ -609,6 +637,9 @@ def main():
         return
     if args.probe == "tree":
         tree_probe()
+        return
+    if args.probe == "rows":
+        rows_probe()
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus})",
