@@ -514,8 +514,8 @@ int mk_sample_cut_tail(mk_ctx* c, void* workspace, int n_rows, int n_vocab, int 
 int mk_sample_draw(mk_ctx* c, const float* values, const int32_t* ids, int stride, int n_rows,
                    const mk_draw_params* params, uint64_t* states, int n_states, int32_t* out, int n_out) {
   return guard([&] {
-    require(c && n_rows >= 0 && stride >= 1 && stride <= 1024 && n_states >= 0 && n_out >= 0,
-            "sample_draw: bad arguments");
+    require(c && n_rows >= 0 && n_states >= 0 && n_out >= 0, "sample_draw: bad arguments");
+    require(stride >= 1 && stride <= 1024, "sample_draw: stride outside 1..1024 (mk_topk's candidate limit)");
     if (n_rows == 0) return;
     require(values && ids && params && states && out, "sample_draw: null array");
     mk::sample_draw(c->stream, values, ids, stride, n_rows, params, states, n_states, out, n_out);

@@ -320,3 +320,51 @@ def oracle_draw(oracle, g, d):
     pp = np.array([p for p, _ in d], np.float32)
     pi = np.array([i for _, i in d], np.int32)
     return int(oracle.lib.or_draw(g.state, pp.ctypes.data, pi.ctypes.data, len(pp)))
+
+
+def test_sample_draw_edges(mk, oracle):
+    """mk_sample_draw's boundaries: a row whose generator or destination index is out of range is skipped (its
+    output and every generator untouched), k is clamped to 1..stride (k <= 0 and k > stride draw as 1 and stride
+    candidates), stride 1 always picks the only candidate without drawing, and a stride above 1024 is refused with
+    a status before anything is queued."""
+    L = mk_.load()
+    rng = np.random.default_rng(29)
+    K, G = 16, 2
+    gens = [oracle.mt64(101), oracle.mt64(202)]
+    states = np.stack([mt_words(g) for g in gens])
+    dstates = mk.to_device(states)
+    l = np.sort(rng.standard_normal((4, K)).astype(np.float32), axis=1)[:, ::-1].copy()
+    ids = np.tile(np.arange(K, dtype=np.int32) * 3, (4, 1))
+    dv, di = mk.to_device(l), mk.to_device(ids)
+    # rows: 0 bad state, 1 bad dst, 2 k = 0 (one candidate), 3 k = 99 (all 16) from generator 1
+    params = np.zeros((4, 6), np.int32)
+    pv = params.view(np.float32)
+    pv[:, 1:4] = (1.0, 0.0, 1.0)  # temperature 1, min_p 0, top_p 1
+    params[:, 0] = (K, K, 0, 99)
+    params[:, 4] = (G, 0, 0, 1)
+    params[:, 5] = (0, 4, 2, 3)
+    out0 = np.full(4, -7, np.int32)
+    dp, dout = mk.to_device(params), mk.to_device(out0)
+    mk_.check(L.mk_sample_draw(mk.h, dv.ptr, di.ptr, K, 4, dp.ptr, dstates.ptr, G, dout.ptr, 4))
+    got = dout.download(np.int32)
+    assert got[0] == -7 and got[1] == -7, got  # skipped rows wrote nothing
+    assert got[2] == ids[2, 0]                  # one candidate: no draw
+    e = oracle.sampler(1, top_k=K, temperature=1.0, top_p=1.0, min_p=0.0).distribution(
+        np.ascontiguousarray(l[3][np.argsort(ids[3] // 3)]))
+    e = [(p, int(ids[3][i])) for p, i in e]
+    assert got[3] == oracle_draw(oracle, gens[1], e)
+    after = dstates.download(np.uint64).reshape(G, 313)
+    assert np.array_equal(after[0], states[0])  # generator 0 served only skipped / one-candidate rows
+    assert np.array_equal(after[1], mt_words(gens[1]))
+    # stride 1: the only candidate, generator untouched
+    params1 = np.array([[5, 0, 0, 0, 0, 0]], np.int32)
+    params1.view(np.float32)[0, 1:4] = (1.0, 0.0, 1.0)
+    dp1 = mk.to_device(params1)
+    mk_.check(L.mk_sample_draw(mk.h, dv.ptr, di.ptr, 1, 1, dp1.ptr, dstates.ptr, G, dout.ptr, 4))
+    assert dout.download(np.int32)[0] == ids[0, 0]
+    assert np.array_equal(dstates.download(np.uint64).reshape(G, 313)[0], states[0])
+    # a stride above mk_topk's 1024 is refused
+    rc = L.mk_sample_draw(mk.h, dv.ptr, di.ptr, 1025, 1, dp1.ptr, dstates.ptr, G, dout.ptr, 4)
+    assert rc == mk_.MK_ERR_INVALID and "1024" in L.mk_last_error().decode()
+    for b in (dv, di, dp, dp1, dout, dstates):
+        b.free()
