@@ -18,8 +18,9 @@
 //
 // A workgroup owns a 128-row x TOK-token tile and walks the K dimension in stages of KB blocks held in a ring of NS
 // LDS buffers; its wave w computes rows 32 (w % 4) .. + 31 and WT tokens of the tile. Three forms:
-//   TOK = WT = 64, 4 waves, KB = 4 (26 KB per stage, 3 stages: two workgroups per CU): a step is one block, its two
-//     int8 MFMAs the two 32-token halves;
+//   TOK = WT = 64, 4 waves, KB = 4 (26 KB per stage, 3 stages: two workgroups per CU; or 2 stages with one result
+//     set, each step folding its own MFMA results: three workgroups per CU): a step is one block, its two int8 MFMAs
+//     the two 32-token halves;
 //   TOK = 64, WT = 32, 8 waves, KB = 8 (52 KB per stage, 3 stages: one workgroup per CU, two waves per SIMD): waves
 //     w and w + 4 take the two 32-token halves of the same rows;
 //   TOK = WT = 32, 4 waves, KB = 8 (43 KB per stage, 3 stages): for grids that fit the CUs once at 32 tokens.
@@ -97,7 +98,7 @@ __device__ __forceinline__ void load_lds4(const void* g, uint8_t* l) { lds_copy4
 // RA: how many steps ahead the operands are read from LDS (two where two waves share a SIMD: each wave then runs
 // about half as fast and the other wave's reads queue in front of its own).
 template <int TOK, int WT, int NS>
-constexpr int gemm_waves() { return TOK == 64 ? 2 : 1; }
+constexpr int gemm_waves() { return TOK == 64 ? (NS == 2 ? 3 : 2) : 1; }
 template <int TOK, int WT, int NS, int RA>
 __global__ __launch_bounds__((64 * StageLds<TOK, WT>::NW)) __attribute__((amdgpu_waves_per_eu(
     gemm_waves<TOK, WT, NS>(), gemm_waves<TOK, WT, NS>()))) void k_gemm_q8_0(const uint8_t* W, int64_t rows, int64_t cols,
@@ -253,19 +254,30 @@ __global__ __launch_bounds__((64 * StageLds<TOK, WT>::NW)) __attribute__((amdgpu
     v32f p;
   };
   Ops op[RA + 1];
-  Res rs[2];
-  rs[1].f0 = {};
-  rs[1].f1 = {};
-  rs[1].p = {};
+  Res rs[NS == 2 ? 1 : 2];
+  rs[NS == 2 ? 0 : 1].f0 = {};
+  rs[NS == 2 ? 0 : 1].f1 = {};
+  rs[NS == 2 ? 0 : 1].p = {};
   v16f& acc_b = WT == 64 ? acc1 : acc0;  // the second MFMA's accumulator
+  constexpr bool SINGLE = NS == 2;  // one result set: a step folds its own results (three waves per SIMD cover it)
   auto step = [&]<int I, int RB, int RBL>(int bl) __attribute__((always_inline)) {
     const Ops& o = op[I % (RA + 1)];
-    Res& r = rs[I % 2];
-    const Res& pr = rs[1 - I % 2];
+    Res& r = rs[SINGLE ? 0 : I % 2];
+    const Res& pr = rs[SINGLE ? 0 : 1 - I % 2];
     Ops& nx = op[(I + RA) % (RA + 1)];
     const bool live = (WT == 64 ? bl : bl + h) < nb;
     const float dw = live ? half_to_float(o.dw) : 0.0f, dx = live ? o.dx : 0.0f;
     read.template operator()<RB, RBL>(nx.a0, nx.a1, nx.b0, nx.b1, nx.dw, nx.dx);
+    if constexpr (SINGLE) {
+      r.p = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, dx, zero, 0, 0, 0);
+      r.f0 = __builtin_bit_cast(v16f, __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a0, o.b0, magic, 0, 0, 0));
+      r.f1 = __builtin_bit_cast(v16f, __builtin_amdgcn_mfma_i32_32x32x32_i8(WT == 64 ? o.a0 : o.a1, o.b1, magic, 0, 0, 0));
+      r.f0 = __builtin_amdgcn_mfma_f32_16x16x1f32(-kMagicF, 1.0f, r.f0, 0, 0, 0);
+      r.f1 = __builtin_amdgcn_mfma_f32_16x16x1f32(-kMagicF, 1.0f, r.f1, 0, 0, 0);
+      fold(acc0, r.f0, r.p, 0, 0, 16);
+      fold(acc_b, r.f1, r.p, 1, 0, 16);
+      return;
+    }
     r.p = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, dx, zero, 0, 0, 0);
     fold(acc0, pr.f0, pr.p, 0, 0, 16);
     __builtin_amdgcn_sched_barrier(0);
@@ -330,8 +342,10 @@ __global__ __launch_bounds__((64 * StageLds<TOK, WT>::NW)) __attribute__((amdgpu
       (void)((s + I < nstages ? (stage.template operator()<I>(s + I), true) : false) && ...);
     }(std::make_integer_sequence<int, NS>{});
   }
-  fold(acc0, rs[1].f0, rs[1].p, 0, 0, 16);
-  fold(acc_b, rs[1].f1, rs[1].p, 1, 0, 16);
+  if constexpr (!SINGLE) {
+    fold(acc0, rs[1].f0, rs[1].p, 0, 0, 16);
+    fold(acc_b, rs[1].f1, rs[1].p, 1, 0, 16);
+  }
   // The last stage's loads were waited for (vmcnt(0)) when it was entered; nothing is in flight past the loop.
 
   // Element i of tile j: row 32 rg + 8 (i / 4) + 4 h + i % 4, token tw + 32 j + li.
@@ -390,15 +404,18 @@ void gemm_q8_0(hipStream_t s, const void* w, int64_t rows, int64_t cols, const B
   // the CUs once at 32-token tiles takes them (4096 x 4096 at 256 tokens: 23.8 us against 29.7 with eight waves); one
   // that fits once at 64-token tiles takes the eight-wave form, two waves per SIMD in one workgroup (4096 x 4096 at 512
   // tokens 40.5 -> 34.0 us, 4096 x 12288 103.1 -> 85.2, 6144 x 4096 at 256 tokens 38.8 -> 32.0, against the
-  // four-wave 6-stage ring); larger grids take two four-wave workgroups per CU (config 1: 60.0 us against 63.1 with
-  // eight waves, gate|up 24576 x 4096 at 512 tokens 170.6 against 187.6).
+  // four-wave 6-stage ring); grids that fit two four-wave workgroups per CU take those; larger ones three (a two-stage
+  // ring and one result set, so that 168 registers hold a wave: config 1's 608 tiles 58.1 -> 53.8 us, gate|up 24576 x
+  // 4096 at 512 tokens 187.2 -> 183.2; a grid of one round at two per CU runs slower in it, 6144 x 4096 56.3 -> 56.9).
   const int64_t cus = device_cus();
   if ((int64_t)n_rt * ((n + 31) / 32) <= cus)
     go.template operator()<32, 32, 3, 1>();
   else if ((int64_t)n_rt * ((n + 63) / 64) <= cus)
     go.template operator()<64, 32, 3, 2>();
-  else
+  else if ((int64_t)n_rt * ((n + 63) / 64) <= 2 * cus)
     go.template operator()<64, 64, 3, 2>();
+  else
+    go.template operator()<64, 64, 2, 1>();
   check_launch("gemm_q8_0");
 }
 
