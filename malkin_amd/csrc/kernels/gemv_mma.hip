@@ -81,6 +81,7 @@ __global__ __launch_bounds__(kThreads) void k_mmv(const uint8_t* W, int64_t rows
                                                   int n, float* __restrict__ y, int64_t ys, int accumulate) {
   using S = MmvLds<TYPE, NTT>;
   static_assert((NS - 1) * S::loads < 64, "the ring's loads must fit the vmcnt counter");
+  constexpr int TS = 16 * NTT;                      // token slots per unit in X and DX
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wu = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -201,8 +202,8 @@ __global__ __launch_bounds__(kThreads) void k_mmv(const uint8_t* W, int64_t rows
         const float dw = half_to_float(*reinterpret_cast<const uint16_t*>(wv + S::s_off + gi * 128 + u * 16 + rr * 2));
 #pragma unroll
         for (int m = 0; m < NTT; ++m) {
-          const long a = *reinterpret_cast<const long*>(st + S::x + ((u * NTT + m) * 16 + r) * 32 + 8 * c);
-          const float4 dx = *reinterpret_cast<const float4*>(st + S::dx + ((u * NTT + m) * 16 + 4 * c) * 4);
+          const long a = *reinterpret_cast<const long*>(st + S::x + (u * TS + 16 * m + r) * 32 + 8 * c);
+          const float4 dx = *reinterpret_cast<const float4*>(st + S::dx + (u * TS + 16 * m + 4 * c) * 4);
           const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero4, 0, 0, 0);
           acc[m][0] = fma_((float)d[0], dw * dx.x, acc[m][0]);
           acc[m][1] = fma_((float)d[1], dw * dx.y, acc[m][1]);
@@ -228,8 +229,8 @@ __global__ __launch_bounds__(kThreads) void k_mmv(const uint8_t* W, int64_t rows
         const float dsc0 = dd * (float)(int8_t)(scw & 0xFF), dsc1 = dd * (float)(int8_t)(scw >> 8);
 #pragma unroll
         for (int m = 0; m < NTT; ++m) {
-          const long a = *reinterpret_cast<const long*>(st + S::x + ((u * NTT + m) * 16 + r) * 32 + 8 * c);
-          const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + ((u * NTT + m) * 16 + 4 * c) * 4);
+          const long a = *reinterpret_cast<const long*>(st + S::x + (u * TS + 16 * m + r) * 32 + 8 * c);
+          const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + (u * TS + 16 * m + 4 * c) * 4);
           const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
           const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b0, zero4, 0, 0, 0);
           const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, zero4, 0, 0, 0);
@@ -273,8 +274,8 @@ __global__ __launch_bounds__(kThreads) void k_mmv(const uint8_t* W, int64_t rows
           const float fsc = d * (float)sc, nmn = -(dmin * (float)mn);
 #pragma unroll
           for (int m = 0; m < NTT; ++m) {
-            const long a = *reinterpret_cast<const long*>(st + S::x + ((u * NTT + m) * 16 + r) * 32 + 8 * c);
-            const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + ((u * NTT + m) * 16 + 4 * c) * 4);
+            const long a = *reinterpret_cast<const long*>(st + S::x + (u * TS + 16 * m + r) * 32 + 8 * c);
+            const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + (u * TS + 16 * m + 4 * c) * 4);
             const float4 xs4 = *reinterpret_cast<const float4*>(xsum_w + ((u * NTT + m) * 16 + 4 * c));
             const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
             const float xsum[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
@@ -324,23 +325,32 @@ template <int TYPE, bool WIDE>
 struct Ks {
   static constexpr int E = (TYPE == kQ8_0 || TYPE == kQ4_K || (TYPE == kQ6_K && WIDE)) ? 2 : 4;
 };
-template <int TYPE, bool WIDE, int NTT, int KW>
+// TS: token slots per unit in X, DX, XS and the terms (16 NTT, or 20 for two token tiles holding at most 20 tokens,
+// the tree verification batch: rows of padding tokens are neither copied nor stored).
+template <int TYPE, bool WIDE, int NTT, int KW, int TS>
 struct KsLds {
   static constexpr int w_bytes = TYPE == kQ8_0 ? 2 * 8 * 256 : TYPE == kQ6_K ? 2 * 1536 : 2 * 1024;
   static constexpr int s_off = w_bytes, d_off = w_bytes + 256;
   static constexpr int x = w_bytes + 256 + (TYPE == kQ6_K ? 256 : 0);
-  static constexpr int dx = x + kUnits * 16 * NTT * 32;
-  static constexpr int xs = dx + kUnits * 16 * NTT * 4;
-  static constexpr int bytes = xs + (TYPE == kQ4_K ? kUnits * 16 * NTT * 4 : 0);  // one ring stage
-  static constexpr int terms1 = kUnits * 16 * NTT * 16 * Ks<TYPE, WIDE>::E * 4;   // one stage's terms
+  static constexpr int dx_bytes = (kUnits * TS * 4 + 255) / 256 * 256;  // whole 256-byte copies
+  static constexpr int dx = x + kUnits * TS * 32;
+  static constexpr int xs = dx + dx_bytes;
+  static constexpr int bytes = xs + (TYPE == kQ4_K ? dx_bytes : 0);  // one ring stage
+  static constexpr int terms1 = kUnits * TS * 16 * Ks<TYPE, WIDE>::E * 4;   // one stage's terms
   // Double-buffered (stage s's terms written while stage s - 1's chains run) where two workgroups per CU still get
   // a three-stage ring in 80 KB each.
   static constexpr bool db = (80 * 1024 - 2 * terms1) / bytes >= 3;
   static constexpr int terms = (db ? 2 : 1) * terms1;
-  // X: 4 NTT pieces of 1 KB per stage, xp per wave (KW waves)
+  // One token tile: X in 4 pieces of 1 KB per stage, xp per wave (KW waves); loads per wave per stage: W, S, (D), X,
+  // DX, (XS), pieces past a wave's share repeating another wave's copy.
   static constexpr int xp = (4 * NTT + KW - 1) / KW;
-  // loads per wave per stage: W, S, (D), X, DX, (XS); pieces past a wave's share repeat another wave's copy
-  static constexpr int loads = 1 + 1 + (TYPE == kQ6_K ? 1 : 0) + xp + 1 + (TYPE == kQ4_K ? 1 : 0);
+  // Two token tiles: the stage is a list of pieces, 1 KB ones (W, then X) and 256-byte ones (S, D, DX, XS), and
+  // wave w copies pieces w, w + KW, ... (lpw of them, the last piece repeated past the end).
+  static constexpr int n_x4 = w_bytes / 1024 + kUnits * TS * 32 / 1024;
+  static constexpr int n_dw = 1 + (TYPE == kQ6_K ? 1 : 0) + dx_bytes / 256 * (TYPE == kQ4_K ? 2 : 1);
+  static constexpr int lpw = (n_x4 + n_dw + KW - 1) / KW;
+  static constexpr int loads = NTT == 2 ? lpw : 1 + 1 + (TYPE == kQ6_K ? 1 : 0) + xp + 1 + (TYPE == kQ4_K ? 1 : 0);
+  static_assert(kUnits * TS * 32 % 1024 == 0, "X in whole 1 KB pieces");
 };
 
 // KW waves per workgroup (4 or 8): each wave computes the dots and terms of 8 / KW of a stage's 8 units.
@@ -349,11 +359,12 @@ struct KsLds {
 // 0..7 (zero elsewhere) against unit u's weights, the second accumulates unit u + 1's activations in rows 8..15
 // against unit u + 1's weights, so result element i of lane quarter c is (unit u + c / 2, token 4 (c % 2) + i):
 // exact int dots of both units, and no epilogue work for padding token columns.
-template <int TYPE, bool WIDE, int NTT, int NS, int KW, bool PAIR>
+template <int TYPE, bool WIDE, int NTT, int NS, int KW, bool PAIR, int TS>
 __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t rows, int64_t cols, const BlockQ8* x,
                                                      int n, float* __restrict__ y, int64_t ys, int accumulate) {
-  using S = KsLds<TYPE, WIDE, NTT, KW>;
+  using S = KsLds<TYPE, WIDE, NTT, KW, TS>;
   static_assert(!PAIR || (NTT == 1 && kUnits / KW % 2 == 0), "pairs: one token tile, an even number of units per wave");
+  static_assert(NTT == 2 ? TS > 16 && TS <= 32 && TS % 4 == 0 : TS == 16, "token slots");
   constexpr int E = Ks<TYPE, WIDE>::E;
   constexpr int UPW = kUnits / KW;                  // units per wave and stage
   constexpr int CT = 4 * KW;                        // token rows of the chain threads (16 rows x CT tokens)
@@ -370,26 +381,31 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
   const int nst = nq8 / kUnits;
   const int64_t g0 = (int64_t)rt * 2;               // first 8-row group
 
-  // Copies. W: 1 KB pieces, wave w takes piece min(w, pieces - 1); S, D: one 256-byte piece, every wave; X: xp
-  // 1 KB pieces per wave (piece min(xp w + k, 4 NTT - 1)); DX, XS: 256-byte pieces, wave w takes piece w % (2 NTT).
+  // Copies (one token tile). W: 1 KB pieces, wave w takes piece min(w, pieces - 1); S, D: one 256-byte piece, every
+  // wave; X: xp 1 KB pieces per wave (piece min(xp w + k, 4 NTT - 1)); DX, XS: 256-byte pieces, wave w takes piece
+  // w % (2 NTT). Two token tiles: the piece list of KsLds.
   constexpr int WP = S::w_bytes / 1024;
   const uint8_t* xb = reinterpret_cast<const uint8_t*>(x + (int64_t)t0 * nq8);
+  // Source offset of the activation byte copied by this lane into X byte p (1 KB pieces: 16 bytes a lane) or DX / XS
+  // byte p (256-byte pieces: 4 bytes a lane). Slots of padding tokens copy the last token's bytes.
+  auto x_src = [&](int p) __attribute__((always_inline)) {
+    const int unit = p / (TS * 32), rem = p % (TS * 32);
+    const int tok = min(rem / 32, ntok - 1), half = (rem % 32) / 16;
+    return (uint32_t)((tok * nq8 + unit) * 40 + 8 + 16 * half);
+  };
+  auto dx_src = [&](int p) __attribute__((always_inline)) {
+    const int unit = min(p / (TS * 4), kUnits - 1), tok = min((p % (TS * 4)) / 4, ntok - 1);
+    return (uint32_t)((tok * nq8 + unit) * 40);
+  };
   uint32_t x_off[S::xp], dx_off;
   int x_pc[S::xp];
 #pragma unroll
   for (int k = 0; k < S::xp; ++k) {
     x_pc[k] = min(S::xp * wu + k, 4 * NTT - 1);
-    const int p = 1024 * x_pc[k] + 16 * lane;
-    const int unit = p / (512 * NTT), rem = p % (512 * NTT);
-    const int tok = min(rem / 32, ntok - 1), half = (rem % 32) / 16;
-    x_off[k] = (uint32_t)((tok * nq8 + unit) * 40 + 8 + 16 * half);
+    x_off[k] = x_src(1024 * x_pc[k] + 16 * lane);
   }
   const int dxp = wu % (2 * NTT);
-  {
-    const int p = 256 * dxp + 4 * lane;
-    const int unit = p / (64 * NTT), tok = min((p % (64 * NTT)) / 4, ntok - 1);
-    dx_off = (uint32_t)((tok * nq8 + unit) * 40);
-  }
+  dx_off = dx_src(256 * dxp + 4 * lane);
   const int wp = min(wu, WP - 1);
   const uint8_t *wq, *ws, *wd = nullptr;
   uint32_t w_off, s_off, d_off = 0;
@@ -429,8 +445,48 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
     ws_step = 128;
   }
 
+  // Two token tiles: slot j of this wave copies piece min(KW j + w, pieces - 1) of every stage (source sl_src + stage
+  // sl_step, LDS offset sl_dst in the stage buffer, 16 or 4 bytes a lane). W pieces are the first WP < KW, so only
+  // slot 0 of waves below WP holds one, the wave's own piece wp.
+  const uint8_t* sl_src[S::lpw];
+  int64_t sl_step[S::lpw];
+  uint32_t sl_dst[S::lpw];
+  bool sl_x4[S::lpw];
+  if constexpr (NTT == 2) {
+#pragma unroll
+    for (int j = 0; j < S::lpw; ++j) {
+      const int p = min(KW * j + wu, S::n_x4 + S::n_dw - 1);
+      sl_x4[j] = p < S::n_x4;
+      if (p < WP) {
+        sl_src[j] = wq + w_off, sl_step[j] = wq_step, sl_dst[j] = 1024 * p;
+      } else if (p < S::n_x4) {
+        const int k = p - WP;
+        sl_src[j] = xb + x_src(1024 * k + 16 * lane), sl_step[j] = kUnits * 40, sl_dst[j] = S::x + 1024 * k;
+      } else if (p == S::n_x4) {
+        sl_src[j] = ws + s_off, sl_step[j] = ws_step, sl_dst[j] = S::s_off;
+      } else if (TYPE == kQ6_K && p == S::n_x4 + 1) {
+        sl_src[j] = wd + d_off, sl_step[j] = 16, sl_dst[j] = S::d_off;
+      } else {
+        constexpr int per = S::dx_bytes / 256;
+        const int k = p - S::n_x4 - 1 - (TYPE == kQ6_K ? 1 : 0), which = k / per, kk = k % per;  // which 1: XS
+        sl_src[j] = xb + dx_src(256 * kk + 4 * lane) + 4 * which, sl_step[j] = kUnits * 40;
+        sl_dst[j] = (which ? S::xs : S::dx) + 256 * kk;
+      }
+    }
+  }
+
   auto issue = [&]<int BUF>(int sn) __attribute__((always_inline)) {
     uint8_t* st = smem + BUF * S::bytes;
+    if constexpr (NTT == 2) {
+#pragma unroll
+      for (int j = 0; j < S::lpw; ++j) {
+        if (sl_x4[j])
+          ld16(sl_src[j] + sn * sl_step[j], st + sl_dst[j]);
+        else
+          ld4(sl_src[j] + sn * sl_step[j], st + sl_dst[j]);
+      }
+      return;
+    }
     ld16(wq + (size_t)sn * wq_step + w_off, st + 1024 * wp);
     ld4(ws + (size_t)sn * ws_step + s_off, st + S::s_off);
     if constexpr (TYPE == kQ6_K) ld4(wd + (size_t)sn * 16 + d_off, st + S::d_off);
@@ -445,9 +501,10 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
   // elements i: tokens 4 c + i (+ 16 m). Chain role: row cr = tid % 16, tokens ct + CT m (those below 16 NTT).
   const int r = lane & 15, c = lane >> 4, gi = r >> 3, rr = r & 7;
   const int cr = tid & 15, ct = tid >> 4;
-  // Result element i of the second token tile holds tokens 16 + 4 c + i: elements i >= ntok - 16 are padding in every
-  // lane, and their terms are neither formed nor read (17 tokens, the tree verification batch: only i = 0).
-  const int lim1 = min(4, ntok - 16);
+  // Result element i of the second token tile holds token 16 + 4 c + i: elements i >= lim1 are padding in every lane
+  // (wave-uniform, skipped), and in this lane quarter elements i >= live1; padding terms are neither stored nor read
+  // (17 tokens, the tree verification batch: only element 0 of lane quarter 0).
+  const int lim1 = min(4, ntok - 16), live1 = ntok - 16 - 4 * c;
   float acc[CPT];
 #pragma unroll
   for (int m = 0; m < CPT; ++m) acc[m] = 0.0f;
@@ -467,7 +524,7 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
     }
   };
   auto put = [&](int u, int tok, const float (&e)[E]) __attribute__((always_inline)) {
-    float* p = terms + (((u * 16 * NTT) + tok) * 16 + r) * E;
+    float* p = terms + ((u * TS + tok) * 16 + r) * E;
     if constexpr (E == 2)
       *reinterpret_cast<float2*>(p) = make_float2(e[0], e[1]);
     else
@@ -500,7 +557,7 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
       }
 #pragma unroll
       for (int u = 0; u < kUnits; ++u) {
-        const float* p = terms + (((u * 16 * NTT) + tk) * 16 + cr) * E;
+        const float* p = terms + ((u * TS + tk) * 16 + cr) * E;
         if constexpr (E == 2) {
           const float2 e = *reinterpret_cast<const float2*>(p);
           acc[m] = fma_(e.x, e.y, acc[m]);
@@ -528,10 +585,10 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
       const int ph = c >> 1, pt = c & 1;
       const bool lo = r < 8;
       auto xa = [&](int u) __attribute__((always_inline)) {  // operand bytes of token r % 8 of unit u
-        return *reinterpret_cast<const long*>(st + S::x + (u * 16 + (r & 7)) * 32 + 8 * c);
+        return *reinterpret_cast<const long*>(st + S::x + (u * TS + (r & 7)) * 32 + 8 * c);
       };
       auto dxs = [&](int u0) __attribute__((always_inline)) {  // dx of this lane's result tokens
-        return *reinterpret_cast<const float4*>(st + S::dx + ((u0 + ph) * 16 + 4 * pt) * 4);
+        return *reinterpret_cast<const float4*>(st + S::dx + ((u0 + ph) * TS + 4 * pt) * 4);
       };
       if constexpr (TYPE == kQ8_0) {
 #pragma unroll
@@ -596,7 +653,7 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
             const int idx = lane + 64 * k;
             if (idx < UPW * 16) {
               const int u = UPW * wu + idx / 16, tok = idx % 16;
-              const int at = u * 16 + tok;
+              const int at = u * TS + tok;
               const uint32_t sx = *reinterpret_cast<const uint32_t*>(st + S::xs + at * 4);
               const float dxv = *reinterpret_cast<const float*>(st + S::dx + at * 4);
               xs_t[tok * kUnits + u] = dxv * (float)((int)(int16_t)(sx & 0xFFFF) + (int)(int16_t)(sx >> 16));
@@ -637,13 +694,16 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
         const float dw = half_to_float(*reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + u * 16 + rr * 2));
 #pragma unroll
         for (int m = 0; m < NTT; ++m) {
-          const long a = *reinterpret_cast<const long*>(st + S::x + ((u * NTT + m) * 16 + r) * 32 + 8 * c);
-          const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + ((u * NTT + m) * 16 + 4 * c) * 4);
+          const long a = *reinterpret_cast<const long*>(st + S::x + (u * TS + 16 * m + r) * 32 + 8 * c);
+          const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + (u * TS + 16 * m + 4 * c) * 4);
           const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
           const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero4, 0, 0, 0);
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (m == 0 || i < lim1) put(u, 16 * m + 4 * c + i, {(float)d[i], dw * dx[i]});
+            if (m == 0 || i < lim1) {
+              const float e0 = (float)d[i], e1 = dw * dx[i];
+              if (m == 0 || i < live1) put(u, 16 * m + 4 * c + i, {e0, e1});
+            }
         }
       }
     } else if constexpr (TYPE == kQ6_K) {
@@ -664,30 +724,32 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
         const float dsc0 = dd * (float)(int8_t)(scw & 0xFF), dsc1 = dd * (float)(int8_t)(scw >> 8);
 #pragma unroll
         for (int m = 0; m < NTT; ++m) {
-          const long a = *reinterpret_cast<const long*>(st + S::x + ((u * NTT + m) * 16 + r) * 32 + 8 * c);
-          const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + ((u * NTT + m) * 16 + 4 * c) * 4);
+          const long a = *reinterpret_cast<const long*>(st + S::x + (u * TS + 16 * m + r) * 32 + 8 * c);
+          const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + (u * TS + 16 * m + 4 * c) * 4);
           const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
           const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b0, zero4, 0, 0, 0);
           const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, zero4, 0, 0, 0);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             if (m > 0 && i >= lim1) continue;
-            if constexpr (WIDE)
-              put(u, 16 * m + 4 * c + i, {fma_((float)d1[i], dsc1, (float)d0[i] * dsc0), dx[i]});
-            else
-              put(u, 16 * m + 4 * c + i, {(float)d0[i], dsc0 * dx[i], (float)d1[i], dsc1 * dx[i]});
+            if constexpr (WIDE) {
+              const float e0 = fma_((float)d1[i], dsc1, (float)d0[i] * dsc0);
+              if (m == 0 || i < live1) put(u, 16 * m + 4 * c + i, {e0, dx[i]});
+            } else {
+              const float e0 = (float)d0[i], e1 = dsc0 * dx[i], e2 = (float)d1[i], e3 = dsc1 * dx[i];
+              if (m == 0 || i < live1) put(u, 16 * m + 4 * c + i, {e0, e1, e2, e3});
+            }
           }
         }
       }
     } else {  // Q4_K: the wave's units UPW w .. (64-weight chunk u / 2: even units low nibbles, odd high)
       {  // dx (s0 + s1) of the wave's units' tokens, once per (unit, token)
-        constexpr int TOKS = 16 * NTT;
 #pragma unroll
-        for (int k = 0; k < (UPW * TOKS + 63) / 64; ++k) {
+        for (int k = 0; k < (UPW * TS + 63) / 64; ++k) {
           const int idx = lane + 64 * k;
-          if (idx < UPW * TOKS) {
-            const int u = UPW * wu + idx / TOKS, tok = idx % TOKS;
-            const int at = (u * NTT + tok / 16) * 16 + tok % 16;
+          if (idx < UPW * TS) {
+            const int u = UPW * wu + idx / TS, tok = idx % TS;
+            const int at = u * TS + tok;
             const uint32_t sx = *reinterpret_cast<const uint32_t*>(st + S::xs + at * 4);
             const float dxv = *reinterpret_cast<const float*>(st + S::dx + at * 4);
             xs_t[tok * kUnits + u] = dxv * (float)((int)(int16_t)(sx & 0xFFFF) + (int)(int16_t)(sx >> 16));
@@ -709,13 +771,16 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
         if (c == 0) nmn_t[r * kUnits + u] = -(dmin * (float)mn);
 #pragma unroll
         for (int m = 0; m < NTT; ++m) {
-          const long a = *reinterpret_cast<const long*>(st + S::x + ((u * NTT + m) * 16 + r) * 32 + 8 * c);
-          const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + ((u * NTT + m) * 16 + 4 * c) * 4);
+          const long a = *reinterpret_cast<const long*>(st + S::x + (u * TS + 16 * m + r) * 32 + 8 * c);
+          const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + (u * TS + 16 * m + 4 * c) * 4);
           const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
           const v4i dq = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq, zero4, 0, 0, 0);
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (m == 0 || i < lim1) put(u, 16 * m + 4 * c + i, {(float)dq[i], fsc * dx[i]});
+            if (m == 0 || i < lim1) {
+              const float e0 = (float)dq[i], e1 = fsc * dx[i];
+              if (m == 0 || i < live1) put(u, 16 * m + 4 * c + i, {e0, e1});
+            }
         }
       }
     }
@@ -758,21 +823,22 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
   }
 }
 
-template <int TYPE, bool WIDE, int NTT, int NS, int KW, bool PAIR>
+template <int TYPE, bool WIDE, int NTT, int NS, int KW, bool PAIR, int TS>
 void launch_ks_ns(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
                   int64_t ys, bool accumulate) {
-  using S = KsLds<TYPE, WIDE, NTT, KW>;
+  using S = KsLds<TYPE, WIDE, NTT, KW, TS>;
   const size_t lds = NS * (size_t)S::bytes + S::terms;
   static bool attr = false;
   if (!attr) {
-    check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_mmv_ks<TYPE, WIDE, NTT, NS, KW, PAIR>),
+    check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_mmv_ks<TYPE, WIDE, NTT, NS, KW, PAIR, TS>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
           "hipFuncSetAttribute");
     attr = true;
   }
   const int tiles = (n + 16 * NTT - 1) / (16 * NTT);
-  hipLaunchKernelGGL((k_mmv_ks<TYPE, WIDE, NTT, NS, KW, PAIR>), dim3((unsigned)(rows / 16), (unsigned)tiles), dim3(64 * KW),
-                     lds, s, static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0);
+  require(TS == 16 * NTT || (tiles == 1 && n <= TS), "mmv_ks: more tokens than token slots");
+  hipLaunchKernelGGL((k_mmv_ks<TYPE, WIDE, NTT, NS, KW, PAIR, TS>), dim3((unsigned)(rows / 16), (unsigned)tiles),
+                     dim3(64 * KW), lds, s, static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0);
 }
 
 // Waves per 16-row tile of the K-split kernel, measured on MI355X: eight (one unit per wave and stage) for two token
@@ -784,33 +850,35 @@ constexpr int ks_waves() { return PAIR ? 4 : NTT == 2 || TYPE == kQ8_0 ? 8 : 4; 
 
 // Ring depth: the deepest ring that fits one workgroup per CU when the grid fits the GPU once, else one that lets
 // two workgroups share a CU (80 KB each).
-template <int TYPE, bool WIDE, int NTT, bool PAIR>
+template <int TYPE, bool WIDE, int NTT, bool PAIR, int TS>
 void launch_ks_ntt(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
                    int64_t ys, bool accumulate) {
   constexpr int KW = ks_waves<TYPE, NTT, PAIR>();
-  using S = KsLds<TYPE, WIDE, NTT, KW>;
+  using S = KsLds<TYPE, WIDE, NTT, KW, TS>;
   const int64_t wgs = rows / 16 * ((n + 16 * NTT - 1) / (16 * NTT)), cus = device_cus();
   constexpr int kDeep = (150 * 1024 - S::terms) / S::bytes >= 8 ? 8 : (150 * 1024 - S::terms) / S::bytes;
   constexpr int kTwo = (80 * 1024 - S::terms) / S::bytes;
   static_assert(kDeep >= 3, "the K-split ring needs three stages");
   if constexpr (kTwo >= 3) {
     if (wgs > cus) {
-      launch_ks_ns<TYPE, WIDE, NTT, (kTwo > 6 ? 6 : kTwo), KW, PAIR>(s, w, rows, cols, x, n, y, ys, accumulate);
+      launch_ks_ns<TYPE, WIDE, NTT, (kTwo > 6 ? 6 : kTwo), KW, PAIR, TS>(s, w, rows, cols, x, n, y, ys, accumulate);
       return;
     }
   }
-  launch_ks_ns<TYPE, WIDE, NTT, kDeep, KW, PAIR>(s, w, rows, cols, x, n, y, ys, accumulate);
+  launch_ks_ns<TYPE, WIDE, NTT, kDeep, KW, PAIR, TS>(s, w, rows, cols, x, n, y, ys, accumulate);
 }
 
 template <int TYPE, bool WIDE>
 void launch_ks(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
                int64_t ys, bool accumulate) {
   if (n <= 8)
-    launch_ks_ntt<TYPE, WIDE, 1, true>(s, w, rows, cols, x, n, y, ys, accumulate);
+    launch_ks_ntt<TYPE, WIDE, 1, true, 16>(s, w, rows, cols, x, n, y, ys, accumulate);
   else if (n <= 16)
-    launch_ks_ntt<TYPE, WIDE, 1, false>(s, w, rows, cols, x, n, y, ys, accumulate);
+    launch_ks_ntt<TYPE, WIDE, 1, false, 16>(s, w, rows, cols, x, n, y, ys, accumulate);
+  else if (n <= 20)
+    launch_ks_ntt<TYPE, WIDE, 2, false, 20>(s, w, rows, cols, x, n, y, ys, accumulate);
   else
-    launch_ks_ntt<TYPE, WIDE, 2, false>(s, w, rows, cols, x, n, y, ys, accumulate);
+    launch_ks_ntt<TYPE, WIDE, 2, false, 32>(s, w, rows, cols, x, n, y, ys, accumulate);
 }
 
 template <int TYPE, bool WIDE, int NTT, int NS>

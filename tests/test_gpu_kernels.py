@@ -263,6 +263,9 @@ SHORT = [
     (mk_.Q4_K, 3, 8224, 512), (mk_.Q4_K, 4, 8224, 256), (mk_.Q8_0, 3, 24576, 256),  # 3-4 tokens on many rows
     (mk_.Q6_K, 5, 96, 512), (mk_.Q8_0, 8, 4096, 1024), (mk_.Q4_K, 6, 2048, 2048),  # up to 8 tokens: two units a tile
     (mk_.Q6_K, 17, 16384, 512), (mk_.Q4_K, 17, 16384, 256),   # K-quant GEMM at 17 tokens: padding elements skipped
+    # K split, two token tiles in 20 token slots (17..20 tokens): every count, both grid shapes; 21 tokens: 32 slots
+    (mk_.Q6_K, 18, 2048, 512), (mk_.Q6_K, 19, 4096, 256), (mk_.Q6_K, 20, 96, 1024), (mk_.Q6_K, 21, 160, 512),
+    (mk_.Q8_0, 20, 160, 512), (mk_.Q8_0, 19, 4096, 256), (mk_.Q8_0, 17, 5120, 512),
 ]
 
 
