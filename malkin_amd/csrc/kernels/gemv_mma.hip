@@ -341,16 +341,13 @@ struct KsLds {
   // a three-stage ring in 80 KB each.
   static constexpr bool db = (80 * 1024 - 2 * terms1) / bytes >= 3;
   static constexpr int terms = (db ? 2 : 1) * terms1;
-  // One token tile: X in 4 pieces of 1 KB per stage, xp per wave (KW waves); loads per wave per stage: W, S, (D), X,
-  // DX, (XS), pieces past a wave's share repeating another wave's copy.
-  static constexpr int xp = (4 * NTT + KW - 1) / KW;
-  // Two token tiles: the stage is a list of pieces, 1 KB ones (W, then X) and 256-byte ones (S, D, DX, XS), and
-  // wave w copies pieces w, w + KW, ... (lpw of them, the last piece repeated past the end).
+  // The stage's copies are a list of pieces, 1 KB ones (W, then X) and 256-byte ones (S, D, DX, XS); wave w copies
+  // pieces w, w + KW, ... (loads of them per stage, the last piece repeated past the end of the list).
   static constexpr int n_x4 = w_bytes / 1024 + kUnits * TS * 32 / 1024;
   static constexpr int n_dw = 1 + (TYPE == kQ6_K ? 1 : 0) + dx_bytes / 256 * (TYPE == kQ4_K ? 2 : 1);
-  static constexpr int lpw = (n_x4 + n_dw + KW - 1) / KW;
-  static constexpr int loads = NTT == 2 ? lpw : 1 + 1 + (TYPE == kQ6_K ? 1 : 0) + xp + 1 + (TYPE == kQ4_K ? 1 : 0);
+  static constexpr int loads = (n_x4 + n_dw + KW - 1) / KW;
   static_assert(kUnits * TS * 32 % 1024 == 0, "X in whole 1 KB pieces");
+  static_assert(w_bytes / 1024 <= KW, "every W piece in a wave's first slot");
 };
 
 // KW waves per workgroup (4 or 8): each wave computes the dots and terms of 8 / KW of a stage's 8 units.
@@ -364,7 +361,7 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
                                                      int n, float* __restrict__ y, int64_t ys, int accumulate) {
   using S = KsLds<TYPE, WIDE, NTT, KW, TS>;
   static_assert(!PAIR || (NTT == 1 && kUnits / KW % 2 == 0), "pairs: one token tile, an even number of units per wave");
-  static_assert(NTT == 2 ? TS > 16 && TS <= 32 && TS % 4 == 0 : TS == 16, "token slots");
+  static_assert(NTT == 2 ? TS > 16 && TS <= 32 && TS % 4 == 0 : TS == (PAIR ? 8 : 16), "token slots");
   constexpr int E = Ks<TYPE, WIDE>::E;
   constexpr int UPW = kUnits / KW;                  // units per wave and stage
   constexpr int CT = 4 * KW;                        // token rows of the chain threads (16 rows x CT tokens)
@@ -381,13 +378,11 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
   const int nst = nq8 / kUnits;
   const int64_t g0 = (int64_t)rt * 2;               // first 8-row group
 
-  // Copies (one token tile). W: 1 KB pieces, wave w takes piece min(w, pieces - 1); S, D: one 256-byte piece, every
-  // wave; X: xp 1 KB pieces per wave (piece min(xp w + k, 4 NTT - 1)); DX, XS: 256-byte pieces, wave w takes piece
-  // w % (2 NTT). Two token tiles: the piece list of KsLds.
+  // Copies: the piece list of KsLds. Source offset of the activation bytes this lane copies into X byte p (1 KB
+  // pieces: 16 bytes a lane) or DX / XS byte p (256-byte pieces: 4 bytes a lane); slots of padding tokens copy the last
+  // token's bytes.
   constexpr int WP = S::w_bytes / 1024;
   const uint8_t* xb = reinterpret_cast<const uint8_t*>(x + (int64_t)t0 * nq8);
-  // Source offset of the activation byte copied by this lane into X byte p (1 KB pieces: 16 bytes a lane) or DX / XS
-  // byte p (256-byte pieces: 4 bytes a lane). Slots of padding tokens copy the last token's bytes.
   auto x_src = [&](int p) __attribute__((always_inline)) {
     const int unit = p / (TS * 32), rem = p % (TS * 32);
     const int tok = min(rem / 32, ntok - 1), half = (rem % 32) / 16;
@@ -397,15 +392,6 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
     const int unit = min(p / (TS * 4), kUnits - 1), tok = min((p % (TS * 4)) / 4, ntok - 1);
     return (uint32_t)((tok * nq8 + unit) * 40);
   };
-  uint32_t x_off[S::xp], dx_off;
-  int x_pc[S::xp];
-#pragma unroll
-  for (int k = 0; k < S::xp; ++k) {
-    x_pc[k] = min(S::xp * wu + k, 4 * NTT - 1);
-    x_off[k] = x_src(1024 * x_pc[k] + 16 * lane);
-  }
-  const int dxp = wu % (2 * NTT);
-  dx_off = dx_src(256 * dxp + 4 * lane);
   const int wp = min(wu, WP - 1);
   const uint8_t *wq, *ws, *wd = nullptr;
   uint32_t w_off, s_off, d_off = 0;
@@ -445,16 +431,16 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
     ws_step = 128;
   }
 
-  // Two token tiles: slot j of this wave copies piece min(KW j + w, pieces - 1) of every stage (source sl_src + stage
-  // sl_step, LDS offset sl_dst in the stage buffer, 16 or 4 bytes a lane). W pieces are the first WP < KW, so only
-  // slot 0 of waves below WP holds one, the wave's own piece wp.
-  const uint8_t* sl_src[S::lpw];
-  int64_t sl_step[S::lpw];
-  uint32_t sl_dst[S::lpw];
-  bool sl_x4[S::lpw];
-  if constexpr (NTT == 2) {
+  // Slot j of this wave copies piece min(KW j + w, pieces - 1) of every stage (source sl_src + stage sl_step, LDS
+  // offset sl_dst in the stage buffer, 16 or 4 bytes a lane). W pieces are the first WP <= KW, so only slot 0 of waves
+  // below WP holds one, the wave's own piece wp.
+  const uint8_t* sl_src[S::loads];
+  int64_t sl_step[S::loads];
+  uint32_t sl_dst[S::loads];
+  bool sl_x4[S::loads];
+  {
 #pragma unroll
-    for (int j = 0; j < S::lpw; ++j) {
+    for (int j = 0; j < S::loads; ++j) {
       const int p = min(KW * j + wu, S::n_x4 + S::n_dw - 1);
       sl_x4[j] = p < S::n_x4;
       if (p < WP) {
@@ -477,24 +463,13 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
 
   auto issue = [&]<int BUF>(int sn) __attribute__((always_inline)) {
     uint8_t* st = smem + BUF * S::bytes;
-    if constexpr (NTT == 2) {
 #pragma unroll
-      for (int j = 0; j < S::lpw; ++j) {
-        if (sl_x4[j])
-          ld16(sl_src[j] + sn * sl_step[j], st + sl_dst[j]);
-        else
-          ld4(sl_src[j] + sn * sl_step[j], st + sl_dst[j]);
-      }
-      return;
+    for (int j = 0; j < S::loads; ++j) {
+      if (sl_x4[j])
+        ld16(sl_src[j] + sn * sl_step[j], st + sl_dst[j]);
+      else
+        ld4(sl_src[j] + sn * sl_step[j], st + sl_dst[j]);
     }
-    ld16(wq + (size_t)sn * wq_step + w_off, st + 1024 * wp);
-    ld4(ws + (size_t)sn * ws_step + s_off, st + S::s_off);
-    if constexpr (TYPE == kQ6_K) ld4(wd + (size_t)sn * 16 + d_off, st + S::d_off);
-    const uint8_t* xs = xb + (size_t)sn * kUnits * 40;
-#pragma unroll
-    for (int k = 0; k < S::xp; ++k) ld16(xs + x_off[k], st + S::x + 1024 * x_pc[k]);
-    ld4(xs + dx_off, st + S::dx + 256 * dxp);
-    if constexpr (TYPE == kQ4_K) ld4(xs + dx_off + 4, st + S::xs + 256 * dxp);
   };
 
   // MFMA lane roles: row r = lane % 16 (group gi = r / 8, row rr = r % 8), weight quarter c = lane / 16, result
@@ -649,10 +624,10 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
       } else {  // Q4_K: the wave's pairs are whole 64-weight chunks (even unit: low nibbles, odd: high)
         {  // dx (s0 + s1) of the wave's units' tokens, once per (unit, token)
 #pragma unroll
-          for (int k = 0; k < (UPW * 16 + 63) / 64; ++k) {
+          for (int k = 0; k < (UPW * TS + 63) / 64; ++k) {
             const int idx = lane + 64 * k;
-            if (idx < UPW * 16) {
-              const int u = UPW * wu + idx / 16, tok = idx % 16;
+            if (idx < UPW * TS) {
+              const int u = UPW * wu + idx / TS, tok = idx % TS;
               const int at = u * TS + tok;
               const uint32_t sx = *reinterpret_cast<const uint32_t*>(st + S::xs + at * 4);
               const float dxv = *reinterpret_cast<const float*>(st + S::dx + at * 4);
@@ -836,7 +811,7 @@ void launch_ks_ns(hipStream_t s, const void* w, int64_t rows, int64_t cols, cons
     attr = true;
   }
   const int tiles = (n + 16 * NTT - 1) / (16 * NTT);
-  require(TS == 16 * NTT || (tiles == 1 && n <= TS), "mmv_ks: more tokens than token slots");
+  require(n <= TS || TS == 16 * NTT, "mmv_ks: more tokens than token slots");
   hipLaunchKernelGGL((k_mmv_ks<TYPE, WIDE, NTT, NS, KW, PAIR, TS>), dim3((unsigned)(rows / 16), (unsigned)tiles),
                      dim3(64 * KW), lds, s, static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0);
 }
@@ -872,7 +847,7 @@ template <int TYPE, bool WIDE>
 void launch_ks(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
                int64_t ys, bool accumulate) {
   if (n <= 8)
-    launch_ks_ntt<TYPE, WIDE, 1, true, 16>(s, w, rows, cols, x, n, y, ys, accumulate);
+    launch_ks_ntt<TYPE, WIDE, 1, true, 8>(s, w, rows, cols, x, n, y, ys, accumulate);
   else if (n <= 16)
     launch_ks_ntt<TYPE, WIDE, 1, false, 16>(s, w, rows, cols, x, n, y, ys, accumulate);
   else if (n <= 20)
