@@ -327,7 +327,7 @@ struct Ks {
 };
 // TS: token slots per unit in X, DX, XS and the terms (16 NTT, or 20 for two token tiles holding at most 20 tokens,
 // the tree verification batch: rows of padding tokens are neither copied nor stored).
-template <int TYPE, bool WIDE, int NTT, int KW, int TS>
+template <int TYPE, bool WIDE, int NTT, int KW, int TS, int CW>
 struct KsLds {
   static constexpr int w_bytes = TYPE == kQ8_0 ? 2 * 8 * 256 : TYPE == kQ6_K ? 2 * 1536 : 2 * 1024;
   static constexpr int s_off = w_bytes, d_off = w_bytes + 256;
@@ -339,7 +339,7 @@ struct KsLds {
   static constexpr int terms1 = kUnits * TS * 16 * Ks<TYPE, WIDE>::E * 4;   // one stage's terms
   // Double-buffered (stage s's terms written while stage s - 1's chains run) where two workgroups per CU still get
   // a three-stage ring in 80 KB each.
-  static constexpr bool db = (80 * 1024 - 2 * terms1) / bytes >= 3;
+  static constexpr bool db = CW > 0 || (80 * 1024 - 2 * terms1) / bytes >= 3;
   static constexpr int terms = (db ? 2 : 1) * terms1;
   // The stage's copies are a list of pieces, 1 KB ones (W, then X) and 256-byte ones (S, D, DX, XS); wave w copies
   // pieces w, w + KW, ... (loads of them per stage, the last piece repeated past the end of the list).
@@ -356,16 +356,17 @@ struct KsLds {
 // 0..7 (zero elsewhere) against unit u's weights, the second accumulates unit u + 1's activations in rows 8..15
 // against unit u + 1's weights, so result element i of lane quarter c is (unit u + c / 2, token 4 (c % 2) + i):
 // exact int dots of both units, and no epilogue work for padding token columns.
-template <int TYPE, bool WIDE, int NTT, int NS, int KW, bool PAIR, int TS>
-__global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t rows, int64_t cols, const BlockQ8* x,
-                                                     int n, float* __restrict__ y, int64_t ys, int accumulate) {
-  using S = KsLds<TYPE, WIDE, NTT, KW, TS>;
+template <int TYPE, bool WIDE, int NTT, int NS, int KW, bool PAIR, int TS, int CW>
+__global__ __launch_bounds__(64 * (KW + CW)) void k_mmv_ks(const uint8_t* W, int64_t rows, int64_t cols,
+                                                            const BlockQ8* x, int n, float* __restrict__ y,
+                                                            int64_t ys, int accumulate) {
+  using S = KsLds<TYPE, WIDE, NTT, KW, TS, CW>;
   static_assert(!PAIR || (NTT == 1 && kUnits / KW % 2 == 0), "pairs: one token tile, an even number of units per wave");
   static_assert(NTT == 2 ? TS > 16 && TS <= 32 && TS % 4 == 0 : TS == (PAIR ? 8 : 16), "token slots");
   constexpr int E = Ks<TYPE, WIDE>::E;
   constexpr int UPW = kUnits / KW;                  // units per wave and stage
-  constexpr int CT = 4 * KW;                        // token rows of the chain threads (16 rows x CT tokens)
-  constexpr int CPT = (16 * NTT + CT - 1) / CT;     // chains per thread
+  constexpr int CT = 4 * (CW ? CW : KW);            // token rows of the chain threads (16 rows x CT tokens)
+  constexpr int CPT = (TS + CT - 1) / CT;           // chains per thread
   static_assert((NS - 1) * S::loads < 64, "the ring's loads must fit the vmcnt counter");
   extern __shared__ __align__(16) uint8_t smem[];
   float* terms_base = reinterpret_cast<float*>(smem + NS * S::bytes);  // [2][unit][token][row][E]
@@ -475,7 +476,11 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
   // MFMA lane roles: row r = lane % 16 (group gi = r / 8, row rr = r % 8), weight quarter c = lane / 16, result
   // elements i: tokens 4 c + i (+ 16 m). Chain role: row cr = tid % 16, tokens ct + CT m (those below 16 NTT).
   const int r = lane & 15, c = lane >> 4, gi = r >> 3, rr = r & 7;
-  const int cr = tid & 15, ct = tid >> 4;
+  // CW > 0: waves KW .. KW + CW - 1 run only the chains (of the previous stage, while waves 0 .. KW - 1 copy and
+  // form the terms of this one); CW = 0: every wave does both, one after the other.
+  const bool doter = CW == 0 || wu < KW, chainer = CW == 0 || wu >= KW;
+  const int ctid = CW ? tid - 64 * KW : tid;
+  const int cr = ctid & 15, ct = ctid >> 4;
   // Result element i of the second token tile holds token 16 + 4 c + i: elements i >= lim1 are padding in every lane
   // (wave-uniform, skipped), and in this lane quarter elements i >= live1; padding terms are neither stored nor read
   // (17 tokens, the tree verification batch: only element 0 of lane quarter 0).
@@ -520,7 +525,7 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
 #pragma unroll
     for (int m = 0; m < CPT; ++m) {
       const int tk = ct + CT * m;
-      if (CT * CPT > 16 * NTT && tk >= 16 * NTT) break;  // wave-uniform: threads past the tile's tokens
+      if (CT * CPT > TS && tk >= TS) break;               // wave-uniform: threads past the token slots
       if (tk >= ntok) break;                              // padding token: its output is never stored
       float xsv[kUnits];
       if constexpr (TYPE == kQ4_K) {
@@ -552,76 +557,173 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
     // stage s landed everywhere; double-buffered terms: stage s - 1's are written and the chains of stage s - 2
     // (which read the buffer stage s writes) are done; single: the chains of stage s - 1 are done
     ring_barrier();
-    if (s + NS - 1 < nst) issue.template operator()<(BUF + NS - 1) % NS>(s + NS - 1);
+    if (doter && s + NS - 1 < nst) issue.template operator()<(BUF + NS - 1) % NS>(s + NS - 1);
     const uint8_t* st = smem + BUF * S::bytes;
-    select(s);
-    if constexpr (PAIR) {
-      // Lane (r, c): MFMA operand rows r (token r % 8 of unit u, or of u + 1), result unit u + ph, tokens 4 pt + i.
-      const int ph = c >> 1, pt = c & 1;
-      const bool lo = r < 8;
-      auto xa = [&](int u) __attribute__((always_inline)) {  // operand bytes of token r % 8 of unit u
-        return *reinterpret_cast<const long*>(st + S::x + (u * TS + (r & 7)) * 32 + 8 * c);
-      };
-      auto dxs = [&](int u0) __attribute__((always_inline)) {  // dx of this lane's result tokens
-        return *reinterpret_cast<const float4*>(st + S::dx + ((u0 + ph) * TS + 4 * pt) * 4);
-      };
-      if constexpr (TYPE == kQ8_0) {
+    if (doter) {
+      select(s);
+      if constexpr (PAIR) {
+        // Lane (r, c): MFMA operand rows r (token r % 8 of unit u, or of u + 1), result unit u + ph, tokens 4 pt + i.
+        const int ph = c >> 1, pt = c & 1;
+        const bool lo = r < 8;
+        auto xa = [&](int u) __attribute__((always_inline)) {  // operand bytes of token r % 8 of unit u
+          return *reinterpret_cast<const long*>(st + S::x + (u * TS + (r & 7)) * 32 + 8 * c);
+        };
+        auto dxs = [&](int u0) __attribute__((always_inline)) {  // dx of this lane's result tokens
+          return *reinterpret_cast<const float4*>(st + S::dx + ((u0 + ph) * TS + 4 * pt) * 4);
+        };
+        if constexpr (TYPE == kQ8_0) {
 #pragma unroll
-        for (int k = 0; k < UPW; k += 2) {
-          const int u0 = UPW * wu + k;
-          long bw[2];
-          float dw[2];
+          for (int k = 0; k < UPW; k += 2) {
+            const int u0 = UPW * wu + k;
+            long bw[2];
+            float dw[2];
 #pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            bw[e] = *reinterpret_cast<const long*>(st + gi * 2048 + (u0 + e) * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
-            dw[e] = half_to_float(*reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + (u0 + e) * 16 + rr * 2));
+            for (int e = 0; e < 2; ++e) {
+              bw[e] = *reinterpret_cast<const long*>(st + gi * 2048 + (u0 + e) * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
+              dw[e] = half_to_float(*reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + (u0 + e) * 16 + rr * 2));
+            }
+            const long a0 = lo ? xa(u0) : 0, a1 = lo ? 0 : xa(u0 + 1);
+            const float4 dx4 = dxs(u0);
+            const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+            const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bw[1], __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bw[0], zero4, 0, 0, 0), 0, 0, 0);
+            const float dwl = ph ? dw[1] : dw[0];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) put(u0 + ph, 4 * pt + i, {(float)d[i], dwl * dx[i]});
           }
-          const long a0 = lo ? xa(u0) : 0, a1 = lo ? 0 : xa(u0 + 1);
-          const float4 dx4 = dxs(u0);
-          const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
-          const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bw[1], __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bw[0], zero4, 0, 0, 0), 0, 0, 0);
-          const float dwl = ph ? dw[1] : dw[0];
+        } else if constexpr (TYPE == kQ6_K) {
+          const float dd = half_to_float(*reinterpret_cast<const uint16_t*>(st + S::d_off + gi * 16 + rr * 2));
+          const int hw = c >> 1, h = c & 1;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) put(u0 + ph, 4 * pt + i, {(float)d[i], dwl * dx[i]});
+          for (int k = 0; k < UPW; k += 2) {
+            const int u0 = UPW * wu + k;
+            long bl[2], bh[2];
+            float s0[2], s1[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const uint8_t* au = st + gi * 1536 + (u0 + e) * 192;
+              const uint2 nib = *reinterpret_cast<const uint2*>(au + rr * 16 + 8 * h);
+              const uint2 hb = *reinterpret_cast<const uint2*>(au + 128 + rr * 8);
+              const uint32_t hv = (hw ? hb.y : hb.x) >> (4 * h);
+              const uint32_t q0 = ((nib.x >> (4 * hw)) & 0x0F0F0F0Fu) | ((hv & 0x03030303u) << 4);
+              const uint32_t q1 = ((nib.y >> (4 * hw)) & 0x0F0F0F0Fu) | (((hv >> 2) & 0x03030303u) << 4);
+              const long bq = (long)(((uint64_t)minus32(q1) << 32) | minus32(q0));
+              bl[e] = hw ? 0 : bq;
+              bh[e] = hw ? bq : 0;
+              const uint32_t scw = *reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + rr * 16 + 2 * (u0 + e));
+              s0[e] = dd * (float)(int8_t)(scw & 0xFF);
+              s1[e] = dd * (float)(int8_t)(scw >> 8);
+            }
+            const long a0 = lo ? xa(u0) : 0, a1 = lo ? 0 : xa(u0 + 1);
+            const float4 dx4 = dxs(u0);
+            const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+            const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bl[1], __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bl[0], zero4, 0, 0, 0), 0, 0, 0);
+            const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bh[1], __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bh[0], zero4, 0, 0, 0), 0, 0, 0);
+            const float dsc0 = ph ? s0[1] : s0[0], dsc1 = ph ? s1[1] : s1[0];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              if constexpr (WIDE)
+                put(u0 + ph, 4 * pt + i, {fma_((float)d1[i], dsc1, (float)d0[i] * dsc0), dx[i]});
+              else
+                put(u0 + ph, 4 * pt + i, {(float)d0[i], dsc0 * dx[i], (float)d1[i], dsc1 * dx[i]});
+            }
+          }
+        } else {  // Q4_K: the wave's pairs are whole 64-weight chunks (even unit: low nibbles, odd: high)
+          {  // dx (s0 + s1) of the wave's units' tokens, once per (unit, token)
+#pragma unroll
+            for (int k = 0; k < (UPW * TS + 63) / 64; ++k) {
+              const int idx = lane + 64 * k;
+              if (idx < UPW * TS) {
+                const int u = UPW * wu + idx / TS, tok = idx % TS;
+                const int at = u * TS + tok;
+                const uint32_t sx = *reinterpret_cast<const uint32_t*>(st + S::xs + at * 4);
+                const float dxv = *reinterpret_cast<const float*>(st + S::dx + at * 4);
+                xs_t[tok * kUnits + u] = dxv * (float)((int)(int16_t)(sx & 0xFFFF) + (int)(int16_t)(sx >> 16));
+              }
+            }
+          }
+          const uint4 hd = *reinterpret_cast<const uint4*>(st + S::s_off + gi * 128 + rr * 16);
+          const float d = half_to_float((uint16_t)(hd.x & 0xFFFF)), dmin = half_to_float((uint16_t)(hd.x >> 16));
+#pragma unroll
+          for (int k = 0; k < UPW; k += 2) {
+            const int u0 = UPW * wu + k, j2 = u0 / 2;
+            const uint2 raw =
+                *reinterpret_cast<const uint2*>(st + gi * 1024 + j2 * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
+            long bq[2];
+            float fsc[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              bq[e] = (long)(((uint64_t)((raw.y >> (4 * e)) & 0x0F0F0F0Fu) << 32) | ((raw.x >> (4 * e)) & 0x0F0F0F0Fu));
+              int sc, mn;
+              scale_min(u0 + e, hd.y, hd.z, hd.w, sc, mn);
+              fsc[e] = d * (float)sc;
+              if (c == 0) nmn_t[r * kUnits + u0 + e] = -(dmin * (float)mn);
+            }
+            const long a0 = lo ? xa(u0) : 0, a1 = lo ? 0 : xa(u0 + 1);
+            const float4 dx4 = dxs(u0);
+            const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+            const v4i dq = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bq[1], __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bq[0], zero4, 0, 0, 0), 0, 0, 0);
+            const float fs = ph ? fsc[1] : fsc[0];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) put(u0 + ph, 4 * pt + i, {(float)dq[i], fs * dx[i]});
+          }
+        }
+      } else if constexpr (TYPE == kQ8_0) {
+#pragma unroll
+        for (int k = 0; k < UPW; ++k) {
+          const int u = UPW * wu + k;
+          const long b = *reinterpret_cast<const long*>(st + gi * 2048 + u * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
+          const float dw = half_to_float(*reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + u * 16 + rr * 2));
+#pragma unroll
+          for (int m = 0; m < NTT; ++m) {
+            const long a = *reinterpret_cast<const long*>(st + S::x + (u * TS + 16 * m + r) * 32 + 8 * c);
+            const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + (u * TS + 16 * m + 4 * c) * 4);
+            const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+            const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero4, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (m == 0 || i < lim1) {
+                const float e0 = (float)d[i], e1 = dw * dx[i];
+                if (m == 0 || i < live1) put(u, 16 * m + 4 * c + i, {e0, e1});
+              }
+          }
         }
       } else if constexpr (TYPE == kQ6_K) {
         const float dd = half_to_float(*reinterpret_cast<const uint16_t*>(st + S::d_off + gi * 16 + rr * 2));
         const int hw = c >> 1, h = c & 1;
 #pragma unroll
-        for (int k = 0; k < UPW; k += 2) {
-          const int u0 = UPW * wu + k;
-          long bl[2], bh[2];
-          float s0[2], s1[2];
+        for (int k = 0; k < UPW; ++k) {
+          const int u = UPW * wu + k;
+          const uint8_t* au = st + gi * 1536 + u * 192;
+          const uint2 nib = *reinterpret_cast<const uint2*>(au + rr * 16 + 8 * h);
+          const uint2 hb = *reinterpret_cast<const uint2*>(au + 128 + rr * 8);
+          const uint32_t hv = (hw ? hb.y : hb.x) >> (4 * h);
+          const uint32_t q0 = ((nib.x >> (4 * hw)) & 0x0F0F0F0Fu) | ((hv & 0x03030303u) << 4);
+          const uint32_t q1 = ((nib.y >> (4 * hw)) & 0x0F0F0F0Fu) | (((hv >> 2) & 0x03030303u) << 4);
+          const long bq = (long)(((uint64_t)minus32(q1) << 32) | minus32(q0));
+          const long b0 = hw ? 0 : bq, b1 = hw ? bq : 0;
+          const uint32_t scw = *reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + rr * 16 + 2 * u);
+          const float dsc0 = dd * (float)(int8_t)(scw & 0xFF), dsc1 = dd * (float)(int8_t)(scw >> 8);
 #pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            const uint8_t* au = st + gi * 1536 + (u0 + e) * 192;
-            const uint2 nib = *reinterpret_cast<const uint2*>(au + rr * 16 + 8 * h);
-            const uint2 hb = *reinterpret_cast<const uint2*>(au + 128 + rr * 8);
-            const uint32_t hv = (hw ? hb.y : hb.x) >> (4 * h);
-            const uint32_t q0 = ((nib.x >> (4 * hw)) & 0x0F0F0F0Fu) | ((hv & 0x03030303u) << 4);
-            const uint32_t q1 = ((nib.y >> (4 * hw)) & 0x0F0F0F0Fu) | (((hv >> 2) & 0x03030303u) << 4);
-            const long bq = (long)(((uint64_t)minus32(q1) << 32) | minus32(q0));
-            bl[e] = hw ? 0 : bq;
-            bh[e] = hw ? bq : 0;
-            const uint32_t scw = *reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + rr * 16 + 2 * (u0 + e));
-            s0[e] = dd * (float)(int8_t)(scw & 0xFF);
-            s1[e] = dd * (float)(int8_t)(scw >> 8);
-          }
-          const long a0 = lo ? xa(u0) : 0, a1 = lo ? 0 : xa(u0 + 1);
-          const float4 dx4 = dxs(u0);
-          const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
-          const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bl[1], __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bl[0], zero4, 0, 0, 0), 0, 0, 0);
-          const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bh[1], __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bh[0], zero4, 0, 0, 0), 0, 0, 0);
-          const float dsc0 = ph ? s0[1] : s0[0], dsc1 = ph ? s1[1] : s1[0];
+          for (int m = 0; m < NTT; ++m) {
+            const long a = *reinterpret_cast<const long*>(st + S::x + (u * TS + 16 * m + r) * 32 + 8 * c);
+            const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + (u * TS + 16 * m + 4 * c) * 4);
+            const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+            const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b0, zero4, 0, 0, 0);
+            const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, zero4, 0, 0, 0);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            if constexpr (WIDE)
-              put(u0 + ph, 4 * pt + i, {fma_((float)d1[i], dsc1, (float)d0[i] * dsc0), dx[i]});
-            else
-              put(u0 + ph, 4 * pt + i, {(float)d0[i], dsc0 * dx[i], (float)d1[i], dsc1 * dx[i]});
+            for (int i = 0; i < 4; ++i) {
+              if (m > 0 && i >= lim1) continue;
+              if constexpr (WIDE) {
+                const float e0 = fma_((float)d1[i], dsc1, (float)d0[i] * dsc0);
+                if (m == 0 || i < live1) put(u, 16 * m + 4 * c + i, {e0, dx[i]});
+              } else {
+                const float e0 = (float)d0[i], e1 = dsc0 * dx[i], e2 = (float)d1[i], e3 = dsc1 * dx[i];
+                if (m == 0 || i < live1) put(u, 16 * m + 4 * c + i, {e0, e1, e2, e3});
+              }
+            }
           }
         }
-      } else {  // Q4_K: the wave's pairs are whole 64-weight chunks (even unit: low nibbles, odd: high)
+      } else {  // Q4_K: the wave's units UPW w .. (64-weight chunk u / 2: even units low nibbles, odd high)
         {  // dx (s0 + s1) of the wave's units' tokens, once per (unit, token)
 #pragma unroll
           for (int k = 0; k < (UPW * TS + 63) / 64; ++k) {
@@ -637,132 +739,37 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
         }
         const uint4 hd = *reinterpret_cast<const uint4*>(st + S::s_off + gi * 128 + rr * 16);
         const float d = half_to_float((uint16_t)(hd.x & 0xFFFF)), dmin = half_to_float((uint16_t)(hd.x >> 16));
+        const int j2 = UPW * wu / 2;  // the wave's 64-weight chunk
+        const uint2 raw =
+            *reinterpret_cast<const uint2*>(st + gi * 1024 + j2 * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
 #pragma unroll
-        for (int k = 0; k < UPW; k += 2) {
-          const int u0 = UPW * wu + k, j2 = u0 / 2;
-          const uint2 raw =
-              *reinterpret_cast<const uint2*>(st + gi * 1024 + j2 * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
-          long bq[2];
-          float fsc[2];
+        for (int k = 0; k < UPW; ++k) {
+          const int u = UPW * wu + k, e = u & 1;
+          const long bq = (long)(((uint64_t)((raw.y >> (4 * e)) & 0x0F0F0F0Fu) << 32) | ((raw.x >> (4 * e)) & 0x0F0F0F0Fu));
+          int sc, mn;
+          scale_min(u, hd.y, hd.z, hd.w, sc, mn);
+          const float fsc = d * (float)sc;
+          if (c == 0) nmn_t[r * kUnits + u] = -(dmin * (float)mn);
 #pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            bq[e] = (long)(((uint64_t)((raw.y >> (4 * e)) & 0x0F0F0F0Fu) << 32) | ((raw.x >> (4 * e)) & 0x0F0F0F0Fu));
-            int sc, mn;
-            scale_min(u0 + e, hd.y, hd.z, hd.w, sc, mn);
-            fsc[e] = d * (float)sc;
-            if (c == 0) nmn_t[r * kUnits + u0 + e] = -(dmin * (float)mn);
+          for (int m = 0; m < NTT; ++m) {
+            const long a = *reinterpret_cast<const long*>(st + S::x + (u * TS + 16 * m + r) * 32 + 8 * c);
+            const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + (u * TS + 16 * m + 4 * c) * 4);
+            const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+            const v4i dq = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq, zero4, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (m == 0 || i < lim1) {
+                const float e0 = (float)dq[i], e1 = fsc * dx[i];
+                if (m == 0 || i < live1) put(u, 16 * m + 4 * c + i, {e0, e1});
+              }
           }
-          const long a0 = lo ? xa(u0) : 0, a1 = lo ? 0 : xa(u0 + 1);
-          const float4 dx4 = dxs(u0);
-          const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
-          const v4i dq = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bq[1], __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bq[0], zero4, 0, 0, 0), 0, 0, 0);
-          const float fs = ph ? fsc[1] : fsc[0];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) put(u0 + ph, 4 * pt + i, {(float)dq[i], fs * dx[i]});
-        }
-      }
-    } else if constexpr (TYPE == kQ8_0) {
-#pragma unroll
-      for (int k = 0; k < UPW; ++k) {
-        const int u = UPW * wu + k;
-        const long b = *reinterpret_cast<const long*>(st + gi * 2048 + u * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
-        const float dw = half_to_float(*reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + u * 16 + rr * 2));
-#pragma unroll
-        for (int m = 0; m < NTT; ++m) {
-          const long a = *reinterpret_cast<const long*>(st + S::x + (u * TS + 16 * m + r) * 32 + 8 * c);
-          const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + (u * TS + 16 * m + 4 * c) * 4);
-          const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
-          const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero4, 0, 0, 0);
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (m == 0 || i < lim1) {
-              const float e0 = (float)d[i], e1 = dw * dx[i];
-              if (m == 0 || i < live1) put(u, 16 * m + 4 * c + i, {e0, e1});
-            }
-        }
-      }
-    } else if constexpr (TYPE == kQ6_K) {
-      const float dd = half_to_float(*reinterpret_cast<const uint16_t*>(st + S::d_off + gi * 16 + rr * 2));
-      const int hw = c >> 1, h = c & 1;
-#pragma unroll
-      for (int k = 0; k < UPW; ++k) {
-        const int u = UPW * wu + k;
-        const uint8_t* au = st + gi * 1536 + u * 192;
-        const uint2 nib = *reinterpret_cast<const uint2*>(au + rr * 16 + 8 * h);
-        const uint2 hb = *reinterpret_cast<const uint2*>(au + 128 + rr * 8);
-        const uint32_t hv = (hw ? hb.y : hb.x) >> (4 * h);
-        const uint32_t q0 = ((nib.x >> (4 * hw)) & 0x0F0F0F0Fu) | ((hv & 0x03030303u) << 4);
-        const uint32_t q1 = ((nib.y >> (4 * hw)) & 0x0F0F0F0Fu) | (((hv >> 2) & 0x03030303u) << 4);
-        const long bq = (long)(((uint64_t)minus32(q1) << 32) | minus32(q0));
-        const long b0 = hw ? 0 : bq, b1 = hw ? bq : 0;
-        const uint32_t scw = *reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + rr * 16 + 2 * u);
-        const float dsc0 = dd * (float)(int8_t)(scw & 0xFF), dsc1 = dd * (float)(int8_t)(scw >> 8);
-#pragma unroll
-        for (int m = 0; m < NTT; ++m) {
-          const long a = *reinterpret_cast<const long*>(st + S::x + (u * TS + 16 * m + r) * 32 + 8 * c);
-          const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + (u * TS + 16 * m + 4 * c) * 4);
-          const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
-          const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b0, zero4, 0, 0, 0);
-          const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, zero4, 0, 0, 0);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            if (m > 0 && i >= lim1) continue;
-            if constexpr (WIDE) {
-              const float e0 = fma_((float)d1[i], dsc1, (float)d0[i] * dsc0);
-              if (m == 0 || i < live1) put(u, 16 * m + 4 * c + i, {e0, dx[i]});
-            } else {
-              const float e0 = (float)d0[i], e1 = dsc0 * dx[i], e2 = (float)d1[i], e3 = dsc1 * dx[i];
-              if (m == 0 || i < live1) put(u, 16 * m + 4 * c + i, {e0, e1, e2, e3});
-            }
-          }
-        }
-      }
-    } else {  // Q4_K: the wave's units UPW w .. (64-weight chunk u / 2: even units low nibbles, odd high)
-      {  // dx (s0 + s1) of the wave's units' tokens, once per (unit, token)
-#pragma unroll
-        for (int k = 0; k < (UPW * TS + 63) / 64; ++k) {
-          const int idx = lane + 64 * k;
-          if (idx < UPW * TS) {
-            const int u = UPW * wu + idx / TS, tok = idx % TS;
-            const int at = u * TS + tok;
-            const uint32_t sx = *reinterpret_cast<const uint32_t*>(st + S::xs + at * 4);
-            const float dxv = *reinterpret_cast<const float*>(st + S::dx + at * 4);
-            xs_t[tok * kUnits + u] = dxv * (float)((int)(int16_t)(sx & 0xFFFF) + (int)(int16_t)(sx >> 16));
-          }
-        }
-      }
-      const uint4 hd = *reinterpret_cast<const uint4*>(st + S::s_off + gi * 128 + rr * 16);
-      const float d = half_to_float((uint16_t)(hd.x & 0xFFFF)), dmin = half_to_float((uint16_t)(hd.x >> 16));
-      const int j2 = UPW * wu / 2;  // the wave's 64-weight chunk
-      const uint2 raw =
-          *reinterpret_cast<const uint2*>(st + gi * 1024 + j2 * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
-#pragma unroll
-      for (int k = 0; k < UPW; ++k) {
-        const int u = UPW * wu + k, e = u & 1;
-        const long bq = (long)(((uint64_t)((raw.y >> (4 * e)) & 0x0F0F0F0Fu) << 32) | ((raw.x >> (4 * e)) & 0x0F0F0F0Fu));
-        int sc, mn;
-        scale_min(u, hd.y, hd.z, hd.w, sc, mn);
-        const float fsc = d * (float)sc;
-        if (c == 0) nmn_t[r * kUnits + u] = -(dmin * (float)mn);
-#pragma unroll
-        for (int m = 0; m < NTT; ++m) {
-          const long a = *reinterpret_cast<const long*>(st + S::x + (u * TS + 16 * m + r) * 32 + 8 * c);
-          const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + (u * TS + 16 * m + 4 * c) * 4);
-          const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
-          const v4i dq = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq, zero4, 0, 0, 0);
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (m == 0 || i < lim1) {
-              const float e0 = (float)dq[i], e1 = fsc * dx[i];
-              if (m == 0 || i < live1) put(u, 16 * m + 4 * c + i, {e0, e1});
-            }
         }
       }
     }
     if constexpr (S::db) {
       // The previous stage's terms were written before this stage's barrier: its chains run now, alongside this
       // stage's term work (the last stage's chains run after the loop).
-      if (s > 0) chain(s - 1);
+      if (chainer && s > 0) chain(s - 1);
     } else {
       // Terms written (LDS only): then every lane runs its chains over the stage's units in order.
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -784,8 +791,9 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();  // the last stage's terms are written
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-    chain(nst - 1);
+    if (chainer) chain(nst - 1);
   }
+  if (!chainer) return;
 
   const int64_t row = (int64_t)rt * 16 + cr;
 #pragma unroll
@@ -798,49 +806,56 @@ __global__ __launch_bounds__(64 * KW) void k_mmv_ks(const uint8_t* W, int64_t ro
   }
 }
 
-template <int TYPE, bool WIDE, int NTT, int NS, int KW, bool PAIR, int TS>
+template <int TYPE, bool WIDE, int NTT, int NS, int KW, bool PAIR, int TS, int CW>
 void launch_ks_ns(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
                   int64_t ys, bool accumulate) {
-  using S = KsLds<TYPE, WIDE, NTT, KW, TS>;
+  using S = KsLds<TYPE, WIDE, NTT, KW, TS, CW>;
   const size_t lds = NS * (size_t)S::bytes + S::terms;
   static bool attr = false;
   if (!attr) {
-    check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_mmv_ks<TYPE, WIDE, NTT, NS, KW, PAIR, TS>),
+    check(hipFuncSetAttribute(reinterpret_cast<const void*>(k_mmv_ks<TYPE, WIDE, NTT, NS, KW, PAIR, TS, CW>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
           "hipFuncSetAttribute");
     attr = true;
   }
   const int tiles = (n + 16 * NTT - 1) / (16 * NTT);
   require(n <= TS || TS == 16 * NTT, "mmv_ks: more tokens than token slots");
-  hipLaunchKernelGGL((k_mmv_ks<TYPE, WIDE, NTT, NS, KW, PAIR, TS>), dim3((unsigned)(rows / 16), (unsigned)tiles),
-                     dim3(64 * KW), lds, s, static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0);
+  hipLaunchKernelGGL((k_mmv_ks<TYPE, WIDE, NTT, NS, KW, PAIR, TS, CW>), dim3((unsigned)(rows / 16), (unsigned)tiles),
+                     dim3(64 * (KW + CW)), lds, s, static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0);
 }
 
-// Waves per 16-row tile of the K-split kernel, measured on MI355X: eight (one unit per wave and stage) for two token
-// tiles (17-32 tokens: Qwen3-14B Q6_K at 17 tokens, 5120 x 17408 95.4 -> 86.3 us, 5120 x 5120 30.1 -> 27.4 us) and
-// for Q8_0 (4096 x 12288 at 8 tokens 26.4 -> 24.5 us); four for one K-quant token tile (Q4_K 5120 x 17408 at 8
-// tokens: 63.6 vs 74.4 us with eight).
+// Term waves per 16-row tile of the K-split kernel, measured on MI355X: eight (one unit per wave and stage) for two
+// token tiles (17-32 tokens: Qwen3-14B Q6_K at 17 tokens, 5120 x 17408 95.4 -> 86.3 us, 5120 x 5120 30.1 -> 27.4 us),
+// for Q6_K and for Q8_0 (4096 x 12288 at 8 tokens 26.4 -> 24.5 us); four for Q4_K's single token tile (5120 x 17408
+// at 8 tokens: 63.6 vs 74.4 us with eight) and for the pairs.
 template <int TYPE, int NTT, bool PAIR>
-constexpr int ks_waves() { return PAIR ? 4 : NTT == 2 || TYPE == kQ8_0 ? 8 : 4; }
+constexpr int ks_waves() { return PAIR ? 4 : NTT == 2 || TYPE != kQ4_K ? 8 : 4; }
 
 // Ring depth: the deepest ring that fits one workgroup per CU when the grid fits the GPU once, else one that lets
 // two workgroups share a CU (80 KB each).
-template <int TYPE, bool WIDE, int NTT, bool PAIR, int TS>
+// Chain waves (one chain per thread, 16 rows x TS tokens) for the single token tile of Q8_0 and Q4_K and for the
+// pairs; measured on MI355X (8 tokens, Q4_K 5120 x 17408: 46.4 -> 38.6 us, Q6_K 46.5 -> 43.4, Q8_0 4096 x 12288 19.6
+// -> 18.6; 12 tokens, Q4_K 57.6 -> 53.5). Without them (the chains on the term waves after their terms) for the two
+// token tiles (17 tokens, Q6_K: within 3 % either way) and for Q6_K's single tile (12 tokens: 71.9 vs 94.0 us).
+template <int TYPE, int NTT, bool PAIR, int TS>
+constexpr int ks_chain_waves() { return PAIR || (NTT == 1 && TYPE != kQ6_K) ? TS / 4 : 0; }
+
+template <int TYPE, bool WIDE, int NTT, bool PAIR, int TS, int CW = ks_chain_waves<TYPE, NTT, PAIR, TS>()>
 void launch_ks_ntt(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
                    int64_t ys, bool accumulate) {
   constexpr int KW = ks_waves<TYPE, NTT, PAIR>();
-  using S = KsLds<TYPE, WIDE, NTT, KW, TS>;
+  using S = KsLds<TYPE, WIDE, NTT, KW, TS, CW>;
   const int64_t wgs = rows / 16 * ((n + 16 * NTT - 1) / (16 * NTT)), cus = device_cus();
   constexpr int kDeep = (150 * 1024 - S::terms) / S::bytes >= 8 ? 8 : (150 * 1024 - S::terms) / S::bytes;
   constexpr int kTwo = (80 * 1024 - S::terms) / S::bytes;
   static_assert(kDeep >= 3, "the K-split ring needs three stages");
   if constexpr (kTwo >= 3) {
     if (wgs > cus) {
-      launch_ks_ns<TYPE, WIDE, NTT, (kTwo > 6 ? 6 : kTwo), KW, PAIR, TS>(s, w, rows, cols, x, n, y, ys, accumulate);
+      launch_ks_ns<TYPE, WIDE, NTT, (kTwo > 6 ? 6 : kTwo), KW, PAIR, TS, CW>(s, w, rows, cols, x, n, y, ys, accumulate);
       return;
     }
   }
-  launch_ks_ns<TYPE, WIDE, NTT, kDeep, KW, PAIR, TS>(s, w, rows, cols, x, n, y, ys, accumulate);
+  launch_ks_ns<TYPE, WIDE, NTT, kDeep, KW, PAIR, TS, CW>(s, w, rows, cols, x, n, y, ys, accumulate);
 }
 
 template <int TYPE, bool WIDE>
