@@ -266,6 +266,8 @@ SHORT = [
     # K split, two token tiles in 20 token slots (17..20 tokens): every count, both grid shapes; 21 tokens: 32 slots
     (mk_.Q6_K, 18, 2048, 512), (mk_.Q6_K, 19, 4096, 256), (mk_.Q6_K, 20, 96, 1024), (mk_.Q6_K, 21, 160, 512),
     (mk_.Q8_0, 20, 160, 512), (mk_.Q8_0, 19, 4096, 256), (mk_.Q8_0, 17, 5120, 512),
+    # 4 tokens on 2048..8192 rows: the K-split pairs (chain waves); 12 tokens: Q6_K on eight term waves
+    (mk_.Q4_K, 4, 2048, 1024), (mk_.Q6_K, 4, 5120, 512), (mk_.Q8_0, 4, 8192, 256), (mk_.Q6_K, 12, 320, 1024),
 ]
 
 
