@@ -49,6 +49,13 @@ __device__ __forceinline__ int hbyte(uint32_t q0, uint32_t q1, uint32_t q2, int 
   const uint32_t w = i < 4 ? q0 : (i < 8 ? q1 : q2);
   return (int)((w >> (8 * (i & 3))) & 0xFFu);
 }
+// The same for a wave-uniform j known only at run time, without branches: both forms, merged under a mask.
+__device__ __forceinline__ void scale_min_sel(int j, uint32_t q0, uint32_t q1, uint32_t q2, int& sc, int& m) {
+  const int sh = 8 * (j & 3), low = -(int)(j < 4);  // all ones for j < 4
+  const int b0 = (int)((q0 >> sh) & 0xFFu), b1 = (int)((q1 >> sh) & 0xFFu), b2 = (int)((q2 >> sh) & 0xFFu);
+  sc = ((b0 & 63) & low) | (((b2 & 0xF) | ((b0 >> 6) << 4)) & ~low);
+  m = ((b1 & 63) & low) | (((b2 >> 4) | ((b1 >> 6) << 4)) & ~low);
+}
 __device__ __forceinline__ void scale_min(int j, uint32_t q0, uint32_t q1, uint32_t q2, int& sc, int& m) {
   if (j < 4) {
     sc = hbyte(q0, q1, q2, j) & 63;
@@ -492,6 +499,7 @@ __global__ __launch_bounds__(64 * (KW + CW)) void k_mmv_ks(const uint8_t* W, int
   // Q4_K per stage (double-buffered like the terms): -(dmin m) per (row, unit) and dx (s0 + s1) per (token, unit)
   __shared__ __align__(16) float nmn_tab[TYPE == kQ4_K ? 2 * 16 * kUnits : 4];
   __shared__ __align__(16) float xs_tab[TYPE == kQ4_K ? 2 * 16 * NTT * kUnits : 4];
+  __shared__ __align__(16) float pair_sink[TYPE == kQ4_K && PAIR ? 64 : 4];  // stores of lanes without a slot
   float* terms = terms_base;
   float* nmn_t = nmn_tab;
   float* xs_t = xs_tab;
@@ -628,39 +636,47 @@ __global__ __launch_bounds__(64 * (KW + CW)) void k_mmv_ks(const uint8_t* W, int
             }
           }
         } else {  // Q4_K: the wave's pairs are whole 64-weight chunks (even unit: low nibbles, odd: high)
-          {  // dx (s0 + s1) of the wave's units' tokens, once per (unit, token)
-#pragma unroll
-            for (int k = 0; k < (UPW * TS + 63) / 64; ++k) {
-              const int idx = lane + 64 * k;
-              if (idx < UPW * TS) {
-                const int u = UPW * wu + idx / TS, tok = idx % TS;
-                const int at = u * TS + tok;
-                const uint32_t sx = *reinterpret_cast<const uint32_t*>(st + S::xs + at * 4);
-                const float dxv = *reinterpret_cast<const float*>(st + S::dx + at * 4);
-                xs_t[tok * kUnits + u] = dxv * (float)((int)(int16_t)(sx & 0xFFFF) + (int)(int16_t)(sx >> 16));
-              }
-            }
-          }
+          // Every LDS read of the stage first and the arithmetic without branches (only the stores predicated): a
+          // branch ends the scheduler's region, and each read behind one waits out its own round trip.
+          static_assert(UPW * TS <= 64, "one (unit, token) of the wave per lane");
+          constexpr int NP = UPW / 2;  // the wave's pairs
+          const int xi = min(lane, UPW * TS - 1), xu = UPW * wu + xi / TS, xt = xi % TS;
+          const uint32_t sx = *reinterpret_cast<const uint32_t*>(st + S::xs + (xu * TS + xt) * 4);
+          const float dxv = *reinterpret_cast<const float*>(st + S::dx + (xu * TS + xt) * 4);
           const uint4 hd = *reinterpret_cast<const uint4*>(st + S::s_off + gi * 128 + rr * 16);
+          uint2 raw[NP];
+          long xa0[NP], xa1[NP];
+          float4 dx4[NP];
+#pragma unroll
+          for (int k = 0; k < NP; ++k) {
+            const int u0 = UPW * wu + 2 * k;
+            raw[k] = *reinterpret_cast<const uint2*>(st + gi * 1024 + (u0 / 2) * 256 + (c >> 1) * 128 + rr * 16 +
+                                                     8 * (c & 1));
+            xa0[k] = xa(u0), xa1[k] = xa(u0 + 1);
+            dx4[k] = dxs(u0);
+          }
+          // dx (s0 + s1) of the wave's units' tokens, once per (unit, token); the other lanes store to a sink
+          const float xsv = dxv * (float)((int)(int16_t)(sx & 0xFFFF) + (int)(int16_t)(sx >> 16));
+          *(lane < UPW * TS ? xs_t + xt * kUnits + xu : pair_sink + lane) = xsv;
           const float d = half_to_float((uint16_t)(hd.x & 0xFFFF)), dmin = half_to_float((uint16_t)(hd.x >> 16));
 #pragma unroll
-          for (int k = 0; k < UPW; k += 2) {
-            const int u0 = UPW * wu + k, j2 = u0 / 2;
-            const uint2 raw =
-                *reinterpret_cast<const uint2*>(st + gi * 1024 + j2 * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
+          for (int k = 0; k < NP; ++k) {
+            const int u0 = UPW * wu + 2 * k;
             long bq[2];
-            float fsc[2];
+            float fsc[2], nmv[2];
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-              bq[e] = (long)(((uint64_t)((raw.y >> (4 * e)) & 0x0F0F0F0Fu) << 32) | ((raw.x >> (4 * e)) & 0x0F0F0F0Fu));
+              bq[e] = (long)(((uint64_t)((raw[k].y >> (4 * e)) & 0x0F0F0F0Fu) << 32) |
+                             ((raw[k].x >> (4 * e)) & 0x0F0F0F0Fu));
               int sc, mn;
-              scale_min(u0 + e, hd.y, hd.z, hd.w, sc, mn);
+              scale_min_sel(u0 + e, hd.y, hd.z, hd.w, sc, mn);
               fsc[e] = d * (float)sc;
-              if (c == 0) nmn_t[r * kUnits + u0 + e] = -(dmin * (float)mn);
+              nmv[e] = -(dmin * (float)mn);
             }
-            const long a0 = lo ? xa(u0) : 0, a1 = lo ? 0 : xa(u0 + 1);
-            const float4 dx4 = dxs(u0);
-            const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+            *reinterpret_cast<float2*>(c == 0 ? nmn_t + r * kUnits + u0 : pair_sink + 2 * (lane & 31)) =
+                make_float2(nmv[0], nmv[1]);
+            const long a0 = lo ? xa0[k] : 0, a1 = lo ? 0 : xa1[k];
+            const float dx[4] = {dx4[k].x, dx4[k].y, dx4[k].z, dx4[k].w};
             const v4i dq = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bq[1], __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bq[0], zero4, 0, 0, 0), 0, 0, 0);
             const float fs = ph ? fsc[1] : fsc[0];
 #pragma unroll
