@@ -499,7 +499,7 @@ __global__ __launch_bounds__(64 * (KW + CW)) void k_mmv_ks(const uint8_t* W, int
   // Q4_K per stage (double-buffered like the terms): -(dmin m) per (row, unit) and dx (s0 + s1) per (token, unit)
   __shared__ __align__(16) float nmn_tab[TYPE == kQ4_K ? 2 * 16 * kUnits : 4];
   __shared__ __align__(16) float xs_tab[TYPE == kQ4_K ? 2 * 16 * NTT * kUnits : 4];
-  __shared__ __align__(16) float pair_sink[TYPE == kQ4_K && PAIR ? 64 : 4];  // stores of lanes without a slot
+  __shared__ __align__(16) float pair_sink[TYPE == kQ4_K ? 64 : 4];  // Q4_K stores of lanes without a slot
   float* terms = terms_base;
   float* nmn_t = nmn_tab;
   float* xs_t = xs_tab;
@@ -590,7 +590,7 @@ __global__ __launch_bounds__(64 * (KW + CW)) void k_mmv_ks(const uint8_t* W, int
               bw[e] = *reinterpret_cast<const long*>(st + gi * 2048 + (u0 + e) * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
               dw[e] = half_to_float(*reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + (u0 + e) * 16 + rr * 2));
             }
-            const long a0 = lo ? xa(u0) : 0, a1 = lo ? 0 : xa(u0 + 1);
+            const long x0 = xa(u0), x1 = xa(u0 + 1), a0 = lo ? x0 : 0, a1 = lo ? 0 : x1;  // both read, then selected
             const float4 dx4 = dxs(u0);
             const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
             const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bw[1], __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bw[0], zero4, 0, 0, 0), 0, 0, 0);
@@ -684,48 +684,72 @@ __global__ __launch_bounds__(64 * (KW + CW)) void k_mmv_ks(const uint8_t* W, int
           }
         }
       } else if constexpr (TYPE == kQ8_0) {
+        // Every LDS read of the stage first: the term stores could alias them as far as the compiler can tell and
+        // would hold each read behind the stores before it.
+        long bw[UPW], av[UPW][NTT];
+        float dw[UPW];
+        float4 dv[UPW][NTT];
 #pragma unroll
         for (int k = 0; k < UPW; ++k) {
           const int u = UPW * wu + k;
-          const long b = *reinterpret_cast<const long*>(st + gi * 2048 + u * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
-          const float dw = half_to_float(*reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + u * 16 + rr * 2));
+          bw[k] = *reinterpret_cast<const long*>(st + gi * 2048 + u * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
+          dw[k] = half_to_float(*reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + u * 16 + rr * 2));
 #pragma unroll
           for (int m = 0; m < NTT; ++m) {
-            const long a = *reinterpret_cast<const long*>(st + S::x + (u * TS + 16 * m + r) * 32 + 8 * c);
-            const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + (u * TS + 16 * m + 4 * c) * 4);
-            const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
-            const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero4, 0, 0, 0);
+            av[k][m] = *reinterpret_cast<const long*>(st + S::x + (u * TS + 16 * m + r) * 32 + 8 * c);
+            dv[k][m] = *reinterpret_cast<const float4*>(st + S::dx + (u * TS + 16 * m + 4 * c) * 4);
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < UPW; ++k) {
+          const int u = UPW * wu + k;
+#pragma unroll
+          for (int m = 0; m < NTT; ++m) {
+            const float dx[4] = {dv[k][m].x, dv[k][m].y, dv[k][m].z, dv[k][m].w};
+            const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[k][m], bw[k], zero4, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
               if (m == 0 || i < lim1) {
-                const float e0 = (float)d[i], e1 = dw * dx[i];
+                const float e0 = (float)d[i], e1 = dw[k] * dx[i];
                 if (m == 0 || i < live1) put(u, 16 * m + 4 * c + i, {e0, e1});
               }
           }
         }
       } else if constexpr (TYPE == kQ6_K) {
+        // Every LDS read of the stage first (as for Q8_0).
         const float dd = half_to_float(*reinterpret_cast<const uint16_t*>(st + S::d_off + gi * 16 + rr * 2));
         const int hw = c >> 1, h = c & 1;
+        uint2 nib[UPW], hb[UPW];
+        uint32_t scw[UPW];
+        long av[UPW][NTT];
+        float4 dv[UPW][NTT];
 #pragma unroll
         for (int k = 0; k < UPW; ++k) {
           const int u = UPW * wu + k;
           const uint8_t* au = st + gi * 1536 + u * 192;
-          const uint2 nib = *reinterpret_cast<const uint2*>(au + rr * 16 + 8 * h);
-          const uint2 hb = *reinterpret_cast<const uint2*>(au + 128 + rr * 8);
-          const uint32_t hv = (hw ? hb.y : hb.x) >> (4 * h);
-          const uint32_t q0 = ((nib.x >> (4 * hw)) & 0x0F0F0F0Fu) | ((hv & 0x03030303u) << 4);
-          const uint32_t q1 = ((nib.y >> (4 * hw)) & 0x0F0F0F0Fu) | (((hv >> 2) & 0x03030303u) << 4);
-          const long bq = (long)(((uint64_t)minus32(q1) << 32) | minus32(q0));
-          const long b0 = hw ? 0 : bq, b1 = hw ? bq : 0;
-          const uint32_t scw = *reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + rr * 16 + 2 * u);
-          const float dsc0 = dd * (float)(int8_t)(scw & 0xFF), dsc1 = dd * (float)(int8_t)(scw >> 8);
+          nib[k] = *reinterpret_cast<const uint2*>(au + rr * 16 + 8 * h);
+          hb[k] = *reinterpret_cast<const uint2*>(au + 128 + rr * 8);
+          scw[k] = *reinterpret_cast<const uint16_t*>(st + S::s_off + gi * 128 + rr * 16 + 2 * u);
 #pragma unroll
           for (int m = 0; m < NTT; ++m) {
-            const long a = *reinterpret_cast<const long*>(st + S::x + (u * TS + 16 * m + r) * 32 + 8 * c);
-            const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + (u * TS + 16 * m + 4 * c) * 4);
-            const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
-            const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b0, zero4, 0, 0, 0);
-            const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, zero4, 0, 0, 0);
+            av[k][m] = *reinterpret_cast<const long*>(st + S::x + (u * TS + 16 * m + r) * 32 + 8 * c);
+            dv[k][m] = *reinterpret_cast<const float4*>(st + S::dx + (u * TS + 16 * m + 4 * c) * 4);
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < UPW; ++k) {
+          const int u = UPW * wu + k;
+          const uint32_t hv = (hw ? hb[k].y : hb[k].x) >> (4 * h);
+          const uint32_t q0 = ((nib[k].x >> (4 * hw)) & 0x0F0F0F0Fu) | ((hv & 0x03030303u) << 4);
+          const uint32_t q1 = ((nib[k].y >> (4 * hw)) & 0x0F0F0F0Fu) | (((hv >> 2) & 0x03030303u) << 4);
+          const long bq = (long)(((uint64_t)minus32(q1) << 32) | minus32(q0));
+          const long b0 = hw ? 0 : bq, b1 = hw ? bq : 0;
+          const float dsc0 = dd * (float)(int8_t)(scw[k] & 0xFF), dsc1 = dd * (float)(int8_t)(scw[k] >> 8);
+#pragma unroll
+          for (int m = 0; m < NTT; ++m) {
+            const float dx[4] = {dv[k][m].x, dv[k][m].y, dv[k][m].z, dv[k][m].w};
+            const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[k][m], b0, zero4, 0, 0, 0);
+            const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[k][m], b1, zero4, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               if (m > 0 && i >= lim1) continue;
@@ -740,38 +764,42 @@ __global__ __launch_bounds__(64 * (KW + CW)) void k_mmv_ks(const uint8_t* W, int
           }
         }
       } else {  // Q4_K: the wave's units UPW w .. (64-weight chunk u / 2: even units low nibbles, odd high)
-        {  // dx (s0 + s1) of the wave's units' tokens, once per (unit, token)
-#pragma unroll
-          for (int k = 0; k < (UPW * TS + 63) / 64; ++k) {
-            const int idx = lane + 64 * k;
-            if (idx < UPW * TS) {
-              const int u = UPW * wu + idx / TS, tok = idx % TS;
-              const int at = u * TS + tok;
-              const uint32_t sx = *reinterpret_cast<const uint32_t*>(st + S::xs + at * 4);
-              const float dxv = *reinterpret_cast<const float*>(st + S::dx + at * 4);
-              xs_t[tok * kUnits + u] = dxv * (float)((int)(int16_t)(sx & 0xFFFF) + (int)(int16_t)(sx >> 16));
-            }
-          }
-        }
+        // Every LDS read of the stage first and the arithmetic without branches, as for the pairs.
+        static_assert(UPW * TS <= 64, "one (unit, token) of the wave per lane");
+        const int xi = min(lane, UPW * TS - 1), xu = UPW * wu + xi / TS, xt = xi % TS;
+        const uint32_t sx = *reinterpret_cast<const uint32_t*>(st + S::xs + (xu * TS + xt) * 4);
+        const float dxv = *reinterpret_cast<const float*>(st + S::dx + (xu * TS + xt) * 4);
         const uint4 hd = *reinterpret_cast<const uint4*>(st + S::s_off + gi * 128 + rr * 16);
-        const float d = half_to_float((uint16_t)(hd.x & 0xFFFF)), dmin = half_to_float((uint16_t)(hd.x >> 16));
         const int j2 = UPW * wu / 2;  // the wave's 64-weight chunk
         const uint2 raw =
             *reinterpret_cast<const uint2*>(st + gi * 1024 + j2 * 256 + (c >> 1) * 128 + rr * 16 + 8 * (c & 1));
+        long av[UPW][NTT];
+        float4 dv[UPW][NTT];
+#pragma unroll
+        for (int k = 0; k < UPW; ++k) {
+          const int u = UPW * wu + k;
+#pragma unroll
+          for (int m = 0; m < NTT; ++m) {
+            av[k][m] = *reinterpret_cast<const long*>(st + S::x + (u * TS + 16 * m + r) * 32 + 8 * c);
+            dv[k][m] = *reinterpret_cast<const float4*>(st + S::dx + (u * TS + 16 * m + 4 * c) * 4);
+          }
+        }
+        // dx (s0 + s1) of the wave's units' tokens, once per (unit, token); the other lanes store to a sink
+        const float xsv = dxv * (float)((int)(int16_t)(sx & 0xFFFF) + (int)(int16_t)(sx >> 16));
+        *(lane < UPW * TS ? xs_t + xt * kUnits + xu : pair_sink + lane) = xsv;
+        const float d = half_to_float((uint16_t)(hd.x & 0xFFFF)), dmin = half_to_float((uint16_t)(hd.x >> 16));
 #pragma unroll
         for (int k = 0; k < UPW; ++k) {
           const int u = UPW * wu + k, e = u & 1;
           const long bq = (long)(((uint64_t)((raw.y >> (4 * e)) & 0x0F0F0F0Fu) << 32) | ((raw.x >> (4 * e)) & 0x0F0F0F0Fu));
           int sc, mn;
-          scale_min(u, hd.y, hd.z, hd.w, sc, mn);
+          scale_min_sel(u, hd.y, hd.z, hd.w, sc, mn);
           const float fsc = d * (float)sc;
-          if (c == 0) nmn_t[r * kUnits + u] = -(dmin * (float)mn);
+          *(c == 0 ? nmn_t + r * kUnits + u : pair_sink + lane) = -(dmin * (float)mn);
 #pragma unroll
           for (int m = 0; m < NTT; ++m) {
-            const long a = *reinterpret_cast<const long*>(st + S::x + (u * TS + 16 * m + r) * 32 + 8 * c);
-            const float4 dx4 = *reinterpret_cast<const float4*>(st + S::dx + (u * TS + 16 * m + 4 * c) * 4);
-            const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
-            const v4i dq = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq, zero4, 0, 0, 0);
+            const float dx[4] = {dv[k][m].x, dv[k][m].y, dv[k][m].z, dv[k][m].w};
+            const v4i dq = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[k][m], bq, zero4, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
               if (m == 0 || i < lim1) {
