@@ -684,19 +684,26 @@ bool kq_gemm_first(int type, int64_t rows, int n) { return n > 16 && (rows >= 16
 // Short batches on the MFMA short-batch kernels (mmv). Measured on MI355X over the Qwen3-0.6B/4B/8B/14B shapes (Q8_0,
 // Q4_K, Q6_K; results of every kernel compared bit for bit): the GEMV wins up to 2 tokens, and up to 4 except on
 // matrices of more than 8192 rows in Q4_K (17408 x 5120 at 4 tokens: 46.1 vs 26.5 us) or of 24576 rows and more in
-// Q8_0 (the LM head: 140 vs 116 us), and at 4 tokens on 2048..8192 rows, where the K-split pairs win (5120 x 17408:
-// Q4_K 42.0 -> 37.7 us, Q6_K 50.5 -> 42.5; 7168 x 5120 Q6_K 19.7 -> 15.6; 1024 x 3072: 5.9 vs 8.1 with the GEMV);
-// from 5 to 16 tokens mmv, with the K split inside the workgroup on matrices of up to 8192 rows and one wave per
-// tile on wider ones; from 17 to 32 tokens the same, except that the GEMMs' 32- and 64-token tiles win on the widest
-// matrices and the one-wave form on Q4_K.
+// Q8_0 (the LM head: 140 vs 116 us), and at 4 tokens on 2048..8192 rows (up to 17408 in K-quants), where the K-split
+// pairs win (5120 x 17408: Q4_K 42.0 -> 37.7 us, Q6_K 50.5 -> 42.5; 7168 x 5120 Q6_K 19.7 -> 15.6; 17408 x 5120 Q6_K
+// 36.3 -> 35.2; 1024 x 3072: 5.9 vs 8.1 with the GEMV); from 5 to 16 tokens mmv; from 17 to 32 tokens the same,
+// except that the GEMMs' 32- and 64-token tiles win on the widest matrices and the one-wave form on Q4_K.
 bool mmv_first(int type, int64_t rows, int64_t cols, int n) {
   if (n <= 2 || n > 32 || !mmv_supported(type, rows, cols, n)) return false;
-  if (n == 4 && rows >= 2048 && rows <= 8192) return true;
+  if (n == 4 && rows >= 2048 && rows <= (type == kQ8_0 ? 8192 : 17408)) return true;
   if (n <= 4) return type == kQ4_K ? rows > 8192 : type == kQ8_0 && rows >= 24576;
   if (n <= 16) return true;
   return rows < (type == kQ8_0 ? 16384 : 24576);
 }
-bool mmv_ksplit(int type, int64_t rows, int64_t cols, int n) { return rows <= 8192 && (n <= 16 || type != kQ4_K); }
+// K split inside the workgroup (k_mmv_ks) or one wave per 16-row tile (k_mmv), measured on MI355X: the K split on up
+// to 8192 rows (Q4_K: up to 16 tokens), and up to 8 tokens on up to 17408 rows of K-quants (17408 x 5120 at 8 tokens:
+// Q4_K 27.2 -> 26.4 us, Q6_K 38.8 -> 35.5) and 12288 of Q8_0 (12288 x 4096: 17.5 -> 15.6; 24576 x 4096: 22.4 vs
+// 28.7), and Q6_K at 17..32 tokens up to 17408 rows (17408 x 5120 at 17 tokens: 53.5 -> 47.2; at 12 tokens the one-
+// wave form wins there, 39.4 vs 50.2).
+bool mmv_ksplit(int type, int64_t rows, int64_t cols, int n) {
+  if (rows <= 8192) return n <= 16 || type != kQ4_K;
+  return n <= 8 ? rows <= (type == kQ8_0 ? 12288 : 17408) : n > 16 && type == kQ6_K && rows <= 17408;
+}
 
 }  // namespace
 

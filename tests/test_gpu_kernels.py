@@ -268,6 +268,8 @@ SHORT = [
     (mk_.Q8_0, 20, 160, 512), (mk_.Q8_0, 19, 4096, 256), (mk_.Q8_0, 17, 5120, 512),
     # 4 tokens on 2048..8192 rows: the K-split pairs (chain waves); 12 tokens: Q6_K on eight term waves
     (mk_.Q4_K, 4, 2048, 1024), (mk_.Q6_K, 4, 5120, 512), (mk_.Q8_0, 4, 8192, 256), (mk_.Q6_K, 12, 320, 1024),
+    # K split past 8192 rows: up to 8 tokens (17408 rows of K-quants, 12288 of Q8_0), Q6_K at 17..32 tokens
+    (mk_.Q4_K, 8, 8224, 512), (mk_.Q6_K, 4, 17408, 256), (mk_.Q8_0, 6, 12288, 256), (mk_.Q6_K, 18, 8224, 256),
 ]
 
 
