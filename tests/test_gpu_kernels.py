@@ -270,6 +270,8 @@ SHORT = [
     (mk_.Q4_K, 4, 2048, 1024), (mk_.Q6_K, 4, 5120, 512), (mk_.Q8_0, 4, 8192, 256), (mk_.Q6_K, 12, 320, 1024),
     # K split past 8192 rows: up to 8 tokens (17408 rows of K-quants, 12288 of Q8_0), Q6_K at 17..32 tokens
     (mk_.Q4_K, 8, 8224, 512), (mk_.Q6_K, 4, 17408, 256), (mk_.Q8_0, 6, 12288, 256), (mk_.Q6_K, 18, 8224, 256),
+    # pairs on 16-unit stages (K a multiple of 512) and on 8-unit ones (768)
+    (mk_.Q6_K, 8, 64, 768), (mk_.Q4_K, 3, 8224, 768), (mk_.Q8_0, 7, 2048, 1536),
 ]
 
 
