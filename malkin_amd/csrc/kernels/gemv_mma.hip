@@ -320,10 +320,12 @@ __global__ __launch_bounds__(kThreads) void k_mmv(const uint8_t* W, int64_t rows
     }
 }
 
-// K-split form for matrices with few rows (down and attn_output projections): KW = 4 or 8 waves share one 16-row
-// tile. Per stage of 8 units, wave w computes the MFMA dots of units (8 / KW) w .. and their per-unit float terms
-// (the operands of the reference's fmas, rounded as the reference rounds them) into LDS; after a barrier the lanes
-// run the sequential chains of the tile's (row, token) outputs over the stage's 8 units in order. Terms per unit and
+// K-split form for matrices with few rows (down and attn_output projections): KW = 4 or 8 term waves share one
+// 16-row tile. Per stage of 8 units, term wave w computes the MFMA dots of units (8 / KW) w .. and their per-unit float
+// terms (the operands of the reference's fmas, rounded as the reference rounds them) into LDS; the sequential chains
+// of the tile's (row, token) outputs then run over the stage's 8 units in order, either on CW chain waves of their
+// own one stage behind (double-buffered terms, one barrier per stage) or on the term waves themselves (after the
+// next stage's terms when the terms are double-buffered, else after a second barrier). Terms per unit and
 // output, E floats: Q8_0 {float(ai), dw dx}; Q6_K compact {float(ai_0), (d sc_0) dx, float(ai_1), (d sc_1) dx};
 // Q6_K wide {fma(float(ai_1), d sc_1, float(ai_0) (d sc_0)), dx}; Q4_K {float(ai), (d sc) dx}; the chain applies
 // acc = fma(e0, e1, acc) (and acc = fma(e2, e3, acc)). Q4_K's second fma, acc = fma(-(dmin m), dx (s0 + s1), acc),
@@ -357,7 +359,8 @@ struct KsLds {
   static_assert(w_bytes / 1024 <= KW, "every W piece in a wave's first slot");
 };
 
-// KW waves per workgroup (4 or 8): each wave computes the dots and terms of 8 / KW of a stage's 8 units.
+// KW term waves (4 or 8), then CW chain waves (0: the term waves run the chains): each term wave computes the dots
+// and terms of 8 / KW of a stage's 8 units.
 // PAIR (at most 8 tokens, one token tile): a wave takes its units two at a time in one 16 x 16 MFMA tile, unit u's
 // tokens in the tile's token rows 0..7 and unit u + 1's in rows 8..15. The first MFMA has unit u's activations in rows
 // 0..7 (zero elsewhere) against unit u's weights, the second accumulates unit u + 1's activations in rows 8..15
