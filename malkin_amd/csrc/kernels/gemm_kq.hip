@@ -16,8 +16,9 @@
 // layout.h into int8 in registers: Q4_K nibbles 0..15; Q6_K q - 32 per byte as ((q | 0x80) - 0x20) ^ 0x80, which
 // never borrows across bytes for q < 64.
 //
-// A workgroup (4 waves) owns a 128-row x 32-token tile, 32 rows per wave, and walks K in stages of half a super-block
-// (4 units of 32 weights) held in a ring of NS LDS buffers filled by direct global -> LDS loads NS - 1 stages ahead.
+// A workgroup (4 waves) owns a 128-row x 32-token tile (or a 32-row tail tile), 32 rows per wave, and walks K in
+// stages of half a super-block (4 units of 32 weights) held in a ring of NS LDS buffers filled by direct global -> LDS
+// loads NS - 1 stages ahead.
 #include <utility>
 
 #include "ctx.h"
@@ -102,17 +103,22 @@ __device__ __forceinline__ void scale_min(int j, uint32_t q0, uint32_t q1, uint3
 template <int TYPE, bool WIDE, int NS, int NE>
 __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t rows, int64_t cols,
                                                       const BlockQ8* x, int n, float* __restrict__ y, int64_t ys,
-                                                      int accumulate, int n_rt, int n_tt) {
+                                                      int accumulate, int n_rt, int n_tt, int n_big) {
   using S = KqLds<TYPE>;
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wu = __builtin_amdgcn_readfirstlane(w);
   // Workgroup -> (row tile, token tile): tiles numbered row-major, each XCD a contiguous run of them (token tiles of a
   // row tile on one XCD, rows read once into its L2).
-  const int tile = xcd_run((int)blockIdx.x, n_rt * n_tt), rt = tile / n_tt, tt = tile % n_tt;
+  // With 32-row tail tiles (n_big < n_rt, one token tile): tiles in launch order, so the n_big = CU count full tiles
+  // take one CU each and the tail tiles a second slot on CUs of every XCD.
+  const int tile = n_big < n_rt ? (int)blockIdx.x : xcd_run((int)blockIdx.x, n_rt * n_tt);
+  const int rt = tile / n_tt, tt = tile % n_tt;
   const int nb = (int)(cols / 32), nsb = (int)(cols / 256);
-  const int64_t g0 = (int64_t)rt * (kRowsT / 8);
-  const int ngroups = (int)min<int64_t>(kRowsT / 8, rows / 8 - g0);  // 4 .. 16 (rows % 32 == 0)
+  const int64_t r0 = rt < n_big ? (int64_t)rt * kRowsT : (int64_t)n_big * kRowsT + (int64_t)(rt - n_big) * 32;
+  const int64_t g0 = r0 / 8;
+  const int ngroups = (int)min<int64_t>(rt < n_big ? kRowsT / 8 : 4, rows / 8 - g0);  // 4 .. 16 (rows % 32 == 0)
+  const bool live = 32 * wu < 8 * ngroups;  // this wave's 32 rows hold a row of the matrix (else: copies only)
   const int t0 = tt * kTokT;
   const int nstages = nb / kKB;  // cols % 256 == 0: whole stages
 
@@ -227,6 +233,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t 
     wait_vm_stages<S::loads, NS - 2>(min(NS - 2, nstages - 1 - s));
     ring_barrier();
     if (s + NS - 1 < nstages) issue.template operator()<(BUF + NS - 1) % NS>(s + NS - 1);
+    if (!live) return;
     uint8_t* st = smem + BUF * S::bytes;
     const int hf = s & 1;
     if constexpr (TYPE == kQ6_K) {
@@ -328,8 +335,8 @@ __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t 
   }
 
   // Element i: token t0 + 8 (i / 4) + 4 h + i % 4, row 128 rt + 32 w + li.
-  if (32 * w < 8 * ngroups) {
-    float* yr = y + (int64_t)rt * kRowsT + 32 * w + li;
+  if (live) {
+    float* yr = y + r0 + 32 * w + li;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int t = t0 + 8 * (i / 4) + tok_i + i % 4;
@@ -343,7 +350,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t 
 
 template <int TYPE, bool WIDE, int NS, int NE>
 void launch_kq_ns(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y,
-                  int64_t ys, bool accumulate, int n_rt, int n_tt) {
+                  int64_t ys, bool accumulate, int n_rt, int n_tt, int n_big) {
   const size_t lds = NS * (size_t)KqLds<TYPE>::bytes;
   static bool attr = false;  // per instantiation: rings past 64 KB of dynamic LDS
   if (!attr) {
@@ -353,7 +360,7 @@ void launch_kq_ns(hipStream_t s, const void* w, int64_t rows, int64_t cols, cons
     attr = true;
   }
   hipLaunchKernelGGL((k_gemm_kq<TYPE, WIDE, NS, NE>), dim3((unsigned)((int64_t)n_rt * n_tt)), dim3(kThreads), lds, s,
-                     static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0, n_rt, n_tt);
+                     static_cast<const uint8_t*>(w), rows, cols, x, n, y, ys, accumulate ? 1 : 0, n_rt, n_tt, n_big);
 }
 
 // Ring depth by grid size: one workgroup per CU takes an 8-stage ring (7 stages, about 130 KB, in flight), two per CU
@@ -361,17 +368,26 @@ void launch_kq_ns(hipStream_t s, const void* w, int64_t rows, int64_t cols, cons
 template <int TYPE, bool WIDE>
 void launch_kq(hipStream_t s, const void* w, int64_t rows, int64_t cols, const BlockQ8* x, int n, float* y, int64_t ys,
                bool accumulate) {
-  const int n_rt = (int)((rows + kRowsT - 1) / kRowsT);
+  int n_rt = (int)((rows + kRowsT - 1) / kRowsT), n_big = n_rt;
   const int n_tt = (n + kTokT - 1) / kTokT;
-  const int64_t wgs = (int64_t)n_rt * n_tt, cus = device_cus();
+  const int64_t cus = device_cus();
+  // A short batch over slightly more than one 128-row tile per CU (the 14B gate|up, 34816 rows: 272 tiles) takes one
+  // full tile per CU and covers the rest with 32-row tiles (one live wave), so that no CU runs two full tiles.
+  // Measured at 17 tokens (bit-identical): Q6_K 34816 x 5120 65.3 -> 62.3 us, 40960 x 5120 66.4 -> 63.6, Q4_K
+  // 34816 x 5120 50.5 -> 48.4; at 24 tokens Q6_K 34816 x 5120 78.2 -> 75.6.
+  if (n_tt == 1 && n_rt > cus && rows <= (kRowsT + 32) * cus) {
+    n_big = (int)cus;
+    n_rt = n_big + (int)((rows - kRowsT * cus) / 32);
+  }
+  const int64_t wgs = (int64_t)n_rt * n_tt;
   if (wgs <= cus)
-    n <= 17 ? launch_kq_ns<TYPE, WIDE, 8, 9>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt)
-            : launch_kq_ns<TYPE, WIDE, 8, 16>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt);
+    n <= 17 ? launch_kq_ns<TYPE, WIDE, 8, 9>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt, n_big)
+            : launch_kq_ns<TYPE, WIDE, 8, 16>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt, n_big);
   else if (wgs <= 2 * cus)
-    n <= 17 ? launch_kq_ns<TYPE, WIDE, 4, 9>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt)
-            : launch_kq_ns<TYPE, WIDE, 4, 16>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt);
+    n <= 17 ? launch_kq_ns<TYPE, WIDE, 4, 9>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt, n_big)
+            : launch_kq_ns<TYPE, WIDE, 4, 16>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt, n_big);
   else
-    launch_kq_ns<TYPE, WIDE, 3, 16>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt);
+    launch_kq_ns<TYPE, WIDE, 3, 16>(s, w, rows, cols, x, n, y, ys, accumulate, n_rt, n_tt, n_big);
 }
 
 }  // namespace

@@ -272,6 +272,8 @@ SHORT = [
     (mk_.Q4_K, 8, 8224, 512), (mk_.Q6_K, 4, 17408, 256), (mk_.Q8_0, 6, 12288, 256), (mk_.Q6_K, 18, 8224, 256),
     # pairs on 16-unit stages (K a multiple of 512) and on 8-unit ones (768)
     (mk_.Q6_K, 8, 64, 768), (mk_.Q4_K, 3, 8224, 768), (mk_.Q8_0, 7, 2048, 1536),
+    # K-quant GEMM past one 128-row tile per CU: a full tile per CU plus 32-row tail tiles (8, 64 and 256 of them)
+    (mk_.Q6_K, 17, 33024, 256), (mk_.Q4_K, 20, 34816, 256), (mk_.Q6_K, 32, 40960, 256),
 ]
 
 
