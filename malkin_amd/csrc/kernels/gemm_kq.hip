@@ -51,6 +51,7 @@ struct KqLds<kQ6_K> {
   static constexpr int dx = x + 4 * 32 * 32;     // [4 units][32 tok] f32
   static constexpr int bytes = dx + 4 * 32 * 4;  // 19200
   static constexpr int loads = 6;                // global -> LDS loads per wave per stage
+  static constexpr int tail_loads = 4;           // ... in a 32-row tail tile
 };
 template <>
 struct KqLds<kQ4_K> {
@@ -130,7 +131,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t 
   const uint32_t tw_off = (uint32_t)(tw * nb * 40 + (lane >> 5) * 40);  // + 80 c for unit 2 c + lane / 32
 
   // Weight copies: every piece is 16 (or 4) bytes of a packed (group, unit) record, LDS destinations lane-linear.
-  uint32_t a_off[3], m_off;
+  uint32_t a_off[3], m_off, t_off = 0;
   const uint8_t *a_base, *m_base, *d_base = nullptr;
   uint32_t d_off = 0;
   if constexpr (TYPE == kQ6_K) {
@@ -149,6 +150,9 @@ __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t 
     }
     d_off = (uint32_t)(min(lane / 4, ngroups - 1) * nsb * 16 + 4 * (lane % 4));
     d_base = W + L.dscale(g0, 0);
+    // Tail tile (4 groups): wave w copies unit w of the stage, lanes 0..47 its 4 x 12 pieces; lanes 48..63 re-read
+    // group 3 into the unused group 4-5 slots.
+    t_off = (uint32_t)((min(lane / 12, ngroups - 1) * nsb * 8 + w) * 192 + 16 * (lane % 12));
   } else {
     const PackedQ4_K L{rows, nsb};
 #pragma unroll
@@ -167,12 +171,30 @@ __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t 
   }
 
   // Stage sn (units 4 sn .. 4 sn + 3: super-block sn / 2, half sn % 2) into buffer BUF. Every wave issues S::loads
-  // loads (a wave with fewer repeats its activation copy), so one wait count fits all.
-  auto issue = [&]<int BUF>(int sn) __attribute__((always_inline)) {
+  // loads (a wave with fewer repeats its activation copy), so one wait count fits all; Q6_K tail tiles (TAIL) copy
+  // only the 4 groups' quants and scales, S::tail_loads per wave.
+  auto issue = [&]<int BUF, bool TAIL>(int sn) __attribute__((always_inline)) {
     uint8_t* st = smem + BUF * S::bytes;
     const int sb = sn >> 1, hf = sn & 1;
     const uint8_t* xb = x_base + (size_t)(4 * sn) * 40;
-    if constexpr (TYPE == kQ6_K) {
+    if constexpr (TYPE == kQ6_K && TAIL) {
+      using T = KqLds<kQ6_K>;
+      const uint8_t* ab = a_base + ((size_t)sb * 8 + 4 * hf) * 192;
+      load_lds16(ab + t_off, st + T::a + 3072 * wu);
+      if (wu == 0)
+        load_lds16(m_base + (size_t)sb * 128 + m_off, st + T::sc);
+      else if (wu == 1)
+        load_lds16(xb + (size_t)wu * 40 + x_off, st + T::x + 1024 * wu);
+      else if (wu == 2)
+        load_lds4(d_base + (size_t)sb * 16 + d_off, st + T::d);
+      else
+        load_lds4(xb + tw_off, st + T::dx);
+      if (wu == 3)
+        load_lds4(xb + 80 + tw_off, st + T::dx + 256);
+      else
+        load_lds16(xb + (size_t)wu * 40 + x_off, st + T::x + 1024 * wu);
+      load_lds16(xb + (size_t)wu * 40 + x_off, st + T::x + 1024 * wu);
+    } else if constexpr (TYPE == kQ6_K) {
       const uint8_t* ab = a_base + ((size_t)sb * 8 + 4 * hf) * 192;
 #pragma unroll
       for (int c = 0; c < 3; ++c) load_lds16(ab + a_off[c], st + S::a + 1024 * (3 * wu + c));
@@ -225,14 +247,17 @@ __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t 
     return v;
   };
 
-  auto stage = [&]<int BUF>(int s) __attribute__((always_inline)) {
+  auto stage = [&]<int BUF, bool TAIL>(int s) __attribute__((always_inline)) {
     // Stage s has landed once at most the loads of the stages issued after it (s + 1 .. s + NS - 2, fewer at the
     // end) are outstanding; the buffer stage s + NS - 1 goes into was read in stage s - 1, finished by every wave
     // before this barrier.
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    wait_vm_stages<S::loads, NS - 2>(min(NS - 2, nstages - 1 - s));
+    if constexpr (TAIL)
+      wait_vm_stages<KqLds<kQ6_K>::tail_loads, NS - 2>(min(NS - 2, nstages - 1 - s));
+    else
+      wait_vm_stages<S::loads, NS - 2>(min(NS - 2, nstages - 1 - s));
     ring_barrier();
-    if (s + NS - 1 < nstages) issue.template operator()<(BUF + NS - 1) % NS>(s + NS - 1);
+    if (s + NS - 1 < nstages) issue.template operator()<(BUF + NS - 1) % NS, TAIL>(s + NS - 1);
     if (!live) return;
     uint8_t* st = smem + BUF * S::bytes;
     const int hf = s & 1;
@@ -325,13 +350,23 @@ __global__ __launch_bounds__(kThreads) void k_gemm_kq(const uint8_t* W, int64_t 
     }
   };
 
-  [&]<int... B>(std::integer_sequence<int, B...>) __attribute__((always_inline)) {
-    ((B < nstages ? issue.template operator()<B>(B) : void()), ...);
-  }(std::make_integer_sequence<int, NS - 1>{});
-  for (int s = 0; s < nstages; s += NS) {
+  auto run = [&]<bool TAIL>() __attribute__((always_inline)) {
     [&]<int... B>(std::integer_sequence<int, B...>) __attribute__((always_inline)) {
-      ((s + B < nstages ? stage.template operator()<B>(s + B) : void()), ...);
-    }(std::make_integer_sequence<int, NS>{});
+      ((B < nstages ? issue.template operator()<B, TAIL>(B) : void()), ...);
+    }(std::make_integer_sequence<int, NS - 1>{});
+    for (int s = 0; s < nstages; s += NS) {
+      [&]<int... B>(std::integer_sequence<int, B...>) __attribute__((always_inline)) {
+        ((s + B < nstages ? stage.template operator()<B, TAIL>(s + B) : void()), ...);
+      }(std::make_integer_sequence<int, NS>{});
+    }
+  };
+  if constexpr (TYPE == kQ6_K) {
+    if (rt >= n_big)
+      run.template operator()<true>();
+    else
+      run.template operator()<false>();
+  } else {
+    run.template operator()<false>();
   }
 
   // Element i: token t0 + 8 (i / 4) + 4 h + i % 4, row 128 rt + 32 w + li.
@@ -374,7 +409,8 @@ void launch_kq(hipStream_t s, const void* w, int64_t rows, int64_t cols, const B
   // A short batch over slightly more than one 128-row tile per CU (the 14B gate|up, 34816 rows: 272 tiles) takes one
   // full tile per CU and covers the rest with 32-row tiles (one live wave), so that no CU runs two full tiles.
   // Measured at 17 tokens (bit-identical): Q6_K 34816 x 5120 65.3 -> 62.3 us, 40960 x 5120 66.4 -> 63.6, Q4_K
-  // 34816 x 5120 50.5 -> 48.4; at 24 tokens Q6_K 34816 x 5120 78.2 -> 75.6.
+  // 34816 x 5120 50.5 -> 48.4; at 24 tokens Q6_K 34816 x 5120 78.2 -> 75.6. Q6_K tail tiles copying only their
+  // 4 groups' quants and scales (4 instead of 6 copies per wave and stage): 61.9 -> 60.9 us, at 24 tokens 73.3 -> 70.8.
   if (n_tt == 1 && n_rt > cus && rows <= (kRowsT + 32) * cus) {
     n_big = (int)cus;
     n_rt = n_big + (int)((rows - kRowsT * cus) / 32);
