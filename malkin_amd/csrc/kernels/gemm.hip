@@ -117,6 +117,10 @@ __global__ __launch_bounds__((64 * StageLds<TOK, WT>::NW)) __attribute__((amdgpu
   const PackedQ8_0 L{rows, nb};
   const int64_t g0 = (int64_t)rt * (kRowsT / 8);                  // first 8-row group of the tile
   const int ngroups = (int)min<int64_t>(kRowsT / 8, rows / 8 - g0);  // 4 .. 16 (rows % 32 == 0)
+  // Waves whose 32 rows lie past the matrix (a partial last row tile) only copy in the three-per-CU form (NS = 2):
+  // there the branch also lets the wave fit its 168 registers without spilling (5 spilled before; config 1 54.2 ->
+  // 53.4 us, 24576 x 4096 at 512 tokens 180.1 -> 177.6, bit-identical); the other forms run 1-4 % slower with it.
+  const bool live = NS != 2 || 32 * rg < 8 * ngroups;
   const int t0 = tt * TOK;
   const int nstages = (nb + KB - 1) / KB;
 
@@ -319,7 +323,7 @@ __global__ __launch_bounds__((64 * StageLds<TOK, WT>::NW)) __attribute__((amdgpu
       (((K == 4 - RA) ? enter(s) : void(),
         (K >= 4 - RA) ? quarter.template operator()<BUF, (K + RA) % 4>(s + NS)
                       : (s >= 1 ? quarter.template operator()<PBUF, (K + RA) % 4>(s - 1 + NS) : void()),
-        step.template operator()<4 * BUF + K, (K + RA < 4 ? BUF : NBUF), (K + RA) % 4>(j + K * BPS)),
+        live ? step.template operator()<4 * BUF + K, (K + RA < 4 ? BUF : NBUF), (K + RA) % 4>(j + K * BPS) : void()),
        ...);
     }(std::make_integer_sequence<int, 4>{});
   };
@@ -333,8 +337,10 @@ __global__ __launch_bounds__((64 * StageLds<TOK, WT>::NW)) __attribute__((amdgpu
   wait_vm_stages<S::loads, NS - 2>(nstages - 1);
   ring_barrier();
   if (NS - 1 < nstages) issue.template operator()<NS - 1>(NS - 1);
-  read.template operator()<0, 0>(op[0].a0, op[0].a1, op[0].b0, op[0].b1, op[0].dw, op[0].dx);
-  if constexpr (RA == 2) read.template operator()<0, 1>(op[1].a0, op[1].a1, op[1].b0, op[1].b1, op[1].dw, op[1].dx);
+  if (live) {
+    read.template operator()<0, 0>(op[0].a0, op[0].a1, op[0].b0, op[0].b1, op[0].dw, op[0].dx);
+    if constexpr (RA == 2) read.template operator()<0, 1>(op[1].a0, op[1].a1, op[1].b0, op[1].b1, op[1].dw, op[1].dx);
+  }
   // Ring cycles, left after the last stage: every stage is four steps, so the register sets are in place at any stage
   // boundary and the last step's results are in rs[1].
   for (int s = 0; s < nstages; s += NS) {
